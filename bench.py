@@ -1,0 +1,174 @@
+"""Benchmark: seconds per denoise step of the Qwen-Image-shaped dual-stream MMDiT at 1024x1024 on one MI355X.
+
+Workload (a step): 60 dual-stream blocks, hidden 3072, 24 heads x 128, FFN 12288 (GELU-tanh), shift/scale/gate
+adaLN; 4096 image tokens (a 64 x 64 grid of 2x2-patched 16-channel latents) + 256 text tokens of width 3584 projected
+to 3072; classifier-free guidance as a batch of 2 (positive and negative prompt), then the guidance combine and the
+Euler update. bf16 weights (random-init N(0, 0.02), 40.8 GB) and activations, fp32 accumulation and residual stream.
+Synthetic inputs: prompts and latents N(0, 1), resident on the device when the timed region starts.
+
+Prints one JSON line. `roofline` is the dominant kernel class (the GEMMs): algorithmic FLOPs of its launches divided
+by their summed durations, from HIP events recorded around each launch on the engine's stream in a separate timed
+pass of the same steps. `cpu_baseline` is the oracle (CPU restatement of the same step) on a bounded sample of one
+block, timed on this host's cores and scaled by FLOPs to a whole step.
+"""
+import argparse
+import json
+import os
+import pathlib
+import sys
+import time
+
+ROOT = pathlib.Path(__file__).resolve().parent
+sys.path[:0] = [str(ROOT / "mako-image_amd"), str(ROOT / "oracle")]
+
+METRIC = "s/denoise-step Qwen-Image MMDiT 1024² bf16; attention+GEMM % of MFMA peak"
+PEAK_BF16 = 2.5e15  # MI355X dense bf16 MFMA, published
+CFG = dict(blocks=60, dim=3072, heads=24, head_dim=128, ffn=12288, text_dim=3584)
+H = W = 64
+S = 256
+
+
+def step_flops(blocks=60, D=3072, F=12288, N=4096, S=256, B=2, heads=24):
+    """Algorithmic FLOPs of one step (the blocks' GEMMs and attention; padding excluded)."""
+    T = N + S
+    lin = 2 * (N + S) * D * (3 * D + D + 2 * F)
+    attn = 4 * T * T * 128 * heads
+    return B * blocks * (lin + attn), B * blocks * lin, B * blocks * attn
+
+
+def cpu_baseline(seconds_target=12.0):
+    """The oracle on one dual-stream block of one sample at a reduced image size (32 x 32 tokens + 256 text), timed
+    on this host; throughput scaled to the full step's FLOPs."""
+    import numpy as np
+
+    import mkref as R
+
+    m = R.Model(R.DUAL, **{**CFG, "blocks": 1}, seed=0)
+    rng = np.random.default_rng(0)
+    n_side = 32
+    N = n_side * n_side
+    img = rng.standard_normal((N, 3072)).astype(np.float32)
+    txt = rng.standard_normal((S, 3072)).astype(np.float32)
+    mods = (rng.standard_normal((2, 6, 3072)) * 0.02).astype(np.float32)
+    cs = R.rope_table(S, n_side, n_side)
+    flops = step_flops(blocks=1, N=N, S=S, B=1)[0]
+    reps, t_total = 0, 0.0
+    while t_total < seconds_target and reps < 50:
+        a, b = img.copy(), txt.copy()
+        t0 = time.perf_counter()
+        m.dual_block(0, a, b, mods[0], mods[1], cs)
+        t_total += time.perf_counter() - t0
+        reps += 1
+    rate = flops * reps / t_total
+    return {"value": step_flops()[0] / rate, "unit": "s/step", "cores": R.lib().mkref_threads(), "kind": "port",
+            "sample": f"oracle (C++/OpenMP, fp32 over bf16 weights): {reps} x one dual-stream block of one sample at "
+                      f"{N} image + {S} text tokens ({flops / 1e9:.0f} GFLOP each, {t_total:.1f} s, "
+                      f"{rate / 1e9:.1f} GFLOP/s), scaled by FLOPs to the 60-block batch-2 step at 4096 + 256 tokens"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU: this build runs the step on one MI355X (asked for {max(args.gpus, world)}); "
+              f"run it with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+
+    import mkimage as M
+
+    M.call("mk_set_device", 0)
+    info = M.device_info()
+    eng = M.Engine(M.FAMILY_DUAL, **CFG)
+    t0 = time.perf_counter()
+    eng.init_random(0)
+    t_init = time.perf_counter() - t0
+    rng = np.random.default_rng(0)
+    for s in (0, 1):
+        eng.begin(rng.standard_normal((S, 3584)).astype(np.float32), H, W, s)
+    lat = [M.Dev.from_array(rng.standard_normal((H * W, 64)).astype(np.float32)), M.Dev(H * W * 64 * 4)]
+    sigmas = [1.0 - 0.02 * i for i in range(args.warmup + args.steps + 2)]
+    stream = eng.stream()
+
+    def run(i):
+        eng.step_cfg_device(lat[i % 2], sigmas[i], sigmas[i + 1], 4.0, lat[(i + 1) % 2], stream)
+
+    for i in range(args.warmup):
+        run(i)
+    M.call("mk_stream_synchronize", stream)
+    e0, e1 = M.Event(), M.Event()
+    M.call("mk_synchronize")
+    w0 = time.perf_counter()
+    e0.record(stream)
+    for i in range(args.steps):
+        run(args.warmup + i)
+    e1.record(stream)
+    M.call("mk_stream_synchronize", stream)
+    wall = time.perf_counter() - w0
+    ms = e0.elapsed_ms(e1) / args.steps
+    out = lat[(args.warmup + args.steps) % 2].to_array(np.float32, (H * W, 64))
+    if not np.isfinite(out).all():
+        raise RuntimeError("non-finite latents after the timed steps")
+
+    # per-kernel pass: events around every launch, same steps
+    eng.set_timing(True)
+    per = {}
+    for i in range(args.steps):
+        run(args.warmup + i)
+        for k, v in eng.timing().items():
+            acc = per.setdefault(k, {"ms": 0.0, "launches": 0, "flops": 0.0})
+            acc["ms"] += v["ms"]
+            acc["launches"] += v["launches"]
+            acc["flops"] += v["flops"]
+    eng.set_timing(False)
+    total, lin, attn = step_flops()
+    g, a = per["gemm"], per["attention"]
+    gemm_tf = g["flops"] / (g["ms"] / 1e3) / 1e12
+    attn_tf = a["flops"] / (a["ms"] / 1e3) / 1e12
+    both = (g["flops"] + a["flops"]) / ((g["ms"] + a["ms"]) / 1e3)
+    kernels = {k: {"ms_per_step": round(v["ms"] / args.steps, 3), "launches_per_step": v["launches"] // args.steps,
+                   **({"tflops": round(v["flops"] / (v["ms"] / 1e3) / 1e12, 1)} if v["flops"] else {})}
+               for k, v in sorted(per.items(), key=lambda kv: -kv[1]["ms"])}
+    line = {
+        "metric": METRIC,
+        "value": round(ms / 1e3, 5),
+        "unit": "s/step",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 3),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (random-init N(0,0.02) weights, N(0,1) latents and prompts)",
+        "config": {"workload": "Qwen-Image-shaped dual-stream MMDiT denoise step at 1024x1024, CFG batch 2",
+                   "blocks": 60, "dim": 3072, "heads": 24, "head_dim": 128, "ffn": 12288, "text_dim": 3584,
+                   "image_tokens": H * W, "text_tokens": S, "batch": 2, "weights": "bf16"},
+        "roofline": {"bound": "mfma", "kernel": "gemm (bf16 MFMA, all block and projection GEMMs)",
+                     "achieved": round(gemm_tf, 1), "peak": PEAK_BF16 / 1e12, "unit": "TFLOP/s",
+                     "frac": round(gemm_tf * 1e12 / PEAK_BF16, 4), "traffic": None},
+        "attention_gemm_mfma_frac": round(both / PEAK_BF16, 4),
+        "step_mfma_frac": round(total / (ms / 1e3) / PEAK_BF16, 4),
+        "attention": {"achieved": round(attn_tf, 1), "unit": "TFLOP/s", "frac": round(attn_tf * 1e12 / PEAK_BF16, 4)},
+        "step_tflop": round(total / 1e12, 2),
+        "kernels": kernels,
+        "wall_s_per_step": round(wall / args.steps, 5),
+        "device": info,
+        "weights_gb": round(eng.weight_bytes() / 1e9, 2),
+        "init_s": round(t_init, 2),
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

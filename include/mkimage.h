@@ -1,0 +1,261 @@
+/* mkimage — MI355X (gfx950) denoising hot path of mako-image, as a C ABI.
+ *
+ * Two surfaces, both plain C (pointers, sizes, status codes; no HIP or C++ types):
+ *  1. The engine: the sampler-facing API the reference's Engine subclasses expose,
+ *       begin(prompt, h, w, slot) / step(latents, sigma, slot)   (src/image/engine.hpp:161-166)
+ *     plus a batched classifier-free-guidance step that runs both slots as one batch of 2 and applies the guidance
+ *     combine and the Euler update on the device (src/image/engine.cpp:471-503).
+ *  2. The kernel-dispatch surface the step is built from: the runtime primitives the reference calls by name
+ *     (proj, attention, heads_norm_half, heads_half, ln_modulate, gate_add, silu, gelu_tanh, swiglu_rows, geglu_rows,
+ *     layer_norm, group_norm, norm; src/image/qwen_image.cpp:196-288, src/image/sdxl.cpp:425-457,742-796), taking
+ *     device pointers and a stream.
+ *
+ * Conventions: every call returns MK_OK or an error code and never throws; mk_last_error() gives the message of the
+ * calling thread's last failure. Device memory is the library's (mk_malloc) or the caller's; host buffers belong to
+ * the caller and are copied in and out. Streams are opaque `void*` (a hipStream_t; NULL = the default stream).
+ * An engine is not re-entrant: one thread drives it at a time (the reference serialises requests the same way,
+ * src/server/image_server.cpp:583).
+ */
+#ifndef MKIMAGE_H
+#define MKIMAGE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum mk_status {
+    MK_OK = 0,
+    MK_ERR_ARG = 1,     /* a bad size, slot, null pointer or shape (the reference throws std::runtime_error) */
+    MK_ERR_STATE = 2,   /* step before begin, missing weights */
+    MK_ERR_DEVICE = 3,  /* a HIP runtime error */
+    MK_ERR_NOMEM = 4,
+    MK_ERR_UNSUPPORTED = 5
+} mk_status;
+
+const char* mk_last_error(void);
+const char* mk_version(void);
+
+/* ------------------------------------------------------------------------------------------------------------
+ * Device plumbing (so callers need no other GPU runtime in the process).
+ * ------------------------------------------------------------------------------------------------------------ */
+mk_status mk_device_count(int* n);
+mk_status mk_set_device(int dev);
+/* name, compute units, max clock in kHz, gcn arch name ("gfx950...") */
+mk_status mk_device_info(int dev, char* name, size_t name_len, int* cus, int* clock_khz, char* arch, size_t arch_len);
+mk_status mk_malloc(void** p, size_t bytes);   /* zero-filled */
+mk_status mk_free(void* p);
+mk_status mk_memcpy_h2d(void* dst, const void* src, size_t bytes);
+mk_status mk_memcpy_d2h(void* dst, const void* src, size_t bytes);
+mk_status mk_memset(void* p, int v, size_t bytes);
+mk_status mk_synchronize(void);
+mk_status mk_stream_create(void** s);
+mk_status mk_stream_destroy(void* s);
+mk_status mk_stream_synchronize(void* s);
+mk_status mk_event_create(void** e);
+mk_status mk_event_destroy(void* e);
+mk_status mk_event_record(void* e, void* stream);
+mk_status mk_event_elapsed_ms(void* start, void* stop, float* ms);
+
+/* ------------------------------------------------------------------------------------------------------------
+ * Kernel-dispatch surface. Layouts: activations row-major [rows][cols]; weights row-major [out][in] (the
+ * reference's Tensor with dims[0] = in features, qwen_image.cpp:79-111); bf16 = uint16 bit patterns; fp8 = OCP e4m3.
+ * ------------------------------------------------------------------------------------------------------------ */
+
+enum mk_dtype { MK_F32 = 0, MK_BF16 = 1, MK_FP8_E4M3 = 2 };
+
+/* The GEMM's fused epilogue: what happens to acc = A W^T (* wscale[n]) + bias[n]. */
+enum mk_epilogue {
+    MK_EPI_STORE = 0,      /* C = acc (C dtype f32 or bf16) */
+    MK_EPI_GELU_TANH = 1,  /* C = gelu_tanh(acc) */
+    MK_EPI_GATE_ADD = 2,   /* X += gate[n] * acc, X fp32 (the dual-stream gated residual) */
+    MK_EPI_GATE_TANH = 3,  /* X += tanh(gate[n]) * acc (gate_add, image.metal:55-65) */
+    MK_EPI_SILU = 4,       /* C = silu(acc) */
+    MK_EPI_ADD = 5,        /* X += acc (plain residual) */
+    MK_EPI_HEADS = 6       /* q|k|v columns scattered to heads with per-head RMSNorm + RoPE (see mk_heads_args) */
+};
+
+typedef struct mk_heads_args {
+    /* Destination of the fused q/k/v epilogue: Q, K [batch][heads][n_pad][d] bf16 and V^T [batch][heads][d][k_pad]
+     * bf16, written at rows row0 + r (r the GEMM row within the batch). */
+    void* q;
+    void* k;
+    void* vt;
+    uint32_t heads, head_dim, q_pad, k_pad;
+    uint32_t row0;        /* sequence position of GEMM row 0: its RoPE table row and its K / V^T row */
+    uint32_t q_row0;      /* Q row of GEMM row 0 (the 2.1 graph's later steps write Q from 0, K / V from S) */
+    const float* norm_q;  /* [head_dim] or NULL (no norm) */
+    const float* norm_k;
+    const float* rope;    /* [rows][head_dim/2][2] (cos, sin) at row0 + r, or NULL */
+    uint32_t rope_mode;   /* 0 none, 1 half-split pairs (i, i + d/2), 2 interleaved pairs (2i, 2i+1) */
+    float eps;
+} mk_heads_args;
+
+typedef struct mk_gemm_args {
+    const void* a;        /* bf16 [batch][M][lda] */
+    const void* w;        /* [N][K] bf16 or fp8 */
+    const float* wscale;  /* [N] per-output-channel scale (fp8), or NULL */
+    const float* bias;    /* [N] or NULL */
+    void* c;              /* output [batch][M][ldc] (f32 or bf16), or the fp32 residual X for GATE/ADD */
+    const float* gate;    /* [N] gate row (GATE_ADD / GATE_TANH); rows r % seg_rows < split read gate + gate_alt */
+    int64_t gate_alt;
+    uint32_t split, seg_rows;
+    uint32_t M, N, K;
+    int64_t lda, ldc;
+    int64_t stride_a, stride_c; /* between batches, in elements */
+    uint32_t batch;
+    uint32_t w_dtype;     /* MK_BF16 or MK_FP8_E4M3 */
+    uint32_t c_dtype;     /* MK_F32 or MK_BF16 */
+    uint32_t epilogue;    /* mk_epilogue */
+    const mk_heads_args* heads; /* MK_EPI_HEADS only */
+} mk_gemm_args;
+
+/* proj (the reference's GEMM, engine.cpp:768 / qwen_image.cpp:196-288): C = A W^T with the fused epilogue.
+ * K % 64 == 0, N % 64 == 0. */
+mk_status mk_gemm(const mk_gemm_args* a, void* stream);
+
+/* GEMV for a few rows (the time embedding and modulation projections, rows <= 4):
+ * y[r][n] = act(sum_k W[n][k] x[r][k] + b[n]), x fp32 [rows][K], W bf16 [N][K], y fp32; act 0 none, 1 silu
+ * applied to x first (silu(x) is the modulation layers' input). */
+mk_status mk_gemv(const float* x, uint32_t rows, uint32_t K, const void* w, const float* bias, uint32_t N, float* y,
+                  int silu_x, void* stream);
+
+/* ln_modulate (image.metal:32-53): y = LN(x) (1 + scale) + shift, eps, no affine; x fp32 [rows][n], y bf16.
+ * Row r takes the modulation at scale/shift + alt (floats) when r % seg_rows < split, else at scale/shift. */
+mk_status mk_ln_modulate(const float* x, uint32_t rows, uint32_t n, const float* scale, const float* shift,
+                         int64_t alt, uint32_t split, uint32_t seg_rows, float eps, void* y, void* stream);
+
+/* gate_add (image.metal:55-65): x += g(gate) * y, g = tanh (tanh_gate = 1) or identity; x fp32, y fp32 or bf16
+ * [rows][n]; row selection of the gate as in mk_ln_modulate. */
+mk_status mk_gate_add(float* x, const void* y, uint32_t y_dtype, uint32_t rows, uint32_t n, const float* gate,
+                      int64_t alt, uint32_t split, uint32_t seg_rows, int tanh_gate, void* stream);
+
+/* heads_norm_half / heads_half (qwen_image.cpp:226-250, sdxl.cpp:439-448): per (row, head) of x bf16
+ * [batch][rows][ld] at column col0 + head * d: optional RMSNorm * w, RoPE from table rows rope[row0 + r], written
+ * bf16 to out [batch][heads][n_pad][d] at row0 + r (transpose = 0), or to out [batch][heads][d][n_pad] at column
+ * row0 + r (transpose = 1: the V^T layout the attention reads). */
+mk_status mk_heads(const void* x, uint32_t batch, uint32_t rows, int64_t ld, int64_t stride_x, uint32_t col0,
+                   uint32_t heads, uint32_t d, const float* w, float eps, const float* rope, uint32_t rope_mode,
+                   void* out, uint32_t n_pad, uint32_t row0, int transpose, void* stream);
+
+/* attention (qwen_image.cpp:271, sdxl.cpp:450-457): softmax(Q K^T scale) V, fp32 online softmax on bf16 MFMA.
+ * q [batch][heads][q_pad][d], k [batch][heads][k_pad][d], vt [batch][heads][d][k_pad] bf16 (padding keys zero);
+ * out bf16 [batch][n_q][ldo] at column head * d. Query row i (absolute q_pos0 + i) sees key c < n_k iff
+ * q_pos0 + i >= block or c <= q_pos0 + i (block 0: no mask; UINT32_MAX: causal; S: causal text prefix).
+ * d in {64, 128}; q_pad % 128 == 0; k_pad % 64 == 0. */
+mk_status mk_attention(const void* q, const void* k, const void* vt, void* out, uint32_t batch, uint32_t heads,
+                       uint32_t d, uint32_t n_q, uint32_t q_pad, uint32_t n_k, uint32_t k_pad, int64_t ldo,
+                       int64_t stride_o, uint32_t q_pos0, uint32_t block, float scale, void* stream);
+
+/* Elementwise and norms (fp32 unless stated). */
+mk_status mk_silu(float* x, size_t n, void* stream);
+mk_status mk_gelu_tanh(float* x, size_t n, void* stream);
+/* m[r][i] = silu(gu[r][i]) * gu[r][F + i] (swiglu_rows); m bf16 */
+mk_status mk_swiglu(const void* gu, uint32_t gu_dtype, uint32_t rows, uint32_t F, void* m, void* stream);
+/* m[r][i] = hg[r][i] * gelu_erf(hg[r][F + i]) (geglu_rows, image.metal:475-484); m bf16 */
+mk_status mk_geglu(const void* hg, uint32_t hg_dtype, uint32_t rows, uint32_t F, void* m, void* stream);
+/* y = x * rsqrt(mean(x^2) + eps) * w (+ w_offset), x fp32, y bf16 (norm) */
+mk_status mk_rms_norm(const float* x, uint32_t rows, uint32_t n, const float* w, float w_offset, float eps, void* y,
+                      void* stream);
+/* layer_norm with gamma, beta (sdxl.cpp:425-437): x fp32, y bf16 */
+mk_status mk_layer_norm(const float* x, uint32_t rows, uint32_t n, const float* g, const float* b, float eps, void* y,
+                        void* stream);
+/* group_norm over channels-last [batch][rows][c], `groups` groups, affine; y bf16 */
+mk_status mk_group_norm(const float* x, uint32_t batch, uint32_t rows, uint32_t c, uint32_t groups, const float* g,
+                        const float* b, float eps, void* y, void* stream);
+/* x_out = x + dt * (neg + guidance * (pos - neg)) over n floats (engine.cpp:476-502); guidance 1 / neg NULL:
+ * x + dt * pos. */
+mk_status mk_cfg_euler(const float* x, const float* pos, const float* neg, size_t n, float guidance, float dt,
+                       float* x_out, void* stream);
+/* 2x2 patchify: lat [batch][C][2h][2w] -> tokens [batch][h*w][4C] (feature c*4 + py*2 + px), and back. */
+mk_status mk_patchify(const float* lat, uint32_t batch, uint32_t C, uint32_t h, uint32_t w, float* tokens,
+                      void* stream);
+mk_status mk_unpatchify(const float* tokens, uint32_t batch, uint32_t C, uint32_t h, uint32_t w, float* lat,
+                        void* stream);
+/* Counter RNG fill (synthetic weights and inputs): value i = mean + std * N(0,1)[key, i], stored as dtype
+ * (bf16 rounded to nearest even). */
+mk_status mk_fill_normal(void* p, size_t n, uint32_t dtype, uint64_t key, double mean, double std, void* stream);
+uint64_t mk_tensor_key(uint64_t seed, const char* name);
+/* Per-output-row fp8 quantisation: scale[r] = max|W[r]| / 448 (1 for a zero row), dst[r][c] = e4m3(W[r][c] /
+ * scale[r]) rounded to nearest even, saturating; src bf16 [rows][cols]. */
+mk_status mk_quantize_fp8_rows(const void* src, uint64_t rows, uint64_t cols, void* dst, float* scale, void* stream);
+/* fp32 <-> bf16 conversions on the device */
+mk_status mk_f32_to_bf16(const float* x, size_t n, void* y, void* stream);
+mk_status mk_bf16_to_f32(const void* x, size_t n, float* y, void* stream);
+
+/* ------------------------------------------------------------------------------------------------------------
+ * Engine: the denoiser of one model family, weights resident on the device.
+ * ------------------------------------------------------------------------------------------------------------ */
+
+enum mk_family {
+    MK_FAMILY_DUAL = 0,  /* Qwen-Image (v1)-shaped dual-stream MMDiT (text and image weight sets, shift/scale/gate
+                            adaLN, GELU-tanh FFN, non-causal joint attention) */
+    MK_FAMILY_Q21 = 1,   /* Qwen-Image 2.1 as the reference runs it (qwen_image.cpp): one weight set, scale + tanh
+                            gate, SwiGLU, causal text prefix, text K/V cached after the first step */
+    MK_FAMILY_SDXL = 2   /* SDXL spatial transformer (sdxl.cpp:742-796) */
+};
+
+typedef struct mk_config {
+    uint32_t family;     /* mk_family */
+    uint32_t blocks;
+    uint32_t dim;        /* hidden width (SDXL: channels) */
+    uint32_t heads;
+    uint32_t head_dim;   /* 128 (SDXL: 64) */
+    uint32_t ffn;        /* FFN inner width (SwiGLU / GEGLU inner) */
+    uint32_t text_dim;   /* prompt embedding width */
+    uint32_t latent;     /* token latent width (64) */
+    uint32_t weight_dtype; /* MK_BF16 or MK_FP8_E4M3 for the block linears */
+    uint32_t max_batch;  /* 1 or 2 (CFG) */
+} mk_config;
+
+typedef struct mk_engine mk_engine;
+
+mk_status mk_engine_create(const mk_config* cfg, mk_engine** out);
+mk_status mk_engine_destroy(mk_engine* e);
+/* Upload one named weight (the reference's upload / upload_rows, qwen_image.cpp:79-111): `data` holds rows x cols
+ * values of `dtype` (fp32 vectors, bf16 matrices, e4m3 matrices; an fp8 matrix's scale is the fp32 tensor
+ * name + ".scale"). Names are the checkpoint's (Diffusers layout). */
+mk_status mk_engine_load(mk_engine* e, const char* name, const void* data, uint32_t dtype, uint64_t rows,
+                         uint64_t cols);
+/* Every weight from the counter RNG on the device: matrices N(0, 0.02), biases N(0, 0.02), norm scales 1 + N(0, 0.02),
+ * keyed by (seed, name) exactly as the CPU reference keys them. */
+mk_status mk_engine_init_random(mk_engine* e, uint64_t seed);
+/* Bytes of device memory the weights hold. */
+mk_status mk_engine_weight_bytes(const mk_engine* e, uint64_t* bytes);
+
+/* begin (engine.hpp:165): prompt [rows][text_dim] fp32 for a grid of h x w tokens; slot 0 or 1. */
+mk_status mk_begin(mk_engine* e, const float* prompt, size_t rows, uint32_t h, uint32_t w, uint32_t slot);
+/* step (engine.hpp:166): latents [h*w][latent] fp32 -> velocity [h*w][latent] fp32. */
+mk_status mk_step(mk_engine* e, const float* latents, size_t n, float sigma, uint32_t slot, float* out);
+/* Classifier-free guidance as one batch of 2 (slot 0 positive, slot 1 negative, both begun), then the Euler update:
+ * latents_out = latents + (sigma_next - sigma) (neg + guidance (pos - neg)). Host buffers. */
+mk_status mk_step_cfg(mk_engine* e, const float* latents, size_t n, float sigma, float sigma_next, float guidance,
+                      float* latents_out);
+/* The same on device buffers already resident (no host copies): lat and lat_out [h*w][latent] fp32 device pointers
+ * (may alias). The bench times this. */
+mk_status mk_step_cfg_device(mk_engine* e, const float* lat, float sigma, float sigma_next, float guidance,
+                             float* lat_out, void* stream);
+/* The step's stream (kernels are launched on it). */
+mk_status mk_engine_stream(mk_engine* e, void** stream);
+
+/* Probe of intermediates (the reference's set_probe, tests/image_ref_test.cpp:133-136): called synchronously on the
+ * host after a stage with its name ("temb", "modulation", "txt_in", "img_in", "block", "norm_out"), its layer
+ * (-1 none), the data copied to host fp32 and its length. NULL turns it off. Slows the step (synchronises). */
+typedef void (*mk_probe_fn)(void* user, const char* name, int layer, const float* data, size_t n);
+mk_status mk_engine_set_probe(mk_engine* e, mk_probe_fn fn, void* user);
+
+/* Per-kernel timing of the last step with events on the step's stream (enable before the step): names and total
+ * milliseconds per kernel class ("gemm", "attention", ...). */
+mk_status mk_engine_set_timing(mk_engine* e, int on);
+mk_status mk_engine_timing(mk_engine* e, uint32_t i, const char** name, float* ms, uint32_t* launches, double* flops);
+
+/* SDXL spatial transformer (config: MK_FAMILY_SDXL): x [batch][n][c] fp32 device -> y [batch][n][c] fp32 device,
+ * cross-attending to the context of mk_begin (slot 0 for batch row 0, slot 1 for row 1). */
+mk_status mk_sdxl_forward(mk_engine* e, const float* x, uint32_t batch, uint32_t n, float* y, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

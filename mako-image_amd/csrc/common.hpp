@@ -1,0 +1,131 @@
+// Shared device helpers for the gfx950 kernels: bf16 / fp8 conversions, wave64 reductions, vector types, the
+// counter RNG, and the thread-local error state of the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstring>
+#include <string>
+
+#include "../../include/mkimage.h"
+
+namespace mk {
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
+typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4;
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
+typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4;
+typedef __attribute__((__vector_size__(2 * sizeof(uint32_t)))) uint32_t u32x2;
+
+constexpr int kWave = 64;
+
+typedef __attribute__((address_space(3))) void lds_void;
+// 16 bytes global -> LDS without a register round trip (global_load_lds_dwordx4): lane i's bytes land at
+// lds + 16 * i (lds wave-uniform). The source goes through `const void*`: a typed pointer there makes the host pass
+// drop the kernel's launch stub without a diagnostic.
+__device__ inline void load_lds16(const void* src, lds_void* lds) { __builtin_amdgcn_global_load_lds(src, lds, 16, 0, 0); }
+
+// ---- error state (thread-local, read by mk_last_error) ----
+void set_error(const std::string& msg);
+mk_status fail(mk_status s, const std::string& msg);
+mk_status hip_check(hipError_t e, const char* what);
+
+#define MK_HIP(call)                                                                                               \
+    do {                                                                                                           \
+        hipError_t e_ = (call);                                                                                    \
+        if (e_ != hipSuccess)                                                                                      \
+            return ::mk::hip_check(e_, #call);                                                                     \
+    } while (0)
+
+#define MK_LAUNCH_CHECK(what)                                                                                      \
+    do {                                                                                                           \
+        hipError_t e_ = hipGetLastError();                                                                         \
+        if (e_ != hipSuccess)                                                                                      \
+            return ::mk::hip_check(e_, what);                                                                      \
+    } while (0)
+
+// ---- bf16: round-to-nearest-even, bit-exact with the CPU reference's rule ----
+__host__ __device__ inline uint16_t f2bf_bits(float x)
+{
+    uint32_t u = __builtin_bit_cast(uint32_t, x);
+    if ((u & 0x7fffffffu) > 0x7f800000u)
+        return uint16_t((u >> 16) | 0x40);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return uint16_t(u >> 16);
+}
+__host__ __device__ inline float bf2f_bits(uint16_t b) { return __builtin_bit_cast(float, uint32_t(b) << 16); }
+// Two floats to a packed pair of bf16 (low half = a).
+__device__ inline uint32_t pack_bf16x2(float a, float b)
+{
+    return uint32_t(f2bf_bits(a)) | (uint32_t(f2bf_bits(b)) << 16);
+}
+
+// ---- OCP fp8 e4m3 -> float (exact) ----
+__host__ __device__ inline float e4m3_to_f32(uint8_t b)
+{
+    const uint32_t s = b >> 7, e = (b >> 3) & 15u, m = b & 7u;
+    float v;
+    if (e == 0)
+        v = float(m) * 0.001953125f; // m / 8 * 2^-6
+    else
+        v = __builtin_bit_cast(float, ((e + 120u) << 23) | (m << 20));
+    if (e == 15 && m == 7)
+        v = __builtin_nanf("");
+    return s ? -v : v;
+}
+
+// ---- wave64 reductions (DPP-free: the compiler lowers shfl_xor to ds_swizzle / permute) ----
+__device__ inline float wave_sum(float v)
+{
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1)
+        v += __shfl_xor(v, o, 64);
+    return v;
+}
+__device__ inline float wave_max(float v)
+{
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1)
+        v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+// ---- activations (fp32) ----
+__device__ inline float silu_f(float x) { return x / (1.0f + __expf(-x)); }
+__device__ inline float gelu_tanh_f(float x)
+{
+    const float u = 0.7978845608028654f * (x + 0.044715f * x * x * x);
+    return 0.5f * x * (1.0f + tanhf(u));
+}
+// erf by the Numerical Recipes erfc Chebyshev fit (max error ~1.2e-7), the form the reference's geglu uses
+// (image.metal:450-463).
+__device__ inline float erf_fit(float x)
+{
+    const float z = fabsf(x), t = 1.0f / (1.0f + 0.5f * z);
+    const float r =
+        t * __expf(-z * z - 1.26551223f +
+                   t * (1.00002368f +
+                        t * (0.37409196f +
+                             t * (0.09678418f +
+                                  t * (-0.18628806f +
+                                       t * (0.27886807f +
+                                            t * (-1.13520398f + t * (1.48851587f + t * (-0.82215223f + t * 0.17087277f)))))))));
+    return x >= 0.0f ? 1.0f - r : r - 1.0f;
+}
+
+// ---- counter RNG: splitmix64, Box-Muller in double (the same sequence as the CPU reference's) ----
+__host__ __device__ inline uint64_t splitmix64(uint64_t z)
+{
+    z += 0x9e3779b97f4a7c15ull;
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    return z ^ (z >> 31);
+}
+uint64_t tensor_key(uint64_t seed, const char* name);
+
+inline uint32_t cdiv(uint64_t a, uint64_t b) { return uint32_t((a + b - 1) / b); }
+inline uint64_t round_up(uint64_t a, uint64_t b) { return (a + b - 1) / b * b; }
+
+} // namespace mk

@@ -1,0 +1,1082 @@
+// The engine: one model family's denoiser with its weights resident on the device, driving the kernel-dispatch
+// surface of the C ABI on one stream. It mirrors the reference's Engine subclasses:
+//   - load / upload_rows: named checkpoint tensors, q|k|v and gate|up fused along output rows at load
+//     (src/image/qwen_image.cpp:79-111, src/image/sdxl.cpp:264-310);
+//   - begin(prompt, h, w, slot): the RoPE table and per-slot text state (qwen_image.cpp:113-142; sdxl.cpp:672-720);
+//   - step(latents, sigma, slot): one transformer pass (qwen_image.cpp:144-293), here for three graphs over one kernel
+//     set: the dual-stream MMDiT (text and image weight sets, shift/scale/gate adaLN, GELU-tanh FFN), Qwen-Image 2.1
+//     as the reference runs it (shared weights, scale + tanh gate, SwiGLU, causal text prefix, text K/V cached after
+//     the first step), and the SDXL spatial transformer (sdxl.cpp:742-796);
+//   - the guided Euler step of the sampler loop (engine.cpp:471-503) with both guidance passes as one batch of 2.
+#include "common.hpp"
+
+#include <cmath>
+#include <map>
+#include <memory>
+#include <vector>
+
+namespace mk {
+
+namespace {
+
+// Device buffer that grows (zero-filled) on demand.
+struct Buf {
+    void* p = nullptr;
+    size_t bytes = 0;
+    Buf() = default;
+    Buf(const Buf&) = delete;
+    Buf& operator=(const Buf&) = delete;
+    ~Buf()
+    {
+        if (p)
+            (void)hipFree(p);
+    }
+    mk_status ensure(size_t b)
+    {
+        if (b <= bytes)
+            return MK_OK;
+        if (p)
+            MK_HIP(hipFree(p));
+        p = nullptr;
+        bytes = 0;
+        MK_HIP(hipMalloc(&p, b));
+        MK_HIP(hipMemset(p, 0, b));
+        bytes = b;
+        return MK_OK;
+    }
+    float* f() const { return static_cast<float*>(p); }
+    uint16_t* h() const { return static_cast<uint16_t*>(p); }
+};
+
+#define MK_TRY(x)                                                                                                  \
+    do {                                                                                                           \
+        mk_status s_ = (x);                                                                                        \
+        if (s_ != MK_OK)                                                                                           \
+            return s_;                                                                                             \
+    } while (0)
+
+// A linear layer on the device: W [out][in] (bf16 or fp8 with per-row scale), optional bias.
+struct Linear {
+    void* w = nullptr;
+    uint32_t dtype = MK_BF16;
+    float* scale = nullptr;
+    float* bias = nullptr;
+    uint32_t out = 0, in = 0;
+};
+
+// Where a checkpoint tensor goes: a device region (part of a fused tensor) and how to synthesise it.
+struct Dest {
+    void* p = nullptr;     // first element of this tensor's rows
+    uint32_t dtype = MK_F32;
+    uint64_t rows = 0, cols = 0;
+    float* scale = nullptr; // fp8: per-row scale destination
+    double mean = 0, std = 0.02;
+};
+
+// Bookkeeping of kernel time per class (events on the step's stream).
+struct Timing {
+    bool on = false;
+    struct Ev {
+        hipEvent_t a, b;
+        int cls;
+        double flops;
+    };
+    std::vector<Ev> evs;
+    std::vector<std::string> names;
+    std::vector<float> ms;
+    std::vector<uint32_t> launches;
+    std::vector<double> flops;
+    int cls(const char* n)
+    {
+        for (size_t i = 0; i < names.size(); ++i)
+            if (names[i] == n)
+                return int(i);
+        names.push_back(n);
+        ms.push_back(0);
+        launches.push_back(0);
+        flops.push_back(0);
+        return int(names.size() - 1);
+    }
+};
+
+} // namespace
+} // namespace mk
+
+using namespace mk;
+
+struct mk_engine {
+    mk_config cfg{};
+    hipStream_t stream = nullptr;
+    std::vector<void*> allocs; // weight storage
+    std::map<std::string, Dest> dests;
+    uint64_t weight_bytes = 0;
+
+    // ---- weights (dual: index 0 image stream, 1 text stream) ----
+    Linear img_in, txt_in, t_lin1, t_lin2, norm_out, proj_out, mods;
+    Linear txt_in1, txt_in2;        // Q21 text in
+    float* txt_norm = nullptr;      // Q21: stored zero-centred, +1 applied by the kernel
+    struct Block {
+        Linear qkv[2], o[2], ff1[2], ff2[2];
+        float *nq[2] = {}, *nk[2] = {};
+        // SDXL
+        Linear q2, kv2;
+        float *n1g = nullptr, *n1b = nullptr, *n2g = nullptr, *n2b = nullptr, *n3g = nullptr, *n3b = nullptr;
+    };
+    std::vector<Block> blocks;
+    // SDXL transformer ends
+    float *gn_g = nullptr, *gn_b = nullptr;
+    Linear proj_in;
+
+    // ---- begin state ----
+    struct Slot {
+        bool begun = false;
+        uint32_t S = 0, steps = 0;
+        Buf prompt;               // [S][text_dim] fp32
+        Buf kcache, vcache;       // Q21: [blocks][H][S][128] K and [blocks][H][128][S] V^T
+        Buf ck, cvt;              // SDXL: per-block cross K [blocks][H][s_pad][64], V^T [blocks][H][64][s_pad]
+    } slots[2];
+    uint32_t gh = 0, gw = 0;
+    std::vector<float> rope_host;
+    Buf rope;                     // [S + N][64][2]
+    uint32_t rope_S = 0xffffffffu;
+
+    // ---- scratch ----
+    Buf x_img, x_txt, xn_img, xn_txt, q, k, vt, att, hid, out, lat, lat_bf, tn, tproj, temb_h, temb, mod, omod, qkv,
+        gu;
+    Buf xo; // SDXL
+
+    // ---- probe / timing ----
+    mk_probe_fn probe = nullptr;
+    void* probe_user = nullptr;
+    Timing timing;
+
+    // ---------------------------------------------------------------------------------------------------------
+    mk_status alloc_w(size_t bytes, void** p)
+    {
+        MK_HIP(hipMalloc(p, bytes));
+        MK_HIP(hipMemset(*p, 0, bytes));
+        allocs.push_back(*p);
+        weight_bytes += bytes;
+        return MK_OK;
+    }
+    static size_t esize(uint32_t dt) { return dt == MK_F32 ? 4 : dt == MK_BF16 ? 2 : 1; }
+
+    // A fused linear layer from `parts` checkpoint names stacked along output rows (upload_rows).
+    mk_status linear(Linear& L, const std::vector<std::string>& parts, uint32_t rows_each, uint32_t in, bool bias,
+                     uint32_t dtype = MK_BF16)
+    {
+        L.out = rows_each * uint32_t(parts.size());
+        L.in = in;
+        L.dtype = dtype;
+        MK_TRY(alloc_w(size_t(L.out) * in * esize(dtype), &L.w));
+        if (dtype == MK_FP8_E4M3)
+            MK_TRY(alloc_w(size_t(L.out) * 4, reinterpret_cast<void**>(&L.scale)));
+        if (bias)
+            MK_TRY(alloc_w(size_t(L.out) * 4, reinterpret_cast<void**>(&L.bias)));
+        for (size_t i = 0; i < parts.size(); ++i) {
+            Dest d;
+            d.p = static_cast<char*>(L.w) + i * size_t(rows_each) * in * esize(dtype);
+            d.dtype = dtype;
+            d.rows = rows_each;
+            d.cols = in;
+            d.scale = L.scale ? L.scale + i * rows_each : nullptr;
+            dests[parts[i] + ".weight"] = d;
+            if (bias) {
+                Dest b;
+                b.p = L.bias + i * rows_each;
+                b.rows = rows_each;
+                b.cols = 1;
+                dests[parts[i] + ".bias"] = b;
+            }
+        }
+        return MK_OK;
+    }
+    mk_status vec(float** p, const std::string& name, uint32_t n, double mean)
+    {
+        MK_TRY(alloc_w(size_t(n) * 4, reinterpret_cast<void**>(p)));
+        Dest d;
+        d.p = *p;
+        d.rows = n;
+        d.cols = 1;
+        d.mean = mean;
+        dests[name] = d;
+        return MK_OK;
+    }
+
+    mk_status build()
+    {
+        const uint32_t D = cfg.dim, F = cfg.ffn, E = cfg.text_dim, L = cfg.latent, hd = cfg.head_dim;
+        const uint32_t wdt = cfg.weight_dtype;
+        blocks.resize(cfg.blocks);
+        if (cfg.family == MK_FAMILY_DUAL) {
+            MK_TRY(linear(img_in, {"img_in"}, D, L, true));
+            MK_TRY(vec(&txt_norm, "txt_norm.weight", E, 1.0));
+            MK_TRY(linear(txt_in, {"txt_in"}, D, E, true));
+            MK_TRY(linear(t_lin1, {"time_text_embed.timestep_embedder.linear_1"}, D, 256, true));
+            MK_TRY(linear(t_lin2, {"time_text_embed.timestep_embedder.linear_2"}, D, D, true));
+            MK_TRY(linear(norm_out, {"norm_out.linear"}, 2 * D, D, true));
+            MK_TRY(linear(proj_out, {"proj_out"}, L, D, true));
+            // Every block's image and text modulation stacked: [blocks][2][6D] rows, one GEMV a step.
+            std::vector<std::string> mparts;
+            for (uint32_t i = 0; i < cfg.blocks; ++i) {
+                const std::string b = "transformer_blocks." + std::to_string(i) + ".";
+                mparts.push_back(b + "img_mod.1");
+                mparts.push_back(b + "txt_mod.1");
+            }
+            MK_TRY(linear(mods, mparts, 6 * D, D, true));
+            for (uint32_t i = 0; i < cfg.blocks; ++i) {
+                const std::string b = "transformer_blocks." + std::to_string(i) + ".";
+                Block& B = blocks[i];
+                MK_TRY(linear(B.qkv[0], {b + "attn.to_q", b + "attn.to_k", b + "attn.to_v"}, D, D, true, wdt));
+                MK_TRY(linear(B.qkv[1], {b + "attn.add_q_proj", b + "attn.add_k_proj", b + "attn.add_v_proj"}, D, D,
+                              true, wdt));
+                MK_TRY(linear(B.o[0], {b + "attn.to_out.0"}, D, D, true, wdt));
+                MK_TRY(linear(B.o[1], {b + "attn.to_add_out"}, D, D, true, wdt));
+                MK_TRY(vec(&B.nq[0], b + "attn.norm_q.weight", hd, 1.0));
+                MK_TRY(vec(&B.nk[0], b + "attn.norm_k.weight", hd, 1.0));
+                MK_TRY(vec(&B.nq[1], b + "attn.norm_added_q.weight", hd, 1.0));
+                MK_TRY(vec(&B.nk[1], b + "attn.norm_added_k.weight", hd, 1.0));
+                MK_TRY(linear(B.ff1[0], {b + "img_mlp.net.0.proj"}, F, D, true, wdt));
+                MK_TRY(linear(B.ff2[0], {b + "img_mlp.net.2"}, D, F, true, wdt));
+                MK_TRY(linear(B.ff1[1], {b + "txt_mlp.net.0.proj"}, F, D, true, wdt));
+                MK_TRY(linear(B.ff2[1], {b + "txt_mlp.net.2"}, D, F, true, wdt));
+            }
+        } else if (cfg.family == MK_FAMILY_Q21) {
+            MK_TRY(linear(img_in, {"img_in"}, D, L, false));
+            MK_TRY(vec(&txt_norm, "txt_in.text_norm.weight", E, 0.0));
+            MK_TRY(linear(txt_in1, {"txt_in.in_layer"}, D, E, false));
+            MK_TRY(linear(txt_in2, {"txt_in.out_layer"}, D, D, false));
+            MK_TRY(linear(t_lin1, {"time_text_embed.timestep_embedder.linear_1"}, D, 256, false));
+            MK_TRY(linear(t_lin2, {"time_text_embed.timestep_embedder.linear_2"}, D, D, false));
+            MK_TRY(linear(mods, {"modulation.1"}, 4 * D, D, false));
+            MK_TRY(linear(norm_out, {"norm_out.linear"}, D, D, false));
+            MK_TRY(linear(proj_out, {"proj_out"}, L, D, false));
+            for (uint32_t i = 0; i < cfg.blocks; ++i) {
+                const std::string b = "transformer_blocks." + std::to_string(i) + ".";
+                Block& B = blocks[i];
+                MK_TRY(linear(B.qkv[0], {b + "attn.to_q", b + "attn.to_k", b + "attn.to_v"}, D, D, false, wdt));
+                MK_TRY(linear(B.o[0], {b + "attn.to_out.0"}, D, D, false, wdt));
+                MK_TRY(vec(&B.nq[0], b + "attn.norm_q.weight", hd, 1.0));
+                MK_TRY(vec(&B.nk[0], b + "attn.norm_k.weight", hd, 1.0));
+                // gate rows first (qwen_image.cpp:104-105, 315-316)
+                MK_TRY(linear(B.ff1[0], {b + "img_mlp.gate_layer", b + "img_mlp.proj"}, F, D, false, wdt));
+                MK_TRY(linear(B.ff2[0], {b + "img_mlp.out"}, D, F, false, wdt));
+            }
+        } else if (cfg.family == MK_FAMILY_SDXL) {
+            MK_TRY(vec(&gn_g, "norm.weight", D, 1.0));
+            MK_TRY(vec(&gn_b, "norm.bias", D, 0.0));
+            MK_TRY(linear(proj_in, {"proj_in"}, D, D, true));
+            MK_TRY(linear(proj_out, {"proj_out"}, D, D, true));
+            for (uint32_t i = 0; i < cfg.blocks; ++i) {
+                const std::string b = "transformer_blocks." + std::to_string(i) + ".";
+                Block& B = blocks[i];
+                MK_TRY(vec(&B.n1g, b + "norm1.weight", D, 1.0));
+                MK_TRY(vec(&B.n1b, b + "norm1.bias", D, 0.0));
+                MK_TRY(vec(&B.n2g, b + "norm2.weight", D, 1.0));
+                MK_TRY(vec(&B.n2b, b + "norm2.bias", D, 0.0));
+                MK_TRY(vec(&B.n3g, b + "norm3.weight", D, 1.0));
+                MK_TRY(vec(&B.n3b, b + "norm3.bias", D, 0.0));
+                MK_TRY(linear(B.qkv[0], {b + "attn1.to_q", b + "attn1.to_k", b + "attn1.to_v"}, D, D, false, wdt));
+                MK_TRY(linear(B.o[0], {b + "attn1.to_out.0"}, D, D, true, wdt));
+                MK_TRY(linear(B.q2, {b + "attn2.to_q"}, D, D, false, wdt));
+                MK_TRY(linear(B.kv2, {b + "attn2.to_k", b + "attn2.to_v"}, D, E, false, wdt));
+                MK_TRY(linear(B.o[1], {b + "attn2.to_out.0"}, D, D, true, wdt));
+                MK_TRY(linear(B.ff1[0], {b + "ff.net.0.proj"}, 2 * F, D, true, wdt));
+                MK_TRY(linear(B.ff2[0], {b + "ff.net.2"}, D, F, true, wdt));
+            }
+        } else {
+            return fail(MK_ERR_ARG, "engine: unknown family");
+        }
+        return MK_OK;
+    }
+
+    // ---------------------------------------------------------------------------------------------------------
+    // launches with optional timing
+    template <typename F>
+    mk_status timed(const char* cls, double flops, F&& f)
+    {
+        if (!timing.on)
+            return f();
+        Timing::Ev ev{};
+        MK_HIP(hipEventCreate(&ev.a));
+        MK_HIP(hipEventCreate(&ev.b));
+        ev.cls = timing.cls(cls);
+        ev.flops = flops;
+        MK_HIP(hipEventRecord(ev.a, stream));
+        mk_status s = f();
+        MK_HIP(hipEventRecord(ev.b, stream));
+        timing.evs.push_back(ev);
+        return s;
+    }
+    mk_status finish_timing()
+    {
+        if (!timing.on)
+            return MK_OK;
+        MK_HIP(hipStreamSynchronize(stream));
+        for (size_t i = 0; i < timing.names.size(); ++i) {
+            timing.ms[i] = 0;
+            timing.launches[i] = 0;
+            timing.flops[i] = 0;
+        }
+        for (auto& e : timing.evs) {
+            float ms = 0;
+            MK_HIP(hipEventElapsedTime(&ms, e.a, e.b));
+            timing.ms[e.cls] += ms;
+            timing.launches[e.cls] += 1;
+            timing.flops[e.cls] += e.flops;
+            (void)hipEventDestroy(e.a);
+            (void)hipEventDestroy(e.b);
+        }
+        timing.evs.clear();
+        return MK_OK;
+    }
+
+    // GEMM: C[batch][M][ldc] (epilogue) = A[batch][M][lda] W^T
+    mk_status gemm(const Linear& L, const void* A, int64_t lda, int64_t sa, uint32_t M, uint32_t batch, void* C,
+                   int64_t ldc, int64_t sc, uint32_t epi, uint32_t cdt, const float* gate = nullptr,
+                   int64_t gate_alt = 0, uint32_t split = 0, uint32_t seg = 0, const mk_heads_args* heads = nullptr,
+                   const char* cls = "gemm")
+    {
+        mk_gemm_args g{};
+        g.a = A;
+        g.w = L.w;
+        g.wscale = L.scale;
+        g.bias = L.bias;
+        g.c = C;
+        g.gate = gate;
+        g.gate_alt = gate_alt;
+        g.split = split;
+        g.seg_rows = seg;
+        g.M = M;
+        g.N = L.out;
+        g.K = L.in;
+        g.lda = lda;
+        g.ldc = ldc;
+        g.stride_a = sa;
+        g.stride_c = sc;
+        g.batch = batch;
+        g.w_dtype = L.dtype;
+        g.c_dtype = cdt;
+        g.epilogue = epi;
+        g.heads = heads;
+        return timed(cls, 2.0 * M * L.out * L.in * batch, [&] { return mk_gemm(&g, stream); });
+    }
+
+    mk_status probe_f32(const char* name, int layer, const float* d, size_t n)
+    {
+        if (!probe)
+            return MK_OK;
+        std::vector<float> h(n);
+        MK_HIP(hipStreamSynchronize(stream));
+        MK_HIP(hipMemcpy(h.data(), d, n * 4, hipMemcpyDeviceToHost));
+        probe(probe_user, name, layer, h.data(), n);
+        return MK_OK;
+    }
+    mk_status probe_bf16(const char* name, int layer, const uint16_t* d, size_t n)
+    {
+        if (!probe)
+            return MK_OK;
+        std::vector<uint16_t> h(n);
+        std::vector<float> f(n);
+        MK_HIP(hipStreamSynchronize(stream));
+        MK_HIP(hipMemcpy(h.data(), d, n * 2, hipMemcpyDeviceToHost));
+        for (size_t i = 0; i < n; ++i)
+            f[i] = bf2f_bits(h[i]);
+        probe(probe_user, name, layer, f.data(), n);
+        return MK_OK;
+    }
+
+    // The rope3 table (qwen_image.cpp:31-45,132-141): text at (t, t, t), image at frame S with a centred grid.
+    static void rope3(float* cs, int64_t f, int64_t hpos, int64_t wpos)
+    {
+        const int dims[3] = {16, 56, 56};
+        const int64_t pos[3] = {f, hpos, wpos};
+        int i = 0;
+        for (int a = 0; a < 3; ++a)
+            for (int j = 0; j < dims[a] / 2; ++j, ++i) {
+                const float inv = 1.0f / std::pow(10000.0f, float(2 * j) / float(dims[a]));
+                const float ang = float(pos[a]) * inv;
+                cs[2 * i] = std::cos(ang);
+                cs[2 * i + 1] = std::sin(ang);
+            }
+    }
+    mk_status make_rope(uint32_t S)
+    {
+        if (S == rope_S && !rope_host.empty())
+            return MK_OK;
+        const uint64_t T = uint64_t(S) + uint64_t(gh) * gw;
+        rope_host.assign(T * 128, 0.0f);
+        for (uint32_t t = 0; t < S; ++t)
+            rope3(rope_host.data() + uint64_t(t) * 128, t, t, t);
+        for (uint32_t y = 0; y < gh; ++y)
+            for (uint32_t x = 0; x < gw; ++x)
+                rope3(rope_host.data() + (uint64_t(S) + y * gw + x) * 128, S, int64_t(y) - int64_t(gh - gh / 2),
+                      int64_t(x) - int64_t(gw - gw / 2));
+        MK_TRY(rope.ensure(rope_host.size() * 4));
+        MK_HIP(hipMemcpy(rope.p, rope_host.data(), rope_host.size() * 4, hipMemcpyHostToDevice));
+        rope_S = S;
+        return MK_OK;
+    }
+
+    // Sinusoidal embedding, cos half first (qwen_image.cpp:179-187), of v (= 1000 sigma) for each row.
+    static void sinusoid(float v, float* out)
+    {
+        for (uint32_t i = 0; i < 128; ++i) {
+            const float freq = std::exp(-std::log(10000.0f) * float(i) / 128.0f);
+            out[i] = std::cos(v * freq);
+            out[128 + i] = std::sin(v * freq);
+        }
+    }
+
+    // ---------------------------------------------------------------------------------------------------------
+    // Dual-stream step over `nb` samples sharing sigma: lat [nb][N][L] fp32 (device) -> out [nb][N][L] fp32.
+    // slot_of[b] names the text state of sample b; all samples' texts have S rows.
+    mk_status dual_step(const float* lat_dev, float sigma, const uint32_t* slot_of, uint32_t nb)
+    {
+        const uint32_t D = cfg.dim, H = cfg.heads, F = cfg.ffn, E = cfg.text_dim, L = cfg.latent;
+        const uint32_t S = slots[slot_of[0]].S, N = gh * gw, T = S + N;
+        const uint32_t q_pad = uint32_t(round_up(T, 256)), k_pad = uint32_t(round_up(T, 64));
+        const float eps = 1e-6f;
+        MK_TRY(make_rope(S));
+        // scratch
+        MK_TRY(x_img.ensure(size_t(nb) * N * D * 4));
+        MK_TRY(x_txt.ensure(size_t(nb) * S * D * 4));
+        MK_TRY(xn_img.ensure(size_t(nb) * N * D * 2));
+        MK_TRY(xn_txt.ensure(size_t(nb) * S * D * 2));
+        MK_TRY(q.ensure(size_t(nb) * H * q_pad * 128 * 2));
+        MK_TRY(k.ensure(size_t(nb) * H * k_pad * 128 * 2));
+        MK_TRY(vt.ensure(size_t(nb) * H * 128 * k_pad * 2));
+        MK_TRY(att.ensure(size_t(nb) * T * D * 2));
+        MK_TRY(hid.ensure(size_t(nb) * std::max(N, S) * F * 2));
+        MK_TRY(out.ensure(size_t(nb) * N * L * 4));
+        MK_TRY(lat_bf.ensure(size_t(nb) * N * L * 2));
+        MK_TRY(tn.ensure(size_t(nb) * S * E * 2));
+        MK_TRY(tproj.ensure(256 * 4));
+        MK_TRY(temb_h.ensure(size_t(D) * 4));
+        MK_TRY(temb.ensure(size_t(D) * 4));
+        MK_TRY(mod.ensure(size_t(cfg.blocks) * 12 * D * 4));
+        MK_TRY(omod.ensure(size_t(2) * D * 4));
+        if (k_pad_last != k_pad) {
+            // a new key padding: the padded keys / values must be zero
+            MK_HIP(hipMemsetAsync(k.p, 0, k.bytes, stream));
+            MK_HIP(hipMemsetAsync(vt.p, 0, vt.bytes, stream));
+            k_pad_last = k_pad;
+        }
+        // time embedding -> every block's modulation (silu(temb) feeds them all) and the output norm's
+        float tp[256];
+        sinusoid(1000.0f * sigma, tp);
+        MK_HIP(hipMemcpyAsync(tproj.p, tp, sizeof(tp), hipMemcpyHostToDevice, stream));
+        MK_TRY(timed("gemv", 2.0 * D * 256, [&] { return mk_gemv(tproj.f(), 1, 256, t_lin1.w, t_lin1.bias, D, temb_h.f(), 0, stream); }));
+        MK_TRY(timed("gemv", 2.0 * D * D, [&] { return mk_gemv(temb_h.f(), 1, D, t_lin2.w, t_lin2.bias, D, temb.f(), 1, stream); }));
+        MK_TRY(probe_f32("temb", -1, temb.f(), D));
+        MK_TRY(timed("gemv", 2.0 * mods.out * D, [&] { return mk_gemv(temb.f(), 1, D, mods.w, mods.bias, mods.out, mod.f(), 1, stream); }));
+        MK_TRY(probe_f32("modulation", -1, mod.f(), size_t(cfg.blocks) * 12 * D));
+        MK_TRY(timed("gemv", 2.0 * 2 * D * D, [&] { return mk_gemv(temb.f(), 1, D, norm_out.w, norm_out.bias, 2 * D, omod.f(), 1, stream); }));
+        // text in: RMSNorm(w) -> Linear; image in: Linear
+        for (uint32_t b = 0; b < nb; ++b)
+            MK_TRY(timed("norm", 0, [&] {
+                return mk_rms_norm(slots[slot_of[b]].prompt.f(), S, E, txt_norm, 0.0f, eps,
+                                   tn.h() + size_t(b) * S * E, stream);
+            }));
+        MK_TRY(gemm(txt_in, tn.p, E, 0, nb * S, 1, x_txt.p, D, 0, MK_EPI_STORE, MK_F32));
+        MK_TRY(timed("convert", 0, [&] { return mk_f32_to_bf16(lat_dev, size_t(nb) * N * L, lat_bf.p, stream); }));
+        MK_TRY(gemm(img_in, lat_bf.p, L, 0, nb * N, 1, x_img.p, D, 0, MK_EPI_STORE, MK_F32));
+        if (probe)
+            for (uint32_t b = 0; b < nb; ++b) {
+                MK_TRY(probe_f32("txt_in", int(b), x_txt.f() + size_t(b) * S * D, size_t(S) * D));
+                MK_TRY(probe_f32("img_in", int(b), x_img.f() + size_t(b) * N * D, size_t(N) * D));
+            }
+        const double attn_flops = 4.0 * double(T) * T * 128 * H * nb;
+        for (uint32_t i = 0; i < cfg.blocks; ++i) {
+            const Block& B = blocks[i];
+            const float* mi = mod.f() + size_t(i) * 12 * D; // image: shift1, scale1, gate1, shift2, scale2, gate2
+            const float* mt = mi + 6 * D;                    // text
+            struct St {
+                Buf *x, *xn;
+                uint32_t rows, row0, which;
+                const float* m;
+            } st[2] = {{&x_img, &xn_img, N, S, 0, mi}, {&x_txt, &xn_txt, S, 0, 1, mt}};
+            for (const St& s : st) {
+                MK_TRY(timed("ln_modulate", 0, [&] {
+                    return mk_ln_modulate(s.x->f(), nb * s.rows, D, s.m + D, s.m, 0, 0, 1, eps, s.xn->p, stream);
+                }));
+                mk_heads_args ha{};
+                ha.q = q.p;
+                ha.k = k.p;
+                ha.vt = vt.p;
+                ha.heads = H;
+                ha.head_dim = 128;
+                ha.q_pad = q_pad;
+                ha.k_pad = k_pad;
+                ha.row0 = s.row0;
+                ha.q_row0 = s.row0;
+                ha.norm_q = B.nq[s.which];
+                ha.norm_k = B.nk[s.which];
+                ha.rope = rope.f();
+                ha.rope_mode = 2;
+                ha.eps = eps;
+                MK_TRY(gemm(B.qkv[s.which], s.xn->p, D, int64_t(s.rows) * D, s.rows, nb, nullptr, 0, 0, MK_EPI_HEADS,
+                            MK_BF16, nullptr, 0, 0, 0, &ha));
+            }
+            MK_TRY(timed("attention", attn_flops, [&] {
+                return mk_attention(q.p, k.p, vt.p, att.p, nb, H, 128, T, q_pad, T, k_pad, D, int64_t(T) * D, 0, 0,
+                                    1.0f / std::sqrt(128.0f), stream);
+            }));
+            for (const St& s : st) {
+                const uint16_t* a = att.h() + size_t(s.row0) * D; // image rows after the text's
+                MK_TRY(gemm(B.o[s.which], a, D, int64_t(T) * D, s.rows, nb, s.x->p, D, int64_t(s.rows) * D,
+                            MK_EPI_GATE_ADD, MK_F32, s.m + 2 * D));
+                MK_TRY(timed("ln_modulate", 0, [&] {
+                    return mk_ln_modulate(s.x->f(), nb * s.rows, D, s.m + 4 * D, s.m + 3 * D, 0, 0, 1, eps, s.xn->p,
+                                          stream);
+                }));
+                MK_TRY(gemm(B.ff1[s.which], s.xn->p, D, 0, nb * s.rows, 1, hid.p, F, 0, MK_EPI_GELU_TANH, MK_BF16));
+                MK_TRY(gemm(B.ff2[s.which], hid.p, F, 0, nb * s.rows, 1, s.x->p, D, 0, MK_EPI_GATE_ADD, MK_F32,
+                            s.m + 5 * D));
+            }
+            if (probe)
+                for (uint32_t b = 0; b < nb; ++b)
+                    MK_TRY(probe_f32("block", int(i * nb + b), x_img.f() + size_t(b) * N * D, size_t(N) * D));
+        }
+        // output norm (scale first, then shift: AdaLayerNormContinuous) -> proj_out on the image rows
+        MK_TRY(timed("ln_modulate", 0, [&] {
+            return mk_ln_modulate(x_img.f(), nb * N, D, omod.f(), omod.f() + D, 0, 0, 1, eps, xn_img.p, stream);
+        }));
+        if (probe)
+            for (uint32_t b = 0; b < nb; ++b)
+                MK_TRY(probe_bf16("norm_out", int(b), xn_img.h() + size_t(b) * N * D, size_t(N) * D));
+        MK_TRY(gemm(proj_out, xn_img.p, D, 0, nb * N, 1, out.p, L, 0, MK_EPI_STORE, MK_F32));
+        return MK_OK;
+    }
+    uint32_t k_pad_last = 0;
+
+    // ---------------------------------------------------------------------------------------------------------
+    // Qwen-Image 2.1 step for one slot (qwen_image.cpp:144-293): the first step runs [text; image] and keeps the
+    // text's K / V per block; later steps run the image rows against them.
+    mk_status q21_step(const float* lat_dev, float sigma, uint32_t slot)
+    {
+        Slot& g = slots[slot];
+        const uint32_t D = cfg.dim, H = cfg.heads, F = cfg.ffn, E = cfg.text_dim, L = cfg.latent;
+        const uint32_t N = gh * gw, S = g.S;
+        const bool first = g.steps++ == 0;
+        const uint32_t T = first ? S + N : N, row0 = first ? 0 : S, n_k = S + N;
+        const uint32_t q_pad = uint32_t(round_up(T, 256)), k_pad = uint32_t(round_up(n_k, 64)),
+                       split = first ? S : 0;
+        const float eps = 1e-6f;
+        MK_TRY(make_rope(S));
+        MK_TRY(x_img.ensure(size_t(T) * D * 4));
+        MK_TRY(xn_img.ensure(size_t(T) * D * 2));
+        MK_TRY(q.ensure(size_t(H) * q_pad * 128 * 2));
+        MK_TRY(k.ensure(size_t(H) * k_pad * 128 * 2));
+        MK_TRY(vt.ensure(size_t(H) * 128 * k_pad * 2));
+        MK_TRY(att.ensure(size_t(T) * D * 2));
+        MK_TRY(gu.ensure(size_t(T) * 2 * F * 2));
+        MK_TRY(hid.ensure(size_t(T) * F * 2));
+        MK_TRY(out.ensure(size_t(T) * L * 4));
+        MK_TRY(lat_bf.ensure(size_t(N) * L * 2));
+        MK_TRY(tn.ensure(size_t(S) * E * 2));
+        MK_TRY(tproj.ensure(2 * 256 * 4));
+        MK_TRY(temb_h.ensure(size_t(2) * D * 4));
+        MK_TRY(temb.ensure(size_t(2) * D * 4));
+        MK_TRY(mod.ensure(size_t(2) * 4 * D * 4));
+        MK_TRY(omod.ensure(size_t(2) * D * 4));
+        if (k_pad_last != k_pad) {
+            MK_HIP(hipMemsetAsync(k.p, 0, k.bytes, stream));
+            MK_HIP(hipMemsetAsync(vt.p, 0, vt.bytes, stream));
+            k_pad_last = k_pad;
+        }
+        if (first) {
+            MK_TRY(g.kcache.ensure(size_t(cfg.blocks) * H * S * 128 * 2));
+            MK_TRY(g.vcache.ensure(size_t(cfg.blocks) * H * 128 * S * 2));
+        }
+        // rows [sigma, t = 0]: t_lin1 -> silu -> t_lin2 -> (probe) -> silu -> modulation / out_lin
+        float tp[512];
+        sinusoid(1000.0f * sigma, tp);
+        sinusoid(0.0f, tp + 256);
+        MK_HIP(hipMemcpyAsync(tproj.p, tp, sizeof(tp), hipMemcpyHostToDevice, stream));
+        MK_TRY(timed("gemv", 0, [&] { return mk_gemv(tproj.f(), 2, 256, t_lin1.w, nullptr, D, temb_h.f(), 0, stream); }));
+        MK_TRY(timed("gemv", 0, [&] { return mk_gemv(temb_h.f(), 2, D, t_lin2.w, nullptr, D, temb.f(), 1, stream); }));
+        MK_TRY(probe_f32("temb", -1, temb.f(), 2 * D));
+        MK_TRY(timed("gemv", 0, [&] { return mk_gemv(temb.f(), 2, D, mods.w, nullptr, 4 * D, mod.f(), 1, stream); }));
+        MK_TRY(probe_f32("modulation", -1, mod.f(), 8 * D));
+        MK_TRY(timed("gemv", 0, [&] { return mk_gemv(temb.f(), 2, D, norm_out.w, nullptr, D, omod.f(), 1, stream); }));
+        if (first) {
+            MK_TRY(timed("norm", 0, [&] { return mk_rms_norm(g.prompt.f(), S, E, txt_norm, 1.0f, eps, tn.p, stream); }));
+            MK_TRY(gemm(txt_in1, tn.p, E, 0, S, 1, hid.p, D, 0, MK_EPI_GELU_TANH, MK_BF16));
+            MK_TRY(gemm(txt_in2, hid.p, D, 0, S, 1, x_img.p, D, 0, MK_EPI_STORE, MK_F32));
+            MK_TRY(probe_f32("txt_in", -1, x_img.f(), size_t(S) * D));
+        }
+        MK_TRY(timed("convert", 0, [&] { return mk_f32_to_bf16(lat_dev, size_t(N) * L, lat_bf.p, stream); }));
+        float* ximg = x_img.f() + size_t(T - N) * D;
+        MK_TRY(gemm(img_in, lat_bf.p, L, 0, N, 1, ximg, D, 0, MK_EPI_STORE, MK_F32));
+        MK_TRY(probe_f32("img_in", -1, ximg, size_t(N) * D));
+        // attention flops: image rows see all keys; text rows (first step) see their causal prefix
+        const double pairs = double(N) * n_k + (first ? double(S) * (S + 1) / 2 : 0.0);
+        for (uint32_t i = 0; i < cfg.blocks; ++i) {
+            const Block& B = blocks[i];
+            MK_TRY(timed("ln_modulate", 0, [&] {
+                return mk_ln_modulate(x_img.f(), T, D, mod.f(), nullptr, 4 * D, split, T, eps, xn_img.p, stream);
+            }));
+            mk_heads_args ha{};
+            ha.q = q.p;
+            ha.k = k.p;
+            ha.vt = vt.p;
+            ha.heads = H;
+            ha.head_dim = 128;
+            ha.q_pad = q_pad;
+            ha.k_pad = k_pad;
+            ha.row0 = row0;
+            ha.q_row0 = 0;
+            ha.norm_q = B.nq[0];
+            ha.norm_k = B.nk[0];
+            ha.rope = rope.f();
+            ha.rope_mode = 2;
+            ha.eps = eps;
+            MK_TRY(gemm(B.qkv[0], xn_img.p, D, 0, T, 1, nullptr, 0, 0, MK_EPI_HEADS, MK_BF16, nullptr, 0, 0, 0, &ha));
+            // the text's keys and values: kept after the first step, restored after (heads_rows)
+            uint16_t* kc = g.kcache.h() + size_t(i) * H * S * 128;
+            uint16_t* vc = g.vcache.h() + size_t(i) * H * 128 * S;
+            if (first) {
+                MK_HIP(hipMemcpy2DAsync(kc, size_t(S) * 256, k.p, size_t(k_pad) * 256, size_t(S) * 256, H,
+                                        hipMemcpyDeviceToDevice, stream));
+                MK_HIP(hipMemcpy2DAsync(vc, size_t(S) * 2, vt.p, size_t(k_pad) * 2, size_t(S) * 2, size_t(H) * 128,
+                                        hipMemcpyDeviceToDevice, stream));
+            } else {
+                MK_HIP(hipMemcpy2DAsync(k.p, size_t(k_pad) * 256, kc, size_t(S) * 256, size_t(S) * 256, H,
+                                        hipMemcpyDeviceToDevice, stream));
+                MK_HIP(hipMemcpy2DAsync(vt.p, size_t(k_pad) * 2, vc, size_t(S) * 2, size_t(S) * 2, size_t(H) * 128,
+                                        hipMemcpyDeviceToDevice, stream));
+            }
+            MK_TRY(timed("attention", 4.0 * pairs * 128 * H, [&] {
+                return mk_attention(q.p, k.p, vt.p, att.p, 1, H, 128, T, q_pad, n_k, k_pad, D, 0, row0, S,
+                                    1.0f / std::sqrt(128.0f), stream);
+            }));
+            MK_TRY(gemm(B.o[0], att.p, D, 0, T, 1, x_img.p, D, 0, MK_EPI_GATE_TANH, MK_F32, mod.f() + D, 4 * D, split,
+                        T));
+            MK_TRY(timed("ln_modulate", 0, [&] {
+                return mk_ln_modulate(x_img.f(), T, D, mod.f() + 2 * D, nullptr, 4 * D, split, T, eps, xn_img.p,
+                                      stream);
+            }));
+            MK_TRY(gemm(B.ff1[0], xn_img.p, D, 0, T, 1, gu.p, 2 * F, 0, MK_EPI_STORE, MK_BF16));
+            MK_TRY(timed("swiglu", 0, [&] { return mk_swiglu(gu.p, MK_BF16, T, F, hid.p, stream); }));
+            MK_TRY(gemm(B.ff2[0], hid.p, F, 0, T, 1, x_img.p, D, 0, MK_EPI_GATE_TANH, MK_F32, mod.f() + 3 * D, 4 * D,
+                        split, T));
+            MK_TRY(probe_f32("block", int(i), x_img.f(), size_t(T) * D));
+        }
+        MK_TRY(timed("ln_modulate", 0, [&] {
+            return mk_ln_modulate(x_img.f(), T, D, omod.f(), nullptr, D, split, T, eps, xn_img.p, stream);
+        }));
+        MK_TRY(probe_bf16("norm_out", -1, xn_img.h(), size_t(T) * D));
+        MK_TRY(gemm(proj_out, xn_img.h() + size_t(T - N) * D, D, 0, N, 1, out.p, L, 0, MK_EPI_STORE, MK_F32));
+        return MK_OK;
+    }
+
+    // ---------------------------------------------------------------------------------------------------------
+    // SDXL: the context's keys / values per block for a slot (sdxl.cpp:693-719).
+    mk_status sdxl_begin(uint32_t slot)
+    {
+        Slot& g = slots[slot];
+        const uint32_t c = cfg.dim, H = c / 64, E = cfg.text_dim, S = g.S, s_pad = uint32_t(round_up(S, 64));
+        MK_TRY(tn.ensure(size_t(S) * E * 2));
+        MK_TRY(qkv.ensure(size_t(S) * 2 * c * 2));
+        // layout [blocks][slot][H][s_pad][64] (K) and [blocks][slot][H][64][s_pad] (V^T): both slots of a block
+        // form a batch of 2 for the cross attention.
+        MK_TRY(slots[0].ck.ensure(size_t(cfg.blocks) * 2 * H * s_pad * 64 * 2));
+        MK_TRY(slots[0].cvt.ensure(size_t(cfg.blocks) * 2 * H * 64 * s_pad * 2));
+        sdxl_spad = s_pad;
+        MK_TRY(timed("convert", 0, [&] { return mk_f32_to_bf16(g.prompt.f(), size_t(S) * E, tn.p, stream); }));
+        for (uint32_t i = 0; i < cfg.blocks; ++i) {
+            MK_TRY(gemm(blocks[i].kv2, tn.p, E, 0, S, 1, qkv.p, 2 * c, 0, MK_EPI_STORE, MK_BF16));
+            uint16_t* kd = slots[0].ck.h() + (size_t(i) * 2 + slot) * H * s_pad * 64;
+            uint16_t* vd = slots[0].cvt.h() + (size_t(i) * 2 + slot) * H * 64 * s_pad;
+            MK_TRY(mk_heads(qkv.p, 1, S, 2 * c, 0, 0, H, 64, nullptr, 0, nullptr, 0, kd, s_pad, 0, 0, stream));
+            MK_TRY(mk_heads(qkv.p, 1, S, 2 * c, 0, c, H, 64, nullptr, 0, nullptr, 0, vd, s_pad, 0, 1, stream));
+        }
+        return MK_OK;
+    }
+    uint32_t sdxl_spad = 0;
+
+    // trans_fwd (sdxl.cpp:742-796) for nb samples: x [nb][n][c] fp32 -> y [nb][n][c] fp32.
+    mk_status sdxl_forward(const float* x, uint32_t nb, uint32_t n, float* y)
+    {
+        const uint32_t c = cfg.dim, H = c / 64, F = cfg.ffn, S = slots[0].S;
+        const uint32_t q_pad = uint32_t(round_up(n, 256)), k_pad = uint32_t(round_up(n, 64)), s_pad = sdxl_spad;
+        MK_TRY(xn_img.ensure(size_t(nb) * n * c * 2));
+        MK_TRY(x_img.ensure(size_t(nb) * n * c * 4));
+        MK_TRY(qkv.ensure(size_t(nb) * n * 3 * c * 2));
+        MK_TRY(q.ensure(size_t(nb) * H * q_pad * 64 * 2));
+        MK_TRY(k.ensure(size_t(nb) * H * k_pad * 64 * 2));
+        MK_TRY(vt.ensure(size_t(nb) * H * 64 * k_pad * 2));
+        MK_TRY(att.ensure(size_t(nb) * n * c * 2));
+        MK_TRY(gu.ensure(size_t(nb) * n * 2 * F * 2));
+        MK_TRY(hid.ensure(size_t(nb) * n * F * 2));
+        if (k_pad_last != k_pad) {
+            MK_HIP(hipMemsetAsync(k.p, 0, k.bytes, stream));
+            MK_HIP(hipMemsetAsync(vt.p, 0, vt.bytes, stream));
+            k_pad_last = k_pad;
+        }
+        float* hs = x_img.f();
+        const int64_t nc = int64_t(n) * c;
+        MK_TRY(timed("norm", 0, [&] { return mk_group_norm(x, nb, n, c, 32, gn_g, gn_b, 1e-6f, xn_img.p, stream); }));
+        MK_TRY(gemm(proj_in, xn_img.p, c, 0, nb * n, 1, hs, c, 0, MK_EPI_STORE, MK_F32));
+        const float scale = 0.125f;
+        for (uint32_t i = 0; i < cfg.blocks; ++i) {
+            const Block& B = blocks[i];
+            MK_TRY(timed("norm", 0, [&] { return mk_layer_norm(hs, nb * n, c, B.n1g, B.n1b, 1e-5f, xn_img.p, stream); }));
+            MK_TRY(gemm(B.qkv[0], xn_img.p, c, 0, nb * n, 1, qkv.p, 3 * c, 0, MK_EPI_STORE, MK_BF16));
+            MK_TRY(timed("heads", 0, [&] {
+                mk_status s = mk_heads(qkv.p, nb, n, 3 * c, int64_t(n) * 3 * c, 0, H, 64, nullptr, 0, nullptr, 0, q.p,
+                                       q_pad, 0, 0, stream);
+                if (s == MK_OK)
+                    s = mk_heads(qkv.p, nb, n, 3 * c, int64_t(n) * 3 * c, c, H, 64, nullptr, 0, nullptr, 0, k.p, k_pad,
+                                 0, 0, stream);
+                if (s == MK_OK)
+                    s = mk_heads(qkv.p, nb, n, 3 * c, int64_t(n) * 3 * c, 2 * c, H, 64, nullptr, 0, nullptr, 0, vt.p,
+                                 k_pad, 0, 1, stream);
+                return s;
+            }));
+            MK_TRY(timed("attention", 4.0 * double(n) * n * 64 * H * nb, [&] {
+                return mk_attention(q.p, k.p, vt.p, att.p, nb, H, 64, n, q_pad, n, k_pad, c, nc, 0, 0, scale, stream);
+            }));
+            MK_TRY(gemm(B.o[0], att.p, c, 0, nb * n, 1, hs, c, 0, MK_EPI_ADD, MK_F32));
+            MK_TRY(timed("norm", 0, [&] { return mk_layer_norm(hs, nb * n, c, B.n2g, B.n2b, 1e-5f, xn_img.p, stream); }));
+            MK_TRY(gemm(B.q2, xn_img.p, c, 0, nb * n, 1, qkv.p, c, 0, MK_EPI_STORE, MK_BF16));
+            MK_TRY(timed("heads", 0, [&] {
+                return mk_heads(qkv.p, nb, n, c, int64_t(n) * c, 0, H, 64, nullptr, 0, nullptr, 0, q.p, q_pad, 0, 0,
+                                stream);
+            }));
+            // cross attention: batch b reads slot b's context keys (consecutive in the cache)
+            const uint16_t* kc = slots[0].ck.h() + size_t(i) * 2 * H * s_pad * 64;
+            const uint16_t* vc = slots[0].cvt.h() + size_t(i) * 2 * H * 64 * s_pad;
+            MK_TRY(timed("attention", 4.0 * double(n) * S * 64 * H * nb, [&] {
+                return mk_attention(q.p, kc, vc, att.p, nb, H, 64, n, q_pad, S, s_pad, c, nc, 0, 0, scale, stream);
+            }));
+            MK_TRY(gemm(B.o[1], att.p, c, 0, nb * n, 1, hs, c, 0, MK_EPI_ADD, MK_F32));
+            MK_TRY(timed("norm", 0, [&] { return mk_layer_norm(hs, nb * n, c, B.n3g, B.n3b, 1e-5f, xn_img.p, stream); }));
+            MK_TRY(gemm(B.ff1[0], xn_img.p, c, 0, nb * n, 1, gu.p, 2 * F, 0, MK_EPI_STORE, MK_BF16));
+            MK_TRY(timed("geglu", 0, [&] { return mk_geglu(gu.p, MK_BF16, nb * n, F, hid.p, stream); }));
+            MK_TRY(gemm(B.ff2[0], hid.p, F, 0, nb * n, 1, hs, c, 0, MK_EPI_ADD, MK_F32));
+        }
+        // proj_out + bias + the transformer's input
+        MK_HIP(hipMemcpyAsync(y, x, size_t(nb) * nc * 4, hipMemcpyDeviceToDevice, stream));
+        MK_TRY(timed("convert", 0, [&] { return mk_f32_to_bf16(hs, size_t(nb) * nc, xn_img.p, stream); }));
+        MK_TRY(gemm(proj_out, xn_img.p, c, 0, nb * n, 1, y, c, 0, MK_EPI_ADD, MK_F32));
+        return MK_OK;
+    }
+};
+
+// =====================================================================================================================
+// C ABI: engine
+// =====================================================================================================================
+
+namespace {
+
+bool fill_dest(mk_engine* e, const std::string& name, const Dest& d, uint64_t seed, mk_status& st)
+{
+    const uint64_t key = tensor_key(seed, name.c_str());
+    const uint64_t n = d.rows * d.cols;
+    if (d.dtype == MK_FP8_E4M3) {
+        // bf16 N(0, 0.02), then per-row fp8 quantisation (the CPU reference's rule)
+        void* tmp = nullptr;
+        if (hipMalloc(&tmp, n * 2) != hipSuccess) {
+            st = fail(MK_ERR_NOMEM, "init_random: temporary");
+            return false;
+        }
+        st = mk_fill_normal(tmp, n, MK_BF16, key, d.mean, d.std, e->stream);
+        if (st == MK_OK)
+            st = mk_quantize_fp8_rows(tmp, d.rows, d.cols, d.p, d.scale, e->stream);
+        (void)hipStreamSynchronize(e->stream);
+        (void)hipFree(tmp);
+        return st == MK_OK;
+    }
+    st = mk_fill_normal(d.p, n, d.dtype, key, d.mean, d.std, e->stream);
+    return st == MK_OK;
+}
+
+} // namespace
+
+extern "C" {
+
+mk_status mk_engine_create(const mk_config* cfg, mk_engine** out)
+{
+    if (!cfg || !out)
+        return fail(MK_ERR_ARG, "engine_create: null");
+    *out = nullptr;
+    const mk_config& c = *cfg;
+    if (c.family > MK_FAMILY_SDXL || !c.blocks || !c.dim || !c.heads || !c.ffn || !c.text_dim)
+        return fail(MK_ERR_ARG, "engine_create: bad family or zero size");
+    if (c.family != MK_FAMILY_SDXL && (c.head_dim != 128 || c.heads * 128 != c.dim || c.latent != 64))
+        return fail(MK_ERR_ARG, "engine_create: MMDiT families need heads x 128 = dim and 64 latent channels");
+    if (c.family == MK_FAMILY_SDXL && (c.head_dim != 64 || c.dim % 64))
+        return fail(MK_ERR_ARG, "engine_create: SDXL needs heads of 64");
+    if ((c.family == MK_FAMILY_SDXL ? c.dim % 64 : c.dim % 256) || c.ffn % 64 || c.text_dim % 64 || c.dim > 4096 ||
+        c.text_dim > 4096)
+        return fail(MK_ERR_ARG, "engine_create: dim a multiple of 256 (SDXL: 64) up to 4096, ffn and text_dim "
+                                "multiples of 64");
+    if (c.weight_dtype != MK_BF16 && c.weight_dtype != MK_FP8_E4M3)
+        return fail(MK_ERR_ARG, "engine_create: weights bf16 or fp8-e4m3");
+    auto e = std::make_unique<mk_engine>();
+    e->cfg = c;
+    if (!e->cfg.max_batch)
+        e->cfg.max_batch = 2;
+    MK_HIP(hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking));
+    mk_status s = e->build();
+    if (s != MK_OK)
+        return s;
+    *out = e.release();
+    return MK_OK;
+}
+
+mk_status mk_engine_destroy(mk_engine* e)
+{
+    if (!e)
+        return MK_OK;
+    (void)hipStreamSynchronize(e->stream);
+    for (void* p : e->allocs)
+        (void)hipFree(p);
+    (void)hipStreamDestroy(e->stream);
+    delete e;
+    return MK_OK;
+}
+
+mk_status mk_engine_load(mk_engine* e, const char* name, const void* data, uint32_t dtype, uint64_t rows,
+                         uint64_t cols)
+{
+    if (!e || !name || !data)
+        return fail(MK_ERR_ARG, "engine_load: null");
+    std::string n(name);
+    bool is_scale = false;
+    if (n.size() > 6 && n.compare(n.size() - 6, 6, ".scale") == 0) {
+        n = n.substr(0, n.size() - 6);
+        is_scale = true;
+    }
+    auto it = e->dests.find(n);
+    if (it == e->dests.end())
+        return fail(MK_ERR_ARG, "engine_load: no tensor named " + std::string(name));
+    const Dest& d = it->second;
+    if (is_scale) {
+        if (d.dtype != MK_FP8_E4M3 || dtype != MK_F32 || rows * cols != d.rows)
+            return fail(MK_ERR_ARG, "engine_load: " + std::string(name) + ": a scale is fp32 per row of an fp8 matrix");
+        MK_HIP(hipMemcpy(d.scale, data, d.rows * 4, hipMemcpyHostToDevice));
+        return MK_OK;
+    }
+    if (dtype != d.dtype || rows * cols != d.rows * d.cols)
+        return fail(MK_ERR_ARG, "engine_load: " + std::string(name) + ": expected " + std::to_string(d.rows) + " x " +
+                                    std::to_string(d.cols) + " of dtype " + std::to_string(d.dtype));
+    MK_HIP(hipMemcpy(d.p, data, d.rows * d.cols * mk_engine::esize(d.dtype), hipMemcpyHostToDevice));
+    return MK_OK;
+}
+
+mk_status mk_engine_init_random(mk_engine* e, uint64_t seed)
+{
+    if (!e)
+        return fail(MK_ERR_ARG, "engine_init_random: null");
+    for (const auto& [name, d] : e->dests) {
+        mk_status st;
+        if (!fill_dest(e, name, d, seed, st))
+            return st;
+    }
+    MK_HIP(hipStreamSynchronize(e->stream));
+    return MK_OK;
+}
+
+mk_status mk_engine_weight_bytes(const mk_engine* e, uint64_t* bytes)
+{
+    if (!e || !bytes)
+        return fail(MK_ERR_ARG, "engine_weight_bytes: null");
+    *bytes = e->weight_bytes;
+    return MK_OK;
+}
+
+mk_status mk_begin(mk_engine* e, const float* prompt, size_t rows, uint32_t h, uint32_t w, uint32_t slot)
+{
+    if (!e || !prompt)
+        return fail(MK_ERR_ARG, "begin: null");
+    if (slot > 1)
+        return fail(MK_ERR_ARG, "slot must be 0 or 1");
+    if (!rows)
+        return fail(MK_ERR_ARG, "prompt embeddings must be rows of " + std::to_string(e->cfg.text_dim));
+    if (!h || !w)
+        return fail(MK_ERR_ARG, "begin: empty latent grid");
+    auto& g = e->slots[slot];
+    if (e->gh != h || e->gw != w)
+        e->rope_S = 0xffffffffu;
+    e->gh = h;
+    e->gw = w;
+    g.S = uint32_t(rows);
+    g.steps = 0;
+    MK_TRY(g.prompt.ensure(rows * e->cfg.text_dim * 4));
+    MK_HIP(hipMemcpy(g.prompt.p, prompt, rows * e->cfg.text_dim * 4, hipMemcpyHostToDevice));
+    g.begun = true;
+    if (e->cfg.family == MK_FAMILY_SDXL)
+        MK_TRY(e->sdxl_begin(slot));
+    return MK_OK;
+}
+
+mk_status mk_step(mk_engine* e, const float* latents, size_t n, float sigma, uint32_t slot, float* out)
+{
+    if (!e || !latents || !out)
+        return fail(MK_ERR_ARG, "step: null");
+    if (slot > 1)
+        return fail(MK_ERR_ARG, "slot must be 0 or 1");
+    if (e->cfg.family == MK_FAMILY_SDXL)
+        return fail(MK_ERR_UNSUPPORTED, "step: the SDXL family runs mk_sdxl_forward");
+    auto& g = e->slots[slot];
+    if (!g.begun)
+        return fail(MK_ERR_STATE, "step before begin");
+    const size_t N = size_t(e->gh) * e->gw, L = e->cfg.latent;
+    if (n != N * L)
+        return fail(MK_ERR_ARG, "latents must be [h * w][" + std::to_string(L) + "]");
+    MK_TRY(e->lat.ensure(N * L * 4));
+    MK_HIP(hipMemcpyAsync(e->lat.p, latents, N * L * 4, hipMemcpyHostToDevice, e->stream));
+    if (e->cfg.family == MK_FAMILY_DUAL) {
+        const uint32_t so[1] = {slot};
+        MK_TRY(e->dual_step(e->lat.f(), sigma, so, 1));
+    } else {
+        MK_TRY(e->q21_step(e->lat.f(), sigma, slot));
+    }
+    MK_HIP(hipMemcpyAsync(out, e->out.p, N * L * 4, hipMemcpyDeviceToHost, e->stream));
+    MK_HIP(hipStreamSynchronize(e->stream));
+    MK_TRY(e->finish_timing());
+    return MK_OK;
+}
+
+mk_status mk_step_cfg_device(mk_engine* e, const float* lat, float sigma, float sigma_next, float guidance,
+                             float* lat_out, void* stream)
+{
+    if (!e || !lat || !lat_out)
+        return fail(MK_ERR_ARG, "step_cfg: null");
+    if (e->cfg.family != MK_FAMILY_DUAL && e->cfg.family != MK_FAMILY_Q21)
+        return fail(MK_ERR_UNSUPPORTED, "step_cfg: MMDiT families only");
+    if (!e->slots[0].begun || !e->slots[1].begun)
+        return fail(MK_ERR_STATE, "step_cfg: begin both slots first");
+    const size_t N = size_t(e->gh) * e->gw, L = e->cfg.latent;
+    if (stream && stream != e->stream) {
+        // order after the caller's stream
+        hipEvent_t ev;
+        MK_HIP(hipEventCreate(&ev));
+        MK_HIP(hipEventRecord(ev, static_cast<hipStream_t>(stream)));
+        MK_HIP(hipStreamWaitEvent(e->stream, ev, 0));
+        MK_HIP(hipEventDestroy(ev));
+    }
+    const float dt = sigma_next - sigma;
+    if (e->cfg.family == MK_FAMILY_DUAL && e->slots[0].S == e->slots[1].S) {
+        // both guidance passes as one batch of 2
+        MK_TRY(e->lat.ensure(2 * N * L * 4));
+        MK_HIP(hipMemcpyAsync(e->lat.p, lat, N * L * 4, hipMemcpyDeviceToDevice, e->stream));
+        MK_HIP(hipMemcpyAsync(e->lat.f() + N * L, lat, N * L * 4, hipMemcpyDeviceToDevice, e->stream));
+        const uint32_t so[2] = {0, 1};
+        MK_TRY(e->dual_step(e->lat.f(), sigma, so, 2));
+        MK_TRY(e->timed("cfg_euler", 0, [&] {
+            return mk_cfg_euler(lat, e->out.f(), e->out.f() + N * L, N * L, guidance, dt, lat_out, e->stream);
+        }));
+    } else {
+        // two passes (different text lengths, or the 2.1 graph whose slots keep their own K / V)
+        Buf pos;
+        MK_TRY(pos.ensure(N * L * 4));
+        MK_TRY(e->lat.ensure(N * L * 4));
+        MK_HIP(hipMemcpyAsync(e->lat.p, lat, N * L * 4, hipMemcpyDeviceToDevice, e->stream));
+        for (uint32_t s = 0; s < 2; ++s) {
+            if (e->cfg.family == MK_FAMILY_DUAL) {
+                const uint32_t so[1] = {s};
+                MK_TRY(e->dual_step(e->lat.f(), sigma, so, 1));
+            } else {
+                MK_TRY(e->q21_step(e->lat.f(), sigma, s));
+            }
+            if (s == 0)
+                MK_HIP(hipMemcpyAsync(pos.p, e->out.p, N * L * 4, hipMemcpyDeviceToDevice, e->stream));
+        }
+        MK_TRY(e->timed("cfg_euler", 0, [&] {
+            return mk_cfg_euler(lat, pos.f(), e->out.f(), N * L, guidance, dt, lat_out, e->stream);
+        }));
+        MK_HIP(hipStreamSynchronize(e->stream)); // `pos` is freed on return
+    }
+    if (stream && stream != e->stream) {
+        hipEvent_t ev;
+        MK_HIP(hipEventCreate(&ev));
+        MK_HIP(hipEventRecord(ev, e->stream));
+        MK_HIP(hipStreamWaitEvent(static_cast<hipStream_t>(stream), ev, 0));
+        MK_HIP(hipEventDestroy(ev));
+    }
+    if (e->timing.on)
+        MK_TRY(e->finish_timing());
+    return MK_OK;
+}
+
+mk_status mk_step_cfg(mk_engine* e, const float* latents, size_t n, float sigma, float sigma_next, float guidance,
+                      float* latents_out)
+{
+    if (!e || !latents || !latents_out)
+        return fail(MK_ERR_ARG, "step_cfg: null");
+    const size_t N = size_t(e->gh) * e->gw, L = e->cfg.latent;
+    if (n != N * L)
+        return fail(MK_ERR_ARG, "latents must be [h * w][" + std::to_string(L) + "]");
+    Buf in, out;
+    MK_TRY(in.ensure(n * 4));
+    MK_TRY(out.ensure(n * 4));
+    MK_HIP(hipMemcpy(in.p, latents, n * 4, hipMemcpyHostToDevice));
+    MK_TRY(mk_step_cfg_device(e, in.f(), sigma, sigma_next, guidance, out.f(), nullptr));
+    MK_HIP(hipStreamSynchronize(e->stream));
+    MK_HIP(hipMemcpy(latents_out, out.p, n * 4, hipMemcpyDeviceToHost));
+    return MK_OK;
+}
+
+mk_status mk_engine_stream(mk_engine* e, void** stream)
+{
+    if (!e || !stream)
+        return fail(MK_ERR_ARG, "engine_stream: null");
+    *stream = e->stream;
+    return MK_OK;
+}
+
+mk_status mk_engine_set_probe(mk_engine* e, mk_probe_fn fn, void* user)
+{
+    if (!e)
+        return fail(MK_ERR_ARG, "set_probe: null");
+    e->probe = fn;
+    e->probe_user = user;
+    return MK_OK;
+}
+
+mk_status mk_engine_set_timing(mk_engine* e, int on)
+{
+    if (!e)
+        return fail(MK_ERR_ARG, "set_timing: null");
+    e->timing.on = on != 0;
+    return MK_OK;
+}
+
+mk_status mk_engine_timing(mk_engine* e, uint32_t i, const char** name, float* ms, uint32_t* launches, double* flops)
+{
+    if (!e || !name || !ms || !launches || !flops)
+        return fail(MK_ERR_ARG, "engine_timing: null");
+    if (i >= e->timing.names.size())
+        return fail(MK_ERR_ARG, "engine_timing: no such class");
+    *name = e->timing.names[i].c_str();
+    *ms = e->timing.ms[i];
+    *launches = e->timing.launches[i];
+    *flops = e->timing.flops[i];
+    return MK_OK;
+}
+
+mk_status mk_sdxl_forward(mk_engine* e, const float* x, uint32_t batch, uint32_t n, float* y, void* stream)
+{
+    if (!e || !x || !y)
+        return fail(MK_ERR_ARG, "sdxl_forward: null");
+    if (e->cfg.family != MK_FAMILY_SDXL)
+        return fail(MK_ERR_UNSUPPORTED, "sdxl_forward: not an SDXL engine");
+    if (batch == 0 || batch > 2 || !n)
+        return fail(MK_ERR_ARG, "sdxl_forward: batch 1 or 2, n > 0");
+    for (uint32_t b = 0; b < batch; ++b)
+        if (!e->slots[b].begun)
+            return fail(MK_ERR_STATE, "sdxl_forward: begin slot " + std::to_string(b) + " first");
+    if (batch == 2 && e->slots[0].S != e->slots[1].S)
+        return fail(MK_ERR_ARG, "sdxl_forward: both slots' contexts must have the same length");
+    (void)stream;
+    MK_TRY(e->sdxl_forward(x, batch, n, y));
+    MK_HIP(hipStreamSynchronize(e->stream));
+    MK_TRY(e->finish_timing());
+    return MK_OK;
+}
+
+} // extern "C"

@@ -1,0 +1,680 @@
+// Bandwidth-bound kernels of the step: modulated layer norm, gated residual, heads pack with per-head RMSNorm and
+// RoPE, the V^T transpose, GEMV for the time / modulation projections, activations, norms, guidance + Euler,
+// patchify, and the counter-RNG fill. Each is a wave64 kernel with 16-byte coalesced accesses where the row allows.
+#include "common.hpp"
+
+#include <cmath>
+
+namespace mk {
+
+namespace {
+
+constexpr int kMaxVec = 16; // float4s per lane a row-resident norm keeps in registers (rows up to 4096 floats)
+
+// ------------------------------------------------------------------------------------------------------------
+// ln_modulate (image.metal:32-53): one wave per row, the row held in registers; two-pass mean / variance in fp32.
+// y = (x - mean) rsqrt(var + eps) (1 + scale) + shift, bf16 out.
+// ------------------------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void ln_modulate_kernel(const float* __restrict__ x, uint32_t rows, uint32_t n,
+                                                          const float* __restrict__ scale,
+                                                          const float* __restrict__ shift, int64_t alt, uint32_t split,
+                                                          uint32_t seg_rows, float eps, uint16_t* __restrict__ y)
+{
+    const uint32_t lane = threadIdx.x & 63, row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows)
+        return;
+    const f32x4* xr = reinterpret_cast<const f32x4*>(x + uint64_t(row) * n);
+    const uint32_t nv = n / 4;
+    f32x4 v[kMaxVec];
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kMaxVec; ++i) {
+        const uint32_t c = lane + 64u * i;
+        v[i] = c < nv ? xr[c] : f32x4{0, 0, 0, 0};
+        s += v[i][0] + v[i][1] + v[i][2] + v[i][3];
+    }
+    const float mean = wave_sum(s) / float(n);
+    float q = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kMaxVec; ++i) {
+        const uint32_t c = lane + 64u * i;
+        if (c < nv)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float d = v[i][j] - mean;
+                q += d * d;
+            }
+    }
+    const float inv = rsqrtf(wave_sum(q) / float(n) + eps);
+    const int64_t off = (row % seg_rows) < split ? alt : 0;
+    const f32x4* sc = reinterpret_cast<const f32x4*>(scale + off);
+    const f32x4* sh = shift ? reinterpret_cast<const f32x4*>(shift + off) : nullptr;
+    u32x2* yr = reinterpret_cast<u32x2*>(y + uint64_t(row) * n);
+#pragma unroll
+    for (int i = 0; i < kMaxVec; ++i) {
+        const uint32_t c = lane + 64u * i;
+        if (c < nv) {
+            const f32x4 a = sc[c];
+            const f32x4 b = sh ? sh[c] : f32x4{0, 0, 0, 0};
+            float o[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                o[j] = (v[i][j] - mean) * inv * (1.0f + a[j]) + b[j];
+            yr[c] = u32x2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+        }
+    }
+}
+
+// Layer norm with gamma / beta (sdxl.cpp:425-437), or RMSNorm * (w + w_offset) (rms = 1): bf16 out.
+template <bool kRms>
+__global__ __launch_bounds__(256) void norm_kernel(const float* __restrict__ x, uint32_t rows, uint32_t n,
+                                                   const float* __restrict__ g, const float* __restrict__ b,
+                                                   float w_offset, float eps, uint16_t* __restrict__ y)
+{
+    const uint32_t lane = threadIdx.x & 63, row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows)
+        return;
+    const f32x4* xr = reinterpret_cast<const f32x4*>(x + uint64_t(row) * n);
+    const uint32_t nv = n / 4;
+    f32x4 v[kMaxVec];
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kMaxVec; ++i) {
+        const uint32_t c = lane + 64u * i;
+        v[i] = c < nv ? xr[c] : f32x4{0, 0, 0, 0};
+        s += kRms ? v[i][0] * v[i][0] + v[i][1] * v[i][1] + v[i][2] * v[i][2] + v[i][3] * v[i][3]
+                  : v[i][0] + v[i][1] + v[i][2] + v[i][3];
+    }
+    float mean = 0.0f, inv;
+    if (kRms) {
+        inv = rsqrtf(wave_sum(s) / float(n) + eps);
+    } else {
+        mean = wave_sum(s) / float(n);
+        float q = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kMaxVec; ++i)
+            if (lane + 64u * i < nv)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    q += (v[i][j] - mean) * (v[i][j] - mean);
+        inv = rsqrtf(wave_sum(q) / float(n) + eps);
+    }
+    u32x2* yr = reinterpret_cast<u32x2*>(y + uint64_t(row) * n);
+#pragma unroll
+    for (int i = 0; i < kMaxVec; ++i) {
+        const uint32_t c = lane + 64u * i;
+        if (c < nv) {
+            const f32x4 gg = reinterpret_cast<const f32x4*>(g)[c];
+            const f32x4 bb = kRms ? f32x4{0, 0, 0, 0} : reinterpret_cast<const f32x4*>(b)[c];
+            float o[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                o[j] = kRms ? v[i][j] * inv * (gg[j] + w_offset) : (v[i][j] - mean) * inv * gg[j] + bb[j];
+            yr[c] = u32x2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+        }
+    }
+}
+
+// Group norm statistics: one block per (batch, group) over rows x (c / groups) channels, then the apply kernel.
+__global__ __launch_bounds__(256) void group_stats_kernel(const float* __restrict__ x, uint32_t rows, uint32_t c,
+                                                          uint32_t groups, float eps, float2* __restrict__ stats)
+{
+    __shared__ float red[8];
+    const uint32_t g = blockIdx.x, bi = blockIdx.y, cg = c / groups;
+    const float* xb = x + uint64_t(bi) * rows * c + uint64_t(g) * cg;
+    const uint64_t cnt = uint64_t(rows) * cg;
+    double s = 0.0;
+    for (uint64_t i = threadIdx.x; i < cnt; i += 256)
+        s += xb[(i / cg) * c + i % cg];
+    float sf = wave_sum(float(s));
+    if ((threadIdx.x & 63) == 0)
+        red[threadIdx.x >> 6] = sf;
+    __syncthreads();
+    const float mean = (red[0] + red[1] + red[2] + red[3]) / float(cnt);
+    __syncthreads();
+    float q = 0.0f;
+    for (uint64_t i = threadIdx.x; i < cnt; i += 256) {
+        const float d = xb[(i / cg) * c + i % cg] - mean;
+        q += d * d;
+    }
+    q = wave_sum(q);
+    if ((threadIdx.x & 63) == 0)
+        red[4 + (threadIdx.x >> 6)] = q;
+    __syncthreads();
+    if (threadIdx.x == 0)
+        stats[bi * groups + g] = float2{mean, rsqrtf((red[4] + red[5] + red[6] + red[7]) / float(cnt) + eps)};
+}
+
+__global__ __launch_bounds__(256) void group_apply_kernel(const float* __restrict__ x, uint32_t rows, uint32_t c,
+                                                          uint32_t groups, const float2* __restrict__ stats,
+                                                          const float* __restrict__ g, const float* __restrict__ b,
+                                                          uint16_t* __restrict__ y)
+{
+    const uint64_t n = uint64_t(rows) * c;
+    const uint32_t bi = blockIdx.y;
+    for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < n; i += uint64_t(gridDim.x) * 256) {
+        const uint32_t ch = uint32_t(i % c);
+        const float2 st = stats[bi * groups + ch / (c / groups)];
+        y[uint64_t(bi) * n + i] = f2bf_bits((x[uint64_t(bi) * n + i] - st.x) * st.y * g[ch] + b[ch]);
+    }
+}
+
+// gate_add (image.metal:55-65) with an identity or tanh gate; y fp32 or bf16.
+template <typename Y, bool kTanh>
+__global__ __launch_bounds__(256) void gate_add_kernel(float* __restrict__ x, const Y* __restrict__ y, uint32_t rows,
+                                                       uint32_t n, const float* __restrict__ gate, int64_t alt,
+                                                       uint32_t split, uint32_t seg_rows)
+{
+    const uint64_t total = uint64_t(rows) * n;
+    for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < total; i += uint64_t(gridDim.x) * 256) {
+        const uint32_t row = uint32_t(i / n), c = uint32_t(i % n);
+        float g = gate[((row % seg_rows) < split ? alt : 0) + c];
+        if (kTanh)
+            g = tanhf(g);
+        float v;
+        if constexpr (sizeof(Y) == 2)
+            v = bf2f_bits(y[i]);
+        else
+            v = y[i];
+        x[i] += g * v;
+    }
+}
+
+// heads_norm_half / heads_half (qwen_image.cpp:226-250): one wave per (row, head); lane l holds the pair it rotates:
+// (2l, 2l+1) in mode 2 (interleaved, also used with no rope), (l, l + d/2) in mode 1.
+__global__ __launch_bounds__(256) void heads_kernel(const uint16_t* __restrict__ x, uint32_t rows, int64_t ld,
+                                                    int64_t stride_x, uint32_t col0, uint32_t heads, uint32_t d,
+                                                    const float* __restrict__ w, float eps,
+                                                    const float* __restrict__ rope, uint32_t mode,
+                                                    uint16_t* __restrict__ out, uint32_t n_pad, uint32_t row0)
+{
+    const uint32_t lane = threadIdx.x & 63, bi = blockIdx.y;
+    const uint64_t idx = uint64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (idx >= uint64_t(rows) * heads)
+        return;
+    const uint32_t r = uint32_t(idx / heads), h = uint32_t(idx % heads);
+    const uint16_t* xr = x + uint64_t(bi) * stride_x + uint64_t(r) * ld + col0 + uint64_t(h) * d;
+    const bool act = lane < d / 2;
+    const uint32_t i0 = mode == 1 ? lane : 2 * lane, i1 = mode == 1 ? lane + d / 2 : 2 * lane + 1;
+    float a = act ? bf2f_bits(xr[i0]) : 0.0f, b = act ? bf2f_bits(xr[i1]) : 0.0f;
+    if (w) {
+        const float inv = rsqrtf(wave_sum(a * a + b * b) / float(d) + eps);
+        if (act) {
+            a = a * inv * w[i0];
+            b = b * inv * w[i1];
+        }
+    }
+    if (rope && mode && act) {
+        const float* cs = rope + (uint64_t(row0) + r) * d + 2 * lane; // pair `lane` of the row's d/2 (cos, sin)
+        const float co = cs[0], si = cs[1];
+        const float na = a * co - b * si, nb = a * si + b * co;
+        a = na;
+        b = nb;
+    }
+    if (act) {
+        uint16_t* o = out + ((uint64_t(bi) * heads + h) * n_pad + row0 + r) * d;
+        o[i0] = f2bf_bits(a);
+        o[i1] = f2bf_bits(b);
+    }
+}
+
+// V^T pack: x bf16 [batch][rows][ld] columns col0 + h*d .. -> out [batch][heads][d][n_pad] at column row0 + r.
+// One block per (64 rows, head, batch), transposed through LDS so both sides are coalesced.
+template <int kD>
+__global__ __launch_bounds__(256) void heads_t_kernel(const uint16_t* __restrict__ x, uint32_t rows, int64_t ld,
+                                                      int64_t stride_x, uint32_t col0, uint32_t heads,
+                                                      uint16_t* __restrict__ out, uint32_t n_pad, uint32_t row0)
+{
+    __shared__ uint16_t t[64][kD + 2];
+    const uint32_t r0 = blockIdx.x * 64, h = blockIdx.y, bi = blockIdx.z, tid = threadIdx.x;
+    // load: 64 rows x kD values, 2 per thread-step (u32)
+    for (uint32_t i = tid; i < 64 * kD / 2; i += 256) {
+        const uint32_t r = i / (kD / 2), c = (i % (kD / 2)) * 2;
+        uint32_t v = 0;
+        if (r0 + r < rows)
+            v = *reinterpret_cast<const uint32_t*>(x + uint64_t(bi) * stride_x + uint64_t(r0 + r) * ld + col0 +
+                                                   uint64_t(h) * kD + c);
+        t[r][c] = uint16_t(v);
+        t[r][c + 1] = uint16_t(v >> 16);
+    }
+    __syncthreads();
+    // store: kD rows of 64 columns, 2 per thread-step
+    for (uint32_t i = tid; i < kD * 32; i += 256) {
+        const uint32_t dd = i / 32, c = (i % 32) * 2;
+        if (r0 + c >= rows)
+            continue;
+        uint16_t* o = out + ((uint64_t(bi) * heads + h) * kD + dd) * n_pad + row0 + r0 + c;
+        if (r0 + c + 1 < rows)
+            *reinterpret_cast<uint32_t*>(o) = uint32_t(t[c][dd]) | (uint32_t(t[c + 1][dd]) << 16);
+        else
+            o[0] = t[c][dd];
+    }
+}
+
+// GEMV for rows <= 4: y[r][n] = sum_k W[n][k] x'[r][k] + b[n], x' = silu(x) if asked; x' staged in LDS.
+// Each wave computes 4 outputs at a time, 16-byte weight loads.
+__global__ __launch_bounds__(256) void gemv_kernel(const float* __restrict__ x, uint32_t rows, uint32_t K,
+                                                   const uint16_t* __restrict__ w, const float* __restrict__ bias,
+                                                   uint32_t N, float* __restrict__ y, int silu_x)
+{
+    extern __shared__ float xs[];
+    for (uint32_t i = threadIdx.x; i < rows * K; i += 256) {
+        const float v = x[i];
+        xs[i] = silu_x ? v / (1.0f + __expf(-v)) : v;
+    }
+    __syncthreads();
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t n0 = (blockIdx.x * 4 + wave) * 4;
+    if (n0 >= N)
+        return;
+    float acc[4][4] = {};
+    for (uint32_t k = lane * 8; k < K; k += 512) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const u32x4 wv = *reinterpret_cast<const u32x4*>(w + uint64_t(min(n0 + j, N - 1)) * K + k);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float w0 = bf2f_bits(uint16_t(wv[e])), w1 = bf2f_bits(uint16_t(wv[e] >> 16));
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (uint32_t(r) < rows)
+                        acc[j][r] += w0 * xs[r * K + k + 2 * e] + w1 * xs[r * K + k + 2 * e + 1];
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            acc[j][r] = wave_sum(acc[j][r]);
+    if (lane < 16) {
+        const uint32_t j = lane / 4, r = lane % 4;
+        float v = 0.0f;
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj)
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr)
+                if (uint32_t(jj) == j && uint32_t(rr) == r)
+                    v = acc[jj][rr];
+        if (n0 + j < N && r < rows)
+            y[uint64_t(r) * N + n0 + j] = v + (bias ? bias[n0 + j] : 0.0f);
+    }
+}
+
+template <int kOp>
+__global__ __launch_bounds__(256) void unary_kernel(float* __restrict__ x, uint64_t n)
+{
+    for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < n; i += uint64_t(gridDim.x) * 256)
+        x[i] = kOp == 0 ? silu_f(x[i]) : gelu_tanh_f(x[i]);
+}
+
+// swiglu_rows (gate rows first) and geglu_rows (h first, then g): m bf16 [rows][F].
+template <typename In, bool kGeglu>
+__global__ __launch_bounds__(256) void glu_kernel(const In* __restrict__ in, uint32_t rows, uint32_t F,
+                                                  uint16_t* __restrict__ m)
+{
+    const uint64_t n = uint64_t(rows) * F;
+    for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < n; i += uint64_t(gridDim.x) * 256) {
+        const uint64_t r = i / F, c = i % F;
+        float a, b;
+        if constexpr (sizeof(In) == 2) {
+            a = bf2f_bits(in[r * 2 * F + c]);
+            b = bf2f_bits(in[r * 2 * F + F + c]);
+        } else {
+            a = in[r * 2 * F + c];
+            b = in[r * 2 * F + F + c];
+        }
+        m[i] = f2bf_bits(kGeglu ? a * 0.5f * b * (1.0f + erf_fit(b * 0.70710678f)) : silu_f(a) * b);
+    }
+}
+
+__global__ __launch_bounds__(256) void cfg_euler_kernel(const float* __restrict__ x, const float* __restrict__ pos,
+                                                        const float* __restrict__ neg, uint64_t n, float guidance,
+                                                        float dt, float* __restrict__ out)
+{
+    for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < n; i += uint64_t(gridDim.x) * 256) {
+        const float v = neg ? neg[i] + guidance * (pos[i] - neg[i]) : pos[i];
+        out[i] = x[i] + dt * v;
+    }
+}
+
+template <bool kPack>
+__global__ __launch_bounds__(256) void patch_kernel(const float* __restrict__ src, uint32_t C, uint32_t h, uint32_t w,
+                                                    float* __restrict__ dst)
+{
+    const uint64_t n = uint64_t(C) * 4 * h * w, bi = blockIdx.y;
+    for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < n; i += uint64_t(gridDim.x) * 256) {
+        // i indexes the latent [C][2h][2w]
+        const uint32_t xx = uint32_t(i % (2 * w)), yy = uint32_t((i / (2 * w)) % (2 * h)), c = uint32_t(i / (4ull * h * w));
+        const uint64_t t = (uint64_t(yy / 2) * w + xx / 2) * C * 4 + c * 4 + (yy % 2) * 2 + xx % 2;
+        if (kPack)
+            dst[bi * n + t] = src[bi * n + i];
+        else
+            dst[bi * n + i] = src[bi * n + t];
+    }
+}
+
+__global__ __launch_bounds__(256) void fill_normal_kernel(void* __restrict__ p, uint64_t n, uint32_t dtype,
+                                                          uint64_t key, double mean, double std)
+{
+    for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < n; i += uint64_t(gridDim.x) * 256) {
+        const uint64_t a = splitmix64(key + 2 * i), b = splitmix64(key + 2 * i + 1);
+        const double u1 = double((a >> 11) + 1) * 0x1.0p-53, u2 = double(b >> 11) * 0x1.0p-53;
+        const double z = sqrt(-2.0 * log(u1)) * cos(6.283185307179586 * u2);
+        const float v = float(mean + std * z);
+        if (dtype == MK_F32)
+            static_cast<float*>(p)[i] = v;
+        else
+            static_cast<uint16_t*>(p)[i] = f2bf_bits(v);
+    }
+}
+
+__global__ __launch_bounds__(256) void f2bf_kernel(const float* __restrict__ x, uint64_t n, uint16_t* __restrict__ y)
+{
+    for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < n; i += uint64_t(gridDim.x) * 256)
+        y[i] = f2bf_bits(x[i]);
+}
+__global__ __launch_bounds__(256) void bf2f_kernel(const uint16_t* __restrict__ x, uint64_t n, float* __restrict__ y)
+{
+    for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < n; i += uint64_t(gridDim.x) * 256)
+        y[i] = bf2f_bits(x[i]);
+}
+
+
+// e4m3 encode of a finite float, nearest with ties to the even code, saturating at 448 (the CPU reference's rule).
+__device__ inline uint8_t e4m3_encode(float x)
+{
+    const uint8_t sign = __builtin_bit_cast(uint32_t, x) >> 31 ? 0x80 : 0;
+    const float a = fabsf(x);
+    if (!(a < 448.0f))
+        return sign | 0x7e;
+    int e;
+    frexpf(a, &e); // a = f * 2^e, f in [0.5, 1): binade 2^(e-1)
+    int b = max(e - 1, -6); // subnormals share the step of binade -6
+    const float step = ldexpf(1.0f, b - 3);
+    const float q = rintf(a / step); // exact scaling by a power of two, then round half to even
+    int code;
+    if (b == -6 && q < 8.0f)
+        code = int(q); // subnormal (or zero)
+    else {
+        int m = int(q);
+        if (m == 16) {
+            m = 8;
+            ++b;
+        }
+        code = ((b + 7) << 3) | (m - 8);
+    }
+    return sign | uint8_t(min(code, 0x7e));
+}
+
+// One block per row: the row's max |w| -> scale = max / 448 (1 for a zero row), then the e4m3 codes.
+__global__ __launch_bounds__(256) void quant_fp8_kernel(const uint16_t* __restrict__ src, uint64_t cols,
+                                                        uint8_t* __restrict__ dst, float* __restrict__ scale)
+{
+    __shared__ float red[4];
+    const uint64_t r = blockIdx.x;
+    const uint16_t* s = src + r * cols;
+    float mx = 0.0f;
+    for (uint64_t c = threadIdx.x; c < cols; c += 256)
+        mx = fmaxf(mx, fabsf(bf2f_bits(s[c])));
+    mx = wave_max(mx);
+    if ((threadIdx.x & 63) == 0)
+        red[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const float sc = mx > 0.0f ? mx / 448.0f : 1.0f;
+    if (threadIdx.x == 0)
+        scale[r] = sc;
+    for (uint64_t c = threadIdx.x; c < cols; c += 256)
+        dst[r * cols + c] = e4m3_encode(bf2f_bits(s[c]) / sc);
+}
+
+inline uint32_t grid_for(uint64_t n)
+{
+    const uint64_t b = (n + 255) / 256;
+    return uint32_t(b < 65536 ? (b ? b : 1) : 65536);
+}
+inline hipStream_t S(void* s) { return static_cast<hipStream_t>(s); }
+
+} // namespace
+} // namespace mk
+
+using namespace mk;
+
+extern "C" {
+
+mk_status mk_ln_modulate(const float* x, uint32_t rows, uint32_t n, const float* scale, const float* shift,
+                         int64_t alt, uint32_t split, uint32_t seg_rows, float eps, void* y, void* stream)
+{
+    if (!x || !scale || !y || n % 4 || n > 4u * 64 * kMaxVec || !seg_rows)
+        return fail(MK_ERR_ARG, "ln_modulate: null pointer, or n not a multiple of 4 up to 4096, or seg_rows 0");
+    if (!rows)
+        return MK_OK;
+    ln_modulate_kernel<<<cdiv(rows, 4), 256, 0, S(stream)>>>(x, rows, n, scale, shift, alt, split, seg_rows, eps,
+                                                              static_cast<uint16_t*>(y));
+    MK_LAUNCH_CHECK("ln_modulate");
+    return MK_OK;
+}
+
+mk_status mk_rms_norm(const float* x, uint32_t rows, uint32_t n, const float* w, float w_offset, float eps, void* y,
+                      void* stream)
+{
+    if (!x || !w || !y || n % 4 || n > 4u * 64 * kMaxVec)
+        return fail(MK_ERR_ARG, "rms_norm: null pointer, or n not a multiple of 4 up to 4096");
+    if (!rows)
+        return MK_OK;
+    norm_kernel<true><<<cdiv(rows, 4), 256, 0, S(stream)>>>(x, rows, n, w, nullptr, w_offset, eps,
+                                                             static_cast<uint16_t*>(y));
+    MK_LAUNCH_CHECK("rms_norm");
+    return MK_OK;
+}
+
+mk_status mk_layer_norm(const float* x, uint32_t rows, uint32_t n, const float* g, const float* b, float eps, void* y,
+                        void* stream)
+{
+    if (!x || !g || !b || !y || n % 4 || n > 4u * 64 * kMaxVec)
+        return fail(MK_ERR_ARG, "layer_norm: null pointer, or n not a multiple of 4 up to 4096");
+    if (!rows)
+        return MK_OK;
+    norm_kernel<false><<<cdiv(rows, 4), 256, 0, S(stream)>>>(x, rows, n, g, b, 0.0f, eps, static_cast<uint16_t*>(y));
+    MK_LAUNCH_CHECK("layer_norm");
+    return MK_OK;
+}
+
+mk_status mk_group_norm(const float* x, uint32_t batch, uint32_t rows, uint32_t c, uint32_t groups, const float* g,
+                        const float* b, float eps, void* y, void* stream)
+{
+    if (!x || !g || !b || !y || !groups || c % groups || !batch)
+        return fail(MK_ERR_ARG, "group_norm: null pointer or channels not a multiple of groups");
+    float2* stats = nullptr;
+    MK_HIP(hipMallocAsync(reinterpret_cast<void**>(&stats), sizeof(float2) * batch * groups, S(stream)));
+    group_stats_kernel<<<dim3(groups, batch), 256, 0, S(stream)>>>(x, rows, c, groups, eps, stats);
+    group_apply_kernel<<<dim3(std::min<uint32_t>(cdiv(uint64_t(rows) * c, 256), 4096), batch), 256, 0, S(stream)>>>(
+        x, rows, c, groups, stats, g, b, static_cast<uint16_t*>(y));
+    MK_LAUNCH_CHECK("group_norm");
+    MK_HIP(hipFreeAsync(stats, S(stream)));
+    return MK_OK;
+}
+
+mk_status mk_gate_add(float* x, const void* y, uint32_t y_dtype, uint32_t rows, uint32_t n, const float* gate,
+                      int64_t alt, uint32_t split, uint32_t seg_rows, int tanh_gate, void* stream)
+{
+    if (!x || !y || !gate || !seg_rows || (y_dtype != MK_F32 && y_dtype != MK_BF16))
+        return fail(MK_ERR_ARG, "gate_add: null pointer, seg_rows 0 or bad y dtype");
+    const uint32_t g = grid_for(uint64_t(rows) * n);
+    if (y_dtype == MK_F32) {
+        if (tanh_gate)
+            gate_add_kernel<float, true><<<g, 256, 0, S(stream)>>>(x, static_cast<const float*>(y), rows, n, gate, alt,
+                                                                  split, seg_rows);
+        else
+            gate_add_kernel<float, false><<<g, 256, 0, S(stream)>>>(x, static_cast<const float*>(y), rows, n, gate,
+                                                                   alt, split, seg_rows);
+    } else {
+        if (tanh_gate)
+            gate_add_kernel<uint16_t, true><<<g, 256, 0, S(stream)>>>(x, static_cast<const uint16_t*>(y), rows, n,
+                                                                     gate, alt, split, seg_rows);
+        else
+            gate_add_kernel<uint16_t, false><<<g, 256, 0, S(stream)>>>(x, static_cast<const uint16_t*>(y), rows, n,
+                                                                      gate, alt, split, seg_rows);
+    }
+    MK_LAUNCH_CHECK("gate_add");
+    return MK_OK;
+}
+
+mk_status mk_heads(const void* x, uint32_t batch, uint32_t rows, int64_t ld, int64_t stride_x, uint32_t col0,
+                   uint32_t heads, uint32_t d, const float* w, float eps, const float* rope, uint32_t rope_mode,
+                   void* out, uint32_t n_pad, uint32_t row0, int transpose, void* stream)
+{
+    if (!x || !out || !batch || (d != 64 && d != 128) || rope_mode > 2 || (rope_mode && !rope) ||
+        uint64_t(row0) + rows > n_pad)
+        return fail(MK_ERR_ARG, "heads: null pointer, d not 64 / 128, bad rope mode, or rows past n_pad");
+    if (!rows)
+        return MK_OK;
+    if (transpose) {
+        if (w || rope_mode)
+            return fail(MK_ERR_UNSUPPORTED, "heads: the transposed (V) layout takes no norm or rope");
+        const dim3 grid(cdiv(rows, 64), heads, batch);
+        if (d == 128)
+            heads_t_kernel<128><<<grid, 256, 0, S(stream)>>>(static_cast<const uint16_t*>(x), rows, ld, stride_x, col0,
+                                                             heads, static_cast<uint16_t*>(out), n_pad, row0);
+        else
+            heads_t_kernel<64><<<grid, 256, 0, S(stream)>>>(static_cast<const uint16_t*>(x), rows, ld, stride_x, col0,
+                                                            heads, static_cast<uint16_t*>(out), n_pad, row0);
+    } else {
+        heads_kernel<<<dim3(cdiv(uint64_t(rows) * heads, 4), batch), 256, 0, S(stream)>>>(
+            static_cast<const uint16_t*>(x), rows, ld, stride_x, col0, heads, d, w, eps, rope, rope_mode,
+            static_cast<uint16_t*>(out), n_pad, row0);
+    }
+    MK_LAUNCH_CHECK("heads");
+    return MK_OK;
+}
+
+mk_status mk_gemv(const float* x, uint32_t rows, uint32_t K, const void* w, const float* bias, uint32_t N, float* y,
+                  int silu_x, void* stream)
+{
+    if (!x || !w || !y || rows == 0 || rows > 4 || K % 8 || uint64_t(rows) * K * 4 > 64 * 1024)
+        return fail(MK_ERR_ARG, "gemv: null pointer, rows not 1..4, K not a multiple of 8 or rows*K over 16384");
+    gemv_kernel<<<cdiv(N, 16), 256, rows * K * 4, S(stream)>>>(x, rows, K, static_cast<const uint16_t*>(w), bias, N, y,
+                                                               silu_x);
+    MK_LAUNCH_CHECK("gemv");
+    return MK_OK;
+}
+
+mk_status mk_silu(float* x, size_t n, void* stream)
+{
+    if (!x)
+        return fail(MK_ERR_ARG, "silu: null pointer");
+    unary_kernel<0><<<grid_for(n), 256, 0, S(stream)>>>(x, n);
+    MK_LAUNCH_CHECK("silu");
+    return MK_OK;
+}
+
+mk_status mk_gelu_tanh(float* x, size_t n, void* stream)
+{
+    if (!x)
+        return fail(MK_ERR_ARG, "gelu_tanh: null pointer");
+    unary_kernel<1><<<grid_for(n), 256, 0, S(stream)>>>(x, n);
+    MK_LAUNCH_CHECK("gelu_tanh");
+    return MK_OK;
+}
+
+mk_status mk_swiglu(const void* gu, uint32_t gu_dtype, uint32_t rows, uint32_t F, void* m, void* stream)
+{
+    if (!gu || !m || (gu_dtype != MK_F32 && gu_dtype != MK_BF16))
+        return fail(MK_ERR_ARG, "swiglu: null pointer or bad dtype");
+    const uint32_t g = grid_for(uint64_t(rows) * F);
+    if (gu_dtype == MK_F32)
+        glu_kernel<float, false><<<g, 256, 0, S(stream)>>>(static_cast<const float*>(gu), rows, F,
+                                                           static_cast<uint16_t*>(m));
+    else
+        glu_kernel<uint16_t, false><<<g, 256, 0, S(stream)>>>(static_cast<const uint16_t*>(gu), rows, F,
+                                                              static_cast<uint16_t*>(m));
+    MK_LAUNCH_CHECK("swiglu");
+    return MK_OK;
+}
+
+mk_status mk_geglu(const void* hg, uint32_t hg_dtype, uint32_t rows, uint32_t F, void* m, void* stream)
+{
+    if (!hg || !m || (hg_dtype != MK_F32 && hg_dtype != MK_BF16))
+        return fail(MK_ERR_ARG, "geglu: null pointer or bad dtype");
+    const uint32_t g = grid_for(uint64_t(rows) * F);
+    if (hg_dtype == MK_F32)
+        glu_kernel<float, true><<<g, 256, 0, S(stream)>>>(static_cast<const float*>(hg), rows, F,
+                                                          static_cast<uint16_t*>(m));
+    else
+        glu_kernel<uint16_t, true><<<g, 256, 0, S(stream)>>>(static_cast<const uint16_t*>(hg), rows, F,
+                                                             static_cast<uint16_t*>(m));
+    MK_LAUNCH_CHECK("geglu");
+    return MK_OK;
+}
+
+mk_status mk_cfg_euler(const float* x, const float* pos, const float* neg, size_t n, float guidance, float dt,
+                       float* x_out, void* stream)
+{
+    if (!x || !pos || !x_out)
+        return fail(MK_ERR_ARG, "cfg_euler: null pointer");
+    cfg_euler_kernel<<<grid_for(n), 256, 0, S(stream)>>>(x, pos, neg, n, guidance, dt, x_out);
+    MK_LAUNCH_CHECK("cfg_euler");
+    return MK_OK;
+}
+
+mk_status mk_patchify(const float* lat, uint32_t batch, uint32_t C, uint32_t h, uint32_t w, float* tokens,
+                      void* stream)
+{
+    if (!lat || !tokens || !batch)
+        return fail(MK_ERR_ARG, "patchify: null pointer");
+    patch_kernel<true><<<dim3(grid_for(uint64_t(C) * 4 * h * w), batch), 256, 0, S(stream)>>>(lat, C, h, w, tokens);
+    MK_LAUNCH_CHECK("patchify");
+    return MK_OK;
+}
+
+mk_status mk_unpatchify(const float* tokens, uint32_t batch, uint32_t C, uint32_t h, uint32_t w, float* lat,
+                        void* stream)
+{
+    if (!lat || !tokens || !batch)
+        return fail(MK_ERR_ARG, "unpatchify: null pointer");
+    patch_kernel<false><<<dim3(grid_for(uint64_t(C) * 4 * h * w), batch), 256, 0, S(stream)>>>(tokens, C, h, w, lat);
+    MK_LAUNCH_CHECK("unpatchify");
+    return MK_OK;
+}
+
+mk_status mk_fill_normal(void* p, size_t n, uint32_t dtype, uint64_t key, double mean, double std, void* stream)
+{
+    if (!p || (dtype != MK_F32 && dtype != MK_BF16))
+        return fail(MK_ERR_ARG, "fill_normal: null pointer or dtype not f32 / bf16");
+    fill_normal_kernel<<<grid_for(n), 256, 0, S(stream)>>>(p, n, dtype, key, mean, std);
+    MK_LAUNCH_CHECK("fill_normal");
+    return MK_OK;
+}
+
+mk_status mk_quantize_fp8_rows(const void* src, uint64_t rows, uint64_t cols, void* dst, float* scale, void* stream)
+{
+    if (!src || !dst || !scale || rows > 0x7fffffffu)
+        return fail(MK_ERR_ARG, "quantize_fp8_rows: null pointer or too many rows");
+    if (!rows)
+        return MK_OK;
+    quant_fp8_kernel<<<uint32_t(rows), 256, 0, S(stream)>>>(static_cast<const uint16_t*>(src), cols,
+                                                            static_cast<uint8_t*>(dst), scale);
+    MK_LAUNCH_CHECK("quantize_fp8_rows");
+    return MK_OK;
+}
+
+mk_status mk_f32_to_bf16(const float* x, size_t n, void* y, void* stream)
+{
+    if (!x || !y)
+        return fail(MK_ERR_ARG, "f32_to_bf16: null pointer");
+    f2bf_kernel<<<grid_for(n), 256, 0, S(stream)>>>(x, n, static_cast<uint16_t*>(y));
+    MK_LAUNCH_CHECK("f32_to_bf16");
+    return MK_OK;
+}
+
+mk_status mk_bf16_to_f32(const void* x, size_t n, float* y, void* stream)
+{
+    if (!x || !y)
+        return fail(MK_ERR_ARG, "bf16_to_f32: null pointer");
+    bf2f_kernel<<<grid_for(n), 256, 0, S(stream)>>>(static_cast<const uint16_t*>(x), n, y);
+    MK_LAUNCH_CHECK("bf16_to_f32");
+    return MK_OK;
+}
+
+} // extern "C"

@@ -1,0 +1,353 @@
+"""ctypes binding of libmkimage.so, the C ABI of include/mkimage.h.
+
+Device memory, streams and events come from the library itself, so a process needs no other GPU runtime. The
+library must be built (`make -C mako-image_amd`); nothing here falls back to a CPU path.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import pathlib
+
+import numpy as np
+
+HERE = pathlib.Path(__file__).resolve().parent
+LIB_PATH = HERE / "libmkimage.so"
+
+F32, BF16, FP8 = 0, 1, 2
+EPI_STORE, EPI_GELU_TANH, EPI_GATE_ADD, EPI_GATE_TANH, EPI_SILU, EPI_ADD, EPI_HEADS = range(7)
+FAMILY_DUAL, FAMILY_Q21, FAMILY_SDXL = 0, 1, 2
+
+_vp, _sz, _u32, _u64, _i64, _f, _d, _i = (C.c_void_p, C.c_size_t, C.c_uint32, C.c_uint64, C.c_int64, C.c_float,
+                                          C.c_double, C.c_int)
+_fp = C.POINTER(C.c_float)
+
+
+class MkError(RuntimeError):
+    pass
+
+
+class HeadsArgs(C.Structure):
+    _fields_ = [("q", _vp), ("k", _vp), ("vt", _vp), ("heads", _u32), ("head_dim", _u32), ("q_pad", _u32),
+                ("k_pad", _u32), ("row0", _u32), ("q_row0", _u32), ("norm_q", _vp), ("norm_k", _vp), ("rope", _vp),
+                ("rope_mode", _u32), ("eps", _f)]
+
+
+class GemmArgs(C.Structure):
+    _fields_ = [("a", _vp), ("w", _vp), ("wscale", _vp), ("bias", _vp), ("c", _vp), ("gate", _vp),
+                ("gate_alt", _i64), ("split", _u32), ("seg_rows", _u32), ("M", _u32), ("N", _u32), ("K", _u32),
+                ("lda", _i64), ("ldc", _i64), ("stride_a", _i64), ("stride_c", _i64), ("batch", _u32),
+                ("w_dtype", _u32), ("c_dtype", _u32), ("epilogue", _u32), ("heads", C.POINTER(HeadsArgs))]
+
+
+class Config(C.Structure):
+    _fields_ = [(n, _u32) for n in ("family", "blocks", "dim", "heads", "head_dim", "ffn", "text_dim", "latent",
+                                     "weight_dtype", "max_batch")]
+
+
+PROBE = C.CFUNCTYPE(None, _vp, C.c_char_p, _i, _fp, _sz)
+
+_SIGS = {
+    "mk_last_error": (C.c_char_p, []),
+    "mk_version": (C.c_char_p, []),
+    "mk_device_count": (_i, [C.POINTER(_i)]),
+    "mk_set_device": (_i, [_i]),
+    "mk_device_info": (_i, [_i, C.c_char_p, _sz, C.POINTER(_i), C.POINTER(_i), C.c_char_p, _sz]),
+    "mk_malloc": (_i, [C.POINTER(_vp), _sz]),
+    "mk_free": (_i, [_vp]),
+    "mk_memcpy_h2d": (_i, [_vp, _vp, _sz]),
+    "mk_memcpy_d2h": (_i, [_vp, _vp, _sz]),
+    "mk_memset": (_i, [_vp, _i, _sz]),
+    "mk_synchronize": (_i, []),
+    "mk_stream_create": (_i, [C.POINTER(_vp)]),
+    "mk_stream_destroy": (_i, [_vp]),
+    "mk_stream_synchronize": (_i, [_vp]),
+    "mk_event_create": (_i, [C.POINTER(_vp)]),
+    "mk_event_destroy": (_i, [_vp]),
+    "mk_event_record": (_i, [_vp, _vp]),
+    "mk_event_elapsed_ms": (_i, [_vp, _vp, C.POINTER(_f)]),
+    "mk_gemm": (_i, [C.POINTER(GemmArgs), _vp]),
+    "mk_gemv": (_i, [_vp, _u32, _u32, _vp, _vp, _u32, _vp, _i, _vp]),
+    "mk_ln_modulate": (_i, [_vp, _u32, _u32, _vp, _vp, _i64, _u32, _u32, _f, _vp, _vp]),
+    "mk_gate_add": (_i, [_vp, _vp, _u32, _u32, _u32, _vp, _i64, _u32, _u32, _i, _vp]),
+    "mk_heads": (_i, [_vp, _u32, _u32, _i64, _i64, _u32, _u32, _u32, _vp, _f, _vp, _u32, _vp, _u32, _u32, _i, _vp]),
+    "mk_attention": (_i, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _i64, _i64, _u32, _u32, _f,
+                          _vp]),
+    "mk_silu": (_i, [_vp, _sz, _vp]),
+    "mk_gelu_tanh": (_i, [_vp, _sz, _vp]),
+    "mk_swiglu": (_i, [_vp, _u32, _u32, _u32, _vp, _vp]),
+    "mk_geglu": (_i, [_vp, _u32, _u32, _u32, _vp, _vp]),
+    "mk_rms_norm": (_i, [_vp, _u32, _u32, _vp, _f, _f, _vp, _vp]),
+    "mk_layer_norm": (_i, [_vp, _u32, _u32, _vp, _vp, _f, _vp, _vp]),
+    "mk_group_norm": (_i, [_vp, _u32, _u32, _u32, _u32, _vp, _vp, _f, _vp, _vp]),
+    "mk_cfg_euler": (_i, [_vp, _vp, _vp, _sz, _f, _f, _vp, _vp]),
+    "mk_patchify": (_i, [_vp, _u32, _u32, _u32, _u32, _vp, _vp]),
+    "mk_unpatchify": (_i, [_vp, _u32, _u32, _u32, _u32, _vp, _vp]),
+    "mk_fill_normal": (_i, [_vp, _sz, _u32, _u64, _d, _d, _vp]),
+    "mk_tensor_key": (_u64, [_u64, C.c_char_p]),
+    "mk_quantize_fp8_rows": (_i, [_vp, _u64, _u64, _vp, _vp, _vp]),
+    "mk_f32_to_bf16": (_i, [_vp, _sz, _vp, _vp]),
+    "mk_bf16_to_f32": (_i, [_vp, _sz, _vp, _vp]),
+    "mk_engine_create": (_i, [C.POINTER(Config), C.POINTER(_vp)]),
+    "mk_engine_destroy": (_i, [_vp]),
+    "mk_engine_load": (_i, [_vp, C.c_char_p, _vp, _u32, _u64, _u64]),
+    "mk_engine_init_random": (_i, [_vp, _u64]),
+    "mk_engine_weight_bytes": (_i, [_vp, C.POINTER(_u64)]),
+    "mk_begin": (_i, [_vp, _vp, _sz, _u32, _u32, _u32]),
+    "mk_step": (_i, [_vp, _vp, _sz, _f, _u32, _vp]),
+    "mk_step_cfg": (_i, [_vp, _vp, _sz, _f, _f, _f, _vp]),
+    "mk_step_cfg_device": (_i, [_vp, _vp, _f, _f, _f, _vp, _vp]),
+    "mk_engine_stream": (_i, [_vp, C.POINTER(_vp)]),
+    "mk_engine_set_probe": (_i, [_vp, PROBE, _vp]),
+    "mk_engine_set_timing": (_i, [_vp, _i]),
+    "mk_engine_timing": (_i, [_vp, _u32, C.POINTER(C.c_char_p), C.POINTER(_f), C.POINTER(_u32), C.POINTER(_d)]),
+    "mk_sdxl_forward": (_i, [_vp, _vp, _u32, _u32, _vp, _vp]),
+}
+
+EXPORTS = tuple(_SIGS)
+_lib = None
+
+
+def lib():
+    """The loaded library (raises if it is not built)."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise MkError(f"{LIB_PATH} is not built: run `make -C mako-image_amd` (or __graft_entry__.build())")
+        L = C.CDLL(str(LIB_PATH))
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(status, what=""):
+    if status != 0:
+        raise MkError(f"{what}: status {status}: {lib().mk_last_error().decode()}")
+
+
+def call(name, *args):
+    check(getattr(lib(), name)(*args), name)
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# device memory
+# ---------------------------------------------------------------------------------------------------------------
+
+_NP = {F32: np.float32, BF16: np.uint16, FP8: np.uint8}
+
+
+class Dev:
+    """A device allocation (zero-filled), freed with the object."""
+
+    def __init__(self, nbytes):
+        p = _vp()
+        call("mk_malloc", C.byref(p), max(int(nbytes), 16))
+        self.p = p.value
+        self.nbytes = int(nbytes)
+
+    @classmethod
+    def from_array(cls, a):
+        a = np.ascontiguousarray(a)
+        d = cls(a.nbytes)
+        call("mk_memcpy_h2d", d.p, a.ctypes.data, a.nbytes)
+        return d
+
+    def to_array(self, dtype, shape):
+        out = np.empty(shape, dtype=dtype)
+        assert out.nbytes <= self.nbytes
+        call("mk_memcpy_d2h", out.ctypes.data, self.p, out.nbytes)
+        return out
+
+    def write(self, a, offset=0):
+        a = np.ascontiguousarray(a)
+        assert offset + a.nbytes <= self.nbytes
+        call("mk_memcpy_h2d", self.p + offset, a.ctypes.data, a.nbytes)
+
+    def __del__(self):
+        if getattr(self, "p", None) and _lib is not None:
+            _lib.mk_free(self.p)
+            self.p = None
+
+    def __int__(self):
+        return self.p
+
+
+def sync():
+    call("mk_synchronize")
+
+
+def device_info(dev=0):
+    name = C.create_string_buffer(256)
+    arch = C.create_string_buffer(256)
+    cus, clk = _i(), _i()
+    call("mk_device_info", dev, name, 256, C.byref(cus), C.byref(clk), arch, 256)
+    return {"name": name.value.decode(), "arch": arch.value.decode(), "cus": cus.value, "clock_khz": clk.value}
+
+
+def device_count():
+    n = _i()
+    check(lib().mk_device_count(C.byref(n)), "mk_device_count")
+    return n.value
+
+
+class Event:
+    def __init__(self):
+        p = _vp()
+        call("mk_event_create", C.byref(p))
+        self.p = p.value
+
+    def record(self, stream=None):
+        call("mk_event_record", self.p, stream)
+
+    def elapsed_ms(self, end):
+        ms = _f()
+        call("mk_event_elapsed_ms", self.p, end.p, C.byref(ms))
+        return ms.value
+
+    def __del__(self):
+        if getattr(self, "p", None) and _lib is not None:
+            _lib.mk_event_destroy(self.p)
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# engine
+# ---------------------------------------------------------------------------------------------------------------
+
+def bf16_bits(a):
+    """float32 -> bf16 bit patterns, round to nearest even (the library's rule)."""
+    u = np.ascontiguousarray(a, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    r[nan] = ((u[nan] >> 16) | 0x40).astype(np.uint16)
+    return r
+
+
+def bf16_to_f32(b):
+    return (np.asarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+class Engine:
+    def __init__(self, family, blocks, dim, heads, head_dim, ffn, text_dim, latent=64, weight_dtype=BF16,
+                 max_batch=2):
+        self.cfg = Config(family, blocks, dim, heads, head_dim, ffn, text_dim, latent, weight_dtype, max_batch)
+        p = _vp()
+        call("mk_engine_create", C.byref(self.cfg), C.byref(p))
+        self.h = p.value
+        self._probe_cb = None
+
+    def close(self):
+        if getattr(self, "h", None) and _lib is not None:
+            _lib.mk_engine_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def load(self, name, array, dtype):
+        a = np.ascontiguousarray(array, dtype=_NP[dtype])
+        rows = a.shape[0] if a.ndim else 1
+        cols = a.size // max(rows, 1)
+        call("mk_engine_load", self.h, name.encode(), a.ctypes.data, dtype, rows, cols)
+
+    def init_random(self, seed):
+        call("mk_engine_init_random", self.h, seed)
+
+    def weight_bytes(self):
+        b = _u64()
+        call("mk_engine_weight_bytes", self.h, C.byref(b))
+        return b.value
+
+    def begin(self, prompt, h, w, slot=0):
+        prompt = np.ascontiguousarray(prompt, dtype=np.float32)
+        call("mk_begin", self.h, prompt.ctypes.data, prompt.shape[0], h, w, slot)
+
+    def step(self, latents, sigma, slot=0):
+        latents = np.ascontiguousarray(latents, dtype=np.float32)
+        out = np.empty_like(latents)
+        call("mk_step", self.h, latents.ctypes.data, latents.size, sigma, slot, out.ctypes.data)
+        return out
+
+    def step_cfg(self, latents, sigma, sigma_next, guidance):
+        latents = np.ascontiguousarray(latents, dtype=np.float32)
+        out = np.empty_like(latents)
+        call("mk_step_cfg", self.h, latents.ctypes.data, latents.size, sigma, sigma_next, guidance, out.ctypes.data)
+        return out
+
+    def step_cfg_device(self, lat, sigma, sigma_next, guidance, lat_out, stream=None):
+        call("mk_step_cfg_device", self.h, int(lat), sigma, sigma_next, guidance, int(lat_out), stream)
+
+    def stream(self):
+        s = _vp()
+        call("mk_engine_stream", self.h, C.byref(s))
+        return s.value
+
+    def set_probe(self, probes):
+        """Collect probes into the dict `probes` ((name, layer) -> array); None turns probing off."""
+        if probes is None:
+            self._probe_cb = None
+            call("mk_engine_set_probe", self.h, PROBE(), None)
+            return
+
+        def cb(_u, name, layer, data, n):
+            probes[(name.decode(), layer)] = np.ctypeslib.as_array(data, shape=(n,)).copy()
+
+        self._probe_cb = PROBE(cb)
+        call("mk_engine_set_probe", self.h, self._probe_cb, None)
+
+    def set_timing(self, on):
+        call("mk_engine_set_timing", self.h, int(on))
+
+    def timing(self):
+        out = {}
+        i = 0
+        while True:
+            name, ms, n, fl = C.c_char_p(), _f(), _u32(), _d()
+            if lib().mk_engine_timing(self.h, i, C.byref(name), C.byref(ms), C.byref(n), C.byref(fl)) != 0:
+                break
+            out[name.value.decode()] = {"ms": ms.value, "launches": n.value, "flops": fl.value}
+            i += 1
+        return out
+
+    def sdxl_forward(self, x_dev, batch, n, y_dev):
+        call("mk_sdxl_forward", self.h, int(x_dev), batch, n, int(y_dev), None)
+
+
+def upload_model(engine, tensors):
+    """Upload (name, float32 array, kind) triples (kind 0 vector, 1 bf16 matrix, 2 fp8 matrix whose values are exact
+    e4m3 and whose scale is the tensor name + '.scale')."""
+    table = None
+    for name, a, kind in tensors:
+        if kind == 0:
+            engine.load(name, a, F32)
+        elif kind == 1:
+            engine.load(name, bf16_bits(a), BF16)
+        else:
+            if table is None:
+                table = _e4m3_table()
+            engine.load(name, _e4m3_codes(a, table), FP8)
+
+
+def _e4m3_table():
+    t = np.zeros(256, dtype=np.float32)
+    for b in range(256):
+        s, e, m = b >> 7, (b >> 3) & 15, b & 7
+        if e == 15 and m == 7:
+            v = np.nan
+        elif e == 0:
+            v = m * 2.0 ** -9
+        else:
+            v = (1 + m / 8) * 2.0 ** (e - 7)
+        t[b] = -v if s else v
+    return t
+
+
+def _e4m3_codes(a, table):
+    a = np.asarray(a, dtype=np.float32)
+    mags = table[:127]
+    idx = np.clip(np.searchsorted(mags, np.abs(a)), 0, 126).astype(np.uint8)
+    codes = idx | np.where(np.signbit(a), 0x80, 0).astype(np.uint8)
+    if not np.array_equal(table[codes], a):
+        raise ValueError("fp8 weights are not exact e4m3 values")
+    return codes

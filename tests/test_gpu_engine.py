@@ -1,0 +1,177 @@
+"""Engine parity on the GPU: whole steps through the C ABI (mk_begin / mk_step / mk_step_cfg, mk_sdxl_forward)
+against the oracle's graphs on the same seeded weights and inputs.
+
+Tolerances (block and step outputs): cosine >= 0.9995 and max-rel = max|g - w| / max|w| <= 2e-2 with bf16 weights,
+<= 5e-2 with fp8 weights. The reference's own Diff (relative RMS error, lowest row cosine) is reported with them.
+"""
+import numpy as np
+import pytest
+
+import mkimage as M
+import mkref as R
+
+pytestmark = pytest.mark.gpu
+
+# The tiny MMDiT: 2 dual-stream blocks, hidden 512, 4 heads x 128, FFN 2048; 256 image tokens (a 16 x 16 grid of
+# 2x2-patched 16-channel latents), 64 text tokens of width 512; sigma 0.5, seed 0.
+TINY = dict(blocks=2, dim=512, heads=4, head_dim=128, ffn=2048, text_dim=512)
+H_, W_, S_ = 16, 16, 64
+
+
+def within(got, want, width, cos=0.9995, max_rel=2e-2):
+    d = R.diff(got, want, width)
+    assert d["cos"] >= cos and d["max_rel"] <= max_rel, d
+    return d
+
+
+def make_pair(family, fp8=False, seed=0, wstd=0.02, dims=TINY):
+    m = R.Model({M.FAMILY_DUAL: R.DUAL, M.FAMILY_Q21: R.Q21, M.FAMILY_SDXL: R.SDXL}[family], **dims, fp8=fp8,
+                seed=seed, wstd=wstd)
+    e = M.Engine(family, **dims, weight_dtype=M.FP8 if fp8 else M.BF16)
+    M.upload_model(e, m.tensors())
+    return m, e
+
+
+def inputs(seed=0, B=2, S=S_, h=H_, w=W_, E=512):
+    rng = np.random.default_rng(seed)
+    return (rng.standard_normal((B, S, E)).astype(np.float32),
+            rng.standard_normal((B, h * w, 64)).astype(np.float32))
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+def test_dual_step_matches_oracle(gpu, fp8):
+    m, e = make_pair(M.FAMILY_DUAL, fp8)
+    prompt, lat = inputs()
+    want_p = {}
+    want = m.dual_step(prompt[:1], lat[:1], H_, W_, 0.5, want_p)
+    e.begin(prompt[0], H_, W_, 0)
+    got_p = {}
+    e.set_probe(got_p)
+    got = e.step(lat[0], 0.5, 0)
+    tol = 5e-2 if fp8 else 2e-2
+    within(got, want[0], 64, max_rel=tol)
+    within(got_p[("temb", -1)], want_p[("temb", -1)], 512, cos=0.99999, max_rel=1e-3)
+    within(got_p[("modulation", -1)], want_p[("modulation", -1)], 512, cos=0.99999, max_rel=1e-3)
+    for i in range(TINY["blocks"]):
+        within(got_p[("block", i)], want_p[("block", i)], 512, max_rel=tol)
+
+
+def test_dual_cfg_batch_matches_two_oracle_passes(gpu):
+    m, e = make_pair(M.FAMILY_DUAL)
+    prompt, lat = inputs(1)
+    for s in (0, 1):
+        e.begin(prompt[s], H_, W_, s)
+    x = lat[0]
+    sig, sig_next, g = 0.75, 0.6, 4.0
+    got = e.step_cfg(x, sig, sig_next, g)
+    v = m.dual_step(prompt, np.stack([x, x]), H_, W_, sig)  # [pos, neg]
+    want = x + (sig_next - sig) * (v[1] + g * (v[0] - v[1]))
+    # compare the update (the latents themselves dominate the value)
+    within(got - x, want - x, 64)
+    # and the batch of 2 equals the single-sample steps it stands for
+    pos = e.step(x, sig, 0)
+    neg = e.step(x, sig, 1)
+    within(got - x, (sig_next - sig) * (neg + g * (pos - neg)), 64, cos=0.99999, max_rel=1e-3)
+
+
+def test_init_random_equals_uploaded_oracle_weights(gpu):
+    # the device RNG reproduces the CPU reference's weights bit for bit: the same step, the same bits
+    m, e = make_pair(M.FAMILY_DUAL, seed=3)
+    e2 = M.Engine(M.FAMILY_DUAL, **TINY)
+    e2.init_random(3)
+    prompt, lat = inputs(2)
+    for eng in (e, e2):
+        eng.begin(prompt[0], H_, W_, 0)
+    assert np.array_equal(e.step(lat[0], 0.3, 0), e2.step(lat[0], 0.3, 0))
+
+
+def test_init_random_fp8_equals_uploaded(gpu):
+    m, e = make_pair(M.FAMILY_DUAL, fp8=True, seed=4)
+    e2 = M.Engine(M.FAMILY_DUAL, **TINY, weight_dtype=M.FP8)
+    e2.init_random(4)
+    prompt, lat = inputs(3)
+    for eng in (e, e2):
+        eng.begin(prompt[0], H_, W_, 0)
+    assert np.array_equal(e.step(lat[0], 0.3, 0), e2.step(lat[0], 0.3, 0))
+
+
+Q21 = dict(blocks=2, dim=512, heads=4, head_dim=128, ffn=1536, text_dim=512)
+
+
+def test_q21_steps_with_text_cache_match_oracle(gpu):
+    # the reference's own graph: step 1 runs [text; image], step 2 only the image against the cached text K / V;
+    # the oracle recomputes the whole sequence each time (equal, since text rows see only text keys at t = 0)
+    m, e = make_pair(M.FAMILY_Q21, dims=Q21, wstd=0.05)
+    prompt, lat = inputs(4, B=1, S=40, h=12, w=10)
+    e.begin(prompt[0], 12, 10, 0)
+    for step, sig in enumerate((0.9, 0.7)):
+        got_p, want_p = {}, {}
+        e.set_probe(got_p)
+        got = e.step(lat[0], sig, 0)
+        want = m.q21_step(prompt[0], lat[0], 12, 10, sig, want_p)
+        within(got, want, 64)
+        N = 12 * 10
+        for i in range(2):  # the image rows of each block (step 2 runs only those)
+            within(got_p[("block", i)].reshape(-1, 512)[-N:], want_p[("block", i)].reshape(-1, 512)[-N:], 512)
+
+
+def test_q21_step_errors(gpu):
+    e = M.Engine(M.FAMILY_Q21, **Q21)
+    with pytest.raises(M.MkError, match="before begin"):
+        e.step(np.zeros((4, 64), np.float32), 0.5, 0)
+    with pytest.raises(M.MkError, match="slot"):
+        e.begin(np.zeros((3, 512), np.float32), 2, 2, 2)
+    e.begin(np.zeros((3, 512), np.float32), 2, 2, 0)
+    with pytest.raises(M.MkError, match="latents"):
+        e.step(np.zeros((5, 64), np.float32), 0.5, 0)
+
+
+SDXL_A = dict(blocks=1, dim=640, heads=10, head_dim=64, ffn=2560, text_dim=2048)
+
+
+def test_sdxl_block_matches_oracle(gpu):
+    m, e = make_pair(M.FAMILY_SDXL, dims=SDXL_A, wstd=0.05)
+    rng = np.random.default_rng(5)
+    n, S = 1024, 77
+    x = rng.standard_normal((2, n, 640)).astype(np.float32)
+    ctx = rng.standard_normal((2, S, 2048)).astype(np.float32)
+    for s in (0, 1):
+        e.begin(ctx[s], 32, 32, s)
+    xd, yd = M.Dev.from_array(x), M.Dev(x.nbytes)
+    e.sdxl_forward(xd, 2, n, yd)
+    got = yd.to_array(np.float32, x.shape)
+    for b in range(2):
+        want = m.sdxl_trans(x[b], ctx[b])
+        within(got[b] - x[b], want - x[b], 640)
+
+
+def test_attention_full_size_sampled_rows(gpu):
+    # config 2 at its full size: B=2, 24 heads x 128, 4096 image + 256 text tokens, QK-RMSNorm and RoPE applied by
+    # the heads kernel; 48 sampled query rows per (batch, head) checked against the oracle's softmax over all keys
+    B, H, T, S = 2, 24, 4352, 256
+    rng = np.random.default_rng(6)
+    D = H * 128
+    qkv = R.bf16_round(rng.standard_normal((B, T, 3 * D)).astype(np.float32))
+    cs = R.rope_table(S, 64, 64)
+    nq = (1 + 0.02 * rng.standard_normal(128)).astype(np.float32)
+    nk = (1 + 0.02 * rng.standard_normal(128)).astype(np.float32)
+    q_pad, k_pad = 4352, 4352
+    Q, K, V = M.Dev(B * H * q_pad * 256), M.Dev(B * H * k_pad * 256), M.Dev(B * H * k_pad * 256)
+    X, csd, nqd, nkd = M.Dev.from_array(M.bf16_bits(qkv)), M.Dev.from_array(cs), M.Dev.from_array(nq), \
+        M.Dev.from_array(nk)
+    for col0, w_, out, pad, tr in ((0, nqd, Q, q_pad, 0), (D, nkd, K, k_pad, 0), (2 * D, None, V, k_pad, 1)):
+        M.call("mk_heads", X.p, B, T, 3 * D, T * 3 * D, col0, H, 128, w_.p if w_ else None, 1e-6,
+               None if tr else csd.p, 0 if tr else 2, out.p, pad, 0, tr, None)
+    O = M.Dev(B * T * D * 2)
+    M.call("mk_attention", Q.p, K.p, V.p, O.p, B, H, 128, T, q_pad, T, k_pad, D, T * D, 0, 0,
+           float(1 / np.sqrt(128)), None)
+    M.sync()
+    got = M.bf16_to_f32(O.to_array(np.uint16, (B, T, D)))
+    rows = np.sort(rng.choice(T, 48, replace=False))
+    for b in range(B):
+        qh = R.heads_norm_rope(qkv[b], H, 128, col0=0, w=nq, cs=cs, rope=2)
+        kh = R.heads_norm_rope(qkv[b], H, 128, col0=D, w=nk, cs=cs, rope=2)
+        vh = R.heads_norm_rope(qkv[b], H, 128, col0=2 * D)
+        qh, kh, vh = (R.bf16_round(a) for a in (qh, kh, vh))
+        want = R.attention(np.ascontiguousarray(qh[None, :, rows]), kh[None], vh[None], 1 / np.sqrt(128))
+        within(got[b, rows], want[0], 128, cos=0.9999, max_rel=2e-2)

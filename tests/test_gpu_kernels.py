@@ -1,0 +1,367 @@
+"""Kernel parity on the GPU: each entry point of the kernel-dispatch surface (include/mkimage.h), called through the C
+ABI on seeded inputs, against the oracle (oracle/mkref.cpp). Index / byte work (patchify, the RNG fill, fp8 codes,
+layouts) is bit-exact; floating point is within the stated tolerance."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import mkimage as M
+import mkref as R
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(a):
+    return M.Dev.from_array(np.ascontiguousarray(a))
+
+
+def bdev(a):
+    """bf16 device copy of a float array."""
+    return M.Dev.from_array(M.bf16_bits(a))
+
+
+def fetch(d, shape, dtype=np.float32):
+    return d.to_array(dtype, shape)
+
+
+def fetch_bf16(d, shape):
+    return M.bf16_to_f32(d.to_array(np.uint16, shape))
+
+
+def maxrel(got, want):
+    got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
+    return float(np.abs(got - want).max() / max(np.abs(want).max(), 1e-30))
+
+
+def gemm(A, W, *, bias=None, wscale=None, epi=M.EPI_STORE, c=None, c_dtype=M.F32, M_=None, batch=1, lda=None,
+         ldc=None, sa=0, sc=0, gate=None, gate_alt=0, split=0, seg=0, w_dtype=M.BF16, heads=None, a_off=0):
+    g = M.GemmArgs()
+    g.a, g.w = A.p + a_off, W.p
+    g.wscale = wscale.p if wscale is not None else None
+    g.bias = bias.p if bias is not None else None
+    g.c = c.p if c is not None else None
+    g.gate = gate.p if gate is not None else None
+    g.gate_alt, g.split, g.seg_rows = gate_alt, split, seg
+    g.M, g.N, g.K = M_
+    g.lda, g.ldc, g.stride_a, g.stride_c, g.batch = lda, ldc, sa, sc, batch
+    g.w_dtype, g.c_dtype, g.epilogue = w_dtype, c_dtype, epi
+    g.heads = C.pointer(heads) if heads is not None else None
+    M.call("mk_gemm", C.byref(g), None)
+    M.sync()
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# GEMM
+# ---------------------------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("Mr,N,K", [(300, 256, 192), (512, 1024, 256), (77, 128, 64), (1000, 64, 128), (5, 640, 2560)])
+def test_gemm_store_f32(gpu, rng, Mr, N, K):
+    A = rng.standard_normal((Mr, K)).astype(np.float32)
+    W = R.bf16_round(rng.standard_normal((N, K)).astype(np.float32) * 0.05)
+    b = rng.standard_normal(N).astype(np.float32)
+    out = M.Dev(Mr * N * 4)
+    gemm(bdev(A), bdev(W), bias=dev(b), c=out, M_=(Mr, N, K), lda=K, ldc=N)
+    want = R.gemm(A, W, b)
+    assert maxrel(fetch(out, (Mr, N)), want) < 1e-5
+
+
+def test_gemm_gelu_bf16(gpu, rng):
+    Mr, N, K = 260, 512, 320
+    A = rng.standard_normal((Mr, K)).astype(np.float32)
+    W = R.bf16_round(rng.standard_normal((N, K)).astype(np.float32) * 0.1)
+    b = rng.standard_normal(N).astype(np.float32)
+    out = M.Dev(Mr * N * 2)
+    gemm(bdev(A), bdev(W), bias=dev(b), c=out, c_dtype=M.BF16, epi=M.EPI_GELU_TANH, M_=(Mr, N, K), lda=K, ldc=N)
+    want = R.gelu_tanh(R.gemm(A, W, b))
+    got = fetch_bf16(out, (Mr, N))
+    assert np.abs(got - want).max() <= 2 ** -8 * np.abs(want).max() + 1e-6
+
+
+@pytest.mark.parametrize("epi", [M.EPI_GATE_ADD, M.EPI_GATE_TANH, M.EPI_ADD])
+def test_gemm_residual_epilogues(gpu, rng, epi):
+    # batched with strides (rows of one batch item inside a longer sequence), gate rows split as the 2.1 graph's
+    B, Mr, N, K, T = 2, 200, 256, 128, 230
+    A = rng.standard_normal((B, T, K)).astype(np.float32)
+    W = R.bf16_round(rng.standard_normal((N, K)).astype(np.float32) * 0.05)
+    b = rng.standard_normal(N).astype(np.float32)
+    gates = rng.standard_normal((2, N)).astype(np.float32)
+    X = rng.standard_normal((B, Mr, N)).astype(np.float32)
+    Xd = dev(X)
+    split = 37
+    # A holds the whole sequence [B][T][K]; the GEMM reads rows 30 .. 30 + Mr of each batch item
+    gemm(bdev(A), bdev(W), bias=dev(b), c=Xd, epi=epi, M_=(Mr, N, K), batch=B, lda=K, ldc=N, sa=T * K, sc=Mr * N,
+         gate=dev(gates), gate_alt=N, split=split, seg=Mr, a_off=30 * K * 2)
+    want = X.astype(np.float64).copy()
+    for bi in range(B):
+        y = R.gemm(A[bi, 30:], W, b)
+        if epi == M.EPI_ADD:
+            want[bi] += y
+        else:
+            g = np.where(np.arange(Mr)[:, None] < split, gates[1], gates[0])
+            want[bi] += (np.tanh(g) if epi == M.EPI_GATE_TANH else g) * y
+    assert maxrel(fetch(Xd, (B, Mr, N)), want) < 1e-5
+
+
+def test_gemm_fp8_weights(gpu, rng):
+    Mr, N, K = 333, 256, 256
+    A = rng.standard_normal((Mr, K)).astype(np.float32)
+    Wf = rng.standard_normal((N, K)).astype(np.float32) * 0.02
+    scale = (np.abs(Wf).max(1) / 448).astype(np.float32)
+    codes = np.array([[R.lib().mkref_f32_to_e4m3(float(v)) for v in row] for row in Wf / scale[:, None]],
+                     dtype=np.uint8)
+    q = R.e4m3_table()[codes]
+    b = rng.standard_normal(N).astype(np.float32)
+    out = M.Dev(Mr * N * 4)
+    gemm(bdev(A), dev(codes), bias=dev(b), wscale=dev(scale), c=out, M_=(Mr, N, K), lda=K, ldc=N, w_dtype=M.FP8)
+    assert maxrel(fetch(out, (Mr, N)), R.gemm(A, q, b, wscale=scale)) < 1e-5
+
+
+@pytest.mark.parametrize("mode,row0,q_row0", [(2, 40, 40), (1, 0, 0), (0, 17, 0)])
+def test_gemm_heads_epilogue(gpu, rng, mode, row0, q_row0):
+    # q | k | v columns -> per-head RMSNorm + RoPE -> Q, K [b][h][pad][128] and V^T [b][h][128][pad]
+    B, Mr, H = 2, 150, 2
+    D = H * 128
+    K_ = 256
+    q_pad, k_pad = 256, 256
+    A = rng.standard_normal((B, Mr, K_)).astype(np.float32)
+    W = R.bf16_round(rng.standard_normal((3 * D, K_)).astype(np.float32) * 0.05)
+    b = rng.standard_normal(3 * D).astype(np.float32) * 0.1
+    nq = (1 + 0.1 * rng.standard_normal(128)).astype(np.float32)
+    nk = (1 + 0.1 * rng.standard_normal(128)).astype(np.float32)
+    cs = R.rope_table(row0, 14, 14)[: row0 + Mr] if row0 else R.rope_table(0, 15, 10)[:Mr]
+    Q, Kd, Vt = M.Dev(B * H * q_pad * 256), M.Dev(B * H * k_pad * 256), M.Dev(B * H * k_pad * 256)
+    ha = M.HeadsArgs(Q.p, Kd.p, Vt.p, H, 128, q_pad, k_pad, row0, q_row0, None, None, None, mode, 1e-6)
+    nqd, nkd, csd = dev(nq), dev(nk), dev(cs)
+    ha.norm_q, ha.norm_k, ha.rope = nqd.p, nkd.p, csd.p
+    Ad = bdev(A)
+    gemm(Ad, bdev(W), bias=dev(b), epi=M.EPI_HEADS, c_dtype=M.BF16, M_=(Mr, 3 * D, K_), batch=B, lda=K_,
+         sa=Mr * K_, heads=ha)
+    gq = fetch_bf16(Q, (B, H, q_pad, 128))
+    gk = fetch_bf16(Kd, (B, H, k_pad, 128))
+    gv = fetch_bf16(Vt, (B, H, 128, k_pad))
+    for bi in range(B):
+        y = R.gemm(A[bi], W, b)
+        tab = cs[row0:]
+        wq = R.heads_norm_rope(y, H, 128, col0=0, w=nq, cs=tab, rope=mode)
+        wk = R.heads_norm_rope(y, H, 128, col0=D, w=nk, cs=tab, rope=mode)
+        wv = R.heads_norm_rope(y, H, 128, col0=2 * D)
+        for got, want in ((gq[bi][:, q_row0:q_row0 + Mr], wq), (gk[bi][:, row0:row0 + Mr], wk),
+                          (gv[bi][:, :, row0:row0 + Mr].transpose(0, 2, 1), wv)):
+            assert np.abs(got - want).max() <= 2 ** -8 * np.abs(want).max() + 1e-6
+    # rows outside the written range stay zero
+    assert not gk[:, :, :row0].any() and not gk[:, :, row0 + Mr:].any()
+
+
+def test_gemm_rejects_bad_shapes(gpu):
+    g = M.GemmArgs()
+    d = M.Dev(1024)
+    g.a = g.w = g.c = d.p
+    g.M, g.N, g.K, g.lda, g.ldc, g.batch, g.w_dtype = 4, 60, 64, 64, 60, 1, M.BF16
+    assert M.lib().mk_gemm(C.byref(g), None) == 1
+    assert b"multiples of 64" in M.lib().mk_last_error()
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# attention
+# ---------------------------------------------------------------------------------------------------------------
+
+def run_attention(q, k, v, scale, q_pos0=0, block=0):
+    """q [B][H][Tq][d], k, v [B][H][Tk][d] (bf16-exact floats) through mk_attention; returns [B][Tq][H*d]."""
+    B, H, Tq, d = q.shape
+    Tk = k.shape[2]
+    q_pad = (Tq + 255) // 256 * 256
+    k_pad = (Tk + 63) // 64 * 64
+    qp = np.zeros((B, H, q_pad, d), np.float32)
+    qp[:, :, :Tq] = q
+    kp = np.zeros((B, H, k_pad, d), np.float32)
+    kp[:, :, :Tk] = k
+    vt = np.zeros((B, H, d, k_pad), np.float32)
+    vt[:, :, :, :Tk] = v.transpose(0, 1, 3, 2)
+    out = M.Dev(B * Tq * H * d * 2)
+    M.call("mk_attention", bdev(qp).p, bdev(kp).p, bdev(vt).p, out.p, B, H, d, Tq, q_pad, Tk, k_pad, H * d,
+           Tq * H * d, q_pos0, block, scale, None)
+    M.sync()
+    return fetch_bf16(out, (B, Tq, H * d))
+
+
+@pytest.mark.parametrize("d,Tq,Tk,block,q_pos0", [(128, 300, 300, 0, 0), (128, 64, 4352 // 17, 0, 0),
+                                                  (64, 333, 77, 0, 0), (64, 256, 1000, 0, 0),
+                                                  (128, 200, 260, 60, 60), (128, 260, 260, 60, 0),
+                                                  (128, 190, 190, 0xFFFFFFFF, 0)])
+def test_attention_matches_oracle(gpu, rng, d, Tq, Tk, block, q_pos0):
+    B, H = 2, 3
+    q = R.bf16_round(rng.standard_normal((B, H, Tq, d)).astype(np.float32))
+    k = R.bf16_round(rng.standard_normal((B, H, Tk, d)).astype(np.float32))
+    v = R.bf16_round(rng.standard_normal((B, H, Tk, d)).astype(np.float32))
+    got = run_attention(q, k, v, 1 / np.sqrt(d), q_pos0, block)
+    want = R.attention(q, k, v, 1 / np.sqrt(d), q_pos0, block)
+    dd = R.diff(got, want, d)
+    # P is rounded to bf16 for the MFMA, the output stored bf16
+    assert dd["min_cos"] > 0.9999 and dd["max_rel"] < 1e-2, dd
+
+
+def test_attention_golden(gpu):
+    import pathlib
+    G = np.load(pathlib.Path(__file__).resolve().parent / "golden" / "golden.npz")
+    for name, block in (("attn", 0), ("attn64", 0), ("attnc", 0xFFFFFFFF), ("attnp", 12)):
+        q, k, v = G[name + "_q"], G[name + "_k"], G[name + "_v"]
+        got = run_attention(q, k, v, 1 / np.sqrt(q.shape[-1]), 0, block)
+        dd = R.diff(got, G[name + "_o"], q.shape[-1])
+        assert dd["min_cos"] > 0.9999 and dd["max_rel"] < 1e-2, (name, dd)
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# bandwidth-bound kernels
+# ---------------------------------------------------------------------------------------------------------------
+
+def test_ln_modulate(gpu, rng):
+    rows, n = 230, 3072
+    x = (rng.standard_normal((rows, n)) * 3 + 1).astype(np.float32)
+    mod = rng.standard_normal((2, 2, n)).astype(np.float32) * 0.3  # row r<split takes mod[1]: [shift, scale]
+    y = M.Dev(rows * n * 2)
+    md = dev(mod)
+    split, seg = 20, 115
+    M.call("mk_ln_modulate", dev(x).p, rows, n, md.p + n * 4, md.p, 2 * n, split, seg, 1e-6, y.p, None)
+    M.sync()
+    got = fetch_bf16(y, (rows, n))
+    alt = (np.arange(rows) % seg) < split
+    for r in (0, 19, 20, 114, 115, 134, 135, 229):
+        m = mod[1] if alt[r] else mod[0]
+        want = R.ln_modulate(x[r:r + 1], m[1], m[0])
+        assert np.abs(got[r] - want).max() <= 2 ** -8 * np.abs(want).max() + 1e-6
+
+
+def test_gate_add_tanh_bf16(gpu, rng):
+    rows, n = 100, 512
+    x = rng.standard_normal((rows, n)).astype(np.float32)
+    y = R.bf16_round(rng.standard_normal((rows, n)).astype(np.float32))
+    g = rng.standard_normal((2, n)).astype(np.float32)
+    xd = dev(x)
+    M.call("mk_gate_add", xd.p, bdev(y).p, M.BF16, rows, n, dev(g).p, n, 30, rows, 1, None)
+    M.sync()
+    want = x + np.tanh(np.where(np.arange(rows)[:, None] < 30, g[1], g[0])) * y
+    assert maxrel(fetch(xd, (rows, n)), want) < 1e-6
+
+
+@pytest.mark.parametrize("d,mode,transpose", [(128, 2, 0), (128, 1, 0), (64, 0, 0), (128, 0, 1), (64, 0, 1)])
+def test_heads(gpu, rng, d, mode, transpose):
+    B, rows, H = 2, 90, 3
+    ld = 3 * H * d
+    x = R.bf16_round(rng.standard_normal((B, rows, ld)).astype(np.float32))
+    w = None if transpose or d == 64 else (1 + 0.1 * rng.standard_normal(d)).astype(np.float32)
+    cs = R.rope_table(10, 10, 10)
+    row0, n_pad = 7, 128
+    out = M.Dev(B * H * n_pad * d * 2)
+    wd = dev(w) if w is not None else None
+    csd = dev(cs)
+    M.call("mk_heads", bdev(x).p, B, rows, ld, rows * ld, H * d, H, d, wd.p if wd else None, 1e-6,
+           csd.p if mode else None, mode, out.p, n_pad, row0, transpose, None)
+    M.sync()
+    got = fetch_bf16(out, (B, H, d, n_pad) if transpose else (B, H, n_pad, d))
+    for bi in range(B):
+        want = R.heads_norm_rope(x[bi], H, d, col0=H * d, w=w, cs=cs[row0:] if mode else None, rope=mode)
+        g = got[bi][:, :, row0:row0 + rows].transpose(0, 2, 1) if transpose else got[bi][:, row0:row0 + rows]
+        assert np.abs(g - want).max() <= 2 ** -8 * np.abs(want).max() + 1e-6
+
+
+def test_gemv_modulation(gpu, rng):
+    K, N = 3072, 6 * 3072 + 64
+    x = rng.standard_normal((1, K)).astype(np.float32)
+    W = R.bf16_round(rng.standard_normal((N, K)).astype(np.float32) * 0.02)
+    b = rng.standard_normal(N).astype(np.float32)
+    y = M.Dev(N * 4)
+    M.call("mk_gemv", dev(x).p, 1, K, bdev(W).p, dev(b).p, N, y.p, 1, None)
+    M.sync()
+    xs = R.silu(x).astype(np.float64)
+    want = xs @ W.T.astype(np.float64) + b  # the GEMV keeps x in fp32
+    assert maxrel(fetch(y, (1, N)), want) < 1e-5
+
+
+def test_norms(gpu, rng):
+    rows, n = 70, 1280
+    x = (rng.standard_normal((rows, n)) * 2 + 0.3).astype(np.float32)
+    g = (1 + 0.1 * rng.standard_normal(n)).astype(np.float32)
+    b = (0.1 * rng.standard_normal(n)).astype(np.float32)
+    y = M.Dev(rows * n * 2)
+    M.call("mk_layer_norm", dev(x).p, rows, n, dev(g).p, dev(b).p, 1e-5, y.p, None)
+    M.sync()
+    want = R.layer_norm(x, g, b, 1e-5)
+    assert np.abs(fetch_bf16(y, (rows, n)) - want).max() <= 2 ** -8 * np.abs(want).max()
+    M.call("mk_rms_norm", dev(x).p, rows, n, dev(g - 1).p, 1.0, 1e-6, y.p, None)  # zero-centred weight + 1
+    M.sync()
+    want = R.rms_norm(x, g)
+    assert np.abs(fetch_bf16(y, (rows, n)) - want).max() <= 2 ** -8 * np.abs(want).max()
+    xg = rng.standard_normal((2, 300, 640)).astype(np.float32)
+    gg = (1 + 0.1 * rng.standard_normal(640)).astype(np.float32)
+    yg = M.Dev(2 * 300 * 640 * 2)
+    M.call("mk_group_norm", dev(xg).p, 2, 300, 640, 32, dev(gg).p, dev(b[:640]).p, 1e-6, yg.p, None)
+    M.sync()
+    got = fetch_bf16(yg, (2, 300, 640))
+    for bi in range(2):
+        want = R.group_norm(xg[bi], gg, b[:640], 32, 1e-6)
+        assert np.abs(got[bi] - want).max() <= 2 ** -8 * np.abs(want).max() + 1e-5
+
+
+def test_glu(gpu, rng):
+    rows, F = 50, 640
+    hg = rng.standard_normal((rows, 2 * F)).astype(np.float32) * 2
+    m = M.Dev(rows * F * 2)
+    for name, ref in (("mk_swiglu", R.swiglu), ("mk_geglu", R.geglu)):
+        M.call(name, dev(hg).p, M.F32, rows, F, m.p, None)
+        M.sync()
+        want = ref(hg)
+        assert np.abs(fetch_bf16(m, (rows, F)) - want).max() <= 2 ** -8 * np.abs(want).max() + 1e-6
+
+
+def test_cfg_euler_exact(gpu, rng):
+    n = 4096 * 64
+    x, pos, neg = (rng.standard_normal(n).astype(np.float32) for _ in range(3))
+    out = M.Dev(n * 4)
+    M.call("mk_cfg_euler", dev(x).p, dev(pos).p, dev(neg).p, n, np.float32(4.0), np.float32(-0.05), out.p, None)
+    M.sync()
+    v = (neg + np.float32(4.0) * (pos - neg)).astype(np.float32)
+    want = (x + np.float32(-0.05) * v).astype(np.float32)
+    assert np.abs(fetch(out, (n,)) - want).max() <= 1e-6 * np.abs(want).max()
+
+
+def test_patchify_bit_exact(gpu, rng):
+    B, Cc, h, w = 2, 16, 12, 10
+    lat = rng.standard_normal((B, Cc, 2 * h, 2 * w)).astype(np.float32)
+    tok = M.Dev(lat.nbytes)
+    M.call("mk_patchify", dev(lat).p, B, Cc, h, w, tok.p, None)
+    M.sync()
+    got = fetch(tok, (B, h * w, 4 * Cc))
+    for bi in range(B):
+        assert np.array_equal(got[bi], R.patchify(lat[bi], h, w))
+    back = M.Dev(lat.nbytes)
+    M.call("mk_unpatchify", tok.p, B, Cc, h, w, back.p, None)
+    M.sync()
+    assert np.array_equal(fetch(back, lat.shape), lat)
+
+
+@pytest.mark.parametrize("dtype", [M.F32, M.BF16])
+def test_fill_normal_matches_oracle_rng(gpu, dtype):
+    n = 1 << 20
+    key = R.tensor_key(0, "transformer_blocks.3.img_mlp.net.0.proj.weight")
+    d = M.Dev(n * 4)
+    M.call("mk_fill_normal", d.p, n, dtype, key, 0.0, 0.02, None)
+    M.sync()
+    want = np.empty(n, np.float32)
+    R.lib().mkref_fill_normal(R.fp(want), n, key, 0.0, 0.02, int(dtype == M.BF16))
+    got = fetch(d, (n,)) if dtype == M.F32 else fetch_bf16(d, (n,))
+    assert np.array_equal(got, want)
+
+
+def test_quantize_fp8_matches_oracle(gpu):
+    m = R.Model(R.DUAL, 1, 256, 2, 128, 512, 256, fp8=True, seed=9)
+    name = "transformer_blocks.0.img_mlp.net.0.proj.weight"
+    q, scale = m.get(name), m.get(name + ".scale")
+    rows, cols = q.shape
+    # the same bf16 source the oracle quantised: N(0, 0.02) rounded to bf16
+    src = R.normal(rows * cols, 9, name, 0.0, 0.02, round_bf16=True).reshape(rows, cols)
+    codes, sc = M.Dev(rows * cols), M.Dev(rows * 4)
+    M.call("mk_quantize_fp8_rows", bdev(src).p, rows, cols, codes.p, sc.p, None)
+    M.sync()
+    assert np.array_equal(fetch(sc, (rows,)), scale)
+    assert np.array_equal(R.e4m3_table()[fetch(codes, (rows, cols), np.uint8)], q)
