@@ -117,8 +117,9 @@ typedef struct mk_gemm_args {
 mk_status mk_gemm(const mk_gemm_args* a, void* stream);
 
 /* GEMV for a few rows (the time embedding and modulation projections, rows <= 4):
- * y[r][n] = act(sum_k W[n][k] x[r][k] + b[n]), x fp32 [rows][K], W bf16 [N][K], y fp32; act 0 none, 1 silu
- * applied to x first (silu(x) is the modulation layers' input). */
+ * y[r][n] = sum_k W[n][k] bf16(x'[r][k]) + b[n] with x' = silu(x) when silu_x (silu(temb) is the modulation
+ * layers' input), else x; x fp32 [rows][K], W bf16 [N][K], y fp32. The activation is rounded to bf16 as every GEMM's
+ * is. */
 mk_status mk_gemv(const float* x, uint32_t rows, uint32_t K, const void* w, const float* bias, uint32_t N, float* y,
                   int silu_x, void* stream);
 

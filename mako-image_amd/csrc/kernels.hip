@@ -244,14 +244,17 @@ __global__ __launch_bounds__(256) void heads_t_kernel(const uint16_t* __restrict
         if (r0 + c >= rows)
             continue;
         uint16_t* o = out + ((uint64_t(bi) * heads + h) * kD + dd) * n_pad + row0 + r0 + c;
-        if (r0 + c + 1 < rows)
+        if (r0 + c + 1 < rows && ((row0 + r0 + c) & 1) == 0) {
             *reinterpret_cast<uint32_t*>(o) = uint32_t(t[c][dd]) | (uint32_t(t[c + 1][dd]) << 16);
-        else
+        } else {
             o[0] = t[c][dd];
+            if (r0 + c + 1 < rows)
+                o[1] = t[c + 1][dd];
+        }
     }
 }
 
-// GEMV for rows <= 4: y[r][n] = sum_k W[n][k] x'[r][k] + b[n], x' = silu(x) if asked; x' staged in LDS.
+// GEMV for rows <= 4: y[r][n] = sum_k W[n][k] bf16(x'[r][k]) + b[n], x' = silu(x) if asked; x' staged in LDS.
 // Each wave computes 4 outputs at a time, 16-byte weight loads.
 __global__ __launch_bounds__(256) void gemv_kernel(const float* __restrict__ x, uint32_t rows, uint32_t K,
                                                    const uint16_t* __restrict__ w, const float* __restrict__ bias,
@@ -260,7 +263,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(const float* __restrict__ x, 
     extern __shared__ float xs[];
     for (uint32_t i = threadIdx.x; i < rows * K; i += 256) {
         const float v = x[i];
-        xs[i] = silu_x ? v / (1.0f + __expf(-v)) : v;
+        xs[i] = bf2f_bits(f2bf_bits(silu_x ? v / (1.0f + __expf(-v)) : v)); // the GEMMs' bf16 activation operand
     }
     __syncthreads();
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;

@@ -12,13 +12,27 @@ import mkref as R
 pytestmark = pytest.mark.gpu
 
 
+_live = []  # device buffers of the running test: kept until it ends, so no pointer outlives its allocation
+
+
+@pytest.fixture(autouse=True)
+def _keep_buffers():
+    yield
+    M.sync()
+    _live.clear()
+
+
 def dev(a):
-    return M.Dev.from_array(np.ascontiguousarray(a))
+    d = M.Dev.from_array(np.ascontiguousarray(a))
+    _live.append(d)
+    return d
 
 
 def bdev(a):
     """bf16 device copy of a float array."""
-    return M.Dev.from_array(M.bf16_bits(a))
+    d = M.Dev.from_array(M.bf16_bits(a))
+    _live.append(d)
+    return d
 
 
 def fetch(d, shape, dtype=np.float32):
@@ -35,7 +49,7 @@ def maxrel(got, want):
 
 
 def gemm(A, W, *, bias=None, wscale=None, epi=M.EPI_STORE, c=None, c_dtype=M.F32, M_=None, batch=1, lda=None,
-         ldc=None, sa=0, sc=0, gate=None, gate_alt=0, split=0, seg=0, w_dtype=M.BF16, heads=None, a_off=0):
+         ldc=0, sa=0, sc=0, gate=None, gate_alt=0, split=0, seg=0, w_dtype=M.BF16, heads=None, a_off=0):
     g = M.GemmArgs()
     g.a, g.w = A.p + a_off, W.p
     g.wscale = wscale.p if wscale is not None else None
@@ -273,8 +287,7 @@ def test_gemv_modulation(gpu, rng):
     y = M.Dev(N * 4)
     M.call("mk_gemv", dev(x).p, 1, K, bdev(W).p, dev(b).p, N, y.p, 1, None)
     M.sync()
-    xs = R.silu(x).astype(np.float64)
-    want = xs @ W.T.astype(np.float64) + b  # the GEMV keeps x in fp32
+    want = R.gemm(R.silu(x), W, b)  # silu(x) rounded to bf16 as the GEMMs' activation operand
     assert maxrel(fetch(y, (1, N)), want) < 1e-5
 
 
