@@ -79,7 +79,7 @@ enum mk_epilogue {
 
 typedef struct mk_heads_args {
     /* Destination of the fused q/k/v epilogue: Q, K [batch][heads][n_pad][d] bf16 and V^T [batch][heads][d][k_pad]
-     * bf16, written at rows row0 + r (r the GEMM row within the batch). */
+     * bf16 (keys in the MK_VT_COL order), written at rows row0 + r (r the GEMM row within the batch). */
     void* q;
     void* k;
     void* vt;
@@ -136,13 +136,18 @@ mk_status mk_gate_add(float* x, const void* y, uint32_t y_dtype, uint32_t rows, 
 /* heads_norm_half / heads_half (qwen_image.cpp:226-250, sdxl.cpp:439-448): per (row, head) of x bf16
  * [batch][rows][ld] at column col0 + head * d: optional RMSNorm * w, RoPE from table rows rope[row0 + r], written
  * bf16 to out [batch][heads][n_pad][d] at row0 + r (transpose = 0), or to out [batch][heads][d][n_pad] at column
- * row0 + r (transpose = 1: the V^T layout the attention reads). */
+ * MK_VT_COL(row0 + r) (transpose = 1: the V^T layout the attention reads). */
 mk_status mk_heads(const void* x, uint32_t batch, uint32_t rows, int64_t ld, int64_t stride_x, uint32_t col0,
                    uint32_t heads, uint32_t d, const float* w, float eps, const float* rope, uint32_t rope_mode,
                    void* out, uint32_t n_pad, uint32_t row0, int transpose, void* stream);
 
+/* V^T key order: within each group of 16 keys, key k sits at column k with bits 2 and 3 swapped (the order in which
+ * a lane of the P V matrix product reads 8 keys as one 16-byte load). */
+#define MK_VT_COL(k) (((k) & ~12u) | (((k) & 4u) << 1) | (((k) & 8u) >> 1))
+
 /* attention (qwen_image.cpp:271, sdxl.cpp:450-457): softmax(Q K^T scale) V, fp32 online softmax on bf16 MFMA.
- * q [batch][heads][q_pad][d], k [batch][heads][k_pad][d], vt [batch][heads][d][k_pad] bf16 (padding keys zero);
+ * q [batch][heads][q_pad][d], k [batch][heads][k_pad][d], vt [batch][heads][d][k_pad] bf16 with keys in the
+ * MK_VT_COL order (padding keys zero);
  * out bf16 [batch][n_q][ldo] at column head * d. Query row i (absolute q_pos0 + i) sees key c < n_k iff
  * q_pos0 + i >= block or c <= q_pos0 + i (block 0: no mask; UINT32_MAX: causal; S: causal text prefix).
  * d in {64, 128}; q_pad % 128 == 0; k_pad % 64 == 0. */

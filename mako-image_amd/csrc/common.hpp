@@ -94,10 +94,13 @@ __device__ inline float wave_max(float v)
 
 // ---- activations (fp32) ----
 __device__ inline float silu_f(float x) { return x / (1.0f + __expf(-x)); }
+// tanh(u) = 2 sigmoid(2u) - 1 (one exp, one divide; saturates cleanly at both ends)
+__device__ inline float tanh_f(float u) { return 2.0f / (1.0f + __expf(-2.0f * u)) - 1.0f; }
+// GELU with the tanh approximation: 0.5 x (1 + tanh(u)) = x sigmoid(2u), u = sqrt(2/pi) (x + 0.044715 x^3)
 __device__ inline float gelu_tanh_f(float x)
 {
     const float u = 0.7978845608028654f * (x + 0.044715f * x * x * x);
-    return 0.5f * x * (1.0f + tanhf(u));
+    return x / (1.0f + __expf(-2.0f * u));
 }
 // erf by the Numerical Recipes erfc Chebyshev fit (max error ~1.2e-7), the form the reference's geglu uses
 // (image.metal:450-463).
@@ -124,6 +127,11 @@ __host__ __device__ inline uint64_t splitmix64(uint64_t z)
     return z ^ (z >> 31);
 }
 uint64_t tensor_key(uint64_t seed, const char* name);
+
+// V^T column of key k: within each group of 16 keys, k with its bits 2 and 3 swapped. The P V MFMA's A operand lane
+// reads keys 4h .. 4h + 3 and 8 + 4h .. 8 + 4h + 3 of a 16-key step (h its half-wave); in this order they are 8
+// contiguous bf16, one 16-byte LDS read.
+__host__ __device__ inline uint32_t vt_col(uint32_t k) { return (k & ~12u) | ((k & 4u) << 1) | ((k & 8u) >> 1); }
 
 inline uint32_t cdiv(uint64_t a, uint64_t b) { return uint32_t((a + b - 1) / b); }
 inline uint64_t round_up(uint64_t a, uint64_t b) { return (a + b - 1) / b * b; }

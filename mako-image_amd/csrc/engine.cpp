@@ -585,9 +585,10 @@ struct mk_engine {
             MK_HIP(hipMemsetAsync(vt.p, 0, vt.bytes, stream));
             k_pad_last = k_pad;
         }
+        const uint32_t S16 = uint32_t(round_up(S, 16)); // V^T cache columns: whole groups of 16 keys
         if (first) {
             MK_TRY(g.kcache.ensure(size_t(cfg.blocks) * H * S * 128 * 2));
-            MK_TRY(g.vcache.ensure(size_t(cfg.blocks) * H * 128 * S * 2));
+            MK_TRY(g.vcache.ensure(size_t(cfg.blocks) * H * 128 * S16 * 2));
         }
         // rows [sigma, t = 0]: t_lin1 -> silu -> t_lin2 -> (probe) -> silu -> modulation / out_lin
         float tp[512];
@@ -632,20 +633,23 @@ struct mk_engine {
             ha.rope = rope.f();
             ha.rope_mode = 2;
             ha.eps = eps;
-            MK_TRY(gemm(B.qkv[0], xn_img.p, D, 0, T, 1, nullptr, 0, 0, MK_EPI_HEADS, MK_BF16, nullptr, 0, 0, 0, &ha));
-            // the text's keys and values: kept after the first step, restored after (heads_rows)
+            // the text's keys and values (heads_rows): kept after the first step's q/k/v, restored before the later
+            // steps'. V^T keeps whole groups of 16 keys (its columns permute keys within a group); a group shared
+            // with image keys is rewritten by the image rows' q/k/v that follow the restore.
             uint16_t* kc = g.kcache.h() + size_t(i) * H * S * 128;
-            uint16_t* vc = g.vcache.h() + size_t(i) * H * 128 * S;
+            uint16_t* vc = g.vcache.h() + size_t(i) * H * 128 * S16;
+            if (!first) {
+                MK_HIP(hipMemcpy2DAsync(k.p, size_t(k_pad) * 256, kc, size_t(S) * 256, size_t(S) * 256, H,
+                                        hipMemcpyDeviceToDevice, stream));
+                MK_HIP(hipMemcpy2DAsync(vt.p, size_t(k_pad) * 2, vc, size_t(S16) * 2, size_t(S16) * 2,
+                                        size_t(H) * 128, hipMemcpyDeviceToDevice, stream));
+            }
+            MK_TRY(gemm(B.qkv[0], xn_img.p, D, 0, T, 1, nullptr, 0, 0, MK_EPI_HEADS, MK_BF16, nullptr, 0, 0, 0, &ha));
             if (first) {
                 MK_HIP(hipMemcpy2DAsync(kc, size_t(S) * 256, k.p, size_t(k_pad) * 256, size_t(S) * 256, H,
                                         hipMemcpyDeviceToDevice, stream));
-                MK_HIP(hipMemcpy2DAsync(vc, size_t(S) * 2, vt.p, size_t(k_pad) * 2, size_t(S) * 2, size_t(H) * 128,
-                                        hipMemcpyDeviceToDevice, stream));
-            } else {
-                MK_HIP(hipMemcpy2DAsync(k.p, size_t(k_pad) * 256, kc, size_t(S) * 256, size_t(S) * 256, H,
-                                        hipMemcpyDeviceToDevice, stream));
-                MK_HIP(hipMemcpy2DAsync(vt.p, size_t(k_pad) * 2, vc, size_t(S) * 2, size_t(S) * 2, size_t(H) * 128,
-                                        hipMemcpyDeviceToDevice, stream));
+                MK_HIP(hipMemcpy2DAsync(vc, size_t(S16) * 2, vt.p, size_t(k_pad) * 2, size_t(S16) * 2,
+                                        size_t(H) * 128, hipMemcpyDeviceToDevice, stream));
             }
             MK_TRY(timed("attention", 4.0 * pairs * 128 * H, [&] {
                 return mk_attention(q.p, k.p, vt.p, att.p, 1, H, 128, T, q_pad, n_k, k_pad, D, 0, row0, S,

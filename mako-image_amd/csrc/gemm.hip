@@ -7,7 +7,7 @@
 //
 // Tiling: BM tokens x BN channels x 64 k per workgroup of 4 waves (2 x 2), each wave BN/2 x BM/2 as (BN/64) x (BM/64)
 // MFMA blocks of 32 x 32. Both tiles are K-contiguous and staged in LDS with a 16-byte-chunk XOR swizzle
-// (chunk ^ (row & 7)) so the fragment reads of 32 rows at one k offset are bank-conflict free; two LDS buffers, the
+// (chunk ^ ((row >> 1) & 7)) so the fragment reads of 32 rows at one k offset are bank-conflict free; two LDS buffers, the
 // next tile's global loads in flight in registers during the current tile's MFMAs, one barrier per k step.
 // Workgroups map to tiles XCD-aware (consecutive tiles on one XCD share its L2) and grouped along M.
 #include "common.hpp"
@@ -40,7 +40,11 @@ struct GemmP {
 
 constexpr int BK = 64;
 
-__device__ inline int swz(int row, int kc) { return row * 64 + ((kc ^ (row & 7)) << 3); }
+// LDS tile rows are 64 bf16 (128 bytes, 8 chunks of 16). gfx950's LDS has 64 banks (256 bytes a cycle): a 16-byte read
+// serves 16 lanes a cycle, here 16 consecutive rows at one logical chunk. Rows r and r + 1 fall in opposite halves of
+// the banks, so the chunk is XOR-ed with (row >> 1) & 7: the 8 rows of each half get 8 distinct chunks.
+__device__ inline int swz_chunk(int row, int kc) { return kc ^ ((row >> 1) & 7); }
+__device__ inline int swz(int row, int kc) { return row * 64 + (swz_chunk(row, kc) << 3); }
 
 // fp8 e4m3 (16 values in a u32x4) -> two bf16x8 chunks, exact.
 __device__ inline void f8x16_to_bf16(const u32x4& v, u32x4& lo, u32x4& hi)
@@ -58,49 +62,91 @@ __device__ inline void f8x16_to_bf16(const u32x4& v, u32x4& lo, u32x4& hi)
     hi = u32x4{o[4], o[5], o[6], o[7]};
 }
 
-// Epilogue of one 4-channel group of one token: acc -> (scale, bias) -> activation / residual / store.
-__device__ inline void epi_store(const GemmP& p, int64_t rowoff, int ch, bool alt, f32x4 v)
+// Epilogue kinds (template): a plain store, an activation, a read-modify-write of the fp32 residual, the q/k/v heads.
+enum { EK_STORE = 0, EK_ACT = 1, EK_RMW = 2, EK_HEADS = 3 };
+
+// Per-tile channel constants of a lane's 4 channels (the same for every token row it writes).
+struct EpiCh {
+    f32x4 scale, bias, g0, g1; // g0: the gate row, g1: the alternate gate row (rows r % seg_rows < split)
+};
+
+__device__ inline EpiCh epi_channels(const GemmP& p, int ch)
 {
-    if (p.wscale) {
-        const f32x4 s = *reinterpret_cast<const f32x4*>(p.wscale + ch);
+    EpiCh c;
+    c.scale = p.wscale ? *reinterpret_cast<const f32x4*>(p.wscale + ch) : f32x4{1, 1, 1, 1};
+    c.bias = p.bias ? *reinterpret_cast<const f32x4*>(p.bias + ch) : f32x4{0, 0, 0, 0};
+    if (p.gate) {
+        c.g0 = *reinterpret_cast<const f32x4*>(p.gate + ch);
+        c.g1 = p.split ? *reinterpret_cast<const f32x4*>(p.gate + p.gate_alt + ch) : c.g0;
+        if (p.epi == MK_EPI_GATE_TANH)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-            v[j] *= s[j];
+            for (int e = 0; e < 4; ++e) {
+                c.g0[e] = tanh_f(c.g0[e]);
+                c.g1[e] = tanh_f(c.g1[e]);
+            }
     }
-    if (p.bias) {
-        const f32x4 b = *reinterpret_cast<const f32x4*>(p.bias + ch);
+    return c;
+}
+
+// Epilogue of a wave's staged slice: 32 token rows x WC channels in LDS (row stride ld floats), rows tok0 .. of the
+// GEMM, channels from chw. Lanes run along the channels (4 each, WC/4 lanes a row), so LDS reads are conflict free and
+// every store instruction writes whole row segments. For the residual the rows' x loads go out together before the
+// stores (vmcnt also counts stores: a load among the stores would wait for all of them).
+template <int EK, int WC>
+__device__ inline void epi_slice(const GemmP& p, const float* st, int ld, int tok0, int chw, int lane, int64_t zc,
+                                 const EpiCh& k)
+{
+    constexpr int LPR = WC / 4, RPI = 64 / LPR, NI = 32 / RPI; // lanes a row, rows an instruction, rows a lane
+    const int c = lane % LPR, r0 = lane / LPR, ch = chw + 4 * c;
+    f32x4 v[NI];
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-            v[j] += b[j];
+    for (int i = 0; i < NI; ++i) {
+        v[i] = *reinterpret_cast<const f32x4*>(st + (r0 + RPI * i) * ld + 4 * c);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            v[i][e] = v[i][e] * k.scale[e] + k.bias[e];
     }
-    if (p.epi == MK_EPI_GELU_TANH) {
+    if constexpr (EK == EK_RMW) {
+        f32x4 x[NI];
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-            v[j] = gelu_tanh_f(v[j]);
-    } else if (p.epi == MK_EPI_SILU) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-            v[j] = silu_f(v[j]);
-    }
-    if (p.epi == MK_EPI_GATE_ADD || p.epi == MK_EPI_GATE_TANH || p.epi == MK_EPI_ADD) {
-        f32x4* x = reinterpret_cast<f32x4*>(static_cast<float*>(p.c) + rowoff + ch);
-        f32x4 xv = *x;
-        if (p.epi == MK_EPI_ADD) {
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                xv[j] += v[j];
-        } else {
-            const f32x4 g = *reinterpret_cast<const f32x4*>(p.gate + (alt ? p.gate_alt : 0) + ch);
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                xv[j] += (p.epi == MK_EPI_GATE_TANH ? tanhf(g[j]) : g[j]) * v[j];
+        for (int i = 0; i < NI; ++i) {
+            const int t = tok0 + r0 + RPI * i;
+            if (t < int(p.M))
+                x[i] = *reinterpret_cast<const f32x4*>(static_cast<float*>(p.c) + zc + int64_t(t) * p.ldc + ch);
         }
-        *x = xv;
-    } else if (p.c_bf16) {
-        *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(p.c) + rowoff + ch) =
-            u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
-    } else {
-        *reinterpret_cast<f32x4*>(static_cast<float*>(p.c) + rowoff + ch) = v;
+        const bool add = p.epi == MK_EPI_ADD;
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const int t = tok0 + r0 + RPI * i;
+            if (t < int(p.M)) {
+                const f32x4& g = (uint32_t(t) % p.seg_rows) < p.split ? k.g1 : k.g0;
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    x[i][e] += (add ? 1.0f : g[e]) * v[i][e];
+                *reinterpret_cast<f32x4*>(static_cast<float*>(p.c) + zc + int64_t(t) * p.ldc + ch) = x[i];
+            }
+        }
+        return;
+    }
+    if constexpr (EK == EK_ACT) {
+        const bool gelu = p.epi == MK_EPI_GELU_TANH;
+#pragma unroll
+        for (int i = 0; i < NI; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                v[i][e] = gelu ? gelu_tanh_f(v[i][e]) : silu_f(v[i][e]);
+    }
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+        const int t = tok0 + r0 + RPI * i;
+        if (t >= int(p.M))
+            continue;
+        const int64_t off = zc + int64_t(t) * p.ldc + ch;
+        if (p.c_bf16)
+            *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(p.c) + off) =
+                u32x2{pack_bf16x2(v[i][0], v[i][1]), pack_bf16x2(v[i][2], v[i][3])};
+        else
+            *reinterpret_cast<f32x4*>(static_cast<float*>(p.c) + off) = v[i];
     }
 }
 
@@ -114,24 +160,28 @@ __device__ __attribute__((noinline)) void epi_heads(const GemmP& p, const float*
     const int which = nw0 / int(h.dim), head = (nw0 % int(h.dim)) / 128;
     const int64_t bh = int64_t(blockIdx.z) * h.heads + head;
     if (which == 2) {
+        // V^T rows, keys in the vt_col order (bits 2 and 3 of the key swapped within groups of 16)
 #pragma unroll
         for (int dd = 0; dd < 2; ++dd) {
             const int d = 2 * lane + dd, ch = nw0 + d;
             const float sc = p.wscale ? p.wscale[ch] : 1.0f, bi = p.bias ? p.bias[ch] : 0.0f;
-            uint16_t* dst = h.vt + (bh * 128 + d) * int64_t(h.k_pad) + h.row0 + tok0;
-            const bool vec = ((h.row0 + tok0) % 8) == 0 && tok0 + 32 <= int(p.M);
-            if (vec) {
+            uint16_t* dst = h.vt + (bh * 128 + d) * int64_t(h.k_pad);
+            const uint32_t k0 = h.row0 + tok0;
+            if (k0 % 16 == 0 && tok0 + 32 <= int(p.M)) {
 #pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    uint32_t w[4];
-#pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        w[e] = pack_bf16x2(st[(8 * c + 2 * e) * ld + d] * sc + bi, st[(8 * c + 2 * e + 1) * ld + d] * sc + bi);
-                    *reinterpret_cast<u32x4*>(dst + 8 * c) = u32x4{w[0], w[1], w[2], w[3]};
+                for (int g = 0; g < 2; ++g) {
+                    // physical columns 16g + 0..15 hold keys 16g + {0..3, 8..11, 4..7, 12..15}
+                    auto v = [&](int j) { return st[(16 * g + j) * ld + d] * sc + bi; };
+                    *reinterpret_cast<u32x4*>(dst + k0 + 16 * g) =
+                        u32x4{pack_bf16x2(v(0), v(1)), pack_bf16x2(v(2), v(3)), pack_bf16x2(v(8), v(9)),
+                              pack_bf16x2(v(10), v(11))};
+                    *reinterpret_cast<u32x4*>(dst + k0 + 16 * g + 8) =
+                        u32x4{pack_bf16x2(v(4), v(5)), pack_bf16x2(v(6), v(7)), pack_bf16x2(v(12), v(13)),
+                              pack_bf16x2(v(14), v(15))};
                 }
             } else {
                 for (int t = 0; t < 32 && tok0 + t < int(p.M); ++t)
-                    dst[t] = f2bf_bits(st[t * ld + d] * sc + bi);
+                    dst[vt_col(k0 + t)] = f2bf_bits(st[t * ld + d] * sc + bi);
             }
         }
         return;
@@ -207,14 +257,18 @@ __device__ __attribute__((noinline)) void epi_heads(const GemmP& p, const float*
     }
 }
 
-template <int BM, int BN, bool kF8, bool kHeads>
-__global__ __launch_bounds__(256, 1) void gemm_kernel(GemmP p)
+template <int BM, int BN, bool kF8, int EK, int NW>
+__global__ __launch_bounds__(64 * NW, 1) __attribute__((amdgpu_waves_per_eu(NW / 4, NW / 4))) void gemm_kernel(GemmP p)
 {
-    constexpr int TB = BM / 64, CB = BN / 64;  // 32-row MFMA blocks per wave along tokens / channels
-    constexpr int RA = BM * 8 / 256;           // direct-load rounds for the activation tile (64 chunks per wave)
-    constexpr int RW = BN * 8 / 256;           // ... for a bf16 weight tile
-    constexpr int LW = BN * 4 / 256;           // 16-byte fp8 weight chunks per thread (register staged)
-    __shared__ __attribute__((aligned(16))) uint16_t smem[2 * (BN + BM) * 64];
+    constexpr int NT = 64 * NW;                 // threads
+    constexpr int WM = BM / (NW / 2);           // tokens per wave (waves: 2 along channels x NW/2 along tokens)
+    constexpr int TB = WM / 32, CB = BN / 64;   // 32-row MFMA blocks per wave along tokens / channels
+    constexpr int RA = BM * 8 / NT;             // direct-load rounds for the activation tile (64 chunks per wave)
+    constexpr int RW = BN * 8 / NT;             // ... for a bf16 weight tile
+    constexpr int LW = BN * 4 / NT;             // 16-byte fp8 weight chunks per thread (register staged)
+    constexpr int WC = BN / 2, LDW = WC + 4;    // epilogue staging: a wave's 32 tokens x WC channels, padded rows
+    constexpr int SMEM = 2 * (BN + BM) * 64 * 2 > NW * 32 * LDW * 4 ? 2 * (BN + BM) * 64 * 2 : NW * 32 * LDW * 4;
+    __shared__ __attribute__((aligned(16))) uint16_t smem[SMEM / 2];
     uint16_t(*sW)[BN * 64] = reinterpret_cast<uint16_t(*)[BN * 64]>(smem);
     uint16_t(*sA)[BM * 64] = reinterpret_cast<uint16_t(*)[BM * 64]>(smem + 2 * BN * 64);
 
@@ -236,12 +290,12 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmP p)
     const uint16_t* A = p.a + int64_t(blockIdx.z) * p.sa;
     const int KT = int(p.K) / BK;
 
-    // Direct loads: wave w's round i fills LDS chunks P = (i * 4 + w) * 64 + lane of the tile; chunk P holds
-    // row P / 8 and logical k-chunk (P % 8) ^ (row & 7), so the lane loads that one.
+    // Direct loads: wave w's round i fills LDS chunks P = (i * NW + w) * 64 + lane of the tile; chunk P holds
+    // row P / 8 and logical k-chunk swz_chunk(row, P % 8), so the lane loads that one.
     const uint16_t* ga[RA];
 #pragma unroll
     for (int i = 0; i < RA; ++i) {
-        const int P = (i * 4 + wave) * 64 + lane, row = P >> 3, kc = (P & 7) ^ (row & 7);
+        const int P = (i * NW + wave) * 64 + lane, row = P >> 3, kc = swz_chunk(row, P & 7);
         ga[i] = A + int64_t(min(m0 + row, int(p.M) - 1)) * p.lda + kc * 8;
     }
     const uint16_t* gw[kF8 ? 1 : RW];
@@ -249,13 +303,13 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmP p)
     if constexpr (!kF8) {
 #pragma unroll
         for (int i = 0; i < RW; ++i) {
-            const int P = (i * 4 + wave) * 64 + lane, row = P >> 3, kc = (P & 7) ^ (row & 7);
+            const int P = (i * NW + wave) * 64 + lane, row = P >> 3, kc = swz_chunk(row, P & 7);
             gw[i] = static_cast<const uint16_t*>(p.w) + int64_t(n0 + row) * p.K + kc * 8;
         }
     } else {
 #pragma unroll
         for (int i = 0; i < LW; ++i) {
-            const int c = tid + 256 * i, row = c >> 2, kc = c & 3;
+            const int c = tid + NT * i, row = c >> 2, kc = c & 3;
             gw8[i] = static_cast<const uint8_t*>(p.w) + int64_t(n0 + row) * p.K + kc * 16;
         }
     }
@@ -264,11 +318,11 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmP p)
         const int k0 = kt * BK;
 #pragma unroll
         for (int i = 0; i < RA; ++i)
-            load_lds16(ga[i] + k0, (lds_void*)&sA[buf][(i * 4 + wave) * 64 * 8]);
+            load_lds16(ga[i] + k0, (lds_void*)&sA[buf][(i * NW + wave) * 64 * 8]);
         if constexpr (!kF8) {
 #pragma unroll
             for (int i = 0; i < RW; ++i)
-                load_lds16(gw[i] + k0, (lds_void*)&sW[buf][(i * 4 + wave) * 64 * 8]);
+                load_lds16(gw[i] + k0, (lds_void*)&sW[buf][(i * NW + wave) * 64 * 8]);
         } else {
 #pragma unroll
             for (int i = 0; i < LW; ++i)
@@ -279,7 +333,7 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmP p)
         if constexpr (kF8) {
 #pragma unroll
             for (int i = 0; i < LW; ++i) {
-                const int c = tid + 256 * i, row = c >> 2, kc = c & 3;
+                const int c = tid + NT * i, row = c >> 2, kc = c & 3;
                 u32x4 lo, hi;
                 f8x16_to_bf16(rw[i], lo, hi);
                 *reinterpret_cast<u32x4*>(&sW[buf][swz(row, 2 * kc)]) = lo;
@@ -295,44 +349,75 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmP p)
         for (int j = 0; j < TB; ++j)
             acc[i][j] = f32x16{};
 
+    const int r32 = lane & 31, hk = lane >> 5;
+    auto frags = [&](int buf, int ks, bf16x8 (&wf)[CB], bf16x8 (&af)[TB]) {
+        const int kc = ks * 2 + hk;
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb)
+            wf[cb] = *reinterpret_cast<const bf16x8*>(&sW[buf][swz(wn * (BN / 2) + cb * 32 + r32, kc)]);
+#pragma unroll
+        for (int tb = 0; tb < TB; ++tb)
+            af[tb] = *reinterpret_cast<const bf16x8*>(&sA[buf][swz(wm * WM + tb * 32 + r32, kc)]);
+    };
+    auto mfma = [&](const bf16x8 (&wf)[CB], const bf16x8 (&af)[TB]) {
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+            for (int tb = 0; tb < TB; ++tb)
+                acc[cb][tb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[cb], af[tb], acc[cb][tb], 0, 0, 0);
+    };
+    // Interleave a k step's MFMAs with the LDS reads of the next step's fragments: the reads go out with the first
+    // MFMAs (one each), so the rest of the step covers their latency before its closing wait.
+    auto interleave = [&]() {
+#pragma unroll
+        for (int i = 0; i < CB + TB; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0); // DS read
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); // MFMA
+        }
+        if constexpr (CB * TB > CB + TB)
+            __builtin_amdgcn_sched_group_barrier(0x008, CB * TB - (CB + TB), 0);
+    };
+
+    // Software pipeline: tile t is in LDS buffer t & 1, tile t + 1 lands in the other during tile t's MFMAs, and the
+    // fragments of k step s + 1 are read from LDS while step s's MFMAs run. The loop body has no branches (prefetch
+    // tile indices are clamped; past-the-end prefetches reload the last tile), so the interleave covers all of it.
     issue(0, 0);
     commit_f8(0);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    const int r32 = lane & 31, hk = lane >> 5;
+    issue(min(1, KT - 1), 1);
+    bf16x8 wf0[CB], af0[TB], wf1[CB], af1[TB];
+    frags(0, 0, wf0, af0);
     for (int kt = 0; kt < KT; ++kt) {
         const int buf = kt & 1;
-        if (kt + 1 < KT)
-            issue(kt + 1, buf ^ 1);
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-            bf16x8 wf[CB], af[TB];
-            const int kc = ks * 2 + hk;
-#pragma unroll
-            for (int cb = 0; cb < CB; ++cb)
-                wf[cb] = *reinterpret_cast<const bf16x8*>(&sW[buf][swz(wn * (BN / 2) + cb * 32 + r32, kc)]);
-#pragma unroll
-            for (int tb = 0; tb < TB; ++tb)
-                af[tb] = *reinterpret_cast<const bf16x8*>(&sA[buf][swz(wm * (BM / 2) + tb * 32 + r32, kc)]);
-#pragma unroll
-            for (int cb = 0; cb < CB; ++cb)
-#pragma unroll
-                for (int tb = 0; tb < TB; ++tb)
-                    acc[cb][tb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[cb], af[tb], acc[cb][tb], 0, 0, 0);
-        }
-        if (kt + 1 < KT)
-            commit_f8(buf ^ 1);
+        frags(buf, 1, wf1, af1);
+        mfma(wf0, af0);
+        interleave();
+        frags(buf, 2, wf0, af0);
+        mfma(wf1, af1);
+        interleave();
+        frags(buf, 3, wf1, af1);
+        mfma(wf0, af0);
+        interleave();
+        // tile kt + 1 complete in the other buffer, every wave done reading this one
+        commit_f8(buf ^ 1);
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
+        frags(buf ^ 1, 0, wf0, af0);
+        issue(min(kt + 2, KT - 1), buf);
+        mfma(wf1, af1);
+        interleave();
     }
+    __builtin_amdgcn_s_waitcnt(0); // the last (unused) prefetch must land before the LDS is reused
+    __syncthreads();
 
     // ---- epilogue through LDS: per 32-token block, each wave stages its 32 x WC slice (fp32, padded rows), then
-    // reads it back row-contiguous: two lanes per token, WC/2 channels each ----
-    constexpr int WC = BN / 2, LDW = WC + 4, CW = WC / 2;
-    static_assert(4 * 32 * LDW * 4 <= 2 * (BN + BM) * 64 * 2, "staging does not fit");
+    // reads it back with the lanes along the channels ----
     float* st = reinterpret_cast<float*>(smem) + wave * 32 * LDW;
-    const int rt = lane >> 1, half = lane & 1;
     const int64_t zc = int64_t(blockIdx.z) * p.sc;
+    EpiCh kch{};
+    if constexpr (EK != EK_HEADS)
+        kch = epi_channels(p, n0 + wn * WC + 4 * (lane % (WC / 4)));
 #pragma unroll
     for (int tb = 0; tb < TB; ++tb) {
 #pragma unroll
@@ -342,30 +427,23 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmP p)
                 *reinterpret_cast<f32x4*>(st + r32 * LDW + cb * 32 + 8 * i + 4 * hk) =
                     f32x4{acc[cb][tb][4 * i], acc[cb][tb][4 * i + 1], acc[cb][tb][4 * i + 2], acc[cb][tb][4 * i + 3]};
         __syncthreads();
-        const int tok0 = m0 + wm * (BM / 2) + tb * 32;
-        if constexpr (kHeads) {
+        const int tok0 = m0 + wm * WM + tb * 32;
+        if constexpr (EK == EK_HEADS) {
             epi_heads(p, st, LDW, tok0, n0 + wn * WC, lane);
         } else {
-            const int t = tok0 + rt;
-            if (t < int(p.M)) {
-                const int64_t rowoff = zc + int64_t(t) * p.ldc;
-                const bool alt = (uint32_t(t) % p.seg_rows) < p.split;
-                const int ch0 = n0 + wn * WC + half * CW;
-                for (int j = 0; j < CW; j += 4)
-                    epi_store(p, rowoff, ch0 + j, alt, *reinterpret_cast<const f32x4*>(st + rt * LDW + half * CW + j));
-            }
+            epi_slice<EK, WC>(p, st, LDW, tok0, n0 + wn * WC, lane, zc, kch);
         }
         __syncthreads();
     }
 }
 
-template <int BM, int BN, bool kF8, bool kHeads = false>
+template <int BM, int BN, bool kF8, int EK, int NW = 4>
 hipError_t launch(const GemmP& p, uint32_t batch, hipStream_t s)
 {
     GemmP q = p;
     q.tiles_m = cdiv(p.M, BM);
     q.tiles_n = p.N / BN;
-    gemm_kernel<BM, BN, kF8, kHeads><<<dim3(q.tiles_m * q.tiles_n, 1, batch), 256, 0, s>>>(q);
+    gemm_kernel<BM, BN, kF8, EK, NW><<<dim3(q.tiles_m * q.tiles_n, 1, batch), 64 * NW, 0, s>>>(q);
     return hipGetLastError();
 }
 
@@ -416,25 +494,52 @@ extern "C" mk_status mk_gemm(const mk_gemm_args* a, void* stream)
         return fail(MK_ERR_ARG, "gemm: fp8 weights need per-channel scales");
     const bool f8 = a->w_dtype == MK_FP8_E4M3;
     hipStream_t s = static_cast<hipStream_t>(stream);
+    const int ek = a->epilogue == MK_EPI_HEADS ? EK_HEADS
+                   : a->epilogue == MK_EPI_STORE ? EK_STORE
+                   : (a->epilogue == MK_EPI_GELU_TANH || a->epilogue == MK_EPI_SILU) ? EK_ACT
+                                                                                     : EK_RMW;
+    // tile: 256 x 256 where the grid fills the chip, else 256 x 128, else 256 x 64 (N = 64: stores, residuals)
+    const int bn = ek == EK_HEADS ? 256
+                   : (a->N % 256 == 0 && uint64_t(cdiv(a->M, 256)) * (a->N / 256) * a->batch >= 512) ? 256
+                   : a->N % 128 == 0 ? 128
+                                     : 64;
+    if (bn == 64 && ek == EK_ACT)
+        return fail(MK_ERR_UNSUPPORTED, "gemm: activation epilogues need N a multiple of 128");
     hipError_t e;
-    if (a->epilogue == MK_EPI_HEADS) {
+#define MK_GEMM_EK(BN, EK)                                                                                        \
+    e = f8 ? launch<256, BN, true, EK>(p, a->batch, s) : launch<256, BN, false, EK>(p, a->batch, s)
+    if (ek == EK_HEADS) {
         const mk_heads_args* h = a->heads;
         if (!h || !h->q || !h->k || !h->vt || h->head_dim != 128 || a->N % 256 || (a->N / 3) % 128 ||
-            a->N / 3 != h->heads * 128 || h->rope_mode > 2 || (h->rope_mode && !h->rope) ||
+            a->N / 3 != h->heads * 128 || h->rope_mode > 2 || (h->rope_mode && !h->rope) || h->k_pad % 16 ||
             uint64_t(h->row0) + a->M > h->k_pad || uint64_t(h->q_row0) + a->M > h->q_pad)
             return fail(MK_ERR_ARG, "gemm heads epilogue: needs q, k, vt, head_dim 128, N = 3 * heads * 128 a multiple "
-                                    "of 256, and row0 + M within the padded rows");
+                                    "of 256, k_pad a multiple of 16, and row0 + M within the padded rows");
         p.hp = HeadsP{static_cast<uint16_t*>(h->q), static_cast<uint16_t*>(h->k), static_cast<uint16_t*>(h->vt),
-                      h->heads, h->q_pad, h->k_pad, h->row0, h->q_row0, h->rope_mode, a->N / 3, h->norm_q, h->norm_k, h->rope,
-                      h->eps};
-        e = f8 ? launch<256, 256, true, true>(p, a->batch, s) : launch<256, 256, false, true>(p, a->batch, s);
-    } else if (a->N % 256 == 0 && uint64_t(cdiv(a->M, 256)) * (a->N / 256) * a->batch >= 512) {
-        e = f8 ? launch<256, 256, true>(p, a->batch, s) : launch<256, 256, false>(p, a->batch, s);
-    } else if (a->N % 128 == 0) {
-        e = f8 ? launch<256, 128, true>(p, a->batch, s) : launch<256, 128, false>(p, a->batch, s);
+                      h->heads, h->q_pad, h->k_pad, h->row0, h->q_row0, h->rope_mode, a->N / 3, h->norm_q, h->norm_k,
+                      h->rope, h->eps};
+        MK_GEMM_EK(256, EK_HEADS);
+    } else if (bn == 256) {
+        if (ek == EK_STORE)
+            MK_GEMM_EK(256, EK_STORE);
+        else if (ek == EK_ACT)
+            MK_GEMM_EK(256, EK_ACT);
+        else
+            MK_GEMM_EK(256, EK_RMW);
+    } else if (bn == 128) {
+        if (ek == EK_STORE)
+            MK_GEMM_EK(128, EK_STORE);
+        else if (ek == EK_ACT)
+            MK_GEMM_EK(128, EK_ACT);
+        else
+            MK_GEMM_EK(128, EK_RMW);
     } else {
-        e = f8 ? launch<256, 64, true>(p, a->batch, s) : launch<256, 64, false>(p, a->batch, s);
+        if (ek == EK_STORE)
+            MK_GEMM_EK(64, EK_STORE);
+        else
+            MK_GEMM_EK(64, EK_RMW);
     }
+#undef MK_GEMM_EK
     if (e != hipSuccess)
         return hip_check(e, "gemm launch");
     return MK_OK;

@@ -170,7 +170,7 @@ __global__ __launch_bounds__(256) void gate_add_kernel(float* __restrict__ x, co
         const uint32_t row = uint32_t(i / n), c = uint32_t(i % n);
         float g = gate[((row % seg_rows) < split ? alt : 0) + c];
         if (kTanh)
-            g = tanhf(g);
+            g = tanh_f(g);
         float v;
         if constexpr (sizeof(Y) == 2)
             v = bf2f_bits(y[i]);
@@ -218,7 +218,8 @@ __global__ __launch_bounds__(256) void heads_kernel(const uint16_t* __restrict__
     }
 }
 
-// V^T pack: x bf16 [batch][rows][ld] columns col0 + h*d .. -> out [batch][heads][d][n_pad] at column row0 + r.
+// V^T pack: x bf16 [batch][rows][ld] columns col0 + h*d .. -> out [batch][heads][d][n_pad] at column
+// vt_col(row0 + r).
 // One block per (64 rows, head, batch), transposed through LDS so both sides are coalesced.
 template <int kD>
 __global__ __launch_bounds__(256) void heads_t_kernel(const uint16_t* __restrict__ x, uint32_t rows, int64_t ld,
@@ -243,13 +244,15 @@ __global__ __launch_bounds__(256) void heads_t_kernel(const uint16_t* __restrict
         const uint32_t dd = i / 32, c = (i % 32) * 2;
         if (r0 + c >= rows)
             continue;
-        uint16_t* o = out + ((uint64_t(bi) * heads + h) * kD + dd) * n_pad + row0 + r0 + c;
-        if (r0 + c + 1 < rows && ((row0 + r0 + c) & 1) == 0) {
-            *reinterpret_cast<uint32_t*>(o) = uint32_t(t[c][dd]) | (uint32_t(t[c + 1][dd]) << 16);
+        // keys in the vt_col order; an even key and the next share bits 2 and 3, so they stay adjacent
+        uint16_t* o = out + ((uint64_t(bi) * heads + h) * kD + dd) * n_pad;
+        const uint32_t key = row0 + r0 + c;
+        if (r0 + c + 1 < rows && (key & 1) == 0) {
+            *reinterpret_cast<uint32_t*>(o + vt_col(key)) = uint32_t(t[c][dd]) | (uint32_t(t[c + 1][dd]) << 16);
         } else {
-            o[0] = t[c][dd];
+            o[vt_col(key)] = t[c][dd];
             if (r0 + c + 1 < rows)
-                o[1] = t[c + 1][dd];
+                o[vt_col(key + 1)] = t[c + 1][dd];
         }
     }
 }
@@ -536,6 +539,8 @@ mk_status mk_heads(const void* x, uint32_t batch, uint32_t rows, int64_t ld, int
     if (transpose) {
         if (w || rope_mode)
             return fail(MK_ERR_UNSUPPORTED, "heads: the transposed (V) layout takes no norm or rope");
+        if (n_pad % 16)
+            return fail(MK_ERR_ARG, "heads: the transposed (V) layout needs n_pad a multiple of 16");
         const dim3 grid(cdiv(rows, 64), heads, batch);
         if (d == 128)
             heads_t_kernel<128><<<grid, 256, 0, S(stream)>>>(static_cast<const uint16_t*>(x), rows, ld, stride_x, col0,

@@ -215,6 +215,12 @@ class Event:
 # engine
 # ---------------------------------------------------------------------------------------------------------------
 
+def vt_col(k):
+    """Column of key k in a V^T buffer (MK_VT_COL): bits 2 and 3 of the key swapped within groups of 16."""
+    k = np.asarray(k)
+    return (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1)
+
+
 def bf16_bits(a):
     """float32 -> bf16 bit patterns, round to nearest even (the library's rule)."""
     u = np.ascontiguousarray(a, dtype=np.float32).view(np.uint32).astype(np.uint64)

@@ -160,11 +160,19 @@ def test_gemm_heads_epilogue(gpu, rng, mode, row0, q_row0):
         wq = R.heads_norm_rope(y, H, 128, col0=0, w=nq, cs=tab, rope=mode)
         wk = R.heads_norm_rope(y, H, 128, col0=D, w=nk, cs=tab, rope=mode)
         wv = R.heads_norm_rope(y, H, 128, col0=2 * D)
+        vcols = M.vt_col(np.arange(row0, row0 + Mr))
         for got, want in ((gq[bi][:, q_row0:q_row0 + Mr], wq), (gk[bi][:, row0:row0 + Mr], wk),
-                          (gv[bi][:, :, row0:row0 + Mr].transpose(0, 2, 1), wv)):
+                          (gv[bi][:, :, vcols].transpose(0, 2, 1), wv)):
             assert np.abs(got - want).max() <= 2 ** -8 * np.abs(want).max() + 1e-6
     # rows outside the written range stay zero
     assert not gk[:, :, :row0].any() and not gk[:, :, row0 + Mr:].any()
+
+
+def test_vt_col_is_an_involution_within_groups():
+    k = np.arange(4096)
+    assert np.array_equal(M.vt_col(M.vt_col(k)), k)
+    assert np.array_equal(np.sort(M.vt_col(k[:16])), k[:16])
+    assert list(M.vt_col(np.arange(16))) == [0, 1, 2, 3, 8, 9, 10, 11, 4, 5, 6, 7, 12, 13, 14, 15]
 
 
 def test_gemm_rejects_bad_shapes(gpu):
@@ -191,7 +199,7 @@ def run_attention(q, k, v, scale, q_pos0=0, block=0):
     kp = np.zeros((B, H, k_pad, d), np.float32)
     kp[:, :, :Tk] = k
     vt = np.zeros((B, H, d, k_pad), np.float32)
-    vt[:, :, :, :Tk] = v.transpose(0, 1, 3, 2)
+    vt[:, :, :, M.vt_col(np.arange(Tk))] = v.transpose(0, 1, 3, 2)
     out = M.Dev(B * Tq * H * d * 2)
     M.call("mk_attention", bdev(qp).p, bdev(kp).p, bdev(vt).p, out.p, B, H, d, Tq, q_pad, Tk, k_pad, H * d,
            Tq * H * d, q_pos0, block, scale, None)
@@ -275,7 +283,10 @@ def test_heads(gpu, rng, d, mode, transpose):
     got = fetch_bf16(out, (B, H, d, n_pad) if transpose else (B, H, n_pad, d))
     for bi in range(B):
         want = R.heads_norm_rope(x[bi], H, d, col0=H * d, w=w, cs=cs[row0:] if mode else None, rope=mode)
-        g = got[bi][:, :, row0:row0 + rows].transpose(0, 2, 1) if transpose else got[bi][:, row0:row0 + rows]
+        if transpose:
+            g = got[bi][:, :, M.vt_col(np.arange(row0, row0 + rows))].transpose(0, 2, 1)
+        else:
+            g = got[bi][:, row0:row0 + rows]
         assert np.abs(g - want).max() <= 2 ** -8 * np.abs(want).max() + 1e-6
 
 
