@@ -246,6 +246,24 @@ mk_status mk_step_cfg_device(mk_engine* e, const float* lat, float sigma, float 
 /* The step's stream (kernels are launched on it). */
 mk_status mk_engine_stream(mk_engine* e, void** stream);
 
+/* The noise schedule of Engine::sigmas (engine.cpp:335-365; Schedule defaults engine.hpp:251-254): mu = the fixed
+ * shift when has_mu, else linear in the token count from (base_seq, base_shift) to (max_seq, max_shift). */
+typedef struct mk_schedule {
+    double base_seq, max_seq, base_shift, max_shift, terminal;
+    int has_mu;
+    double mu;
+} mk_schedule;
+/* sigmas of `steps` steps for an image of `tokens` tokens, then 0: out[steps + 1]. t = linspace(1, 1/steps) in float,
+ * sigma = e^mu / (e^mu + 1/t - 1) in double rounded to float, stretched so the last is `terminal` when terminal > 0.
+ * sched NULL: the defaults (256, 4096, 0.5, 1.15, terminal 0, no fixed mu). Host arithmetic only. */
+mk_status mk_sigmas(uint32_t steps, uint32_t tokens, const mk_schedule* sched, float* out);
+/* The Euler flow-matching loop of Engine::generate (engine.cpp:459-506) with the latents resident on the device:
+ * x = noise [h*w][latent] fp32 (host); for i < steps: v = step(x, sigmas[i]) guided as neg + guidance (pos - neg)
+ * (slot 1 the negative prompt; no negative pass when guidance == 1), x += (sigmas[i+1] - sigmas[i]) v; the final
+ * latents are copied to latents_out (host). Slot 0 (and slot 1 when guidance != 1) must have been begun. */
+mk_status mk_generate(mk_engine* e, const float* noise, size_t n, const float* sigmas, uint32_t steps, float guidance,
+                      float* latents_out);
+
 /* Probe of intermediates (the reference's set_probe, tests/image_ref_test.cpp:133-136): called synchronously on the
  * host after a stage with its name ("temb", "modulation", "txt_in", "img_in", "block", "norm_out"), its layer
  * (-1 none), the data copied to host fp32 and its length. NULL turns it off. Slows the step (synchronises). */

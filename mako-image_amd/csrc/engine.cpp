@@ -1025,6 +1025,76 @@ mk_status mk_step_cfg(mk_engine* e, const float* latents, size_t n, float sigma,
     return MK_OK;
 }
 
+mk_status mk_sigmas(uint32_t steps, uint32_t tokens, const mk_schedule* sched, float* out)
+{
+    if (!out)
+        return fail(MK_ERR_ARG, "sigmas: null");
+    const mk_schedule d{256.0, 4096.0, 0.5, 1.15, 0.0, 0, 0.0};
+    const mk_schedule& s = sched ? *sched : d;
+    if (!s.has_mu && s.max_seq == s.base_seq)
+        return fail(MK_ERR_ARG, "sigmas: max_seq == base_seq");
+    // the shift: fixed, or on the line through (base_seq, base_shift) and (max_seq, max_shift)
+    const double slope = s.has_mu ? 0.0 : (s.max_shift - s.base_shift) / (s.max_seq - s.base_seq);
+    const double mu = s.has_mu ? s.mu : double(tokens) * slope + (s.base_shift - slope * s.base_seq);
+    const double em = std::exp(mu);
+    for (uint32_t i = 0; i < steps; ++i) {
+        // t on linspace(1, 1 / steps, steps), held in float as the scheduler holds it
+        const float t = steps == 1 ? 1.0f : float(1.0 + (1.0 / steps - 1.0) * double(i) / double(steps - 1));
+        out[i] = float(em / (em + (1.0 / double(t) - 1.0)));
+    }
+    // stretched so that the last level is the terminal one (nothing to stretch when it is 1)
+    if (s.terminal > 0 && steps > 0 && out[steps - 1] < 1.0f) {
+        const float k = (1.0f - out[steps - 1]) / (1.0f - float(s.terminal));
+        for (uint32_t i = 0; i < steps; ++i)
+            out[i] = 1.0f - (1.0f - out[i]) / k;
+    }
+    out[steps] = 0.0f;
+    return MK_OK;
+}
+
+mk_status mk_generate(mk_engine* e, const float* noise, size_t n, const float* sigmas, uint32_t steps, float guidance,
+                      float* latents_out)
+{
+    if (!e || !noise || !sigmas || !latents_out)
+        return fail(MK_ERR_ARG, "generate: null");
+    if (e->cfg.family != MK_FAMILY_DUAL && e->cfg.family != MK_FAMILY_Q21)
+        return fail(MK_ERR_UNSUPPORTED, "generate: MMDiT families only");
+    const bool guided = guidance != 1.0f;
+    if (!e->slots[0].begun || (guided && !e->slots[1].begun))
+        return fail(MK_ERR_STATE, guided ? "generate: begin both slots first" : "generate: begin slot 0 first");
+    const size_t N = size_t(e->gh) * e->gw, L = e->cfg.latent;
+    if (n != N * L)
+        return fail(MK_ERR_ARG, "latents must be [h * w][" + std::to_string(L) + "]");
+    Buf x[2];
+    MK_TRY(x[0].ensure(n * 4));
+    MK_TRY(x[1].ensure(n * 4));
+    MK_HIP(hipMemcpyAsync(x[0].p, noise, n * 4, hipMemcpyHostToDevice, e->stream));
+    for (uint32_t i = 0; i < steps; ++i) {
+        float* cur = x[i % 2].f();
+        float* nxt = x[(i + 1) % 2].f();
+        const float dt = sigmas[i + 1] - sigmas[i];
+        if (guided) {
+            MK_TRY(mk_step_cfg_device(e, cur, sigmas[i], sigmas[i + 1], guidance, nxt, nullptr));
+        } else {
+            if (e->cfg.family == MK_FAMILY_DUAL) {
+                const uint32_t so[1] = {0};
+                MK_TRY(e->dual_step(cur, sigmas[i], so, 1));
+            } else {
+                MK_TRY(e->q21_step(cur, sigmas[i], 0));
+            }
+            // guidance 1: neg + 1 (pos - neg) with pos = neg is the prompt's own velocity
+            MK_TRY(e->timed("cfg_euler", 0, [&] {
+                return mk_cfg_euler(cur, e->out.f(), e->out.f(), n, 1.0f, dt, nxt, e->stream);
+            }));
+            if (e->timing.on)
+                MK_TRY(e->finish_timing());
+        }
+    }
+    MK_HIP(hipMemcpyAsync(latents_out, x[steps % 2].p, n * 4, hipMemcpyDeviceToHost, e->stream));
+    MK_HIP(hipStreamSynchronize(e->stream));
+    return MK_OK;
+}
+
 mk_status mk_engine_stream(mk_engine* e, void** stream)
 {
     if (!e || !stream)

@@ -44,6 +44,11 @@ class Config(C.Structure):
                                      "weight_dtype", "max_batch")]
 
 
+class Schedule(C.Structure):
+    _fields_ = [("base_seq", _d), ("max_seq", _d), ("base_shift", _d), ("max_shift", _d), ("terminal", _d),
+                ("has_mu", _i), ("mu", _d)]
+
+
 PROBE = C.CFUNCTYPE(None, _vp, C.c_char_p, _i, _fp, _sz)
 
 _SIGS = {
@@ -97,6 +102,8 @@ _SIGS = {
     "mk_step_cfg": (_i, [_vp, _vp, _sz, _f, _f, _f, _vp]),
     "mk_step_cfg_device": (_i, [_vp, _vp, _f, _f, _f, _vp, _vp]),
     "mk_engine_stream": (_i, [_vp, C.POINTER(_vp)]),
+    "mk_sigmas": (_i, [_u32, _u32, C.POINTER(Schedule), _vp]),
+    "mk_generate": (_i, [_vp, _vp, _sz, _vp, _u32, _f, _vp]),
     "mk_engine_set_probe": (_i, [_vp, PROBE, _vp]),
     "mk_engine_set_timing": (_i, [_vp, _i]),
     "mk_engine_timing": (_i, [_vp, _u32, C.POINTER(C.c_char_p), C.POINTER(_f), C.POINTER(_u32), C.POINTER(_d)]),
@@ -284,6 +291,15 @@ class Engine:
     def step_cfg_device(self, lat, sigma, sigma_next, guidance, lat_out, stream=None):
         call("mk_step_cfg_device", self.h, int(lat), sigma, sigma_next, guidance, int(lat_out), stream)
 
+    def generate(self, noise, sigmas, guidance):
+        """The Euler loop over `sigmas` (len steps + 1) from `noise` [h*w][latent]; returns the final latents."""
+        noise = np.ascontiguousarray(noise, dtype=np.float32)
+        sigmas = np.ascontiguousarray(sigmas, dtype=np.float32)
+        out = np.empty_like(noise)
+        call("mk_generate", self.h, noise.ctypes.data, noise.size, sigmas.ctypes.data, sigmas.size - 1, guidance,
+             out.ctypes.data)
+        return out
+
     def stream(self):
         s = _vp()
         call("mk_engine_stream", self.h, C.byref(s))
@@ -318,6 +334,14 @@ class Engine:
 
     def sdxl_forward(self, x_dev, batch, n, y_dev):
         call("mk_sdxl_forward", self.h, int(x_dev), batch, n, int(y_dev), None)
+
+
+def sigmas(steps, tokens, terminal=0.0, mu=None, base_seq=256.0, max_seq=4096.0, base_shift=0.5, max_shift=1.15):
+    """The schedule of Engine::sigmas (engine.cpp:335-365): `steps` noise levels for `tokens` latent tokens, then 0."""
+    sc = Schedule(base_seq, max_seq, base_shift, max_shift, terminal, mu is not None, 0.0 if mu is None else mu)
+    out = np.empty(steps + 1, np.float32)
+    call("mk_sigmas", steps, tokens, C.byref(sc), out.ctypes.data)
+    return out
 
 
 def upload_model(engine, tensors):

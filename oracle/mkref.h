@@ -10,6 +10,14 @@
  *  - attention operands Q, K, V are rounded to bf16; the softmax is fp32;
  *  - norms reduce in double (more exact than any kernel), elementwise math is fp32.
  *
+ * Parity unpinned: the reference's GEMM / attention / heads kernels live in an un-vendored submodule
+ * (external/mako-common, no source or pinned commit in the tree) and the reference holds no vectors for this path,
+ * so these choices are inferred, not pinned to the reference: the GEMM's bf16 rounding of its activation operand;
+ * RoPE mode 2 as interleaved pairs (2i, 2i+1); the causal-prefix rule of attention(block = S); the textbook
+ * gelu_tanh and swiglu forms; the precision of P in P V (fp32 here; a kernel may round it to bf16 within the
+ * tolerance). Everything else is pinned by tests/test_oracle.py and
+ * tests/test_oracle_graph.py (library routines in float64, closed forms, invariants).
+ *
  * Reference files restated (see each function in mkref.cpp for its file:line):
  *   src/image/qwen_image.cpp, src/kernels/image.metal:9-65,450-484, src/image/engine.cpp:335-365,459-506,
  *   src/image/sdxl.cpp:68-87,425-457,672-796.

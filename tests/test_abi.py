@@ -57,3 +57,25 @@ def test_e4m3_codes_match_oracle():
     ref = mkref.e4m3_table()
     ok = ~np.isnan(ref)
     assert np.array_equal(t[ok], ref[ok])
+
+
+def test_sigmas_match_oracle():
+    import numpy as np
+
+    for steps, tokens, terminal in [(40, 4096, 0.0), (1, 256, 0.0), (2, 256, 0.0), (30, 1024, 0.02), (7, 16384, 0.1),
+                                    (1, 4096, 0.05)]:
+        got = mkimage.sigmas(steps, tokens, terminal)
+        want = mkref.sigmas(steps, tokens, terminal=terminal)
+        assert np.array_equal(got, want), (steps, tokens, terminal)
+
+
+def test_sigmas_fixed_shift_and_errors():
+    import numpy as np
+
+    # a fixed mu replaces the size-dependent line: the 2-step schedule is e^mu / (e^mu + 1) at t = 1/2
+    s = mkimage.sigmas(2, 999, mu=1.5)
+    assert s[0] == 1.0 and s[2] == 0.0
+    assert abs(s[1] - np.exp(1.5) / (np.exp(1.5) + 1)) < 1e-7
+    assert np.array_equal(mkimage.sigmas(5, 1, mu=0.7), mkimage.sigmas(5, 123456, mu=0.7))
+    with __import__("pytest").raises(mkimage.MkError, match="max_seq"):
+        mkimage.sigmas(4, 256, base_seq=100.0, max_seq=100.0)

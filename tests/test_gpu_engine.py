@@ -175,3 +175,33 @@ def test_attention_full_size_sampled_rows(gpu):
         qh, kh, vh = (R.bf16_round(a) for a in (qh, kh, vh))
         want = R.attention(np.ascontiguousarray(qh[None, :, rows]), kh[None], vh[None], 1 / np.sqrt(128))
         within(got[b, rows], want[0], 128, cos=0.9999, max_rel=2e-2)
+
+
+def test_generate_guided_equals_the_stepwise_loop(gpu):
+    # the device loop is the host loop of Engine::generate over mk_step_cfg, bit for bit
+    m, e = make_pair(M.FAMILY_DUAL)
+    prompt, lat = inputs(7)
+    for s in (0, 1):
+        e.begin(prompt[s], H_, W_, s)
+    sig = M.sigmas(3, H_ * W_)
+    got = e.generate(lat[0], sig, 4.0)
+    x = lat[0]
+    for i in range(3):
+        x = e.step_cfg(x, sig[i], sig[i + 1], 4.0)
+    assert np.array_equal(got, x)
+
+
+def test_generate_unguided_matches_oracle_euler(gpu):
+    # guidance 1: slot 0 only; two Euler steps against the oracle's velocity at each step
+    m, e = make_pair(M.FAMILY_DUAL)
+    prompt, lat = inputs(8)
+    e.begin(prompt[0], H_, W_, 0)
+    sig = M.sigmas(2, H_ * W_, terminal=0.1)
+    got = e.generate(lat[0], sig, 1.0)
+    x = lat[0].copy()
+    for i in range(2):
+        v = m.dual_step(prompt[:1], x[None], H_, W_, float(sig[i]))[0]
+        x = x + (sig[i + 1] - sig[i]) * v
+    within(got - lat[0], x - lat[0], 64)
+    with pytest.raises(M.MkError, match="begin both"):
+        e.generate(lat[0], sig, 3.0)
