@@ -151,110 +151,149 @@ __device__ inline void epi_slice(const GemmP& p, const float* st, int ld, int to
 }
 
 // The q / k / v epilogue from a wave's staged slice: 32 tokens x 128 channels (one head of q, k or v) in LDS, row
-// stride ld floats, tokens tok0 .. tok0 + 31 (GEMM rows). q, k: two lanes per token, RMSNorm * w over the head (one
-// cross-lane add), RoPE, bf16 rows to [batch][heads][pad][128]; v: each lane two head dims across the 32 tokens, bf16
-// to V^T [batch][heads][128][k_pad] rows.
-__device__ __attribute__((noinline)) void epi_heads(const GemmP& p, const float* st, int ld, int tok0, int nw0, int lane)
+// stride ld floats, tokens tok0 .. tok0 + 31 (GEMM rows).
+//  - q, k: lanes along the head's channels (4 each, 32 lanes a row, rows r0 + 2i for i < 16): per-head RMSNorm * w
+//    (the row's sum of squares reduced across its 32 lanes), RoPE, bf16 rows to [batch][heads][pad][128]. Every
+//    global load (channel constants, RoPE factors) is issued before the first store: vmcnt also counts stores, so a
+//    load behind stores would wait for all of them.
+//  - v: each lane two head dims across the 32 tokens, bf16 to V^T [batch][heads][128][k_pad] rows (keys in the
+//    vt_col order).
+__device__ inline void epi_heads(const GemmP& p, const float* st, int ld, int tok0, int nw0, int lane)
 {
     const HeadsP& h = p.hp;
     const int which = nw0 / int(h.dim), head = (nw0 % int(h.dim)) / 128;
     const int64_t bh = int64_t(blockIdx.z) * h.heads + head;
     if (which == 2) {
-        // V^T rows, keys in the vt_col order (bits 2 and 3 of the key swapped within groups of 16)
+        float sc[2], bi[2];
 #pragma unroll
         for (int dd = 0; dd < 2; ++dd) {
-            const int d = 2 * lane + dd, ch = nw0 + d;
-            const float sc = p.wscale ? p.wscale[ch] : 1.0f, bi = p.bias ? p.bias[ch] : 0.0f;
+            sc[dd] = p.wscale ? p.wscale[nw0 + 2 * lane + dd] : 1.0f;
+            bi[dd] = p.bias ? p.bias[nw0 + 2 * lane + dd] : 0.0f;
+        }
+        const uint32_t k0 = h.row0 + tok0;
+        const bool full = k0 % 16 == 0 && tok0 + 32 <= int(p.M);
+#pragma unroll
+        for (int dd = 0; dd < 2; ++dd) {
+            const int d = 2 * lane + dd;
             uint16_t* dst = h.vt + (bh * 128 + d) * int64_t(h.k_pad);
-            const uint32_t k0 = h.row0 + tok0;
-            if (k0 % 16 == 0 && tok0 + 32 <= int(p.M)) {
+            auto v = [&](int j) { return st[j * ld + d] * sc[dd] + bi[dd]; };
+            if (full) {
 #pragma unroll
                 for (int g = 0; g < 2; ++g) {
                     // physical columns 16g + 0..15 hold keys 16g + {0..3, 8..11, 4..7, 12..15}
-                    auto v = [&](int j) { return st[(16 * g + j) * ld + d] * sc + bi; };
-                    *reinterpret_cast<u32x4*>(dst + k0 + 16 * g) =
-                        u32x4{pack_bf16x2(v(0), v(1)), pack_bf16x2(v(2), v(3)), pack_bf16x2(v(8), v(9)),
-                              pack_bf16x2(v(10), v(11))};
-                    *reinterpret_cast<u32x4*>(dst + k0 + 16 * g + 8) =
-                        u32x4{pack_bf16x2(v(4), v(5)), pack_bf16x2(v(6), v(7)), pack_bf16x2(v(12), v(13)),
-                              pack_bf16x2(v(14), v(15))};
+                    const int j0 = 16 * g;
+                    *reinterpret_cast<u32x4*>(dst + k0 + j0) =
+                        u32x4{pack_bf16x2(v(j0 + 0), v(j0 + 1)), pack_bf16x2(v(j0 + 2), v(j0 + 3)),
+                              pack_bf16x2(v(j0 + 8), v(j0 + 9)), pack_bf16x2(v(j0 + 10), v(j0 + 11))};
+                    *reinterpret_cast<u32x4*>(dst + k0 + j0 + 8) =
+                        u32x4{pack_bf16x2(v(j0 + 4), v(j0 + 5)), pack_bf16x2(v(j0 + 6), v(j0 + 7)),
+                              pack_bf16x2(v(j0 + 12), v(j0 + 13)), pack_bf16x2(v(j0 + 14), v(j0 + 15))};
                 }
             } else {
                 for (int t = 0; t < 32 && tok0 + t < int(p.M); ++t)
-                    dst[vt_col(k0 + t)] = f2bf_bits(st[t * ld + d] * sc + bi);
+                    dst[vt_col(k0 + t)] = f2bf_bits(v(t));
             }
         }
         return;
     }
     const float* nw = which == 0 ? h.norm_q : h.norm_k;
-    const int rt = lane >> 1, half = lane & 1, t = tok0 + rt;
-    const float* row = st + rt * ld;
-    // the lane's 64 channels: half*64 .. +64 (rope mode 0 / 2), or half*32 .. +32 and 64 + half*32 .. +32 (mode 1,
-    // whose pairs (d, d + 64) then sit in one lane)
-    const bool m1 = h.rope_mode == 1;
-    auto load4 = [&](int d) {
-        f32x4 x = *reinterpret_cast<const f32x4*>(row + d);
+    const int c = lane & 31, r0 = lane >> 5, ch = 4 * c;
+    const f32x4 sc = p.wscale ? *reinterpret_cast<const f32x4*>(p.wscale + nw0 + ch) : f32x4{1, 1, 1, 1};
+    const f32x4 bi = p.bias ? *reinterpret_cast<const f32x4*>(p.bias + nw0 + ch) : f32x4{0, 0, 0, 0};
+    const f32x4 wn = nw ? *reinterpret_cast<const f32x4*>(nw + ch) : f32x4{1, 1, 1, 1};
+    const int mode = int(h.rope_mode);
+    const int last = int(p.M) - 1;
+    // RoPE factors of a row (clamped to the last valid row): mode 2, pairs (2c, 2c + 1) -> (cos, sin, cos, sin) of
+    // the lane's 4 channels; mode 1, channel d and d + 64 pair at angle d -> cos / sin of angles 4 (c % 16) .. + 3
+    auto rope_lo = [&](int i) {
+        const int t = min(tok0 + r0 + 2 * i, last);
+        const float* cs = h.rope + (int64_t(h.row0) + t) * 128;
+        return *reinterpret_cast<const f32x4*>(cs + (mode == 2 ? ch : 8 * (c & 15)));
+    };
+    auto rope_hi = [&](int i) {
+        const int t = min(tok0 + r0 + 2 * i, last);
+        return *reinterpret_cast<const f32x4*>(h.rope + (int64_t(h.row0) + t) * 128 + 8 * (c & 15) + 4);
+    };
+    auto val = [&](int i) {
+        f32x4 x = *reinterpret_cast<const f32x4*>(st + (r0 + 2 * i) * ld + ch);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            if (p.wscale)
-                x[j] *= p.wscale[nw0 + d + j];
-            if (p.bias)
-                x[j] += p.bias[nw0 + d + j];
-        }
+        for (int e = 0; e < 4; ++e)
+            x[e] = x[e] * sc[e] + bi[e];
         return x;
     };
-    float inv = 1.0f;
+    // the first half's RoPE factors go out before anything else
+    f32x4 ra[8], rb[8];
+    if (mode)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            ra[i] = rope_lo(i);
+            if (mode == 1)
+                rb[i] = rope_hi(i);
+        }
+    // per-row 1 / rms over the head: partial sums of squares, then a reduce across the row's 32 lanes
+    float inv[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+        inv[i] = 1.0f;
     if (nw) {
-        float ss = 0.0f;
-        for (int i = 0; i < 64; i += 4) {
-            const int d = m1 ? (i < 32 ? half * 32 + i : 32 + half * 32 + i) : half * 64 + i;
-            const f32x4 x = load4(d);
-            ss += x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3];
-        }
-        ss += __shfl_xor(ss, 1, 64);
-        inv = rsqrtf(ss / 128.0f + h.eps);
-    }
-    if (t >= int(p.M))
-        return;
-    auto normed = [&](int d) {
-        f32x4 x = load4(d);
-        if (nw)
+        float ss[16];
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                x[j] *= inv * nw[d + j];
-        return x;
+        for (int i = 0; i < 16; ++i) {
+            const f32x4 x = val(i);
+            ss[i] = x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3];
+        }
+#pragma unroll
+        for (int m = 1; m < 32; m <<= 1)
+#pragma unroll
+            for (int i = 0; i < 16; ++i)
+                ss[i] += __shfl_xor(ss[i], m, 64);
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+            inv[i] = rsqrtf(ss[i] * (1.0f / 128.0f) + h.eps);
+    }
+    const int64_t pad = which == 0 ? h.q_pad : h.k_pad;
+    uint16_t* base = (which == 0 ? h.q : h.k) + (bh * pad + (which == 0 ? h.q_row0 : h.row0)) * 128 + ch;
+    auto emit = [&](int i, const f32x4& r_lo, const f32x4& r_hi) {
+        f32x4 x = val(i);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            x[e] *= inv[i] * wn[e];
+        if (mode == 2) {
+#pragma unroll
+            for (int e = 0; e < 4; e += 2) {
+                const float co = r_lo[e], si = r_lo[e + 1], a = x[e], b = x[e + 1];
+                x[e] = a * co - b * si;
+                x[e + 1] = a * si + b * co;
+            }
+        } else if (mode == 1) {
+            // lanes c and c + 16 hold channels d and d + 64 (d = 4 (c % 16) + e): the partner's value by one swap
+            const bool lo = c < 16;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float other = __shfl_xor(x[e], 16, 64);
+                const float co = e < 2 ? r_lo[2 * e] : r_hi[2 * e - 4];
+                const float si = e < 2 ? r_lo[2 * e + 1] : r_hi[2 * e - 3];
+                x[e] = lo ? x[e] * co - other * si : other * si + x[e] * co;
+            }
+        }
+        const int t = tok0 + r0 + 2 * i;
+        if (t <= last)
+            *reinterpret_cast<u32x2*>(base + int64_t(t) * 128) =
+                u32x2{pack_bf16x2(x[0], x[1]), pack_bf16x2(x[2], x[3])};
     };
-    const float* cs = h.rope_mode ? h.rope + (int64_t(h.row0) + t) * 128 : nullptr;
-    uint16_t* dst = (which == 0 ? h.q : h.k) +
-                    (bh * (which == 0 ? h.q_pad : h.k_pad) + (which == 0 ? h.q_row0 : h.row0) + t) * 128;
-    if (m1) {
-        for (int i = 0; i < 32; i += 4) {
-            const int d = half * 32 + i;
-            f32x4 a = normed(d), b = normed(d + 64);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const float co = cs[2 * (d + j)], si = cs[2 * (d + j) + 1], x = a[j], y = b[j];
-                a[j] = x * co - y * si;
-                b[j] = x * si + y * co;
-            }
-            *reinterpret_cast<u32x2*>(dst + d) = u32x2{pack_bf16x2(a[0], a[1]), pack_bf16x2(a[2], a[3])};
-            *reinterpret_cast<u32x2*>(dst + d + 64) = u32x2{pack_bf16x2(b[0], b[1]), pack_bf16x2(b[2], b[3])};
-        }
-        return;
-    }
-    for (int i = 0; i < 64; i += 4) {
-        const int d = half * 64 + i;
-        f32x4 a = normed(d);
-        if (cs) {
+    for (int i = 0; i < 8; ++i)
+        emit(i, ra[i], rb[i]);
+    if (mode)
 #pragma unroll
-            for (int j = 0; j < 4; j += 2) { // pair (d + j) / 2: (cos, sin) at cs[d + j], cs[d + j + 1]
-                const float co = cs[d + j], si = cs[d + j + 1], x = a[j], y = a[j + 1];
-                a[j] = x * co - y * si;
-                a[j + 1] = x * si + y * co;
-            }
+        for (int i = 0; i < 8; ++i) {
+            ra[i] = rope_lo(8 + i);
+            if (mode == 1)
+                rb[i] = rope_hi(8 + i);
         }
-        *reinterpret_cast<u32x2*>(dst + d) = u32x2{pack_bf16x2(a[0], a[1]), pack_bf16x2(a[2], a[3])};
-    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+        emit(8 + i, ra[i], rb[i]);
 }
 
 template <int BM, int BN, bool kF8, int EK, int NW>
@@ -415,9 +454,30 @@ __global__ __launch_bounds__(64 * NW, 1) __attribute__((amdgpu_waves_per_eu(NW /
     // reads it back with the lanes along the channels ----
     float* st = reinterpret_cast<float*>(smem) + wave * 32 * LDW;
     const int64_t zc = int64_t(blockIdx.z) * p.sc;
-    EpiCh kch{};
-    if constexpr (EK != EK_HEADS)
-        kch = epi_channels(p, n0 + wn * WC + 4 * (lane % (WC / 4)));
+    if constexpr (EK == EK_HEADS) {
+        // the heads epilogue is large: one copy of it in a rolled loop over the 32-token blocks, which always
+        // stages block 0 of the accumulators and then rotates the next block into its place (static register
+        // indices, so the accumulators stay in registers)
+#pragma unroll 1
+        for (int tb = 0; tb < TB; ++tb) {
+#pragma unroll
+            for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    *reinterpret_cast<f32x4*>(st + r32 * LDW + cb * 32 + 8 * i + 4 * hk) =
+                        f32x4{acc[cb][0][4 * i], acc[cb][0][4 * i + 1], acc[cb][0][4 * i + 2], acc[cb][0][4 * i + 3]};
+            __syncthreads();
+            epi_heads(p, st, LDW, m0 + wm * WM + tb * 32, n0 + wn * WC, lane);
+            __syncthreads();
+#pragma unroll
+            for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+                for (int t = 0; t + 1 < TB; ++t)
+                    acc[cb][t] = acc[cb][t + 1];
+        }
+        return;
+    }
+    EpiCh kch = epi_channels(p, n0 + wn * WC + 4 * (lane % (WC / 4)));
 #pragma unroll
     for (int tb = 0; tb < TB; ++tb) {
 #pragma unroll
@@ -427,12 +487,7 @@ __global__ __launch_bounds__(64 * NW, 1) __attribute__((amdgpu_waves_per_eu(NW /
                 *reinterpret_cast<f32x4*>(st + r32 * LDW + cb * 32 + 8 * i + 4 * hk) =
                     f32x4{acc[cb][tb][4 * i], acc[cb][tb][4 * i + 1], acc[cb][tb][4 * i + 2], acc[cb][tb][4 * i + 3]};
         __syncthreads();
-        const int tok0 = m0 + wm * WM + tb * 32;
-        if constexpr (EK == EK_HEADS) {
-            epi_heads(p, st, LDW, tok0, n0 + wn * WC, lane);
-        } else {
-            epi_slice<EK, WC>(p, st, LDW, tok0, n0 + wn * WC, lane, zc, kch);
-        }
+        epi_slice<EK, WC>(p, st, LDW, m0 + wm * WM + tb * 32, n0 + wn * WC, lane, zc, kch);
         __syncthreads();
     }
 }
