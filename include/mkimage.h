@@ -115,6 +115,11 @@ typedef struct mk_gemm_args {
 /* proj (the reference's GEMM, engine.cpp:768 / qwen_image.cpp:196-288): C = A W^T with the fused epilogue.
  * K % 64 == 0, N % 64 == 0. */
 mk_status mk_gemm(const mk_gemm_args* a, void* stream);
+/* count (1 or 2) GEMMs of equal N, K, weight dtype and epilogue kind in one launch: the dual-stream blocks' image and
+ * text projections, whose separate launches would leave most of the chip idle on the text's few tiles. Each problem
+ * keeps its own A, W, C, bias, gate, M, batch, strides and heads arguments. No counterpart in the reference (its 2.1
+ * graph has one stream). */
+mk_status mk_gemm_grouped(const mk_gemm_args* a, uint32_t count, void* stream);
 
 /* GEMV for a few rows (the time embedding and modulation projections, rows <= 4):
  * y[r][n] = sum_k W[n][k] bf16(x'[r][k]) + b[n] with x' = silu(x) when silu_x (silu(temb) is the modulation

@@ -337,6 +337,21 @@ struct mk_engine {
                    int64_t gate_alt = 0, uint32_t split = 0, uint32_t seg = 0, const mk_heads_args* heads = nullptr,
                    const char* cls = "gemm")
     {
+        const mk_gemm_args g = gemm_args(L, A, lda, sa, M, batch, C, ldc, sc, epi, cdt, gate, gate_alt, split, seg,
+                                         heads);
+        return timed(cls, 2.0 * M * L.out * L.in * batch, [&] { return mk_gemm(&g, stream); });
+    }
+    // Two GEMMs of equal N, K and epilogue kind (a block's image and text projections) in one launch.
+    mk_status gemm2(const mk_gemm_args (&g)[2])
+    {
+        const double fl = 2.0 * g[0].N * g[0].K * (double(g[0].M) * g[0].batch + double(g[1].M) * g[1].batch);
+        return timed("gemm", fl, [&] { return mk_gemm_grouped(g, 2, stream); });
+    }
+    static mk_gemm_args gemm_args(const Linear& L, const void* A, int64_t lda, int64_t sa, uint32_t M, uint32_t batch,
+                                  void* C, int64_t ldc, int64_t sc, uint32_t epi, uint32_t cdt,
+                                  const float* gate = nullptr, int64_t gate_alt = 0, uint32_t split = 0,
+                                  uint32_t seg = 0, const mk_heads_args* heads = nullptr)
+    {
         mk_gemm_args g{};
         g.a = A;
         g.w = L.w;
@@ -359,7 +374,7 @@ struct mk_engine {
         g.c_dtype = cdt;
         g.epilogue = epi;
         g.heads = heads;
-        return timed(cls, 2.0 * M * L.out * L.in * batch, [&] { return mk_gemm(&g, stream); });
+        return g;
     }
 
     mk_status probe_f32(const char* name, int layer, const float* d, size_t n)
@@ -447,7 +462,7 @@ struct mk_engine {
         MK_TRY(k.ensure(size_t(nb) * H * k_pad * 128 * 2));
         MK_TRY(vt.ensure(size_t(nb) * H * 128 * k_pad * 2));
         MK_TRY(att.ensure(size_t(nb) * T * D * 2));
-        MK_TRY(hid.ensure(size_t(nb) * std::max(N, S) * F * 2));
+        MK_TRY(hid.ensure(size_t(nb) * (N + S) * F * 2)); // image rows, then text rows
         MK_TRY(out.ensure(size_t(nb) * N * L * 4));
         MK_TRY(lat_bf.ensure(size_t(nb) * N * L * 2));
         MK_TRY(tn.ensure(size_t(nb) * S * E * 2));
@@ -495,45 +510,60 @@ struct mk_engine {
                 Buf *x, *xn;
                 uint32_t rows, row0, which;
                 const float* m;
-            } st[2] = {{&x_img, &xn_img, N, S, 0, mi}, {&x_txt, &xn_txt, S, 0, 1, mt}};
-            for (const St& s : st) {
+                uint16_t* hid;
+            } st[2] = {{&x_img, &xn_img, N, S, 0, mi, hid.h()}, {&x_txt, &xn_txt, S, 0, 1, mt, hid.h() + size_t(nb) * N * F}};
+            mk_heads_args ha[2];
+            mk_gemm_args g[2];
+            for (int j = 0; j < 2; ++j) {
+                const St& s = st[j];
                 MK_TRY(timed("ln_modulate", 0, [&] {
                     return mk_ln_modulate(s.x->f(), nb * s.rows, D, s.m + D, s.m, 0, 0, 1, eps, s.xn->p, stream);
                 }));
-                mk_heads_args ha{};
-                ha.q = q.p;
-                ha.k = k.p;
-                ha.vt = vt.p;
-                ha.heads = H;
-                ha.head_dim = 128;
-                ha.q_pad = q_pad;
-                ha.k_pad = k_pad;
-                ha.row0 = s.row0;
-                ha.q_row0 = s.row0;
-                ha.norm_q = B.nq[s.which];
-                ha.norm_k = B.nk[s.which];
-                ha.rope = rope.f();
-                ha.rope_mode = 2;
-                ha.eps = eps;
-                MK_TRY(gemm(B.qkv[s.which], s.xn->p, D, int64_t(s.rows) * D, s.rows, nb, nullptr, 0, 0, MK_EPI_HEADS,
-                            MK_BF16, nullptr, 0, 0, 0, &ha));
+                ha[j] = mk_heads_args{};
+                ha[j].q = q.p;
+                ha[j].k = k.p;
+                ha[j].vt = vt.p;
+                ha[j].heads = H;
+                ha[j].head_dim = 128;
+                ha[j].q_pad = q_pad;
+                ha[j].k_pad = k_pad;
+                ha[j].row0 = s.row0;
+                ha[j].q_row0 = s.row0;
+                ha[j].norm_q = B.nq[s.which];
+                ha[j].norm_k = B.nk[s.which];
+                ha[j].rope = rope.f();
+                ha[j].rope_mode = 2;
+                ha[j].eps = eps;
+                g[j] = gemm_args(B.qkv[s.which], s.xn->p, D, int64_t(s.rows) * D, s.rows, nb, nullptr, 0, 0,
+                                 MK_EPI_HEADS, MK_BF16, nullptr, 0, 0, 0, &ha[j]);
             }
+            MK_TRY(gemm2(g));
             MK_TRY(timed("attention", attn_flops, [&] {
                 return mk_attention(q.p, k.p, vt.p, att.p, nb, H, 128, T, q_pad, T, k_pad, D, int64_t(T) * D, 0, 0,
                                     1.0f / std::sqrt(128.0f), stream);
             }));
-            for (const St& s : st) {
+            for (int j = 0; j < 2; ++j) {
+                const St& s = st[j];
                 const uint16_t* a = att.h() + size_t(s.row0) * D; // image rows after the text's
-                MK_TRY(gemm(B.o[s.which], a, D, int64_t(T) * D, s.rows, nb, s.x->p, D, int64_t(s.rows) * D,
-                            MK_EPI_GATE_ADD, MK_F32, s.m + 2 * D));
+                g[j] = gemm_args(B.o[s.which], a, D, int64_t(T) * D, s.rows, nb, s.x->p, D, int64_t(s.rows) * D,
+                                 MK_EPI_GATE_ADD, MK_F32, s.m + 2 * D);
+            }
+            MK_TRY(gemm2(g));
+            for (int j = 0; j < 2; ++j) {
+                const St& s = st[j];
                 MK_TRY(timed("ln_modulate", 0, [&] {
                     return mk_ln_modulate(s.x->f(), nb * s.rows, D, s.m + 4 * D, s.m + 3 * D, 0, 0, 1, eps, s.xn->p,
                                           stream);
                 }));
-                MK_TRY(gemm(B.ff1[s.which], s.xn->p, D, 0, nb * s.rows, 1, hid.p, F, 0, MK_EPI_GELU_TANH, MK_BF16));
-                MK_TRY(gemm(B.ff2[s.which], hid.p, F, 0, nb * s.rows, 1, s.x->p, D, 0, MK_EPI_GATE_ADD, MK_F32,
-                            s.m + 5 * D));
+                g[j] = gemm_args(B.ff1[s.which], s.xn->p, D, 0, nb * s.rows, 1, s.hid, F, 0, MK_EPI_GELU_TANH, MK_BF16);
             }
+            MK_TRY(gemm2(g));
+            for (int j = 0; j < 2; ++j) {
+                const St& s = st[j];
+                g[j] = gemm_args(B.ff2[s.which], s.hid, F, 0, nb * s.rows, 1, s.x->p, D, 0, MK_EPI_GATE_ADD, MK_F32,
+                                 s.m + 5 * D);
+            }
+            MK_TRY(gemm2(g));
             if (probe)
                 for (uint32_t b = 0; b < nb; ++b)
                     MK_TRY(probe_f32("block", int(i * nb + b), x_img.f() + size_t(b) * N * D, size_t(N) * D));

@@ -34,8 +34,15 @@ struct GemmP {
     uint32_t split, seg_rows, M, N, K;
     int64_t lda, ldc, sa, sc;
     uint32_t epi, c_bf16;
-    uint32_t tiles_m, tiles_n;
+    uint32_t tiles_m, tiles_n, batch;
     HeadsP hp;
+};
+
+// One launch of up to two GEMMs of equal N, K and epilogue kind (the dual-stream blocks' image and text
+// projections): workgroups [0, tiles0 * ...) take problem 0, the rest problem 1 (grid z = the larger batch).
+struct GemmG {
+    GemmP g[2];
+    uint32_t tiles0;
 };
 
 constexpr int BK = 64;
@@ -107,24 +114,30 @@ __device__ inline void epi_slice(const GemmP& p, const float* st, int ld, int to
             v[i][e] = v[i][e] * k.scale[e] + k.bias[e];
     }
     if constexpr (EK == EK_RMW) {
+        // rows past M read (and leave) the last valid row
+        float* c = static_cast<float*>(p.c) + zc + ch;
         f32x4 x[NI];
 #pragma unroll
-        for (int i = 0; i < NI; ++i) {
-            const int t = tok0 + r0 + RPI * i;
-            if (t < int(p.M))
-                x[i] = *reinterpret_cast<const f32x4*>(static_cast<float*>(p.c) + zc + int64_t(t) * p.ldc + ch);
-        }
+        for (int i = 0; i < NI; ++i)
+            x[i] = *reinterpret_cast<const f32x4*>(c + int64_t(min(tok0 + r0 + RPI * i, int(p.M) - 1)) * p.ldc);
         const bool add = p.epi == MK_EPI_ADD;
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
             const int t = tok0 + r0 + RPI * i;
-            if (t < int(p.M)) {
-                const f32x4& g = (uint32_t(t) % p.seg_rows) < p.split ? k.g1 : k.g0;
+            const f32x4& g = (uint32_t(t) % p.seg_rows) < p.split ? k.g1 : k.g0;
 #pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    x[i][e] += (add ? 1.0f : g[e]) * v[i][e];
-                *reinterpret_cast<f32x4*>(static_cast<float*>(p.c) + zc + int64_t(t) * p.ldc + ch) = x[i];
-            }
+            for (int e = 0; e < 4; ++e)
+                x[i][e] += (add ? 1.0f : g[e]) * v[i][e];
+        }
+        const int64_t step = int64_t(RPI) * p.ldc;
+        float* c0 = c + int64_t(tok0 + r0) * p.ldc;
+        if (tok0 + 32 <= int(p.M)) {
+#pragma unroll
+            for (int i = 0; i < NI; ++i)
+                *reinterpret_cast<f32x4*>(c0 + i * step) = x[i];
+        } else {
+            for (int i = 0; i < NI && tok0 + r0 + RPI * i < int(p.M); ++i)
+                *reinterpret_cast<f32x4*>(c0 + i * step) = x[i];
         }
         return;
     }
@@ -136,17 +149,34 @@ __device__ inline void epi_slice(const GemmP& p, const float* st, int ld, int to
             for (int e = 0; e < 4; ++e)
                 v[i][e] = gelu ? gelu_tanh_f(v[i][e]) : silu_f(v[i][e]);
     }
+    // the stores: straight-line when the slice is whole (row-guard branches between stores make the compiler wait
+    // for each store before the next)
+    const bool whole = tok0 + 32 <= int(p.M);
+    const int64_t off0 = zc + int64_t(tok0 + r0) * p.ldc + ch, step = int64_t(RPI) * p.ldc;
+    if (p.c_bf16) {
+        u32x2 o[NI];
 #pragma unroll
-    for (int i = 0; i < NI; ++i) {
-        const int t = tok0 + r0 + RPI * i;
-        if (t >= int(p.M))
-            continue;
-        const int64_t off = zc + int64_t(t) * p.ldc + ch;
-        if (p.c_bf16)
-            *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(p.c) + off) =
-                u32x2{pack_bf16x2(v[i][0], v[i][1]), pack_bf16x2(v[i][2], v[i][3])};
-        else
-            *reinterpret_cast<f32x4*>(static_cast<float*>(p.c) + off) = v[i];
+        for (int i = 0; i < NI; ++i)
+            o[i] = u32x2{pack_bf16x2(v[i][0], v[i][1]), pack_bf16x2(v[i][2], v[i][3])};
+        uint16_t* c = static_cast<uint16_t*>(p.c) + off0;
+        if (whole) {
+#pragma unroll
+            for (int i = 0; i < NI; ++i)
+                *reinterpret_cast<u32x2*>(c + i * step) = o[i];
+        } else {
+            for (int i = 0; i < NI && tok0 + r0 + RPI * i < int(p.M); ++i)
+                *reinterpret_cast<u32x2*>(c + i * step) = o[i];
+        }
+    } else {
+        float* c = static_cast<float*>(p.c) + off0;
+        if (whole) {
+#pragma unroll
+            for (int i = 0; i < NI; ++i)
+                *reinterpret_cast<f32x4*>(c + i * step) = v[i];
+        } else {
+            for (int i = 0; i < NI && tok0 + r0 + RPI * i < int(p.M); ++i)
+                *reinterpret_cast<f32x4*>(c + i * step) = v[i];
+        }
     }
 }
 
@@ -297,8 +327,12 @@ __device__ inline void epi_heads(const GemmP& p, const float* st, int ld, int to
 }
 
 template <int BM, int BN, bool kF8, int EK, int NW>
-__global__ __launch_bounds__(64 * NW, 1) __attribute__((amdgpu_waves_per_eu(NW / 4, NW / 4))) void gemm_kernel(GemmP p)
+__global__ __launch_bounds__(64 * NW, 1) __attribute__((amdgpu_waves_per_eu(NW / 4, NW / 4))) void gemm_kernel(GemmG G)
 {
+    const bool second = blockIdx.x >= G.tiles0;
+    const GemmP& p = G.g[second];
+    if (blockIdx.z >= p.batch)
+        return;
     constexpr int NT = 64 * NW;                 // threads
     constexpr int WM = BM / (NW / 2);           // tokens per wave (waves: 2 along channels x NW/2 along tokens)
     constexpr int TB = WM / 32, CB = BN / 64;   // 32-row MFMA blocks per wave along tokens / channels
@@ -317,7 +351,7 @@ __global__ __launch_bounds__(64 * NW, 1) __attribute__((amdgpu_waves_per_eu(NW /
     // Tile of this workgroup: XCD-aware (round-robin dispatch puts workgroup i on XCD i % 8; give each XCD a
     // contiguous run of tiles), then grouped 8 m-tiles at a time so a run shares weight columns.
     const uint32_t total = p.tiles_m * p.tiles_n;
-    uint32_t pid = blockIdx.x;
+    uint32_t pid = second ? blockIdx.x - G.tiles0 : blockIdx.x;
     if (total % 8 == 0)
         pid = (pid % 8) * (total / 8) + pid / 8;
     const uint32_t GM = 8, in_group = GM * p.tiles_n;
@@ -406,12 +440,13 @@ __global__ __launch_bounds__(64 * NW, 1) __attribute__((amdgpu_waves_per_eu(NW /
                 acc[cb][tb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[cb], af[tb], acc[cb][tb], 0, 0, 0);
     };
     // Interleave a k step's MFMAs with the LDS reads of the next step's fragments: the reads go out with the first
-    // MFMAs (one each), so the rest of the step covers their latency before its closing wait.
+    // MFMAs (one after each), so the rest of the step covers their latency. The step's first MFMA goes before any
+    // new read: its operands' wait (lgkmcnt) then has no fresh read to wait for.
     auto interleave = [&]() {
 #pragma unroll
         for (int i = 0; i < CB + TB; ++i) {
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0); // DS read
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0); // DS read
         }
         if constexpr (CB * TB > CB + TB)
             __builtin_amdgcn_sched_group_barrier(0x008, CB * TB - (CB + TB), 0);
@@ -450,8 +485,10 @@ __global__ __launch_bounds__(64 * NW, 1) __attribute__((amdgpu_waves_per_eu(NW /
     __builtin_amdgcn_s_waitcnt(0); // the last (unused) prefetch must land before the LDS is reused
     __syncthreads();
 
-    // ---- epilogue through LDS: per 32-token block, each wave stages its 32 x WC slice (fp32, padded rows), then
-    // reads it back with the lanes along the channels ----
+    // ---- epilogue through LDS: per 32-token block, each wave stages its 32 x WC slice (fp32, padded rows) in a
+    // region of its own, then reads it back with the lanes along the channels. A wave's LDS operations complete in
+    // order, so the slices need no barrier (a __syncthreads() here would also wait for every global store in flight:
+    // its release fence waits for vmcnt 0) ----
     float* st = reinterpret_cast<float*>(smem) + wave * 32 * LDW;
     const int64_t zc = int64_t(blockIdx.z) * p.sc;
     if constexpr (EK == EK_HEADS) {
@@ -466,9 +503,7 @@ __global__ __launch_bounds__(64 * NW, 1) __attribute__((amdgpu_waves_per_eu(NW /
                 for (int i = 0; i < 4; ++i)
                     *reinterpret_cast<f32x4*>(st + r32 * LDW + cb * 32 + 8 * i + 4 * hk) =
                         f32x4{acc[cb][0][4 * i], acc[cb][0][4 * i + 1], acc[cb][0][4 * i + 2], acc[cb][0][4 * i + 3]};
-            __syncthreads();
             epi_heads(p, st, LDW, m0 + wm * WM + tb * 32, n0 + wn * WC, lane);
-            __syncthreads();
 #pragma unroll
             for (int cb = 0; cb < CB; ++cb)
 #pragma unroll
@@ -486,29 +521,38 @@ __global__ __launch_bounds__(64 * NW, 1) __attribute__((amdgpu_waves_per_eu(NW /
             for (int i = 0; i < 4; ++i)
                 *reinterpret_cast<f32x4*>(st + r32 * LDW + cb * 32 + 8 * i + 4 * hk) =
                     f32x4{acc[cb][tb][4 * i], acc[cb][tb][4 * i + 1], acc[cb][tb][4 * i + 2], acc[cb][tb][4 * i + 3]};
-        __syncthreads();
         epi_slice<EK, WC>(p, st, LDW, m0 + wm * WM + tb * 32, n0 + wn * WC, lane, zc, kch);
-        __syncthreads();
     }
 }
 
 template <int BM, int BN, bool kF8, int EK, int NW = 4>
-hipError_t launch(const GemmP& p, uint32_t batch, hipStream_t s)
+hipError_t launch(GemmP* p, uint32_t count, hipStream_t s)
 {
-    GemmP q = p;
-    q.tiles_m = cdiv(p.M, BM);
-    q.tiles_n = p.N / BN;
-    gemm_kernel<BM, BN, kF8, EK, NW><<<dim3(q.tiles_m * q.tiles_n, 1, batch), 64 * NW, 0, s>>>(q);
+    GemmG G{};
+    uint32_t tiles = 0, batch = 0;
+    for (uint32_t i = 0; i < count; ++i) {
+        p[i].tiles_m = cdiv(p[i].M, BM);
+        p[i].tiles_n = p[i].N / BN;
+        G.g[i] = p[i];
+        tiles += p[i].tiles_m * p[i].tiles_n;
+        batch = max(batch, p[i].batch);
+    }
+    G.tiles0 = count > 1 ? p[0].tiles_m * p[0].tiles_n : tiles;
+    gemm_kernel<BM, BN, kF8, EK, NW><<<dim3(tiles, 1, batch), 64 * NW, 0, s>>>(G);
     return hipGetLastError();
 }
 
-} // namespace gemm_detail
-} // namespace mk
+// The epilogue kind of an mk_epilogue.
+int epi_kind(uint32_t e)
+{
+    return e == MK_EPI_HEADS ? EK_HEADS
+           : e == MK_EPI_STORE ? EK_STORE
+           : (e == MK_EPI_GELU_TANH || e == MK_EPI_SILU) ? EK_ACT
+                                                         : EK_RMW;
+}
 
-using namespace mk;
-using namespace mk::gemm_detail;
-
-extern "C" mk_status mk_gemm(const mk_gemm_args* a, void* stream)
+// Checks one problem's arguments and fills its kernel parameters.
+mk_status prepare(const mk_gemm_args* a, GemmP& p)
 {
     if (!a || !a->a || !a->w || (!a->c && a->epilogue != MK_EPI_HEADS))
         return fail(MK_ERR_ARG, "gemm: null argument");
@@ -524,9 +568,9 @@ extern "C" mk_status mk_gemm(const mk_gemm_args* a, void* stream)
     const bool gated = a->epilogue == MK_EPI_GATE_ADD || a->epilogue == MK_EPI_GATE_TANH;
     if (gated && !a->gate)
         return fail(MK_ERR_ARG, "gemm: gated epilogue without a gate");
-    if (a->M == 0 || a->batch == 0)
-        return MK_OK;
-    GemmP p{};
+    if (a->w_dtype == MK_FP8_E4M3 && !a->wscale)
+        return fail(MK_ERR_ARG, "gemm: fp8 weights need per-channel scales");
+    p = GemmP{};
     p.a = static_cast<const uint16_t*>(a->a);
     p.w = a->w;
     p.wscale = a->wscale;
@@ -545,25 +589,8 @@ extern "C" mk_status mk_gemm(const mk_gemm_args* a, void* stream)
     p.sc = a->stride_c;
     p.epi = a->epilogue;
     p.c_bf16 = a->c_dtype == MK_BF16;
-    if (a->w_dtype == MK_FP8_E4M3 && !a->wscale)
-        return fail(MK_ERR_ARG, "gemm: fp8 weights need per-channel scales");
-    const bool f8 = a->w_dtype == MK_FP8_E4M3;
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    const int ek = a->epilogue == MK_EPI_HEADS ? EK_HEADS
-                   : a->epilogue == MK_EPI_STORE ? EK_STORE
-                   : (a->epilogue == MK_EPI_GELU_TANH || a->epilogue == MK_EPI_SILU) ? EK_ACT
-                                                                                     : EK_RMW;
-    // tile: 256 x 256 where the grid fills the chip, else 256 x 128, else 256 x 64 (N = 64: stores, residuals)
-    const int bn = ek == EK_HEADS ? 256
-                   : (a->N % 256 == 0 && uint64_t(cdiv(a->M, 256)) * (a->N / 256) * a->batch >= 512) ? 256
-                   : a->N % 128 == 0 ? 128
-                                     : 64;
-    if (bn == 64 && ek == EK_ACT)
-        return fail(MK_ERR_UNSUPPORTED, "gemm: activation epilogues need N a multiple of 128");
-    hipError_t e;
-#define MK_GEMM_EK(BN, EK)                                                                                        \
-    e = f8 ? launch<256, BN, true, EK>(p, a->batch, s) : launch<256, BN, false, EK>(p, a->batch, s)
-    if (ek == EK_HEADS) {
+    p.batch = a->batch;
+    if (a->epilogue == MK_EPI_HEADS) {
         const mk_heads_args* h = a->heads;
         if (!h || !h->q || !h->k || !h->vt || h->head_dim != 128 || a->N % 256 || (a->N / 3) % 128 ||
             a->N / 3 != h->heads * 128 || h->rope_mode > 2 || (h->rope_mode && !h->rope) || h->k_pad % 16 ||
@@ -573,6 +600,49 @@ extern "C" mk_status mk_gemm(const mk_gemm_args* a, void* stream)
         p.hp = HeadsP{static_cast<uint16_t*>(h->q), static_cast<uint16_t*>(h->k), static_cast<uint16_t*>(h->vt),
                       h->heads, h->q_pad, h->k_pad, h->row0, h->q_row0, h->rope_mode, a->N / 3, h->norm_q, h->norm_k,
                       h->rope, h->eps};
+    }
+    return MK_OK;
+}
+
+} // namespace gemm_detail
+} // namespace mk
+
+using namespace mk;
+using namespace mk::gemm_detail;
+
+extern "C" mk_status mk_gemm_grouped(const mk_gemm_args* a, uint32_t count, void* stream)
+{
+    if (!a)
+        return fail(MK_ERR_ARG, "gemm: null argument");
+    if (count == 0 || count > 2)
+        return fail(MK_ERR_ARG, "gemm: 1 or 2 problems a launch");
+    GemmP p[2];
+    uint32_t n = 0;
+    for (uint32_t i = 0; i < count; ++i) {
+        const mk_status st = prepare(&a[i], p[n]);
+        if (st != MK_OK)
+            return st;
+        if (i > 0 && (a[i].N != a[0].N || a[i].K != a[0].K || a[i].w_dtype != a[0].w_dtype ||
+                      epi_kind(a[i].epilogue) != epi_kind(a[0].epilogue)))
+            return fail(MK_ERR_ARG, "gemm: grouped problems need equal N, K, weight dtype and epilogue kind");
+        if (a[i].M && a[i].batch)
+            ++n; // empty problems drop out
+    }
+    if (n == 0)
+        return MK_OK;
+    const bool f8 = a[0].w_dtype == MK_FP8_E4M3;
+    const int ek = epi_kind(a[0].epilogue);
+    uint64_t tiles256 = 0;
+    for (uint32_t i = 0; i < n; ++i)
+        tiles256 += uint64_t(cdiv(p[i].M, 256)) * p[i].batch * (a[0].N / 256);
+    // tile: 256 x 256 where the grid fills the chip, else 256 x 128, else 256 x 64 (N = 64: stores, residuals)
+    const int bn = ek == EK_HEADS ? 256 : (a[0].N % 256 == 0 && tiles256 >= 512) ? 256 : a[0].N % 128 == 0 ? 128 : 64;
+    if (bn == 64 && ek == EK_ACT)
+        return fail(MK_ERR_UNSUPPORTED, "gemm: activation epilogues need N a multiple of 128");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipError_t e;
+#define MK_GEMM_EK(BN, EK) e = f8 ? launch<256, BN, true, EK>(p, n, s) : launch<256, BN, false, EK>(p, n, s)
+    if (ek == EK_HEADS) {
         MK_GEMM_EK(256, EK_HEADS);
     } else if (bn == 256) {
         if (ek == EK_STORE)
@@ -599,3 +669,5 @@ extern "C" mk_status mk_gemm(const mk_gemm_args* a, void* stream)
         return hip_check(e, "gemm launch");
     return MK_OK;
 }
+
+extern "C" mk_status mk_gemm(const mk_gemm_args* a, void* stream) { return mk_gemm_grouped(a, 1, stream); }

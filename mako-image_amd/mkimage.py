@@ -71,6 +71,7 @@ _SIGS = {
     "mk_event_record": (_i, [_vp, _vp]),
     "mk_event_elapsed_ms": (_i, [_vp, _vp, C.POINTER(_f)]),
     "mk_gemm": (_i, [C.POINTER(GemmArgs), _vp]),
+    "mk_gemm_grouped": (_i, [_vp, _u32, _vp]),
     "mk_gemv": (_i, [_vp, _u32, _u32, _vp, _vp, _u32, _vp, _i, _vp]),
     "mk_ln_modulate": (_i, [_vp, _u32, _u32, _vp, _vp, _i64, _u32, _u32, _f, _vp, _vp]),
     "mk_gate_add": (_i, [_vp, _vp, _u32, _u32, _u32, _vp, _i64, _u32, _u32, _i, _vp]),

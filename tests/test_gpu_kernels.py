@@ -48,8 +48,13 @@ def maxrel(got, want):
     return float(np.abs(got - want).max() / max(np.abs(want).max(), 1e-30))
 
 
-def gemm(A, W, *, bias=None, wscale=None, epi=M.EPI_STORE, c=None, c_dtype=M.F32, M_=None, batch=1, lda=None,
-         ldc=0, sa=0, sc=0, gate=None, gate_alt=0, split=0, seg=0, w_dtype=M.BF16, heads=None, a_off=0):
+def gemm(A, W, **kw):
+    M.call("mk_gemm", C.byref(gemm_args(A, W, **kw)), None)
+    M.sync()
+
+
+def gemm_args(A, W, *, bias=None, wscale=None, epi=M.EPI_STORE, c=None, c_dtype=M.F32, M_=None, batch=1, lda=None,
+              ldc=0, sa=0, sc=0, gate=None, gate_alt=0, split=0, seg=0, w_dtype=M.BF16, heads=None, a_off=0):
     g = M.GemmArgs()
     g.a, g.w = A.p + a_off, W.p
     g.wscale = wscale.p if wscale is not None else None
@@ -61,7 +66,13 @@ def gemm(A, W, *, bias=None, wscale=None, epi=M.EPI_STORE, c=None, c_dtype=M.F32
     g.lda, g.ldc, g.stride_a, g.stride_c, g.batch = lda, ldc, sa, sc, batch
     g.w_dtype, g.c_dtype, g.epilogue = w_dtype, c_dtype, epi
     g.heads = C.pointer(heads) if heads is not None else None
-    M.call("mk_gemm", C.byref(g), None)
+    g._keep = heads
+    return g
+
+
+def gemm_grouped(*args):
+    arr = (M.GemmArgs * len(args))(*args)
+    M.call("mk_gemm_grouped", C.cast(arr, C.c_void_p), len(args), None)
     M.sync()
 
 
@@ -166,6 +177,91 @@ def test_gemm_heads_epilogue(gpu, rng, mode, row0, q_row0):
             assert np.abs(got - want).max() <= 2 ** -8 * np.abs(want).max() + 1e-6
     # rows outside the written range stay zero
     assert not gk[:, :, :row0].any() and not gk[:, :, row0 + Mr:].any()
+
+
+def test_gemm_grouped_residual_equals_separate_launches(gpu, rng):
+    # an image-like and a text-like problem (own A, W, bias, gate, residual, M and strides) in one launch give the
+    # bits of two launches, and match the oracle
+    N, K = 256, 192
+    probs = []
+    for Mr, B in ((300, 2), (40, 2)):
+        A = rng.standard_normal((B, Mr, K)).astype(np.float32)
+        W = R.bf16_round(rng.standard_normal((N, K)).astype(np.float32) * 0.05)
+        b = rng.standard_normal(N).astype(np.float32)
+        gt = rng.standard_normal(N).astype(np.float32)
+        X = rng.standard_normal((B, Mr, N)).astype(np.float32)
+        probs.append((Mr, B, A, W, b, gt, X, bdev(A), bdev(W), dev(b), dev(gt)))
+    outs = []
+    for grouped in (False, True):
+        xs = [dev(pr[6]) for pr in probs]
+        args = [gemm_args(Ad, Wd, bias=bd, c=xd, epi=M.EPI_GATE_ADD, M_=(Mr, N, K), batch=B, lda=K, ldc=N,
+                          sa=Mr * K, sc=Mr * N, gate=gd)
+                for (Mr, B, _, _, _, _, _, Ad, Wd, bd, gd), xd in zip(probs, xs)]
+        if grouped:
+            gemm_grouped(*args)
+        else:
+            for g in args:
+                M.call("mk_gemm", C.byref(g), None)
+            M.sync()
+        outs.append([fetch(xd, pr[6].shape) for xd, pr in zip(xs, probs)])
+    for sep, grp, (Mr, B, A, W, b, gt, X, *_) in zip(outs[0], outs[1], probs):
+        assert np.array_equal(sep, grp)
+        want = X.astype(np.float64) + gt * np.stack([R.gemm(A[i], W, b) for i in range(B)])
+        assert maxrel(grp, want) < 1e-5
+
+
+def test_gemm_grouped_heads_and_gelu(gpu, rng):
+    # the QKV pair of a dual-stream block: text rows at 0, image rows at row0 = S, own norms, one Q / K / V^T
+    Bt, H, S, Nimg, K_ = 2, 2, 24, 136, 256
+    D = H * 128
+    q_pad = k_pad = 256
+    Q, Kd, Vt = [M.Dev(Bt * H * q_pad * 256) for _ in range(3)]
+    cs = R.rope_table(S, 8, 17)
+    csd = dev(cs)
+    args, ref = [], []
+    for rows, row0 in ((Nimg, S), (S, 0)):
+        A = rng.standard_normal((Bt, rows, K_)).astype(np.float32)
+        W = R.bf16_round(rng.standard_normal((3 * D, K_)).astype(np.float32) * 0.05)
+        b = rng.standard_normal(3 * D).astype(np.float32) * 0.1
+        nq = (1 + 0.1 * rng.standard_normal(128)).astype(np.float32)
+        nk = (1 + 0.1 * rng.standard_normal(128)).astype(np.float32)
+        ha = M.HeadsArgs(Q.p, Kd.p, Vt.p, H, 128, q_pad, k_pad, row0, row0, dev(nq).p, dev(nk).p, csd.p, 2, 1e-6)
+        args.append(gemm_args(bdev(A), bdev(W), bias=dev(b), epi=M.EPI_HEADS, c_dtype=M.BF16, M_=(rows, 3 * D, K_),
+                              batch=Bt, lda=K_, sa=rows * K_, heads=ha))
+        ref.append((rows, row0, A, W, b, nq, nk))
+    gemm_grouped(*args)
+    gq = fetch_bf16(Q, (Bt, H, q_pad, 128))
+    gk = fetch_bf16(Kd, (Bt, H, k_pad, 128))
+    gv = fetch_bf16(Vt, (Bt, H, 128, k_pad))
+    for rows, row0, A, W, b, nq, nk in ref:
+        for bi in range(Bt):
+            y = R.gemm(A[bi], W, b)
+            tab = cs[row0:row0 + rows]
+            vcols = M.vt_col(np.arange(row0, row0 + rows))
+            wq = R.heads_norm_rope(y, H, 128, col0=0, w=nq, cs=tab, rope=2)
+            wk = R.heads_norm_rope(y, H, 128, col0=D, w=nk, cs=tab, rope=2)
+            wv = R.heads_norm_rope(y, H, 128, col0=2 * D)
+            for got, want in ((gq[bi][:, row0:row0 + rows], wq), (gk[bi][:, row0:row0 + rows], wk),
+                              (gv[bi][:, :, vcols].transpose(0, 2, 1), wv)):
+                assert np.abs(got - want).max() <= 2 ** -8 * np.abs(want).max() + 1e-6
+    # GELU pair into one hidden buffer (image rows, then text rows)
+    N, K = 512, 128
+    A0, A1 = (rng.standard_normal((r, K)).astype(np.float32) for r in (300, 48))
+    W0, W1 = (R.bf16_round(rng.standard_normal((N, K)).astype(np.float32) * 0.1) for _ in range(2))
+    hid = M.Dev((300 + 48) * N * 2)
+    _live.append(hid)
+    g0 = gemm_args(bdev(A0), bdev(W0), c=hid, c_dtype=M.BF16, epi=M.EPI_GELU_TANH, M_=(300, N, K), lda=K, ldc=N)
+    g1 = gemm_args(bdev(A1), bdev(W1), c_dtype=M.BF16, epi=M.EPI_GELU_TANH, M_=(48, N, K), lda=K, ldc=N)
+    g1.c = hid.p + 300 * N * 2
+    gemm_grouped(g0, g1)
+    got = fetch_bf16(hid, (348, N))
+    for g, want in ((got[:300], R.gelu_tanh(R.gemm(A0, W0))), (got[300:], R.gelu_tanh(R.gemm(A1, W1)))):
+        assert np.abs(g - want).max() <= 2 ** -8 * np.abs(want).max() + 1e-6
+    # problems of unequal N are refused
+    g1.N = 256
+    arr = (M.GemmArgs * 2)(g0, g1)
+    assert M.lib().mk_gemm_grouped(C.cast(arr, C.c_void_p), 2, None) == 1
+    assert b"equal N" in M.lib().mk_last_error()
 
 
 def test_vt_col_is_an_involution_within_groups():
