@@ -91,6 +91,7 @@ typedef struct mk_heads_args {
     const float* rope;    /* [rows][head_dim/2][2] (cos, sin) at row0 + r, or NULL */
     uint32_t rope_mode;   /* 0 none, 1 half-split pairs (i, i + d/2), 2 interleaved pairs (2i, 2i+1) */
     float eps;
+    float k_scale;        /* K rows times this (0: 1), e.g. the softmax scale times log2(e) for mk_attention's scale 0 */
 } mk_heads_args;
 
 typedef struct mk_gemm_args {

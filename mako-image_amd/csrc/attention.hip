@@ -39,7 +39,12 @@ __device__ inline uint32_t cvt_bf16x2(float a, float b)
     return __builtin_bit_cast(uint32_t, v);
 }
 
-template <int D>
+// U: K carries the softmax scale in log2 units (scale 0 at the API). The running max then enters the S^T MFMAs as
+// one more 16-deep product, a constant fragment of ones (K side, dim 0) times a fragment holding -m (Q side), so
+// S - m comes out of the matrix core: the softmax needs no per-score multiply-add, and the row sums are taken on the
+// bf16 probabilities the P V product uses (v_dot2 against ones), which halves those adds too. m is kept
+// bf16-representable so the product subtracts it exactly.
+template <int D, bool U>
 __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn2_kernel(AttnP p)
 {
     constexpr int DS = D / 16, DT = D / 32, KC = D / 8;
@@ -87,8 +92,13 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
             load_lds16(gv[i] + k0, (lds_void*)&sV[buf][(i * 4 + wave) * 512]);
     };
     // S^T of keys kt*32 .. +32 of the tile in buf: value r <-> key 8(r/4) + 4hk + r%4
+    bf16x8 kone = {}, qm = {}; // U: ones at dim 0 (K side); -m at dim 0 (Q side), lanes of the first k half
+    if (hk == 0)
+        kone[0] = (__bf16)1.0f;
     auto qk = [&](int buf, int kt, f32x16& sacc) {
         sacc = f32x16{};
+        if constexpr (U)
+            sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kone, qm, sacc, 0, 0, 0);
 #pragma unroll
         for (int ds = 0; ds < DS; ++ds) {
             const int key = kt * 32 + r32, c = kswz(key, ds * 2 + hk);
@@ -100,9 +110,62 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
         oacc[dt] = f32x16{};
-    float m = -1e30f, l = 0.0f;
+    float m = U ? 0.0f : -1e30f, l = 0.0f;
     const int qpos = int(p.q_pos0) + q0 + r32;
     const bool wave_causal = uint32_t(int(p.q_pos0) + q0) < p.block;
+    // U: the scores arrive as S - m; the first half-tile sets m to its max (every query sees key 0), later ones move
+    // it lazily as below.
+    auto softmax_u = [&](f32x16& sacc, int k0, u32x4 (&pb)[2], bool first, f32x16* other) {
+        if (k0 + 32 > int(p.n_k) || (wave_causal && k0 + 31 > int(p.q_pos0) + q0)) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int key = k0 + 8 * (r / 4) + 4 * hk + (r % 4);
+                if (key >= int(p.n_k) || (uint32_t(qpos) < p.block && key > qpos))
+                    sacc[r] = -__builtin_inff();
+            }
+        }
+        float mx = -1e30f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+            mx = fmaxf(mx, sacc[r]);
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        if (first || __any(mx > kLazy)) {
+            const float mn = float((__bf16)(m + (first ? mx : fmaxf(mx, 0.0f))));
+            const float dm = mn - m;
+            const float alpha = first ? 1.0f : __builtin_amdgcn_exp2f(-dm);
+            m = mn;
+            if (hk == 0)
+                qm[0] = (__bf16)(-m);
+            l *= alpha;
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                sacc[r] -= dm;
+            if (other) // the next half's scores, computed against the old m
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    (*other)[r] -= dm;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    oacc[dt][r] *= alpha;
+        }
+        const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+            const int o = 8 * st;
+            u32x4 v;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                // (bit-cast from a scalar: this compiler miscompiles a bit-cast of a vector element here)
+                const uint32_t pj = cvt_bf16x2(__builtin_amdgcn_exp2f(sacc[o + 2 * j]),
+                                               __builtin_amdgcn_exp2f(sacc[o + 2 * j + 1]));
+                v[j] = pj;
+                l = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pj), ones, l, false);
+            }
+            pb[st] = v;
+        }
+    };
     auto softmax = [&](f32x16& sacc, int k0, u32x4 (&pb)[2]) {
         if (k0 + 32 > int(p.n_k) || (wave_causal && k0 + 31 > int(p.q_pos0) + q0)) {
 #pragma unroll
@@ -167,9 +230,15 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
         u32x4 pb[2];
         qk(buf, 0, s_a);
         qk(buf, 1, s_b);
-        softmax(s_a, t * kKT, pb);
-        pv(buf, 0, pb);
-        softmax(s_b, t * kKT + 32, pb);
+        if constexpr (U) {
+            softmax_u(s_a, t * kKT, pb, t == 0, &s_b);
+            pv(buf, 0, pb);
+            softmax_u(s_b, t * kKT + 32, pb, false, nullptr);
+        } else {
+            softmax(s_a, t * kKT, pb);
+            pv(buf, 0, pb);
+            softmax(s_b, t * kKT + 32, pb);
+        }
         pv(buf, 1, pb);
     }
     __builtin_amdgcn_s_waitcnt(0);
@@ -213,10 +282,11 @@ extern "C" mk_status mk_attention(const void* q, const void* k, const void* vt, 
             scale * 1.4426950408889634f};
     const dim3 grid(cdiv(n_q, 128), heads, batch);
     hipStream_t s = static_cast<hipStream_t>(stream);
+    const bool unit = scale == 0.0f;
     if (d == 128)
-        attn2_kernel<128><<<grid, 256, 0, s>>>(p);
+        unit ? attn2_kernel<128, true><<<grid, 256, 0, s>>>(p) : attn2_kernel<128, false><<<grid, 256, 0, s>>>(p);
     else
-        attn2_kernel<64><<<grid, 256, 0, s>>>(p);
+        unit ? attn2_kernel<64, true><<<grid, 256, 0, s>>>(p) : attn2_kernel<64, false><<<grid, 256, 0, s>>>(p);
     MK_LAUNCH_CHECK("attention");
     return MK_OK;
 }

@@ -105,6 +105,8 @@ struct Timing {
 using namespace mk;
 
 struct mk_engine {
+    // 1 / sqrt(128) * log2(e): the QKV epilogue scales K by it, so attention takes its scores in log2 units
+    static constexpr float kScaleLog2 = 0.12751743082459868f;
     mk_config cfg{};
     hipStream_t stream = nullptr;
     std::vector<void*> allocs; // weight storage
@@ -534,13 +536,14 @@ struct mk_engine {
                 ha[j].rope = rope.f();
                 ha[j].rope_mode = 2;
                 ha[j].eps = eps;
+                ha[j].k_scale = kScaleLog2; // K carries the softmax scale: attention runs with scale 0
                 g[j] = gemm_args(B.qkv[s.which], s.xn->p, D, int64_t(s.rows) * D, s.rows, nb, nullptr, 0, 0,
                                  MK_EPI_HEADS, MK_BF16, nullptr, 0, 0, 0, &ha[j]);
             }
             MK_TRY(gemm2(g));
             MK_TRY(timed("attention", attn_flops, [&] {
                 return mk_attention(q.p, k.p, vt.p, att.p, nb, H, 128, T, q_pad, T, k_pad, D, int64_t(T) * D, 0, 0,
-                                    1.0f / std::sqrt(128.0f), stream);
+                                    0.0f, stream);
             }));
             for (int j = 0; j < 2; ++j) {
                 const St& s = st[j];
@@ -663,6 +666,7 @@ struct mk_engine {
             ha.rope = rope.f();
             ha.rope_mode = 2;
             ha.eps = eps;
+            ha.k_scale = kScaleLog2;
             // the text's keys and values (heads_rows): kept after the first step's q/k/v, restored before the later
             // steps'. V^T keeps whole groups of 16 keys (its columns permute keys within a group); a group shared
             // with image keys is rewritten by the image rows' q/k/v that follow the restore.
@@ -682,8 +686,8 @@ struct mk_engine {
                                         size_t(H) * 128, hipMemcpyDeviceToDevice, stream));
             }
             MK_TRY(timed("attention", 4.0 * pairs * 128 * H, [&] {
-                return mk_attention(q.p, k.p, vt.p, att.p, 1, H, 128, T, q_pad, n_k, k_pad, D, 0, row0, S,
-                                    1.0f / std::sqrt(128.0f), stream);
+                return mk_attention(q.p, k.p, vt.p, att.p, 1, H, 128, T, q_pad, n_k, k_pad, D, 0, row0, S, 0.0f,
+                                    stream);
             }));
             MK_TRY(gemm(B.o[0], att.p, D, 0, T, 1, x_img.p, D, 0, MK_EPI_GATE_TANH, MK_F32, mod.f() + D, 4 * D, split,
                         T));

@@ -20,7 +20,7 @@ struct HeadsP {
     uint16_t *q, *k, *vt;
     uint32_t heads, q_pad, k_pad, row0, q_row0, rope_mode, dim;
     const float *norm_q, *norm_k, *rope;
-    float eps;
+    float eps, k_scale;
 };
 
 struct GemmP {
@@ -230,7 +230,12 @@ __device__ inline void epi_heads(const GemmP& p, const float* st, int ld, int to
     const int c = lane & 31, r0 = lane >> 5, ch = 4 * c;
     const f32x4 sc = p.wscale ? *reinterpret_cast<const f32x4*>(p.wscale + nw0 + ch) : f32x4{1, 1, 1, 1};
     const f32x4 bi = p.bias ? *reinterpret_cast<const f32x4*>(p.bias + nw0 + ch) : f32x4{0, 0, 0, 0};
-    const f32x4 wn = nw ? *reinterpret_cast<const f32x4*>(nw + ch) : f32x4{1, 1, 1, 1};
+    // the norm weights, with K's scale folded in (norm, RoPE and the scale are all linear in the row)
+    const float ks = which == 1 ? h.k_scale : 1.0f;
+    f32x4 wn = nw ? *reinterpret_cast<const f32x4*>(nw + ch) : f32x4{1, 1, 1, 1};
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+        wn[e] *= ks;
     const int mode = int(h.rope_mode);
     const int last = int(p.M) - 1;
     // RoPE factors of a row (clamped to the last valid row): mode 2, pairs (2c, 2c + 1) -> (cos, sin, cos, sin) of
@@ -599,7 +604,7 @@ mk_status prepare(const mk_gemm_args* a, GemmP& p)
                                     "of 256, k_pad a multiple of 16, and row0 + M within the padded rows");
         p.hp = HeadsP{static_cast<uint16_t*>(h->q), static_cast<uint16_t*>(h->k), static_cast<uint16_t*>(h->vt),
                       h->heads, h->q_pad, h->k_pad, h->row0, h->q_row0, h->rope_mode, a->N / 3, h->norm_q, h->norm_k,
-                      h->rope, h->eps};
+                      h->rope, h->eps, h->k_scale == 0.0f ? 1.0f : h->k_scale};
     }
     return MK_OK;
 }

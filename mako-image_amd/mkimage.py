@@ -29,7 +29,7 @@ class MkError(RuntimeError):
 class HeadsArgs(C.Structure):
     _fields_ = [("q", _vp), ("k", _vp), ("vt", _vp), ("heads", _u32), ("head_dim", _u32), ("q_pad", _u32),
                 ("k_pad", _u32), ("row0", _u32), ("q_row0", _u32), ("norm_q", _vp), ("norm_k", _vp), ("rope", _vp),
-                ("rope_mode", _u32), ("eps", _f)]
+                ("rope_mode", _u32), ("eps", _f), ("k_scale", _f)]
 
 
 class GemmArgs(C.Structure):

@@ -142,8 +142,9 @@ def test_gemm_fp8_weights(gpu, rng):
     assert maxrel(fetch(out, (Mr, N)), R.gemm(A, q, b, wscale=scale)) < 1e-5
 
 
-@pytest.mark.parametrize("mode,row0,q_row0", [(2, 40, 40), (1, 0, 0), (0, 17, 0)])
-def test_gemm_heads_epilogue(gpu, rng, mode, row0, q_row0):
+@pytest.mark.parametrize("mode,row0,q_row0,k_scale", [(2, 40, 40, 0.0), (1, 0, 0, 0.0), (0, 17, 0, 0.0),
+                                                      (2, 40, 40, 0.3)])
+def test_gemm_heads_epilogue(gpu, rng, mode, row0, q_row0, k_scale):
     # q | k | v columns -> per-head RMSNorm + RoPE -> Q, K [b][h][pad][128] and V^T [b][h][128][pad]
     B, Mr, H = 2, 150, 2
     D = H * 128
@@ -156,7 +157,7 @@ def test_gemm_heads_epilogue(gpu, rng, mode, row0, q_row0):
     nk = (1 + 0.1 * rng.standard_normal(128)).astype(np.float32)
     cs = R.rope_table(row0, 14, 14)[: row0 + Mr] if row0 else R.rope_table(0, 15, 10)[:Mr]
     Q, Kd, Vt = M.Dev(B * H * q_pad * 256), M.Dev(B * H * k_pad * 256), M.Dev(B * H * k_pad * 256)
-    ha = M.HeadsArgs(Q.p, Kd.p, Vt.p, H, 128, q_pad, k_pad, row0, q_row0, None, None, None, mode, 1e-6)
+    ha = M.HeadsArgs(Q.p, Kd.p, Vt.p, H, 128, q_pad, k_pad, row0, q_row0, None, None, None, mode, 1e-6, k_scale)
     nqd, nkd, csd = dev(nq), dev(nk), dev(cs)
     ha.norm_q, ha.norm_k, ha.rope = nqd.p, nkd.p, csd.p
     Ad = bdev(A)
@@ -169,7 +170,7 @@ def test_gemm_heads_epilogue(gpu, rng, mode, row0, q_row0):
         y = R.gemm(A[bi], W, b)
         tab = cs[row0:]
         wq = R.heads_norm_rope(y, H, 128, col0=0, w=nq, cs=tab, rope=mode)
-        wk = R.heads_norm_rope(y, H, 128, col0=D, w=nk, cs=tab, rope=mode)
+        wk = R.heads_norm_rope(y, H, 128, col0=D, w=nk, cs=tab, rope=mode) * (k_scale or 1.0)
         wv = R.heads_norm_rope(y, H, 128, col0=2 * D)
         vcols = M.vt_col(np.arange(row0, row0 + Mr))
         for got, want in ((gq[bi][:, q_row0:q_row0 + Mr], wq), (gk[bi][:, row0:row0 + Mr], wk),
@@ -316,6 +317,24 @@ def test_attention_matches_oracle(gpu, rng, d, Tq, Tk, block, q_pos0):
     want = R.attention(q, k, v, 1 / np.sqrt(d), q_pos0, block)
     dd = R.diff(got, want, d)
     # P is rounded to bf16 for the MFMA, the output stored bf16
+    assert dd["min_cos"] > 0.9999 and dd["max_rel"] < 1e-2, dd
+
+
+@pytest.mark.parametrize("d,Tq,Tk,block,q_pos0,kscale", [
+    (128, 300, 300, 0, 0, 1.0), (128, 4352 // 17, 4352, 0, 0, 1.0), (64, 333, 77, 0, 0, 1.0),
+    (128, 200, 260, 60, 60, 1.0), (128, 260, 260, 60, 0, 1.0), (128, 190, 190, 0xFFFFFFFF, 0, 1.0),
+    (128, 256, 512, 0, 0, 6.0)])
+def test_attention_unit_scale(gpu, rng, d, Tq, Tk, block, q_pos0, kscale):
+    # scale 0: K already carries the softmax scale in log2 units (K' = bf16(k / sqrt(d) * log2 e)); equal to the
+    # softmax of q K'^T ln 2. kscale 6 makes the logits large (the running max moves on many tiles).
+    B, H = 2, 3
+    q = R.bf16_round(rng.standard_normal((B, H, Tq, d)).astype(np.float32))
+    k = rng.standard_normal((B, H, Tk, d)).astype(np.float32) * kscale
+    kp = R.bf16_round(k / np.sqrt(d) * np.log2(np.e))
+    v = R.bf16_round(rng.standard_normal((B, H, Tk, d)).astype(np.float32))
+    got = run_attention(q, kp, v, 0.0, q_pos0, block)
+    want = R.attention(q, kp, v, float(np.log(2.0)), q_pos0, block)
+    dd = R.diff(got, want, d)
     assert dd["min_cos"] > 0.9999 and dd["max_rel"] < 1e-2, dd
 
 
