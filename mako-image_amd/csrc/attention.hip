@@ -21,7 +21,7 @@ namespace {
 struct AttnP {
     const uint16_t *q, *k, *vt;
     uint16_t* out;
-    uint32_t heads, n_q, q_pad, n_k, k_pad, q_pos0, block;
+    uint32_t heads, batch, n_q, q_pad, n_k, k_pad, q_pos0, block;
     int64_t ldo, so;
     float c; // scale * log2(e)
 };
@@ -55,12 +55,19 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, r32 = lane & 31, hk = lane >> 5;
     auto kswz = [](int key, int c) { return KC == 16 ? c ^ (key & 15) : c ^ ((key >> 1) & 7); };
-    const uint32_t head = blockIdx.y, bi = blockIdx.z;
+    // XCD-aware order: workgroup i runs on XCD i % 8 (round-robin dispatch), so give each XCD a contiguous run of
+    // (batch, head, query block) items: the query blocks of one head then share its K / V in that XCD's L2, instead
+    // of every XCD streaming every head's K / V.
+    const uint32_t nqb = (p.n_q + 127) / 128, total = nqb * p.heads * p.batch;
+    uint32_t item = blockIdx.x;
+    if (total % 8 == 0)
+        item = (item % 8) * (total / 8) + item / 8;
+    const uint32_t qb = item % nqb, head = (item / nqb) % p.heads, bi = item / (nqb * p.heads);
     const int64_t bh = int64_t(bi) * p.heads + head;
     const uint16_t* Q = p.q + bh * p.q_pad * D;
     const uint16_t* K = p.k + bh * p.k_pad * D;
     const uint16_t* VT = p.vt + bh * int64_t(D) * p.k_pad;
-    const int q0 = int(blockIdx.x) * 128 + wave * 32;
+    const int q0 = int(qb) * 128 + wave * 32;
 
     bf16x8 qf[DS];
     {
@@ -278,9 +285,9 @@ extern "C" mk_status mk_attention(const void* q, const void* k, const void* vt, 
     if (ldo % 4 || (reinterpret_cast<uintptr_t>(out) & 7))
         return fail(MK_ERR_ARG, "attention: output rows must be 8-byte aligned");
     AttnP p{static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(vt),
-            static_cast<uint16_t*>(out), heads, n_q, q_pad, n_k, k_pad, q_pos0, block, ldo, stride_o,
+            static_cast<uint16_t*>(out), heads, batch, n_q, q_pad, n_k, k_pad, q_pos0, block, ldo, stride_o,
             scale * 1.4426950408889634f};
-    const dim3 grid(cdiv(n_q, 128), heads, batch);
+    const dim3 grid(cdiv(n_q, 128) * heads * batch);
     hipStream_t s = static_cast<hipStream_t>(stream);
     const bool unit = scale == 0.0f;
     if (d == 128)

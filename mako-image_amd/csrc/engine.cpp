@@ -109,6 +109,7 @@ struct mk_engine {
     static constexpr float kScaleLog2 = 0.12751743082459868f;
     mk_config cfg{};
     hipStream_t stream = nullptr;
+    uint32_t cus = 256; // compute units of the engine's device
     std::vector<void*> allocs; // weight storage
     std::map<std::string, Dest> dests;
     uint64_t weight_bytes = 0;
@@ -344,10 +345,34 @@ struct mk_engine {
         return timed(cls, 2.0 * M * L.out * L.in * batch, [&] { return mk_gemm(&g, stream); });
     }
     // Two GEMMs of equal N, K and epilogue kind (a block's image and text projections) in one launch.
+    // Two GEMMs of equal N, K and epilogue kind (a block's image and text projections): one launch when that takes
+    // fewer waves of tiles than two (the text's few tiles fill the image's last wave), else two.
     mk_status gemm2(const mk_gemm_args (&g)[2])
     {
-        const double fl = 2.0 * g[0].N * g[0].K * (double(g[0].M) * g[0].batch + double(g[1].M) * g[1].batch);
-        return timed("gemm", fl, [&] { return mk_gemm_grouped(g, 2, stream); });
+        const bool one = launch_cost(g, 2) < launch_cost(g, 1) + launch_cost(g + 1, 1);
+        if (one) {
+            const double fl = 2.0 * g[0].N * g[0].K * (double(g[0].M) * g[0].batch + double(g[1].M) * g[1].batch);
+            return timed("gemm", fl, [&] { return mk_gemm_grouped(g, 2, stream); });
+        }
+        for (int i = 0; i < 2; ++i)
+            MK_TRY(timed("gemm", 2.0 * g[i].N * g[i].K * double(g[i].M) * g[i].batch,
+                         [&] { return mk_gemm_grouped(g + i, 1, stream); }));
+        return MK_OK;
+    }
+    // Channel-tile-waves of a launch: the tile width the GEMM dispatch picks (256 when the grid fills the chip, else
+    // 128), tiles of 256 tokens, one workgroup per CU; a wave of w-channel tiles costs w.
+    double launch_cost(const mk_gemm_args* g, int n) const
+    {
+        uint64_t t256 = 0;
+        for (int i = 0; i < n; ++i)
+            t256 += uint64_t((g[i].M + 255) / 256) * g[i].batch * (g[0].N / 256);
+        const uint32_t bn = g[0].epilogue == MK_EPI_HEADS || (g[0].N % 256 == 0 && t256 >= 512) ? 256
+                            : g[0].N % 128 == 0                                                 ? 128
+                                                                                                : 64;
+        uint64_t tiles = 0;
+        for (int i = 0; i < n; ++i)
+            tiles += uint64_t((g[i].M + 255) / 256) * g[i].batch * (g[0].N / bn);
+        return double((tiles + cus - 1) / cus) * bn;
     }
     static mk_gemm_args gemm_args(const Linear& L, const void* A, int64_t lda, int64_t sa, uint32_t M, uint32_t batch,
                                   void* C, int64_t ldc, int64_t sc, uint32_t epi, uint32_t cdt,
@@ -858,6 +883,10 @@ mk_status mk_engine_create(const mk_config* cfg, mk_engine** out)
     if (!e->cfg.max_batch)
         e->cfg.max_batch = 2;
     MK_HIP(hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking));
+    int dev = 0, ncu = 0;
+    MK_HIP(hipGetDevice(&dev));
+    MK_HIP(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev));
+    e->cus = ncu > 0 ? uint32_t(ncu) : 256;
     mk_status s = e->build();
     if (s != MK_OK)
         return s;

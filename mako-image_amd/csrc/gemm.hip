@@ -12,6 +12,8 @@
 // Workgroups map to tiles XCD-aware (consecutive tiles on one XCD share its L2) and grouped along M.
 #include "common.hpp"
 
+#include <mutex>
+
 namespace mk {
 
 namespace gemm_detail {
@@ -188,11 +190,11 @@ __device__ inline void epi_slice(const GemmP& p, const float* st, int ld, int to
 //    load behind stores would wait for all of them.
 //  - v: each lane two head dims across the 32 tokens, bf16 to V^T [batch][heads][128][k_pad] rows (keys in the
 //    vt_col order).
-__device__ inline void epi_heads(const GemmP& p, const float* st, int ld, int tok0, int nw0, int lane)
+__device__ inline void epi_heads(const GemmP& p, const float* st, int ld, int tok0, int nw0, int lane, uint32_t z)
 {
     const HeadsP& h = p.hp;
     const int which = nw0 / int(h.dim), head = (nw0 % int(h.dim)) / 128;
-    const int64_t bh = int64_t(blockIdx.z) * h.heads + head;
+    const int64_t bh = int64_t(z) * h.heads + head;
     if (which == 2) {
         float sc[2], bi[2];
 #pragma unroll
@@ -331,13 +333,64 @@ __device__ inline void epi_heads(const GemmP& p, const float* st, int ld, int to
         emit(8 + i, ra[i], rb[i]);
 }
 
-template <int BM, int BN, bool kF8, int EK, int NW>
-__global__ __launch_bounds__(64 * NW, 1) __attribute__((amdgpu_waves_per_eu(NW / 4, NW / 4))) void gemm_kernel(GemmG G)
+// Stream-K state of a persistent launch: the tail tiles are split into k ranges over the whole grid; a workgroup
+// whose range ends inside a tile publishes its partial accumulators, the workgroup holding the tile's last k steps
+// adds them (in a fixed order) and runs the epilogue.
+struct SkP {
+    float* ws;          // [2 grid][threads * accumulators] partials, two slots a workgroup (its first and last tile)
+    uint32_t* flags;    // [2 grid]: set to epoch when the slot holds this launch's partial
+    uint32_t epoch;
+    uint32_t total;     // tiles over both problems
+    uint32_t dp;        // tiles done whole, round robin over the grid (a multiple of it)
+    uint32_t kt;        // k steps a tile
+    uint64_t units;     // (total - dp) * kt: the tail's k steps, split evenly over the grid
+};
+
+// Stream-K tail partition: range i (a virtual workgroup index) holds tail units [units i / grid, units (i+1) / grid).
+// Its segment of tail tile tt publishes to slot 2 i (its first tile) or 2 i + 1 (its last).
+__device__ inline uint64_t sk_begin(const SkP& sk, uint32_t i) { return sk.units * i / gridDim.x; }
+__device__ inline int sk_slot(const SkP& sk, uint32_t i, uint64_t tt)
 {
-    const bool second = blockIdx.x >= G.tiles0;
+    return int(2 * i + (tt == sk_begin(sk, i) / sk.kt ? 0 : 1));
+}
+// The physical workgroup of virtual index i: virtual order gives each XCD (workgroups w = x mod 8) a contiguous run
+// of tail tiles, which then share panels in its L2.
+__device__ inline uint32_t sk_phys(uint32_t i)
+{
+    const uint32_t per = gridDim.x / 8;
+    return gridDim.x % 8 ? i : (i % per) * 8 + i / per;
+}
+
+// XCD-aware order of n tiles (n a multiple of 8): round-robin dispatch puts workgroup i on XCD i % 8; give each
+// XCD a contiguous run of tiles.
+__device__ inline uint32_t xcd_order(uint32_t t, uint32_t n) { return n % 8 ? t : (t % 8) * (n / 8) + t / 8; }
+
+// Tile t of a launch (problem 0's tiles, then problem 1's; batch-major within a problem) -> problem, batch and tile
+// coordinates, grouped 8 token tiles at a time so consecutive tiles share weight columns.
+__device__ inline const GemmP& locate(const GemmG& G, uint32_t t, uint32_t& z, uint32_t& tm, uint32_t& tn)
+{
+    const bool second = t >= G.tiles0;
     const GemmP& p = G.g[second];
-    if (blockIdx.z >= p.batch)
-        return;
+    const uint32_t per = p.tiles_m * p.tiles_n;
+    uint32_t pid = second ? t - G.tiles0 : t;
+    z = pid / per;
+    pid %= per;
+    const uint32_t GM = 8, in_group = GM * p.tiles_n;
+    const uint32_t first_m = (pid / in_group) * GM;
+    const uint32_t gsize = min(p.tiles_m - first_m, GM);
+    tm = first_m + (pid % in_group) % gsize;
+    tn = (pid % in_group) / gsize;
+    return p;
+}
+
+// One tile's k steps [kb, ke): the pipelined main loop, then either the partial published to stream-K slot
+// `publish`, or the partials of the tile's other ranges (virtual indices fix_lo .. fix_hi except `self`, tail tile
+// tt) added in index order, and the epilogue.
+template <int BM, int BN, bool kF8, int EK, int NW>
+__device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t tm, uint32_t tn, int kb, int ke,
+                                          uint16_t* smem, const SkP* sk, int publish, int fix_lo = 0,
+                                          int fix_hi = -1, int self = -1, uint64_t tt = 0)
+{
     constexpr int NT = 64 * NW;                 // threads
     constexpr int WM = BM / (NW / 2);           // tokens per wave (waves: 2 along channels x NW/2 along tokens)
     constexpr int TB = WM / 32, CB = BN / 64;   // 32-row MFMA blocks per wave along tokens / channels
@@ -345,28 +398,14 @@ __global__ __launch_bounds__(64 * NW, 1) __attribute__((amdgpu_waves_per_eu(NW /
     constexpr int RW = BN * 8 / NT;             // ... for a bf16 weight tile
     constexpr int LW = BN * 4 / NT;             // 16-byte fp8 weight chunks per thread (register staged)
     constexpr int WC = BN / 2, LDW = WC + 4;    // epilogue staging: a wave's 32 tokens x WC channels, padded rows
-    constexpr int SMEM = 2 * (BN + BM) * 64 * 2 > NW * 32 * LDW * 4 ? 2 * (BN + BM) * 64 * 2 : NW * 32 * LDW * 4;
-    __shared__ __attribute__((aligned(16))) uint16_t smem[SMEM / 2];
     uint16_t(*sW)[BN * 64] = reinterpret_cast<uint16_t(*)[BN * 64]>(smem);
     uint16_t(*sA)[BM * 64] = reinterpret_cast<uint16_t(*)[BM * 64]>(smem + 2 * BN * 64);
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wn = wave & 1, wm = wave >> 1;
-
-    // Tile of this workgroup: XCD-aware (round-robin dispatch puts workgroup i on XCD i % 8; give each XCD a
-    // contiguous run of tiles), then grouped 8 m-tiles at a time so a run shares weight columns.
-    const uint32_t total = p.tiles_m * p.tiles_n;
-    uint32_t pid = second ? blockIdx.x - G.tiles0 : blockIdx.x;
-    if (total % 8 == 0)
-        pid = (pid % 8) * (total / 8) + pid / 8;
-    const uint32_t GM = 8, in_group = GM * p.tiles_n;
-    const uint32_t first_m = (pid / in_group) * GM;
-    const uint32_t gsize = min(p.tiles_m - first_m, GM);
-    const uint32_t tm = first_m + (pid % in_group) % gsize, tn = (pid % in_group) / gsize;
     const int m0 = int(tm) * BM, n0 = int(tn) * BN;
 
-    const uint16_t* A = p.a + int64_t(blockIdx.z) * p.sa;
-    const int KT = int(p.K) / BK;
+    const uint16_t* A = p.a + int64_t(z) * p.sa;
 
     // Direct loads: wave w's round i fills LDS chunks P = (i * NW + w) * 64 + lane of the tile; chunk P holds
     // row P / 8 and logical k-chunk swz_chunk(row, P % 8), so the lane loads that one.
@@ -460,15 +499,15 @@ __global__ __launch_bounds__(64 * NW, 1) __attribute__((amdgpu_waves_per_eu(NW /
     // Software pipeline: tile t is in LDS buffer t & 1, tile t + 1 lands in the other during tile t's MFMAs, and the
     // fragments of k step s + 1 are read from LDS while step s's MFMAs run. The loop body has no branches (prefetch
     // tile indices are clamped; past-the-end prefetches reload the last tile), so the interleave covers all of it.
-    issue(0, 0);
+    issue(kb, 0);
     commit_f8(0);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    issue(min(1, KT - 1), 1);
+    issue(min(kb + 1, ke - 1), 1);
     bf16x8 wf0[CB], af0[TB], wf1[CB], af1[TB];
     frags(0, 0, wf0, af0);
-    for (int kt = 0; kt < KT; ++kt) {
-        const int buf = kt & 1;
+    for (int kt = kb; kt < ke; ++kt) {
+        const int buf = (kt - kb) & 1;
         frags(buf, 1, wf1, af1);
         mfma(wf0, af0);
         interleave();
@@ -483,19 +522,85 @@ __global__ __launch_bounds__(64 * NW, 1) __attribute__((amdgpu_waves_per_eu(NW /
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
         frags(buf ^ 1, 0, wf0, af0);
-        issue(min(kt + 2, KT - 1), buf);
+        issue(min(kt + 2, ke - 1), buf);
         mfma(wf1, af1);
         interleave();
     }
     __builtin_amdgcn_s_waitcnt(0); // the last (unused) prefetch must land before the LDS is reused
     __syncthreads();
 
+    // ---- stream-K: publish this range's partial, or add the earlier ranges' partials ----
+    constexpr int NACC = CB * TB * 16;
+    // Partials go through L2 to the device-coherent level with relaxed agent-scope atomics (sc1 loads and stores),
+    // ordered by waiting for the stores before the flag: no cache-wide writeback or invalidate (an agent-scope fence
+    // would flush or invalidate the whole L2 of the XCD under the other workgroups' operand panels).
+    if (publish >= 0) {
+        uint64_t* w = reinterpret_cast<uint64_t*>(sk->ws + size_t(publish) * NT * NACC) + tid;
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+            for (int tb = 0; tb < TB; ++tb) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    // (bit-casts from scalars: this compiler miscompiles a bit-cast of a vector element)
+                    const float lo = acc[cb][tb][2 * j], hi = acc[cb][tb][2 * j + 1];
+                    const uint64_t bits =
+                        uint64_t(__builtin_bit_cast(uint32_t, lo)) | uint64_t(__builtin_bit_cast(uint32_t, hi)) << 32;
+                    __hip_atomic_store(w + ((cb * TB + tb) * 8 + j) * NT, bits, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+                }
+                __builtin_amdgcn_sched_barrier(0); // one block at a time: few registers in flight
+            }
+        __builtin_amdgcn_s_waitcnt(0); // every store acknowledged at the coherent level
+        __syncthreads();
+        if (tid == 0)
+            __hip_atomic_store(sk->flags + publish, sk->epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
+    if (fix_hi >= fix_lo) {
+        if (tid == 0)
+            for (int i = fix_lo; i <= fix_hi; ++i) {
+                if (i == self)
+                    continue;
+                // every other range of the tile belongs to a workgroup dispatched before this one (the owner is
+                // the tile's highest workgroup), and a workgroup publishes before it waits on anything; the bound
+                // only keeps a broken launch from spinning forever
+                const int slot = sk_slot(*sk, uint32_t(i), tt);
+                for (uint32_t n = 0; n < (1u << 26); ++n) {
+                    if (__hip_atomic_load(sk->flags + slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == sk->epoch)
+                        break;
+                    __builtin_amdgcn_s_sleep(2);
+                }
+            }
+        __syncthreads();
+        // one accumulator block at a time, the other ranges' partials added in index order
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+            for (int tb = 0; tb < TB; ++tb) {
+                for (int i = fix_lo; i <= fix_hi; ++i) {
+                    if (i == self)
+                        continue;
+                    uint64_t* w =
+                        reinterpret_cast<uint64_t*>(sk->ws + size_t(sk_slot(*sk, uint32_t(i), tt)) * NT * NACC) + tid;
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        const uint64_t bits = __hip_atomic_load(w + ((cb * TB + tb) * 8 + j) * NT, __ATOMIC_RELAXED,
+                                                                __HIP_MEMORY_SCOPE_AGENT);
+                        acc[cb][tb][2 * j] += __builtin_bit_cast(float, uint32_t(bits));
+                        acc[cb][tb][2 * j + 1] += __builtin_bit_cast(float, uint32_t(bits >> 32));
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+    }
+
     // ---- epilogue through LDS: per 32-token block, each wave stages its 32 x WC slice (fp32, padded rows) in a
     // region of its own, then reads it back with the lanes along the channels. A wave's LDS operations complete in
     // order, so the slices need no barrier (a __syncthreads() here would also wait for every global store in flight:
     // its release fence waits for vmcnt 0) ----
     float* st = reinterpret_cast<float*>(smem) + wave * 32 * LDW;
-    const int64_t zc = int64_t(blockIdx.z) * p.sc;
+    const int64_t zc = int64_t(z) * p.sc;
     if constexpr (EK == EK_HEADS) {
         // the heads epilogue is large: one copy of it in a rolled loop over the 32-token blocks, which always
         // stages block 0 of the accumulators and then rotates the next block into its place (static register
@@ -508,7 +613,7 @@ __global__ __launch_bounds__(64 * NW, 1) __attribute__((amdgpu_waves_per_eu(NW /
                 for (int i = 0; i < 4; ++i)
                     *reinterpret_cast<f32x4*>(st + r32 * LDW + cb * 32 + 8 * i + 4 * hk) =
                         f32x4{acc[cb][0][4 * i], acc[cb][0][4 * i + 1], acc[cb][0][4 * i + 2], acc[cb][0][4 * i + 3]};
-            epi_heads(p, st, LDW, m0 + wm * WM + tb * 32, n0 + wn * WC, lane);
+            epi_heads(p, st, LDW, m0 + wm * WM + tb * 32, n0 + wn * WC, lane, z);
 #pragma unroll
             for (int cb = 0; cb < CB; ++cb)
 #pragma unroll
@@ -530,21 +635,153 @@ __global__ __launch_bounds__(64 * NW, 1) __attribute__((amdgpu_waves_per_eu(NW /
     }
 }
 
-template <int BM, int BN, bool kF8, int EK, int NW = 4>
-hipError_t launch(GemmP* p, uint32_t count, hipStream_t s)
+
+template <int BM, int BN, int NW>
+constexpr int gemm_smem()
 {
+    constexpr int LDW = BN / 2 + 4;
+    return 2 * (BN + BM) * 64 * 2 > NW * 32 * LDW * 4 ? 2 * (BN + BM) * 64 * 2 : NW * 32 * LDW * 4;
+}
+
+// One tile a workgroup.
+template <int BM, int BN, bool kF8, int EK, int NW>
+__global__ __launch_bounds__(64 * NW, 1) __attribute__((amdgpu_waves_per_eu(NW / 4, NW / 4))) void gemm_kernel(GemmG G)
+{
+    __shared__ __attribute__((aligned(16))) uint16_t smem[gemm_smem<BM, BN, NW>() / 2];
+    uint32_t z, tm, tn;
+    const GemmP& p = locate(G, xcd_order(blockIdx.x, gridDim.x), z, tm, tn);
+    gemm_tile<BM, BN, kF8, EK, NW>(p, z, tm, tn, 0, int(p.K) / BK, smem, nullptr, -1);
+}
+
+// Persistent stream-K: a grid of one workgroup a CU takes the first sk.dp tiles whole (round robin), then splits
+// the rest's k steps evenly into one range a workgroup. A tile split over several ranges is finished by the one
+// held by the highest workgroup: it adds the partials the others publish. Waits thus only ever point at workgroups
+// dispatched earlier, which publish before they wait on anything, so the launch always completes.
+template <int BM, int BN, bool kF8, int EK, int NW>
+__global__ __launch_bounds__(64 * NW, 1) __attribute__((amdgpu_waves_per_eu(NW / 4, NW / 4))) void gemm_sk_kernel(
+    GemmG G, SkP sk)
+{
+    __shared__ __attribute__((aligned(16))) uint16_t smem[gemm_smem<BM, BN, NW>() / 2];
+    const uint32_t w = blockIdx.x, grid = gridDim.x;
+    for (uint32_t t = w; t < sk.dp; t += grid) {
+        uint32_t z, tm, tn;
+        const GemmP& p = locate(G, xcd_order(t, sk.dp), z, tm, tn);
+        __syncthreads(); // the previous tile's epilogue is done with the LDS
+        gemm_tile<BM, BN, kF8, EK, NW>(p, z, tm, tn, 0, int(sk.kt), smem, nullptr, -1);
+    }
+    // the tail: this workgroup's range (virtual index v), two passes over its tiles: first the ranges it publishes,
+    // then the tiles it owns (the tile's range held by its highest workgroup, which adds the others' partials)
+    const uint32_t per = grid / 8;
+    const uint32_t v = grid % 8 ? w : (w % 8) * per + w / 8;
+    const uint64_t b = sk_begin(sk, v), e = sk_begin(sk, v + 1);
+    if (b < e) {
+        const uint64_t t0 = b / sk.kt, t1 = (e - 1) / sk.kt;
+        for (int pass = 0; pass < 2; ++pass)
+            for (uint64_t tt = t1 + 1; tt-- > t0;) {
+                const uint64_t ts = tt * sk.kt, lo = ts > b ? ts : b, hi = ts + sk.kt < e ? ts + sk.kt : e;
+                // the ranges of this tile: virtual indices lo_i .. hi_i
+                uint32_t lo_i = v, hi_i = v;
+                while (lo_i > 0 && sk_begin(sk, lo_i) > ts)
+                    --lo_i;
+                while (hi_i + 1 < grid && sk_begin(sk, hi_i + 1) < ts + sk.kt)
+                    ++hi_i;
+                uint32_t owner = lo_i;
+                for (uint32_t i = lo_i + 1; i <= hi_i; ++i)
+                    if (sk_phys(i) > sk_phys(owner))
+                        owner = i;
+                const bool own = owner == v;
+                if (own != (pass == 1))
+                    continue;
+                uint32_t z, tm, tn;
+                const GemmP& p = locate(G, sk.dp + uint32_t(tt), z, tm, tn);
+                __syncthreads();
+                if (own)
+                    gemm_tile<BM, BN, kF8, EK, NW>(p, z, tm, tn, int(lo - ts), int(hi - ts), smem, &sk, -1,
+                                                   int(lo_i), int(hi_i), int(v), tt);
+                else
+                    gemm_tile<BM, BN, kF8, EK, NW>(p, z, tm, tn, int(lo - ts), int(hi - ts), smem, &sk,
+                                                   sk_slot(sk, v, tt));
+            }
+    }
+}
+
+// Stream-K workspace of a device: two partial slots and flags per workgroup of a one-a-CU grid, and the launch epoch
+// the flags are compared with (so they never need clearing). Launches that use it on one device must not overlap.
+// It is uncached device memory: a partial written by a CU of one XCD is read by a CU of another, whose L2 is not
+// coherent with the writer's for ordinary allocations. Allocated once at its full size and never freed (uncached
+// memory a kernel has read stays allocated until the process ends).
+struct SkWork {
+    float* ws = nullptr;
+    size_t ws_bytes = 0;
+    uint32_t* flags = nullptr;
+    uint32_t nflags = 0, epoch = 0, cus = 0;
+};
+constexpr int kMaxDevices = 64;
+std::mutex g_sk_mutex;
+SkWork g_sk[kMaxDevices];
+
+template <int BM, int BN, bool kF8, int EK, int NW = 4>
+mk_status launch(GemmP* p, uint32_t count, hipStream_t s)
+{
+    constexpr int NT = 64 * NW, NACC = (BN / 64) * (BM / (NW / 2) / 32) * 16;
     GemmG G{};
-    uint32_t tiles = 0, batch = 0;
+    uint32_t tiles = 0;
     for (uint32_t i = 0; i < count; ++i) {
         p[i].tiles_m = cdiv(p[i].M, BM);
         p[i].tiles_n = p[i].N / BN;
         G.g[i] = p[i];
-        tiles += p[i].tiles_m * p[i].tiles_n;
-        batch = max(batch, p[i].batch);
+        tiles += p[i].tiles_m * p[i].tiles_n * p[i].batch;
     }
-    G.tiles0 = count > 1 ? p[0].tiles_m * p[0].tiles_n : tiles;
-    gemm_kernel<BM, BN, kF8, EK, NW><<<dim3(tiles, 1, batch), 64 * NW, 0, s>>>(G);
-    return hipGetLastError();
+    G.tiles0 = count > 1 ? p[0].tiles_m * p[0].tiles_n * p[0].batch : tiles;
+    const uint32_t kt = p[0].K / BK;
+    if constexpr (BN == 256) {
+        int dev = 0;
+        MK_HIP(hipGetDevice(&dev));
+        if (dev < 0 || dev >= kMaxDevices)
+            return fail(MK_ERR_DEVICE, "gemm: device index out of range");
+        std::lock_guard<std::mutex> lock(g_sk_mutex);
+        SkWork& W = g_sk[dev];
+        if (!W.cus) {
+            int n = 0;
+            MK_HIP(hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev));
+            W.cus = n > 0 ? uint32_t(n) : 1;
+        }
+        // stream-K when whole tiles would leave a twentieth or more of the launch's CU time idle in its last wave;
+        // all but one full wave go round robin, the rest is split by k steps (at least 4 a workgroup)
+        const uint32_t grid = W.cus, waves = tiles / grid, rounds = (tiles + grid - 1) / grid;
+        const uint64_t idle = uint64_t(rounds) * grid - tiles;
+        if (waves >= 1 && idle * 20 >= uint64_t(rounds) * grid) {
+            SkP sk{};
+            sk.total = tiles;
+            sk.dp = (waves - 1) * grid;
+            sk.kt = kt;
+            sk.units = uint64_t(tiles - sk.dp) * kt;
+            if (sk.units >= uint64_t(4) * grid) {
+                const size_t need = size_t(2) * grid * NT * NACC * sizeof(float);
+                if (!W.ws) {
+                    MK_HIP(hipExtMallocWithFlags(reinterpret_cast<void**>(&W.ws), need, hipDeviceMallocUncached));
+                    W.ws_bytes = need;
+                    MK_HIP(hipExtMallocWithFlags(reinterpret_cast<void**>(&W.flags), 2 * grid * sizeof(uint32_t),
+                                                 hipDeviceMallocUncached));
+                    MK_HIP(hipMemset(W.flags, 0, 2 * grid * sizeof(uint32_t)));
+                    W.nflags = 2 * grid;
+                }
+                if (W.ws_bytes < need || W.nflags < 2 * grid)
+                    return fail(MK_ERR_UNSUPPORTED, "gemm: stream-K workspace smaller than this launch needs");
+                if (++W.epoch == 0)
+                    W.epoch = 1;
+                sk.ws = W.ws;
+                sk.flags = W.flags;
+                sk.epoch = W.epoch;
+                gemm_sk_kernel<BM, BN, kF8, EK, NW><<<grid, NT, 0, s>>>(G, sk);
+                MK_HIP(hipGetLastError());
+                return MK_OK;
+            }
+        }
+    }
+    gemm_kernel<BM, BN, kF8, EK, NW><<<tiles, NT, 0, s>>>(G);
+    MK_HIP(hipGetLastError());
+    return MK_OK;
 }
 
 // The epilogue kind of an mk_epilogue.
@@ -640,12 +877,19 @@ extern "C" mk_status mk_gemm_grouped(const mk_gemm_args* a, uint32_t count, void
     uint64_t tiles256 = 0;
     for (uint32_t i = 0; i < n; ++i)
         tiles256 += uint64_t(cdiv(p[i].M, 256)) * p[i].batch * (a[0].N / 256);
-    // tile: 256 x 256 where the grid fills the chip, else 256 x 128, else 256 x 64 (N = 64: stores, residuals)
-    const int bn = ek == EK_HEADS ? 256 : (a[0].N % 256 == 0 && tiles256 >= 512) ? 256 : a[0].N % 128 == 0 ? 128 : 64;
+    // tile: 256 x 256 once there is a wave of them (stream-K balances the last), else 256 x 128, else 256 x 64 (N =
+    // 64: stores, residuals)
+    int cus = 0, dev = 0;
+    MK_HIP(hipGetDevice(&dev));
+    MK_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    const int bn = ek == EK_HEADS                                       ? 256
+                   : (a[0].N % 256 == 0 && tiles256 >= uint64_t(cus)) ? 256
+                   : a[0].N % 128 == 0                                  ? 128
+                                                                        : 64;
     if (bn == 64 && ek == EK_ACT)
         return fail(MK_ERR_UNSUPPORTED, "gemm: activation epilogues need N a multiple of 128");
     hipStream_t s = static_cast<hipStream_t>(stream);
-    hipError_t e;
+    mk_status e;
 #define MK_GEMM_EK(BN, EK) e = f8 ? launch<256, BN, true, EK>(p, n, s) : launch<256, BN, false, EK>(p, n, s)
     if (ek == EK_HEADS) {
         MK_GEMM_EK(256, EK_HEADS);
@@ -670,9 +914,7 @@ extern "C" mk_status mk_gemm_grouped(const mk_gemm_args* a, uint32_t count, void
             MK_GEMM_EK(64, EK_RMW);
     }
 #undef MK_GEMM_EK
-    if (e != hipSuccess)
-        return hip_check(e, "gemm launch");
-    return MK_OK;
+    return e;
 }
 
 extern "C" mk_status mk_gemm(const mk_gemm_args* a, void* stream) { return mk_gemm_grouped(a, 1, stream); }

@@ -265,6 +265,81 @@ def test_gemm_grouped_heads_and_gelu(gpu, rng):
     assert b"equal N" in M.lib().mk_last_error()
 
 
+# Stream-K: launches of a wave or more of 256 x 256 tiles whose last wave would leave CUs idle split the tail's k
+# steps over the whole chip (partials published by one workgroup, added by the one closing the tile).
+@pytest.mark.parametrize("epi,cdt,w8", [(M.EPI_GATE_ADD, M.F32, False), (M.EPI_GATE_ADD, M.F32, True),
+                                        (M.EPI_GELU_TANH, M.BF16, False)])
+def test_gemm_stream_k_matches_oracle_and_repeats(gpu, rng, epi, cdt, w8):
+    N = 3072 if epi == M.EPI_GATE_ADD else 12288
+    K = 256
+    shapes = ((8192, 1), (512, 1))  # 34 token tiles: 408 (or 1632) tiles, 1.6 (6.4) waves
+    A = [rng.standard_normal((Mr, K)).astype(np.float32) for Mr, _ in shapes]
+    if w8:
+        Wf = rng.standard_normal((N, K)).astype(np.float32) * 0.05
+        scale = (np.abs(Wf).max(1) / 448).astype(np.float32)
+        table = R.e4m3_table()
+        mags, a = table[:127], np.abs(Wf / scale[:, None])
+        i = np.clip(np.searchsorted(mags, a), 1, 126)
+        near = np.where(a - mags[i - 1] <= mags[i] - a, i - 1, i).astype(np.uint8)
+        codes = near | np.where(Wf < 0, 0x80, 0).astype(np.uint8)
+        Wq, Wd, sd = table[codes] * scale[:, None], dev(codes), dev(scale)
+    else:
+        Wq = R.bf16_round(rng.standard_normal((N, K)).astype(np.float32) * 0.05)
+        Wd, sd = bdev(Wq), None
+    b = dev(rng.standard_normal(N).astype(np.float32))
+    gt = rng.standard_normal(N).astype(np.float32)
+    X = [rng.standard_normal((Mr, N)).astype(np.float32) for Mr, _ in shapes]
+    outs = []
+    for rep in range(2):
+        cs = [dev(x) if epi == M.EPI_GATE_ADD else M.Dev(Mr * N * 2) for x, (Mr, _) in zip(X, shapes)]
+        _live.extend(cs)
+        args = [gemm_args(bdev(a), Wd, bias=b, wscale=sd, c=c, c_dtype=cdt, epi=epi, M_=(Mr, N, K), lda=K, ldc=N,
+                          gate=dev(gt), w_dtype=M.FP8 if w8 else M.BF16)
+                for a, c, (Mr, _) in zip(A, cs, shapes)]
+        gemm_grouped(*args)
+        outs.append([fetch(c, (Mr, N)) if cdt == M.F32 else fetch_bf16(c, (Mr, N)) for c, (Mr, _) in zip(cs, shapes)])
+    bias = fetch(b, (N,))
+    for i, (Mr, _) in enumerate(shapes):
+        assert np.array_equal(outs[0][i], outs[1][i])  # the fixed reduction order repeats bit for bit
+        y = R.gemm(A[i], Wq, bias)
+        if epi == M.EPI_GATE_ADD:
+            assert maxrel(outs[0][i], X[i].astype(np.float64) + gt * y) < 1e-5
+        else:
+            want = R.gelu_tanh(y)
+            assert np.abs(outs[0][i] - want).max() <= 2 ** -8 * np.abs(want).max() + 1e-6
+
+
+def test_gemm_stream_k_heads(gpu, rng):
+    # the QKV heads epilogue on 4.5 waves of tiles: 2 x 4096 rows, 24 heads
+    B, Mr, H, K_ = 2, 4096, 24, 256
+    D = H * 128
+    q_pad = k_pad = 4096
+    A = rng.standard_normal((B, Mr, K_)).astype(np.float32)
+    W = R.bf16_round(rng.standard_normal((3 * D, K_)).astype(np.float32) * 0.05)
+    bb = rng.standard_normal(3 * D).astype(np.float32) * 0.1
+    nq = (1 + 0.1 * rng.standard_normal(128)).astype(np.float32)
+    nk = (1 + 0.1 * rng.standard_normal(128)).astype(np.float32)
+    cs = R.rope_table(0, 64, 64)
+    Q, Kd, Vt = M.Dev(B * H * q_pad * 256), M.Dev(B * H * k_pad * 256), M.Dev(B * H * k_pad * 256)
+    _live.extend([Q, Kd, Vt])
+    ha = M.HeadsArgs(Q.p, Kd.p, Vt.p, H, 128, q_pad, k_pad, 0, 0, dev(nq).p, dev(nk).p, dev(cs).p, 2, 1e-6, 0.0)
+    gemm(bdev(A), bdev(W), bias=dev(bb), epi=M.EPI_HEADS, c_dtype=M.BF16, M_=(Mr, 3 * D, K_), batch=B, lda=K_,
+         sa=Mr * K_, heads=ha)
+    rows = np.sort(rng.choice(Mr, 200, replace=False))
+    gq = fetch_bf16(Q, (B, H, q_pad, 128))
+    gk = fetch_bf16(Kd, (B, H, k_pad, 128))
+    gv = fetch_bf16(Vt, (B, H, 128, k_pad))
+    for bi in range(B):
+        y = R.gemm(A[bi][rows], W, bb)
+        tab = cs[rows]
+        wq = R.heads_norm_rope(y, H, 128, col0=0, w=nq, cs=tab, rope=2)
+        wk = R.heads_norm_rope(y, H, 128, col0=D, w=nk, cs=tab, rope=2)
+        wv = R.heads_norm_rope(y, H, 128, col0=2 * D)
+        for got, want in ((gq[bi][:, rows], wq), (gk[bi][:, rows], wk),
+                          (gv[bi][:, :, M.vt_col(rows)].transpose(0, 2, 1), wv)):
+            assert np.abs(got - want).max() <= 2 ** -8 * np.abs(want).max() + 1e-6
+
+
 def test_vt_col_is_an_involution_within_groups():
     k = np.arange(4096)
     assert np.array_equal(M.vt_col(M.vt_col(k)), k)
