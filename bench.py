@@ -36,6 +36,18 @@ def step_flops(blocks=60, D=3072, F=12288, N=4096, S=256, B=2, heads=24):
     return B * blocks * (lin + attn), B * blocks * lin, B * blocks * attn
 
 
+def gemm_traffic():
+    """HBM-side bytes per GEMM launch (L2 fetch + write, calibrated against a copy of known size), from the committed
+    rocprofv3 counter summary of this build's step; None when the summary is absent."""
+    f = ROOT / "profiles" / "mmdit_step_1024_traffic.md"
+    if not f.exists():
+        return None
+    for line in f.read_text().splitlines():
+        if line.startswith("gemm_bytes_per_launch:"):
+            return int(line.split(":")[1])
+    return None
+
+
 def cpu_baseline(seconds_target=12.0):
     """The oracle on one dual-stream block of one sample at a reduced image size (32 x 32 tokens + 256 text), timed
     on this host; throughput scaled to the full step's FLOPs."""
@@ -154,7 +166,8 @@ def main():
                    "image_tokens": H * W, "text_tokens": S, "batch": 2, "weights": "bf16"},
         "roofline": {"bound": "mfma", "kernel": "gemm (bf16 MFMA, all block and projection GEMMs)",
                      "achieved": round(gemm_tf, 1), "peak": PEAK_BF16 / 1e12, "unit": "TFLOP/s",
-                     "frac": round(gemm_tf * 1e12 / PEAK_BF16, 4), "traffic": None},
+                     "frac": round(gemm_tf * 1e12 / PEAK_BF16, 4), "traffic": gemm_traffic(),
+                     "traffic_unit": "bytes/launch (profiles/mmdit_step_1024_traffic.md)"},
         "attention_gemm_mfma_frac": round(both / PEAK_BF16, 4),
         "step_mfma_frac": round(total / (ms / 1e3) / PEAK_BF16, 4),
         "attention": {"achieved": round(attn_tf, 1), "unit": "TFLOP/s", "frac": round(attn_tf * 1e12 / PEAK_BF16, 4)},
