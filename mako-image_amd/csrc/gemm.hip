@@ -890,7 +890,10 @@ extern "C" mk_status mk_gemm_grouped(const mk_gemm_args* a, uint32_t count, void
         return fail(MK_ERR_UNSUPPORTED, "gemm: activation epilogues need N a multiple of 128");
     hipStream_t s = static_cast<hipStream_t>(stream);
     mk_status e;
-#define MK_GEMM_EK(BN, EK) e = f8 ? launch<256, BN, true, EK>(p, n, s) : launch<256, BN, false, EK>(p, n, s)
+    // 256-wide tiles with bf16 weights: 8 waves (two a SIMD, 64 x 128 wave tiles), so one wave's waits (barrier,
+    // loads) leave the other's MFMAs running; fp8 weights stage through registers and keep 4 waves
+#define MK_GEMM_EK(BN, EK)                                                                                        \
+    e = f8 ? launch<256, BN, true, EK, 4>(p, n, s) : launch<256, BN, false, EK, BN == 256 ? 8 : 4>(p, n, s)
     if (ek == EK_HEADS) {
         MK_GEMM_EK(256, EK_HEADS);
     } else if (bn == 256) {
