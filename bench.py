@@ -24,6 +24,14 @@ sys.path[:0] = [str(ROOT / "mako-image_amd"), str(ROOT / "oracle")]
 METRIC = "s/denoise-step Qwen-Image MMDiT 1024² bf16; attention+GEMM % of MFMA peak"
 PEAK_BF16 = 2.5e15  # MI355X dense bf16 MFMA, published
 CFG = dict(blocks=60, dim=3072, heads=24, head_dim=128, ffn=12288, text_dim=3584)
+# (latent grid side, text tokens, weight dtype) of each workload; the default is the metric's (1024x1024, bf16)
+WORKLOADS = {
+    "mmdit-1024-bf16": dict(side=64, text=256, fp8=False,
+                            name="Qwen-Image-shaped dual-stream MMDiT denoise step at 1024x1024, CFG batch 2"),
+    "mmdit-2048-fp8": dict(side=128, text=512, fp8=True,
+                           name="Qwen-Image-shaped dual-stream MMDiT denoise step at 2048x2048, CFG batch 2, "
+                                "fp8-e4m3 linear weights with per-channel scales"),
+}
 H = W = 64
 S = 256
 
@@ -48,14 +56,14 @@ def gemm_traffic():
     return None
 
 
-def cpu_baseline(seconds_target=12.0):
-    """The oracle on one dual-stream block of one sample at a reduced image size (32 x 32 tokens + 256 text), timed
-    on this host; throughput scaled to the full step's FLOPs."""
+def cpu_baseline(seconds_target=12.0, fp8=False):
+    """The oracle on one dual-stream block of one sample at a reduced image size (32 x 32 tokens + the workload's text
+    tokens), timed on this host; throughput scaled to the full step's FLOPs."""
     import numpy as np
 
     import mkref as R
 
-    m = R.Model(R.DUAL, **{**CFG, "blocks": 1}, seed=0)
+    m = R.Model(R.DUAL, **{**CFG, "blocks": 1}, fp8=fp8, seed=0)
     rng = np.random.default_rng(0)
     n_side = 32
     N = n_side * n_side
@@ -72,10 +80,12 @@ def cpu_baseline(seconds_target=12.0):
         t_total += time.perf_counter() - t0
         reps += 1
     rate = flops * reps / t_total
-    return {"value": step_flops()[0] / rate, "unit": "s/step", "cores": R.lib().mkref_threads(), "kind": "port",
-            "sample": f"oracle (C++/OpenMP, fp32 over bf16 weights): {reps} x one dual-stream block of one sample at "
+    return {"value": step_flops(N=H * W, S=S)[0] / rate, "unit": "s/step", "cores": R.lib().mkref_threads(),
+            "kind": "port",
+            "sample": f"oracle (C++/OpenMP, fp32 over {'fp8' if fp8 else 'bf16'} weights): {reps} x one dual-stream "
+                      f"block of one sample at "
                       f"{N} image + {S} text tokens ({flops / 1e9:.0f} GFLOP each, {t_total:.1f} s, "
-                      f"{rate / 1e9:.1f} GFLOP/s), scaled by FLOPs to the 60-block batch-2 step at 4096 + 256 tokens"}
+                      f"{rate / 1e9:.1f} GFLOP/s), scaled by FLOPs to the 60-block batch-2 step at {H * W} + {S} tokens"}
 
 
 def main():
@@ -85,7 +95,12 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="mmdit-1024-bf16")
     args = ap.parse_args()
+    wl = WORKLOADS[args.workload]
+    global H, W, S
+    H = W = wl["side"]
+    S = wl["text"]
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py measures one GPU: this build runs the step on one MI355X (asked for {max(args.gpus, world)}); "
@@ -98,7 +113,7 @@ def main():
 
     M.call("mk_set_device", 0)
     info = M.device_info()
-    eng = M.Engine(M.FAMILY_DUAL, **CFG)
+    eng = M.Engine(M.FAMILY_DUAL, **CFG, weight_dtype=M.FP8 if wl["fp8"] else M.BF16)
     t0 = time.perf_counter()
     eng.init_random(0)
     t_init = time.perf_counter() - t0
@@ -140,7 +155,7 @@ def main():
             acc["launches"] += v["launches"]
             acc["flops"] += v["flops"]
     eng.set_timing(False)
-    total, lin, attn = step_flops()
+    total, lin, attn = step_flops(N=H * W, S=S)
     g, a = per["gemm"], per["attention"]
     gemm_tf = g["flops"] / (g["ms"] / 1e3) / 1e12
     attn_tf = a["flops"] / (a["ms"] / 1e3) / 1e12
@@ -161,9 +176,9 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic (random-init N(0,0.02) weights, N(0,1) latents and prompts)",
-        "config": {"workload": "Qwen-Image-shaped dual-stream MMDiT denoise step at 1024x1024, CFG batch 2",
-                   "blocks": 60, "dim": 3072, "heads": 24, "head_dim": 128, "ffn": 12288, "text_dim": 3584,
-                   "image_tokens": H * W, "text_tokens": S, "batch": 2, "weights": "bf16"},
+        "config": {"workload": wl["name"], "blocks": 60, "dim": 3072, "heads": 24, "head_dim": 128, "ffn": 12288,
+                   "text_dim": 3584, "image_tokens": H * W, "text_tokens": S, "batch": 2,
+                   "weights": "fp8-e4m3" if wl["fp8"] else "bf16"},
         "roofline": {"bound": "mfma", "kernel": "gemm (bf16 MFMA, all block and projection GEMMs)",
                      "achieved": round(gemm_tf, 1), "peak": PEAK_BF16 / 1e12, "unit": "TFLOP/s",
                      "frac": round(gemm_tf * 1e12 / PEAK_BF16, 4), "traffic": gemm_traffic(),
@@ -178,8 +193,11 @@ def main():
         "weights_gb": round(eng.weight_bytes() / 1e9, 2),
         "init_s": round(t_init, 2),
     }
+    if wl["fp8"]:
+        line["roofline"]["kernel"] = "gemm (fp8-e4m3 weights converted to bf16 in LDS, bf16 MFMA)"
+        line["roofline"]["traffic"] = None
     if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+        line["cpu_baseline"] = cpu_baseline(args.cpu_seconds, wl["fp8"])
     print(json.dumps(line), flush=True)
 
 

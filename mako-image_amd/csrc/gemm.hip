@@ -55,17 +55,19 @@ constexpr int BK = 64;
 __device__ inline int swz_chunk(int row, int kc) { return kc ^ ((row >> 1) & 7); }
 __device__ inline int swz(int row, int kc) { return row * 64 + (swz_chunk(row, kc) << 3); }
 
-// fp8 e4m3 (16 values in a u32x4) -> two bf16x8 chunks, exact.
+// fp8 e4m3 (16 values in a u32x4) -> two bf16x8 chunks, exact (every e4m3 value is a bf16 value): gfx950's
+// conversion instruction, two values each.
+typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
 __device__ inline void f8x16_to_bf16(const u32x4& v, u32x4& lo, u32x4& hi)
 {
     uint32_t o[8];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const uint32_t x = v[i];
-        const float f0 = e4m3_to_f32(uint8_t(x)), f1 = e4m3_to_f32(uint8_t(x >> 8));
-        const float f2 = e4m3_to_f32(uint8_t(x >> 16)), f3 = e4m3_to_f32(uint8_t(x >> 24));
-        o[2 * i] = (__builtin_bit_cast(uint32_t, f0) >> 16) | (__builtin_bit_cast(uint32_t, f1) & 0xffff0000u);
-        o[2 * i + 1] = (__builtin_bit_cast(uint32_t, f2) >> 16) | (__builtin_bit_cast(uint32_t, f3) & 0xffff0000u);
+        const bf16x2v a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(x, 1.0f, false); // bytes 0, 1
+        const bf16x2v b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(x, 1.0f, true);  // bytes 2, 3
+        o[2 * i] = __builtin_bit_cast(uint32_t, a);
+        o[2 * i + 1] = __builtin_bit_cast(uint32_t, b);
     }
     lo = u32x4{o[0], o[1], o[2], o[3]};
     hi = u32x4{o[4], o[5], o[6], o[7]};
@@ -890,10 +892,11 @@ extern "C" mk_status mk_gemm_grouped(const mk_gemm_args* a, uint32_t count, void
         return fail(MK_ERR_UNSUPPORTED, "gemm: activation epilogues need N a multiple of 128");
     hipStream_t s = static_cast<hipStream_t>(stream);
     mk_status e;
-    // 256-wide tiles with bf16 weights: 8 waves (two a SIMD, 64 x 128 wave tiles), so one wave's waits (barrier,
-    // loads) leave the other's MFMAs running; fp8 weights stage through registers and keep 4 waves
+    // 256-wide tiles: 8 waves (two a SIMD, 64 x 128 wave tiles), so one wave's waits (barrier, loads) leave the
+    // other's MFMAs running
 #define MK_GEMM_EK(BN, EK)                                                                                        \
-    e = f8 ? launch<256, BN, true, EK, 4>(p, n, s) : launch<256, BN, false, EK, BN == 256 ? 8 : 4>(p, n, s)
+    e = f8 ? launch<256, BN, true, EK, BN == 256 ? 8 : 4>(p, n, s)                                                 \
+           : launch<256, BN, false, EK, BN == 256 ? 8 : 4>(p, n, s)
     if (ek == EK_HEADS) {
         MK_GEMM_EK(256, EK_HEADS);
     } else if (bn == 256) {

@@ -205,3 +205,27 @@ def test_generate_unguided_matches_oracle_euler(gpu):
     within(got - lat[0], x - lat[0], 64)
     with pytest.raises(M.MkError, match="begin both"):
         e.generate(lat[0], sig, 3.0)
+
+
+FULL = dict(blocks=1, dim=3072, heads=24, head_dim=128, ffn=12288, text_dim=3584)
+
+
+@pytest.mark.parametrize("fp8,side", [(False, 64), (True, 32)])
+def test_full_size_block_matches_oracle(gpu, fp8, side):
+    # the benchmark's shapes (hidden 3072, 24 x 128 heads, FFN 12288, 4096 image + 256 text tokens of width 3584; the
+    # fp8 case at 1024 image tokens to keep the oracle quick), one block, one sample: the GPU step (device-initialised
+    # weights, bit-equal to the oracle's) against the oracle
+    m = R.Model(R.DUAL, **FULL, fp8=fp8, seed=11)
+    e = M.Engine(M.FAMILY_DUAL, **FULL, weight_dtype=M.FP8 if fp8 else M.BF16)
+    e.init_random(11)
+    rng = np.random.default_rng(12)
+    prompt = rng.standard_normal((256, 3584)).astype(np.float32)
+    lat = rng.standard_normal((side * side, 64)).astype(np.float32)
+    e.begin(prompt, side, side, 0)
+    got_p, want_p = {}, {}
+    e.set_probe(got_p)
+    got = e.step(lat, 0.8, 0)
+    want = m.dual_step(prompt[None], lat[None], side, side, 0.8, want_p)[0]
+    tol = 5e-2 if fp8 else 2e-2
+    within(got_p[("block", 0)], want_p[("block", 0)], 3072, max_rel=tol)
+    within(got, want, 64, max_rel=tol)

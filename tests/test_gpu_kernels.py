@@ -142,6 +142,23 @@ def test_gemm_fp8_weights(gpu, rng):
     assert maxrel(fetch(out, (Mr, N)), R.gemm(A, q, b, wscale=scale)) < 1e-5
 
 
+def test_gemm_fp8_every_code(gpu):
+    # one-hot activations pick single weight columns: C[m][n] = e4m3(code m) * scale[n], exactly, for every
+    # non-NaN code (the fp8 -> bf16 conversion on the way into LDS is exact)
+    table = R.e4m3_table()
+    codes = np.arange(256, dtype=np.uint8)
+    codes[np.isnan(table)] = 0
+    N, K = 64, 256
+    W = np.tile(codes, (N, 1))
+    A = np.eye(K, dtype=np.float32)
+    scale = np.linspace(0.5, 2.0, N).astype(np.float32)
+    out = M.Dev(K * N * 4)
+    _live.append(out)
+    gemm(bdev(A), dev(W), wscale=dev(scale), c=out, M_=(K, N, K), lda=K, ldc=N, w_dtype=M.FP8)
+    want = (table[codes][:, None].astype(np.float32) * scale[None, :]).astype(np.float32)
+    assert np.array_equal(fetch(out, (K, N)), want)
+
+
 @pytest.mark.parametrize("mode,row0,q_row0,k_scale", [(2, 40, 40, 0.0), (1, 0, 0, 0.0), (0, 17, 0, 0.0),
                                                       (2, 40, 40, 0.3)])
 def test_gemm_heads_epilogue(gpu, rng, mode, row0, q_row0, k_scale):
