@@ -65,6 +65,55 @@ __global__ __launch_bounds__(256) void ln_modulate_kernel(const float* __restric
     }
 }
 
+// ln_modulate for rows of exactly 256 NV floats: the lane's NV float4s of scale and shift are loaded before the row's
+// statistics are reduced (their L2 latency overlaps the row's HBM read), and the register arrays are sized to the row.
+template <int NV>
+__global__ __launch_bounds__(256) void ln_modulate_nv_kernel(const float* __restrict__ x, uint32_t rows,
+                                                             const float* __restrict__ scale,
+                                                             const float* __restrict__ shift, int64_t alt,
+                                                             uint32_t split, uint32_t seg_rows, float eps,
+                                                             uint16_t* __restrict__ y)
+{
+    constexpr uint32_t n = 256 * NV;
+    const uint32_t lane = threadIdx.x & 63, row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows)
+        return;
+    const int64_t off = (row % seg_rows) < split ? alt : 0;
+    const f32x4* sc = reinterpret_cast<const f32x4*>(scale + off);
+    const f32x4* sh = shift ? reinterpret_cast<const f32x4*>(shift + off) : nullptr;
+    const f32x4* xr = reinterpret_cast<const f32x4*>(x + uint64_t(row) * n);
+    f32x4 a[NV], b[NV], v[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        a[i] = sc[lane + 64 * i];
+        b[i] = sh ? sh[lane + 64 * i] : f32x4{0, 0, 0, 0};
+        v[i] = xr[lane + 64 * i];
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+        s += v[i][0] + v[i][1] + v[i][2] + v[i][3];
+    const float mean = wave_sum(s) / float(n);
+    float q = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float d = v[i][j] - mean;
+            q += d * d;
+        }
+    const float inv = rsqrtf(wave_sum(q) / float(n) + eps);
+    u32x2* yr = reinterpret_cast<u32x2*>(y + uint64_t(row) * n);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        float o[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            o[j] = (v[i][j] - mean) * inv * (1.0f + a[i][j]) + b[i][j];
+        yr[lane + 64 * i] = u32x2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+    }
+}
+
 // Layer norm with gamma / beta (sdxl.cpp:425-437), or RMSNorm * (w + w_offset) (rms = 1): bf16 out.
 template <bool kRms>
 __global__ __launch_bounds__(256) void norm_kernel(const float* __restrict__ x, uint32_t rows, uint32_t n,
@@ -307,6 +356,60 @@ __global__ __launch_bounds__(256) void gemv_kernel(const float* __restrict__ x, 
     }
 }
 
+// GEMV for one row with K = 512 * KI: x' is read straight into registers (lane l holds k = 8 l + 512 i), so no LDS
+// staging or barrier precedes the weight stream; each wave computes 4 outputs with all 4 * KI of its 16-byte weight
+// loads issued up front.
+template <int KI>
+__global__ __launch_bounds__(256) void gemv1_kernel(const float* __restrict__ x, const uint16_t* __restrict__ w,
+                                                    const float* __restrict__ bias, uint32_t N, float* __restrict__ y,
+                                                    int silu_x)
+{
+    constexpr uint32_t K = 512 * KI;
+    const uint32_t lane = threadIdx.x & 63, n0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 4;
+    if (n0 >= N)
+        return;
+    u32x4 wv[4][KI];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int i = 0; i < KI; ++i)
+            wv[j][i] = *reinterpret_cast<const u32x4*>(w + uint64_t(min(n0 + j, N - 1)) * K + lane * 8 + 512 * i);
+    float xv[KI][8];
+#pragma unroll
+    for (int i = 0; i < KI; ++i) {
+        const f32x4* xp = reinterpret_cast<const f32x4*>(x + lane * 8 + 512 * i);
+        const f32x4 a = xp[0], b = xp[1];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            xv[i][e] = a[e];
+            xv[i][4 + e] = b[e];
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float v = xv[i][e];
+            xv[i][e] = bf2f_bits(f2bf_bits(silu_x ? v / (1.0f + __expf(-v)) : v)); // the GEMMs' bf16 activation operand
+        }
+    }
+    float acc[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        float s = 0.0f;
+#pragma unroll
+        for (int i = 0; i < KI; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t u = wv[j][i][e];
+                s += bf2f_bits(uint16_t(u)) * xv[i][2 * e] + bf2f_bits(uint16_t(u >> 16)) * xv[i][2 * e + 1];
+            }
+        acc[j] = wave_sum(s);
+    }
+    if (lane < 4) {
+        const float v = lane == 0 ? acc[0] : lane == 1 ? acc[1] : lane == 2 ? acc[2] : acc[3];
+        if (n0 + lane < N)
+            y[n0 + lane] = v + (bias ? bias[n0 + lane] : 0.0f);
+    }
+}
+
 template <int kOp>
 __global__ __launch_bounds__(256) void unary_kernel(float* __restrict__ x, uint64_t n)
 {
@@ -456,8 +559,16 @@ mk_status mk_ln_modulate(const float* x, uint32_t rows, uint32_t n, const float*
         return fail(MK_ERR_ARG, "ln_modulate: null pointer, or n not a multiple of 4 up to 4096, or seg_rows 0");
     if (!rows)
         return MK_OK;
-    ln_modulate_kernel<<<cdiv(rows, 4), 256, 0, S(stream)>>>(x, rows, n, scale, shift, alt, split, seg_rows, eps,
-                                                              static_cast<uint16_t*>(y));
+    uint16_t* yb = static_cast<uint16_t*>(y);
+    const dim3 grid(cdiv(rows, 4));
+    if (n == 3072)
+        ln_modulate_nv_kernel<12><<<grid, 256, 0, S(stream)>>>(x, rows, scale, shift, alt, split, seg_rows, eps, yb);
+    else if (n == 4096)
+        ln_modulate_nv_kernel<16><<<grid, 256, 0, S(stream)>>>(x, rows, scale, shift, alt, split, seg_rows, eps, yb);
+    else if (n == 2048)
+        ln_modulate_nv_kernel<8><<<grid, 256, 0, S(stream)>>>(x, rows, scale, shift, alt, split, seg_rows, eps, yb);
+    else
+        ln_modulate_kernel<<<grid, 256, 0, S(stream)>>>(x, rows, n, scale, shift, alt, split, seg_rows, eps, yb);
     MK_LAUNCH_CHECK("ln_modulate");
     return MK_OK;
 }
@@ -562,8 +673,16 @@ mk_status mk_gemv(const float* x, uint32_t rows, uint32_t K, const void* w, cons
 {
     if (!x || !w || !y || rows == 0 || rows > 4 || K % 8 || uint64_t(rows) * K * 4 > 64 * 1024)
         return fail(MK_ERR_ARG, "gemv: null pointer, rows not 1..4, K not a multiple of 8 or rows*K over 16384");
-    gemv_kernel<<<cdiv(N, 16), 256, rows * K * 4, S(stream)>>>(x, rows, K, static_cast<const uint16_t*>(w), bias, N, y,
-                                                               silu_x);
+    const uint16_t* wb = static_cast<const uint16_t*>(w);
+    const dim3 grid(cdiv(N, 16));
+    if (rows == 1 && K == 3072)
+        gemv1_kernel<6><<<grid, 256, 0, S(stream)>>>(x, wb, bias, N, y, silu_x);
+    else if (rows == 1 && K == 4096)
+        gemv1_kernel<8><<<grid, 256, 0, S(stream)>>>(x, wb, bias, N, y, silu_x);
+    else if (rows == 1 && K == 2048)
+        gemv1_kernel<4><<<grid, 256, 0, S(stream)>>>(x, wb, bias, N, y, silu_x);
+    else
+        gemv_kernel<<<grid, 256, rows * K * 4, S(stream)>>>(x, rows, K, wb, bias, N, y, silu_x);
     MK_LAUNCH_CHECK("gemv");
     return MK_OK;
 }

@@ -444,8 +444,9 @@ def test_attention_golden(gpu):
 # bandwidth-bound kernels
 # ---------------------------------------------------------------------------------------------------------------
 
-def test_ln_modulate(gpu, rng):
-    rows, n = 230, 3072
+@pytest.mark.parametrize("n", [3072, 2048, 4096, 1280])  # row-sized kernels for 2048/3072/4096, generic otherwise
+def test_ln_modulate(gpu, rng, n):
+    rows = 230
     x = (rng.standard_normal((rows, n)) * 3 + 1).astype(np.float32)
     mod = rng.standard_normal((2, 2, n)).astype(np.float32) * 0.3  # row r<split takes mod[1]: [shift, scale]
     y = M.Dev(rows * n * 2)
@@ -497,16 +498,19 @@ def test_heads(gpu, rng, d, mode, transpose):
         assert np.abs(g - want).max() <= 2 ** -8 * np.abs(want).max() + 1e-6
 
 
-def test_gemv_modulation(gpu, rng):
-    K, N = 3072, 6 * 3072 + 64
-    x = rng.standard_normal((1, K)).astype(np.float32)
+# one-row kernels for K in {2048, 3072, 4096}; the LDS-staged kernel for the rest and for rows 2..4
+@pytest.mark.parametrize("rows,K,silu", [(1, 3072, 1), (1, 2048, 0), (1, 4096, 1), (1, 1024, 1), (2, 3072, 1),
+                                         (4, 2048, 0)])
+def test_gemv_modulation(gpu, rng, rows, K, silu):
+    N = 6 * 3072 + 63  # a ragged last group of outputs
+    x = rng.standard_normal((rows, K)).astype(np.float32)
     W = R.bf16_round(rng.standard_normal((N, K)).astype(np.float32) * 0.02)
     b = rng.standard_normal(N).astype(np.float32)
-    y = M.Dev(N * 4)
-    M.call("mk_gemv", dev(x).p, 1, K, bdev(W).p, dev(b).p, N, y.p, 1, None)
+    y = M.Dev(rows * N * 4)
+    M.call("mk_gemv", dev(x).p, rows, K, bdev(W).p, dev(b).p, N, y.p, silu, None)
     M.sync()
-    want = R.gemm(R.silu(x), W, b)  # silu(x) rounded to bf16 as the GEMMs' activation operand
-    assert maxrel(fetch(y, (1, N)), want) < 1e-5
+    want = R.gemm(R.silu(x) if silu else x, W, b)  # x' rounded to bf16 as the GEMMs' activation operand
+    assert maxrel(fetch(y, (rows, N)), want) < 1e-5
 
 
 def test_norms(gpu, rng):
