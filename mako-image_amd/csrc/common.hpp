@@ -27,6 +27,18 @@ typedef __attribute__((address_space(3))) void lds_void;
 // drop the kernel's launch stub without a diagnostic.
 __device__ inline void load_lds16(const void* src, lds_void* lds) { __builtin_amdgcn_global_load_lds(src, lds, 16, 0, 0); }
 
+// ---- GEMM dispatch plan (gemm.hip), shared with the engine's launch-grouping cost model ----
+struct GemmPlan {
+    int bn;          // tile width in channels (256, 128 or 64); tiles are 256 tokens
+    uint64_t tiles;  // tiles of the launch
+    bool sk;         // stream-K: whole waves round robin, the last partial wave split by k steps
+    uint64_t dp;     // tiles done whole (stream-K)
+};
+// The plan of a launch of n grouped problems (equal N, K, weight type, epilogue kind) on `cus` compute units.
+GemmPlan gemm_plan(const mk_gemm_args* a, uint32_t n, uint32_t cus);
+// Its estimated duration in units of one 256-channel k step.
+double gemm_cost(const mk_gemm_args* a, uint32_t n, uint32_t cus);
+
 // ---- error state (thread-local, read by mk_last_error) ----
 void set_error(const std::string& msg);
 mk_status fail(mk_status s, const std::string& msg);

@@ -359,27 +359,8 @@ struct mk_engine {
                          [&] { return mk_gemm_grouped(g + i, 1, stream); }));
         return MK_OK;
     }
-    // Cost of a launch in channel-tile-waves, mirroring the GEMM dispatch: 256-channel tiles once there is a wave of
-    // them, else 128 (or 64); tiles of 256 tokens, one workgroup a CU; whole waves cost rounds x width, and a launch
-    // the dispatch balances by splitting k (stream-K: a wave or more, a twentieth or more of the last wave idle,
-    // four k steps or more a workgroup) costs its fractional waves plus a fixup overhead.
-    double launch_cost(const mk_gemm_args* g, int n) const
-    {
-        uint64_t t256 = 0;
-        for (int i = 0; i < n; ++i)
-            t256 += uint64_t((g[i].M + 255) / 256) * g[i].batch * (g[0].N / 256);
-        const uint32_t bn = g[0].epilogue == MK_EPI_HEADS || (g[0].N % 256 == 0 && t256 >= cus) ? 256
-                            : g[0].N % 128 == 0                                                 ? 128
-                                                                                                : 64;
-        uint64_t tiles = 0;
-        for (int i = 0; i < n; ++i)
-            tiles += uint64_t((g[i].M + 255) / 256) * g[i].batch * (g[0].N / bn);
-        const uint64_t waves = tiles / cus, rounds = (tiles + cus - 1) / cus, idle = rounds * cus - tiles;
-        const uint64_t units = (tiles - (waves ? waves - 1 : 0) * cus) * (g[0].K / 64);
-        if (bn == 256 && waves >= 1 && idle * 20 >= rounds * cus && units >= uint64_t(4) * cus)
-            return double(tiles) / cus * 1.08 * bn;
-        return double(rounds) * bn;
-    }
+    // Estimated duration of a launch (the GEMM dispatch's own plan: tile width, waves, stream-K).
+    double launch_cost(const mk_gemm_args* g, int n) const { return gemm_cost(g, uint32_t(n), cus); }
     static mk_gemm_args gemm_args(const Linear& L, const void* A, int64_t lda, int64_t sa, uint32_t M, uint32_t batch,
                                   void* C, int64_t ldc, int64_t sc, uint32_t epi, uint32_t cdt,
                                   const float* gate = nullptr, int64_t gate_alt = 0, uint32_t split = 0,

@@ -5,14 +5,17 @@
 // read-modify-write 16 bytes per lane, and a head's 128 channels sit in one lane pair (per-head RMSNorm is one
 // cross-lane add, RoPE pairs are lane-local).
 //
-// Tiling: BM tokens x BN channels x 64 k per workgroup of 4 waves (2 x 2), each wave BN/2 x BM/2 as (BN/64) x (BM/64)
-// MFMA blocks of 32 x 32. Both tiles are K-contiguous and staged in LDS with a 16-byte-chunk XOR swizzle
-// (chunk ^ ((row >> 1) & 7)) so the fragment reads of 32 rows at one k offset are bank-conflict free; two LDS buffers, the
-// next tile's global loads in flight in registers during the current tile's MFMAs, one barrier per k step.
-// Workgroups map to tiles XCD-aware (consecutive tiles on one XCD share its L2) and grouped along M.
+// Tiling: BM = 256 tokens x BN channels x 64 k per workgroup; 256-wide tiles run 8 waves (two a SIMD: 2 along
+// channels x 4 along tokens, 128 x 64 per wave), narrower ones 4 waves (2 x 2). Both tiles are K-contiguous and
+// staged in LDS with a 16-byte-chunk XOR swizzle (chunk ^ ((row >> 1) & 7)) so the fragment reads of 32 rows at one
+// k offset are bank-conflict free. Two LDS buffers: buffer loads write the next k step straight into LDS while the
+// current one's MFMAs run, one barrier per k step. The main loop's instruction order is fixed by hand (every MFMA,
+// fragment read and load fenced): loads and reads spread over the MFMAs, each read issued in the order its MFMA
+// needs it. Workgroups map to tiles XCD-aware (consecutive tiles on one XCD share its L2) and grouped along M.
 #include "common.hpp"
 
 #include <mutex>
+#include <type_traits>
 
 namespace mk {
 
@@ -48,6 +51,25 @@ struct GemmG {
 };
 
 constexpr int BK = 64;
+
+// Buffer resource (raw, dword format) over `bytes` bytes from `base`, and a 16-byte load through it into LDS at
+// byte offset voff + soff: the buffer form of the direct-to-LDS load. Unlike the global form it does not count as
+// an LDS access, so the LDS reads around it keep precise (partial) waits.
+#if defined(__HIP_DEVICE_COMPILE__)
+typedef __amdgpu_buffer_rsrc_t BufRes;
+__device__ inline BufRes buf_res(const void* base, uint32_t bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, int(bytes), 0x00020000);
+}
+__device__ inline void buf_load_lds16(BufRes r, lds_void* lds, uint32_t voff, uint32_t soff)
+{
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds, 16, voff, soff, 0, 0);
+}
+#else
+typedef int BufRes; // host pass: never called
+__device__ inline BufRes buf_res(const void*, uint32_t) { return 0; }
+__device__ inline void buf_load_lds16(BufRes, lds_void*, uint32_t, uint32_t) {}
+#endif
 
 // LDS tile rows are 64 bf16 (128 bytes, 8 chunks of 16). gfx950's LDS has 64 banks (256 bytes a cycle): a 16-byte read
 // serves 16 lanes a cycle, here 16 consecutive rows at one logical chunk. Rows r and r + 1 fall in opposite halves of
@@ -103,16 +125,19 @@ __device__ inline EpiCh epi_channels(const GemmP& p, int ch)
 // GEMM, channels from chw. Lanes run along the channels (4 each, WC/4 lanes a row), so LDS reads are conflict free and
 // every store instruction writes whole row segments. For the residual the rows' x loads go out together before the
 // stores (vmcnt also counts stores: a load among the stores would wait for all of them).
-template <int EK, int WC>
+// With SW the slice is 32 x 32 in unpadded 32-float rows whose 16-byte chunks are XOR-swizzled (stage_sw).
+template <int EK, int WC, bool SW = false>
 __device__ inline void epi_slice(const GemmP& p, const float* st, int ld, int tok0, int chw, int lane, int64_t zc,
                                  const EpiCh& k)
 {
     constexpr int LPR = WC / 4, RPI = 64 / LPR, NI = 32 / RPI; // lanes a row, rows an instruction, rows a lane
+    static_assert(!SW || WC == 32, "swizzled staging holds 32 channels");
     const int c = lane % LPR, r0 = lane / LPR, ch = chw + 4 * c;
     f32x4 v[NI];
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
-        v[i] = *reinterpret_cast<const f32x4*>(st + (r0 + RPI * i) * ld + 4 * c);
+        const int row = r0 + RPI * i;
+        v[i] = *reinterpret_cast<const f32x4*>(SW ? st + row * 32 + 4 * (c ^ ((row >> 1) & 7)) : st + row * ld + 4 * c);
 #pragma unroll
         for (int e = 0; e < 4; ++e)
             v[i][e] = v[i][e] * k.scale[e] + k.bias[e];
@@ -385,6 +410,16 @@ __device__ inline const GemmP& locate(const GemmG& G, uint32_t t, uint32_t& z, u
     return p;
 }
 
+// 16-byte accumulator groups a stream-K fixup pass brings into LDS: the largest divisor of the qn groups that fits
+// the cap the operand buffers allow.
+constexpr int fixup_groups(int qn, int cap)
+{
+    int q = qn < cap ? qn : cap;
+    while (qn % q)
+        --q;
+    return q;
+}
+
 // One tile's k steps [kb, ke): the pipelined main loop, then either the partial published to stream-K slot
 // `publish`, or the partials of the tile's other ranges (virtual indices fix_lo .. fix_hi except `self`, tail tile
 // tt) added in index order, and the epilogue.
@@ -395,58 +430,71 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
 {
     constexpr int NT = 64 * NW;                 // threads
     constexpr int WM = BM / (NW / 2);           // tokens per wave (waves: 2 along channels x NW/2 along tokens)
-    constexpr int TB = WM / 32, CB = BN / 64;   // 32-row MFMA blocks per wave along tokens / channels
+    constexpr int WC = BN / 2;                  // channels per wave
+    constexpr int TB = WM / 32, CB = WC / 32;   // 32-row MFMA blocks per wave along tokens / channels
     constexpr int RA = BM * 8 / NT;             // direct-load rounds for the activation tile (64 chunks per wave)
     constexpr int RW = BN * 8 / NT;             // ... for a bf16 weight tile
     constexpr int LW = BN * 4 / NT;             // 16-byte fp8 weight chunks per thread (register staged)
-    constexpr int WC = BN / 2, LDW = WC + 4;    // epilogue staging: a wave's 32 tokens x WC channels, padded rows
+    constexpr int ND = RA + (kF8 ? 0 : RW);     // direct loads a thread issues per k step
+    constexpr int LDW = WC + 4;                 // epilogue staging: a wave's 32 tokens x WC channels, padded rows
     uint16_t(*sW)[BN * 64] = reinterpret_cast<uint16_t(*)[BN * 64]>(smem);
     uint16_t(*sA)[BM * 64] = reinterpret_cast<uint16_t(*)[BM * 64]>(smem + 2 * BN * 64);
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // the wave index is uniform: readfirstlane keeps it (and the LDS bases of the direct loads) in scalar registers
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wn = wave & 1, wm = wave >> 1;
     const int m0 = int(tm) * BM, n0 = int(tn) * BN;
 
-    const uint16_t* A = p.a + int64_t(z) * p.sa;
-
     // Direct loads: wave w's round i fills LDS chunks P = (i * NW + w) * 64 + lane of the tile; chunk P holds
-    // row P / 8 and logical k-chunk swz_chunk(row, P % 8), so the lane loads that one.
-    const uint16_t* ga[RA];
+    // row P / 8 and logical k-chunk swz_chunk(row, P % 8), so the lane loads that one. Buffer loads: the resource
+    // spans the tile's rows (base = its first row), the lane's 32-bit byte offset selects row and chunk, the k
+    // offset is a scalar; activation rows past M read the last row.
+    const char* gA = reinterpret_cast<const char*>(p.a + int64_t(z) * p.sa + int64_t(m0) * p.lda);
+    const char* gW = static_cast<const char*>(p.w) + int64_t(n0) * p.K * (kF8 ? 1 : 2);
+    const BufRes rsA = buf_res(gA, uint32_t(((min(int(p.M) - m0, BM) - 1) * int64_t(p.lda) + p.K) * 2));
+    const BufRes rsW = buf_res(gW, uint32_t(int64_t(BN) * p.K * 2));
+    uint32_t oa[RA];
 #pragma unroll
     for (int i = 0; i < RA; ++i) {
         const int P = (i * NW + wave) * 64 + lane, row = P >> 3, kc = swz_chunk(row, P & 7);
-        ga[i] = A + int64_t(min(m0 + row, int(p.M) - 1)) * p.lda + kc * 8;
+        oa[i] = uint32_t(min(row, int(p.M) - 1 - m0) * int(p.lda) + kc * 8) * 2;
     }
-    const uint16_t* gw[kF8 ? 1 : RW];
+    uint32_t ow[kF8 ? 1 : RW];
     const uint8_t* gw8[kF8 ? LW : 1];
     if constexpr (!kF8) {
 #pragma unroll
         for (int i = 0; i < RW; ++i) {
             const int P = (i * NW + wave) * 64 + lane, row = P >> 3, kc = swz_chunk(row, P & 7);
-            gw[i] = static_cast<const uint16_t*>(p.w) + int64_t(n0 + row) * p.K + kc * 8;
+            ow[i] = uint32_t(row * int(p.K) + kc * 8) * 2;
         }
     } else {
 #pragma unroll
         for (int i = 0; i < LW; ++i) {
             const int c = tid + NT * i, row = c >> 2, kc = c & 3;
-            gw8[i] = static_cast<const uint8_t*>(p.w) + int64_t(n0 + row) * p.K + kc * 16;
+            gw8[i] = reinterpret_cast<const uint8_t*>(gW) + int64_t(row) * p.K + kc * 16;
         }
     }
     u32x4 rw[kF8 ? LW : 1];
-    auto issue = [&](int kt, int buf) {
-        const int k0 = kt * BK;
-#pragma unroll
-        for (int i = 0; i < RA; ++i)
-            load_lds16(ga[i] + k0, (lds_void*)&sA[buf][(i * NW + wave) * 64 * 8]);
-        if constexpr (!kF8) {
-#pragma unroll
-            for (int i = 0; i < RW; ++i)
-                load_lds16(gw[i] + k0, (lds_void*)&sW[buf][(i * NW + wave) * 64 * 8]);
-        } else {
+    // direct load i (activation rounds first, then bf16 weight rounds) of k step kt into buffer buf
+    auto dma1 = [&](int kt, int buf, int i) {
+        if (i < RA)
+            buf_load_lds16(rsA, (lds_void*)&sA[buf][(i * NW + wave) * 64 * 8], oa[i], uint32_t(kt * BK * 2));
+        else if constexpr (!kF8)
+            buf_load_lds16(rsW, (lds_void*)&sW[buf][((i - RA) * NW + wave) * 64 * 8], ow[i - RA],
+                           uint32_t(kt * BK * 2));
+    };
+    auto load_f8 = [&](int kt) {
+        if constexpr (kF8) {
 #pragma unroll
             for (int i = 0; i < LW; ++i)
-                rw[i] = *reinterpret_cast<const u32x4*>(gw8[i] + k0);
+                rw[i] = *reinterpret_cast<const u32x4*>(gw8[i] + kt * BK);
         }
+    };
+    auto issue = [&](int kt, int buf) {
+#pragma unroll
+        for (int i = 0; i < ND; ++i)
+            dma1(kt, buf, i);
+        load_f8(kt);
     };
     auto commit_f8 = [&](int buf) {
         if constexpr (kF8) {
@@ -468,91 +516,108 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
         for (int j = 0; j < TB; ++j)
             acc[i][j] = f32x16{};
 
+    // v_mfma_f32_32x32x16_bf16: lane (r32, hk) supplies row r32 of a 32-row block and k values 8 hk .. 8 hk + 7 of
+    // a 16-wide substep, and holds output rows (channels) 8 i + 4 hk .. + 3 (i < 4) of column r32 (token).
     const int r32 = lane & 31, hk = lane >> 5;
-    auto frags = [&](int buf, int ks, bf16x8 (&wf)[CB], bf16x8 (&af)[TB]) {
+    // fragment j of a substep in first-use order (the MFMAs run channel-block-major): weight block 0, the token
+    // blocks, then weight blocks 1 ..
+    auto frag = [&](int buf, int ks, int j, bf16x8(&wf)[CB], bf16x8(&af)[TB]) {
         const int kc = ks * 2 + hk;
-#pragma unroll
-        for (int cb = 0; cb < CB; ++cb)
-            wf[cb] = *reinterpret_cast<const bf16x8*>(&sW[buf][swz(wn * (BN / 2) + cb * 32 + r32, kc)]);
-#pragma unroll
-        for (int tb = 0; tb < TB; ++tb)
-            af[tb] = *reinterpret_cast<const bf16x8*>(&sA[buf][swz(wm * WM + tb * 32 + r32, kc)]);
-    };
-    auto mfma = [&](const bf16x8 (&wf)[CB], const bf16x8 (&af)[TB]) {
-#pragma unroll
-        for (int cb = 0; cb < CB; ++cb)
-#pragma unroll
-            for (int tb = 0; tb < TB; ++tb)
-                acc[cb][tb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[cb], af[tb], acc[cb][tb], 0, 0, 0);
-    };
-    // Interleave a k step's MFMAs with the LDS reads of the next step's fragments: the reads go out with the first
-    // MFMAs (one after each), so the rest of the step covers their latency. The step's first MFMA goes before any
-    // new read: its operands' wait (lgkmcnt) then has no fresh read to wait for.
-    auto interleave = [&]() {
-#pragma unroll
-        for (int i = 0; i < CB + TB; ++i) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); // MFMA
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0); // DS read
+        if (j == 0 || j > TB) {
+            const int cb = j == 0 ? 0 : j - TB;
+            wf[cb] = *reinterpret_cast<const bf16x8*>(&sW[buf][swz(wn * WC + cb * 32 + r32, kc)]);
+        } else {
+            af[j - 1] = *reinterpret_cast<const bf16x8*>(&sA[buf][swz(wm * WM + (j - 1) * 32 + r32, kc)]);
         }
-        if constexpr (CB * TB > CB + TB)
-            __builtin_amdgcn_sched_group_barrier(0x008, CB * TB - (CB + TB), 0);
+    };
+    // One substep's MFMAs from fragments wf / af in a fixed order (every instruction fenced): one read of the next
+    // substep's fragments (buffer nbuf, substep nks; none if nks < 0) after each of the first MFMAs, and direct
+    // loads d0 .. d1 - 1 of step dkt into buffer dbuf likewise (what is left after the last MFMA follows it).
+    auto group = [&](const bf16x8(&wf)[CB], const bf16x8(&af)[TB], int nbuf, int nks, bf16x8(&nwf)[CB],
+                     bf16x8(&naf)[TB], int dkt, int dbuf, int d0, int d1) {
+        int d = d0;
+#pragma unroll
+        for (int i = 0; i < CB * TB; ++i) {
+            const int cb = i / TB, tb = i % TB;
+            acc[cb][tb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[cb], af[tb], acc[cb][tb], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            if (nks >= 0 && i < CB + TB) {
+                frag(nbuf, nks, i, nwf, naf);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            if (d < d1) {
+                dma1(dkt, dbuf, d);
+                ++d;
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        // narrow tiles have fewer MFMAs a substep than reads or loads
+        if (nks >= 0) {
+#pragma unroll
+            for (int j = CB * TB; j < CB + TB; ++j)
+                frag(nbuf, nks, j, nwf, naf);
+        }
+#pragma unroll
+        for (int i = 0; i < ND; ++i)
+            if (d < d1) {
+                dma1(dkt, dbuf, d);
+                ++d;
+            }
     };
 
-    // Software pipeline: tile t is in LDS buffer t & 1, tile t + 1 lands in the other during tile t's MFMAs, and the
-    // fragments of k step s + 1 are read from LDS while step s's MFMAs run. The loop body has no branches (prefetch
-    // tile indices are clamped; past-the-end prefetches reload the last tile), so the interleave covers all of it.
+    // Software pipeline over k steps of four 16-wide substeps: step t is in LDS buffer t & 1; step t + 1 lands in
+    // the other buffer during step t (the first half of its direct loads goes out with the last substep of step
+    // t - 1, right after the barrier frees the buffer, the second half with the first substep of step t); each
+    // substep reads the next one's fragments. Past-the-end steps are clamped (they reload the last step).
     issue(kb, 0);
     commit_f8(0);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     issue(min(kb + 1, ke - 1), 1);
     bf16x8 wf0[CB], af0[TB], wf1[CB], af1[TB];
-    frags(0, 0, wf0, af0);
-    for (int kt = kb; kt < ke; ++kt) {
-        const int buf = (kt - kb) & 1;
-        frags(buf, 1, wf1, af1);
-        mfma(wf0, af0);
-        interleave();
-        frags(buf, 2, wf0, af0);
-        mfma(wf1, af1);
-        interleave();
-        frags(buf, 3, wf1, af1);
-        mfma(wf0, af0);
-        interleave();
-        // tile kt + 1 complete in the other buffer, every wave done reading this one
+#pragma unroll
+    for (int j = 0; j < CB + TB; ++j)
+        frag(0, 0, j, wf0, af0);
+    // one k step from buffer `buf` (a constant: the loop is unrolled by two, so every LDS address is a register
+    // base plus an immediate offset)
+    auto step = [&](int kt, auto buf_c) {
+        constexpr int buf = decltype(buf_c)::value;
+        group(wf0, af0, buf, 1, wf1, af1, min(kt + 1, ke - 1), buf ^ 1, ND / 2, kt == kb ? ND / 2 : ND);
+        group(wf1, af1, buf, 2, wf0, af0, 0, 0, 0, 0);
+        group(wf0, af0, buf, 3, wf1, af1, 0, 0, 0, 0);
+        // step kt + 1 complete in the other buffer, every wave done reading this one
         commit_f8(buf ^ 1);
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
-        frags(buf ^ 1, 0, wf0, af0);
-        issue(min(kt + 2, ke - 1), buf);
-        mfma(wf1, af1);
-        interleave();
+        load_f8(min(kt + 2, ke - 1));
+        group(wf1, af1, buf ^ 1, 0, wf0, af0, min(kt + 2, ke - 1), buf, 0, ND / 2);
+    };
+    int kt = kb;
+    for (; kt + 1 < ke; kt += 2) {
+        step(kt, std::integral_constant<int, 0>{});
+        step(kt + 1, std::integral_constant<int, 1>{});
     }
+    if (kt < ke)
+        step(kt, std::integral_constant<int, 0>{});
     __builtin_amdgcn_s_waitcnt(0); // the last (unused) prefetch must land before the LDS is reused
     __syncthreads();
 
     // ---- stream-K: publish this range's partial, or add the earlier ranges' partials ----
     constexpr int NACC = CB * TB * 16;
-    // Partials go through L2 to the device-coherent level with relaxed agent-scope atomics (sc1 loads and stores),
-    // ordered by waiting for the stores before the flag: no cache-wide writeback or invalidate (an agent-scope fence
-    // would flush or invalidate the whole L2 of the XCD under the other workgroups' operand panels).
+    // The workspace is uncached (not held in any XCD's L2): a partial is plain 16-byte stores, complete at the memory
+    // once acknowledged; the flag store follows every wave's acknowledgements. Slot layout: 16-byte groups
+    // q = 4 * block + j / 4 of the accumulators as [q][thread][4 floats], so one group of a wave is 1 KB contiguous
+    // (whole-line writes; the fixup's direct-to-LDS loads take it whole).
     if (publish >= 0) {
-        uint64_t* w = reinterpret_cast<uint64_t*>(sk->ws + size_t(publish) * NT * NACC) + tid;
+        f32x4* w = reinterpret_cast<f32x4*>(sk->ws + size_t(publish) * NT * NACC) + tid;
 #pragma unroll
         for (int cb = 0; cb < CB; ++cb)
 #pragma unroll
-            for (int tb = 0; tb < TB; ++tb) {
+            for (int tb = 0; tb < TB; ++tb)
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    // (bit-casts from scalars: this compiler miscompiles a bit-cast of a vector element)
-                    const float lo = acc[cb][tb][2 * j], hi = acc[cb][tb][2 * j + 1];
-                    const uint64_t bits =
-                        uint64_t(__builtin_bit_cast(uint32_t, lo)) | uint64_t(__builtin_bit_cast(uint32_t, hi)) << 32;
-                    __hip_atomic_store(w + ((cb * TB + tb) * 8 + j) * NT, bits, __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
-                }
-                __builtin_amdgcn_sched_barrier(0); // one block at a time: few registers in flight
-            }
+                for (int m = 0; m < 4; ++m)
+                    w[size_t((cb * TB + tb) * 4 + m) * NT] =
+                        f32x4{acc[cb][tb][4 * m], acc[cb][tb][4 * m + 1], acc[cb][tb][4 * m + 2], acc[cb][tb][4 * m + 3]};
         __builtin_amdgcn_s_waitcnt(0); // every store acknowledged at the coherent level
         __syncthreads();
         if (tid == 0)
@@ -575,26 +640,35 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
                 }
             }
         __syncthreads();
-        // one accumulator block at a time, the other ranges' partials added in index order
+        // The other ranges' partials, in index order, each in passes of QL 16-byte groups: every wave streams its
+        // own groups into its own region of the (now free) operand buffers with direct-to-LDS loads (device-coherent,
+        // sc1), many in flight, then adds them from LDS.
+        constexpr int QN = NACC / 4, QL = fixup_groups(QN, (2 * (BN + BM) * 64 * 2) / (NT * 16));
+        const f32x4* mine = reinterpret_cast<const f32x4*>(smem) + wave * QL * 64 + lane;
+        for (int i = fix_lo; i <= fix_hi; ++i) {
+            if (i == self)
+                continue;
+            const float* src = sk->ws + size_t(sk_slot(*sk, uint32_t(i), tt)) * NT * NACC + 4 * tid;
 #pragma unroll
-        for (int cb = 0; cb < CB; ++cb)
+            for (int pass = 0; pass < QN / QL; ++pass) {
 #pragma unroll
-            for (int tb = 0; tb < TB; ++tb) {
-                for (int i = fix_lo; i <= fix_hi; ++i) {
-                    if (i == self)
-                        continue;
-                    uint64_t* w =
-                        reinterpret_cast<uint64_t*>(sk->ws + size_t(sk_slot(*sk, uint32_t(i), tt)) * NT * NACC) + tid;
+                for (int q = 0; q < QL; ++q)
+                    __builtin_amdgcn_global_load_lds(src + size_t(pass * QL + q) * NT * 4,
+                                                     (lds_void*)(reinterpret_cast<f32x4*>(smem) + (wave * QL + q) * 64),
+                                                     16, 0, 16 /* sc1 */);
+                __builtin_amdgcn_s_waitcnt(0);
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) {
-                        const uint64_t bits = __hip_atomic_load(w + ((cb * TB + tb) * 8 + j) * NT, __ATOMIC_RELAXED,
-                                                                __HIP_MEMORY_SCOPE_AGENT);
-                        acc[cb][tb][2 * j] += __builtin_bit_cast(float, uint32_t(bits));
-                        acc[cb][tb][2 * j + 1] += __builtin_bit_cast(float, uint32_t(bits >> 32));
-                    }
+                for (int q = 0; q < QL; ++q) {
+                    const int g = pass * QL + q, b = g / 4, j0 = (g % 4) * 4;
+                    const f32x4 v = mine[q * 64];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        acc[b / TB][b % TB][j0 + e] += v[e];
                 }
-                __builtin_amdgcn_sched_barrier(0);
+                __builtin_amdgcn_s_waitcnt(0); // this pass's LDS reads done before the next pass's loads land
             }
+        }
+        __syncthreads(); // the epilogue's staging regions span other waves' fixup regions
     }
 
     // ---- epilogue through LDS: per 32-token block, each wave stages its 32 x WC slice (fp32, padded rows) in a
@@ -723,7 +797,7 @@ std::mutex g_sk_mutex;
 SkWork g_sk[kMaxDevices];
 
 template <int BM, int BN, bool kF8, int EK, int NW = 4>
-mk_status launch(GemmP* p, uint32_t count, hipStream_t s)
+mk_status launch(GemmP* p, uint32_t count, const GemmPlan& plan, hipStream_t s)
 {
     constexpr int NT = 64 * NW, NACC = (BN / 64) * (BM / (NW / 2) / 32) * 16;
     GemmG G{};
@@ -748,37 +822,32 @@ mk_status launch(GemmP* p, uint32_t count, hipStream_t s)
             MK_HIP(hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev));
             W.cus = n > 0 ? uint32_t(n) : 1;
         }
-        // stream-K when whole tiles would leave a twentieth or more of the launch's CU time idle in its last wave;
-        // all but one full wave go round robin, the rest is split by k steps (at least 4 a workgroup)
-        const uint32_t grid = W.cus, waves = tiles / grid, rounds = (tiles + grid - 1) / grid;
-        const uint64_t idle = uint64_t(rounds) * grid - tiles;
-        if (waves >= 1 && idle * 20 >= uint64_t(rounds) * grid) {
+        const uint32_t grid = W.cus;
+        if (plan.sk && plan.dp % grid == 0 && plan.dp < tiles) {
             SkP sk{};
             sk.total = tiles;
-            sk.dp = (waves - 1) * grid;
+            sk.dp = uint32_t(plan.dp);
             sk.kt = kt;
             sk.units = uint64_t(tiles - sk.dp) * kt;
-            if (sk.units >= uint64_t(4) * grid) {
-                const size_t need = size_t(2) * grid * NT * NACC * sizeof(float);
-                if (!W.ws) {
-                    MK_HIP(hipExtMallocWithFlags(reinterpret_cast<void**>(&W.ws), need, hipDeviceMallocUncached));
-                    W.ws_bytes = need;
-                    MK_HIP(hipExtMallocWithFlags(reinterpret_cast<void**>(&W.flags), 2 * grid * sizeof(uint32_t),
-                                                 hipDeviceMallocUncached));
-                    MK_HIP(hipMemset(W.flags, 0, 2 * grid * sizeof(uint32_t)));
-                    W.nflags = 2 * grid;
-                }
-                if (W.ws_bytes < need || W.nflags < 2 * grid)
-                    return fail(MK_ERR_UNSUPPORTED, "gemm: stream-K workspace smaller than this launch needs");
-                if (++W.epoch == 0)
-                    W.epoch = 1;
-                sk.ws = W.ws;
-                sk.flags = W.flags;
-                sk.epoch = W.epoch;
-                gemm_sk_kernel<BM, BN, kF8, EK, NW><<<grid, NT, 0, s>>>(G, sk);
-                MK_HIP(hipGetLastError());
-                return MK_OK;
+            const size_t need = size_t(2) * grid * NT * NACC * sizeof(float);
+            if (!W.ws) {
+                MK_HIP(hipExtMallocWithFlags(reinterpret_cast<void**>(&W.ws), need, hipDeviceMallocUncached));
+                W.ws_bytes = need;
+                MK_HIP(hipExtMallocWithFlags(reinterpret_cast<void**>(&W.flags), 2 * grid * sizeof(uint32_t),
+                                             hipDeviceMallocUncached));
+                MK_HIP(hipMemset(W.flags, 0, 2 * grid * sizeof(uint32_t)));
+                W.nflags = 2 * grid;
             }
+            if (W.ws_bytes < need || W.nflags < 2 * grid)
+                return fail(MK_ERR_UNSUPPORTED, "gemm: stream-K workspace smaller than this launch needs");
+            if (++W.epoch == 0)
+                W.epoch = 1;
+            sk.ws = W.ws;
+            sk.flags = W.flags;
+            sk.epoch = W.epoch;
+            gemm_sk_kernel<BM, BN, kF8, EK, NW><<<grid, NT, 0, s>>>(G, sk);
+            MK_HIP(hipGetLastError());
+            return MK_OK;
         }
     }
     gemm_kernel<BM, BN, kF8, EK, NW><<<tiles, NT, 0, s>>>(G);
@@ -807,6 +876,8 @@ mk_status prepare(const mk_gemm_args* a, GemmP& p)
         return fail(MK_ERR_ARG, "gemm: weights must be bf16 or fp8-e4m3");
     if (a->lda % 8 || (reinterpret_cast<uintptr_t>(a->a) & 15) || (reinterpret_cast<uintptr_t>(a->w) & 15))
         return fail(MK_ERR_ARG, "gemm: A and W must be 16-byte aligned with lda a multiple of 8");
+    if (a->lda >= (1u << 23) || a->K >= (1u << 23))
+        return fail(MK_ERR_ARG, "gemm: lda and K must be below 2^23 (32-bit byte offsets within a tile)");
     if (a->epilogue > MK_EPI_HEADS)
         return fail(MK_ERR_ARG, "gemm: unknown epilogue");
     const bool gated = a->epilogue == MK_EPI_GATE_ADD || a->epilogue == MK_EPI_GATE_TANH;
@@ -849,6 +920,37 @@ mk_status prepare(const mk_gemm_args* a, GemmP& p)
 }
 
 } // namespace gemm_detail
+
+// Tile width: 256 x 256 tiles once there is a wave of them, else 256 x 128, else 256 x 64 (N = 64: stores, residuals);
+// heads epilogues always 256. Stream-K for 256-wide tiles when the last partial wave would leave a twentieth or more
+// of the launch idle and a tile is long (K of 6144 or more; measured, the partials' exchange costs about 24 k steps
+// of a tile, more than the balance saves on shorter tiles): the whole waves go round robin, the rest is split by k
+// steps (at least 4 a workgroup).
+GemmPlan gemm_plan(const mk_gemm_args* a, uint32_t n, uint32_t cus)
+{
+    GemmPlan pl{};
+    uint64_t t256 = 0;
+    for (uint32_t i = 0; i < n; ++i)
+        t256 += uint64_t((a[i].M + 255) / 256) * a[i].batch * (a[0].N / 256);
+    pl.bn = a[0].epilogue == MK_EPI_HEADS || (a[0].N % 256 == 0 && t256 >= cus) ? 256 : a[0].N % 128 == 0 ? 128 : 64;
+    for (uint32_t i = 0; i < n; ++i)
+        pl.tiles += uint64_t((a[i].M + 255) / 256) * a[i].batch * (a[0].N / pl.bn);
+    const uint64_t waves = pl.tiles / cus, rounds = (pl.tiles + cus - 1) / cus, idle = rounds * cus - pl.tiles;
+    const uint64_t kt = a[0].K / gemm_detail::BK;
+    pl.dp = waves * cus;
+    pl.sk = pl.bn == 256 && waves >= 1 && idle * 20 >= rounds * cus && kt >= 96 &&
+            (pl.tiles - pl.dp) * kt >= uint64_t(4) * cus;
+    return pl;
+}
+
+double gemm_cost(const mk_gemm_args* a, uint32_t n, uint32_t cus)
+{
+    const GemmPlan pl = gemm_plan(a, n, cus);
+    const double kt = double(a[0].K / gemm_detail::BK), w = pl.bn / 256.0;
+    if (pl.sk)
+        return (double(pl.tiles) / cus + 24.0 / kt) * kt * w;
+    return double((pl.tiles + cus - 1) / cus) * kt * w;
+}
 } // namespace mk
 
 using namespace mk;
@@ -876,18 +978,16 @@ extern "C" mk_status mk_gemm_grouped(const mk_gemm_args* a, uint32_t count, void
         return MK_OK;
     const bool f8 = a[0].w_dtype == MK_FP8_E4M3;
     const int ek = epi_kind(a[0].epilogue);
-    uint64_t tiles256 = 0;
-    for (uint32_t i = 0; i < n; ++i)
-        tiles256 += uint64_t(cdiv(p[i].M, 256)) * p[i].batch * (a[0].N / 256);
-    // tile: 256 x 256 once there is a wave of them (stream-K balances the last), else 256 x 128, else 256 x 64 (N =
-    // 64: stores, residuals)
     int cus = 0, dev = 0;
     MK_HIP(hipGetDevice(&dev));
     MK_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
-    const int bn = ek == EK_HEADS                                       ? 256
-                   : (a[0].N % 256 == 0 && tiles256 >= uint64_t(cus)) ? 256
-                   : a[0].N % 128 == 0                                  ? 128
-                                                                        : 64;
+    // the non-empty problems, for the plan
+    mk_gemm_args live[2];
+    for (uint32_t i = 0, j = 0; i < count; ++i)
+        if (a[i].M && a[i].batch)
+            live[j++] = a[i];
+    const GemmPlan plan = gemm_plan(live, n, uint32_t(cus > 0 ? cus : 1));
+    const int bn = plan.bn;
     if (bn == 64 && ek == EK_ACT)
         return fail(MK_ERR_UNSUPPORTED, "gemm: activation epilogues need N a multiple of 128");
     hipStream_t s = static_cast<hipStream_t>(stream);
@@ -895,8 +995,8 @@ extern "C" mk_status mk_gemm_grouped(const mk_gemm_args* a, uint32_t count, void
     // 256-wide tiles: 8 waves (two a SIMD, 64 x 128 wave tiles), so one wave's waits (barrier, loads) leave the
     // other's MFMAs running
 #define MK_GEMM_EK(BN, EK)                                                                                        \
-    e = f8 ? launch<256, BN, true, EK, BN == 256 ? 8 : 4>(p, n, s)                                                 \
-           : launch<256, BN, false, EK, BN == 256 ? 8 : 4>(p, n, s)
+    e = f8 ? launch<256, BN, true, EK, BN == 256 ? 8 : 4>(p, n, plan, s)                                           \
+           : launch<256, BN, false, EK, BN == 256 ? 8 : 4>(p, n, plan, s)
     if (ek == EK_HEADS) {
         MK_GEMM_EK(256, EK_HEADS);
     } else if (bn == 256) {
