@@ -533,9 +533,10 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
     // One substep's MFMAs from fragments wf / af in a fixed order (every instruction fenced): one read of the next
     // substep's fragments (buffer nbuf, substep nks; none if nks < 0) after each of the first MFMAs, and direct
     // loads d0 .. d1 - 1 of step dkt into buffer dbuf likewise (what is left after the last MFMA follows it).
+    // (d0, d1 compile-time: the load index then is a constant, so the offset arrays stay in registers)
     auto group = [&](const bf16x8(&wf)[CB], const bf16x8(&af)[TB], int nbuf, int nks, bf16x8(&nwf)[CB],
-                     bf16x8(&naf)[TB], int dkt, int dbuf, int d0, int d1) {
-        int d = d0;
+                     bf16x8(&naf)[TB], int dkt, int dbuf, auto d0_c, auto d1_c) {
+        constexpr int d0 = decltype(d0_c)::value, d1 = decltype(d1_c)::value;
 #pragma unroll
         for (int i = 0; i < CB * TB; ++i) {
             const int cb = i / TB, tb = i % TB;
@@ -545,9 +546,8 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
                 frag(nbuf, nks, i, nwf, naf);
                 __builtin_amdgcn_sched_barrier(0);
             }
-            if (d < d1) {
-                dma1(dkt, dbuf, d);
-                ++d;
+            if (d0 + i < d1) {
+                dma1(dkt, dbuf, d0 + i);
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
@@ -558,11 +558,8 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
                 frag(nbuf, nks, j, nwf, naf);
         }
 #pragma unroll
-        for (int i = 0; i < ND; ++i)
-            if (d < d1) {
-                dma1(dkt, dbuf, d);
-                ++d;
-            }
+        for (int d = d0 + CB * TB; d < d1; ++d)
+            dma1(dkt, dbuf, d);
     };
 
     // Software pipeline over k steps of four 16-wide substeps: step t is in LDS buffer t & 1; step t + 1 lands in
@@ -573,7 +570,11 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
     commit_f8(0);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    issue(min(kb + 1, ke - 1), 1);
+    // the first half of step kb + 1 (the first step issues the second, as every step does)
+#pragma unroll
+    for (int i = 0; i < ND / 2; ++i)
+        dma1(min(kb + 1, ke - 1), 1, i);
+    load_f8(min(kb + 1, ke - 1));
     bf16x8 wf0[CB], af0[TB], wf1[CB], af1[TB];
 #pragma unroll
     for (int j = 0; j < CB + TB; ++j)
@@ -582,15 +583,18 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
     // base plus an immediate offset)
     auto step = [&](int kt, auto buf_c) {
         constexpr int buf = decltype(buf_c)::value;
-        group(wf0, af0, buf, 1, wf1, af1, min(kt + 1, ke - 1), buf ^ 1, ND / 2, kt == kb ? ND / 2 : ND);
-        group(wf1, af1, buf, 2, wf0, af0, 0, 0, 0, 0);
-        group(wf0, af0, buf, 3, wf1, af1, 0, 0, 0, 0);
+        using C0 = std::integral_constant<int, 0>;
+        using CH = std::integral_constant<int, ND / 2>;
+        using CN = std::integral_constant<int, ND>;
+        group(wf0, af0, buf, 1, wf1, af1, min(kt + 1, ke - 1), buf ^ 1, CH{}, CN{});
+        group(wf1, af1, buf, 2, wf0, af0, 0, 0, C0{}, C0{});
+        group(wf0, af0, buf, 3, wf1, af1, 0, 0, C0{}, C0{});
         // step kt + 1 complete in the other buffer, every wave done reading this one
         commit_f8(buf ^ 1);
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
         load_f8(min(kt + 2, ke - 1));
-        group(wf1, af1, buf ^ 1, 0, wf0, af0, min(kt + 2, ke - 1), buf, 0, ND / 2);
+        group(wf1, af1, buf ^ 1, 0, wf0, af0, min(kt + 2, ke - 1), buf, C0{}, CH{});
     };
     int kt = kb;
     for (; kt + 1 < ke; kt += 2) {
