@@ -59,19 +59,28 @@ mk_status hip_check(hipError_t e, const char* what);
     } while (0)
 
 // ---- bf16: round-to-nearest-even, bit-exact with the CPU reference's rule ----
+// On the device gfx950's conversion instruction (v_cvt_pk_bf16_f32) does it: it matches the integer rule below on
+// every one of the 2^32 float bit patterns (NaNs quieted the same way), checked exhaustively on the GPU.
+typedef float f32x2v __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2cv __attribute__((ext_vector_type(2)));
 __host__ __device__ inline uint16_t f2bf_bits(float x)
 {
+#if defined(__HIP_DEVICE_COMPILE__)
+    const uint32_t p = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2v{x, 0.0f}, bf16x2cv));
+    return uint16_t(p);
+#else
     uint32_t u = __builtin_bit_cast(uint32_t, x);
     if ((u & 0x7fffffffu) > 0x7f800000u)
         return uint16_t((u >> 16) | 0x40);
     u += 0x7fffu + ((u >> 16) & 1u);
     return uint16_t(u >> 16);
+#endif
 }
 __host__ __device__ inline float bf2f_bits(uint16_t b) { return __builtin_bit_cast(float, uint32_t(b) << 16); }
-// Two floats to a packed pair of bf16 (low half = a).
+// Two floats to a packed pair of bf16 (low half = a), one conversion instruction.
 __device__ inline uint32_t pack_bf16x2(float a, float b)
 {
-    return uint32_t(f2bf_bits(a)) | (uint32_t(f2bf_bits(b)) << 16);
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2v{a, b}, bf16x2cv));
 }
 
 // ---- OCP fp8 e4m3 -> float (exact) ----
@@ -105,14 +114,16 @@ __device__ inline float wave_max(float v)
 }
 
 // ---- activations (fp32) ----
-__device__ inline float silu_f(float x) { return x / (1.0f + __expf(-x)); }
+// The per-element activations divide by the hardware reciprocal (v_rcp_f32, within 1 ulp) rather than an IEEE
+// division (a dozen instructions): in the step their outputs are rounded to bf16 or feed a bf16 operand.
+__device__ inline float silu_f(float x) { return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
 // tanh(u) = 2 sigmoid(2u) - 1 (one exp, one divide; saturates cleanly at both ends)
 __device__ inline float tanh_f(float u) { return 2.0f / (1.0f + __expf(-2.0f * u)) - 1.0f; }
 // GELU with the tanh approximation: 0.5 x (1 + tanh(u)) = x sigmoid(2u), u = sqrt(2/pi) (x + 0.044715 x^3)
 __device__ inline float gelu_tanh_f(float x)
 {
     const float u = 0.7978845608028654f * (x + 0.044715f * x * x * x);
-    return x / (1.0f + __expf(-2.0f * u));
+    return x * __builtin_amdgcn_rcpf(1.0f + __expf(-2.0f * u));
 }
 // erf by the Numerical Recipes erfc Chebyshev fit (max error ~1.2e-7), the form the reference's geglu uses
 // (image.metal:450-463).
