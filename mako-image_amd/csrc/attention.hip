@@ -14,6 +14,8 @@
 // wave of a SIMD runs its softmax on the VALUs, the other's MFMAs keep the matrix core busy.
 #include "common.hpp"
 
+#include <type_traits>
+
 namespace mk {
 
 namespace {
@@ -76,27 +78,29 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
         for (int ds = 0; ds < DS; ++ds)
             qf[ds] = *reinterpret_cast<const bf16x8*>(Q + int64_t(qi) * D + ds * 16 + hk * 8);
     }
-    const uint16_t* gk[RK];
+    // K / V^T tiles go to LDS by buffer loads (resources over the head's rows; lane byte offsets select key / dim and
+    // chunk, the tile's key offset is a scalar): unlike the global form they leave the LDS counter alone.
+    const BufRes rsK = buf_res(K, uint32_t(p.k_pad) * D * 2), rsV = buf_res(VT, uint32_t(p.k_pad) * D * 2);
+    uint32_t ok[RK], ov[RV];
 #pragma unroll
     for (int i = 0; i < RK; ++i) {
         const int P = (i * 4 + wave) * 64 + lane, key = P / KC, c = kswz(key, P % KC);
-        gk[i] = K + int64_t(key) * D + c * 8;
+        ok[i] = uint32_t(key * D + c * 8) * 2;
     }
-    const uint16_t* gv[RV];
 #pragma unroll
     for (int i = 0; i < RV; ++i) {
         const int P = (i * 4 + wave) * 64 + lane, d = P >> 3, c = (P & 7) ^ ((d >> 1) & 7);
-        gv[i] = VT + int64_t(d) * p.k_pad + c * 8;
+        ov[i] = uint32_t(d * int(p.k_pad) + c * 8) * 2;
     }
     const int ntiles = int((p.n_k + kKT - 1) / kKT);
-    auto issue = [&](int t) {
-        const int buf = t % NB, k0 = min(t, ntiles - 1) * kKT;
+    auto issue = [&](int t, int buf) {
+        const uint32_t k0 = uint32_t(min(t, ntiles - 1) * kKT);
 #pragma unroll
         for (int i = 0; i < RK; ++i)
-            load_lds16(gk[i] + int64_t(k0) * D, (lds_void*)&sK[buf][(i * 4 + wave) * 512]);
+            buf_load_lds16(rsK, (lds_void*)&sK[buf][(i * 4 + wave) * 512], ok[i], k0 * D * 2);
 #pragma unroll
         for (int i = 0; i < RV; ++i)
-            load_lds16(gv[i] + k0, (lds_void*)&sV[buf][(i * 4 + wave) * 512]);
+            buf_load_lds16(rsV, (lds_void*)&sV[buf][(i * 4 + wave) * 512], ov[i], k0 * 2);
     };
     // S^T of keys kt*32 .. +32 of the tile in buf: value r <-> key 8(r/4) + 4hk + r%4
     bf16x8 kone = {}, qm = {}; // U: ones at dim 0 (K side); -m at dim 0 (Q side), lanes of the first k half
@@ -227,13 +231,15 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
         }
     };
 
-    issue(0);
+    issue(0, 0);
     f32x16 s_a, s_b;
-    for (int t = 0; t < ntiles; ++t) {
+    // one 64-key tile from buffer `buf` (a constant: the loop is unrolled by two, so the LDS reads and the next
+    // tile's loads provably touch different buffers and the reads wait for nothing but themselves)
+    auto tile = [&](int t, auto buf_c) {
+        constexpr int buf = decltype(buf_c)::value;
         __builtin_amdgcn_s_waitcnt(0); // tile t resident
         __syncthreads();               // ... for every wave, and every wave done with tile t - 1's buffer
-        issue(t + 1);                  // past the end: the last tile again (discarded)
-        const int buf = t % NB;
+        issue(t + 1, buf ^ 1);         // past the end: the last tile again (discarded)
         u32x4 pb[2];
         qk(buf, 0, s_a);
         qk(buf, 1, s_b);
@@ -247,7 +253,14 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
             softmax(s_b, t * kKT + 32, pb);
         }
         pv(buf, 1, pb);
+    };
+    int t = 0;
+    for (; t + 1 < ntiles; t += 2) {
+        tile(t, std::integral_constant<int, 0>{});
+        tile(t + 1, std::integral_constant<int, 1>{});
     }
+    if (t < ntiles)
+        tile(t, std::integral_constant<int, 0>{});
     __builtin_amdgcn_s_waitcnt(0);
 
     const float lt = l + __shfl_xor(l, 32, 64);

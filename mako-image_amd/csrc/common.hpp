@@ -27,6 +27,25 @@ typedef __attribute__((address_space(3))) void lds_void;
 // drop the kernel's launch stub without a diagnostic.
 __device__ inline void load_lds16(const void* src, lds_void* lds) { __builtin_amdgcn_global_load_lds(src, lds, 16, 0, 0); }
 
+// Buffer resource (raw, dword format) over `bytes` bytes from `base`, and a 16-byte load through it into LDS at
+// byte offset voff + soff: the buffer form of the direct-to-LDS load. Unlike the global form it does not count as
+// an LDS access, so the LDS reads around it keep precise (partial) waits.
+#if defined(__HIP_DEVICE_COMPILE__)
+typedef __amdgpu_buffer_rsrc_t BufRes;
+__device__ inline BufRes buf_res(const void* base, uint32_t bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, int(bytes), 0x00020000);
+}
+__device__ inline void buf_load_lds16(BufRes r, lds_void* lds, uint32_t voff, uint32_t soff)
+{
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds, 16, voff, soff, 0, 0);
+}
+#else
+typedef int BufRes; // host pass: never called
+__device__ inline BufRes buf_res(const void*, uint32_t) { return 0; }
+__device__ inline void buf_load_lds16(BufRes, lds_void*, uint32_t, uint32_t) {}
+#endif
+
 // ---- GEMM dispatch plan (gemm.hip), shared with the engine's launch-grouping cost model ----
 struct GemmPlan {
     int bn;          // tile width in channels (256, 128 or 64); tiles are 256 tokens

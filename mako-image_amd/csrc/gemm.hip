@@ -52,24 +52,6 @@ struct GemmG {
 
 constexpr int BK = 64;
 
-// Buffer resource (raw, dword format) over `bytes` bytes from `base`, and a 16-byte load through it into LDS at
-// byte offset voff + soff: the buffer form of the direct-to-LDS load. Unlike the global form it does not count as
-// an LDS access, so the LDS reads around it keep precise (partial) waits.
-#if defined(__HIP_DEVICE_COMPILE__)
-typedef __amdgpu_buffer_rsrc_t BufRes;
-__device__ inline BufRes buf_res(const void* base, uint32_t bytes)
-{
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, int(bytes), 0x00020000);
-}
-__device__ inline void buf_load_lds16(BufRes r, lds_void* lds, uint32_t voff, uint32_t soff)
-{
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds, 16, voff, soff, 0, 0);
-}
-#else
-typedef int BufRes; // host pass: never called
-__device__ inline BufRes buf_res(const void*, uint32_t) { return 0; }
-__device__ inline void buf_load_lds16(BufRes, lds_void*, uint32_t, uint32_t) {}
-#endif
 
 // LDS tile rows are 64 bf16 (128 bytes, 8 chunks of 16). gfx950's LDS has 64 banks (256 bytes a cycle): a 16-byte read
 // serves 16 lanes a cycle, here 16 consecutive rows at one logical chunk. Rows r and r + 1 fall in opposite halves of
