@@ -396,8 +396,9 @@ def run_attention(q, k, v, scale, q_pos0=0, block=0):
     return fetch_bf16(out, (B, Tq, H * d))
 
 
+# ragged query blocks and a ragged last key tile over a long key range (d 128: 300 queries, 2000 keys)
 @pytest.mark.parametrize("d,Tq,Tk,block,q_pos0", [(128, 300, 300, 0, 0), (128, 64, 4352 // 17, 0, 0),
-                                                  (64, 333, 77, 0, 0), (64, 256, 1000, 0, 0),
+                                                  (64, 333, 77, 0, 0), (64, 256, 1000, 0, 0), (128, 300, 2000, 0, 0),
                                                   (128, 200, 260, 60, 60), (128, 260, 260, 60, 0),
                                                   (128, 190, 190, 0xFFFFFFFF, 0)])
 def test_attention_matches_oracle(gpu, rng, d, Tq, Tk, block, q_pos0):
