@@ -102,21 +102,10 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
         for (int i = 0; i < RV; ++i)
             buf_load_lds16(rsV, (lds_void*)&sV[buf][(i * 4 + wave) * 512], ov[i], k0 * 2);
     };
-    // S^T of keys kt*32 .. +32 of the tile in buf: value r <-> key 8(r/4) + 4hk + r%4
+    // S^T of a 32-key half of a tile: value r <-> key 8(r/4) + 4hk + r%4 of the half
     bf16x8 kone = {}, qm = {}; // U: ones at dim 0 (K side); -m at dim 0 (Q side), lanes of the first k half
     if (hk == 0)
         kone[0] = (__bf16)1.0f;
-    auto qk = [&](int buf, int kt, f32x16& sacc) {
-        sacc = f32x16{};
-        if constexpr (U)
-            sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kone, qm, sacc, 0, 0, 0);
-#pragma unroll
-        for (int ds = 0; ds < DS; ++ds) {
-            const int key = kt * 32 + r32, c = kswz(key, ds * 2 + hk);
-            const bf16x8 kf = *reinterpret_cast<const bf16x8*>(&sK[buf][key * D + c * 8]);
-            sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[ds], sacc, 0, 0, 0);
-        }
-    };
     f32x16 oacc[DT];
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
@@ -217,42 +206,74 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
                            cvt_bf16x2(sacc[o + 4], sacc[o + 5]), cvt_bf16x2(sacc[o + 6], sacc[o + 7])};
         }
     };
-    auto pv = [&](int buf, int kt, const u32x4 (&pb)[2]) {
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-            const int d = dt * 32 + r32, sw = (d >> 1) & 7;
-#pragma unroll
-            for (int st = 0; st < 2; ++st) {
-                const int s2 = 2 * kt + st;
-                const bf16x8 vf = *reinterpret_cast<const bf16x8*>(&sV[buf][d * kKT + (((2 * s2 + hk) ^ sw) << 3)]);
-                oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, __builtin_bit_cast(bf16x8, pb[st]), oacc[dt],
-                                                                   0, 0, 0);
-            }
-        }
-    };
-
     issue(0, 0);
     f32x16 s_a, s_b;
     // one 64-key tile from buffer `buf` (a constant: the loop is unrolled by two, so the LDS reads and the next
     // tile's loads provably touch different buffers and the reads wait for nothing but themselves)
+    // One 64-key tile from buffer `buf` (a constant: the loop is unrolled by two, so the LDS reads and the next
+    // tile's loads provably touch different buffers and the reads wait for nothing but themselves). The tile's 32
+    // fragment reads (K of both 32-key halves interleaved, then V of each half) stream four ahead of the MFMAs that
+    // use them, in a fixed order (fenced); the two halves' S^T products alternate so neither accumulator chain
+    // waits on its previous MFMA.
+    constexpr int LA = 4; // fragment reads in flight ahead of their MFMA
     auto tile = [&](int t, auto buf_c) {
         constexpr int buf = decltype(buf_c)::value;
         __builtin_amdgcn_s_waitcnt(0); // tile t resident
         __syncthreads();               // ... for every wave, and every wave done with tile t - 1's buffer
         issue(t + 1, buf ^ 1);         // past the end: the last tile again (discarded)
+        bf16x8 fk[2 * DS], fv[4 * DT];
+        // read g: K fragments g < 2 DS as (ds, half) pairs, then V fragments of half 0, then half 1
+        auto rd = [&](int g) {
+            if (g < 2 * DS) {
+                const int ds = g / 2, kt = g % 2, key = kt * 32 + r32, c = kswz(key, ds * 2 + hk);
+                fk[g] = *reinterpret_cast<const bf16x8*>(&sK[buf][key * D + c * 8]);
+            } else if (g < 2 * DS + 4 * DT) {
+                const int j = g - 2 * DS, kt = j / (2 * DT), dt = (j % (2 * DT)) % DT, st = (j % (2 * DT)) / DT;
+                const int d = dt * 32 + r32, s2 = 2 * kt + st;
+                fv[j] = *reinterpret_cast<const bf16x8*>(&sV[buf][d * kKT + (((2 * s2 + hk) ^ ((d >> 1) & 7)) << 3)]);
+            }
+        };
+#pragma unroll
+        for (int g = 0; g < LA; ++g)
+            rd(g);
+        __builtin_amdgcn_sched_barrier(0);
+        s_a = f32x16{};
+        s_b = f32x16{};
+        if constexpr (U) {
+            s_a = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kone, qm, s_a, 0, 0, 0);
+            s_b = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kone, qm, s_b, 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int g = 0; g < 2 * DS; ++g) {
+            f32x16& acc = g % 2 ? s_b : s_a;
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fk[g], qf[g / 2], acc, 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            rd(g + LA);
+            __builtin_amdgcn_sched_barrier(0);
+        }
         u32x4 pb[2];
-        qk(buf, 0, s_a);
-        qk(buf, 1, s_b);
+        auto pv = [&](int kt) {
+#pragma unroll
+            for (int j = 0; j < 2 * DT; ++j) {
+                const int dt = j % DT, st = j / DT;
+                oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fv[kt * 2 * DT + j], __builtin_bit_cast(bf16x8, pb[st]),
+                                                                   oacc[dt], 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
+                rd(2 * DS + kt * 2 * DT + j + LA);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        };
         if constexpr (U) {
             softmax_u(s_a, t * kKT, pb, t == 0, &s_b);
-            pv(buf, 0, pb);
+            pv(0);
             softmax_u(s_b, t * kKT + 32, pb, false, nullptr);
         } else {
             softmax(s_a, t * kKT, pb);
-            pv(buf, 0, pb);
+            pv(0);
             softmax(s_b, t * kKT + 32, pb);
         }
-        pv(buf, 1, pb);
+        pv(1);
     };
     int t = 0;
     for (; t + 1 < ntiles; t += 2) {
