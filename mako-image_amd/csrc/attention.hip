@@ -124,11 +124,7 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
                     sacc[r] = -__builtin_inff();
             }
         }
-        float mx = -1e30f;
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-            mx = fmaxf(mx, sacc[r]);
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float mx = max_xor32(max16(sacc));
         if (first || __any(mx > kLazy)) {
             const float mn = float((__bf16)(m + (first ? mx : fmaxf(mx, 0.0f))));
             const float dm = mn - m;
@@ -150,7 +146,9 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
                 for (int r = 0; r < 16; ++r)
                     oacc[dt][r] *= alpha;
         }
+        // row sums as four two-deep dot2 chains (one chain of eight serialises on the accumulator)
         const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
+        float ls[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int st = 0; st < 2; ++st) {
             const int o = 8 * st;
@@ -161,10 +159,11 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
                 const uint32_t pj = cvt_bf16x2(__builtin_amdgcn_exp2f(sacc[o + 2 * j]),
                                                __builtin_amdgcn_exp2f(sacc[o + 2 * j + 1]));
                 v[j] = pj;
-                l = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pj), ones, l, false);
+                ls[j] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pj), ones, ls[j], false);
             }
             pb[st] = v;
         }
+        l += (ls[0] + ls[1]) + (ls[2] + ls[3]);
     };
     auto softmax = [&](f32x16& sacc, int k0, u32x4 (&pb)[2]) {
         if (k0 + 32 > int(p.n_k) || (wave_causal && k0 + 31 > int(p.q_pos0) + q0)) {
@@ -175,11 +174,7 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
                     sacc[r] = -__builtin_inff();
             }
         }
-        float mx = -1e30f;
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-            mx = fmaxf(mx, sacc[r]);
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * p.c;
+        const float mx = max_xor32(max16(sacc)) * p.c;
         if (__any(mx > m + kLazy)) {
             const float mn = fmaxf(m, mx);
             const float alpha = __builtin_amdgcn_exp2f(m - mn);
@@ -191,14 +186,14 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
                 for (int r = 0; r < 16; ++r)
                     oacc[dt][r] *= alpha;
         }
-        float sum = 0.0f;
+        float sum[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const float e = __builtin_amdgcn_exp2f(fmaf(sacc[r], p.c, -m));
             sacc[r] = e;
-            sum += e;
+            sum[r % 4] += e;
         }
-        l += sum;
+        l += (sum[0] + sum[1]) + (sum[2] + sum[3]);
 #pragma unroll
         for (int st = 0; st < 2; ++st) {
             const int o = 8 * st;
@@ -275,16 +270,186 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
         }
         pv(1);
     };
+    // U: one 64-key tile with the softmax work in the matrix core's shadow. The scores arrive as S - m, so each
+    // half's probabilities are computed speculatively, before its row max is known: P = 2^(S - m) is what the tile
+    // needs whenever no score exceeds m by more than kLazy. The exponentials, conversions and row sums of half a then
+    // run in chunks between the S^T MFMAs of half b, those of half b between the P V MFMAs of half a, and the row max
+    // only decides afterwards whether a half is redone against a new m (the first half of the pass, and the rare
+    // tiles whose max jumps). EDGE tiles (ragged key end, causal diagonal) mask scores in the chunks.
+    constexpr int CH = 16 / DS;                  // scores per chunk: DS S^T MFMAs (= 2 DT P V MFMAs) per half
+    auto tile_u = [&](int t, auto buf_c, auto edge_c) {
+        constexpr int buf = decltype(buf_c)::value;
+        constexpr bool EDGE = decltype(edge_c)::value;
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        issue(t + 1, buf ^ 1);
+        bf16x8 fk[2 * DS], fv[4 * DT];
+        // read g: K fragments of half a, of half b, then V fragments of half a, of half b
+        auto rd = [&](int g) {
+            if (g < 2 * DS) {
+                const int kt = g / DS, ds = g % DS, key = kt * 32 + r32, c = kswz(key, ds * 2 + hk);
+                fk[g] = *reinterpret_cast<const bf16x8*>(&sK[buf][key * D + c * 8]);
+            } else if (g < 2 * DS + 4 * DT) {
+                const int j = g - 2 * DS, kt = j / (2 * DT), dt = (j % (2 * DT)) % DT, st = (j % (2 * DT)) / DT;
+                const int d = dt * 32 + r32, s2 = 2 * kt + st;
+                fv[j] = *reinterpret_cast<const bf16x8*>(&sV[buf][d * kKT + (((2 * s2 + hk) ^ ((d >> 1) & 7)) << 3)]);
+            }
+        };
+        const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
+        // chunk c of a half: scores 2j, 2j + 1 for pairs j of the chunk -> bf16 pair pw[j], row-sum partials, pair max
+        auto chunk = [&](f32x16& sc, int k0, uint32_t (&pw)[8], float (&ls)[4], float (&mp)[8], int c) {
+#pragma unroll
+            for (int i = 0; i < CH / 2; ++i) {
+                const int j = c * (CH / 2) + i;
+                float x0 = sc[2 * j], x1 = sc[2 * j + 1];
+                if constexpr (EDGE) {
+                    const int key = k0 + 8 * (2 * j / 4) + 4 * hk + (2 * j % 4);
+                    const bool causal = uint32_t(qpos) < p.block;
+                    if (key >= int(p.n_k) || (causal && key > qpos))
+                        x0 = -__builtin_inff();
+                    if (key + 1 >= int(p.n_k) || (causal && key + 1 > qpos))
+                        x1 = -__builtin_inff();
+                    sc[2 * j] = x0;
+                    sc[2 * j + 1] = x1;
+                }
+                pw[j] = cvt_bf16x2(__builtin_amdgcn_exp2f(x0), __builtin_amdgcn_exp2f(x1));
+                ls[j % 4] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pw[j]), ones, ls[j % 4], false);
+                mp[j] = fmaxf(x0, x1);
+                // pinned here: the redo path overwrites them, so the compiler would otherwise sink the
+                // speculative work out of the MFMA shadow into the path that keeps it
+                asm volatile("" : "+v"(pw[j]), "+v"(ls[j % 4]));
+            }
+        };
+        auto half_max = [&](const float (&mp)[8]) {
+            const float a = fmaxf(fmaxf(mp[0], mp[1]), fmaxf(mp[2], mp[3]));
+            const float b = fmaxf(fmaxf(mp[4], mp[5]), fmaxf(mp[6], mp[7]));
+            return max_xor32(fmaxf(a, b));
+        };
+        // moves m to cover the half's max (the pass's first half: to its max), rescales what was accumulated against
+        // the old m, and redoes the half's probabilities and row sum
+        auto redo = [&](f32x16& sc, uint32_t (&pw)[8], float& lh, float mx, bool first, f32x16* other) {
+            const float mn = float((__bf16)(m + (first ? mx : fmaxf(mx, 0.0f))));
+            const float dm = mn - m;
+            const float alpha = first ? 1.0f : __builtin_amdgcn_exp2f(-dm);
+            m = mn;
+            if (hk == 0)
+                qm[0] = (__bf16)(-m);
+            l *= alpha;
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                sc[r] -= dm;
+            if (other) // half b's scores, computed against the old m
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    (*other)[r] -= dm;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    oacc[dt][r] *= alpha;
+            float ls[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                pw[j] = cvt_bf16x2(__builtin_amdgcn_exp2f(sc[2 * j]), __builtin_amdgcn_exp2f(sc[2 * j + 1]));
+                ls[j % 4] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pw[j]), ones, ls[j % 4], false);
+            }
+            lh = (ls[0] + ls[1]) + (ls[2] + ls[3]);
+        };
+        const int k0 = t * kKT;
+#pragma unroll
+        for (int g = 0; g < LA; ++g)
+            rd(g);
+        __builtin_amdgcn_sched_barrier(0);
+        s_a = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kone, qm, f32x16{}, 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int ds = 0; ds < DS; ++ds) {
+            s_a = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fk[ds], qf[ds], s_a, 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            rd(ds + LA);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        s_b = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kone, qm, f32x16{}, 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        uint32_t pa[8], pbw[8];
+        float lsa[4] = {0.0f, 0.0f, 0.0f, 0.0f}, lsb[4] = {0.0f, 0.0f, 0.0f, 0.0f}, mpa[8], mpb[8];
+        // S^T of half b || softmax of half a
+#pragma unroll
+        for (int ds = 0; ds < DS; ++ds) {
+            s_b = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fk[DS + ds], qf[ds], s_b, 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            rd(DS + ds + LA);
+            __builtin_amdgcn_sched_barrier(0);
+            chunk(s_a, k0, pa, lsa, mpa, ds);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        float la = (lsa[0] + lsa[1]) + (lsa[2] + lsa[3]);
+        {
+            const float mx = half_max(mpa);
+            if (t == 0 || __any(mx > kLazy))
+                redo(s_a, pa, la, mx, t == 0, &s_b);
+        }
+        l += la;
+        __builtin_amdgcn_sched_barrier(0);
+        const u32x4 pA[2] = {u32x4{pa[0], pa[1], pa[2], pa[3]}, u32x4{pa[4], pa[5], pa[6], pa[7]}};
+        // P V of half a || softmax of half b
+#pragma unroll
+        for (int j = 0; j < 2 * DT; ++j) {
+            const int dt = j % DT, st = j / DT;
+            oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fv[j], __builtin_bit_cast(bf16x8, pA[st]), oacc[dt], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            rd(2 * DS + j + LA);
+            __builtin_amdgcn_sched_barrier(0);
+            chunk(s_b, k0 + 32, pbw, lsb, mpb, j);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        float lb = (lsb[0] + lsb[1]) + (lsb[2] + lsb[3]);
+        {
+            const float mx = half_max(mpb);
+            if (__any(mx > kLazy))
+                redo(s_b, pbw, lb, mx, false, nullptr);
+        }
+        l += lb;
+        __builtin_amdgcn_sched_barrier(0);
+        const u32x4 pB[2] = {u32x4{pbw[0], pbw[1], pbw[2], pbw[3]}, u32x4{pbw[4], pbw[5], pbw[6], pbw[7]}};
+#pragma unroll
+        for (int j = 0; j < 2 * DT; ++j) {
+            const int dt = j % DT, st = j / DT;
+            oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fv[2 * DT + j], __builtin_bit_cast(bf16x8, pB[st]),
+                                                               oacc[dt], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            rd(2 * DS + 2 * DT + j + LA);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
     int t = 0;
-    for (; t + 1 < ntiles; t += 2) {
-        tile(t, std::integral_constant<int, 0>{});
-        tile(t + 1, std::integral_constant<int, 1>{});
+    if constexpr (U) {
+        // a tile needs masking when it passes the key end or, under the causal prefix, reaches past the wave's
+        // first query
+        auto run = [&](int tt, auto buf_c) {
+            const int e = tt * kKT + kKT - 1;
+            if (e >= int(p.n_k) || (wave_causal && e > int(p.q_pos0) + q0))
+                tile_u(tt, buf_c, std::true_type{});
+            else
+                tile_u(tt, buf_c, std::false_type{});
+        };
+        for (; t + 1 < ntiles; t += 2) {
+            run(t, std::integral_constant<int, 0>{});
+            run(t + 1, std::integral_constant<int, 1>{});
+        }
+        if (t < ntiles)
+            run(t, std::integral_constant<int, 0>{});
+    } else {
+        for (; t + 1 < ntiles; t += 2) {
+            tile(t, std::integral_constant<int, 0>{});
+            tile(t + 1, std::integral_constant<int, 1>{});
+        }
+        if (t < ntiles)
+            tile(t, std::integral_constant<int, 0>{});
     }
-    if (t < ntiles)
-        tile(t, std::integral_constant<int, 0>{});
     __builtin_amdgcn_s_waitcnt(0);
 
-    const float lt = l + __shfl_xor(l, 32, 64);
+    const float lt = add_xor32(l);
     const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
     const int qi = q0 + r32;
     if (qi >= int(p.n_q))

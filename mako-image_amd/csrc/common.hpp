@@ -132,6 +132,41 @@ __device__ inline float wave_max(float v)
     return v;
 }
 
+// Combine lane i with lane i ^ 32 through v_permlane32_swap (a VALU op: swaps the upper 32 lanes of one register
+// with the lower 32 of the other), not a ds_bpermute round trip through the LDS unit. Swapping a value with itself
+// leaves lane i holding its own value in one half of the result and the partner's in the other.
+#if defined(__HIP_DEVICE_COMPILE__)
+__device__ inline float max_xor32(float v)
+{
+    const uint32_t u = __builtin_bit_cast(uint32_t, v);
+    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    const uint32_t a = r[0], b = r[1];
+    return fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
+}
+__device__ inline float add_xor32(float v)
+{
+    const uint32_t u = __builtin_bit_cast(uint32_t, v);
+    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    const uint32_t a = r[0], b = r[1];
+    return __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
+}
+#else
+__device__ inline float max_xor32(float v) { return v; }
+__device__ inline float add_xor32(float v) { return v; }
+#endif
+// max of 16 values as a depth-4 tree (a running fmaxf chain is 16 dependent VALU ops on the softmax's critical path)
+template <class V16> __device__ inline float max16(const V16& s)
+{
+    float a[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+        a[i] = fmaxf(s[2 * i], s[2 * i + 1]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        a[i] = fmaxf(a[2 * i], a[2 * i + 1]);
+    return fmaxf(fmaxf(a[0], a[1]), fmaxf(a[2], a[3]));
+}
+
 // ---- activations (fp32) ----
 // The per-element activations divide by the hardware reciprocal (v_rcp_f32, within 1 ulp) rather than an IEEE
 // division (a dozen instructions): in the step their outputs are rounded to bf16 or feed a bf16 operand.

@@ -416,7 +416,7 @@ def test_attention_matches_oracle(gpu, rng, d, Tq, Tk, block, q_pos0):
 @pytest.mark.parametrize("d,Tq,Tk,block,q_pos0,kscale", [
     (128, 300, 300, 0, 0, 1.0), (128, 4352 // 17, 4352, 0, 0, 1.0), (64, 333, 77, 0, 0, 1.0),
     (128, 200, 260, 60, 60, 1.0), (128, 260, 260, 60, 0, 1.0), (128, 190, 190, 0xFFFFFFFF, 0, 1.0),
-    (128, 256, 512, 0, 0, 6.0)])
+    (128, 256, 512, 0, 0, 6.0), (128, 300, 2000, 0, 0, 6.0), (64, 256, 1000, 0xFFFFFFFF, 0, 6.0)])
 def test_attention_unit_scale(gpu, rng, d, Tq, Tk, block, q_pos0, kscale):
     # scale 0: K already carries the softmax scale in log2 units (K' = bf16(k / sqrt(d) * log2 e)); equal to the
     # softmax of q K'^T ln 2. kscale 6 makes the logits large (the running max moves on many tiles).
