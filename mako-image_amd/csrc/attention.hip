@@ -12,6 +12,9 @@
 // at c ^ (key & 15), V^T [d][key] chunk c at c ^ ((d >> 1) & 7). V^T holds its keys in the vt_col order, so a lane's
 // 8 P V keys are one 16-byte read. Two workgroups run on a CU (two waves a SIMD, <= 256 registers each): while one
 // wave of a SIMD runs its softmax on the VALUs, the other's MFMAs keep the matrix core busy.
+// built with -fno-honor-nans (the max needs no canonicalization); the shared header's fp8 decoder names a NaN
+// constant, unused here
+#pragma clang diagnostic ignored "-Wnan-infinity-disabled"
 #include "common.hpp"
 
 #include <type_traits>
@@ -34,6 +37,10 @@ constexpr int kKT = 64; // keys per tile
 constexpr float kLazy = 8.0f;
 
 typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2;
+
+// max of two scores: this file is built without NaN semantics (scores are finite or -inf), so it is one v_max_f32
+// (with NaNs honoured, each operand that comes from a matrix product is first canonicalized: two more VALU ops)
+__device__ inline float max2(float a, float b) { return fmaxf(a, b); }
 
 __device__ inline uint32_t cvt_bf16x2(float a, float b)
 {
@@ -93,6 +100,14 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
         ov[i] = uint32_t(d * int(p.k_pad) + c * 8) * 2;
     }
     const int ntiles = int((p.n_k + kKT - 1) / kKT);
+    // direct load i of tile t into buffer buf: K rounds first, then V^T rounds
+    auto dma1 = [&](int t, int buf, int i) {
+        const uint32_t k0 = uint32_t(min(t, ntiles - 1) * kKT);
+        if (i < RK)
+            buf_load_lds16(rsK, (lds_void*)&sK[buf][(i * 4 + wave) * 512], ok[i], k0 * D * 2);
+        else if (i < RK + RV)
+            buf_load_lds16(rsV, (lds_void*)&sV[buf][((i - RK) * 4 + wave) * 512], ov[i - RK], k0 * 2);
+    };
     auto issue = [&](int t, int buf) {
         const uint32_t k0 = uint32_t(min(t, ntiles - 1) * kKT);
 #pragma unroll
@@ -282,7 +297,6 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
         constexpr bool EDGE = decltype(edge_c)::value;
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
-        issue(t + 1, buf ^ 1);
         bf16x8 fk[2 * DS], fv[4 * DT];
         // read g: K fragments of half a, of half b, then V fragments of half a, of half b
         auto rd = [&](int g) {
@@ -314,16 +328,16 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
                 }
                 pw[j] = cvt_bf16x2(__builtin_amdgcn_exp2f(x0), __builtin_amdgcn_exp2f(x1));
                 ls[j % 4] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pw[j]), ones, ls[j % 4], false);
-                mp[j] = fmaxf(x0, x1);
+                mp[j] = max2(x0, x1);
                 // pinned here: the redo path overwrites them, so the compiler would otherwise sink the
                 // speculative work out of the MFMA shadow into the path that keeps it
                 asm volatile("" : "+v"(pw[j]), "+v"(ls[j % 4]));
             }
         };
         auto half_max = [&](const float (&mp)[8]) {
-            const float a = fmaxf(fmaxf(mp[0], mp[1]), fmaxf(mp[2], mp[3]));
-            const float b = fmaxf(fmaxf(mp[4], mp[5]), fmaxf(mp[6], mp[7]));
-            return max_xor32(fmaxf(a, b));
+            const float a = max2(max2(mp[0], mp[1]), max2(mp[2], mp[3]));
+            const float b = max2(max2(mp[4], mp[5]), max2(mp[6], mp[7]));
+            return max_xor32(max2(a, b));
         };
         // moves m to cover the half's max (the pass's first half: to its max), rescales what was accumulated against
         // the old m, and redoes the half's probabilities and row sum
@@ -362,11 +376,18 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
         __builtin_amdgcn_sched_barrier(0);
         s_a = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kone, qm, f32x16{}, 0, 0, 0);
         __builtin_amdgcn_sched_barrier(0);
+        // the next tile's direct loads (past the end: the last tile again, discarded) go out one after each S^T
+        // MFMA of half a, not as one burst after the barrier (a burst from every wave stalls their issue)
+        constexpr int ND = RK + RV, PER = (ND + DS - 1) / DS;
 #pragma unroll
         for (int ds = 0; ds < DS; ++ds) {
             s_a = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fk[ds], qf[ds], s_a, 0, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
             rd(ds + LA);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int i = ds * PER; i < (ds + 1) * PER && i < ND; ++i)
+                dma1(t + 1, buf ^ 1, i);
             __builtin_amdgcn_sched_barrier(0);
         }
         s_b = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kone, qm, f32x16{}, 0, 0, 0);
