@@ -40,10 +40,16 @@ __device__ inline void buf_load_lds16(BufRes r, lds_void* lds, uint32_t voff, ui
 {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds, 16, voff, soff, 0, 0);
 }
+// the same 16 bytes into registers (buffer_load_dwordx4)
+__device__ inline u32x4 buf_load16(BufRes r, uint32_t voff, uint32_t soff)
+{
+    return __builtin_amdgcn_raw_buffer_load_b128(r, int(voff), int(soff), 0);
+}
 #else
 typedef int BufRes; // host pass: never called
 __device__ inline BufRes buf_res(const void*, uint32_t) { return 0; }
 __device__ inline void buf_load_lds16(BufRes, lds_void*, uint32_t, uint32_t) {}
+__device__ inline u32x4 buf_load16(BufRes, uint32_t, uint32_t) { return u32x4{}; }
 #endif
 
 // ---- GEMM dispatch plan (gemm.hip), shared with the engine's launch-grouping cost model ----
