@@ -64,6 +64,18 @@ GemmPlan gemm_plan(const mk_gemm_args* a, uint32_t n, uint32_t cus);
 // Its estimated duration in units of one 256-channel k step.
 double gemm_cost(const mk_gemm_args* a, uint32_t n, uint32_t cus);
 
+// ---- ln_modulate over one or two problems in one launch (kernels.hip; the engine groups the two streams) ----
+struct LnArgs {
+    const float* x;
+    const float* scale;
+    const float* shift;
+    int64_t alt;
+    uint32_t rows, split, seg_rows;
+    void* y;
+};
+// count 1 or 2 problems of width n (the mk_ln_modulate arguments each); one launch when n is 2048, 3072 or 4096
+mk_status ln_modulate_group(const LnArgs* a, int count, uint32_t n, float eps, void* stream);
+
 // ---- error state (thread-local, read by mk_last_error) ----
 void set_error(const std::string& msg);
 mk_status fail(mk_status s, const std::string& msg);
@@ -122,21 +134,43 @@ __host__ __device__ inline float e4m3_to_f32(uint8_t b)
     return s ? -v : v;
 }
 
-// ---- wave64 reductions (DPP-free: the compiler lowers shfl_xor to ds_swizzle / permute) ----
+// ---- wave64 reductions, every lane gets the result ----
+// On the device on the VALU only: two quad permutations, the half-row and row mirrors (DPP operands), then
+// gfx950's v_permlane16_swap (rows 2k <-> 2k + 1) and v_permlane32_swap (halves); each step adds the partner's value.
+// (A shfl_xor ladder is six ds_bpermute round trips through the LDS unit, the latency that bounds one-wave-a-row
+// kernels.) Patterns stay inside a row, so no lane reads out of range.
+#if defined(__HIP_DEVICE_COMPILE__)
+template <int CTRL> __device__ inline float dpp_f(float v)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+template <class Op> __device__ inline float wave_reduce(float v, Op op)
+{
+    v = op(v, dpp_f<0xB1>(v));  // quad_perm [1,0,3,2]
+    v = op(v, dpp_f<0x4E>(v));  // quad_perm [2,3,0,1]
+    v = op(v, dpp_f<0x141>(v)); // row_half_mirror: lane i <-> 7 - i within each 8
+    v = op(v, dpp_f<0x140>(v)); // row_mirror: lane i <-> 15 - i within each row
+    uint32_t u = __builtin_bit_cast(uint32_t, v);
+    const auto r16 = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    const uint32_t a16 = r16[0], b16 = r16[1];
+    v = op(__builtin_bit_cast(float, a16), __builtin_bit_cast(float, b16));
+    u = __builtin_bit_cast(uint32_t, v);
+    const auto r32 = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    const uint32_t a32 = r32[0], b32 = r32[1];
+    return op(__builtin_bit_cast(float, a32), __builtin_bit_cast(float, b32));
+}
 __device__ inline float wave_sum(float v)
 {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1)
-        v += __shfl_xor(v, o, 64);
-    return v;
+    return wave_reduce(v, [](float a, float b) { return a + b; });
 }
 __device__ inline float wave_max(float v)
 {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1)
-        v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
+    return wave_reduce(v, [](float a, float b) { return fmaxf(a, b); });
 }
+#else
+__device__ inline float wave_sum(float v) { return v; }
+__device__ inline float wave_max(float v) { return v; }
+#endif
 
 // Combine lane i with lane i ^ 32 through v_permlane32_swap (a VALU op: swaps the upper 32 lanes of one register
 // with the lower 32 of the other), not a ds_bpermute round trip through the LDS unit. Swapping a value with itself

@@ -528,11 +528,17 @@ struct mk_engine {
             } st[2] = {{&x_img, &xn_img, N, S, 0, mi, hid.h()}, {&x_txt, &xn_txt, S, 0, 1, mt, hid.h() + size_t(nb) * N * F}};
             mk_heads_args ha[2];
             mk_gemm_args g[2];
+            // both streams' norms in one launch: scale m + D, shift m (and below m + 4D, m + 3D)
+            auto ln2 = [&](int scale_off, int shift_off) {
+                LnArgs la[2];
+                for (int j = 0; j < 2; ++j)
+                    la[j] = LnArgs{st[j].x->f(), st[j].m + scale_off, st[j].m + shift_off, 0, nb * st[j].rows, 0, 1,
+                                   st[j].xn->p};
+                return timed("ln_modulate", 0, [&] { return ln_modulate_group(la, 2, D, eps, stream); });
+            };
+            MK_TRY(ln2(D, 0));
             for (int j = 0; j < 2; ++j) {
                 const St& s = st[j];
-                MK_TRY(timed("ln_modulate", 0, [&] {
-                    return mk_ln_modulate(s.x->f(), nb * s.rows, D, s.m + D, s.m, 0, 0, 1, eps, s.xn->p, stream);
-                }));
                 ha[j] = mk_heads_args{};
                 ha[j].q = q.p;
                 ha[j].k = k.p;
@@ -564,12 +570,9 @@ struct mk_engine {
                                  MK_EPI_GATE_ADD, MK_F32, s.m + 2 * D);
             }
             MK_TRY(gemm2(g));
+            MK_TRY(ln2(4 * D, 3 * D));
             for (int j = 0; j < 2; ++j) {
                 const St& s = st[j];
-                MK_TRY(timed("ln_modulate", 0, [&] {
-                    return mk_ln_modulate(s.x->f(), nb * s.rows, D, s.m + 4 * D, s.m + 3 * D, 0, 0, 1, eps, s.xn->p,
-                                          stream);
-                }));
                 g[j] = gemm_args(B.ff1[s.which], s.xn->p, D, 0, nb * s.rows, 1, s.hid, F, 0, MK_EPI_GELU_TANH, MK_BF16);
             }
             MK_TRY(gemm2(g));

@@ -67,21 +67,34 @@ __global__ __launch_bounds__(256) void ln_modulate_kernel(const float* __restric
 
 // ln_modulate for rows of exactly 256 NV floats: the lane's NV float4s of scale and shift are loaded before the row's
 // statistics are reduced (their L2 latency overlaps the row's HBM read), and the register arrays are sized to the row.
+// Up to two ln_modulate problems in one launch (the image and text streams of a block): blocks [0, blocks0) take
+// problem 0, the rest problem 1, four rows a block.
+struct LnP {
+    const float* x;
+    const float* scale;
+    const float* shift;
+    int64_t alt;
+    uint32_t rows, split, seg_rows;
+    uint16_t* y;
+};
+struct LnG {
+    LnP p[2];
+    uint32_t blocks0;
+};
+
 template <int NV>
-__global__ __launch_bounds__(256) void ln_modulate_nv_kernel(const float* __restrict__ x, uint32_t rows,
-                                                             const float* __restrict__ scale,
-                                                             const float* __restrict__ shift, int64_t alt,
-                                                             uint32_t split, uint32_t seg_rows, float eps,
-                                                             uint16_t* __restrict__ y)
+__global__ __launch_bounds__(256) void ln_modulate_nv_kernel(LnG g, float eps)
 {
     constexpr uint32_t n = 256 * NV;
-    const uint32_t lane = threadIdx.x & 63, row = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (row >= rows)
+    const bool second = blockIdx.x >= g.blocks0;
+    const LnP& P = g.p[second];
+    const uint32_t lane = threadIdx.x & 63, row = (blockIdx.x - (second ? g.blocks0 : 0)) * 4 + (threadIdx.x >> 6);
+    if (row >= P.rows)
         return;
-    const int64_t off = (row % seg_rows) < split ? alt : 0;
-    const f32x4* sc = reinterpret_cast<const f32x4*>(scale + off);
-    const f32x4* sh = shift ? reinterpret_cast<const f32x4*>(shift + off) : nullptr;
-    const f32x4* xr = reinterpret_cast<const f32x4*>(x + uint64_t(row) * n);
+    const int64_t off = (row % P.seg_rows) < P.split ? P.alt : 0;
+    const f32x4* sc = reinterpret_cast<const f32x4*>(P.scale + off);
+    const f32x4* sh = P.shift ? reinterpret_cast<const f32x4*>(P.shift + off) : nullptr;
+    const f32x4* xr = reinterpret_cast<const f32x4*>(P.x + uint64_t(row) * n);
     f32x4 a[NV], b[NV], v[NV];
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
@@ -103,7 +116,7 @@ __global__ __launch_bounds__(256) void ln_modulate_nv_kernel(const float* __rest
             q += d * d;
         }
     const float inv = rsqrtf(wave_sum(q) / float(n) + eps);
-    u32x2* yr = reinterpret_cast<u32x2*>(y + uint64_t(row) * n);
+    u32x2* yr = reinterpret_cast<u32x2*>(P.y + uint64_t(row) * n);
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
         float o[4];
@@ -546,6 +559,46 @@ inline uint32_t grid_for(uint64_t n)
 inline hipStream_t S(void* s) { return static_cast<hipStream_t>(s); }
 
 } // namespace
+
+mk_status ln_modulate_group(const LnArgs* a, int count, uint32_t n, float eps, void* stream)
+{
+    if (count < 1 || count > 2 || n % 4 || n > 4u * 64 * kMaxVec)
+        return fail(MK_ERR_ARG, "ln_modulate: 1 or 2 problems, n a multiple of 4 up to 4096");
+    LnG g{};
+    uint32_t blocks = 0;
+    int m = 0;
+    for (int i = 0; i < count; ++i) {
+        if (!a[i].x || !a[i].scale || !a[i].y || !a[i].seg_rows)
+            return fail(MK_ERR_ARG, "ln_modulate: null pointer or seg_rows 0");
+        if (!a[i].rows)
+            continue;
+        g.p[m] = LnP{a[i].x, a[i].scale, a[i].shift, a[i].alt, a[i].rows, a[i].split, a[i].seg_rows,
+                     static_cast<uint16_t*>(a[i].y)};
+        if (m == 0)
+            g.blocks0 = cdiv(a[i].rows, 4);
+        blocks += cdiv(a[i].rows, 4);
+        ++m;
+    }
+    if (!m)
+        return MK_OK;
+    if (m == 1)
+        g.blocks0 = blocks;
+    const dim3 grid(blocks);
+    if (n == 3072)
+        ln_modulate_nv_kernel<12><<<grid, 256, 0, S(stream)>>>(g, eps);
+    else if (n == 4096)
+        ln_modulate_nv_kernel<16><<<grid, 256, 0, S(stream)>>>(g, eps);
+    else if (n == 2048)
+        ln_modulate_nv_kernel<8><<<grid, 256, 0, S(stream)>>>(g, eps);
+    else
+        for (int i = 0; i < m; ++i) {
+            const LnP& P = g.p[i];
+            ln_modulate_kernel<<<cdiv(P.rows, 4), 256, 0, S(stream)>>>(P.x, P.rows, n, P.scale, P.shift, P.alt,
+                                                                       P.split, P.seg_rows, eps, P.y);
+        }
+    MK_LAUNCH_CHECK("ln_modulate");
+    return MK_OK;
+}
 } // namespace mk
 
 using namespace mk;
@@ -555,22 +608,8 @@ extern "C" {
 mk_status mk_ln_modulate(const float* x, uint32_t rows, uint32_t n, const float* scale, const float* shift,
                          int64_t alt, uint32_t split, uint32_t seg_rows, float eps, void* y, void* stream)
 {
-    if (!x || !scale || !y || n % 4 || n > 4u * 64 * kMaxVec || !seg_rows)
-        return fail(MK_ERR_ARG, "ln_modulate: null pointer, or n not a multiple of 4 up to 4096, or seg_rows 0");
-    if (!rows)
-        return MK_OK;
-    uint16_t* yb = static_cast<uint16_t*>(y);
-    const dim3 grid(cdiv(rows, 4));
-    if (n == 3072)
-        ln_modulate_nv_kernel<12><<<grid, 256, 0, S(stream)>>>(x, rows, scale, shift, alt, split, seg_rows, eps, yb);
-    else if (n == 4096)
-        ln_modulate_nv_kernel<16><<<grid, 256, 0, S(stream)>>>(x, rows, scale, shift, alt, split, seg_rows, eps, yb);
-    else if (n == 2048)
-        ln_modulate_nv_kernel<8><<<grid, 256, 0, S(stream)>>>(x, rows, scale, shift, alt, split, seg_rows, eps, yb);
-    else
-        ln_modulate_kernel<<<grid, 256, 0, S(stream)>>>(x, rows, n, scale, shift, alt, split, seg_rows, eps, yb);
-    MK_LAUNCH_CHECK("ln_modulate");
-    return MK_OK;
+    const LnArgs a{x, scale, shift, alt, rows, split, seg_rows, y};
+    return ln_modulate_group(&a, 1, n, eps, stream);
 }
 
 mk_status mk_rms_norm(const float* x, uint32_t rows, uint32_t n, const float* w, float w_offset, float eps, void* y,
