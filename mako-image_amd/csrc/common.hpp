@@ -163,12 +163,25 @@ __device__ inline float wave_sum(float v)
 {
     return wave_reduce(v, [](float a, float b) { return a + b; });
 }
+// sum over the 32 lanes of each half wave (lanes 0-31, 32-63): the same steps without the final 32-lane swap
+__device__ inline float half_sum(float v)
+{
+    v += dpp_f<0xB1>(v);
+    v += dpp_f<0x4E>(v);
+    v += dpp_f<0x141>(v);
+    v += dpp_f<0x140>(v);
+    const uint32_t u = __builtin_bit_cast(uint32_t, v);
+    const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    const uint32_t a = r[0], b = r[1];
+    return __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
+}
 __device__ inline float wave_max(float v)
 {
     return wave_reduce(v, [](float a, float b) { return fmaxf(a, b); });
 }
 #else
 __device__ inline float wave_sum(float v) { return v; }
+__device__ inline float half_sum(float v) { return v; }
 __device__ inline float wave_max(float v) { return v; }
 #endif
 

@@ -289,10 +289,8 @@ __device__ inline void epi_heads(const GemmP& p, const float* st, int ld, int to
             ss[i] = x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3];
         }
 #pragma unroll
-        for (int m = 1; m < 32; m <<= 1)
-#pragma unroll
-            for (int i = 0; i < 16; ++i)
-                ss[i] += __shfl_xor(ss[i], m, 64);
+        for (int i = 0; i < 16; ++i)
+            ss[i] = half_sum(ss[i]); // lanes 0-31 hold row 2i, lanes 32-63 row 2i + 1
 #pragma unroll
         for (int i = 0; i < 16; ++i)
             inv[i] = rsqrtf(ss[i] * (1.0f / 128.0f) + h.eps);
