@@ -369,53 +369,56 @@ __global__ __launch_bounds__(256) void gemv_kernel(const float* __restrict__ x, 
     }
 }
 
-// GEMV for one row with K = 512 * KI: x' is read straight into registers (lane l holds k = 8 l + 512 i), so no LDS
-// staging or barrier precedes the weight stream; each wave computes 4 outputs with all 4 * KI of its 16-byte weight
-// loads issued up front.
+// GEMV for one row with K = 512 * KI: each wave computes 4 outputs with all 4 * KI of its 16-byte weight loads
+// issued first; while they are in flight the workgroup (8 waves, 32 outputs) converts x' to bf16 in LDS once (each
+// wave converting the whole row itself cost more VALU time than the dot products), and the dot products take the
+// bf16 pairs as they are (v_dot2_f32_bf16).
 template <int KI>
-__global__ __launch_bounds__(256) void gemv1_kernel(const float* __restrict__ x, const uint16_t* __restrict__ w,
+__global__ __launch_bounds__(512) void gemv1_kernel(const float* __restrict__ x, const uint16_t* __restrict__ w,
                                                     const float* __restrict__ bias, uint32_t N, float* __restrict__ y,
                                                     int silu_x)
 {
     constexpr uint32_t K = 512 * KI;
-    const uint32_t lane = threadIdx.x & 63, n0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 4;
+    __shared__ __attribute__((aligned(16))) uint16_t xs[K];
+    const uint32_t lane = threadIdx.x & 63, n0 = (blockIdx.x * 8 + (threadIdx.x >> 6)) * 4;
+    // the wave's 4 weight rows first (16-byte chunks, all in flight; rows past N read the last row)
+    u32x4 wv[4][KI];
+    if (n0 < N)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int i = 0; i < KI; ++i)
+                wv[j][i] = *reinterpret_cast<const u32x4*>(w + uint64_t(min(n0 + j, N - 1)) * K + lane * 8 + 512 * i);
+    // meanwhile the input row, once a workgroup, as the GEMMs' bf16 activation operand (silu first when asked)
+    for (uint32_t k = threadIdx.x; k < K / 2; k += 512) {
+        float a = x[2 * k], b = x[2 * k + 1];
+        if (silu_x) {
+            a = a / (1.0f + __expf(-a));
+            b = b / (1.0f + __expf(-b));
+        }
+        *reinterpret_cast<uint32_t*>(&xs[2 * k]) = pack_bf16x2(a, b);
+    }
+    __syncthreads();
     if (n0 >= N)
         return;
-    u32x4 wv[4][KI];
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int i = 0; i < KI; ++i)
-            wv[j][i] = *reinterpret_cast<const u32x4*>(w + uint64_t(min(n0 + j, N - 1)) * K + lane * 8 + 512 * i);
-    float xv[KI][8];
+    // bf16 pairs straight into v_dot2_f32_bf16 (exact products, fp32 sums)
+    typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int i = 0; i < KI; ++i) {
-        const f32x4* xp = reinterpret_cast<const f32x4*>(x + lane * 8 + 512 * i);
-        const f32x4 a = xp[0], b = xp[1];
+        const u32x4 xv = *reinterpret_cast<const u32x4*>(&xs[lane * 8 + 512 * i]);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            xv[i][e] = a[e];
-            xv[i][4 + e] = b[e];
-        }
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const float v = xv[i][e];
-            xv[i][e] = bf2f_bits(f2bf_bits(silu_x ? v / (1.0f + __expf(-v)) : v)); // the GEMMs' bf16 activation operand
-        }
-    }
-    float acc[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        float s = 0.0f;
-#pragma unroll
-        for (int i = 0; i < KI; ++i)
+        for (int j = 0; j < 4; ++j)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const uint32_t u = wv[j][i][e];
-                s += bf2f_bits(uint16_t(u)) * xv[i][2 * e] + bf2f_bits(uint16_t(u >> 16)) * xv[i][2 * e + 1];
+                const uint32_t wu = wv[j][i][e], xu = xv[e];
+                acc[j] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, wu),
+                                                         __builtin_bit_cast(bf16x2, xu), acc[j], false);
             }
-        acc[j] = wave_sum(s);
     }
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        acc[j] = wave_sum(acc[j]);
     if (lane < 4) {
         const float v = lane == 0 ? acc[0] : lane == 1 ? acc[1] : lane == 2 ? acc[2] : acc[3];
         if (n0 + lane < N)
@@ -713,13 +716,13 @@ mk_status mk_gemv(const float* x, uint32_t rows, uint32_t K, const void* w, cons
     if (!x || !w || !y || rows == 0 || rows > 4 || K % 8 || uint64_t(rows) * K * 4 > 64 * 1024)
         return fail(MK_ERR_ARG, "gemv: null pointer, rows not 1..4, K not a multiple of 8 or rows*K over 16384");
     const uint16_t* wb = static_cast<const uint16_t*>(w);
-    const dim3 grid(cdiv(N, 16));
+    const dim3 grid(cdiv(N, 16)), grid1(cdiv(N, 32));
     if (rows == 1 && K == 3072)
-        gemv1_kernel<6><<<grid, 256, 0, S(stream)>>>(x, wb, bias, N, y, silu_x);
+        gemv1_kernel<6><<<grid1, 512, 0, S(stream)>>>(x, wb, bias, N, y, silu_x);
     else if (rows == 1 && K == 4096)
-        gemv1_kernel<8><<<grid, 256, 0, S(stream)>>>(x, wb, bias, N, y, silu_x);
+        gemv1_kernel<8><<<grid1, 512, 0, S(stream)>>>(x, wb, bias, N, y, silu_x);
     else if (rows == 1 && K == 2048)
-        gemv1_kernel<4><<<grid, 256, 0, S(stream)>>>(x, wb, bias, N, y, silu_x);
+        gemv1_kernel<4><<<grid1, 512, 0, S(stream)>>>(x, wb, bias, N, y, silu_x);
     else
         gemv_kernel<<<grid, 256, rows * K * 4, S(stream)>>>(x, rows, K, wb, bias, N, y, silu_x);
     MK_LAUNCH_CHECK("gemv");
