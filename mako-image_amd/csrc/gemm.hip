@@ -411,7 +411,12 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
     constexpr int NT = 64 * NW;                 // threads
     constexpr int WM = BM / (NW / 2);           // tokens per wave (waves: 2 along channels x NW/2 along tokens)
     constexpr int WC = BN / 2;                  // channels per wave
-    constexpr int TB = WM / 32, CB = WC / 32;   // 32-row MFMA blocks per wave along tokens / channels
+    // 8-wave tiles run v_mfma_f32_16x16x32_bf16 (16 x 16 output blocks, 32-deep substeps: 3-4% faster than the
+    // 32 x 32 x 16 form on the step's shapes, where the matrix cores are held by the power limit; bit-identical
+    // results), 4-wave tiles v_mfma_f32_32x32x16_bf16.
+    constexpr bool M16 = NW == 8;
+    constexpr int MB = M16 ? 16 : 32;
+    constexpr int TB = WM / MB, CB = WC / MB;   // MFMA blocks per wave along tokens / channels
     constexpr int RA = BM * 8 / NT;             // direct-load rounds for the activation tile (64 chunks per wave)
     constexpr int RW = BN * 8 / NT;             // ... for a bf16 weight tile
     constexpr int LW = BN * 4 / NT;             // 16-byte fp8 weight chunks per thread (register staged)
@@ -489,16 +494,18 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
         }
     };
 
-    f32x16 acc[CB][TB];
+    std::conditional_t<M16, f32x4, f32x16> acc[CB][TB];
 #pragma unroll
     for (int i = 0; i < CB; ++i)
 #pragma unroll
         for (int j = 0; j < TB; ++j)
-            acc[i][j] = f32x16{};
+            acc[i][j] = {};
 
     // v_mfma_f32_32x32x16_bf16: lane (r32, hk) supplies row r32 of a 32-row block and k values 8 hk .. 8 hk + 7 of
     // a 16-wide substep, and holds output rows (channels) 8 i + 4 hk .. + 3 (i < 4) of column r32 (token).
-    const int r32 = lane & 31, hk = lane >> 5;
+    // v_mfma_f32_16x16x32_bf16: lane (r16, g4) supplies row r16 of a 16-row block and k values 8 g4 .. 8 g4 + 7 of
+    // a 32-wide substep, and holds output rows 4 g4 .. 4 g4 + 3 of column r16.
+    const int r32 = lane & 31, hk = lane >> 5, r16 = lane & 15, g4 = lane >> 4;
     // fragment j of a substep in first-use order (the MFMAs run channel-block-major): weight block 0, the token
     // blocks, then weight blocks 1 ..
     auto frag = [&](int buf, int ks, int j, bf16x8(&wf)[CB], bf16x8(&af)[TB]) {
@@ -509,6 +516,13 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
         } else {
             af[j - 1] = *reinterpret_cast<const bf16x8*>(&sA[buf][swz(wm * WM + (j - 1) * 32 + r32, kc)]);
         }
+    };
+    // 16 x 16 x 32 fragments: weight block cb, token block tb of substep ks
+    auto rdw = [&](int buf, int ks, int cb, bf16x8(&wf)[CB]) {
+        wf[cb] = *reinterpret_cast<const bf16x8*>(&sW[buf][swz(wn * WC + cb * 16 + r16, ks * 4 + g4)]);
+    };
+    auto rda = [&](int buf, int ks, int tb, bf16x8(&af)[TB]) {
+        af[tb] = *reinterpret_cast<const bf16x8*>(&sA[buf][swz(wm * WM + tb * 16 + r16, ks * 4 + g4)]);
     };
     // 128-channel tiles (4 waves, one a SIMD) with bf16 weights stage the operands through registers: a thread
     // loads its ND 16-byte chunks of a k step into registers (buffer loads) and later writes each to the LDS chunk a
@@ -558,7 +572,8 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
 #pragma unroll
         for (int i = 0; i < CB * TB; ++i) {
             const int cb = i / TB, tb = i % TB;
-            acc[cb][tb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[cb], af[tb], acc[cb][tb], 0, 0, 0);
+            if constexpr (!M16)
+                acc[cb][tb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[cb], af[tb], acc[cb][tb], 0, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
             if (nks >= 0 && i < CB + TB) {
                 frag(nbuf, nks, i, nwf, naf);
@@ -577,10 +592,41 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
             move(i);
     };
 
+    // 16 x 16 x 32 substep (32 MFMAs for a 64 x 128 wave tile): the weight fragments are single-buffered, each
+    // next-substep fragment read into its register right after the MFMA that last uses it; the token fragments of
+    // the next substep go to the other buffer (naf) with the first channel block; direct loads g0 .. g1 - 1 of step
+    // gkt into buffer gbuf follow the MFMAs one each.
+    auto group16 = [&](bf16x8(&wf)[CB], const bf16x8(&af)[TB], int nbuf, int nks, bf16x8(&naf)[TB], int gkt,
+                       int gbuf, auto g0_c, auto g1_c) {
+        constexpr int g0 = decltype(g0_c)::value, g1 = decltype(g1_c)::value;
+#pragma unroll
+        for (int i = 0; i < CB * TB; ++i) {
+            const int cb = i / TB, tb = i % TB;
+            if constexpr (M16)
+                acc[cb][tb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[cb], af[tb], acc[cb][tb], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            if (nks >= 0 && cb == 0) {
+                rda(nbuf, nks, tb, naf);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            if (nks >= 0 && tb == TB - 1) {
+                rdw(nbuf, nks, cb, wf);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            if (g0 + i < g1) {
+                dma1(gkt, gbuf, g0 + i);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+#pragma unroll
+        for (int i = CB * TB; i < g1 - g0; ++i)
+            dma1(gkt, gbuf, g0 + i);
+    };
+
     using C0 = std::integral_constant<int, 0>;
     using CH = std::integral_constant<int, ND / 2>;
     using CN = std::integral_constant<int, ND>;
-    bf16x8 wf0[CB], af0[TB], wf1[CB], af1[TB];
+    bf16x8 wf0[CB], af0[TB], wf1[CB], af1[TB]; // (16 x 16 x 32: wf0 is the single weight buffer)
     if constexpr (!kStage) {
         // Software pipeline over k steps of four 16-wide substeps: step t is in LDS buffer t & 1; step t + 1 lands
         // in the other buffer during step t (the first half of its direct loads goes out with the last substep of
@@ -590,9 +636,10 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
         commit_f8(0);
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
-        // the first half of step kb + 1 (the first step issues the second, as every step does)
+        // step kb + 1: 32 x 32 x 16, its first half (each step issues the next one's second half); 16 x 16 x 32,
+        // all of it (each step issues the whole step after next)
 #pragma unroll
-        for (int i = 0; i < ND / 2; ++i)
+        for (int i = 0; i < (M16 ? ND : ND / 2); ++i)
             dma1(min(kb + 1, ke - 1), 1, i);
         load_f8(min(kb + 1, ke - 1));
     } else {
@@ -616,14 +663,33 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
         for (int i = 0; i < ND / 2; ++i)
             swrite(1, i);
     }
+    if constexpr (M16) {
 #pragma unroll
-    for (int j = 0; j < CB + TB; ++j)
-        frag(0, 0, j, wf0, af0);
+        for (int cb = 0; cb < CB; ++cb)
+            rdw(0, 0, cb, wf0);
+#pragma unroll
+        for (int tb = 0; tb < TB; ++tb)
+            rda(0, 0, tb, af0);
+    } else {
+#pragma unroll
+        for (int j = 0; j < CB + TB; ++j)
+            frag(0, 0, j, wf0, af0);
+    }
     // one k step from buffer `buf` (a constant: the loop is unrolled by two, so every LDS address is a register
     // base plus an immediate offset)
     auto step = [&](int kt, auto buf_c) {
         constexpr int buf = decltype(buf_c)::value;
-        if constexpr (!kStage) {
+        if constexpr (M16) {
+            // two 32-deep substeps: the second substep's fragments are read during the first; after the barrier
+            // (step kt + 1 complete in the other buffer, every wave done with this one) the second substep reads
+            // the next step's first fragments and loads step kt + 2 into this buffer
+            group16(wf0, af0, buf, 1, af1, 0, 0, C0{}, C0{});
+            commit_f8(buf ^ 1);
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+            load_f8(min(kt + 2, ke - 1));
+            group16(wf0, af1, buf ^ 1, 0, af0, min(kt + 2, ke - 1), buf, C0{}, CN{});
+        } else if constexpr (!kStage) {
             group(wf0, af0, buf, 1, wf1, af1, min(kt + 1, ke - 1), buf ^ 1, CH{}, CN{}, 0, C0{}, C0{});
             group(wf1, af1, buf, 2, wf0, af0, 0, 0, C0{}, C0{}, 0, C0{}, C0{});
             group(wf0, af0, buf, 3, wf1, af1, 0, 0, C0{}, C0{}, 0, C0{}, C0{});
@@ -655,7 +721,7 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
     __syncthreads();
 
     // ---- stream-K: publish this range's partial, or add the earlier ranges' partials ----
-    constexpr int NACC = CB * TB * 16;
+    constexpr int NACC = CB * TB * (M16 ? 4 : 16);
     // The workspace is uncached (not held in any XCD's L2): a partial is plain 16-byte stores, complete at the memory
     // once acknowledged; the flag store follows every wave's acknowledgements. Slot layout: 16-byte groups
     // q = 4 * block + j / 4 of the accumulators as [q][thread][4 floats], so one group of a wave is 1 KB contiguous
@@ -665,11 +731,15 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
 #pragma unroll
         for (int cb = 0; cb < CB; ++cb)
 #pragma unroll
-            for (int tb = 0; tb < TB; ++tb)
+            for (int tb = 0; tb < TB; ++tb) {
+                if constexpr (M16)
+                    w[size_t(cb * TB + tb) * NT] = acc[cb][tb];
+                else
 #pragma unroll
-                for (int m = 0; m < 4; ++m)
-                    w[size_t((cb * TB + tb) * 4 + m) * NT] =
-                        f32x4{acc[cb][tb][4 * m], acc[cb][tb][4 * m + 1], acc[cb][tb][4 * m + 2], acc[cb][tb][4 * m + 3]};
+                    for (int m = 0; m < 4; ++m)
+                        w[size_t((cb * TB + tb) * 4 + m) * NT] = f32x4{acc[cb][tb][4 * m], acc[cb][tb][4 * m + 1],
+                                                                      acc[cb][tb][4 * m + 2], acc[cb][tb][4 * m + 3]};
+            }
         __builtin_amdgcn_s_waitcnt(0); // every store acknowledged at the coherent level
         __syncthreads();
         if (tid == 0)
@@ -711,7 +781,7 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
                 __builtin_amdgcn_s_waitcnt(0);
 #pragma unroll
                 for (int q = 0; q < QL; ++q) {
-                    const int g = pass * QL + q, b = g / 4, j0 = (g % 4) * 4;
+                    const int g = pass * QL + q, b = M16 ? g : g / 4, j0 = M16 ? 0 : (g % 4) * 4;
                     const f32x4 v = mine[q * 64];
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
@@ -729,37 +799,44 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
     // its release fence waits for vmcnt 0) ----
     float* st = reinterpret_cast<float*>(smem) + wave * 32 * LDW;
     const int64_t zc = int64_t(z) * p.sc;
-    if constexpr (EK == EK_HEADS) {
-        // the heads epilogue is large: one copy of it in a rolled loop over the 32-token blocks, which always
-        // stages block 0 of the accumulators and then rotates the next block into its place (static register
-        // indices, so the accumulators stay in registers)
-#pragma unroll 1
-        for (int tb = 0; tb < TB; ++tb) {
+    // the wave's 32-token slice s (token blocks s for 32 x 32 x 16, 2 s and 2 s + 1 for 16 x 16 x 32) into st
+    auto stage = [&](int s) {
 #pragma unroll
-            for (int cb = 0; cb < CB; ++cb)
+        for (int cb = 0; cb < CB; ++cb) {
+            if constexpr (M16) {
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+                    *reinterpret_cast<f32x4*>(st + (16 * h + r16) * LDW + cb * 16 + 4 * g4) = acc[cb][2 * s + h];
+            } else {
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
                     *reinterpret_cast<f32x4*>(st + r32 * LDW + cb * 32 + 8 * i + 4 * hk) =
-                        f32x4{acc[cb][0][4 * i], acc[cb][0][4 * i + 1], acc[cb][0][4 * i + 2], acc[cb][0][4 * i + 3]};
-            epi_heads(p, st, LDW, m0 + wm * WM + tb * 32, n0 + wn * WC, lane, z);
+                        f32x4{acc[cb][s][4 * i], acc[cb][s][4 * i + 1], acc[cb][s][4 * i + 2], acc[cb][s][4 * i + 3]};
+            }
+        }
+    };
+    constexpr int NS = WM / 32, RB = TB / NS; // 32-token slices of a wave, MFMA token blocks a slice
+    if constexpr (EK == EK_HEADS) {
+        // the heads epilogue is large: one copy of it in a rolled loop over the 32-token slices, which always
+        // stages slice 0 of the accumulators and then rotates the next slice into its place (static register
+        // indices, so the accumulators stay in registers)
+#pragma unroll 1
+        for (int s = 0; s < NS; ++s) {
+            stage(0);
+            epi_heads(p, st, LDW, m0 + wm * WM + s * 32, n0 + wn * WC, lane, z);
 #pragma unroll
             for (int cb = 0; cb < CB; ++cb)
 #pragma unroll
-                for (int t = 0; t + 1 < TB; ++t)
-                    acc[cb][t] = acc[cb][t + 1];
+                for (int t = 0; t + RB < TB; ++t)
+                    acc[cb][t] = acc[cb][t + RB];
         }
         return;
     }
     EpiCh kch = epi_channels(p, n0 + wn * WC + 4 * (lane % (WC / 4)));
 #pragma unroll
-    for (int tb = 0; tb < TB; ++tb) {
-#pragma unroll
-        for (int cb = 0; cb < CB; ++cb)
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                *reinterpret_cast<f32x4*>(st + r32 * LDW + cb * 32 + 8 * i + 4 * hk) =
-                    f32x4{acc[cb][tb][4 * i], acc[cb][tb][4 * i + 1], acc[cb][tb][4 * i + 2], acc[cb][tb][4 * i + 3]};
-        epi_slice<EK, WC>(p, st, LDW, m0 + wm * WM + tb * 32, n0 + wn * WC, lane, zc, kch);
+    for (int s = 0; s < NS; ++s) {
+        stage(s);
+        epi_slice<EK, WC>(p, st, LDW, m0 + wm * WM + s * 32, n0 + wn * WC, lane, zc, kch);
     }
 }
 
