@@ -109,6 +109,13 @@ struct mk_engine {
     static constexpr float kScaleLog2 = 0.12751743082459868f;
     mk_config cfg{};
     hipStream_t stream = nullptr;
+    // The per-block modulation GEMVs (HBM-bound, 36 us each) run on a second stream, block i's on event mod_ready[i]:
+    // their workgroups fill compute units the block GEMMs' partial last rounds leave idle. Default priority, like the
+    // main stream; the side stream starts a step only after temb_ready, recorded on the main stream after all of
+    // the previous step's work, so it never overwrites modulation a running block still reads.
+    hipStream_t side = nullptr;
+    hipEvent_t temb_ready = nullptr;
+    std::vector<hipEvent_t> mod_ready;
     uint32_t cus = 256; // compute units of the engine's device
     std::vector<void*> allocs; // weight storage
     std::map<std::string, Dest> dests;
@@ -498,8 +505,22 @@ struct mk_engine {
         MK_TRY(timed("gemv", 2.0 * D * 256, [&] { return mk_gemv(tproj.f(), 1, 256, t_lin1.w, t_lin1.bias, D, temb_h.f(), 0, stream); }));
         MK_TRY(timed("gemv", 2.0 * D * D, [&] { return mk_gemv(temb_h.f(), 1, D, t_lin2.w, t_lin2.bias, D, temb.f(), 1, stream); }));
         MK_TRY(probe_f32("temb", -1, temb.f(), D));
-        MK_TRY(timed("gemv", 2.0 * mods.out * D, [&] { return mk_gemv(temb.f(), 1, D, mods.w, mods.bias, mods.out, mod.f(), 1, stream); }));
-        MK_TRY(probe_f32("modulation", -1, mod.f(), size_t(cfg.blocks) * 12 * D));
+        // every block's modulation: one GEMV over the stacked matrix when timing or probing (serial, measured), else
+        // one GEMV a block on the side stream
+        const bool side_mods = !timing.on && !probe && side && mod_ready.size() >= cfg.blocks;
+        if (side_mods) {
+            MK_HIP(hipEventRecord(temb_ready, stream));
+            MK_HIP(hipStreamWaitEvent(side, temb_ready, 0));
+            for (uint32_t i = 0; i < cfg.blocks; ++i) {
+                const size_t r0 = size_t(i) * 12 * D;
+                MK_TRY(mk_gemv(temb.f(), 1, D, static_cast<const uint16_t*>(mods.w) + r0 * D,
+                               mods.bias ? mods.bias + r0 : nullptr, 12 * D, mod.f() + r0, 1, side));
+                MK_HIP(hipEventRecord(mod_ready[i], side));
+            }
+        } else {
+            MK_TRY(timed("gemv", 2.0 * mods.out * D, [&] { return mk_gemv(temb.f(), 1, D, mods.w, mods.bias, mods.out, mod.f(), 1, stream); }));
+            MK_TRY(probe_f32("modulation", -1, mod.f(), size_t(cfg.blocks) * 12 * D));
+        }
         MK_TRY(timed("gemv", 2.0 * 2 * D * D, [&] { return mk_gemv(temb.f(), 1, D, norm_out.w, norm_out.bias, 2 * D, omod.f(), 1, stream); }));
         // text in: RMSNorm(w) -> Linear; image in: Linear
         for (uint32_t b = 0; b < nb; ++b)
@@ -517,6 +538,8 @@ struct mk_engine {
             }
         const double attn_flops = 4.0 * double(T) * T * 128 * H * nb;
         for (uint32_t i = 0; i < cfg.blocks; ++i) {
+            if (side_mods)
+                MK_HIP(hipStreamWaitEvent(stream, mod_ready[i], 0));
             const Block& B = blocks[i];
             const float* mi = mod.f() + size_t(i) * 12 * D; // image: shift1, scale1, gate1, shift2, scale2, gate2
             const float* mt = mi + 6 * D;                    // text
@@ -873,6 +896,11 @@ mk_status mk_engine_create(const mk_config* cfg, mk_engine** out)
     if (!e->cfg.max_batch)
         e->cfg.max_batch = 2;
     MK_HIP(hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking));
+    MK_HIP(hipStreamCreateWithFlags(&e->side, hipStreamNonBlocking));
+    MK_HIP(hipEventCreateWithFlags(&e->temb_ready, hipEventDisableTiming));
+    e->mod_ready.resize(e->cfg.blocks);
+    for (auto& ev : e->mod_ready)
+        MK_HIP(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
     int dev = 0, ncu = 0;
     MK_HIP(hipGetDevice(&dev));
     MK_HIP(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev));
@@ -889,8 +917,16 @@ mk_status mk_engine_destroy(mk_engine* e)
     if (!e)
         return MK_OK;
     (void)hipStreamSynchronize(e->stream);
+    if (e->side)
+        (void)hipStreamSynchronize(e->side);
     for (void* p : e->allocs)
         (void)hipFree(p);
+    for (hipEvent_t ev : e->mod_ready)
+        (void)hipEventDestroy(ev);
+    if (e->temb_ready)
+        (void)hipEventDestroy(e->temb_ready);
+    if (e->side)
+        (void)hipStreamDestroy(e->side);
     (void)hipStreamDestroy(e->stream);
     delete e;
     return MK_OK;
