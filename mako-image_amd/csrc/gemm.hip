@@ -1,17 +1,18 @@
-// proj: C = A W^T on gfx950 bf16 MFMA (v_mfma_f32_32x32x16_bf16), fp32 accumulation, with fused epilogues.
+// proj: C = A W^T on gfx950 bf16 MFMA, fp32 accumulation, with fused epilogues.
 //
 // Roles: the weight tile is the MFMA A operand (its M = output channels) and the activation tile the B operand (its
-// N = tokens), so each lane's accumulators hold 4 consecutive channels of one token: the residual / gate epilogues
-// read-modify-write 16 bytes per lane, and a head's 128 channels sit in one lane pair (per-head RMSNorm is one
-// cross-lane add, RoPE pairs are lane-local).
+// N = tokens), so each lane's accumulators hold 4 consecutive channels of one token: the epilogues stage a wave's
+// 32-token slice through LDS and write whole row segments.
 //
 // Tiling: BM = 256 tokens x BN channels x 64 k per workgroup; 256-wide tiles run 8 waves (two a SIMD: 2 along
-// channels x 4 along tokens, 128 x 64 per wave), narrower ones 4 waves (2 x 2). Both tiles are K-contiguous and
-// staged in LDS with a 16-byte-chunk XOR swizzle (chunk ^ ((row >> 1) & 7)) so the fragment reads of 32 rows at one
-// k offset are bank-conflict free. Two LDS buffers: buffer loads write the next k step straight into LDS while the
-// current one's MFMAs run, one barrier per k step. The main loop's instruction order is fixed by hand (every MFMA,
-// fragment read and load fenced): loads and reads spread over the MFMAs, each read issued in the order its MFMA
-// needs it. Workgroups map to tiles XCD-aware (consecutive tiles on one XCD share its L2) and grouped along M.
+// channels x 4 along tokens, 128 x 64 per wave) on v_mfma_f32_16x16x32_bf16, narrower ones 4 waves (2 x 2) on
+// v_mfma_f32_32x32x16_bf16. Both tiles are K-contiguous and staged in LDS with a 16-byte-chunk XOR swizzle
+// (chunk ^ ((row >> 1) & 7)) so the fragment reads of 16 or 32 rows at one k offset are bank-conflict free. Two LDS
+// buffers, one barrier per k step: buffer loads write a later k step straight into LDS while the current one's
+// MFMAs run (128-channel tiles stage it through registers instead). The main loop's instruction order is fixed by
+// hand (every MFMA, fragment read and load fenced): loads and reads spread over the MFMAs, each read issued in the
+// order its MFMA needs it. Workgroups map to tiles XCD-aware (consecutive tiles on one XCD share its L2) and grouped
+// along M.
 #include "common.hpp"
 
 #include <mutex>
