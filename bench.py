@@ -34,6 +34,10 @@ WORKLOADS = {
 }
 H = W = 64
 S = 256
+# SDXL-UNet-shaped spatial transformers at 1024x1024 (128x128x4 latent): (stage, token grid side, channels, depth)
+SDXL_STAGES = (("A", 64, 640, 2), ("B", 32, 1280, 10))
+SDXL_CTX, SDXL_CTX_DIM = 77, 2048
+SDXL_METRIC = "s/SDXL spatial-transformer pass 1024² bf16 (stage A depth 2 + stage B depth 10, CFG batch 2)"
 
 
 def step_flops(blocks=60, D=3072, F=12288, N=4096, S=256, B=2, heads=24):
@@ -42,6 +46,106 @@ def step_flops(blocks=60, D=3072, F=12288, N=4096, S=256, B=2, heads=24):
     lin = 2 * (N + S) * D * (3 * D + D + 2 * F)
     attn = 4 * T * T * 128 * heads
     return B * blocks * (lin + attn), B * blocks * lin, B * blocks * attn
+
+
+def sdxl_flops(n, C, depth, B=2, S=SDXL_CTX):
+    """Algorithmic FLOPs of one SDXL spatial-transformer forward (sdxl.cpp:742-796): per block the self-attention's
+    QKV and output projections (4 C^2 n), the cross-attention's Q and output projections (2 C^2 n; the context's
+    K / V are projected once at begin), GEGLU C -> 8C -> C over 4C (12 C^2 n), self- and cross-attention
+    (4 n^2 C + 4 n S C); proj_in and proj_out once (2 C^2 n)."""
+    block = 2 * 18 * C * C * n + 4 * n * n * C + 4 * n * S * C
+    return B * (depth * block + 2 * 2 * C * C * n), B * depth * (4 * n * n * C + 4 * n * S * C)
+
+
+def bench_sdxl(args):
+    """The SDXL workload: stage A and stage B transformers (random-init bf16 weights, N(0,1) input and context),
+    each forward timed whole (mk_sdxl_forward returns after its stream has finished)."""
+    import numpy as np
+
+    import mkimage as M
+
+    M.call("mk_set_device", 0)
+    rng = np.random.default_rng(0)
+    stages, per, tot_s, tot_f, tot_attn = {}, {}, 0.0, 0.0, 0.0
+    for name, side, C, depth in SDXL_STAGES:
+        n = side * side
+        eng = M.Engine(M.FAMILY_SDXL, blocks=depth, dim=C, heads=C // 64, head_dim=64, ffn=4 * C,
+                       text_dim=SDXL_CTX_DIM)
+        eng.init_random(0)
+        for s in (0, 1):
+            eng.begin(rng.standard_normal((SDXL_CTX, SDXL_CTX_DIM)).astype(np.float32), side, side, s)
+        x = M.Dev.from_array(rng.standard_normal((2, n, C)).astype(np.float32))
+        y = M.Dev(2 * n * C * 4)
+        for _ in range(args.warmup):
+            eng.sdxl_forward(x, 2, n, y)
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            eng.sdxl_forward(x, 2, n, y)
+        sec = (time.perf_counter() - t0) / args.steps
+        if not np.isfinite(y.to_array(np.float32, (2, n, C))).all():
+            raise RuntimeError("non-finite SDXL output")
+        eng.set_timing(True)
+        for _ in range(args.steps):
+            eng.sdxl_forward(x, 2, n, y)
+            for k, v in eng.timing().items():
+                acc = per.setdefault(k, {"ms": 0.0, "launches": 0, "flops": 0.0})
+                acc["ms"] += v["ms"]
+                acc["launches"] += v["launches"]
+                acc["flops"] += v["flops"]
+        eng.set_timing(False)
+        eng.close()
+        fl, fa = sdxl_flops(n, C, depth)
+        stages[name] = {"tokens": n, "channels": C, "heads": C // 64, "depth": depth, "ms": round(sec * 1e3, 3),
+                        "tflop": round(fl / 1e12, 3), "tflops": round(fl / sec / 1e12, 1)}
+        tot_s, tot_f, tot_attn = tot_s + sec, tot_f + fl, tot_attn + fa
+    kernels = {k: {"ms_per_pass": round(v["ms"] / args.steps, 3), "launches_per_pass": v["launches"] // args.steps,
+                   **({"tflops": round(v["flops"] / (v["ms"] / 1e3) / 1e12, 1)} if v["flops"] else {})}
+               for k, v in sorted(per.items(), key=lambda kv: -kv[1]["ms"])}
+    g = per.get("gemm")
+    gemm_tf = g["flops"] / (g["ms"] / 1e3) / 1e12 if g and g["flops"] else None
+    line = {
+        "metric": SDXL_METRIC, "value": round(tot_s, 5), "unit": "s/pass", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(tot_s * 1e3, 3), "higher_is_better": False, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (random-init N(0,0.02) weights, N(0,1) inputs and 77-token contexts)",
+        "config": {"workload": "SDXL-UNet-shaped spatial transformers at 1024x1024, CFG batch 2",
+                   "stages": stages, "context": [SDXL_CTX, SDXL_CTX_DIM]},
+        "roofline": {"bound": "mfma", "kernel": "gemm (bf16 MFMA)", "achieved": round(gemm_tf, 1) if gemm_tf else None,
+                     "peak": PEAK_BF16 / 1e12, "unit": "TFLOP/s",
+                     "frac": round(gemm_tf * 1e12 / PEAK_BF16, 4) if gemm_tf else None, "traffic": None},
+        "pass_tflops": round(tot_f / tot_s / 1e12, 1),
+        "pass_mfma_frac": round(tot_f / tot_s / PEAK_BF16, 4),
+        "kernels": kernels,
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline_sdxl(args.cpu_seconds, tot_f)
+    print(json.dumps(line), flush=True)
+
+
+def cpu_baseline_sdxl(seconds_target, pass_flops):
+    """The oracle's SDXL transformer (one stage-A block, one sample, 1024 tokens) timed on this host, scaled by FLOPs
+    to the whole pass."""
+    import numpy as np
+
+    import mkref as R
+
+    n_side, C = 32, 640
+    m = R.Model(R.SDXL, blocks=1, dim=C, heads=C // 64, head_dim=64, ffn=4 * C, text_dim=SDXL_CTX_DIM, seed=0)
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((n_side * n_side, C)).astype(np.float32)
+    ctx = rng.standard_normal((SDXL_CTX, SDXL_CTX_DIM)).astype(np.float32)
+    flops = sdxl_flops(n_side * n_side, C, 1, B=1)[0] + 2 * 2 * C * SDXL_CTX_DIM * SDXL_CTX  # + the context K / V
+    reps, t_total = 0, 0.0
+    while t_total < seconds_target and reps < 50:
+        t0 = time.perf_counter()
+        m.sdxl_trans(x, ctx)
+        t_total += time.perf_counter() - t0
+        reps += 1
+    rate = flops * reps / t_total
+    return {"value": pass_flops / rate, "unit": "s/pass", "cores": R.lib().mkref_threads(), "kind": "port",
+            "sample": f"oracle (C++/OpenMP, fp32 over bf16 weights): {reps} x one stage-A block of one sample at "
+                      f"{n_side * n_side} tokens ({flops / 1e9:.1f} GFLOP each, {t_total:.1f} s, "
+                      f"{rate / 1e9:.1f} GFLOP/s), scaled by FLOPs to the whole batch-2 pass"}
 
 
 def gemm_traffic():
@@ -95,13 +199,19 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="mmdit-1024-bf16")
+    ap.add_argument("--workload", choices=sorted(WORKLOADS) + ["sdxl-1024-bf16"], default="mmdit-1024-bf16")
     args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.workload == "sdxl-1024-bf16":
+        if args.gpus != 1 or world != 1:
+            print("bench.py measures one GPU: run it with --gpus 1", file=sys.stderr)
+            sys.exit(2)
+        bench_sdxl(args)
+        return
     wl = WORKLOADS[args.workload]
     global H, W, S
     H = W = wl["side"]
     S = wl["text"]
-    world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py measures one GPU: this build runs the step on one MI355X (asked for {max(args.gpus, world)}); "
               f"run it with --gpus 1", file=sys.stderr)
