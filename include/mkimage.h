@@ -64,7 +64,8 @@ mk_status mk_event_elapsed_ms(void* start, void* stop, float* ms);
  * reference's Tensor with dims[0] = in features, qwen_image.cpp:79-111); bf16 = uint16 bit patterns; fp8 = OCP e4m3.
  * ------------------------------------------------------------------------------------------------------------ */
 
-enum mk_dtype { MK_F32 = 0, MK_BF16 = 1, MK_FP8_E4M3 = 2 };
+enum mk_dtype { MK_F32 = 0, MK_BF16 = 1, MK_FP8_E4M3 = 2, MK_F16 = 3, MK_DTYPE_OTHER = 255 /* a file dtype the
+                                                                                          kernels do not take */ };
 
 /* The GEMM's fused epilogue: what happens to acc = A W^T (* wscale[n]) + bias[n]. */
 enum mk_epilogue {
@@ -197,6 +198,43 @@ mk_status mk_quantize_fp8_rows(const void* src, uint64_t rows, uint64_t cols, vo
 mk_status mk_f32_to_bf16(const float* x, size_t n, void* y, void* stream);
 mk_status mk_bf16_to_f32(const void* x, size_t n, float* y, void* stream);
 
+/* LoRA merge into a weight matrix on the device: W[r][c] += factor * sum_j B[r][j] A[j][c] for rows x cols, A fp32
+ * [rank][cols], B fp32 [rows][rank] (rank <= 1024), the sum in fp32 in ascending j, the result rounded to W's dtype:
+ * bf16 (nearest even), or e4m3 with W's per-row scale recomputed from the merged row (max / 448, cols <= 32768), the
+ * rule mk_quantize_fp8_rows applies. The merge of a LoRA added for good (TransformerRuntime::add_lora, called from
+ * src/image/h3_image.cpp:136; targets from QwenImage::lora_target, src/image/qwen_image.cpp:295-331). */
+mk_status mk_lora_merge(void* w, uint32_t w_dtype, float* w_scale, uint64_t rows, uint64_t cols, const float* a,
+                        const float* b, uint32_t rank, float factor, void* stream);
+
+/* ------------------------------------------------------------------------------------------------------------
+ * Checkpoint files: safetensors (the reference's safetensors::Files, tests/safetensors_test.cpp:36-98). Host code
+ * only: no device is needed to open, list or read.
+ * ------------------------------------------------------------------------------------------------------------ */
+
+typedef struct mk_st mk_st;
+#define MK_ST_MAX_DIMS 8
+typedef struct mk_st_tensor {
+    const char* name;         /* valid until mk_st_close */
+    const char* dtype_name;   /* the header's dtype string: "BF16", "F32", "F8_E4M3", ... */
+    uint32_t dtype;           /* mk_dtype (MK_DTYPE_OTHER for the rest) */
+    uint32_t ndim;
+    uint64_t dims[MK_ST_MAX_DIMS]; /* GGUF order: dims[0] is the contiguous axis (the header's shape reversed) */
+    uint32_t file;            /* index of the file that holds it (mk_st_file_path) */
+    uint64_t offset;          /* absolute byte offset of its data in that file */
+    uint64_t bytes;
+} mk_st_tensor;
+
+/* path: one .safetensors file, or a directory whose *.safetensors files (sorted by name) form one checkpoint. The
+ * headers are validated against the files (offsets, sizes, dtypes, duplicate names): MK_ERR_ARG names the problem. */
+mk_status mk_st_open(const char* path, mk_st** out);
+mk_status mk_st_close(mk_st* st);
+mk_status mk_st_count(const mk_st* st, size_t* tensors, uint32_t* files);
+const char* mk_st_file_path(const mk_st* st, uint32_t file); /* NULL when out of range */
+mk_status mk_st_at(const mk_st* st, size_t i, mk_st_tensor* t);          /* in file order, then header order */
+mk_status mk_st_find(const mk_st* st, const char* name, mk_st_tensor* t); /* MK_ERR_ARG when absent */
+/* The tensor's raw bytes; `bytes` must equal its size. */
+mk_status mk_st_read(const mk_st* st, const char* name, void* dst, size_t bytes);
+
 /* ------------------------------------------------------------------------------------------------------------
  * Engine: the denoiser of one model family, weights resident on the device.
  * ------------------------------------------------------------------------------------------------------------ */
@@ -231,6 +269,32 @@ mk_status mk_engine_destroy(mk_engine* e);
  * name + ".scale"). Names are the checkpoint's (Diffusers layout). */
 mk_status mk_engine_load(mk_engine* e, const char* name, const void* data, uint32_t dtype, uint64_t rows,
                          uint64_t cols);
+/* Every weight of the engine from a safetensors checkpoint (file or shard directory; QwenImage::load_transformer,
+ * src/image/qwen_image.cpp:79-111): each tensor by its checkpoint name (Diffusers layout, also found under a
+ * "model.diffusion_model." or "transformer." prefix), streamed from the file through pinned host buffers into its
+ * place in the fused device tensors (upload_rows). Matrices are [out][in] (dims {in, out} in GGUF order), vectors
+ * [n]. Conversions: F32 / F16 / BF16 to what the engine stores (nearest even); into fp8 weights by the per-row rule
+ * of mk_quantize_fp8_rows after rounding to bf16, or F8_E4M3 as stored with its per-row fp32 scale named
+ * name + ".scale". A missing tensor, a wrong shape or a checkpoint with more blocks than the engine is MK_ERR_ARG
+ * (the reference throws); other tensors in the files are ignored. `loaded` (may be NULL): tensors read. */
+mk_status mk_engine_load_safetensors(mk_engine* e, const char* path, uint64_t* loaded);
+/* Merge a LoRA file into the weights for good (the reference's add_lora with merging, engine.hpp:195-197; targets as
+ * QwenImage::lora_target gives them, qwen_image.cpp:295-331: a module's rows inside the fused tensor that holds it).
+ * Pairs <module>.lora_A.weight / .lora_B.weight or .lora_down.weight / .lora_up.weight, with an optional scalar
+ * <module>.alpha: W += scale * (alpha / rank) * B A (alpha absent: scale * B A). Module names are checkpoint names,
+ * optionally prefixed "transformer.", "diffusion_model.", "base_model.model." or written Kohya-style
+ * ("lora_unet_transformer_blocks_0_attn_to_q": '_' and '.' alike). A pair whose shapes do not match its module is
+ * MK_ERR_ARG and nothing is merged; modules that name no weight of the engine (text encoders) are skipped.
+ * `merged` / `skipped` (may be NULL): module counts. */
+mk_status mk_engine_add_lora(mk_engine* e, const char* path, float scale, uint64_t* merged, uint64_t* skipped);
+/* The engine's weights in name order: checkpoint name, stored dtype, rows and cols (vectors: cols = 1). The name
+ * stays valid while the engine lives. */
+mk_status mk_engine_tensor_count(const mk_engine* e, size_t* n);
+mk_status mk_engine_tensor_at(const mk_engine* e, size_t i, const char** name, uint32_t* dtype, uint64_t* rows,
+                              uint64_t* cols);
+/* Copy one named weight back to the host as stored: bytes = rows x cols x element size (name + ".scale": the fp32
+ * per-row scales of an fp8 matrix). */
+mk_status mk_engine_fetch(const mk_engine* e, const char* name, void* data, size_t bytes);
 /* Every weight from the counter RNG on the device: matrices N(0, 0.02), biases N(0, 0.02), norm scales 1 + N(0, 0.02),
  * keyed by (seed, name) exactly as the CPU reference keys them. */
 mk_status mk_engine_init_random(mk_engine* e, uint64_t seed);

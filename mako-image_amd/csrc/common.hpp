@@ -81,11 +81,21 @@ void set_error(const std::string& msg);
 mk_status fail(mk_status s, const std::string& msg);
 mk_status hip_check(hipError_t e, const char* what);
 
+// Chunked read of a safetensors tensor's bytes [off, off + bytes) (safetensors.cpp).
+bool st_read(const mk_st* st, const mk_st_tensor& t, void* dst, uint64_t bytes, uint64_t off);
+
 #define MK_HIP(call)                                                                                               \
     do {                                                                                                           \
         hipError_t e_ = (call);                                                                                    \
         if (e_ != hipSuccess)                                                                                      \
             return ::mk::hip_check(e_, #call);                                                                     \
+    } while (0)
+
+#define MK_TRY(x)                                                                                                  \
+    do {                                                                                                           \
+        mk_status s_ = (x);                                                                                        \
+        if (s_ != MK_OK)                                                                                           \
+            return s_;                                                                                             \
     } while (0)
 
 #define MK_LAUNCH_CHECK(what)                                                                                      \

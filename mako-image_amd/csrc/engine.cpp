@@ -12,6 +12,8 @@
 
 #include <cmath>
 #include <map>
+#include <string>
+#include <unordered_map>
 #include <memory>
 #include <vector>
 
@@ -47,13 +49,6 @@ struct Buf {
     float* f() const { return static_cast<float*>(p); }
     uint16_t* h() const { return static_cast<uint16_t*>(p); }
 };
-
-#define MK_TRY(x)                                                                                                  \
-    do {                                                                                                           \
-        mk_status s_ = (x);                                                                                        \
-        if (s_ != MK_OK)                                                                                           \
-            return s_;                                                                                             \
-    } while (0)
 
 // A linear layer on the device: W [out][in] (bf16 or fp8 with per-row scale), optional bias.
 struct Linear {
@@ -1239,6 +1234,409 @@ mk_status mk_sdxl_forward(mk_engine* e, const float* x, uint32_t batch, uint32_t
     MK_TRY(e->sdxl_forward(x, batch, n, y));
     MK_HIP(hipStreamSynchronize(e->stream));
     MK_TRY(e->finish_timing());
+    return MK_OK;
+}
+
+} // extern "C"
+
+namespace {
+
+float f16_to_f32(uint16_t h)
+{
+    const int e = (h >> 10) & 31, m = h & 1023;
+    const float v = e == 0 ? std::ldexp(float(m), -24)
+                    : e == 31 ? (m ? NAN : INFINITY)
+                              : std::ldexp(float(1024 + m), e - 25);
+    return h & 0x8000 ? -v : v;
+}
+
+const char* dtype_label(uint32_t dt)
+{
+    return dt == MK_F32 ? "F32" : dt == MK_BF16 ? "BF16" : dt == MK_F16 ? "F16" : dt == MK_FP8_E4M3 ? "F8_E4M3" : "?";
+}
+
+// n values of dtype `from` (F32, BF16 or F16) as `to` (F32 or BF16, nearest even).
+void convert_host(const void* src, uint32_t from, void* dst, uint32_t to, size_t n)
+{
+    for (size_t i = 0; i < n; ++i) {
+        const float v = from == MK_F32    ? static_cast<const float*>(src)[i]
+                        : from == MK_BF16 ? bf2f_bits(static_cast<const uint16_t*>(src)[i])
+                                          : f16_to_f32(static_cast<const uint16_t*>(src)[i]);
+        if (to == MK_F32)
+            static_cast<float*>(dst)[i] = v;
+        else
+            static_cast<uint16_t*>(dst)[i] = f2bf_bits(v);
+    }
+}
+
+// Streams tensors from a checkpoint into device memory: file -> pinned host buffer (converted there when the
+// dtypes differ) -> async copy on the engine's stream, two buffers in turn so a read overlaps the previous copy.
+struct Streamer {
+    static constexpr size_t kChunk = size_t(64) << 20;
+    const mk_st* st;
+    hipStream_t stream;
+    void* pin[2] = {};
+    hipEvent_t ev[2] = {};
+    int cur = 0;
+    std::vector<char> raw;
+    Buf stage; // bf16 rows on their way to fp8 quantisation
+
+    ~Streamer()
+    {
+        if (stream)
+            (void)hipStreamSynchronize(stream);
+        for (int i = 0; i < 2; ++i) {
+            if (pin[i])
+                (void)hipHostFree(pin[i]);
+            if (ev[i])
+                (void)hipEventDestroy(ev[i]);
+        }
+    }
+    mk_status init()
+    {
+        for (int i = 0; i < 2; ++i) {
+            MK_HIP(hipHostMalloc(&pin[i], kChunk, hipHostMallocDefault));
+            MK_HIP(hipEventCreateWithFlags(&ev[i], hipEventDisableTiming));
+        }
+        return MK_OK;
+    }
+    // The tensor's elements as dtype `to` at device address d.
+    mk_status upload(const mk_st_tensor& t, void* d, uint32_t to)
+    {
+        const size_t es_in = mk_engine::esize(t.dtype == MK_F16 ? MK_BF16 : t.dtype), es_out = mk_engine::esize(to);
+        const uint64_t n = t.bytes / es_in;
+        const uint64_t per = kChunk / std::max(es_in, es_out);
+        for (uint64_t i = 0; i < n; i += per) {
+            const uint64_t m = std::min<uint64_t>(per, n - i);
+            MK_HIP(hipEventSynchronize(ev[cur]));
+            if (t.dtype == to) {
+                if (!st_read(st, t, pin[cur], m * es_in, i * es_in))
+                    return fail(MK_ERR_ARG, std::string("safetensors: cannot read ") + t.name);
+            } else {
+                raw.resize(m * es_in);
+                if (!st_read(st, t, raw.data(), m * es_in, i * es_in))
+                    return fail(MK_ERR_ARG, std::string("safetensors: cannot read ") + t.name);
+                convert_host(raw.data(), t.dtype, pin[cur], to, m);
+            }
+            MK_HIP(hipMemcpyAsync(static_cast<char*>(d) + i * es_out, pin[cur], m * es_out, hipMemcpyHostToDevice,
+                                  stream));
+            MK_HIP(hipEventRecord(ev[cur], stream));
+            cur ^= 1;
+        }
+        return MK_OK;
+    }
+    // A small tensor (<= 1024 values) read and converted to fp32 on the host.
+    mk_status host_f32(const mk_st_tensor& t, std::vector<float>& out)
+    {
+        const size_t es = mk_engine::esize(t.dtype == MK_F16 ? MK_BF16 : t.dtype);
+        const size_t n = t.bytes / es;
+        raw.resize(t.bytes);
+        if (!st_read(st, t, raw.data(), t.bytes, 0))
+            return fail(MK_ERR_ARG, std::string("safetensors: cannot read ") + t.name);
+        out.resize(n);
+        convert_host(raw.data(), t.dtype, out.data(), MK_F32, n);
+        return MK_OK;
+    }
+};
+
+uint64_t numel(const mk_st_tensor& t)
+{
+    uint64_t n = 1;
+    for (uint32_t i = 0; i < t.ndim; ++i)
+        n *= t.dims[i];
+    return n;
+}
+
+bool float_dtype(uint32_t dt) { return dt == MK_F32 || dt == MK_BF16 || dt == MK_F16; }
+
+// Checkpoint name under the prefixes single-file checkpoints use.
+const char* const kPrefixes[] = {"", "model.diffusion_model.", "transformer."};
+
+bool find_prefixed(const mk_st* st, const std::string& name, mk_st_tensor* t)
+{
+    for (const char* p : kPrefixes) {
+        const std::string n = p + name;
+        if (mk_st_find(st, n.c_str(), t) == MK_OK)
+            return true;
+    }
+    set_error("");
+    return false;
+}
+
+struct StClose {
+    void operator()(mk_st* s) const { mk_st_close(s); }
+};
+
+} // namespace
+
+extern "C" {
+
+mk_status mk_engine_load_safetensors(mk_engine* e, const char* path, uint64_t* loaded)
+{
+    if (!e || !path)
+        return fail(MK_ERR_ARG, "engine_load_safetensors: null");
+    mk_st* raw_st = nullptr;
+    MK_TRY(mk_st_open(path, &raw_st));
+    std::unique_ptr<mk_st, StClose> st(raw_st);
+    // a checkpoint with more blocks than the engine was made for
+    size_t count = 0;
+    MK_TRY(mk_st_count(st.get(), &count, nullptr));
+    for (size_t i = 0; i < count; ++i) {
+        mk_st_tensor t;
+        MK_TRY(mk_st_at(st.get(), i, &t));
+        std::string n = t.name;
+        for (const char* p : kPrefixes)
+            if (*p && n.rfind(p, 0) == 0)
+                n = n.substr(strlen(p));
+        static const std::string blk = "transformer_blocks.";
+        if (n.rfind(blk, 0) == 0) {
+            const unsigned long b = strtoul(n.c_str() + blk.size(), nullptr, 10);
+            if (b >= e->cfg.blocks)
+                return fail(MK_ERR_ARG, "load_safetensors: the checkpoint has " + std::string(t.name) +
+                                            " but the engine has " + std::to_string(e->cfg.blocks) + " blocks");
+        }
+    }
+    // every tensor the engine holds must be there, with its shape and a usable dtype: checked before any upload
+    struct Job {
+        const Dest* d;
+        mk_st_tensor t, scale;
+        bool has_scale = false;
+    };
+    std::vector<Job> jobs;
+    for (const auto& [name, d] : e->dests) {
+        Job j{&d, {}, {}};
+        if (!find_prefixed(st.get(), name, &j.t))
+            return fail(MK_ERR_ARG, "load_safetensors: the checkpoint has no tensor " + name);
+        const mk_st_tensor& t = j.t;
+        const bool matrix = d.cols > 1;
+        const bool shape_ok = matrix ? t.ndim == 2 && t.dims[0] == d.cols && t.dims[1] == d.rows
+                                     : t.ndim <= 2 && numel(t) == d.rows;
+        if (!shape_ok) {
+            std::string dims;
+            for (uint32_t k = 0; k < t.ndim; ++k)
+                dims += (k ? ", " : "") + std::to_string(t.dims[k]);
+            return fail(MK_ERR_ARG, "load_safetensors: " + name + " has dims {" + dims + "}, the engine needs " +
+                                        (matrix ? "{" + std::to_string(d.cols) + ", " + std::to_string(d.rows) + "}"
+                                                : "{" + std::to_string(d.rows) + "}"));
+        }
+        if (t.dtype == MK_FP8_E4M3) {
+            if (d.dtype != MK_FP8_E4M3)
+                return fail(MK_ERR_ARG, "load_safetensors: " + name + " is F8_E4M3 but the engine stores it as " +
+                                            dtype_label(d.dtype));
+            if (!find_prefixed(st.get(), name + ".scale", &j.scale) || numel(j.scale) != d.rows ||
+                !float_dtype(j.scale.dtype))
+                return fail(MK_ERR_ARG, "load_safetensors: F8_E4M3 " + name + " needs its per-row scale " + name +
+                                            ".scale (" + std::to_string(d.rows) + " values)");
+            j.has_scale = true;
+        } else if (!float_dtype(t.dtype)) {
+            return fail(MK_ERR_ARG, "load_safetensors: " + name + " has dtype " + t.dtype_name);
+        }
+        jobs.push_back(j);
+    }
+    Streamer s{st.get(), e->stream};
+    MK_TRY(s.init());
+    for (const Job& j : jobs) {
+        const Dest& d = *j.d;
+        if (d.dtype != MK_FP8_E4M3) {
+            MK_TRY(s.upload(j.t, d.p, d.dtype));
+        } else if (j.has_scale) {
+            MK_TRY(s.upload(j.t, d.p, MK_FP8_E4M3));
+            MK_TRY(s.upload(j.scale, d.scale, MK_F32));
+        } else {
+            if (d.rows * d.cols * 2 > s.stage.bytes)
+                MK_HIP(hipStreamSynchronize(e->stream)); // the previous quantisation may still read the stage
+            MK_TRY(s.stage.ensure(d.rows * d.cols * 2));
+            MK_TRY(s.upload(j.t, s.stage.p, MK_BF16));
+            MK_TRY(mk_quantize_fp8_rows(s.stage.p, d.rows, d.cols, d.p, d.scale, e->stream));
+        }
+    }
+    MK_HIP(hipStreamSynchronize(e->stream));
+    if (loaded)
+        *loaded = jobs.size();
+    return MK_OK;
+}
+
+mk_status mk_engine_add_lora(mk_engine* e, const char* path, float scale, uint64_t* merged, uint64_t* skipped)
+{
+    if (!e || !path)
+        return fail(MK_ERR_ARG, "engine_add_lora: null");
+    mk_st* raw_st = nullptr;
+    MK_TRY(mk_st_open(path, &raw_st));
+    std::unique_ptr<mk_st, StClose> st(raw_st);
+    size_t count = 0;
+    MK_TRY(mk_st_count(st.get(), &count, nullptr));
+    // modules and their down (A) / up (B) / alpha tensors
+    struct Mod {
+        int a = -1, b = -1, alpha = -1;
+        bool other = false;
+    };
+    std::map<std::string, Mod> mods;
+    static const struct {
+        const char* suffix;
+        int part; // 0 A, 1 B, 2 alpha
+    } kParts[] = {{".lora_A.weight", 0},        {".lora_B.weight", 1},         {".lora_A.default.weight", 0},
+                  {".lora_B.default.weight", 1}, {".lora_down.weight", 0},      {".lora_up.weight", 1},
+                  {".alpha", 2}};
+    std::vector<mk_st_tensor> ts(count);
+    for (size_t i = 0; i < count; ++i) {
+        MK_TRY(mk_st_at(st.get(), i, &ts[i]));
+        const std::string n = ts[i].name;
+        bool hit = false;
+        for (const auto& p : kParts) {
+            const size_t L = strlen(p.suffix);
+            if (n.size() > L && n.compare(n.size() - L, L, p.suffix) == 0) {
+                Mod& m = mods[n.substr(0, n.size() - L)];
+                (p.part == 0 ? m.a : p.part == 1 ? m.b : m.alpha) = int(i);
+                hit = true;
+                break;
+            }
+        }
+        if (!hit) {
+            const size_t dot = n.rfind('.');
+            mods[dot == std::string::npos ? n : n.substr(0, dot)].other = true;
+        }
+    }
+    // '_' and '.' alike: engine module names with dots turned to underscores
+    std::unordered_map<std::string, std::string> flat;
+    for (const auto& [name, d] : e->dests)
+        if (d.cols > 1 && name.size() > 7 && name.compare(name.size() - 7, 7, ".weight") == 0) {
+            std::string m = name.substr(0, name.size() - 7);
+            std::string f = m;
+            for (char& c : f)
+                if (c == '.')
+                    c = '_';
+            flat[f] = m;
+        }
+    struct Merge {
+        std::string module;
+        Dest d;
+        const mk_st_tensor *a, *b;
+        uint32_t rank;
+        float factor;
+    };
+    std::vector<Merge> plan;
+    uint64_t n_skipped = 0;
+    Streamer s{st.get(), e->stream};
+    for (const auto& [module, m] : mods) {
+        std::string mod = module;
+        for (const char* p : {"base_model.model.", "model.diffusion_model.", "diffusion_model.", "transformer.",
+                              "lora_unet_", "lora_transformer_"})
+            if (mod.rfind(p, 0) == 0)
+                mod = mod.substr(strlen(p));
+        if (m.a < 0 && m.b < 0) {
+            ++n_skipped; // no LoRA pair here (a full-weight diff, a DoRA scale, ...)
+            continue;
+        }
+        if (m.a < 0 || m.b < 0)
+            return fail(MK_ERR_ARG, "add_lora: " + module + " has only one of its down / up matrices");
+        // the target: the module's rows in the fused tensor (QwenImage::lora_target); Q21's fused gate_up spans
+        // the gate rows and the up rows that follow them
+        Dest d{};
+        bool found = false;
+        auto it = e->dests.find(mod + ".weight");
+        if (it == e->dests.end()) {
+            auto f = flat.find(mod);
+            if (f != flat.end())
+                it = e->dests.find(f->second + ".weight");
+        }
+        if (it != e->dests.end() && it->second.cols > 1) {
+            d = it->second;
+            found = true;
+        } else if (e->cfg.family == MK_FAMILY_Q21 && mod.size() > 16 &&
+                   mod.compare(mod.size() - 16, 16, ".img_mlp.gate_up") == 0) {
+            auto g = e->dests.find(mod.substr(0, mod.size() - 7) + "gate_layer.weight");
+            if (g != e->dests.end()) {
+                d = g->second;
+                d.rows *= 2;
+                found = true;
+            }
+        }
+        if (!found) {
+            ++n_skipped;
+            continue;
+        }
+        const mk_st_tensor& A = ts[size_t(m.a)];
+        const mk_st_tensor& B = ts[size_t(m.b)];
+        if (A.ndim != 2 || B.ndim != 2 || !float_dtype(A.dtype) || !float_dtype(B.dtype))
+            return fail(MK_ERR_ARG, "add_lora: " + module + ": down / up must be 2-d F32, BF16 or F16 matrices");
+        const uint64_t r = A.dims[1];
+        if (A.dims[0] != d.cols || B.dims[1] != d.rows || B.dims[0] != r || r == 0 || r > 1024)
+            return fail(MK_ERR_ARG, "add_lora: " + module + ": down {" + std::to_string(A.dims[0]) + ", " +
+                                        std::to_string(A.dims[1]) + "}, up {" + std::to_string(B.dims[0]) + ", " +
+                                        std::to_string(B.dims[1]) + "} do not fit a " + std::to_string(d.rows) +
+                                        " x " + std::to_string(d.cols) + " weight at rank <= 1024");
+        float factor = scale;
+        if (m.alpha >= 0) {
+            const mk_st_tensor& al = ts[size_t(m.alpha)];
+            std::vector<float> v;
+            if (numel(al) != 1 || !float_dtype(al.dtype))
+                return fail(MK_ERR_ARG, "add_lora: " + module + ".alpha must be one F32, BF16 or F16 value");
+            MK_TRY(s.host_f32(al, v));
+            factor = scale * v[0] / float(r);
+        }
+        plan.push_back({module, d, &A, &B, uint32_t(r), factor});
+    }
+    if (!plan.empty()) {
+        MK_TRY(s.init());
+        Buf ab; // one module's A then B, fp32; the merge of a module finishes before the next one's upload
+        for (const Merge& p : plan) {
+            const size_t na = size_t(p.rank) * p.d.cols, nb = size_t(p.d.rows) * p.rank;
+            if ((na + nb) * 4 > ab.bytes)
+                MK_HIP(hipStreamSynchronize(e->stream)); // the previous merge may still read the buffer
+            MK_TRY(ab.ensure((na + nb) * 4));
+            MK_TRY(s.upload(*p.a, ab.f(), MK_F32));
+            MK_TRY(s.upload(*p.b, ab.f() + na, MK_F32));
+            MK_TRY(mk_lora_merge(p.d.p, p.d.dtype, p.d.scale, p.d.rows, p.d.cols, ab.f(), ab.f() + na, p.rank,
+                                 p.factor, e->stream));
+        }
+        MK_HIP(hipStreamSynchronize(e->stream));
+    }
+    if (merged)
+        *merged = plan.size();
+    if (skipped)
+        *skipped = n_skipped;
+    return MK_OK;
+}
+
+mk_status mk_engine_tensor_count(const mk_engine* e, size_t* n)
+{
+    if (!e || !n)
+        return fail(MK_ERR_ARG, "engine_tensor_count: null");
+    *n = e->dests.size();
+    return MK_OK;
+}
+
+mk_status mk_engine_tensor_at(const mk_engine* e, size_t i, const char** name, uint32_t* dtype, uint64_t* rows,
+                              uint64_t* cols)
+{
+    if (!e || !name || !dtype || !rows || !cols)
+        return fail(MK_ERR_ARG, "engine_tensor_at: null");
+    if (i >= e->dests.size())
+        return fail(MK_ERR_ARG, "engine_tensor_at: index " + std::to_string(i) + " of " +
+                                    std::to_string(e->dests.size()));
+    auto it = std::next(e->dests.begin(), std::ptrdiff_t(i));
+    *name = it->first.c_str();
+    *dtype = it->second.dtype;
+    *rows = it->second.rows;
+    *cols = it->second.cols;
+    return MK_OK;
+}
+
+mk_status mk_engine_fetch(const mk_engine* e, const char* name, void* data, size_t bytes)
+{
+    if (!e || !name || !data)
+        return fail(MK_ERR_ARG, "engine_fetch: null");
+    std::string n(name);
+    const bool is_scale = n.size() > 6 && n.compare(n.size() - 6, 6, ".scale") == 0;
+    auto it = e->dests.find(is_scale ? n.substr(0, n.size() - 6) : n);
+    if (it == e->dests.end() || (is_scale && it->second.dtype != MK_FP8_E4M3))
+        return fail(MK_ERR_ARG, "engine_fetch: no tensor named " + n);
+    const Dest& d = it->second;
+    const size_t want = is_scale ? d.rows * 4 : d.rows * d.cols * mk_engine::esize(d.dtype);
+    if (bytes != want)
+        return fail(MK_ERR_ARG, "engine_fetch: " + n + " holds " + std::to_string(want) + " bytes");
+    MK_HIP(hipStreamSynchronize(e->stream));
+    MK_HIP(hipMemcpy(data, is_scale ? static_cast<const void*>(d.scale) : d.p, want, hipMemcpyDeviceToHost));
     return MK_OK;
 }
 

@@ -586,6 +586,82 @@ __global__ __launch_bounds__(256) void quant_fp8_kernel(const uint16_t* __restri
         dst[r * cols + c] = e4m3_encode(bf2f_bits(s[c]) / sc);
 }
 
+// e4m3 code -> float: 2^(e-7) (1 + m/8) for e > 0, m 2^-9 for the subnormals (no code above 0x7e is ever written).
+__device__ inline float e4m3_decode(uint8_t v)
+{
+    const int e = (v >> 3) & 15, m = v & 7;
+    const float a = e ? ldexpf(float(8 + m), e - 10) : ldexpf(float(m), -9);
+    return v & 0x80 ? -a : a;
+}
+
+// LoRA merge into bf16 rows: RB rows a block share each A value they load; B's RB rows sit in LDS.
+template <int RB>
+__global__ __launch_bounds__(256) void lora_bf16_kernel(uint16_t* __restrict__ w, uint64_t rows, uint64_t cols,
+                                                        const float* __restrict__ a, const float* __restrict__ b,
+                                                        uint32_t rank, float factor)
+{
+    extern __shared__ float bs[]; // [RB][rank]
+    const uint64_t r0 = uint64_t(blockIdx.x) * RB;
+    for (uint32_t i = threadIdx.x; i < RB * rank; i += 256) {
+        const uint64_t r = r0 + i / rank;
+        bs[i] = r < rows ? b[r * rank + i % rank] : 0.0f;
+    }
+    __syncthreads();
+    const uint64_t c = uint64_t(blockIdx.y) * 256 + threadIdx.x;
+    if (c >= cols)
+        return;
+    float acc[RB];
+    for (int t = 0; t < RB; ++t)
+        acc[t] = 0.0f;
+    for (uint32_t j = 0; j < rank; ++j) {
+        const float av = a[uint64_t(j) * cols + c];
+        for (int t = 0; t < RB; ++t)
+            acc[t] = fmaf(bs[t * rank + j], av, acc[t]);
+    }
+    for (int t = 0; t < RB; ++t)
+        if (r0 + t < rows) {
+            uint16_t* x = w + (r0 + t) * cols + c;
+            *x = f2bf_bits(bf2f_bits(*x) + factor * acc[t]);
+        }
+}
+
+// LoRA merge into e4m3 rows, one row a block: the merged row's max |w| gives the new scale (max / 448, 1 for a zero
+// row), then the codes. Both passes compute each merged value by the same operations, so they agree bit for bit.
+__global__ __launch_bounds__(256) void lora_fp8_kernel(uint8_t* __restrict__ w, float* __restrict__ scale,
+                                                       uint64_t cols, const float* __restrict__ a,
+                                                       const float* __restrict__ b, uint32_t rank, float factor)
+{
+    extern __shared__ float bs[]; // [rank]
+    __shared__ float red[4];
+    const uint64_t r = blockIdx.x;
+    for (uint32_t i = threadIdx.x; i < rank; i += 256)
+        bs[i] = b[r * rank + i];
+    const float sc0 = scale[r];
+    __syncthreads();
+    auto merged = [&](uint64_t c) {
+        float acc = 0.0f;
+        for (uint32_t j = 0; j < rank; ++j)
+            acc = fmaf(bs[j], a[uint64_t(j) * cols + c], acc);
+        return e4m3_decode(w[r * cols + c]) * sc0 + factor * acc;
+    };
+    float mx = 0.0f;
+    for (uint64_t c = threadIdx.x; c < cols; c += 256)
+        mx = fmaxf(mx, fabsf(merged(c)));
+    mx = wave_max(mx);
+    if ((threadIdx.x & 63) == 0)
+        red[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const float sc = mx > 0.0f ? mx / 448.0f : 1.0f;
+    // each thread rewrites only the columns it read in the first pass
+    for (uint64_t c = threadIdx.x; c < cols; c += 256) {
+        const float v = merged(c);
+        w[r * cols + c] = e4m3_encode(v / sc);
+    }
+    if (threadIdx.x == 0)
+        scale[r] = sc;
+}
+
 inline uint32_t grid_for(uint64_t n)
 {
     const uint64_t b = (n + 255) / 256;
@@ -868,6 +944,34 @@ mk_status mk_quantize_fp8_rows(const void* src, uint64_t rows, uint64_t cols, vo
     quant_fp8_kernel<<<uint32_t(rows), 256, 0, S(stream)>>>(static_cast<const uint16_t*>(src), cols,
                                                             static_cast<uint8_t*>(dst), scale);
     MK_LAUNCH_CHECK("quantize_fp8_rows");
+    return MK_OK;
+}
+
+mk_status mk_lora_merge(void* w, uint32_t w_dtype, float* w_scale, uint64_t rows, uint64_t cols, const float* a,
+                        const float* b, uint32_t rank, float factor, void* stream)
+{
+    if (!w || !a || !b || (w_dtype == MK_FP8_E4M3 && !w_scale))
+        return fail(MK_ERR_ARG, "lora_merge: null pointer");
+    if (w_dtype != MK_BF16 && w_dtype != MK_FP8_E4M3)
+        return fail(MK_ERR_ARG, "lora_merge: weights bf16 or fp8-e4m3");
+    if (!rank || rank > 1024)
+        return fail(MK_ERR_ARG, "lora_merge: rank " + std::to_string(rank) + " not in 1..1024");
+    if (!rows || !cols)
+        return MK_OK;
+    if (w_dtype == MK_BF16) {
+        constexpr int RB = 8;
+        const uint64_t gx = (rows + RB - 1) / RB, gy = (cols + 255) / 256;
+        if (gx > 0x7fffffffu || gy > 65535)
+            return fail(MK_ERR_ARG, "lora_merge: matrix too large");
+        lora_bf16_kernel<RB><<<dim3(uint32_t(gx), uint32_t(gy)), 256, RB * rank * 4, S(stream)>>>(
+            static_cast<uint16_t*>(w), rows, cols, a, b, rank, factor);
+    } else {
+        if (rows > 0x7fffffffu)
+            return fail(MK_ERR_ARG, "lora_merge: too many rows");
+        lora_fp8_kernel<<<uint32_t(rows), 256, rank * 4, S(stream)>>>(static_cast<uint8_t*>(w), w_scale, cols, a, b,
+                                                                       rank, factor);
+    }
+    MK_LAUNCH_CHECK("lora_merge");
     return MK_OK;
 }
 

@@ -13,7 +13,7 @@ import numpy as np
 HERE = pathlib.Path(__file__).resolve().parent
 LIB_PATH = HERE / "libmkimage.so"
 
-F32, BF16, FP8 = 0, 1, 2
+F32, BF16, FP8, F16, DTYPE_OTHER = 0, 1, 2, 3, 255
 EPI_STORE, EPI_GELU_TANH, EPI_GATE_ADD, EPI_GATE_TANH, EPI_SILU, EPI_ADD, EPI_HEADS = range(7)
 FAMILY_DUAL, FAMILY_Q21, FAMILY_SDXL = 0, 1, 2
 
@@ -47,6 +47,11 @@ class Config(C.Structure):
 class Schedule(C.Structure):
     _fields_ = [("base_seq", _d), ("max_seq", _d), ("base_shift", _d), ("max_shift", _d), ("terminal", _d),
                 ("has_mu", _i), ("mu", _d)]
+
+
+class StTensor(C.Structure):
+    _fields_ = [("name", C.c_char_p), ("dtype_name", C.c_char_p), ("dtype", _u32), ("ndim", _u32),
+                ("dims", _u64 * 8), ("file", _u32), ("offset", _u64), ("bytes", _u64)]
 
 
 PROBE = C.CFUNCTYPE(None, _vp, C.c_char_p, _i, _fp, _sz)
@@ -109,6 +114,20 @@ _SIGS = {
     "mk_engine_set_timing": (_i, [_vp, _i]),
     "mk_engine_timing": (_i, [_vp, _u32, C.POINTER(C.c_char_p), C.POINTER(_f), C.POINTER(_u32), C.POINTER(_d)]),
     "mk_sdxl_forward": (_i, [_vp, _vp, _u32, _u32, _vp, _vp]),
+    "mk_lora_merge": (_i, [_vp, _u32, _vp, _u64, _u64, _vp, _vp, _u32, _f, _vp]),
+    "mk_st_open": (_i, [C.c_char_p, C.POINTER(_vp)]),
+    "mk_st_close": (_i, [_vp]),
+    "mk_st_count": (_i, [_vp, C.POINTER(_sz), C.POINTER(_u32)]),
+    "mk_st_file_path": (C.c_char_p, [_vp, _u32]),
+    "mk_st_at": (_i, [_vp, _sz, C.POINTER(StTensor)]),
+    "mk_st_find": (_i, [_vp, C.c_char_p, C.POINTER(StTensor)]),
+    "mk_st_read": (_i, [_vp, C.c_char_p, _vp, _sz]),
+    "mk_engine_load_safetensors": (_i, [_vp, C.c_char_p, C.POINTER(_u64)]),
+    "mk_engine_add_lora": (_i, [_vp, C.c_char_p, _f, C.POINTER(_u64), C.POINTER(_u64)]),
+    "mk_engine_tensor_count": (_i, [_vp, C.POINTER(_sz)]),
+    "mk_engine_tensor_at": (_i, [_vp, _sz, C.POINTER(C.c_char_p), C.POINTER(_u32), C.POINTER(_u64),
+                                 C.POINTER(_u64)]),
+    "mk_engine_fetch": (_i, [_vp, C.c_char_p, _vp, _sz]),
 }
 
 EXPORTS = tuple(_SIGS)
@@ -242,6 +261,58 @@ def bf16_to_f32(b):
     return (np.asarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
 
 
+class SafeTensors:
+    """A safetensors file or shard directory through the library's reader (host only, no device needed)."""
+
+    def __init__(self, path):
+        p = _vp()
+        call("mk_st_open", str(path).encode(), C.byref(p))
+        self.h = p.value
+
+    def close(self):
+        if getattr(self, "h", None) and _lib is not None:
+            _lib.mk_st_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def __len__(self):
+        n = _sz()
+        call("mk_st_count", self.h, C.byref(n), None)
+        return n.value
+
+    def files(self):
+        f = _u32()
+        call("mk_st_count", self.h, None, C.byref(f))
+        return [lib().mk_st_file_path(self.h, i).decode() for i in range(f.value)]
+
+    @staticmethod
+    def _info(t):
+        return {"name": t.name.decode(), "dtype": t.dtype, "dtype_name": t.dtype_name.decode(),
+                "dims": [t.dims[i] for i in range(t.ndim)], "file": t.file, "offset": t.offset, "bytes": t.bytes}
+
+    def tensors(self):
+        out = []
+        for i in range(len(self)):
+            t = StTensor()
+            call("mk_st_at", self.h, i, C.byref(t))
+            out.append(self._info(t))
+        return out
+
+    def find(self, name):
+        t = StTensor()
+        call("mk_st_find", self.h, name.encode(), C.byref(t))
+        return self._info(t)
+
+    def read(self, name):
+        """The tensor's raw bytes."""
+        info = self.find(name)
+        buf = np.empty(info["bytes"], dtype=np.uint8)
+        call("mk_st_read", self.h, name.encode(), buf.ctypes.data, buf.nbytes)
+        return buf
+
+
 class Engine:
     def __init__(self, family, blocks, dim, heads, head_dim, ffn, text_dim, latent=64, weight_dtype=BF16,
                  max_batch=2):
@@ -267,6 +338,38 @@ class Engine:
 
     def init_random(self, seed):
         call("mk_engine_init_random", self.h, seed)
+
+    def load_safetensors(self, path):
+        """Every weight from a safetensors file or shard directory; returns the number of tensors read."""
+        n = _u64()
+        call("mk_engine_load_safetensors", self.h, str(path).encode(), C.byref(n))
+        return n.value
+
+    def add_lora(self, path, scale=1.0):
+        """Merges a LoRA file into the weights; returns (modules merged, modules skipped)."""
+        m, k = _u64(), _u64()
+        call("mk_engine_add_lora", self.h, str(path).encode(), scale, C.byref(m), C.byref(k))
+        return m.value, k.value
+
+    def tensors(self):
+        """[(name, dtype, rows, cols)] of the engine's weights."""
+        n = _sz()
+        call("mk_engine_tensor_count", self.h, C.byref(n))
+        out = []
+        for i in range(n.value):
+            name, dt, r, c = C.c_char_p(), _u32(), _u64(), _u64()
+            call("mk_engine_tensor_at", self.h, i, C.byref(name), C.byref(dt), C.byref(r), C.byref(c))
+            out.append((name.value.decode(), dt.value, r.value, c.value))
+        return out
+
+    def fetch(self, name, dtype, rows, cols):
+        """A weight as stored (float32, bf16 bits as uint16, e4m3 codes as uint8); name + ".scale": fp32 scales."""
+        if name.endswith(".scale"):
+            a = np.empty(rows, dtype=np.float32)
+        else:
+            a = np.empty((rows, cols) if cols > 1 else rows, dtype=_NP[dtype])
+        call("mk_engine_fetch", self.h, name.encode(), a.ctypes.data, a.nbytes)
+        return a
 
     def weight_bytes(self):
         b = _u64()
