@@ -123,6 +123,28 @@ mk_status mk_gemm(const mk_gemm_args* a, void* stream);
  * graph has one stream). */
 mk_status mk_gemm_grouped(const mk_gemm_args* a, uint32_t count, void* stream);
 
+/* 3x3 convolution, stride 1, zero padding 1 (the VAE decoder's conv, src/image/engine.cpp:732-746, 907-947), as one
+ * GEMM over the padded pixel grid (implicit im2col on MFMA). Layout "padded grid": an h x w image is stored as the
+ * (h + 2) x (w + 2) grid with a zero ring, preceded and followed by w + 3 zero rows: row S + (y + 1)(w + 2) + x + 1
+ * holds pixel (y, x), S = w + 3, each row c channels.
+ *   x: bf16 padded grid, c channels (ring and slack rows zero);
+ *   w: bf16 [n][9][c], tap = 3 dy + dx (the PyTorch weight [n][c][3][3] with its taps moved in front of c);
+ *   y: (h + 2)(w + 2) rows of ldy values from its first grid row (a padded-grid buffer + S rows): every grid row is
+ *      written (ring rows hold values the next layer must not read as pixels);
+ *   epilogue MK_EPI_STORE (y = acc + bias, fp32 or bf16) or MK_EPI_ADD (y += acc + bias, fp32).
+ * c and n are multiples of 64 (c <= 4096); pad channels with zeros. */
+typedef struct mk_conv_args {
+    const void* x;
+    const void* w;
+    const float* bias; /* [n] or NULL */
+    void* y;
+    uint32_t h, width, c, n;
+    int64_t ldy;
+    uint32_t y_dtype;
+    uint32_t epilogue;
+} mk_conv_args;
+mk_status mk_conv3x3(const mk_conv_args* a, void* stream);
+
 /* GEMV for a few rows (the time embedding and modulation projections, rows <= 4):
  * y[r][n] = sum_k W[n][k] bf16(x'[r][k]) + b[n] with x' = silu(x) when silu_x (silu(temb) is the modulation
  * layers' input), else x; x fp32 [rows][K], W bf16 [N][K], y fp32. The activation is rounded to bf16 as every GEMM's
@@ -205,6 +227,36 @@ mk_status mk_bf16_to_f32(const void* x, size_t n, float* y, void* stream);
  * src/image/h3_image.cpp:136; targets from QwenImage::lora_target, src/image/qwen_image.cpp:295-331). */
 mk_status mk_lora_merge(void* w, uint32_t w_dtype, float* w_scale, uint64_t rows, uint64_t cols, const float* a,
                         const float* b, uint32_t rank, float factor, void* stream);
+
+/* ------------------------------------------------------------------------------------------------------------
+ * VAE decoder: the step after the loop (Engine::decode, src/image/engine.cpp:862-954; weights as load_vae reads
+ * them, :589-628): Qwen-Image's Wan-2.1-layout decoder for one frame. Channels base x {4, 4, 4, 2, 1} per level
+ * (base 96 for Qwen-Image), z latent channels (16), tokens [h][w][4 z] (a 2x2 patch each) -> RGBA [16 h][16 w][4]
+ * fp32 in [-1, 1] with alpha 1. Every 3x3 conv is an mk_conv3x3 launch; the mid block's one-head attention runs as
+ * GEMMs and a row softmax.
+ * ------------------------------------------------------------------------------------------------------------ */
+typedef struct mk_vae mk_vae;
+typedef struct mk_vae_config {
+    uint32_t base;      /* 96 */
+    uint32_t z;         /* 16 */
+    const float* mean;  /* [z]: latents_mean of the VAE's config (copied) */
+    const float* std;   /* [z]: latents_std */
+} mk_vae_config;
+mk_status mk_vae_create(const mk_vae_config* cfg, mk_vae** out);
+mk_status mk_vae_destroy(mk_vae* v);
+/* Weights by checkpoint name (Diffusers AutoencoderKLQwenImage layout: "decoder.up_blocks.0.resnets.0.conv1.weight",
+ * "decoder.mid_block.attentions.0.to_qkv.weight", ...), fp32 in PyTorch layout: conv weights [out][in][k][k], or the
+ * causal 3-D form [out][in][kt][k][k] of which the last time tap is used (a single frame sees only it); vectors
+ * [n] (or [n, 1, 1 ...]). */
+mk_status mk_vae_load(mk_vae* v, const char* name, const float* data, const int64_t* dims, uint32_t ndim);
+mk_status mk_vae_load_safetensors(mk_vae* v, const char* path, uint64_t* loaded);
+/* Counter-RNG weights keyed by (seed, name): convs N(0, 1 / fan_in) as bf16, biases N(0, 0.02), gammas 1 + N(0, 0.1). */
+mk_status mk_vae_init_random(mk_vae* v, uint64_t seed);
+/* tokens [h * w][4 z] host fp32 (n values) -> rgba [16 h][16 w][4] host fp32 */
+mk_status mk_vae_decode(mk_vae* v, const float* tokens, size_t n, uint32_t h, uint32_t w, float* rgba);
+/* the same on device buffers, queued on the VAE's stream (mk_vae_stream) */
+mk_status mk_vae_decode_device(mk_vae* v, const float* tokens, uint32_t h, uint32_t w, float* rgba);
+mk_status mk_vae_stream(mk_vae* v, void** stream);
 
 /* ------------------------------------------------------------------------------------------------------------
  * Checkpoint files: safetensors (the reference's safetensors::Files, tests/safetensors_test.cpp:36-98). Host code
@@ -339,6 +391,8 @@ mk_status mk_generate(mk_engine* e, const float* noise, size_t n, const float* s
  * (-1 none), the data copied to host fp32 and its length. NULL turns it off. Slows the step (synchronises). */
 typedef void (*mk_probe_fn)(void* user, const char* name, int layer, const float* data, size_t n);
 mk_status mk_engine_set_probe(mk_engine* e, mk_probe_fn fn, void* user);
+/* VAE probes: "vae_conv_in", "vae_mid", "vae_up" (layer = up block), "vae_out" (before the clamp), [pixels][channels] */
+mk_status mk_vae_set_probe(mk_vae* v, mk_probe_fn fn, void* user);
 
 /* Per-kernel timing of the last step with events on the step's stream (enable before the step): names and total
  * milliseconds per kernel class ("gemm", "attention", ...). */

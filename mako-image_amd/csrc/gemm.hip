@@ -42,6 +42,9 @@ struct GemmP {
     uint32_t epi, c_bf16;
     uint32_t tiles_m, tiles_n, batch;
     HeadsP hp;
+    // 3 x 3 convolution (EK_CONV): the padded grid's row width w + 2, k tiles a tap (channels / 64), and
+    // ceil(2^16 / conv_tpt) for the tap index by multiply-shift
+    uint32_t conv_pw, conv_tpt, conv_inv;
 };
 
 // One launch of up to two GEMMs of equal N, K and epilogue kind (the dual-stream blocks' image and text
@@ -80,6 +83,8 @@ __device__ inline void f8x16_to_bf16(const u32x4& v, u32x4& lo, u32x4& hi)
 
 // Epilogue kinds (template): a plain store, an activation, a read-modify-write of the fp32 residual, the q/k/v heads.
 enum { EK_STORE = 0, EK_ACT = 1, EK_RMW = 2, EK_HEADS = 3 };
+// Flag on the epilogue kind: the A operand is a 3 x 3 convolution's input (implicit im2col, see conv_koff).
+constexpr int EK_CONV = 8;
 
 // Per-tile channel constants of a lane's 4 channels (the same for every token row it writes).
 struct EpiCh {
@@ -409,6 +414,9 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
                                           uint16_t* smem, const SkP* sk, int publish, int fix_lo = 0,
                                           int fix_hi = -1, int self = -1, uint64_t tt = 0)
 {
+    static_assert((EK & 7) != EK_HEADS || !(EK & EK_CONV), "a convolution has no heads epilogue");
+    constexpr bool kConv = (EK & EK_CONV) != 0;
+    constexpr int EKE = EK & 7;                 // the epilogue kind
     constexpr int NT = 64 * NW;                 // threads
     constexpr int WM = BM / (NW / 2);           // tokens per wave (waves: 2 along channels x NW/2 along tokens)
     constexpr int WC = BN / 2;                  // channels per wave
@@ -437,7 +445,23 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
     // offset is a scalar; activation rows past M read the last row.
     const char* gA = reinterpret_cast<const char*>(p.a + int64_t(z) * p.sa + int64_t(m0) * p.lda);
     const char* gW = static_cast<const char*>(p.w) + int64_t(n0) * p.K * (kF8 ? 1 : 2);
-    const BufRes rsA = buf_res(gA, uint32_t(((min(int(p.M) - m0, BM) - 1) * int64_t(p.lda) + p.K) * 2));
+    // a convolution's tile reads up to 2 (w + 2) + 2 rows past its own (the taps' shifts), all inside the input
+    const BufRes rsA = buf_res(
+        gA, uint32_t(kConv ? (min(int(p.M) - m0, BM) + 2 * int64_t(p.conv_pw) + 2) * p.lda * 2
+                           : ((min(int(p.M) - m0, BM) - 1) * int64_t(p.lda) + p.K) * 2));
+    // A's byte offset of k step kt. Convolution: k = tap * lda + channel, tap = 3 dy + dx reads the row shifted by
+    // dy (w + 2) + dx; the k step lies inside one tap (lda is a multiple of 64). tap = kt / tpt by multiply-shift
+    // (exact for kt < 2^16 / tpt), dy = tap / 3 likewise (exact for tap < 9).
+    auto koffA = [&](int kt) -> uint32_t {
+        if constexpr (kConv) {
+            const uint32_t tap = (uint32_t(kt) * p.conv_inv) >> 16;
+            const uint32_t dy = (tap * 21846u) >> 16, dx = tap - 3 * dy;
+            const uint32_t ch = (uint32_t(kt) - tap * p.conv_tpt) * BK;
+            return ((dy * p.conv_pw + dx) * uint32_t(p.lda) + ch) * 2;
+        } else {
+            return uint32_t(kt * BK * 2);
+        }
+    };
     const BufRes rsW = buf_res(gW, uint32_t(int64_t(BN) * p.K * 2));
     uint32_t oa[RA];
 #pragma unroll
@@ -464,7 +488,7 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
     // direct load i (activation rounds first, then bf16 weight rounds) of k step kt into buffer buf
     auto dma1 = [&](int kt, int buf, int i) {
         if (i < RA)
-            buf_load_lds16(rsA, (lds_void*)&sA[buf][(i * NW + wave) * 64 * 8], oa[i], uint32_t(kt * BK * 2));
+            buf_load_lds16(rsA, (lds_void*)&sA[buf][(i * NW + wave) * 64 * 8], oa[i], koffA(kt));
         else if constexpr (!kF8)
             buf_load_lds16(rsW, (lds_void*)&sW[buf][((i - RA) * NW + wave) * 64 * 8], ow[i - RA],
                            uint32_t(kt * BK * 2));
@@ -535,7 +559,7 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
     auto gload = [&](int kt, int i) {
         if constexpr (kStage) {
             if (i < RA)
-                stg[i] = buf_load16(rsA, oa[i], uint32_t(kt * BK * 2));
+                stg[i] = buf_load16(rsA, oa[i], koffA(kt));
             else
                 stg[i] = buf_load16(rsW, ow[i - RA], uint32_t(kt * BK * 2));
         }
@@ -817,7 +841,7 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
         }
     };
     constexpr int NS = WM / 32, RB = TB / NS; // 32-token slices of a wave, MFMA token blocks a slice
-    if constexpr (EK == EK_HEADS) {
+    if constexpr (EKE == EK_HEADS) {
         // the heads epilogue is large: one copy of it in a rolled loop over the 32-token slices, which always
         // stages slice 0 of the accumulators and then rotates the next slice into its place (static register
         // indices, so the accumulators stay in registers)
@@ -837,7 +861,7 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
         stage(s);
-        epi_slice<EK, WC>(p, st, LDW, m0 + wm * WM + s * 32, n0 + wn * WC, lane, zc, kch);
+        epi_slice<EKE, WC>(p, st, LDW, m0 + wm * WM + s * 32, n0 + wn * WC, lane, zc, kch);
     }
 }
 
@@ -1154,3 +1178,55 @@ extern "C" mk_status mk_gemm_grouped(const mk_gemm_args* a, uint32_t count, void
 }
 
 extern "C" mk_status mk_gemm(const mk_gemm_args* a, void* stream) { return mk_gemm_grouped(a, 1, stream); }
+
+// 3 x 3 convolution as one GEMM over the padded pixel grid: output row r (grid pixel r of (h + 2) x (w + 2)) and tap
+// (dy, dx) read input row r + dy (w + 2) + dx of x, whose w + 3 slack rows before the grid make every shift
+// non-negative; K = 9 c runs tap-major, each 64-wide k step inside one tap, so the tap is a scalar offset of the
+// k step (koffA). The ring's output rows are computed like the others and are the caller's to ignore.
+extern "C" mk_status mk_conv3x3(const mk_conv_args* a, void* stream)
+{
+    if (!a || !a->x || !a->w || !a->y)
+        return fail(MK_ERR_ARG, "conv3x3: null argument");
+    if (!a->h || !a->width || a->c % 64 || !a->c || a->c > 4096 || a->n % 64 || !a->n)
+        return fail(MK_ERR_ARG, "conv3x3: needs h, w >= 1 and channels in, out nonzero multiples of 64 (in <= 4096)");
+    if ((a->epilogue != MK_EPI_STORE && a->epilogue != MK_EPI_ADD) ||
+        (a->epilogue == MK_EPI_ADD && a->y_dtype != MK_F32) || (a->y_dtype != MK_F32 && a->y_dtype != MK_BF16))
+        return fail(MK_ERR_ARG, "conv3x3: epilogue STORE (fp32 or bf16) or ADD (fp32)");
+    const uint64_t pw = uint64_t(a->width) + 2, rows = (uint64_t(a->h) + 2) * pw;
+    if (rows >= (1u << 31) || (256 + 2 * pw + 2) * a->c * 2 >= (uint64_t(1) << 32) || a->ldy < a->n)
+        return fail(MK_ERR_ARG, "conv3x3: image too large or ldy < n");
+    mk_gemm_args g{};
+    g.a = a->x;
+    g.w = a->w;
+    g.bias = a->bias;
+    g.c = a->y;
+    g.M = uint32_t(rows);
+    g.N = a->n;
+    g.K = 9 * a->c;
+    g.lda = a->c;
+    g.ldc = a->ldy;
+    g.batch = 1;
+    g.w_dtype = MK_BF16;
+    g.c_dtype = a->y_dtype;
+    g.epilogue = a->epilogue;
+    GemmP p;
+    MK_TRY(prepare(&g, p));
+    p.conv_pw = uint32_t(pw);
+    p.conv_tpt = a->c / 64;
+    p.conv_inv = (65536u + p.conv_tpt - 1) / p.conv_tpt;
+    int cus = 0, dev = 0;
+    MK_HIP(hipGetDevice(&dev));
+    MK_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    GemmPlan plan = gemm_plan(&g, 1, uint32_t(cus > 0 ? cus : 1));
+    plan.sk = false;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const bool add = a->epilogue == MK_EPI_ADD;
+    if (plan.bn == 256)
+        return add ? launch<256, 256, false, EK_RMW | EK_CONV, 8>(&p, 1, plan, s)
+                   : launch<256, 256, false, EK_STORE | EK_CONV, 8>(&p, 1, plan, s);
+    if (plan.bn == 128)
+        return add ? launch<256, 128, false, EK_RMW | EK_CONV, 4>(&p, 1, plan, s)
+                   : launch<256, 128, false, EK_STORE | EK_CONV, 4>(&p, 1, plan, s);
+    return add ? launch<256, 64, false, EK_RMW | EK_CONV, 4>(&p, 1, plan, s)
+               : launch<256, 64, false, EK_STORE | EK_CONV, 4>(&p, 1, plan, s);
+}

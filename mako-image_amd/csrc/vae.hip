@@ -1,0 +1,863 @@
+// The VAE decoder after the denoise loop (src/image/engine.cpp:862-954; weights as load_vae reads them, :589-628): the
+// Wan-2.1-layout decoder Qwen-Image uses, one frame. Every 3 x 3 convolution is one implicit-GEMM launch on the matrix
+// cores (mk_conv3x3 over the padded pixel grid), 1 x 1 convolutions are plain GEMMs over the same rows, and the kernels
+// here do the rest: token unpacking with the latent denormalisation and post_quant_conv, RMS norms (+ SiLU) that write
+// the next convolution's bf16 input with its zero ring, nearest 2x upsampling into the next grid, the mid block's
+// softmax, and the clamp to RGBA.
+//
+// Image layout "padded grid" (h x w, c channels, row stride cs): (h + 2)(w + 2) grid rows with a one-pixel ring, and
+// S = w + 3 slack rows before and after; pixel (y, x) is row S + (y + 1)(w + 2) + x + 1. fp32 activations use it as
+// written by the convolutions (ring rows hold values nobody reads as pixels); bf16 convolution inputs keep ring and
+// slack rows zero, and channels past c zero.
+#include "common.hpp"
+
+#include <algorithm>
+#include <cmath>
+#include <map>
+#include <memory>
+#include <string>
+#include <vector>
+
+namespace mk {
+namespace {
+
+struct GridDims {
+    uint32_t h, w;
+    __host__ __device__ uint32_t pw() const { return w + 2; }
+    __host__ __device__ uint32_t slack() const { return w + 3; }
+    __host__ __device__ uint64_t grid_rows() const { return uint64_t(h + 2) * (w + 2); }
+    __host__ __device__ uint64_t rows() const { return grid_rows() + 2ull * slack(); }
+    __host__ __device__ uint64_t row_of(uint32_t y, uint32_t x) const { return slack() + uint64_t(y + 1) * pw() + x + 1; }
+    // the pixel of buffer row r, or false for ring and slack rows
+    __host__ __device__ bool pixel(uint64_t r, uint32_t& y, uint32_t& x) const
+    {
+        if (r < slack() || r >= slack() + grid_rows())
+            return false;
+        const uint64_t g = r - slack();
+        const uint32_t gy = uint32_t(g / pw()), gx = uint32_t(g % pw());
+        if (gy == 0 || gy > h || gx == 0 || gx > w)
+            return false;
+        y = gy - 1;
+        x = gx - 1;
+        return true;
+    }
+};
+
+inline uint32_t cpad(uint32_t c) { return (c + 63) / 64 * 64; }
+
+// tokens [th][tw][4 z] -> the latent image (2 th x 2 tw, z channels: value (c * 2 + py) * 2 + px of a token is channel
+// c of pixel (2 y + py, 2 x + px)), denormalised (v * std + mean, engine.cpp:887-898), post_quant_conv in fp32
+// (w [z][z], b [z]), written as the bf16 padded grid with cp channels. One thread a (buffer row, channel).
+__global__ __launch_bounds__(256) void vae_in_kernel(const float* __restrict__ tok, uint32_t tw, GridDims g, uint32_t z,
+                                                     uint32_t cp, const float* __restrict__ mean,
+                                                     const float* __restrict__ sd, const float* __restrict__ w,
+                                                     const float* __restrict__ b, uint16_t* __restrict__ out)
+{
+    const uint64_t i = uint64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= g.rows() * cp)
+        return;
+    const uint64_t r = i / cp;
+    const uint32_t c = uint32_t(i % cp);
+    uint32_t y, x;
+    float v = 0.0f;
+    if (c < z && g.pixel(r, y, x)) {
+        const float* t = tok + (uint64_t(y / 2) * tw + x / 2) * 4 * z + (y % 2) * 2 + (x % 2);
+        float acc = b[c];
+        for (uint32_t ch = 0; ch < z; ++ch)
+            acc = fmaf(w[c * z + ch], t[4 * ch] * sd[ch] + mean[ch], acc);
+        v = acc;
+    }
+    out[i] = f2bf_bits(v);
+}
+
+// RMS norm over a pixel's c channels (x / sqrt(mean(x^2) + 1e-24 / c) * gamma, engine.cpp:725-727), then SiLU (mode
+// 0), or not (mode 1), or a plain bf16 copy (mode 2). One wave a row; x fp32 rows of stride cs; y bf16 rows of stride
+// cp. Grid output (compact = 0): every buffer row of y, ring and slack rows and channels past c zero. Compact output:
+// y row p = pixel p (y * w + x), p < rows.
+__global__ __launch_bounds__(256) void vae_norm_kernel(const float* __restrict__ xg, uint32_t cs, GridDims g,
+                                                       uint32_t c, const float* __restrict__ gamma, int mode,
+                                                       int compact, uint64_t rows, uint16_t* __restrict__ y,
+                                                       uint32_t cp)
+{
+    const uint64_t r = uint64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (r >= rows)
+        return;
+    uint16_t* yr = y + r * cp;
+    uint32_t py, px;
+    bool on;
+    if (compact) {
+        py = uint32_t(r / g.w);
+        px = uint32_t(r % g.w);
+        on = true;
+    } else {
+        on = g.pixel(r, py, px);
+    }
+    if (!on) {
+        for (uint32_t k = lane; k < cp; k += 64)
+            yr[k] = 0;
+        return;
+    }
+    const float* xr = xg + g.row_of(py, px) * cs;
+    constexpr int J = 8; // channels <= 512
+    float v[J];
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const uint32_t k = lane + 64 * j;
+        v[j] = k < c ? xr[k] : 0.0f;
+        ss = fmaf(v[j], v[j], ss);
+    }
+    float s = 1.0f;
+    if (mode != 2) {
+        ss = wave_sum(ss);
+        s = rsqrtf(ss / float(c) + 1e-24f / float(c));
+    }
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const uint32_t k = lane + 64 * j;
+        if (k >= cp)
+            break;
+        float o = 0.0f;
+        if (k < c) {
+            o = mode == 2 ? v[j] : v[j] * s * gamma[k];
+            if (mode == 0)
+                o = o / (1.0f + __expf(-o));
+        }
+        yr[k] = f2bf_bits(o);
+    }
+}
+
+// Nearest 2x: the bf16 padded grid of the 2h x 2w image (cp channels) from the fp32 grid of the h x w one (c
+// channels, stride cs). One thread a (output row, channel).
+__global__ __launch_bounds__(256) void vae_up_kernel(const float* __restrict__ x, uint32_t cs, GridDims gi,
+                                                     uint32_t c, GridDims go, uint32_t cp, uint16_t* __restrict__ y)
+{
+    const uint64_t i = uint64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= go.rows() * cp)
+        return;
+    const uint64_t r = i / cp;
+    const uint32_t k = uint32_t(i % cp);
+    uint32_t py, px;
+    float v = 0.0f;
+    if (k < c && go.pixel(r, py, px))
+        v = x[gi.row_of(py / 2, px / 2) * cs + k];
+    y[i] = f2bf_bits(v);
+}
+
+// Row softmax for the mid block's attention: p[j] = exp(scale (s[j] - max)) / sum over the n real columns, bf16, 0
+// for the padding columns up to ld. One block a row.
+__global__ __launch_bounds__(256) void vae_softmax_kernel(const float* __restrict__ s, uint32_t n, uint32_t ld,
+                                                          float scale, uint16_t* __restrict__ p)
+{
+    __shared__ float red[4];
+    const float* sr = s + uint64_t(blockIdx.x) * ld;
+    uint16_t* pr = p + uint64_t(blockIdx.x) * ld;
+    float m = -INFINITY;
+    for (uint32_t j = threadIdx.x; j < n; j += 256)
+        m = fmaxf(m, sr[j]);
+    m = wave_max(m);
+    if ((threadIdx.x & 63) == 0)
+        red[threadIdx.x >> 6] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    __syncthreads();
+    float sum = 0.0f;
+    for (uint32_t j = threadIdx.x; j < n; j += 256)
+        sum += __expf(scale * (sr[j] - m));
+    sum = wave_sum(sum);
+    if ((threadIdx.x & 63) == 0)
+        red[threadIdx.x >> 6] = sum;
+    __syncthreads();
+    const float inv = 1.0f / (red[0] + red[1] + red[2] + red[3]);
+    for (uint32_t j = threadIdx.x; j < ld; j += 256)
+        pr[j] = j < n ? f2bf_bits(__expf(scale * (sr[j] - m)) * inv) : uint16_t(0);
+}
+
+// x (fp32 grid, stride cs) += y (compact [pixels][cs]) over c channels. One thread a (pixel, channel).
+__global__ __launch_bounds__(256) void vae_add_kernel(float* __restrict__ x, uint32_t cs, GridDims g, uint32_t c,
+                                                      const float* __restrict__ y)
+{
+    const uint64_t i = uint64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= uint64_t(g.h) * g.w * c)
+        return;
+    const uint64_t p = i / c;
+    const uint32_t k = uint32_t(i % c);
+    x[g.row_of(uint32_t(p / g.w), uint32_t(p % g.w)) * cs + k] += y[p * cs + k];
+}
+
+// fp32 grid (stride cs, c channels) -> compact [pixels][c] (probes).
+__global__ __launch_bounds__(256) void vae_compact_kernel(const float* __restrict__ x, uint32_t cs, GridDims g,
+                                                          uint32_t c, float* __restrict__ y)
+{
+    const uint64_t i = uint64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= uint64_t(g.h) * g.w * c)
+        return;
+    const uint64_t p = i / c;
+    y[i] = x[g.row_of(uint32_t(p / g.w), uint32_t(p % g.w)) * cs + i % c];
+}
+
+// conv_out's first 3 channels -> RGBA in [-1, 1], alpha 1 (engine.cpp:948-953). One thread a pixel.
+__global__ __launch_bounds__(256) void vae_out_kernel(const float* __restrict__ x, uint32_t cs, GridDims g,
+                                                      float* __restrict__ rgba)
+{
+    const uint64_t p = uint64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (p >= uint64_t(g.h) * g.w)
+        return;
+    const float* xr = x + g.row_of(uint32_t(p / g.w), uint32_t(p % g.w)) * cs;
+    f32x4 o;
+    for (int k = 0; k < 3; ++k)
+        o[k] = fminf(1.0f, fmaxf(-1.0f, xr[k]));
+    o[3] = 1.0f;
+    *reinterpret_cast<f32x4*>(rgba + 4 * p) = o;
+}
+
+// A PyTorch conv weight [parts * co][ci][kt][k][k] (bf16; kt time taps of a causal 3-D conv, the last one used: a
+// single frame sees only it) -> [parts][cop][k * k][cip] bf16, tap-major, zero-padded. One thread an output value.
+__global__ __launch_bounds__(256) void vae_pack_kernel(const uint16_t* __restrict__ src, uint32_t parts, uint32_t co,
+                                                       uint32_t ci, uint32_t kt, uint32_t kk, uint32_t cop,
+                                                       uint32_t cip, uint16_t* __restrict__ dst)
+{
+    const uint64_t i = uint64_t(blockIdx.x) * 256 + threadIdx.x;
+    const uint64_t n = uint64_t(parts) * cop * kk * cip;
+    if (i >= n)
+        return;
+    const uint32_t c = uint32_t(i % cip);
+    const uint64_t q = i / cip;
+    const uint32_t tap = uint32_t(q % kk);
+    const uint64_t po = q / kk;
+    const uint32_t o = uint32_t(po % cop), part = uint32_t(po / cop);
+    uint16_t v = 0;
+    if (o < co && c < ci)
+        v = src[((uint64_t(part * co + o) * ci + c) * kt + (kt - 1)) * kk + tap];
+    dst[i] = v;
+}
+
+// fp32 vector [parts * n] -> [parts][np] zero-padded.
+__global__ __launch_bounds__(256) void vae_pack_vec_kernel(const float* __restrict__ src, uint32_t parts, uint32_t n,
+                                                           uint32_t np, float* __restrict__ dst)
+{
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= parts * np)
+        return;
+    const uint32_t k = i % np, part = i / np;
+    dst[i] = k < n ? src[part * n + k] : 0.0f;
+}
+
+inline uint32_t blocks_for(uint64_t n) { return uint32_t((n + 255) / 256); }
+
+// MK_OK, or the HIP error as a status (hip_check records a failure; it is only called on one)
+inline mk_status hip_ok(hipError_t e, const char* what) { return e == hipSuccess ? MK_OK : hip_check(e, what); }
+
+} // namespace
+} // namespace mk
+
+using namespace mk;
+
+struct mk_vae {
+    // A convolution's packed weight [parts][cop][k * k][cip] and bias [parts][cop] (fp32).
+    struct Conv {
+        uint16_t* w = nullptr;
+        float* b = nullptr;
+        uint32_t co = 0, ci = 0, k = 0, parts = 1;
+        uint32_t cop() const { return cpad(co); }
+        uint32_t cip() const { return cpad(ci); }
+    };
+    struct Res {
+        float *g1 = nullptr, *g2 = nullptr;
+        Conv c1, c2, sc;
+        bool shortcut = false;
+    };
+    // a checkpoint tensor: where it goes and how
+    struct Slot {
+        enum Kind { CONV_W, CONV_B, VEC, PQ_W } kind;
+        Conv* conv = nullptr;
+        float* vec = nullptr;
+        uint32_t n = 0; // VEC: values
+        std::vector<int64_t> dims; // PyTorch shape of the synthetic tensor
+    };
+
+    uint32_t base = 0, z = 0;
+    std::vector<float> mean, sd;
+    hipStream_t stream = nullptr;
+    std::vector<void*> allocs;
+    std::map<std::string, Slot> slots;
+    std::vector<std::unique_ptr<Conv>> convs;
+
+    float *pq_w = nullptr, *pq_b = nullptr, *d_mean = nullptr, *d_sd = nullptr;
+    Conv conv_in, qkv, proj, conv_out;
+    Res mid0, mid1;
+    float* attn_g = nullptr;
+    struct Up {
+        Res res[3];
+        bool up = false;
+        Conv conv;
+        uint32_t cin = 0, cout = 0;
+    } ups[4];
+    float* out_g = nullptr;
+
+    // scratch
+    struct Buf {
+        void* p = nullptr;
+        size_t bytes = 0;
+    };
+    Buf x, y, t, a, sc, qb, kb, vtb, sb, pb, ob, pj, tok, rgba, probe_buf;
+    mk_probe_fn probe = nullptr;
+    void* probe_user = nullptr;
+
+    ~mk_vae()
+    {
+        if (stream)
+            (void)hipStreamSynchronize(stream);
+        for (void* p : allocs)
+            (void)hipFree(p);
+        for (Buf* b : {&x, &y, &t, &a, &sc, &qb, &kb, &vtb, &sb, &pb, &ob, &pj, &tok, &rgba, &probe_buf})
+            if (b->p)
+                (void)hipFree(b->p);
+        if (stream)
+            (void)hipStreamDestroy(stream);
+    }
+
+    mk_status alloc(size_t bytes, void** p)
+    {
+        MK_HIP(hipMalloc(p, bytes));
+        MK_HIP(hipMemset(*p, 0, bytes));
+        allocs.push_back(*p);
+        return MK_OK;
+    }
+    mk_status ensure(Buf& b, size_t bytes)
+    {
+        if (b.bytes >= bytes)
+            return MK_OK;
+        MK_HIP(hipStreamSynchronize(stream));
+        if (b.p)
+            MK_HIP(hipFree(b.p));
+        b.p = nullptr;
+        b.bytes = 0;
+        MK_HIP(hipMalloc(&b.p, bytes));
+        MK_HIP(hipMemset(b.p, 0, bytes));
+        b.bytes = bytes;
+        return MK_OK;
+    }
+
+    mk_status conv(Conv& c, const std::string& name, uint32_t co, uint32_t ci, uint32_t k, uint32_t parts = 1)
+    {
+        c.co = co;
+        c.ci = ci;
+        c.k = k;
+        c.parts = parts;
+        MK_TRY(alloc(size_t(parts) * c.cop() * k * k * c.cip() * 2, reinterpret_cast<void**>(&c.w)));
+        MK_TRY(alloc(size_t(parts) * c.cop() * 4, reinterpret_cast<void**>(&c.b)));
+        Slot w{Slot::CONV_W, &c, nullptr, 0, {int64_t(parts) * co, ci, k, k}};
+        Slot b{Slot::CONV_B, &c, nullptr, 0, {int64_t(parts) * co}};
+        slots[name + ".weight"] = w;
+        slots[name + ".bias"] = b;
+        return MK_OK;
+    }
+    mk_status vec(float** p, const std::string& name, uint32_t n)
+    {
+        MK_TRY(alloc(size_t(n) * 4, reinterpret_cast<void**>(p)));
+        slots[name] = Slot{Slot::VEC, nullptr, *p, n, {int64_t(n)}};
+        return MK_OK;
+    }
+    mk_status res(Res& r, const std::string& p, uint32_t ci, uint32_t co)
+    {
+        MK_TRY(vec(&r.g1, p + ".norm1.gamma", ci));
+        MK_TRY(conv(r.c1, p + ".conv1", co, ci, 3));
+        MK_TRY(vec(&r.g2, p + ".norm2.gamma", co));
+        MK_TRY(conv(r.c2, p + ".conv2", co, co, 3));
+        r.shortcut = ci != co;
+        if (r.shortcut)
+            MK_TRY(conv(r.sc, p + ".conv_shortcut", co, ci, 1));
+        return MK_OK;
+    }
+
+    mk_status build()
+    {
+        const uint32_t b = base, d0 = 4 * b;
+        MK_HIP(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
+        MK_TRY(alloc(size_t(z) * z * 4, reinterpret_cast<void**>(&pq_w)));
+        MK_TRY(alloc(size_t(z) * 4, reinterpret_cast<void**>(&pq_b)));
+        slots["post_quant_conv.weight"] = Slot{Slot::PQ_W, nullptr, pq_w, z * z, {z, z, 1, 1}};
+        slots["post_quant_conv.bias"] = Slot{Slot::VEC, nullptr, pq_b, z, {z}};
+        MK_TRY(alloc(size_t(z) * 4, reinterpret_cast<void**>(&d_mean)));
+        MK_TRY(alloc(size_t(z) * 4, reinterpret_cast<void**>(&d_sd)));
+        MK_HIP(hipMemcpy(d_mean, mean.data(), z * 4, hipMemcpyHostToDevice));
+        MK_HIP(hipMemcpy(d_sd, sd.data(), z * 4, hipMemcpyHostToDevice));
+        MK_TRY(conv(conv_in, "decoder.conv_in", d0, z, 3));
+        MK_TRY(res(mid0, "decoder.mid_block.resnets.0", d0, d0));
+        MK_TRY(vec(&attn_g, "decoder.mid_block.attentions.0.norm.gamma", d0));
+        MK_TRY(conv(qkv, "decoder.mid_block.attentions.0.to_qkv", d0, d0, 1, 3));
+        MK_TRY(conv(proj, "decoder.mid_block.attentions.0.proj", d0, d0, 1));
+        MK_TRY(res(mid1, "decoder.mid_block.resnets.1", d0, d0));
+        const uint32_t ins[4] = {4 * b, 2 * b, 2 * b, b}, outs[4] = {4 * b, 4 * b, 2 * b, b};
+        for (int i = 0; i < 4; ++i) {
+            const std::string p = "decoder.up_blocks." + std::to_string(i);
+            Up& u = ups[i];
+            u.cin = ins[i];
+            u.cout = outs[i];
+            for (int j = 0; j < 3; ++j)
+                MK_TRY(res(u.res[j], p + ".resnets." + std::to_string(j), j ? outs[i] : ins[i], outs[i]));
+            u.up = i < 3;
+            if (u.up)
+                MK_TRY(conv(u.conv, p + ".upsamplers.0.resample.1", outs[i] / 2, outs[i], 3));
+        }
+        MK_TRY(vec(&out_g, "decoder.norm_out.gamma", b));
+        MK_TRY(conv(conv_out, "decoder.conv_out", 3, b, 3));
+        return MK_OK;
+    }
+
+    // One tensor from device memory in PyTorch layout: conv weights bf16 [parts * co][ci][kt][k][k] (kt >= 1),
+    // everything else fp32.
+    mk_status put(const Slot& s, const void* src, uint32_t kt)
+    {
+        switch (s.kind) {
+        case Slot::CONV_W: {
+            const Conv& c = *s.conv;
+            const uint64_t n = uint64_t(c.parts) * c.cop() * c.k * c.k * c.cip();
+            vae_pack_kernel<<<blocks_for(n), 256, 0, stream>>>(static_cast<const uint16_t*>(src), c.parts, c.co, c.ci,
+                                                              kt, c.k * c.k, c.cop(), c.cip(), c.w);
+            break;
+        }
+        case Slot::CONV_B: {
+            const Conv& c = *s.conv;
+            vae_pack_vec_kernel<<<blocks_for(c.parts * c.cop()), 256, 0, stream>>>(
+                static_cast<const float*>(src), c.parts, c.co, c.cop(), c.b);
+            break;
+        }
+        case Slot::PQ_W: // bf16 [z][z] -> fp32
+            return mk_bf16_to_f32(src, s.n, s.vec, stream);
+        case Slot::VEC:
+            MK_HIP(hipMemcpyAsync(s.vec, src, size_t(s.n) * 4, hipMemcpyDeviceToDevice, stream));
+            return MK_OK;
+        }
+        MK_LAUNCH_CHECK("vae weight pack");
+        return MK_OK;
+    }
+
+    // ---- the decoder ----
+    mk_status conv3(const Conv& c, const void* in, GridDims g, void* out, uint32_t ldo, bool add)
+    {
+        mk_conv_args a{};
+        a.x = in;
+        a.w = c.w;
+        a.bias = c.b;
+        a.y = static_cast<float*>(out) + uint64_t(g.slack()) * ldo;
+        a.h = g.h;
+        a.width = g.w;
+        a.c = c.cip();
+        a.n = c.cop();
+        a.ldy = ldo;
+        a.y_dtype = MK_F32;
+        a.epilogue = add ? MK_EPI_ADD : MK_EPI_STORE;
+        return mk_conv3x3(&a, stream);
+    }
+    // 1 x 1 conv over rows (grid or compact): y[rows][ldo] (fp32 or bf16) = a[rows][cip] W^T + b (or +=)
+    mk_status conv1(const Conv& c, uint32_t part, const void* a, uint64_t rows, void* out, uint32_t ldo,
+                    uint32_t out_dtype, uint32_t epi)
+    {
+        mk_gemm_args g{};
+        g.a = a;
+        g.w = c.w + size_t(part) * c.cop() * c.cip();
+        g.bias = c.b + size_t(part) * c.cop();
+        g.c = out;
+        g.M = uint32_t(rows);
+        g.N = c.cop();
+        g.K = c.cip();
+        g.lda = c.cip();
+        g.ldc = ldo;
+        g.batch = 1;
+        g.w_dtype = MK_BF16;
+        g.c_dtype = out_dtype;
+        g.epilogue = epi;
+        return mk_gemm(&g, stream);
+    }
+    mk_status norm(const void* xg, uint32_t cs, GridDims g, uint32_t c, const float* gamma, int mode, void* out,
+                   uint32_t cp)
+    {
+        const uint64_t rows = g.rows();
+        vae_norm_kernel<<<blocks_for(rows * 64), 256, 0, stream>>>(static_cast<const float*>(xg), cs, g, c, gamma,
+                                                                   mode, 0, rows, static_cast<uint16_t*>(out), cp);
+        MK_LAUNCH_CHECK("vae_norm");
+        return MK_OK;
+    }
+    mk_status probe_grid(const char* name, int layer, const void* xg, uint32_t cs, GridDims g, uint32_t c)
+    {
+        if (!probe)
+            return MK_OK;
+        const uint64_t n = uint64_t(g.h) * g.w * c;
+        MK_TRY(ensure(probe_buf, n * 4));
+        vae_compact_kernel<<<blocks_for(n), 256, 0, stream>>>(static_cast<const float*>(xg), cs, g, c,
+                                                              static_cast<float*>(probe_buf.p));
+        MK_LAUNCH_CHECK("vae_compact");
+        std::vector<float> h(n);
+        MK_HIP(hipMemcpyAsync(h.data(), probe_buf.p, n * 4, hipMemcpyDeviceToHost, stream));
+        MK_HIP(hipStreamSynchronize(stream));
+        probe(probe_user, name, layer, h.data(), n);
+        return MK_OK;
+    }
+
+    // res_block (engine.cpp:732-746): x (fp32 grid, stride cs = cpad(cout) after) <- conv2(silu(norm2(conv1(
+    // silu(norm1(x)))))) + shortcut(x). x and the result may differ in channels; xs is x's stride.
+    mk_status res_block(const Res& r, GridDims g, float*& xp, uint32_t xs, float*& yp)
+    {
+        const Conv &c1 = r.c1, &c2 = r.c2;
+        MK_TRY(norm(xp, xs, g, c1.ci, r.g1, 0, a.p, c1.cip()));
+        MK_TRY(conv3(c1, a.p, g, t.p, c1.cop(), false));
+        MK_TRY(norm(t.p, c1.cop(), g, c1.co, r.g2, 0, a.p, c2.cip()));
+        if (r.shortcut) {
+            // y = shortcut(x) over the grid rows, then y += conv2
+            MK_TRY(norm(xp, xs, g, r.sc.ci, nullptr, 2, sc.p, r.sc.cip()));
+            MK_TRY(conv1(r.sc, 0, static_cast<uint16_t*>(sc.p) + uint64_t(g.slack()) * r.sc.cip(), g.grid_rows(),
+                         yp + uint64_t(g.slack()) * r.sc.cop(), r.sc.cop(), MK_F32, MK_EPI_STORE));
+            MK_TRY(conv3(c2, a.p, g, yp, c2.cop(), true));
+            std::swap(xp, yp);
+        } else {
+            MK_TRY(conv3(c2, a.p, g, xp, c2.cop(), true));
+        }
+        return MK_OK;
+    }
+
+    // vae_attention (engine.cpp:748-777): one head over the n pixels, d = c
+    mk_status attention(GridDims g, float* xp)
+    {
+        const uint32_t c = qkv.co, cp = qkv.cip();
+        const uint64_t n = uint64_t(g.h) * g.w, np = (n + 63) / 64 * 64;
+        // q [np][cp], k [np][cp] (rows past n zero), v^T [cp][np], the normed pixels [np][cp] (rows past n zero)
+        MK_TRY(ensure(qb, np * cp * 2));
+        MK_TRY(ensure(kb, np * cp * 2));
+        MK_TRY(ensure(vtb, np * cp * 2));
+        MK_TRY(ensure(ob, np * cp * 2));
+        MK_TRY(ensure(pj, np * cp * 4));
+        MK_TRY(ensure(sc, np * cp * 2));
+        MK_HIP(hipMemsetAsync(kb.p, 0, np * cp * 2, stream));
+        MK_HIP(hipMemsetAsync(sc.p, 0, np * cp * 2, stream));
+        uint16_t* xn = static_cast<uint16_t*>(sc.p);
+        vae_norm_kernel<<<blocks_for(n * 64), 256, 0, stream>>>(xp, cp, g, c, attn_g, 1, 1, n, xn, cp);
+        MK_LAUNCH_CHECK("vae_norm");
+        MK_TRY(conv1(qkv, 0, xn, n, qb.p, cp, MK_BF16, MK_EPI_STORE));
+        MK_TRY(conv1(qkv, 1, xn, n, kb.p, cp, MK_BF16, MK_EPI_STORE));
+        {
+            // v^T = W_v xn^T, no bias (added after the weighted sum: each softmax row sums to 1)
+            mk_gemm_args v{};
+            v.a = qkv.w + size_t(2) * cp * cp;
+            v.w = xn;
+            v.c = vtb.p;
+            v.M = cp;
+            v.N = uint32_t(np);
+            v.K = cp;
+            v.lda = cp;
+            v.ldc = int64_t(np);
+            v.batch = 1;
+            v.w_dtype = MK_BF16;
+            v.c_dtype = MK_BF16;
+            v.epilogue = MK_EPI_STORE;
+            MK_TRY(mk_gemm(&v, stream));
+        }
+        // queries in chunks whose scores stay near 1 GiB
+        const uint64_t qc = std::min<uint64_t>(n, std::max<uint64_t>(256, (uint64_t(1) << 28) / np / 256 * 256));
+        MK_TRY(ensure(sb, qc * np * 4));
+        MK_TRY(ensure(pb, qc * np * 2));
+        const float scale = 1.0f / std::sqrt(float(c));
+        for (uint64_t q0 = 0; q0 < n; q0 += qc) {
+            const uint64_t m = std::min(qc, n - q0);
+            mk_gemm_args s{};
+            s.a = static_cast<uint16_t*>(qb.p) + q0 * cp;
+            s.w = kb.p;
+            s.c = sb.p;
+            s.M = uint32_t(m);
+            s.N = uint32_t(np);
+            s.K = cp;
+            s.lda = cp;
+            s.ldc = int64_t(np);
+            s.batch = 1;
+            s.w_dtype = MK_BF16;
+            s.c_dtype = MK_F32;
+            s.epilogue = MK_EPI_STORE;
+            MK_TRY(mk_gemm(&s, stream));
+            vae_softmax_kernel<<<uint32_t(m), 256, 0, stream>>>(static_cast<float*>(sb.p), uint32_t(n), uint32_t(np),
+                                                                scale, static_cast<uint16_t*>(pb.p));
+            MK_LAUNCH_CHECK("vae_softmax");
+            mk_gemm_args o{};
+            o.a = pb.p;
+            o.w = vtb.p;
+            o.bias = qkv.b + size_t(2) * cp;
+            o.c = static_cast<uint16_t*>(ob.p) + q0 * cp;
+            o.M = uint32_t(m);
+            o.N = cp;
+            o.K = uint32_t(np);
+            o.lda = int64_t(np);
+            o.ldc = cp;
+            o.batch = 1;
+            o.w_dtype = MK_BF16;
+            o.c_dtype = MK_BF16;
+            o.epilogue = MK_EPI_STORE;
+            MK_TRY(mk_gemm(&o, stream));
+        }
+        MK_TRY(conv1(proj, 0, ob.p, n, pj.p, cp, MK_F32, MK_EPI_STORE));
+        vae_add_kernel<<<blocks_for(n * c), 256, 0, stream>>>(xp, cp, g, c, static_cast<float*>(pj.p));
+        MK_LAUNCH_CHECK("vae_add");
+        return MK_OK;
+    }
+
+    // tokens (device) [th][tw][4 z] -> rgba (device) [16 th][16 tw][4]
+    mk_status decode(const float* tokens, uint32_t th, uint32_t tw, float* out)
+    {
+        const uint32_t b = base, d0 = 4 * b;
+        // the largest level's buffers: rows x the widest channels (padded) any buffer holds at that level; an upsample
+        // conv's input has the previous level's channels (4b at levels 1 and 2, 2b at level 3)
+        uint64_t most = 0;
+        {
+            GridDims g{2 * th, 2 * tw};
+            const uint32_t ch[4] = {cpad(d0), cpad(4 * b), cpad(4 * b), cpad(2 * b)};
+            for (int l = 0; l < 4; ++l) {
+                most = std::max(most, g.rows() * std::max<uint64_t>(ch[l], 64));
+                g = GridDims{2 * g.h, 2 * g.w};
+            }
+        }
+        MK_TRY(ensure(x, most * 4));
+        MK_TRY(ensure(y, most * 4));
+        MK_TRY(ensure(t, most * 4));
+        MK_TRY(ensure(a, most * 2));
+        MK_TRY(ensure(sc, most * 2));
+        GridDims g{2 * th, 2 * tw};
+        vae_in_kernel<<<blocks_for(g.rows() * conv_in.cip()), 256, 0, stream>>>(
+            tokens, tw, g, z, conv_in.cip(), d_mean, d_sd, pq_w, pq_b, static_cast<uint16_t*>(a.p));
+        MK_LAUNCH_CHECK("vae_in");
+        float* xp = static_cast<float*>(x.p);
+        float* yp = static_cast<float*>(y.p);
+        MK_TRY(conv3(conv_in, a.p, g, xp, conv_in.cop(), false));
+        MK_TRY(probe_grid("vae_conv_in", -1, xp, conv_in.cop(), g, d0));
+        MK_TRY(res_block(mid0, g, xp, cpad(d0), yp));
+        MK_TRY(attention(g, xp));
+        MK_TRY(res_block(mid1, g, xp, cpad(d0), yp));
+        MK_TRY(probe_grid("vae_mid", -1, xp, cpad(d0), g, d0));
+        uint32_t cs = cpad(d0);
+        for (int i = 0; i < 4; ++i) {
+            Up& u = ups[i];
+            for (int j = 0; j < 3; ++j) {
+                MK_TRY(res_block(u.res[j], g, xp, cs, yp));
+                cs = u.res[j].c2.cop();
+            }
+            if (u.up) {
+                const GridDims g2{2 * g.h, 2 * g.w};
+                vae_up_kernel<<<blocks_for(g2.rows() * u.conv.cip()), 256, 0, stream>>>(
+                    xp, cs, g, u.cout, g2, u.conv.cip(), static_cast<uint16_t*>(a.p));
+                MK_LAUNCH_CHECK("vae_up");
+                MK_TRY(conv3(u.conv, a.p, g2, yp, u.conv.cop(), false));
+                std::swap(xp, yp);
+                g = g2;
+                cs = u.conv.cop();
+            }
+            MK_TRY(probe_grid("vae_up", i, xp, cs, g, u.up ? u.conv.co : u.cout));
+        }
+        MK_TRY(norm(xp, cs, g, b, out_g, 0, a.p, conv_out.cip()));
+        MK_TRY(conv3(conv_out, a.p, g, yp, conv_out.cop(), false));
+        MK_TRY(probe_grid("vae_out", -1, yp, conv_out.cop(), g, 3));
+        vae_out_kernel<<<blocks_for(uint64_t(g.h) * g.w), 256, 0, stream>>>(yp, conv_out.cop(), g, out);
+        MK_LAUNCH_CHECK("vae_out");
+        return MK_OK;
+    }
+};
+
+namespace {
+
+// conv weight kt (time taps) from a PyTorch shape: 4-D [o][i][k][k] -> 1, 5-D [o][i][kt][k][k] -> kt
+bool shape_fits(const mk_vae::Slot& s, const int64_t* dims, uint32_t ndim, uint32_t* kt)
+{
+    *kt = 1;
+    uint64_t n = 1;
+    for (uint32_t i = 0; i < ndim; ++i)
+        n *= uint64_t(dims[i]);
+    if (s.kind == mk_vae::Slot::CONV_W || s.kind == mk_vae::Slot::PQ_W) {
+        const auto& d = s.dims;
+        if (ndim == 4)
+            return dims[0] == d[0] && dims[1] == d[1] && dims[2] == d[2] && dims[3] == d[3];
+        if (ndim == 5 && dims[0] == d[0] && dims[1] == d[1] && dims[3] == d[2] && dims[4] == d[3] && dims[2] >= 1 &&
+            (s.kind == mk_vae::Slot::CONV_W || dims[2] == 1)) {
+            *kt = uint32_t(dims[2]);
+            return true;
+        }
+        return false;
+    }
+    return n == uint64_t(s.dims[0]); // vectors: [n] or [n, 1, 1(, 1)]
+}
+
+} // namespace
+
+extern "C" {
+
+mk_status mk_vae_create(const mk_vae_config* cfg, mk_vae** out)
+{
+    if (!cfg || !out || !cfg->mean || !cfg->std)
+        return fail(MK_ERR_ARG, "vae_create: null");
+    *out = nullptr;
+    if (!cfg->base || cfg->base > 128 || !cfg->z || cfg->z > 64)
+        return fail(MK_ERR_ARG, "vae_create: base channels 1..128 (levels 4 base <= 512), latent channels 1..64");
+    auto v = std::make_unique<mk_vae>();
+    v->base = cfg->base;
+    v->z = cfg->z;
+    v->mean.assign(cfg->mean, cfg->mean + cfg->z);
+    v->sd.assign(cfg->std, cfg->std + cfg->z);
+    MK_TRY(v->build());
+    *out = v.release();
+    return MK_OK;
+}
+
+mk_status mk_vae_destroy(mk_vae* v)
+{
+    delete v;
+    return MK_OK;
+}
+
+mk_status mk_vae_load(mk_vae* v, const char* name, const float* data, const int64_t* dims, uint32_t ndim)
+{
+    if (!v || !name || !data || (!dims && ndim))
+        return fail(MK_ERR_ARG, "vae_load: null");
+    auto it = v->slots.find(name);
+    if (it == v->slots.end())
+        return fail(MK_ERR_ARG, std::string("vae_load: no tensor named ") + name);
+    uint32_t kt = 1;
+    if (!shape_fits(it->second, dims, ndim, &kt))
+        return fail(MK_ERR_ARG, std::string("vae_load: ") + name + " has the wrong shape");
+    uint64_t n = 1;
+    for (uint32_t i = 0; i < ndim; ++i)
+        n *= uint64_t(dims[i]);
+    const bool mat = it->second.kind == mk_vae::Slot::CONV_W || it->second.kind == mk_vae::Slot::PQ_W;
+    std::vector<uint16_t> hb;
+    const void* host = data;
+    if (mat) {
+        hb.resize(n);
+        for (uint64_t i = 0; i < n; ++i)
+            hb[i] = f2bf_bits(data[i]);
+        host = hb.data();
+    }
+    void* tmp = nullptr;
+    MK_HIP(hipMalloc(&tmp, n * (mat ? 2 : 4)));
+    mk_status st = hip_ok(hipMemcpy(tmp, host, n * (mat ? 2 : 4), hipMemcpyHostToDevice), "vae_load copy");
+    if (st == MK_OK)
+        st = v->put(it->second, tmp, kt);
+    if (st == MK_OK)
+        st = hip_ok(hipStreamSynchronize(v->stream), "vae_load sync");
+    (void)hipFree(tmp);
+    return st;
+}
+
+mk_status mk_vae_init_random(mk_vae* v, uint64_t seed)
+{
+    if (!v)
+        return fail(MK_ERR_ARG, "vae_init_random: null");
+    for (const auto& [name, s] : v->slots) {
+        uint64_t n = 1;
+        for (int64_t d : s.dims)
+            n *= uint64_t(d);
+        const bool mat = s.kind == mk_vae::Slot::CONV_W || s.kind == mk_vae::Slot::PQ_W;
+        const bool gamma = name.size() > 6 && name.compare(name.size() - 6, 6, ".gamma") == 0;
+        const double sd = mat ? 1.0 / std::sqrt(double(s.dims[1] * s.dims[2] * s.dims[3])) : gamma ? 0.1 : 0.02;
+        void* tmp = nullptr;
+        MK_HIP(hipMalloc(&tmp, n * (mat ? 2 : 4)));
+        mk_status st = mk_fill_normal(tmp, n, mat ? MK_BF16 : MK_F32, tensor_key(seed, name.c_str()),
+                                      gamma ? 1.0 : 0.0, sd, v->stream);
+        if (st == MK_OK)
+            st = v->put(s, tmp, 1);
+        if (st == MK_OK)
+            st = hip_ok(hipStreamSynchronize(v->stream), "vae_init_random sync");
+        (void)hipFree(tmp);
+        if (st != MK_OK)
+            return st;
+    }
+    return MK_OK;
+}
+
+mk_status mk_vae_load_safetensors(mk_vae* v, const char* path, uint64_t* loaded)
+{
+    if (!v || !path)
+        return fail(MK_ERR_ARG, "vae_load_safetensors: null");
+    mk_st* st = nullptr;
+    MK_TRY(mk_st_open(path, &st));
+    std::unique_ptr<mk_st, mk_status (*)(mk_st*)> hold(st, mk_st_close);
+    uint64_t count = 0;
+    for (const auto& [name, s] : v->slots) {
+        mk_st_tensor t;
+        if (mk_st_find(st, name.c_str(), &t) != MK_OK)
+            return fail(MK_ERR_ARG, "vae_load_safetensors: the checkpoint has no tensor " + name);
+        if (t.dtype != MK_F32 && t.dtype != MK_BF16 && t.dtype != MK_F16)
+            return fail(MK_ERR_ARG, "vae_load_safetensors: " + name + " has dtype " + t.dtype_name);
+        std::vector<uint8_t> raw(t.bytes);
+        if (!st_read(st, t, raw.data(), t.bytes, 0))
+            return fail(MK_ERR_ARG, "vae_load_safetensors: cannot read " + name);
+        const uint64_t n = t.bytes / (t.dtype == MK_F32 ? 4 : 2);
+        std::vector<float> f(n);
+        for (uint64_t i = 0; i < n; ++i) {
+            if (t.dtype == MK_F32) {
+                std::memcpy(&f[i], &raw[4 * i], 4);
+            } else {
+                uint16_t h;
+                std::memcpy(&h, &raw[2 * i], 2);
+                if (t.dtype == MK_BF16) {
+                    f[i] = bf2f_bits(h);
+                } else {
+                    const int e = (h >> 10) & 31, m = h & 1023;
+                    const float a = e == 0 ? std::ldexp(float(m), -24)
+                                    : e == 31 ? (m ? NAN : INFINITY)
+                                              : std::ldexp(float(1024 + m), e - 25);
+                    f[i] = h & 0x8000 ? -a : a;
+                }
+            }
+        }
+        int64_t dims[MK_ST_MAX_DIMS];
+        for (uint32_t i = 0; i < t.ndim; ++i)
+            dims[i] = int64_t(t.dims[t.ndim - 1 - i]); // back to PyTorch order
+        MK_TRY(mk_vae_load(v, name.c_str(), f.data(), dims, t.ndim));
+        ++count;
+    }
+    if (loaded)
+        *loaded = count;
+    return MK_OK;
+}
+
+mk_status mk_vae_decode_device(mk_vae* v, const float* tokens, uint32_t h, uint32_t w, float* rgba)
+{
+    if (!v || !tokens || !rgba)
+        return fail(MK_ERR_ARG, "vae_decode: null");
+    if (!h || !w || uint64_t(h) * w > (uint64_t(1) << 20))
+        return fail(MK_ERR_ARG, "vae_decode: a grid of 1 .. 2^20 tokens");
+    return v->decode(tokens, h, w, rgba);
+}
+
+mk_status mk_vae_decode(mk_vae* v, const float* tokens, size_t n, uint32_t h, uint32_t w, float* rgba)
+{
+    if (!v || !tokens || !rgba)
+        return fail(MK_ERR_ARG, "vae_decode: null");
+    if (n != uint64_t(h) * w * 4 * v->z)
+        return fail(MK_ERR_ARG, "vae_decode: latents must be [h * w][" + std::to_string(4 * v->z) + "]");
+    if (!h || !w || uint64_t(h) * w > (uint64_t(1) << 20))
+        return fail(MK_ERR_ARG, "vae_decode: a grid of 1 .. 2^20 tokens");
+    const uint64_t out_n = uint64_t(16) * h * 16 * w * 4;
+    MK_TRY(v->ensure(v->tok, n * 4));
+    MK_TRY(v->ensure(v->rgba, out_n * 4));
+    MK_HIP(hipMemcpyAsync(v->tok.p, tokens, n * 4, hipMemcpyHostToDevice, v->stream));
+    MK_TRY(v->decode(static_cast<float*>(v->tok.p), h, w, static_cast<float*>(v->rgba.p)));
+    MK_HIP(hipMemcpyAsync(rgba, v->rgba.p, out_n * 4, hipMemcpyDeviceToHost, v->stream));
+    MK_HIP(hipStreamSynchronize(v->stream));
+    return MK_OK;
+}
+
+mk_status mk_vae_set_probe(mk_vae* v, mk_probe_fn fn, void* user)
+{
+    if (!v)
+        return fail(MK_ERR_ARG, "vae_set_probe: null");
+    v->probe = fn;
+    v->probe_user = user;
+    return MK_OK;
+}
+
+mk_status mk_vae_stream(mk_vae* v, void** stream)
+{
+    if (!v || !stream)
+        return fail(MK_ERR_ARG, "vae_stream: null");
+    *stream = v->stream;
+    return MK_OK;
+}
+
+} // extern "C"

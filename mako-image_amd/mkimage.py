@@ -54,6 +54,15 @@ class StTensor(C.Structure):
                 ("dims", _u64 * 8), ("file", _u32), ("offset", _u64), ("bytes", _u64)]
 
 
+class ConvArgs(C.Structure):
+    _fields_ = [("x", _vp), ("w", _vp), ("bias", _vp), ("y", _vp), ("h", _u32), ("width", _u32), ("c", _u32),
+                ("n", _u32), ("ldy", _i64), ("y_dtype", _u32), ("epilogue", _u32)]
+
+
+class VaeConfig(C.Structure):
+    _fields_ = [("base", _u32), ("z", _u32), ("mean", _fp), ("std", _fp)]
+
+
 PROBE = C.CFUNCTYPE(None, _vp, C.c_char_p, _i, _fp, _sz)
 
 _SIGS = {
@@ -128,6 +137,16 @@ _SIGS = {
     "mk_engine_tensor_at": (_i, [_vp, _sz, C.POINTER(C.c_char_p), C.POINTER(_u32), C.POINTER(_u64),
                                  C.POINTER(_u64)]),
     "mk_engine_fetch": (_i, [_vp, C.c_char_p, _vp, _sz]),
+    "mk_conv3x3": (_i, [C.POINTER(ConvArgs), _vp]),
+    "mk_vae_create": (_i, [C.POINTER(VaeConfig), C.POINTER(_vp)]),
+    "mk_vae_destroy": (_i, [_vp]),
+    "mk_vae_load": (_i, [_vp, C.c_char_p, _vp, C.POINTER(_i64), _u32]),
+    "mk_vae_load_safetensors": (_i, [_vp, C.c_char_p, C.POINTER(_u64)]),
+    "mk_vae_init_random": (_i, [_vp, _u64]),
+    "mk_vae_decode": (_i, [_vp, _vp, _sz, _u32, _u32, _vp]),
+    "mk_vae_decode_device": (_i, [_vp, _vp, _u32, _u32, _vp]),
+    "mk_vae_stream": (_i, [_vp, C.POINTER(_vp)]),
+    "mk_vae_set_probe": (_i, [_vp, PROBE, _vp]),
 }
 
 EXPORTS = tuple(_SIGS)
@@ -311,6 +330,67 @@ class SafeTensors:
         buf = np.empty(info["bytes"], dtype=np.uint8)
         call("mk_st_read", self.h, name.encode(), buf.ctypes.data, buf.nbytes)
         return buf
+
+
+class Vae:
+    """The VAE decoder (mk_vae_*): tokens [h * w][4 z] -> RGBA [16 h][16 w][4]."""
+
+    def __init__(self, base=96, z=16, mean=None, std=None):
+        self.z = z
+        self._mean = np.ascontiguousarray(np.zeros(z) if mean is None else mean, dtype=np.float32)
+        self._std = np.ascontiguousarray(np.ones(z) if std is None else std, dtype=np.float32)
+        cfg = VaeConfig(base, z, self._mean.ctypes.data_as(_fp), self._std.ctypes.data_as(_fp))
+        p = _vp()
+        call("mk_vae_create", C.byref(cfg), C.byref(p))
+        self.h = p.value
+        self._probe_cb = None
+
+    def close(self):
+        if getattr(self, "h", None) and _lib is not None:
+            _lib.mk_vae_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def init_random(self, seed):
+        call("mk_vae_init_random", self.h, seed)
+
+    def load(self, name, array):
+        a = np.ascontiguousarray(array, dtype=np.float32)
+        dims = (_i64 * max(a.ndim, 1))(*a.shape)
+        call("mk_vae_load", self.h, name.encode(), a.ctypes.data, dims, a.ndim)
+
+    def load_safetensors(self, path):
+        n = _u64()
+        call("mk_vae_load_safetensors", self.h, str(path).encode(), C.byref(n))
+        return n.value
+
+    def decode(self, tokens, h, w):
+        t = np.ascontiguousarray(tokens, dtype=np.float32)
+        out = np.empty((16 * h, 16 * w, 4), dtype=np.float32)
+        call("mk_vae_decode", self.h, t.ctypes.data, t.size, h, w, out.ctypes.data)
+        return out
+
+    def decode_device(self, tokens_dev, h, w, rgba_dev):
+        call("mk_vae_decode_device", self.h, int(tokens_dev), h, w, int(rgba_dev))
+
+    def stream(self):
+        s = _vp()
+        call("mk_vae_stream", self.h, C.byref(s))
+        return s.value
+
+    def set_probe(self, probes):
+        if probes is None:
+            self._probe_cb = None
+            call("mk_vae_set_probe", self.h, PROBE(), None)
+            return
+
+        def cb(_u, name, layer, data, n):
+            probes[(name.decode(), layer)] = np.ctypeslib.as_array(data, shape=(n,)).copy()
+
+        self._probe_cb = PROBE(cb)
+        call("mk_vae_set_probe", self.h, self._probe_cb, None)
 
 
 class Engine:

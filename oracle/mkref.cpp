@@ -1025,3 +1025,297 @@ int mkref_sdxl_trans(const mkref_model* mp, const float* x, int64_t n, const flo
 }
 
 } // extern "C"
+
+// =====================================================================================================================
+// VAE decoder: src/image/engine.cpp:589-628 (the weights it loads), 722-746 (norm_silu, res_block), 748-777
+// (vae_attention), 862-954 (decode: latent denormalisation over 2x2 patches, post_quant_conv, conv_in, mid block,
+// up blocks with nearest 2x upsampling, norm_out + SiLU, conv_out, clamp to [-1, 1], alpha 1). Images are
+// [pixels][channels] fp32; every conv input is rounded to bf16 (the device feeds bf16 to its matrix cores), sums in
+// double. The RMS norm is x / sqrt(sum x^2 + 1e-24) * sqrt(c) * gamma (engine.cpp:725-727).
+// =====================================================================================================================
+
+struct mkref_vae {
+    uint32_t base = 0, z = 0;
+    std::vector<float> mean, std_;
+    std::vector<std::string> names;
+    std::map<std::string, std::pair<std::vector<float>, std::vector<int64_t>>> t;
+    const std::vector<float>& w(const std::string& n) const { return t.at(n).first; }
+    int64_t dim(const std::string& n, int i) const { return t.at(n).second[size_t(i)]; }
+};
+
+namespace {
+
+struct Img {
+    uint32_t h = 0, w = 0, c = 0;
+    std::vector<float> v;
+    Img() = default;
+    Img(uint32_t h_, uint32_t w_, uint32_t c_) : h(h_), w(w_), c(c_), v(size_t(h_) * w_ * c_) {}
+};
+
+void vae_add(mkref_vae* m, const std::string& name, std::vector<int64_t> dims, uint64_t seed)
+{
+    size_t n = 1;
+    for (int64_t d : dims)
+        n *= size_t(d);
+    std::vector<float> v(n);
+    const uint64_t key = mkref_tensor_key(seed, name.c_str());
+    const bool conv = dims.size() == 4, gamma = name.size() > 6 && name.compare(name.size() - 6, 6, ".gamma") == 0;
+    if (conv)
+        mkref_fill_normal(v.data(), n, key, 0.0, 1.0 / std::sqrt(double(dims[1] * dims[2] * dims[3])), 1);
+    else
+        mkref_fill_normal(v.data(), n, key, gamma ? 1.0 : 0.0, gamma ? 0.1 : 0.02, 0);
+    m->names.push_back(name);
+    m->t[name] = {std::move(v), std::move(dims)};
+}
+
+// y = conv(bf16(x)) + bias, k = 1 or 3, zero padding; or y += that (accumulate).
+void vae_conv(const mkref_vae* m, const std::string& p, const Img& x, Img& y, bool accumulate)
+{
+    const std::vector<float>& W = m->w(p + ".weight");
+    const std::vector<float>& b = m->w(p + ".bias");
+    const int64_t co = m->dim(p + ".weight", 0), ci = m->dim(p + ".weight", 1), k = m->dim(p + ".weight", 2);
+    if (ci != x.c)
+        throw std::runtime_error("vae_conv: channels");
+    std::vector<float> xb(x.v);
+    mkref_round_bf16(xb.data(), xb.size());
+    if (!accumulate)
+        y = Img(x.h, x.w, uint32_t(co));
+    const int H = int(x.h), Wd = int(x.w), r = int(k / 2);
+#pragma omp parallel for schedule(static)
+    for (int yy = 0; yy < H; ++yy)
+        for (int xx = 0; xx < Wd; ++xx)
+            for (int64_t o = 0; o < co; ++o) {
+                double acc = 0.0;
+                for (int dy = 0; dy < k; ++dy) {
+                    const int sy = yy + dy - r;
+                    if (sy < 0 || sy >= H)
+                        continue;
+                    for (int dx = 0; dx < k; ++dx) {
+                        const int sx = xx + dx - r;
+                        if (sx < 0 || sx >= Wd)
+                            continue;
+                        const float* xp = &xb[(size_t(sy) * Wd + sx) * size_t(ci)];
+                        const float* wp = &W[size_t(o) * ci * k * k + size_t(dy) * k + dx];
+                        for (int64_t c = 0; c < ci; ++c)
+                            acc += double(xp[c]) * wp[size_t(c) * k * k];
+                    }
+                }
+                float& out = y.v[(size_t(yy) * Wd + xx) * size_t(co) + o];
+                const float v = float(acc) + b[size_t(o)];
+                out = accumulate ? out + v : v;
+            }
+}
+
+// RMS norm over each pixel's channels with gamma, then SiLU (silu = true); the result as bf16 values.
+Img vae_norm(const Img& x, const std::vector<float>& g, bool silu)
+{
+    Img y(x.h, x.w, x.c);
+    const size_t px = size_t(x.h) * x.w;
+#pragma omp parallel for schedule(static)
+    for (size_t i = 0; i < px; ++i) {
+        const float* a = &x.v[i * x.c];
+        double ss = 0.0;
+        for (uint32_t c = 0; c < x.c; ++c)
+            ss += double(a[c]) * a[c];
+        const float r = float(1.0 / std::sqrt(ss / x.c + 1e-24 / x.c));
+        for (uint32_t c = 0; c < x.c; ++c) {
+            float v = a[c] * r * g[c];
+            if (silu)
+                v = v / (1.0f + std::exp(-v));
+            y.v[i * x.c + c] = bf16(v);
+        }
+    }
+    return y;
+}
+
+void vae_res(const mkref_vae* m, const std::string& p, Img& x)
+{
+    Img h1, h2;
+    vae_conv(m, p + ".conv1", vae_norm(x, m->w(p + ".norm1.gamma"), true), h1, false);
+    Img y;
+    if (m->t.count(p + ".conv_shortcut.weight"))
+        vae_conv(m, p + ".conv_shortcut", x, y, false);
+    else
+        y = x;
+    vae_conv(m, p + ".conv2", vae_norm(h1, m->w(p + ".norm2.gamma"), true), y, true);
+    x = std::move(y);
+}
+
+// One-head attention over the pixels (engine.cpp:748-777): q, k, v from the 1x1 to_qkv conv of the normed image,
+// softmax(q k^T / sqrt(c)) v with q, k, v and P rounded to bf16, then proj and the residual.
+void vae_attn(const mkref_vae* m, Img& x)
+{
+    const std::string a = "decoder.mid_block.attentions.0.";
+    const uint32_t n = x.h * x.w, c = x.c;
+    Img xn = vae_norm(x, m->w(a + "norm.gamma"), false);
+    Img qkv;
+    vae_conv(m, a + "to_qkv", xn, qkv, false);
+    mkref_round_bf16(qkv.v.data(), qkv.v.size());
+    // the value bias is added after the weighted sum (the weights of a row sum to 1)
+    const std::vector<float>& bq = m->w(a + "to_qkv.bias");
+    std::vector<float> vraw(size_t(n) * c);
+    {
+        // v without its bias, rounded to bf16 as the device stores V^T
+        const std::vector<float>& W = m->w(a + "to_qkv.weight");
+        for (uint32_t i = 0; i < n; ++i)
+            for (uint32_t o = 0; o < c; ++o) {
+                double acc = 0.0;
+                for (uint32_t k = 0; k < c; ++k)
+                    acc += double(xn.v[size_t(i) * c + k]) * W[size_t(2 * c + o) * c + k];
+                vraw[size_t(i) * c + o] = bf16(float(acc));
+            }
+    }
+    Img o(x.h, x.w, c);
+    const double scale = 1.0 / std::sqrt(double(c));
+#pragma omp parallel for schedule(dynamic)
+    for (uint32_t i = 0; i < n; ++i) {
+        std::vector<double> s(n);
+        double mx = -1e300;
+        for (uint32_t j = 0; j < n; ++j) {
+            double acc = 0.0;
+            for (uint32_t k = 0; k < c; ++k)
+                acc += double(qkv.v[size_t(i) * 3 * c + k]) * qkv.v[size_t(j) * 3 * c + c + k];
+            s[j] = float(acc);
+            mx = std::max(mx, s[j]);
+        }
+        double sum = 0.0;
+        for (uint32_t j = 0; j < n; ++j)
+            sum += (s[j] = std::exp((s[j] - mx) * scale));
+        for (uint32_t k = 0; k < c; ++k) {
+            double acc = 0.0;
+            for (uint32_t j = 0; j < n; ++j)
+                acc += double(bf16(float(s[j] / sum))) * vraw[size_t(j) * c + k];
+            o.v[size_t(i) * c + k] = bf16(float(acc) + bq[2 * c + k]);
+        }
+    }
+    vae_conv(m, a + "proj", o, x, true);
+}
+
+Img vae_up2(const Img& x)
+{
+    Img y(2 * x.h, 2 * x.w, x.c);
+    for (uint32_t yy = 0; yy < y.h; ++yy)
+        for (uint32_t xx = 0; xx < y.w; ++xx)
+            std::memcpy(&y.v[(size_t(yy) * y.w + xx) * x.c], &x.v[(size_t(yy / 2) * x.w + xx / 2) * x.c],
+                        x.c * sizeof(float));
+    return y;
+}
+
+} // namespace
+
+mkref_vae* mkref_vae_create(uint32_t base, uint32_t z, uint64_t seed, const float* mean, const float* std)
+{
+    if (!base || !z || !mean || !std)
+        return nullptr;
+    auto m = new mkref_vae;
+    m->base = base;
+    m->z = z;
+    m->mean.assign(mean, mean + z);
+    m->std_.assign(std, std + z);
+    const int64_t b = base, d0 = 4 * b;
+    auto conv = [&](const std::string& p, int64_t co, int64_t ci, int64_t k) {
+        vae_add(m, p + ".weight", {co, ci, k, k}, seed);
+        vae_add(m, p + ".bias", {co}, seed);
+    };
+    auto res = [&](const std::string& p, int64_t ci, int64_t co) {
+        vae_add(m, p + ".norm1.gamma", {ci}, seed);
+        conv(p + ".conv1", co, ci, 3);
+        vae_add(m, p + ".norm2.gamma", {co}, seed);
+        conv(p + ".conv2", co, co, 3);
+        if (ci != co)
+            conv(p + ".conv_shortcut", co, ci, 1);
+    };
+    conv("post_quant_conv", z, z, 1);
+    conv("decoder.conv_in", d0, z, 3);
+    res("decoder.mid_block.resnets.0", d0, d0);
+    vae_add(m, "decoder.mid_block.attentions.0.norm.gamma", {d0}, seed);
+    conv("decoder.mid_block.attentions.0.to_qkv", 3 * d0, d0, 1);
+    conv("decoder.mid_block.attentions.0.proj", d0, d0, 1);
+    res("decoder.mid_block.resnets.1", d0, d0);
+    const int64_t ins[4] = {4 * b, 2 * b, 2 * b, b}, outs[4] = {4 * b, 4 * b, 2 * b, b};
+    for (int i = 0; i < 4; ++i) {
+        const std::string p = "decoder.up_blocks." + std::to_string(i);
+        for (int j = 0; j < 3; ++j)
+            res(p + ".resnets." + std::to_string(j), j ? outs[i] : ins[i], outs[i]);
+        if (i < 3)
+            conv(p + ".upsamplers.0.resample.1", outs[i] / 2, outs[i], 3);
+    }
+    vae_add(m, "decoder.norm_out.gamma", {b}, seed);
+    conv("decoder.conv_out", 3, b, 3);
+    return m;
+}
+
+void mkref_vae_destroy(mkref_vae* v) { delete v; }
+size_t mkref_vae_count(const mkref_vae* v) { return v->names.size(); }
+const char* mkref_vae_name(const mkref_vae* v, size_t i) { return v->names[i].c_str(); }
+
+const float* mkref_vae_tensor(const mkref_vae* v, size_t i, uint32_t* ndim, int64_t* dims)
+{
+    const auto& e = v->t.at(v->names[i]);
+    *ndim = uint32_t(e.second.size());
+    for (size_t k = 0; k < e.second.size(); ++k)
+        dims[k] = e.second[k];
+    return e.first.data();
+}
+
+int mkref_vae_decode(const mkref_vae* m, const float* tokens, uint32_t h, uint32_t w, float* rgba,
+                     mkref_probe_fn probe, void* user)
+{
+    try {
+        const uint32_t z = m->z, L = 4 * z;
+        auto pr = [&](const char* n, int layer, const Img& x) {
+            if (probe)
+                probe(user, n, layer, x.v.data(), x.v.size());
+        };
+        // tokens -> the latent image (2h x 2w x z): value (c * 2 + py) * 2 + px of token (y, x) is channel c of
+        // pixel (2y + py, 2x + px), denormalised by the channel's mean and deviation (engine.cpp:887-898)
+        Img lat(2 * h, 2 * w, z);
+        for (uint32_t y = 0; y < h; ++y)
+            for (uint32_t x = 0; x < w; ++x)
+                for (uint32_t c = 0; c < z; ++c)
+                    for (uint32_t py = 0; py < 2; ++py)
+                        for (uint32_t px = 0; px < 2; ++px)
+                            lat.v[((size_t(2 * y + py)) * 2 * w + 2 * x + px) * z + c] =
+                                tokens[(size_t(y) * w + x) * L + (c * 2 + py) * 2 + px] * m->std_[c] + m->mean[c];
+        // post_quant_conv in fp32 (the device applies it while unpacking the tokens), then conv_in
+        Img pq(lat.h, lat.w, z);
+        {
+            const std::vector<float>& W = m->w("post_quant_conv.weight");
+            const std::vector<float>& b = m->w("post_quant_conv.bias");
+            for (size_t i = 0; i < size_t(lat.h) * lat.w; ++i)
+                for (uint32_t o = 0; o < z; ++o) {
+                    double acc = 0.0;
+                    for (uint32_t c = 0; c < z; ++c)
+                        acc += double(lat.v[i * z + c]) * W[size_t(o) * z + c];
+                    pq.v[i * z + o] = float(acc) + b[o];
+                }
+        }
+        Img x;
+        vae_conv(m, "decoder.conv_in", pq, x, false);
+        pr("vae_conv_in", -1, x);
+        vae_res(m, "decoder.mid_block.resnets.0", x);
+        vae_attn(m, x);
+        vae_res(m, "decoder.mid_block.resnets.1", x);
+        pr("vae_mid", -1, x);
+        for (int i = 0; i < 4; ++i) {
+            const std::string p = "decoder.up_blocks." + std::to_string(i);
+            for (int j = 0; j < 3; ++j)
+                vae_res(m, p + ".resnets." + std::to_string(j), x);
+            if (i < 3) {
+                Img y;
+                vae_conv(m, p + ".upsamplers.0.resample.1", vae_up2(x), y, false);
+                x = std::move(y);
+            }
+            pr("vae_up", i, x);
+        }
+        Img o;
+        vae_conv(m, "decoder.conv_out", vae_norm(x, m->w("decoder.norm_out.gamma"), true), o, false);
+        pr("vae_out", -1, o);
+        for (size_t i = 0; i < size_t(o.h) * o.w; ++i)
+            for (uint32_t c = 0; c < 4; ++c)
+                rgba[i * 4 + c] = c < 3 ? std::min(1.0f, std::max(-1.0f, o.v[i * 3 + c])) : 1.0f;
+        return 0;
+    } catch (...) {
+        return 1;
+    }
+}

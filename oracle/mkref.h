@@ -125,6 +125,23 @@ int mkref_sdxl_trans(const mkref_model* m, const float* x, int64_t n, const floa
 int mkref_dual_block(const mkref_model* m, int block, float* img, int64_t N, float* txt, int64_t S,
                      const float* mod_img, const float* mod_txt, const float* cs);
 
+/* ---- VAE decoder (Qwen-Image's Wan-2.1-layout decoder as src/image/engine.cpp:589-628, 722-760, 862-954 runs it, one
+ * frame): tokens [h][w][4 z] -> RGBA [16 h][16 w][4] in [-1, 1], alpha 1. Channels base x {4, 4, 4, 2, 1} per level
+ * (decoder dims 4b, then up blocks 4b -> 4b, 2b -> 4b, 2b -> 2b, b -> b, each 3 residual blocks, the first three
+ * followed by a nearest 2x upsample and a 3x3 conv to half the channels), RMS norms over channels, one-head attention
+ * in the middle block. Weights by checkpoint name from the counter RNG (PyTorch layout [out][in][k][k]): convs
+ * N(0, 1 / fan_in) as bf16, biases N(0, 0.02), norm gammas 1 + N(0, 0.1). ---- */
+typedef struct mkref_vae mkref_vae;
+mkref_vae* mkref_vae_create(uint32_t base, uint32_t z, uint64_t seed, const float* mean, const float* std);
+void mkref_vae_destroy(mkref_vae* v);
+size_t mkref_vae_count(const mkref_vae* v);
+const char* mkref_vae_name(const mkref_vae* v, size_t i);
+/* tensor i's values and dims (PyTorch order: [out][in][k][k] for convs, [n] otherwise) */
+const float* mkref_vae_tensor(const mkref_vae* v, size_t i, uint32_t* ndim, int64_t* dims);
+/* probes: "vae_conv_in", "vae_mid", "vae_up" (layer = up block) as [pixels][channels], "vae_out" before the clamp */
+int mkref_vae_decode(const mkref_vae* v, const float* tokens, uint32_t h, uint32_t w, float* rgba,
+                     mkref_probe_fn probe, void* user);
+
 int mkref_threads(void);
 
 #ifdef __cplusplus

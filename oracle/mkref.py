@@ -57,6 +57,16 @@ def lib():
                                             _I64]
         L.mkref_attention.argtypes = [_F, _F, _F, _I64, _I64, _I64, _I64, _I64, C.c_float, C.c_uint32, C.c_uint32,
                                       _F]
+        L.mkref_vae_create.restype = C.c_void_p
+        L.mkref_vae_create.argtypes = [C.c_uint32, C.c_uint32, C.c_uint64, _F, _F]
+        L.mkref_vae_destroy.argtypes = [C.c_void_p]
+        L.mkref_vae_count.restype = C.c_size_t
+        L.mkref_vae_count.argtypes = [C.c_void_p]
+        L.mkref_vae_name.restype = C.c_char_p
+        L.mkref_vae_name.argtypes = [C.c_void_p, C.c_size_t]
+        L.mkref_vae_tensor.restype = _F
+        L.mkref_vae_tensor.argtypes = [C.c_void_p, C.c_size_t, C.POINTER(C.c_uint32), C.POINTER(C.c_int64)]
+        L.mkref_vae_decode.argtypes = [C.c_void_p, _F, C.c_uint32, C.c_uint32, _F, C.c_void_p, C.c_void_p]
         L.mkref_gelu_tanh.argtypes = [_F, C.c_size_t]
         L.mkref_silu.argtypes = [_F, C.c_size_t]
         L.mkref_swiglu.argtypes = [_F, _I64, _I64, _F]
@@ -359,6 +369,46 @@ class Model:
                                     fp(f32(mod_txt)), fp(f32(cs)))
         if rc:
             raise RuntimeError("mkref_dual_block failed")
+
+
+class Vae:
+    """The VAE decoder (src/image/engine.cpp:862-954) with counter-RNG weights by checkpoint name."""
+
+    def __init__(self, base, z=16, seed=0, mean=None, std=None):
+        self.base, self.z = base, z
+        self.mean = f32(np.zeros(z) if mean is None else mean)
+        self.std = f32(np.ones(z) if std is None else std)
+        self.h = lib().mkref_vae_create(base, z, seed, fp(self.mean), fp(self.std))
+        if not self.h:
+            raise ValueError("bad VAE configuration")
+
+    def __del__(self):
+        if getattr(self, "h", None) and _lib is not None:
+            _lib.mkref_vae_destroy(self.h)
+            self.h = None
+
+    def tensors(self):
+        """Yields (name, float32 array in PyTorch layout)."""
+        L = lib()
+        for i in range(L.mkref_vae_count(self.h)):
+            nd, dims = C.c_uint32(), (C.c_int64 * 4)()
+            p = L.mkref_vae_tensor(self.h, i, C.byref(nd), dims)
+            shape = tuple(dims[k] for k in range(nd.value))
+            yield L.mkref_vae_name(self.h, i).decode(), np.ctypeslib.as_array(p, shape=(int(np.prod(shape)),)).copy(
+            ).reshape(shape)
+
+    def decode(self, tokens, h, w, probes=None):
+        tokens = f32(tokens)
+        out = np.empty((16 * h, 16 * w, 4), dtype=np.float32)
+        cb = None
+        if probes is not None:
+            def _cb(_u, name, layer, data, n):
+                probes[(name.decode(), layer)] = np.ctypeslib.as_array(data, shape=(n,)).copy()
+            cb = PROBE(_cb)
+        rc = lib().mkref_vae_decode(self.h, fp(tokens), h, w, fp(out), C.cast(cb, C.c_void_p) if cb else None, None)
+        if rc:
+            raise RuntimeError("mkref_vae_decode failed")
+        return out
 
 
 def diff(got, want, width):

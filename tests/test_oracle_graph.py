@@ -226,3 +226,71 @@ def test_sdxl_trans_matches_torch():
     x = rng.standard_normal((40, 128)).astype(np.float32)
     ctx = rng.standard_normal((11, 192)).astype(np.float32)
     agree(m.sdxl_trans(x, ctx), sdxl_reference(m, dims, x, ctx))
+
+
+# ---- VAE decoder (src/image/engine.cpp:862-954), written in the idiom of the public Wan-2.1 decoder: conv2d with
+# padding 1, RMS norm over channels, nearest interpolation, one-head scaled_dot_product_attention ----
+
+def vae_reference(vae, tokens, h, w):
+    t = {n: torch.from_numpy(a).double() for n, a in vae.tensors()}
+    z = vae.z
+
+    def conv(x, name):  # x [1][c][H][W]; the conv input rounded to bf16
+        W = t[name + ".weight"]
+        return F.conv2d(bf(x), W, t[name + ".bias"], padding=W.shape[-1] // 2)
+
+    def rms(x, g, silu=True):
+        c = x.shape[1]
+        y = x / torch.sqrt((x * x).sum(1, keepdim=True) + 1e-24) * (c ** 0.5) * g[None, :, None, None]
+        return bf(F.silu(y) if silu else y)
+
+    def res(x, p):
+        hh = conv(rms(x, t[p + ".norm1.gamma"]), p + ".conv1")
+        hh = conv(rms(hh, t[p + ".norm2.gamma"]), p + ".conv2")
+        return hh + (conv(x, p + ".conv_shortcut") if p + ".conv_shortcut.weight" in t else x)
+
+    def attn(x):
+        a = "decoder.mid_block.attentions.0."
+        _, c, H, W_ = x.shape
+        xn = rms(x, t[a + "norm.gamma"], silu=False)
+        Wq = t[a + "to_qkv.weight"][:, :, 0, 0]
+        bq = t[a + "to_qkv.bias"]
+        seq = xn.flatten(2).transpose(1, 2)[0]  # [n][c]
+        q = bf(F.linear(seq, Wq[:c], bq[:c]))
+        k = bf(F.linear(seq, Wq[c:2 * c], bq[c:2 * c]))
+        v = bf(F.linear(seq, Wq[2 * c:]))  # the value bias joins after the weighted sum
+        p = bf(torch.softmax((q @ k.T).float().double() / c ** 0.5, dim=-1))  # scores fp32, P bf16
+        o = bf(p @ v + bq[2 * c:])
+        o = o.T.reshape(1, c, H, W_)
+        return x + conv(o, a + "proj")
+
+    tok = torch.from_numpy(np.asarray(tokens, np.float64)).reshape(h, w, z, 2, 2)
+    lat = tok.permute(2, 0, 3, 1, 4).reshape(1, z, 2 * h, 2 * w)  # channel c of pixel (2y + py, 2x + px)
+    lat = lat * torch.from_numpy(vae.std).double()[None, :, None, None] + \
+        torch.from_numpy(vae.mean).double()[None, :, None, None]
+    Wp = t["post_quant_conv.weight"]
+    x = F.conv2d(lat, Wp, t["post_quant_conv.bias"])  # fp32 on both sides, no bf16 rounding of its input
+    x = conv(x, "decoder.conv_in")
+    x = res(x, "decoder.mid_block.resnets.0")
+    x = attn(x)
+    x = res(x, "decoder.mid_block.resnets.1")
+    for i in range(4):
+        p = f"decoder.up_blocks.{i}"
+        for j in range(3):
+            x = res(x, f"{p}.resnets.{j}")
+        if i < 3:
+            x = conv(F.interpolate(x, scale_factor=2, mode="nearest"), f"{p}.upsamplers.0.resample.1")
+    x = conv(rms(x, t["decoder.norm_out.gamma"]), "decoder.conv_out")
+    rgb = x[0].permute(1, 2, 0).clamp(-1, 1)
+    return torch.cat([rgb, torch.ones_like(rgb[..., :1])], -1).numpy()
+
+
+@pytest.mark.parametrize("h, w", [(2, 2), (2, 3)])
+def test_vae_decode_matches_torch(h, w):
+    rng = np.random.default_rng(7)
+    vae = R.Vae(16, seed=3, mean=rng.standard_normal(16) * 0.1, std=1 + rng.random(16))
+    tokens = rng.standard_normal((h * w, 64)).astype(np.float32)
+    got = vae.decode(tokens, h, w)
+    want = vae_reference(vae, tokens, h, w)
+    assert got.shape == (16 * h, 16 * w, 4) and np.all(got[..., 3] == 1)
+    agree(got[..., :3], want[..., :3])
