@@ -41,6 +41,104 @@ SDXL_CTX, SDXL_CTX_DIM = 77, 2048
 SDXL_METRIC = "s/SDXL spatial-transformer pass 1024² bf16 (stage A depth 2 + stage B depth 10, CFG batch 2)"
 
 
+# Qwen-Image's VAE decoder (Wan-2.1 layout, base 96, 16 latent channels) on the step's 64 x 64 tokens: a 1024x1024 image
+VAE_BASE, VAE_Z, VAE_SIDE = 96, 16, 64
+VAE_METRIC = "s/VAE decode 1024² bf16 (Qwen-Image decoder, base 96, one frame); conv+attention % of MFMA peak"
+
+
+def vae_flops(th, tw, b=VAE_BASE, z=VAE_Z):
+    """Algorithmic FLOPs of one decode (engine.cpp:862-954; channel padding excluded): 2 k^2 ci co per pixel of each
+    conv, 4 n^2 c for the mid block's attention over its n pixels, 2 n c (3c + c) for its 1x1 projections."""
+    H, W = 2 * th, 2 * tw
+    conv = lambda px, ci, co, k=3: 2 * px * k * k * ci * co
+    n, d0 = H * W, 4 * b
+    f = conv(n, z, z, 1) + conv(n, z, d0)
+    res = lambda px, ci, co: conv(px, ci, co) + conv(px, co, co) + (conv(px, ci, co, 1) if ci != co else 0)
+    f += 2 * res(n, d0, d0)
+    attn = 4 * n * n * d0
+    f += attn + 2 * n * d0 * 4 * d0
+    ins, outs = (4 * b, 2 * b, 2 * b, b), (4 * b, 4 * b, 2 * b, b)
+    px = n
+    for i in range(4):
+        f += res(px, ins[i], outs[i]) + 2 * res(px, outs[i], outs[i])
+        if i < 3:
+            px *= 4
+            f += conv(px, outs[i], outs[i] // 2)
+    f += conv(px, b, 3)
+    return f, attn
+
+
+def bench_vae(args):
+    """The VAE workload: one decode of 64 x 64 tokens to a 1024x1024 image (random-init weights, N(0,1) tokens resident
+    on the device), timed with HIP events on the decoder's stream."""
+    import numpy as np
+
+    import mkimage as M
+
+    M.call("mk_set_device", 0)
+    rng = np.random.default_rng(0)
+    vae = M.Vae(VAE_BASE, VAE_Z, mean=rng.standard_normal(VAE_Z) * 0.5, std=1.0 + rng.random(VAE_Z))
+    vae.init_random(0)
+    th = tw = VAE_SIDE
+    tok = M.Dev.from_array(rng.standard_normal((th * tw, 4 * VAE_Z)).astype(np.float32))
+    out = M.Dev(16 * th * 16 * tw * 4 * 4)
+    stream = vae.stream()
+    for _ in range(args.warmup):
+        vae.decode_device(tok, th, tw, out)
+    M.call("mk_stream_synchronize", stream)
+    e0, e1 = M.Event(), M.Event()
+    e0.record(stream)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        vae.decode_device(tok, th, tw, out)
+    e1.record(stream)
+    M.call("mk_stream_synchronize", stream)
+    wall = (time.perf_counter() - t0) / args.steps
+    sec = e0.elapsed_ms(e1) / 1e3 / args.steps
+    img = out.to_array(np.float32, (16 * th, 16 * tw, 4))
+    if not np.isfinite(img).all():
+        raise RuntimeError("non-finite VAE output")
+    fl, fa = vae_flops(th, tw)
+    line = {
+        "metric": VAE_METRIC, "value": round(sec, 5), "unit": "s/decode", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(sec * 1e3, 3), "higher_is_better": False, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (random-init weights N(0, 1/fan_in), N(0,1) tokens)",
+        "config": {"workload": "Qwen-Image VAE decoder (Wan 2.1 layout), 64x64 tokens -> 1024x1024 RGBA",
+                   "base": VAE_BASE, "z": VAE_Z, "tokens": [th, tw], "gflop": round(fl / 1e9, 1),
+                   "attention_gflop": round(fa / 1e9, 1)},
+        "roofline": {"bound": "mfma", "kernel": "whole decode (implicit-GEMM convs + attention GEMMs)",
+                     "achieved": round(fl / sec / 1e12, 1), "peak": PEAK_BF16 / 1e12, "unit": "TFLOP/s",
+                     "frac": round(fl / sec / PEAK_BF16, 4), "traffic": None},
+        "wall_ms_per_decode": round(wall * 1e3, 3),
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline_vae(args.cpu_seconds, fl)
+    print(json.dumps(line), flush=True)
+
+
+def cpu_baseline_vae(seconds_target, decode_flops):
+    """The oracle's decoder (base 96) on 4 x 4 tokens (a 64x64 image) timed on this host, scaled by FLOPs."""
+    import numpy as np
+
+    import mkref as R
+
+    v = R.Vae(VAE_BASE, VAE_Z, seed=0)
+    tok = np.random.default_rng(0).standard_normal((16, 4 * VAE_Z)).astype(np.float32)
+    flops = vae_flops(4, 4)[0]
+    reps, t_total = 0, 0.0
+    while t_total < seconds_target and reps < 50:
+        t0 = time.perf_counter()
+        v.decode(tok, 4, 4)
+        t_total += time.perf_counter() - t0
+        reps += 1
+    rate = flops * reps / t_total
+    return {"value": decode_flops / rate, "unit": "s/decode", "cores": R.lib().mkref_threads(), "kind": "port",
+            "sample": f"oracle (C++/OpenMP, double sums over bf16 weights): {reps} x a 4x4-token decode (64x64 image, "
+                      f"{flops / 1e9:.1f} GFLOP each, {t_total:.1f} s, {rate / 1e9:.1f} GFLOP/s), scaled by FLOPs to "
+                      f"the 1024x1024 decode"}
+
+
 def step_flops(blocks=60, D=3072, F=12288, N=4096, S=256, B=2, heads=24):
     """Algorithmic FLOPs of one step (the blocks' GEMMs and attention; padding excluded)."""
     T = N + S
@@ -200,14 +298,15 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--workload", choices=sorted(WORKLOADS) + ["sdxl-1024-bf16"], default="mmdit-1024-bf16")
+    ap.add_argument("--workload", choices=sorted(WORKLOADS) + ["sdxl-1024-bf16", "vae-1024-decode"],
+                    default="mmdit-1024-bf16")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
-    if args.workload == "sdxl-1024-bf16":
+    if args.workload in ("sdxl-1024-bf16", "vae-1024-decode"):
         if args.gpus != 1 or world != 1:
             print("bench.py measures one GPU: run it with --gpus 1", file=sys.stderr)
             sys.exit(2)
-        bench_sdxl(args)
+        (bench_sdxl if args.workload == "sdxl-1024-bf16" else bench_vae)(args)
         return
     wl = WORKLOADS[args.workload]
     global H, W, S

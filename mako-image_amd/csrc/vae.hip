@@ -28,6 +28,19 @@ struct GridDims {
     __host__ __device__ uint64_t grid_rows() const { return uint64_t(h + 2) * (w + 2); }
     __host__ __device__ uint64_t rows() const { return grid_rows() + 2ull * slack(); }
     __host__ __device__ uint64_t row_of(uint32_t y, uint32_t x) const { return slack() + uint64_t(y + 1) * pw() + x + 1; }
+    // the pixel of buffer row r (r < 2^32), or false for ring and slack rows: 32-bit arithmetic
+    __device__ bool pixel32(uint32_t r, uint32_t& y, uint32_t& x) const
+    {
+        const uint32_t g = r - slack();
+        if (r < slack() || g >= uint32_t(grid_rows()))
+            return false;
+        const uint32_t gy = g / pw(), gx = g - gy * pw();
+        if (gy == 0 || gy > h || gx == 0 || gx > w)
+            return false;
+        y = gy - 1;
+        x = gx - 1;
+        return true;
+    }
     // the pixel of buffer row r, or false for ring and slack rows
     __host__ __device__ bool pixel(uint64_t r, uint32_t& y, uint32_t& x) const
     {
@@ -71,107 +84,134 @@ __global__ __launch_bounds__(256) void vae_in_kernel(const float* __restrict__ t
 }
 
 // RMS norm over a pixel's c channels (x / sqrt(mean(x^2) + 1e-24 / c) * gamma, engine.cpp:725-727), then SiLU (mode
-// 0), or not (mode 1), or a plain bf16 copy (mode 2). One wave a row; x fp32 rows of stride cs; y bf16 rows of stride
-// cp. Grid output (compact = 0): every buffer row of y, ring and slack rows and channels past c zero. Compact output:
-// y row p = pixel p (y * w + x), p < rows.
+// 0), or not (mode 1), or a plain bf16 copy (mode 2). 16 lanes a row, J = cp / 64 chunks of 4 channels a lane; x fp32
+// rows of stride cs (c a multiple of 4); y bf16 rows of stride cp. Grid output (compact = 0): every buffer row of y,
+// ring and slack rows and channels past c zero. Compact output: y row p = pixel p (y * w + x), p < rows.
+template <int J>
 __global__ __launch_bounds__(256) void vae_norm_kernel(const float* __restrict__ xg, uint32_t cs, GridDims g,
                                                        uint32_t c, const float* __restrict__ gamma, int mode,
-                                                       int compact, uint64_t rows, uint16_t* __restrict__ y,
-                                                       uint32_t cp)
+                                                       int compact, uint32_t rows, uint16_t* __restrict__ y)
 {
-    const uint64_t r = uint64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    if (r >= rows)
+    constexpr uint32_t cp = 64 * J;
+    const uint32_t r = (blockIdx.x * 256 + threadIdx.x) >> 4;
+    const uint32_t l = threadIdx.x & 15;
+    if (r >= rows) // whole 16-lane groups leave together
         return;
-    uint16_t* yr = y + r * cp;
+    uint16_t* yr = y + uint64_t(r) * cp;
     uint32_t py, px;
     bool on;
     if (compact) {
-        py = uint32_t(r / g.w);
-        px = uint32_t(r % g.w);
+        py = r / g.w;
+        px = r - py * g.w;
         on = true;
     } else {
-        on = g.pixel(r, py, px);
+        on = g.pixel32(r, py, px);
     }
     if (!on) {
-        for (uint32_t k = lane; k < cp; k += 64)
-            yr[k] = 0;
+#pragma unroll
+        for (int j = 0; j < J; ++j)
+            *reinterpret_cast<u32x2*>(yr + 4 * (l + 16 * j)) = u32x2{0, 0};
         return;
     }
     const float* xr = xg + g.row_of(py, px) * cs;
-    constexpr int J = 8; // channels <= 512
-    float v[J];
+    f32x4 v[J];
     float ss = 0.0f;
 #pragma unroll
     for (int j = 0; j < J; ++j) {
-        const uint32_t k = lane + 64 * j;
-        v[j] = k < c ? xr[k] : 0.0f;
-        ss = fmaf(v[j], v[j], ss);
+        const uint32_t k = 4 * (l + 16 * j);
+        v[j] = k < c ? *reinterpret_cast<const f32x4*>(xr + k) : f32x4{0, 0, 0, 0};
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            ss = fmaf(v[j][e], v[j][e], ss);
     }
-    float s = 1.0f;
+    float sc = 1.0f;
     if (mode != 2) {
-        ss = wave_sum(ss);
-        s = rsqrtf(ss / float(c) + 1e-24f / float(c));
+#pragma unroll
+        for (int m = 8; m >= 1; m >>= 1)
+            ss += __shfl_xor(ss, m, 16);
+        sc = rsqrtf(ss / float(c) + 1e-24f / float(c));
     }
 #pragma unroll
     for (int j = 0; j < J; ++j) {
-        const uint32_t k = lane + 64 * j;
-        if (k >= cp)
-            break;
-        float o = 0.0f;
+        const uint32_t k = 4 * (l + 16 * j);
+        float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
         if (k < c) {
-            o = mode == 2 ? v[j] : v[j] * s * gamma[k];
-            if (mode == 0)
-                o = o / (1.0f + __expf(-o));
+            const f32x4 gm = mode == 2 ? f32x4{1, 1, 1, 1} : *reinterpret_cast<const f32x4*>(gamma + k);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float t = mode == 2 ? v[j][e] : v[j][e] * sc * gm[e];
+                if (mode == 0)
+                    t = t / (1.0f + __expf(-t));
+                o[e] = t;
+            }
         }
-        yr[k] = f2bf_bits(o);
+        *reinterpret_cast<u32x2*>(yr + k) = u32x2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
     }
 }
 
 // Nearest 2x: the bf16 padded grid of the 2h x 2w image (cp channels) from the fp32 grid of the h x w one (c
-// channels, stride cs). One thread a (output row, channel).
+// channels, a multiple of 4, stride cs). One thread a (output row, 4 channels); 32-bit indexing.
 __global__ __launch_bounds__(256) void vae_up_kernel(const float* __restrict__ x, uint32_t cs, GridDims gi,
                                                      uint32_t c, GridDims go, uint32_t cp, uint16_t* __restrict__ y)
 {
-    const uint64_t i = uint64_t(blockIdx.x) * 256 + threadIdx.x;
-    if (i >= go.rows() * cp)
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x, q = cp / 4;
+    if (i >= uint32_t(go.rows()) * q)
         return;
-    const uint64_t r = i / cp;
-    const uint32_t k = uint32_t(i % cp);
+    const uint32_t r = i / q, k = 4 * (i - r * q);
     uint32_t py, px;
-    float v = 0.0f;
-    if (k < c && go.pixel(r, py, px))
-        v = x[gi.row_of(py / 2, px / 2) * cs + k];
-    y[i] = f2bf_bits(v);
+    f32x4 v{0, 0, 0, 0};
+    if (k < c && go.pixel32(r, py, px))
+        v = *reinterpret_cast<const f32x4*>(x + gi.row_of(py / 2, px / 2) * cs + k);
+    *reinterpret_cast<u32x2*>(y + uint64_t(i) * 4) = u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
 }
 
 // Row softmax for the mid block's attention: p[j] = exp(scale (s[j] - max)) / sum over the n real columns, bf16, 0
-// for the padding columns up to ld. One block a row.
+// for the padding columns up to ld. One block a row: one read for the max and the sum together (each thread keeps a
+// running max and a sum rescaled to it; pairs merge the same way), one more to write P.
+__device__ inline void ms_merge(float& m, float& s, float m2, float s2)
+{
+    const float mm = fmaxf(m, m2);
+    s = (m == -INFINITY ? 0.0f : s * __expf(m - mm)) + (m2 == -INFINITY ? 0.0f : s2 * __expf(m2 - mm));
+    m = mm;
+}
+
 __global__ __launch_bounds__(256) void vae_softmax_kernel(const float* __restrict__ s, uint32_t n, uint32_t ld,
                                                           float scale, uint16_t* __restrict__ p)
 {
-    __shared__ float red[4];
+    __shared__ float rm[4], rs[4];
     const float* sr = s + uint64_t(blockIdx.x) * ld;
     uint16_t* pr = p + uint64_t(blockIdx.x) * ld;
-    float m = -INFINITY;
-    for (uint32_t j = threadIdx.x; j < n; j += 256)
-        m = fmaxf(m, sr[j]);
-    m = wave_max(m);
-    if ((threadIdx.x & 63) == 0)
-        red[threadIdx.x >> 6] = m;
+    float m = -INFINITY, sum = 0.0f; // in units of scale * s
+    for (uint32_t j = 4 * threadIdx.x; j < n; j += 1024) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(sr + j); // n is a multiple of 4 here or the tail is masked
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            if (j + e < n)
+                ms_merge(m, sum, scale * v[e], 1.0f);
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        const float m2 = __shfl_xor(m, o), s2 = __shfl_xor(sum, o);
+        ms_merge(m, sum, m2, s2);
+    }
+    if ((threadIdx.x & 63) == 0) {
+        rm[threadIdx.x >> 6] = m;
+        rs[threadIdx.x >> 6] = sum;
+    }
     __syncthreads();
-    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    __syncthreads();
-    float sum = 0.0f;
-    for (uint32_t j = threadIdx.x; j < n; j += 256)
-        sum += __expf(scale * (sr[j] - m));
-    sum = wave_sum(sum);
-    if ((threadIdx.x & 63) == 0)
-        red[threadIdx.x >> 6] = sum;
-    __syncthreads();
-    const float inv = 1.0f / (red[0] + red[1] + red[2] + red[3]);
-    for (uint32_t j = threadIdx.x; j < ld; j += 256)
-        pr[j] = j < n ? f2bf_bits(__expf(scale * (sr[j] - m)) * inv) : uint16_t(0);
+    m = rm[0];
+    sum = rs[0];
+    for (int i = 1; i < 4; ++i)
+        ms_merge(m, sum, rm[i], rs[i]);
+    const float inv = 1.0f / sum;
+    for (uint32_t j = 4 * threadIdx.x; j < ld; j += 1024) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(sr + j);
+        float o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            o[e] = j + e < n ? __expf(scale * v[e] - m) * inv : 0.0f;
+        *reinterpret_cast<u32x2*>(pr + j) = u32x2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+    }
 }
 
 // x (fp32 grid, stride cs) += y (compact [pixels][cs]) over c channels. One thread a (pixel, channel).
@@ -473,11 +513,30 @@ struct mk_vae {
         return mk_gemm(&g, stream);
     }
     mk_status norm(const void* xg, uint32_t cs, GridDims g, uint32_t c, const float* gamma, int mode, void* out,
-                   uint32_t cp)
+                   uint32_t cp, int compact = 0, uint64_t rows = 0)
     {
-        const uint64_t rows = g.rows();
-        vae_norm_kernel<<<blocks_for(rows * 64), 256, 0, stream>>>(static_cast<const float*>(xg), cs, g, c, gamma,
-                                                                   mode, 0, rows, static_cast<uint16_t*>(out), cp);
+        if (!compact)
+            rows = g.rows();
+        const dim3 grid(blocks_for(rows * 16));
+        const float* x = static_cast<const float*>(xg);
+        uint16_t* y = static_cast<uint16_t*>(out);
+        switch (cp / 64) {
+#define MK_VAE_NORM(J)                                                                                             \
+    case J:                                                                                                        \
+        vae_norm_kernel<J><<<grid, 256, 0, stream>>>(x, cs, g, c, gamma, mode, compact, uint32_t(rows), y);        \
+        break;
+            MK_VAE_NORM(1)
+            MK_VAE_NORM(2)
+            MK_VAE_NORM(3)
+            MK_VAE_NORM(4)
+            MK_VAE_NORM(5)
+            MK_VAE_NORM(6)
+            MK_VAE_NORM(7)
+            MK_VAE_NORM(8)
+#undef MK_VAE_NORM
+        default:
+            return fail(MK_ERR_ARG, "vae norm: more than 512 channels");
+        }
         MK_LAUNCH_CHECK("vae_norm");
         return MK_OK;
     }
@@ -533,8 +592,7 @@ struct mk_vae {
         MK_HIP(hipMemsetAsync(kb.p, 0, np * cp * 2, stream));
         MK_HIP(hipMemsetAsync(sc.p, 0, np * cp * 2, stream));
         uint16_t* xn = static_cast<uint16_t*>(sc.p);
-        vae_norm_kernel<<<blocks_for(n * 64), 256, 0, stream>>>(xp, cp, g, c, attn_g, 1, 1, n, xn, cp);
-        MK_LAUNCH_CHECK("vae_norm");
+        MK_TRY(norm(xp, cp, g, c, attn_g, 1, xn, cp, 1, n));
         MK_TRY(conv1(qkv, 0, xn, n, qb.p, cp, MK_BF16, MK_EPI_STORE));
         MK_TRY(conv1(qkv, 1, xn, n, kb.p, cp, MK_BF16, MK_EPI_STORE));
         {
@@ -641,7 +699,7 @@ struct mk_vae {
             }
             if (u.up) {
                 const GridDims g2{2 * g.h, 2 * g.w};
-                vae_up_kernel<<<blocks_for(g2.rows() * u.conv.cip()), 256, 0, stream>>>(
+                vae_up_kernel<<<blocks_for(g2.rows() * u.conv.cip() / 4), 256, 0, stream>>>(
                     xp, cs, g, u.cout, g2, u.conv.cip(), static_cast<uint16_t*>(a.p));
                 MK_LAUNCH_CHECK("vae_up");
                 MK_TRY(conv3(u.conv, a.p, g2, yp, u.conv.cop(), false));
@@ -692,8 +750,9 @@ mk_status mk_vae_create(const mk_vae_config* cfg, mk_vae** out)
     if (!cfg || !out || !cfg->mean || !cfg->std)
         return fail(MK_ERR_ARG, "vae_create: null");
     *out = nullptr;
-    if (!cfg->base || cfg->base > 128 || !cfg->z || cfg->z > 64)
-        return fail(MK_ERR_ARG, "vae_create: base channels 1..128 (levels 4 base <= 512), latent channels 1..64");
+    if (!cfg->base || cfg->base > 128 || cfg->base % 4 || !cfg->z || cfg->z > 64)
+        return fail(MK_ERR_ARG, "vae_create: base channels a multiple of 4 up to 128 (levels 4 base <= 512), latent "
+                                "channels 1..64");
     auto v = std::make_unique<mk_vae>();
     v->base = cfg->base;
     v->z = cfg->z;
