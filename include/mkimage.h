@@ -252,7 +252,7 @@ mk_status mk_vae_load(mk_vae* v, const char* name, const float* data, const int6
 mk_status mk_vae_load_safetensors(mk_vae* v, const char* path, uint64_t* loaded);
 /* Counter-RNG weights keyed by (seed, name): convs N(0, 1 / fan_in) as bf16, biases N(0, 0.02), gammas 1 + N(0, 0.1). */
 mk_status mk_vae_init_random(mk_vae* v, uint64_t seed);
-/* tokens [h * w][4 z] host fp32 (n values) -> rgba [16 h][16 w][4] host fp32 */
+/* tokens [h * w][4 z] host fp32 (n values) -> rgba [16 h][16 w][4] host fp32; h, w <= 256 (images up to 4096^2) */
 mk_status mk_vae_decode(mk_vae* v, const float* tokens, size_t n, uint32_t h, uint32_t w, float* rgba);
 /* the same on device buffers, queued on the VAE's stream (mk_vae_stream) */
 mk_status mk_vae_decode_device(mk_vae* v, const float* tokens, uint32_t h, uint32_t w, float* rgba);
@@ -336,7 +336,8 @@ mk_status mk_engine_load_safetensors(mk_engine* e, const char* path, uint64_t* l
  * <module>.alpha: W += scale * (alpha / rank) * B A (alpha absent: scale * B A). Module names are checkpoint names,
  * optionally prefixed "transformer.", "diffusion_model.", "base_model.model." or written Kohya-style
  * ("lora_unet_transformer_blocks_0_attn_to_q": '_' and '.' alike). A pair whose shapes do not match its module is
- * MK_ERR_ARG and nothing is merged; modules that name no weight of the engine (text encoders) are skipped.
+ * MK_ERR_ARG and nothing is merged; a module with parts beyond the pair and alpha (DoRA magnitudes, bias diffs) is
+ * MK_ERR_UNSUPPORTED; modules that name no weight of the engine (text encoders, full-weight diffs) are skipped.
  * `merged` / `skipped` (may be NULL): module counts. */
 mk_status mk_engine_add_lora(mk_engine* e, const char* path, float scale, uint64_t* merged, uint64_t* skipped);
 /* The engine's weights in name order: checkpoint name, stored dtype, rows and cols (vectors: cols = 1). The name

@@ -1529,6 +1529,9 @@ mk_status mk_engine_add_lora(mk_engine* e, const char* path, float scale, uint64
         }
         if (m.a < 0 || m.b < 0)
             return fail(MK_ERR_ARG, "add_lora: " + module + " has only one of its down / up matrices");
+        if (m.other) // a DoRA magnitude, a bias difference, ...: merging the pair alone would be wrong
+            return fail(MK_ERR_UNSUPPORTED, "add_lora: " + module + " has parts beside its down / up matrices "
+                                                                    "(DoRA / bias diffs are not merged)");
         // the target: the module's rows in the fused tensor (QwenImage::lora_target); Q21's fused gate_up spans
         // the gate rows and the up rows that follow them
         Dest d{};

@@ -879,8 +879,8 @@ mk_status mk_vae_decode_device(mk_vae* v, const float* tokens, uint32_t h, uint3
 {
     if (!v || !tokens || !rgba)
         return fail(MK_ERR_ARG, "vae_decode: null");
-    if (!h || !w || uint64_t(h) * w > (uint64_t(1) << 20))
-        return fail(MK_ERR_ARG, "vae_decode: a grid of 1 .. 2^20 tokens");
+    if (!h || !w || h > 256 || w > 256)
+        return fail(MK_ERR_ARG, "vae_decode: a grid of 1 .. 256 tokens a side (32-bit indexing of the 4096^2 level)");
     return v->decode(tokens, h, w, rgba);
 }
 
@@ -890,8 +890,8 @@ mk_status mk_vae_decode(mk_vae* v, const float* tokens, size_t n, uint32_t h, ui
         return fail(MK_ERR_ARG, "vae_decode: null");
     if (n != uint64_t(h) * w * 4 * v->z)
         return fail(MK_ERR_ARG, "vae_decode: latents must be [h * w][" + std::to_string(4 * v->z) + "]");
-    if (!h || !w || uint64_t(h) * w > (uint64_t(1) << 20))
-        return fail(MK_ERR_ARG, "vae_decode: a grid of 1 .. 2^20 tokens");
+    if (!h || !w || h > 256 || w > 256)
+        return fail(MK_ERR_ARG, "vae_decode: a grid of 1 .. 256 tokens a side (32-bit indexing of the 4096^2 level)");
     const uint64_t out_n = uint64_t(16) * h * 16 * w * 4;
     MK_TRY(v->ensure(v->tok, n * 4));
     MK_TRY(v->ensure(v->rgba, out_n * 4));

@@ -285,4 +285,9 @@ def test_lora_errors_leave_weights_alone(gpu, tmp_path):
     save_file({"transformer_blocks.0.attn.to_q.lora_A.weight": a}, str(p))
     with pytest.raises(M.MkError, match="only one of"):
         e.add_lora(p)
+    # a DoRA magnitude beside the pair: refused rather than merged without it
+    save_file({"transformer_blocks.0.attn.to_q.lora_A.weight": a, "transformer_blocks.0.attn.to_q.lora_B.weight": b,
+               "transformer_blocks.0.attn.to_q.dora_scale": torch.ones(1, D)}, str(p))
+    with pytest.raises(M.MkError, match="DoRA"):
+        e.add_lora(p)
     same_state(before, state(e))

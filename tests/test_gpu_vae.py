@@ -146,6 +146,8 @@ def test_vae_argument_errors(gpu):
     vae = M.Vae(16, mean=MEAN, std=STD)
     with pytest.raises(M.MkError, match="latents must be"):
         vae.decode(np.zeros((4, 60), np.float32), 2, 2)
+    with pytest.raises(M.MkError, match="256 tokens a side"):
+        vae.decode(np.zeros((257, 64), np.float32), 257, 1)
     with pytest.raises(M.MkError, match="wrong shape"):
         vae.load("decoder.conv_in.weight", np.zeros((64, 16, 3, 2), np.float32))
     with pytest.raises(M.MkError, match="no tensor named"):
