@@ -79,6 +79,7 @@ mk_status mk_malloc(void** p, size_t bytes)
     *p = nullptr;
     MK_HIP(hipMalloc(p, bytes ? bytes : 16));
     MK_HIP(hipMemset(*p, 0, bytes ? bytes : 16));
+    MK_HIP(hipStreamSynchronize(nullptr)); // zero on return: work on non-blocking streams does not wait for it
     return MK_OK;
 }
 
@@ -110,6 +111,7 @@ mk_status mk_memset(void* p, int v, size_t bytes)
     if (bytes && !p)
         return fail(MK_ERR_ARG, "memset: null");
     MK_HIP(hipMemset(p, v, bytes));
+    MK_HIP(hipStreamSynchronize(nullptr));
     return MK_OK;
 }
 

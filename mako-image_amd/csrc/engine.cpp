@@ -43,6 +43,8 @@ struct Buf {
         bytes = 0;
         MK_HIP(hipMalloc(&p, b));
         MK_HIP(hipMemset(p, 0, b));
+        // the null stream's fill must be done before the engine's non-blocking stream uses the buffer
+        MK_HIP(hipStreamSynchronize(nullptr));
         bytes = b;
         return MK_OK;
     }
@@ -160,6 +162,7 @@ struct mk_engine {
     {
         MK_HIP(hipMalloc(p, bytes));
         MK_HIP(hipMemset(*p, 0, bytes));
+        MK_HIP(hipStreamSynchronize(nullptr));
         allocs.push_back(*p);
         weight_bytes += bytes;
         return MK_OK;

@@ -990,6 +990,7 @@ mk_status launch(GemmP* p, uint32_t count, const GemmPlan& plan, hipStream_t s)
                 MK_HIP(hipExtMallocWithFlags(reinterpret_cast<void**>(&W.flags), 2 * grid * sizeof(uint32_t),
                                              hipDeviceMallocUncached));
                 MK_HIP(hipMemset(W.flags, 0, 2 * grid * sizeof(uint32_t)));
+                MK_HIP(hipStreamSynchronize(nullptr)); // cleared before the launch's stream reads them
                 W.nflags = 2 * grid;
             }
             if (W.ws_bytes < need || W.nflags < 2 * grid)

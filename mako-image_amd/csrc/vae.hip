@@ -361,7 +361,7 @@ struct mk_vae {
     mk_status alloc(size_t bytes, void** p)
     {
         MK_HIP(hipMalloc(p, bytes));
-        MK_HIP(hipMemset(*p, 0, bytes));
+        MK_HIP(hipMemsetAsync(*p, 0, bytes, stream)); // ordered before the stream's packing kernels
         allocs.push_back(*p);
         return MK_OK;
     }
@@ -375,7 +375,7 @@ struct mk_vae {
         b.p = nullptr;
         b.bytes = 0;
         MK_HIP(hipMalloc(&b.p, bytes));
-        MK_HIP(hipMemset(b.p, 0, bytes));
+        MK_HIP(hipMemsetAsync(b.p, 0, bytes, stream)); // ordered before the stream's kernels
         b.bytes = bytes;
         return MK_OK;
     }

@@ -90,7 +90,8 @@ MEAN = np.linspace(-0.3, 0.3, 16).astype(np.float32)
 STD = np.linspace(0.5, 2.0, 16).astype(np.float32)
 
 
-@pytest.mark.parametrize("base, h, w", [(16, 2, 2), (16, 2, 3), (32, 4, 4)])
+# base 96 is Qwen-Image's: 384 / 192 / 96 channels (96 padded to 128, 192-wide layers on 64-wide tiles)
+@pytest.mark.parametrize("base, h, w", [(16, 2, 2), (16, 2, 3), (32, 4, 4), (96, 4, 4)])
 def test_vae_decode_matches_oracle(gpu, base, h, w):
     ref = R.Vae(base, seed=5, mean=MEAN, std=STD)
     vae = M.Vae(base, mean=MEAN, std=STD)
