@@ -153,3 +153,23 @@ def test_vae_argument_errors(gpu):
         vae.load("decoder.conv_in.weight", np.zeros((64, 16, 3, 2), np.float32))
     with pytest.raises(M.MkError, match="no tensor named"):
         vae.load("decoder.nope.weight", np.zeros(4, np.float32))
+
+
+def test_vae_full_size_properties(gpu):
+    # the 1024x1024 decode (Qwen-Image's base 96, 64 x 64 tokens): with a constant latent every pixel farther from the
+    # image border than the decoder's reach (about 150 output pixels: 12 convs at 1/8 scale, 7 at 1/4, 7 at 1/2, 7 at
+    # full) sees identical inputs, and the mid block's attention gives identical queries identical outputs, so the
+    # centre must be uniform bit for bit; random tokens decode to finite values deterministically.
+    vae = M.Vae(96, mean=MEAN, std=STD)
+    vae.init_random(1)
+    # one value a channel for all four pixels of each token's 2x2 patch (value (c * 2 + py) * 2 + px): a constant
+    # latent image
+    tok = np.tile(np.repeat(np.random.default_rng(2).standard_normal(16).astype(np.float32), 4), (64 * 64, 1))
+    img = vae.decode(tok, 64, 64)
+    assert img.shape == (1024, 1024, 4) and np.all(img[..., 3] == 1)
+    c = img[200:824, 200:824, :3]
+    assert np.array_equal(c, np.broadcast_to(img[512, 512, :3], c.shape)), np.abs(c - img[512, 512, :3]).max()
+    assert not np.array_equal(img[0, 0, :3], img[512, 512, :3])  # the border does differ
+    rnd = np.random.default_rng(3).standard_normal((64 * 64, 64)).astype(np.float32)
+    a, b = vae.decode(rnd, 64, 64), vae.decode(rnd, 64, 64)
+    assert np.isfinite(a).all() and np.array_equal(a, b) and np.abs(a[..., :3]).max() <= 1
