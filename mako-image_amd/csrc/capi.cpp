@@ -61,7 +61,8 @@ mk_status mk_device_info(int dev, char* name, size_t name_len, int* cus, int* cl
     hipDeviceProp_t p;
     MK_HIP(hipGetDeviceProperties(&p, dev));
     if (name && name_len) {
-        std::snprintf(name, name_len, "%s", p.name);
+        // the marketing name comes from a table the driver package may lack; the architecture name always exists
+        std::snprintf(name, name_len, "%s", p.name[0] ? p.name : p.gcnArchName);
     }
     if (arch && arch_len)
         std::snprintf(arch, arch_len, "%s", p.gcnArchName);
