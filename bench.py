@@ -249,7 +249,7 @@ def cpu_baseline_sdxl(seconds_target, pass_flops):
 
 def gemm_traffic():
     """HBM-side bytes per GEMM launch (L2 fetch + write, calibrated against a copy of known size), from the committed
-    rocprofv3 counter summary of this build's step; None when the summary is absent."""
+    rocprofv3 counter summary of the step; None when the summary is absent."""
     f = ROOT / "profiles" / "mmdit_step_1024_traffic.md"
     if not f.exists():
         return None
@@ -313,7 +313,7 @@ def main():
     H = W = wl["side"]
     S = wl["text"]
     if args.gpus != 1 or world != 1:
-        print(f"bench.py measures one GPU: this build runs the step on one MI355X (asked for {max(args.gpus, world)}); "
+        print(f"bench.py measures one GPU: the step runs on one MI355X (asked for {max(args.gpus, world)}); "
               f"run it with --gpus 1", file=sys.stderr)
         sys.exit(2)
 

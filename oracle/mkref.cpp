@@ -1,5 +1,5 @@
-// mkref — CPU restatement of mako-image's denoising hot path. TEST INFRASTRUCTURE ONLY (the checker of the HIP
-// path; the product library never links or calls it). Arithmetic model and scope: mkref.h.
+// mkref — CPU restatement of mako-image's denoising hot path. TEST INFRASTRUCTURE ONLY (the tests compare the HIP
+// path against it; the product library never links or calls it). Arithmetic model and scope: mkref.h.
 #include "mkref.h"
 
 #include <omp.h>

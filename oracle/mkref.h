@@ -1,6 +1,6 @@
 /* mkref — CPU restatement of mako-image's denoising hot path.
  *
- * TEST INFRASTRUCTURE ONLY. This library is the checker for the HIP path: tests/, the smoke() of
+ * TEST INFRASTRUCTURE ONLY. The HIP path's results are compared against this library: tests/, the smoke() of
  * __graft_entry__.py and bench.py's cpu_baseline leg load it, nothing else. The product library
  * (mako-image_amd/libmkimage.so) never links, loads or calls it.
  *

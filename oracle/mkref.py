@@ -1,7 +1,7 @@
 """ctypes binding of the oracle library (oracle/libmkref.so).
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, by __graft_entry__.smoke() and by bench.py's cpu_baseline leg, always
-as the checker or the CPU baseline, never as the product path. The product library (mako-image_amd/libmkimage.so)
+as the reference results or the CPU baseline, never as the product path. The product library (mako-image_amd/libmkimage.so)
 does not use it.
 """
 from __future__ import annotations
