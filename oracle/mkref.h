@@ -20,7 +20,8 @@
  *
  * Reference files restated (see each function in mkref.cpp for its file:line):
  *   src/image/qwen_image.cpp, src/kernels/image.metal:9-65,450-484, src/image/engine.cpp:335-365,459-506,
- *   src/image/sdxl.cpp:68-87,425-457,672-796.
+ *   src/image/sdxl.cpp:68-87,425-457,672-796; the VAE decoder src/image/engine.cpp:589-628,722-777,862-954 (pinned
+ *   by tests/test_oracle_graph.py against torch's conv2d / interpolate / softmax).
  */
 #ifndef MKREF_H
 #define MKREF_H
