@@ -485,6 +485,32 @@ __global__ __launch_bounds__(256) void glu_kernel(const In* __restrict__ in, uin
     }
 }
 
+// The same for bf16 input 8 values a thread: 16-byte loads and stores, 32-bit indexing (rows * F / 8 < 2^32, F a
+// multiple of 8, rows 16-byte aligned); each value's arithmetic and rounding are glu_kernel's.
+template <bool kGeglu>
+__global__ __launch_bounds__(256) void glu8_kernel(const uint16_t* __restrict__ in, uint32_t rows, uint32_t F,
+                                                   uint16_t* __restrict__ m)
+{
+    const uint32_t F8 = F / 8, n8 = rows * F8;
+    for (uint32_t i = blockIdx.x * 256 + threadIdx.x; i < n8; i += gridDim.x * 256) {
+        const uint32_t r = i / F8, c = (i - r * F8) * 8;
+        const uint16_t* row = in + uint64_t(r) * 2 * F + c;
+        const u32x4 av = *reinterpret_cast<const u32x4*>(row), bv = *reinterpret_cast<const u32x4*>(row + F);
+        u32x4 o;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            float y[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const float a = bf2f_bits(uint16_t(av[k] >> (16 * h))), b = bf2f_bits(uint16_t(bv[k] >> (16 * h)));
+                y[h] = kGeglu ? a * 0.5f * b * (1.0f + erf_fit(b * 0.70710678f)) : silu_f(a) * b;
+            }
+            o[k] = pack_bf16x2(y[0], y[1]);
+        }
+        *reinterpret_cast<u32x4*>(m + uint64_t(r) * F + c) = o;
+    }
+}
+
 __global__ __launch_bounds__(256) void cfg_euler_kernel(const float* __restrict__ x, const float* __restrict__ pos,
                                                         const float* __restrict__ neg, uint64_t n, float guidance,
                                                         float dt, float* __restrict__ out)
@@ -870,6 +896,13 @@ mk_status mk_swiglu(const void* gu, uint32_t gu_dtype, uint32_t rows, uint32_t F
 {
     if (!gu || !m || (gu_dtype != MK_F32 && gu_dtype != MK_BF16))
         return fail(MK_ERR_ARG, "swiglu: null pointer or bad dtype");
+    if (gu_dtype == MK_BF16 && F % 8 == 0 && uint64_t(rows) * F / 8 < (uint64_t(1) << 31) &&
+        !(reinterpret_cast<uintptr_t>(gu) & 15) && !(reinterpret_cast<uintptr_t>(m) & 15)) {
+        glu8_kernel<false><<<grid_for(uint64_t(rows) * F / 8), 256, 0, S(stream)>>>(
+            static_cast<const uint16_t*>(gu), rows, F, static_cast<uint16_t*>(m));
+        MK_LAUNCH_CHECK("swiglu");
+        return MK_OK;
+    }
     const uint32_t g = grid_for(uint64_t(rows) * F);
     if (gu_dtype == MK_F32)
         glu_kernel<float, false><<<g, 256, 0, S(stream)>>>(static_cast<const float*>(gu), rows, F,
@@ -885,6 +918,13 @@ mk_status mk_geglu(const void* hg, uint32_t hg_dtype, uint32_t rows, uint32_t F,
 {
     if (!hg || !m || (hg_dtype != MK_F32 && hg_dtype != MK_BF16))
         return fail(MK_ERR_ARG, "geglu: null pointer or bad dtype");
+    if (hg_dtype == MK_BF16 && F % 8 == 0 && uint64_t(rows) * F / 8 < (uint64_t(1) << 31) &&
+        !(reinterpret_cast<uintptr_t>(hg) & 15) && !(reinterpret_cast<uintptr_t>(m) & 15)) {
+        glu8_kernel<true><<<grid_for(uint64_t(rows) * F / 8), 256, 0, S(stream)>>>(
+            static_cast<const uint16_t*>(hg), rows, F, static_cast<uint16_t*>(m));
+        MK_LAUNCH_CHECK("geglu");
+        return MK_OK;
+    }
     const uint32_t g = grid_for(uint64_t(rows) * F);
     if (hg_dtype == MK_F32)
         glu_kernel<float, true><<<g, 256, 0, S(stream)>>>(static_cast<const float*>(hg), rows, F,

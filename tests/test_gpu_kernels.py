@@ -550,6 +550,28 @@ def test_glu(gpu, rng):
         assert np.abs(fetch_bf16(m, (rows, F)) - want).max() <= 2 ** -8 * np.abs(want).max() + 1e-6
 
 
+@pytest.mark.parametrize("F", [640, 100])
+def test_glu_bf16_vector_path_equals_scalar_path(gpu, rng, F):
+    # bf16 input: 16-byte-aligned buffers with F a multiple of 8 take the 8-wide kernel; the same data 2 bytes off
+    # alignment take the element-wise one. Bit-identical, and within bf16 rounding of the oracle.
+    rows = 37
+    hg = M.bf16_bits(rng.standard_normal((rows, 2 * F)).astype(np.float32) * 2)
+    a_in, b_in = M.Dev(hg.nbytes + 16), M.Dev(hg.nbytes + 16)
+    a_in.write(hg)
+    b_in.write(hg, offset=2)
+    a_out, b_out = M.Dev(rows * F * 2 + 16), M.Dev(rows * F * 2 + 16)
+    for name, ref in (("mk_swiglu", R.swiglu), ("mk_geglu", R.geglu)):
+        M.call(name, a_in.p, M.BF16, rows, F, a_out.p, None)
+        M.call(name, int(b_in.p) + 2, M.BF16, rows, F, int(b_out.p) + 2, None)
+        M.sync()
+        got_a = a_out.to_array(np.uint16, (rows * F + 8,))[:rows * F]
+        got_b = b_out.to_array(np.uint16, (rows * F + 8,))[1:rows * F + 1]
+        assert np.array_equal(got_a, got_b), name
+        want = ref(M.bf16_to_f32(hg))
+        got = M.bf16_to_f32(got_a).reshape(rows, F)
+        assert np.abs(got - want).max() <= 2 ** -8 * np.abs(want).max() + 1e-6, name
+
+
 def test_cfg_euler_exact(gpu, rng):
     n = 4096 * 64
     x, pos, neg = (rng.standard_normal(n).astype(np.float32) for _ in range(3))
