@@ -312,6 +312,21 @@ __global__ __launch_bounds__(256) void heads_kernel(const uint16_t* __restrict__
     }
 }
 
+// The layout alone (no norm, no rope): 16 bytes a thread, 32-bit indexing (rows * heads * d / 8 < 2^31; ld, col0,
+// stride_x multiples of 8; 16-byte aligned buffers). out [batch][heads][n_pad][d] row row0 + r = x's row r.
+__global__ __launch_bounds__(256) void heads_copy_kernel(const uint16_t* __restrict__ x, uint32_t rows, int64_t ld,
+                                                         int64_t stride_x, uint32_t col0, uint32_t heads, uint32_t d,
+                                                         uint16_t* __restrict__ out, uint32_t n_pad, uint32_t row0)
+{
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x, q = d / 8, bi = blockIdx.y;
+    if (i >= rows * heads * q)
+        return;
+    const uint32_t c = (i % q) * 8, p = i / q, r = p / heads, h = p - r * heads;
+    const u32x4 v =
+        *reinterpret_cast<const u32x4*>(x + uint64_t(bi) * stride_x + uint64_t(r) * ld + col0 + uint64_t(h) * d + c);
+    *reinterpret_cast<u32x4*>(out + ((uint64_t(bi) * heads + h) * n_pad + row0 + r) * d + c) = v;
+}
+
 // V^T pack: x bf16 [batch][rows][ld] columns col0 + h*d .. -> out [batch][heads][d][n_pad] at column
 // vt_col(row0 + r).
 // One block per (64 rows, head, batch), transposed through LDS so both sides are coalesced.
@@ -846,6 +861,12 @@ mk_status mk_heads(const void* x, uint32_t batch, uint32_t rows, int64_t ld, int
         else
             heads_t_kernel<64><<<grid, 256, 0, S(stream)>>>(static_cast<const uint16_t*>(x), rows, ld, stride_x, col0,
                                                             heads, static_cast<uint16_t*>(out), n_pad, row0);
+    } else if (!w && !(rope && rope_mode) && ld % 8 == 0 && col0 % 8 == 0 && stride_x % 8 == 0 &&
+               !(reinterpret_cast<uintptr_t>(x) & 15) && !(reinterpret_cast<uintptr_t>(out) & 15) &&
+               uint64_t(rows) * heads * d / 8 < (uint64_t(1) << 31)) {
+        heads_copy_kernel<<<dim3(cdiv(uint64_t(rows) * heads * d / 8, 256), batch), 256, 0, S(stream)>>>(
+            static_cast<const uint16_t*>(x), rows, ld, stride_x, col0, heads, d, static_cast<uint16_t*>(out), n_pad,
+            row0);
     } else {
         heads_kernel<<<dim3(cdiv(uint64_t(rows) * heads, 4), batch), 256, 0, S(stream)>>>(
             static_cast<const uint16_t*>(x), rows, ld, stride_x, col0, heads, d, w, eps, rope, rope_mode,

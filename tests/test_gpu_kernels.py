@@ -499,6 +499,21 @@ def test_heads(gpu, rng, d, mode, transpose):
         assert np.abs(g - want).max() <= 2 ** -8 * np.abs(want).max() + 1e-6
 
 
+@pytest.mark.parametrize("d", [64, 128])
+def test_heads_plain_layout_is_an_exact_copy(gpu, rng, d):
+    # no norm, no rope: the 16-byte copy path; every value lands bit for bit at [batch][head][row0 + r]
+    B, rows, H, row0, n_pad = 2, 77, 5, 3, 96
+    ld = 3 * H * d
+    x = M.bf16_bits(rng.standard_normal((B, rows, ld)).astype(np.float32))
+    out = M.Dev(B * H * n_pad * d * 2)
+    M.call("mk_heads", M.Dev.from_array(x).p, B, rows, ld, rows * ld, H * d, H, d, None, 1e-6, None, 0, out.p, n_pad,
+           row0, 0, None)
+    M.sync()
+    got = out.to_array(np.uint16, (B, H, n_pad, d))[:, :, row0:row0 + rows]
+    want = x[:, :, H * d:2 * H * d].reshape(B, rows, H, d).transpose(0, 2, 1, 3)
+    assert np.array_equal(got, want)
+
+
 # one-row kernels for K in {2048, 3072, 4096}; the LDS-staged kernel for the rest and for rows 2..4
 @pytest.mark.parametrize("rows,K,silu", [(1, 3072, 1), (1, 2048, 0), (1, 4096, 1), (1, 1024, 1), (2, 3072, 1),
                                          (4, 2048, 0)])
