@@ -6,9 +6,10 @@ to 3072; classifier-free guidance as a batch of 2 (positive and negative prompt)
 Euler update. bf16 weights (random-init N(0, 0.02), 40.8 GB) and activations, fp32 accumulation and residual stream.
 Synthetic inputs: prompts and latents N(0, 1), resident on the device when the timed region starts.
 
-Prints one JSON line. `roofline` is the dominant kernel class (the GEMMs): algorithmic FLOPs of its launches divided
-by their summed durations, from HIP events recorded around each launch on the engine's stream in a separate timed
-pass of the same steps. `cpu_baseline` is the oracle (CPU restatement of the same step) on a bounded sample of one
+Prints one JSON line. `roofline` is the dominant kernel (the launch shape with the most time a step: the grouped
+FFN-down GEMM): its algorithmic FLOPs per launch divided by its average launch duration, from HIP events recorded
+around each launch on the engine's stream in a separate timed pass of the same steps; `gemm_class` is the same over
+every GEMM launch, `attention_gemm_mfma_frac` over every GEMM and attention launch. `cpu_baseline` is the oracle (CPU restatement of the same step) on a bounded sample of one
 block, timed on this host's cores and scaled by FLOPs to a whole step.
 """
 import argparse
@@ -247,16 +248,34 @@ def cpu_baseline_sdxl(seconds_target, pass_flops):
                       f"{rate / 1e9:.1f} GFLOP/s), scaled by FLOPs to the whole batch-2 pass"}
 
 
-def gemm_traffic():
-    """HBM-side bytes per GEMM launch (L2 fetch + write, calibrated against a copy of known size), from the committed
-    rocprofv3 counter summary of the step; None when the summary is absent."""
+# The kernel each timing class of the step launches (rocprofv3's name for it), for the traffic figure.
+KERNEL_OF = {"gemm.ff2": "gemm_sk_kernel<256, 256, false, 2, 8>", "gemm.ff1": "gemm_kernel<256, 256, false, 1, 8>",
+             "gemm.qkv": "gemm_kernel<256, 256, false, 3, 8>", "gemm.o": "gemm_kernel<256, 256, false, 2, 8>",
+             "attention": "attn2_kernel<128, true>"}
+
+
+def kernel_traffic(kernel):
+    """Bytes a launch of `kernel` moves between L2 and the fabric (FETCH_SIZE + WRITE_SIZE, calibrated against a copy
+    of known size), from the committed rocprofv3 counter summary of the step; None when absent. The counters see L2
+    misses: Infinity Cache (MALL) hits are included, so this bounds the DRAM bytes from above."""
     f = ROOT / "profiles" / "mmdit_step_1024_traffic.md"
-    if not f.exists():
+    if not f.exists() or not kernel:
         return None
     for line in f.read_text().splitlines():
-        if line.startswith("gemm_bytes_per_launch:"):
-            return int(line.split(":")[1])
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if len(cells) >= 4 and kernel in cells[0]:
+            try:
+                return int((float(cells[2]) + float(cells[3])) * 2 ** 20)
+            except ValueError:
+                return None
     return None
+
+
+def step_bytes_ff2(N=4096, S=256, B=2, D=3072, F=12288):
+    """Algorithmic HBM bytes of one grouped FFN-down launch (image + text rows): the bf16 activations and both
+    streams' bf16 weights read once, the fp32 residual read and written once."""
+    M = B * (N + S)
+    return M * F * 2 + 2 * D * F * 2 + 2 * M * D * 4
 
 
 def cpu_baseline(seconds_target=12.0, fp8=False):
@@ -366,10 +385,18 @@ def main():
             acc["flops"] += v["flops"]
     eng.set_timing(False)
     total, lin, attn = step_flops(N=H * W, S=S)
-    g, a = per["gemm"], per["attention"]
+    g = {"ms": sum(v["ms"] for k, v in per.items() if k.startswith("gemm")),
+         "flops": sum(v["flops"] for k, v in per.items() if k.startswith("gemm"))}
+    a = per["attention"]
     gemm_tf = g["flops"] / (g["ms"] / 1e3) / 1e12
     attn_tf = a["flops"] / (a["ms"] / 1e3) / 1e12
     both = (g["flops"] + a["flops"]) / ((g["ms"] + a["ms"]) / 1e3)
+    # the dominant kernel: the timing class (one launch shape) with the most time a step
+    dom = max((k for k, v in per.items() if v["flops"] and (k.startswith("gemm.") or k == "attention")),
+              key=lambda k: per[k]["ms"])
+    dv = per[dom]
+    dom_launch_s = dv["ms"] / 1e3 / dv["launches"]
+    dom_flops = dv["flops"] / dv["launches"]
     kernels = {k: {"ms_per_step": round(v["ms"] / args.steps, 3), "launches_per_step": v["launches"] // args.steps,
                    **({"tflops": round(v["flops"] / (v["ms"] / 1e3) / 1e12, 1)} if v["flops"] else {})}
                for k, v in sorted(per.items(), key=lambda kv: -kv[1]["ms"])}
@@ -385,14 +412,22 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
+        "weight_dtype": "fp8-e4m3" if wl["fp8"] else "bf16",
         "data": "synthetic (random-init N(0,0.02) weights, N(0,1) latents and prompts)",
         "config": {"workload": wl["name"], "blocks": 60, "dim": 3072, "heads": 24, "head_dim": 128, "ffn": 12288,
                    "text_dim": 3584, "image_tokens": H * W, "text_tokens": S, "batch": 2,
                    "weights": "fp8-e4m3" if wl["fp8"] else "bf16"},
-        "roofline": {"bound": "mfma", "kernel": "gemm (bf16 MFMA, all block and projection GEMMs)",
-                     "achieved": round(gemm_tf, 1), "peak": PEAK_BF16 / 1e12, "unit": "TFLOP/s",
-                     "frac": round(gemm_tf * 1e12 / PEAK_BF16, 4), "traffic": gemm_traffic(),
-                     "traffic_unit": "bytes/launch (profiles/mmdit_step_1024_traffic.md)"},
+        "roofline": {"bound": "mfma", "kernel": f"{dom}: {KERNEL_OF.get(dom, dom)}",
+                     "achieved": round(dom_flops / dom_launch_s / 1e12, 1), "peak": PEAK_BF16 / 1e12,
+                     "unit": "TFLOP/s", "frac": round(dom_flops / dom_launch_s / PEAK_BF16, 4),
+                     "flops_per_launch": dom_flops, "launch_us": round(dom_launch_s * 1e6, 1),
+                     "traffic": None if wl["fp8"] else kernel_traffic(KERNEL_OF.get(dom)),
+                     "traffic_algorithmic": step_bytes_ff2(H * W, S) if dom == "gemm.ff2" and not wl["fp8"] else None,
+                     "traffic_note": "bytes/launch between L2 and the fabric (rocprofv3 FETCH_SIZE + WRITE_SIZE, "
+                                     "calibrated; Infinity Cache hits included) from "
+                                     "profiles/mmdit_step_1024_traffic.md"},
+        "gemm_class": {"achieved": round(gemm_tf, 1), "unit": "TFLOP/s", "frac": round(gemm_tf * 1e12 / PEAK_BF16, 4),
+                       "ms_per_step": round(g["ms"] / args.steps, 3)},
         "attention_gemm_mfma_frac": round(both / PEAK_BF16, 4),
         "step_mfma_frac": round(total / (ms / 1e3) / PEAK_BF16, 4),
         "attention": {"achieved": round(attn_tf, 1), "unit": "TFLOP/s", "frac": round(attn_tf * 1e12 / PEAK_BF16, 4)},
@@ -403,9 +438,6 @@ def main():
         "weights_gb": round(eng.weight_bytes() / 1e9, 2),
         "init_s": round(t_init, 2),
     }
-    if wl["fp8"]:
-        line["roofline"]["kernel"] = "gemm (fp8-e4m3 weights converted to bf16 in LDS, bf16 MFMA)"
-        line["roofline"]["traffic"] = None
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(args.cpu_seconds, wl["fp8"])
     print(json.dumps(line), flush=True)

@@ -122,6 +122,14 @@ mk_status mk_gemm(const mk_gemm_args* a, void* stream);
  * keeps its own A, W, C, bias, gate, M, batch, strides and heads arguments. No counterpart in the reference (its 2.1
  * graph has one stream). */
 mk_status mk_gemm_grouped(const mk_gemm_args* a, uint32_t count, void* stream);
+/* Long GEMMs whose last wave of tiles would leave compute units idle split that wave's k steps over the chip
+ * (stream-K); the tile's owner waits, bounded, for the other ranges' partials. A wait that gives up finishes the tile
+ * from what is there and is reported as MK_ERR_DEVICE by the next mk_synchronize / mk_stream_synchronize / mk_gemm /
+ * engine step. This sets the bound in polls (an uncached load and a 128-cycle sleep each; default MK_GEMM_WAIT_LIMIT,
+ * tens of seconds); a test hook: 0 gives up at once. Stream-K launches on different streams use different workspaces,
+ * so they may run concurrently. No counterpart in the reference. */
+#define MK_GEMM_WAIT_LIMIT (1u << 26)
+mk_status mk_gemm_set_wait_limit(uint32_t polls);
 
 /* 3x3 convolution, stride 1, zero padding 1 (the VAE decoder's conv, src/image/engine.cpp:732-746, 907-947), as one
  * GEMM over the padded pixel grid (implicit im2col on MFMA). Layout "padded grid": an h x w image is stored as the
@@ -174,15 +182,16 @@ mk_status mk_heads(const void* x, uint32_t batch, uint32_t rows, int64_t ld, int
  * a lane of the P V matrix product reads 8 keys as one 16-byte load). */
 #define MK_VT_COL(k) (((k) & ~12u) | (((k) & 4u) << 1) | (((k) & 8u) >> 1))
 
-/* attention (qwen_image.cpp:271, sdxl.cpp:450-457): softmax(Q K^T scale) V, fp32 online softmax on bf16 MFMA.
- * q [batch][heads][q_pad][d], k [batch][heads][k_pad][d], vt [batch][heads][d][k_pad] bf16 with keys in the
- * MK_VT_COL order (padding keys zero);
+/* attention (qwen_image.cpp:271 and the AttnArgs it fills, sdxl.cpp:24-27, 450-457): softmax(Q K^T scale) V, fp32
+ * online softmax on bf16 MFMA. q [batch][heads][q_pad][d], k [batch][kv_heads][k_pad][d], vt
+ * [batch][kv_heads][d][k_pad] bf16 with keys in the MK_VT_COL order (padding keys zero); query head h reads key /
+ * value head h / (heads / kv_heads) (grouped-query attention; kv_heads == heads for every graph here).
  * out bf16 [batch][n_q][ldo] at column head * d. Query row i (absolute q_pos0 + i) sees key c < n_k iff
  * q_pos0 + i >= block or c <= q_pos0 + i (block 0: no mask; UINT32_MAX: causal; S: causal text prefix).
- * d in {64, 128}; q_pad % 128 == 0; k_pad % 64 == 0. */
+ * d in {64, 128}; kv_heads divides heads; q_pad % 128 == 0; k_pad % 64 == 0. */
 mk_status mk_attention(const void* q, const void* k, const void* vt, void* out, uint32_t batch, uint32_t heads,
-                       uint32_t d, uint32_t n_q, uint32_t q_pad, uint32_t n_k, uint32_t k_pad, int64_t ldo,
-                       int64_t stride_o, uint32_t q_pos0, uint32_t block, float scale, void* stream);
+                       uint32_t kv_heads, uint32_t d, uint32_t n_q, uint32_t q_pad, uint32_t n_k, uint32_t k_pad,
+                       int64_t ldo, int64_t stride_o, uint32_t q_pos0, uint32_t block, float scale, void* stream);
 
 /* Elementwise and norms (fp32 unless stated). */
 mk_status mk_silu(float* x, size_t n, void* stream);
@@ -204,6 +213,11 @@ mk_status mk_group_norm(const float* x, uint32_t batch, uint32_t rows, uint32_t 
  * x + dt * pos. */
 mk_status mk_cfg_euler(const float* x, const float* pos, const float* neg, size_t n, float guidance, float dt,
                        float* x_out, void* stream);
+/* The RoPE table mk_begin builds for a prompt of S rows and an h x w token grid (QwenImage::begin with rope3,
+ * src/image/qwen_image.cpp:33-45, 113-142): out [S + h * w][64][2] fp32 (cos, sin) of the 64 rotation pairs, axes of
+ * 16 / 56 / 56 dims (theta 10000); text row t at position (t, t, t), image row S + y * w + x at (S, y - (h - h / 2),
+ * x - (w - w / 2)). Host arithmetic only: the engine uploads exactly this table. */
+mk_status mk_rope_table(uint32_t S, uint32_t h, uint32_t w, float* out);
 /* 2x2 patchify: lat [batch][C][2h][2w] -> tokens [batch][h*w][4C] (feature c*4 + py*2 + px), and back. */
 mk_status mk_patchify(const float* lat, uint32_t batch, uint32_t C, uint32_t h, uint32_t w, float* tokens,
                       void* stream);

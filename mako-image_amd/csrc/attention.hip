@@ -26,7 +26,7 @@ namespace {
 struct AttnP {
     const uint16_t *q, *k, *vt;
     uint16_t* out;
-    uint32_t heads, batch, n_q, q_pad, n_k, k_pad, q_pos0, block;
+    uint32_t heads, group, batch, n_q, q_pad, n_k, k_pad, q_pos0, block; // group: query heads a key / value head
     int64_t ldo, so;
     float c; // scale * log2(e)
 };
@@ -72,10 +72,10 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     if (total % 8 == 0)
         item = (item % 8) * (total / 8) + item / 8;
     const uint32_t qb = item % nqb, head = (item / nqb) % p.heads, bi = item / (nqb * p.heads);
-    const int64_t bh = int64_t(bi) * p.heads + head;
+    const int64_t bh = int64_t(bi) * p.heads + head, bkv = int64_t(bi) * (p.heads / p.group) + head / p.group;
     const uint16_t* Q = p.q + bh * p.q_pad * D;
-    const uint16_t* K = p.k + bh * p.k_pad * D;
-    const uint16_t* VT = p.vt + bh * int64_t(D) * p.k_pad;
+    const uint16_t* K = p.k + bkv * p.k_pad * D;
+    const uint16_t* VT = p.vt + bkv * int64_t(D) * p.k_pad;
     const int q0 = int(qb) * 128 + wave * 32;
 
     bf16x8 qf[DS];
@@ -492,12 +492,14 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
 using namespace mk;
 
 extern "C" mk_status mk_attention(const void* q, const void* k, const void* vt, void* out, uint32_t batch,
-                                  uint32_t heads, uint32_t d, uint32_t n_q, uint32_t q_pad, uint32_t n_k,
-                                  uint32_t k_pad, int64_t ldo, int64_t stride_o, uint32_t q_pos0, uint32_t block,
-                                  float scale, void* stream)
+                                  uint32_t heads, uint32_t kv_heads, uint32_t d, uint32_t n_q, uint32_t q_pad,
+                                  uint32_t n_k, uint32_t k_pad, int64_t ldo, int64_t stride_o, uint32_t q_pos0,
+                                  uint32_t block, float scale, void* stream)
 {
     if (!q || !k || !vt || !out)
         return fail(MK_ERR_ARG, "attention: null pointer");
+    if (!heads || !kv_heads || heads % kv_heads)
+        return fail(MK_ERR_ARG, "attention: kv_heads must divide heads");
     if (d != 64 && d != 128)
         return fail(MK_ERR_ARG, "attention: head dim must be 64 or 128");
     if (n_q == 0 || n_k == 0 || n_q > q_pad || k_pad % kKT || n_k > k_pad)
@@ -505,7 +507,8 @@ extern "C" mk_status mk_attention(const void* q, const void* k, const void* vt, 
     if (ldo % 4 || (reinterpret_cast<uintptr_t>(out) & 7))
         return fail(MK_ERR_ARG, "attention: output rows must be 8-byte aligned");
     AttnP p{static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(vt),
-            static_cast<uint16_t*>(out), heads, batch, n_q, q_pad, n_k, k_pad, q_pos0, block, ldo, stride_o,
+            static_cast<uint16_t*>(out), heads, heads / kv_heads, batch, n_q, q_pad, n_k, k_pad, q_pos0, block, ldo,
+            stride_o,
             scale * 1.4426950408889634f};
     const dim3 grid(cdiv(n_q, 128) * heads * batch);
     hipStream_t s = static_cast<hipStream_t>(stream);

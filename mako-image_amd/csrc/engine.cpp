@@ -96,10 +96,40 @@ struct Timing {
     }
 };
 
+// The rope3 angles of one position (qwen_image.cpp:33-45): axes of 16, 56 and 56 dims, theta 10000, pairs (cos, sin).
+void rope3(float* cs, int64_t f, int64_t hpos, int64_t wpos)
+{
+    const int dims[3] = {16, 56, 56};
+    const int64_t pos[3] = {f, hpos, wpos};
+    int i = 0;
+    for (int a = 0; a < 3; ++a)
+        for (int j = 0; j < dims[a] / 2; ++j, ++i) {
+            const float inv = 1.0f / std::pow(10000.0f, float(2 * j) / float(dims[a]));
+            const float ang = float(pos[a]) * inv;
+            cs[2 * i] = std::cos(ang);
+            cs[2 * i + 1] = std::sin(ang);
+        }
+}
+
 } // namespace
 } // namespace mk
 
 using namespace mk;
+
+// The table begin builds (qwen_image.cpp:113-142): text row t at (t, t, t), image row S + y w + x at frame S and the
+// grid position centred as (y - (h - h / 2), x - (w - w / 2)).
+extern "C" mk_status mk_rope_table(uint32_t S, uint32_t h, uint32_t w, float* out)
+{
+    if (!out)
+        return fail(MK_ERR_ARG, "rope_table: null");
+    for (uint32_t t = 0; t < S; ++t)
+        rope3(out + uint64_t(t) * 128, t, t, t);
+    for (uint32_t y = 0; y < h; ++y)
+        for (uint32_t x = 0; x < w; ++x)
+            rope3(out + (uint64_t(S) + uint64_t(y) * w + x) * 128, S, int64_t(y) - int64_t(h - h / 2),
+                  int64_t(x) - int64_t(w - w / 2));
+    return MK_OK;
+}
 
 struct mk_engine {
     // 1 / sqrt(128) * log2(e): the QKV epilogue scales K by it, so attention takes its scores in log2 units
@@ -352,16 +382,19 @@ struct mk_engine {
     // Two GEMMs of equal N, K and epilogue kind (a block's image and text projections) in one launch.
     // Two GEMMs of equal N, K and epilogue kind (a block's image and text projections): one launch when that takes
     // fewer waves of tiles than two (the text's few tiles fill the image's last wave), else two.
-    mk_status gemm2(const mk_gemm_args (&g)[2])
+    // Timing classes: `cls` for the grouped launch, cls + ".img" / ".txt" when the two go separately.
+    mk_status gemm2(const mk_gemm_args (&g)[2], const char* cls)
     {
         const bool one = launch_cost(g, 2) < launch_cost(g, 1) + launch_cost(g + 1, 1);
         if (one) {
             const double fl = 2.0 * g[0].N * g[0].K * (double(g[0].M) * g[0].batch + double(g[1].M) * g[1].batch);
-            return timed("gemm", fl, [&] { return mk_gemm_grouped(g, 2, stream); });
+            return timed(cls, fl, [&] { return mk_gemm_grouped(g, 2, stream); });
         }
-        for (int i = 0; i < 2; ++i)
-            MK_TRY(timed("gemm", 2.0 * g[i].N * g[i].K * double(g[i].M) * g[i].batch,
+        for (int i = 0; i < 2; ++i) {
+            const std::string c = std::string(cls) + (i ? ".txt" : ".img");
+            MK_TRY(timed(c.c_str(), 2.0 * g[i].N * g[i].K * double(g[i].M) * g[i].batch,
                          [&] { return mk_gemm_grouped(g + i, 1, stream); }));
+        }
         return MK_OK;
     }
     // Estimated duration of a launch (the GEMM dispatch's own plan: tile width, waves, stream-K).
@@ -420,32 +453,12 @@ struct mk_engine {
         return MK_OK;
     }
 
-    // The rope3 table (qwen_image.cpp:31-45,132-141): text at (t, t, t), image at frame S with a centred grid.
-    static void rope3(float* cs, int64_t f, int64_t hpos, int64_t wpos)
-    {
-        const int dims[3] = {16, 56, 56};
-        const int64_t pos[3] = {f, hpos, wpos};
-        int i = 0;
-        for (int a = 0; a < 3; ++a)
-            for (int j = 0; j < dims[a] / 2; ++j, ++i) {
-                const float inv = 1.0f / std::pow(10000.0f, float(2 * j) / float(dims[a]));
-                const float ang = float(pos[a]) * inv;
-                cs[2 * i] = std::cos(ang);
-                cs[2 * i + 1] = std::sin(ang);
-            }
-    }
     mk_status make_rope(uint32_t S)
     {
         if (S == rope_S && !rope_host.empty())
             return MK_OK;
-        const uint64_t T = uint64_t(S) + uint64_t(gh) * gw;
-        rope_host.assign(T * 128, 0.0f);
-        for (uint32_t t = 0; t < S; ++t)
-            rope3(rope_host.data() + uint64_t(t) * 128, t, t, t);
-        for (uint32_t y = 0; y < gh; ++y)
-            for (uint32_t x = 0; x < gw; ++x)
-                rope3(rope_host.data() + (uint64_t(S) + y * gw + x) * 128, S, int64_t(y) - int64_t(gh - gh / 2),
-                      int64_t(x) - int64_t(gw - gw / 2));
+        rope_host.assign((uint64_t(S) + uint64_t(gh) * gw) * 128, 0.0f);
+        MK_TRY(mk_rope_table(S, gh, gw, rope_host.data()));
         MK_TRY(rope.ensure(rope_host.size() * 4));
         MK_HIP(hipMemcpy(rope.p, rope_host.data(), rope_host.size() * 4, hipMemcpyHostToDevice));
         rope_S = S;
@@ -579,9 +592,9 @@ struct mk_engine {
                 g[j] = gemm_args(B.qkv[s.which], s.xn->p, D, int64_t(s.rows) * D, s.rows, nb, nullptr, 0, 0,
                                  MK_EPI_HEADS, MK_BF16, nullptr, 0, 0, 0, &ha[j]);
             }
-            MK_TRY(gemm2(g));
+            MK_TRY(gemm2(g, "gemm.qkv"));
             MK_TRY(timed("attention", attn_flops, [&] {
-                return mk_attention(q.p, k.p, vt.p, att.p, nb, H, 128, T, q_pad, T, k_pad, D, int64_t(T) * D, 0, 0,
+                return mk_attention(q.p, k.p, vt.p, att.p, nb, H, H, 128, T, q_pad, T, k_pad, D, int64_t(T) * D, 0, 0,
                                     0.0f, stream);
             }));
             for (int j = 0; j < 2; ++j) {
@@ -590,19 +603,19 @@ struct mk_engine {
                 g[j] = gemm_args(B.o[s.which], a, D, int64_t(T) * D, s.rows, nb, s.x->p, D, int64_t(s.rows) * D,
                                  MK_EPI_GATE_ADD, MK_F32, s.m + 2 * D);
             }
-            MK_TRY(gemm2(g));
+            MK_TRY(gemm2(g, "gemm.o"));
             MK_TRY(ln2(4 * D, 3 * D));
             for (int j = 0; j < 2; ++j) {
                 const St& s = st[j];
                 g[j] = gemm_args(B.ff1[s.which], s.xn->p, D, 0, nb * s.rows, 1, s.hid, F, 0, MK_EPI_GELU_TANH, MK_BF16);
             }
-            MK_TRY(gemm2(g));
+            MK_TRY(gemm2(g, "gemm.ff1"));
             for (int j = 0; j < 2; ++j) {
                 const St& s = st[j];
                 g[j] = gemm_args(B.ff2[s.which], s.hid, F, 0, nb * s.rows, 1, s.x->p, D, 0, MK_EPI_GATE_ADD, MK_F32,
                                  s.m + 5 * D);
             }
-            MK_TRY(gemm2(g));
+            MK_TRY(gemm2(g, "gemm.ff2"));
             if (probe)
                 for (uint32_t b = 0; b < nb; ++b)
                     MK_TRY(probe_f32("block", int(i * nb + b), x_img.f() + size_t(b) * N * D, size_t(N) * D));
@@ -722,7 +735,7 @@ struct mk_engine {
                                         size_t(H) * 128, hipMemcpyDeviceToDevice, stream));
             }
             MK_TRY(timed("attention", 4.0 * pairs * 128 * H, [&] {
-                return mk_attention(q.p, k.p, vt.p, att.p, 1, H, 128, T, q_pad, n_k, k_pad, D, 0, row0, S, 0.0f,
+                return mk_attention(q.p, k.p, vt.p, att.p, 1, H, H, 128, T, q_pad, n_k, k_pad, D, 0, row0, S, 0.0f,
                                     stream);
             }));
             MK_TRY(gemm(B.o[0], att.p, D, 0, T, 1, x_img.p, D, 0, MK_EPI_GATE_TANH, MK_F32, mod.f() + D, 4 * D, split,
@@ -810,7 +823,7 @@ struct mk_engine {
                 return s;
             }));
             MK_TRY(timed("attention", 4.0 * double(n) * n * 64 * H * nb, [&] {
-                return mk_attention(q.p, k.p, vt.p, att.p, nb, H, 64, n, q_pad, n, k_pad, c, nc, 0, 0, scale, stream);
+                return mk_attention(q.p, k.p, vt.p, att.p, nb, H, H, 64, n, q_pad, n, k_pad, c, nc, 0, 0, scale, stream);
             }));
             MK_TRY(gemm(B.o[0], att.p, c, 0, nb * n, 1, hs, c, 0, MK_EPI_ADD, MK_F32));
             MK_TRY(timed("norm", 0, [&] { return mk_layer_norm(hs, nb * n, c, B.n2g, B.n2b, 1e-5f, xn_img.p, stream); }));
@@ -823,7 +836,7 @@ struct mk_engine {
             const uint16_t* kc = slots[0].ck.h() + size_t(i) * 2 * H * s_pad * 64;
             const uint16_t* vc = slots[0].cvt.h() + size_t(i) * 2 * H * 64 * s_pad;
             MK_TRY(timed("attention", 4.0 * double(n) * S * 64 * H * nb, [&] {
-                return mk_attention(q.p, kc, vc, att.p, nb, H, 64, n, q_pad, S, s_pad, c, nc, 0, 0, scale, stream);
+                return mk_attention(q.p, kc, vc, att.p, nb, H, H, 64, n, q_pad, S, s_pad, c, nc, 0, 0, scale, stream);
             }));
             MK_TRY(gemm(B.o[1], att.p, c, 0, nb * n, 1, hs, c, 0, MK_EPI_ADD, MK_F32));
             MK_TRY(timed("norm", 0, [&] { return mk_layer_norm(hs, nb * n, c, B.n3g, B.n3b, 1e-5f, xn_img.p, stream); }));
@@ -1028,6 +1041,7 @@ mk_status mk_step(mk_engine* e, const float* latents, size_t n, float sigma, uin
     }
     MK_HIP(hipMemcpyAsync(out, e->out.p, N * L * 4, hipMemcpyDeviceToHost, e->stream));
     MK_HIP(hipStreamSynchronize(e->stream));
+    MK_TRY(gemm_take_error());
     MK_TRY(e->finish_timing());
     return MK_OK;
 }
@@ -1108,6 +1122,7 @@ mk_status mk_step_cfg(mk_engine* e, const float* latents, size_t n, float sigma,
     MK_HIP(hipMemcpy(in.p, latents, n * 4, hipMemcpyHostToDevice));
     MK_TRY(mk_step_cfg_device(e, in.f(), sigma, sigma_next, guidance, out.f(), nullptr));
     MK_HIP(hipStreamSynchronize(e->stream));
+    MK_TRY(gemm_take_error());
     MK_HIP(hipMemcpy(latents_out, out.p, n * 4, hipMemcpyDeviceToHost));
     return MK_OK;
 }
@@ -1179,7 +1194,7 @@ mk_status mk_generate(mk_engine* e, const float* noise, size_t n, const float* s
     }
     MK_HIP(hipMemcpyAsync(latents_out, x[steps % 2].p, n * 4, hipMemcpyDeviceToHost, e->stream));
     MK_HIP(hipStreamSynchronize(e->stream));
-    return MK_OK;
+    return gemm_take_error();
 }
 
 mk_status mk_engine_stream(mk_engine* e, void** stream)
@@ -1236,6 +1251,7 @@ mk_status mk_sdxl_forward(mk_engine* e, const float* x, uint32_t batch, uint32_t
     (void)stream;
     MK_TRY(e->sdxl_forward(x, batch, n, y));
     MK_HIP(hipStreamSynchronize(e->stream));
+    MK_TRY(gemm_take_error());
     MK_TRY(e->finish_timing());
     return MK_OK;
 }

@@ -15,8 +15,10 @@
 // along M.
 #include "common.hpp"
 
+#include <memory>
 #include <mutex>
 #include <type_traits>
+#include <vector>
 
 namespace mk {
 
@@ -352,7 +354,9 @@ __device__ inline void epi_heads(const GemmP& p, const float* st, int ld, int to
 struct SkP {
     float* ws;          // [2 grid][threads * accumulators] partials, two slots a workgroup (its first and last tile)
     uint32_t* flags;    // [2 grid]: set to epoch when the slot holds this launch's partial
+    uint32_t* err;      // host-visible word: set to 1 when a wait for a partial gave up (the host reports it)
     uint32_t epoch;
+    uint32_t polls;     // bound of a wait for a partial's flag (polls of ~128 cycles each)
     uint32_t total;     // tiles over both problems
     uint32_t dp;        // tiles done whole, round robin over the grid (a multiple of it)
     uint32_t kt;        // k steps a tile
@@ -780,11 +784,17 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
                 // the tile's highest workgroup), and a workgroup publishes before it waits on anything; the bound
                 // only keeps a broken launch from spinning forever
                 const int slot = sk_slot(*sk, uint32_t(i), tt);
-                for (uint32_t n = 0; n < (1u << 26); ++n) {
-                    if (__hip_atomic_load(sk->flags + slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == sk->epoch)
+                bool seen = false;
+                for (uint32_t n = 0; n < sk->polls; ++n) {
+                    if (__hip_atomic_load(sk->flags + slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == sk->epoch) {
+                        seen = true;
                         break;
+                    }
                     __builtin_amdgcn_s_sleep(2);
                 }
+                // gave up: the tile is finished from what the slot holds, and the host turns the word into an error
+                if (!seen)
+                    __hip_atomic_store(sk->err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
             }
         __syncthreads();
         // The other ranges' partials, in index order, each in passes of QL 16-byte groups: every wave streams its
@@ -935,20 +945,85 @@ __global__ __launch_bounds__(64 * NW, 1) __attribute__((amdgpu_waves_per_eu(NW /
     }
 }
 
-// Stream-K workspace of a device: two partial slots and flags per workgroup of a one-a-CU grid, and the launch epoch
-// the flags are compared with (so they never need clearing). Launches that use it on one device must not overlap.
-// It is uncached device memory: a partial written by a CU of one XCD is read by a CU of another, whose L2 is not
-// coherent with the writer's for ordinary allocations. Allocated once at its full size and never freed (uncached
-// memory a kernel has read stays allocated until the process ends).
+// Stream-K workspaces: two partial slots and flags per workgroup of a one-a-CU grid, and the launch epoch the flags
+// are compared with (so they never need clearing). A workspace serves one launch at a time: a launch takes the
+// workspace its stream used last (stream order keeps the two apart), else one whose last launch has completed (its
+// event), else a new one, and past kSkPool workspaces a device's least recently used one after its last launch (the
+// stream waits for that launch's event). Streams of one device thus never share partials in flight.
+// The memory is uncached: a partial written by a CU of one XCD is read by a CU of another, whose L2 is not coherent
+// with the writer's for ordinary allocations. Allocated at the full size and never freed (uncached memory a kernel has
+// read stays allocated until the process ends). The error word is pinned host memory the kernel writes when a wait
+// gives up; the host checks it at every launch and synchronisation (sk_take_error).
 struct SkWork {
     float* ws = nullptr;
     size_t ws_bytes = 0;
     uint32_t* flags = nullptr;
-    uint32_t nflags = 0, epoch = 0, cus = 0;
+    uint32_t nflags = 0, epoch = 0;
+    uint32_t* err = nullptr;
+    hipStream_t last = nullptr;
+    hipEvent_t done = nullptr;
+    uint64_t used = 0; // launch counter at its last use (least recently used first)
+};
+struct SkDevice {
+    uint32_t cus = 0;
+    uint64_t launches = 0;
+    std::vector<std::unique_ptr<SkWork>> pool;
 };
 constexpr int kMaxDevices = 64;
+constexpr size_t kSkPool = 4;
+constexpr uint32_t kSkPollsDefault = 1u << 26;
 std::mutex g_sk_mutex;
-SkWork g_sk[kMaxDevices];
+SkDevice g_sk[kMaxDevices];
+uint32_t g_sk_polls = kSkPollsDefault;
+
+// A workspace for one stream-K launch of `need` partial bytes on stream s (g_sk_mutex held).
+mk_status sk_acquire(SkDevice& D, hipStream_t s, size_t need, uint32_t nflags, SkWork*& out)
+{
+    SkWork* pick = nullptr;
+    for (auto& w : D.pool)
+        if (w->last == s && w->ws_bytes >= need && w->nflags >= nflags)
+            pick = w.get();
+    if (!pick)
+        for (auto& w : D.pool)
+            if (w->ws_bytes >= need && w->nflags >= nflags && hipEventQuery(w->done) == hipSuccess) {
+                pick = w.get();
+                break;
+            }
+    if (!pick && D.pool.size() < kSkPool) {
+        auto w = std::make_unique<SkWork>();
+        MK_HIP(hipExtMallocWithFlags(reinterpret_cast<void**>(&w->ws), need, hipDeviceMallocUncached));
+        w->ws_bytes = need;
+        MK_HIP(hipExtMallocWithFlags(reinterpret_cast<void**>(&w->flags), nflags * sizeof(uint32_t),
+                                     hipDeviceMallocUncached));
+        MK_HIP(hipMemset(w->flags, 0, nflags * sizeof(uint32_t)));
+        MK_HIP(hipStreamSynchronize(nullptr)); // cleared before the launch's stream reads them
+        w->nflags = nflags;
+        MK_HIP(hipHostMalloc(reinterpret_cast<void**>(&w->err), sizeof(uint32_t), hipHostMallocCoherent));
+        *w->err = 0;
+        MK_HIP(hipEventCreateWithFlags(&w->done, hipEventDisableTiming));
+        pick = w.get();
+        D.pool.push_back(std::move(w));
+    }
+    if (!pick) {
+        for (auto& w : D.pool)
+            if (w->ws_bytes >= need && w->nflags >= nflags && (!pick || w->used < pick->used))
+                pick = w.get();
+        if (!pick)
+            return fail(MK_ERR_UNSUPPORTED, "gemm: stream-K workspaces smaller than this launch needs");
+        MK_HIP(hipStreamWaitEvent(s, pick->done, 0));
+    }
+    out = pick;
+    return MK_OK;
+}
+
+// A stream-K wait that gave up on a device (g_sk_mutex held): MK_ERR_DEVICE once, then cleared.
+mk_status sk_check(SkDevice& D)
+{
+    for (auto& w : D.pool)
+        if (__atomic_exchange_n(w->err, 0u, __ATOMIC_RELAXED))
+            return fail(MK_ERR_DEVICE, "gemm: a stream-K launch gave up waiting for a partial tile; its output is wrong");
+    return MK_OK;
+}
 
 template <int BM, int BN, bool kF8, int EK, int NW = 4>
 mk_status launch(GemmP* p, uint32_t count, const GemmPlan& plan, hipStream_t s)
@@ -970,38 +1045,34 @@ mk_status launch(GemmP* p, uint32_t count, const GemmPlan& plan, hipStream_t s)
         if (dev < 0 || dev >= kMaxDevices)
             return fail(MK_ERR_DEVICE, "gemm: device index out of range");
         std::lock_guard<std::mutex> lock(g_sk_mutex);
-        SkWork& W = g_sk[dev];
-        if (!W.cus) {
+        SkDevice& D = g_sk[dev];
+        if (!D.cus) {
             int n = 0;
             MK_HIP(hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev));
-            W.cus = n > 0 ? uint32_t(n) : 1;
+            D.cus = n > 0 ? uint32_t(n) : 1;
         }
-        const uint32_t grid = W.cus;
+        const uint32_t grid = D.cus;
         if (plan.sk && plan.dp % grid == 0 && plan.dp < tiles) {
+            MK_TRY(sk_check(D));
             SkP sk{};
             sk.total = tiles;
             sk.dp = uint32_t(plan.dp);
             sk.kt = kt;
             sk.units = uint64_t(tiles - sk.dp) * kt;
-            const size_t need = size_t(2) * grid * NT * NACC * sizeof(float);
-            if (!W.ws) {
-                MK_HIP(hipExtMallocWithFlags(reinterpret_cast<void**>(&W.ws), need, hipDeviceMallocUncached));
-                W.ws_bytes = need;
-                MK_HIP(hipExtMallocWithFlags(reinterpret_cast<void**>(&W.flags), 2 * grid * sizeof(uint32_t),
-                                             hipDeviceMallocUncached));
-                MK_HIP(hipMemset(W.flags, 0, 2 * grid * sizeof(uint32_t)));
-                MK_HIP(hipStreamSynchronize(nullptr)); // cleared before the launch's stream reads them
-                W.nflags = 2 * grid;
-            }
-            if (W.ws_bytes < need || W.nflags < 2 * grid)
-                return fail(MK_ERR_UNSUPPORTED, "gemm: stream-K workspace smaller than this launch needs");
-            if (++W.epoch == 0)
-                W.epoch = 1;
-            sk.ws = W.ws;
-            sk.flags = W.flags;
-            sk.epoch = W.epoch;
+            SkWork* W = nullptr;
+            MK_TRY(sk_acquire(D, s, size_t(2) * grid * NT * NACC * sizeof(float), 2 * grid, W));
+            if (++W->epoch == 0)
+                W->epoch = 1;
+            sk.ws = W->ws;
+            sk.flags = W->flags;
+            sk.err = W->err;
+            sk.epoch = W->epoch;
+            sk.polls = g_sk_polls;
             gemm_sk_kernel<BM, BN, kF8, EK, NW><<<grid, NT, 0, s>>>(G, sk);
             MK_HIP(hipGetLastError());
+            MK_HIP(hipEventRecord(W->done, s));
+            W->last = s;
+            W->used = ++D.launches;
             return MK_OK;
         }
     }
@@ -1075,6 +1146,15 @@ mk_status prepare(const mk_gemm_args* a, GemmP& p)
 }
 
 } // namespace gemm_detail
+
+mk_status gemm_take_error()
+{
+    using namespace gemm_detail;
+    std::lock_guard<std::mutex> lock(g_sk_mutex);
+    for (SkDevice& D : g_sk)
+        MK_TRY(sk_check(D));
+    return MK_OK;
+}
 
 // Tile width: 256 x 256 tiles once there is a wave of them, else 256 x 128, else 256 x 64 (N = 64: stores, residuals);
 // heads epilogues always 256. Stream-K for 256-wide tiles when the last partial wave would leave a twentieth or more
@@ -1179,6 +1259,13 @@ extern "C" mk_status mk_gemm_grouped(const mk_gemm_args* a, uint32_t count, void
 }
 
 extern "C" mk_status mk_gemm(const mk_gemm_args* a, void* stream) { return mk_gemm_grouped(a, 1, stream); }
+
+extern "C" mk_status mk_gemm_set_wait_limit(uint32_t polls)
+{
+    std::lock_guard<std::mutex> lock(g_sk_mutex);
+    g_sk_polls = polls;
+    return MK_OK;
+}
 
 // 3 x 3 convolution as one GEMM over the padded pixel grid: output row r (grid pixel r of (h + 2) x (w + 2)) and tap
 // (dy, dx) read input row r + dy (w + 2) + dx of x, whose w + 3 slack rows before the grid make every shift

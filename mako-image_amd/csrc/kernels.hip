@@ -586,9 +586,13 @@ __device__ inline uint8_t e4m3_encode(float x)
     const float a = fabsf(x);
     if (!(a < 448.0f))
         return sign | 0x7e;
-    int e;
-    frexpf(a, &e); // a = f * 2^e, f in [0.5, 1): binade 2^(e-1)
-    int b = max(e - 1, -6); // subnormals share the step of binade -6
+    // the binade 2^b of a: subnormals (and zero, for which frexpf reports exponent 0) share the step of binade -6
+    int b = -6;
+    if (a >= 0x1p-6f) {
+        int e;
+        frexpf(a, &e); // a = f * 2^e, f in [0.5, 1)
+        b = e - 1;
+    }
     const float step = ldexpf(1.0f, b - 3);
     const float q = rintf(a / step); // exact scaling by a power of two, then round half to even
     int code;

@@ -86,12 +86,13 @@ _SIGS = {
     "mk_event_elapsed_ms": (_i, [_vp, _vp, C.POINTER(_f)]),
     "mk_gemm": (_i, [C.POINTER(GemmArgs), _vp]),
     "mk_gemm_grouped": (_i, [_vp, _u32, _vp]),
+    "mk_gemm_set_wait_limit": (_i, [_u32]),
     "mk_gemv": (_i, [_vp, _u32, _u32, _vp, _vp, _u32, _vp, _i, _vp]),
     "mk_ln_modulate": (_i, [_vp, _u32, _u32, _vp, _vp, _i64, _u32, _u32, _f, _vp, _vp]),
     "mk_gate_add": (_i, [_vp, _vp, _u32, _u32, _u32, _vp, _i64, _u32, _u32, _i, _vp]),
     "mk_heads": (_i, [_vp, _u32, _u32, _i64, _i64, _u32, _u32, _u32, _vp, _f, _vp, _u32, _vp, _u32, _u32, _i, _vp]),
-    "mk_attention": (_i, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _i64, _i64, _u32, _u32, _f,
-                          _vp]),
+    "mk_attention": (_i, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _i64, _i64, _u32, _u32,
+                          _f, _vp]),
     "mk_silu": (_i, [_vp, _sz, _vp]),
     "mk_gelu_tanh": (_i, [_vp, _sz, _vp]),
     "mk_swiglu": (_i, [_vp, _u32, _u32, _u32, _vp, _vp]),
@@ -100,6 +101,7 @@ _SIGS = {
     "mk_layer_norm": (_i, [_vp, _u32, _u32, _vp, _vp, _f, _vp, _vp]),
     "mk_group_norm": (_i, [_vp, _u32, _u32, _u32, _u32, _vp, _vp, _f, _vp, _vp]),
     "mk_cfg_euler": (_i, [_vp, _vp, _vp, _sz, _f, _f, _vp, _vp]),
+    "mk_rope_table": (_i, [_u32, _u32, _u32, _vp]),
     "mk_patchify": (_i, [_vp, _u32, _u32, _u32, _u32, _vp, _vp]),
     "mk_unpatchify": (_i, [_vp, _u32, _u32, _u32, _u32, _vp, _vp]),
     "mk_fill_normal": (_i, [_vp, _sz, _u32, _u64, _d, _d, _vp]),
@@ -184,8 +186,37 @@ def call(name, *args):
 _NP = {F32: np.float32, BF16: np.uint16, FP8: np.uint8}
 
 
+# Device memory of dropped Dev objects: freed only after a device-wide synchronisation, so a pointer taken from a
+# temporary (`Dev.from_array(x).p` passed to a call) stays valid for every kernel queued before the object went away.
+_pending = []
+_pending_bytes = 0
+_pending_status = 0
+_PENDING_LIMIT = 1 << 30
+
+
+def _free_pending():
+    global _pending_bytes
+    while _pending:
+        _lib.mk_free(_pending.pop())
+    _pending_bytes = 0
+
+
+def _release(p, nbytes):
+    global _pending_bytes, _pending_status
+    _pending.append(p)
+    _pending_bytes += nbytes
+    if _pending_bytes >= _PENDING_LIMIT:
+        # a finaliser cannot raise: a failed synchronisation is kept for the next sync() to report
+        st = _lib.mk_synchronize()
+        if st != 0 and not _pending_status:
+            _pending_status = st
+        if st == 0:
+            _free_pending()
+
+
 class Dev:
-    """A device allocation (zero-filled), freed with the object."""
+    """A device allocation (zero-filled). Dropping the object releases it after the next device-wide
+    synchronisation (sync()), never before work already queued on it has run."""
 
     def __init__(self, nbytes):
         p = _vp()
@@ -213,7 +244,7 @@ class Dev:
 
     def __del__(self):
         if getattr(self, "p", None) and _lib is not None:
-            _lib.mk_free(self.p)
+            _release(self.p, self.nbytes)
             self.p = None
 
     def __int__(self):
@@ -221,7 +252,13 @@ class Dev:
 
 
 def sync():
+    """Waits for all device work, then frees the memory of dropped Dev objects."""
+    global _pending_status
     call("mk_synchronize")
+    _free_pending()
+    if _pending_status:
+        st, _pending_status = _pending_status, 0
+        check(st, "mk_synchronize (from a release)")
 
 
 def device_info(dev=0):
@@ -525,6 +562,13 @@ def sigmas(steps, tokens, terminal=0.0, mu=None, base_seq=256.0, max_seq=4096.0,
     sc = Schedule(base_seq, max_seq, base_shift, max_shift, terminal, mu is not None, 0.0 if mu is None else mu)
     out = np.empty(steps + 1, np.float32)
     call("mk_sigmas", steps, tokens, C.byref(sc), out.ctypes.data)
+    return out
+
+
+def rope_table(S, h, w):
+    """The RoPE table mk_begin uploads: [S + h*w][64][2] float32 (cos, sin)."""
+    out = np.empty((S + h * w, 64, 2), np.float32)
+    call("mk_rope_table", S, h, w, out.ctypes.data)
     return out
 
 

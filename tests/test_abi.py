@@ -79,3 +79,13 @@ def test_sigmas_fixed_shift_and_errors():
     assert np.array_equal(mkimage.sigmas(5, 1, mu=0.7), mkimage.sigmas(5, 123456, mu=0.7))
     with __import__("pytest").raises(mkimage.MkError, match="max_seq"):
         mkimage.sigmas(4, 256, base_seq=100.0, max_seq=100.0)
+
+
+def test_rope_table_is_the_oracle_table_bit_for_bit():
+    # the engine uploads mk_rope_table's output; the oracle's table is pinned to the closed form in test_oracle.py
+    import numpy as np
+
+    for S, h, w in [(256, 64, 64), (7, 5, 3), (0, 4, 6), (512, 128, 128), (41, 1, 1)]:
+        got = mkimage.rope_table(S, h, w)
+        want = mkref.rope_table(S, h, w)
+        assert got.view(np.uint32).tobytes() == want.view(np.uint32).tobytes(), (S, h, w)

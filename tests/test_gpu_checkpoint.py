@@ -291,3 +291,32 @@ def test_lora_errors_leave_weights_alone(gpu, tmp_path):
     with pytest.raises(M.MkError, match="DoRA"):
         e.add_lora(p)
     same_state(before, state(e))
+
+
+def test_lora_merge_fp8_exact_zeros(gpu, tmp_path):
+    # Merged values that are exactly zero encode as zero: a row of zero codes whose LoRA rows are zero stays a zero
+    # row (scale 1), and columns whose weights and LoRA columns are zero stay zero in every row.
+    rng = np.random.default_rng(3)
+    e = M.Engine(M.FAMILY_DUAL, **TINY, weight_dtype=M.FP8)
+    e.init_random(14)
+    D = TINY["dim"]
+    name = "transformer_blocks.0.attn.to_k.weight"
+    codes = e.fetch(name, M.FP8, D, D).copy()
+    scale = e.fetch(name + ".scale", M.F32, D, 1).copy()
+    codes[5] = 0
+    codes[:, :16] = 0
+    e.load(name, codes, M.FP8)
+    e.load(name + ".scale", scale, M.F32)
+    a, b = lora_pair(rng, D, D, 8)
+    a[:, :16] = 0
+    b[5] = 0
+    save_file({"transformer_blocks.0.attn.to_k.lora_A.weight": a, "transformer_blocks.0.attn.to_k.lora_B.weight": b},
+              str(tmp_path / "z.safetensors"))
+    assert e.add_lora(tmp_path / "z.safetensors", 1.0) == (1, 0)
+    got = e.fetch(name, M.FP8, D, D)
+    got_scale = e.fetch(name + ".scale", M.F32, D, 1)
+    table = R.e4m3_table()
+    assert got_scale[5] == 1.0
+    assert (table[got[5]] == 0).all()
+    assert (table[got[:, :16]] == 0).all()
+    assert (table[got[np.arange(D) != 5][:, 16:]] != 0).mean() > 0.9

@@ -1,0 +1,155 @@
+"""Parity at the workload sizes of the fp8 2048x2048 step and of the SDXL transformer stages, through the C ABI.
+
+- fp8 step at 2048x2048 (16384 image + 512 text tokens, CFG batch 2, 60 blocks, e4m3 weights with per-channel
+  scales): the attention kernel on the engine's path (K carrying the softmax scale in log2 units) over all 16896 keys
+  on 48 sampled query rows per (batch, head) against the oracle's softmax; the four block GEMMs with fp8 weights at
+  2 x 16384 image + 2 x 512 text rows (grouped as the engine launches them) on 48 sampled rows against the oracle's
+  GEMM of the same device-drawn operands; the whole 60-block step twice from the same latents: finite and bit-identical.
+- SDXL: one block of stage B (1024 tokens x 1280 channels, 20 heads x 64) and one of stage A at its full 4096 tokens
+  (640 channels, 10 heads x 64) against the oracle's trans_fwd (sdxl.cpp:742-796).
+Tolerances as everywhere: cosine >= 0.9995, max|g - w| / max|w| <= 2e-2 (bf16), 5e-2 (fp8)."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import mkimage as M
+import mkref as R
+from test_gpu_engine import make_pair, within
+
+pytestmark = pytest.mark.gpu
+
+D, H, F, E = 3072, 24, 12288, 3584
+N5, S5 = 16384, 512  # 2048x2048: a 128 x 128 token grid, 512 text tokens
+T5 = N5 + S5
+
+
+def rows_of(d, ld, rows, esize, dtype):
+    """Rows `rows` of a row-major device matrix of row length ld (elements of esize bytes)."""
+    out = np.empty((len(rows), ld), dtype)
+    for i, r in enumerate(rows):
+        M.call("mk_memcpy_d2h", out[i].ctypes.data, d.p + int(r) * ld * esize, ld * esize)
+    return out
+
+
+def test_fp8_2048_attention_sampled_rows(gpu):
+    B = 2
+    rng = np.random.default_rng(40)
+    q_pad = k_pad = T5  # 16896 = 66 x 256
+    q = R.bf16_round(rng.standard_normal((B, H, T5, 128)).astype(np.float32))
+    # the engine's QKV epilogue scales K by 1/sqrt(128) log2(e): attention then runs with scale 0
+    k = R.bf16_round(rng.standard_normal((B, H, T5, 128)).astype(np.float32) * np.float32(np.log2(np.e) / np.sqrt(128)))
+    v = R.bf16_round(rng.standard_normal((B, H, T5, 128)).astype(np.float32))
+    vt = np.empty((B, H, 128, k_pad), np.float32)
+    vt[:, :, :, M.vt_col(np.arange(T5))] = v.transpose(0, 1, 3, 2)
+    Q, K, V = (M.Dev.from_array(M.bf16_bits(a)) for a in (q, k, vt))
+    del vt
+    O = M.Dev(B * T5 * D * 2)
+    M.call("mk_attention", Q.p, K.p, V.p, O.p, B, H, H, 128, T5, q_pad, T5, k_pad, D, T5 * D, 0, 0, 0.0, None)
+    M.sync()
+    got = M.bf16_to_f32(O.to_array(np.uint16, (B, T5, D)))
+    rows = np.sort(rng.choice(T5, 48, replace=False))
+    want = R.attention(np.ascontiguousarray(q[:, :, rows]), k, v, float(np.log(2.0)))
+    for b in range(B):
+        within(got[b, rows], want[b], 128, cos=0.9999, max_rel=2e-2)
+
+
+def _fill(d, n, dtype, key, std):
+    M.call("mk_fill_normal", d.p, n, dtype, key, 0.0, std, None)
+
+
+@pytest.mark.parametrize("name,N,K,epi", [("qkv", 3 * D, D, M.EPI_STORE), ("o", D, D, M.EPI_GATE_ADD),
+                                          ("ff1", F, D, M.EPI_GELU_TANH), ("ff2", D, F, M.EPI_GATE_ADD)])
+def test_fp8_2048_block_gemms_sampled_rows(gpu, name, N, K, epi):
+    # image rows (2 x 16384) and text rows (2 x 512) with their own fp8 weights, one grouped launch, as the engine runs
+    # a block's projection at 2048x2048
+    rng = np.random.default_rng(41)
+    gated = epi == M.EPI_GATE_ADD
+    probs = []
+    for j, Mr in enumerate((2 * N5, 2 * S5)):
+        A = M.Dev(Mr * K * 2)
+        _fill(A, Mr * K, M.BF16, 1000 + 10 * j, 1.0)
+        Wb = M.Dev(N * K * 2)
+        _fill(Wb, N * K, M.BF16, 1001 + 10 * j, 0.02)
+        W8, sc = M.Dev(N * K), M.Dev(N * 4)
+        M.call("mk_quantize_fp8_rows", Wb.p, N, K, W8.p, sc.p, None)
+        bias = M.Dev.from_array(rng.standard_normal(N).astype(np.float32) * 0.1)
+        gate = M.Dev.from_array(rng.standard_normal(N).astype(np.float32))
+        Cd = M.Dev(Mr * N * (4 if gated or epi == M.EPI_STORE else 2))
+        if gated:
+            _fill(Cd, Mr * N, M.F32, 1002 + 10 * j, 1.0)
+        probs.append(dict(Mr=Mr, A=A, W8=W8, sc=sc, bias=bias, gate=gate, C=Cd))
+    M.sync()
+    rows = [np.sort(rng.choice(p["Mr"], 48, replace=False)) for p in probs]
+    before = [rows_of(p["C"], N, r, 4, np.float32) if gated else None for p, r in zip(probs, rows)]
+    args = []
+    for p in probs:
+        g = M.GemmArgs()
+        g.a, g.w, g.wscale, g.bias, g.c = p["A"].p, p["W8"].p, p["sc"].p, p["bias"].p, p["C"].p
+        g.gate = p["gate"].p if gated else None
+        g.seg_rows = 0
+        g.M, g.N, g.K = p["Mr"], N, K
+        g.lda, g.ldc, g.batch = K, N, 1
+        g.w_dtype, g.epilogue = M.FP8, epi
+        g.c_dtype = M.BF16 if epi == M.EPI_GELU_TANH else M.F32
+        args.append(g)
+    arr = (M.GemmArgs * 2)(*args)
+    M.call("mk_gemm_grouped", C.cast(arr, C.c_void_p), 2, None)
+    M.sync()
+    table = R.e4m3_table()
+    for p, r, x0 in zip(probs, rows, before):
+        a = M.bf16_to_f32(rows_of(p["A"], K, r, 2, np.uint16))
+        w = table[p["W8"].to_array(np.uint8, (N, K))]  # e4m3 values (exact in bf16); the scale per output channel
+        y = R.gemm(a, w, p["bias"].to_array(np.float32, (N,)), wscale=p["sc"].to_array(np.float32, (N,)))
+        if epi == M.EPI_GELU_TANH:
+            got = M.bf16_to_f32(rows_of(p["C"], N, r, 2, np.uint16))
+            want = R.gelu_tanh(y)
+        else:
+            got = rows_of(p["C"], N, r, 4, np.float32)
+            want = x0.astype(np.float64) + p["gate"].to_array(np.float32, (N,)) * y if gated else y
+        within(got - (x0 if gated else 0), want - (x0 if gated else 0), N, cos=0.99999, max_rel=1e-2)
+
+
+def test_fp8_2048_step_twice_finite_and_bit_identical(gpu):
+    # the benchmark's fp8 2048x2048 step (60 blocks, CFG batch 2): two runs from the same latents agree bit for bit
+    e = M.Engine(M.FAMILY_DUAL, blocks=60, dim=D, heads=H, head_dim=128, ffn=F, text_dim=E, weight_dtype=M.FP8)
+    e.init_random(0)
+    rng = np.random.default_rng(42)
+    for s in (0, 1):
+        e.begin(rng.standard_normal((S5, E)).astype(np.float32), 128, 128, s)
+    lat = M.Dev.from_array(rng.standard_normal((N5, 64)).astype(np.float32))
+    outs = []
+    for _ in range(2):
+        o = M.Dev(N5 * 64 * 4)
+        e.step_cfg_device(lat, 0.9, 0.85, 4.0, o, e.stream())
+        M.call("mk_stream_synchronize", e.stream())
+        outs.append(o.to_array(np.float32, (N5, 64)))
+    x = lat.to_array(np.float32, (N5, 64))
+    assert np.isfinite(outs[0]).all()
+    assert np.array_equal(outs[0], outs[1])
+    upd = outs[0] - x
+    assert 0 < np.abs(upd).max() < 1e3  # a real, bounded update of the latents
+    e.close()
+
+
+SDXL_B = dict(blocks=1, dim=1280, heads=20, head_dim=64, ffn=5120, text_dim=2048)
+SDXL_A = dict(blocks=1, dim=640, heads=10, head_dim=64, ffn=2560, text_dim=2048)
+
+
+@pytest.mark.parametrize("dims,side", [(SDXL_B, 32), (SDXL_A, 64)])
+def test_sdxl_stage_block_matches_oracle(gpu, dims, side):
+    # stage B: 1024 tokens x 1280 channels, 20 heads; stage A at its full 4096 tokens; batch 2 (CFG) with 77-token
+    # contexts of width 2048
+    m, e = make_pair(M.FAMILY_SDXL, dims=dims, wstd=0.05)
+    rng = np.random.default_rng(43)
+    n, S, c = side * side, 77, dims["dim"]
+    x = rng.standard_normal((2, n, c)).astype(np.float32)
+    ctx = rng.standard_normal((2, S, 2048)).astype(np.float32)
+    for s in (0, 1):
+        e.begin(ctx[s], side, side, s)
+    xd, yd = M.Dev.from_array(x), M.Dev(x.nbytes)
+    e.sdxl_forward(xd, 2, n, yd)
+    got = yd.to_array(np.float32, x.shape)
+    for b in range(2):
+        want = m.sdxl_trans(x[b], ctx[b])
+        within(got[b] - x[b], want - x[b], c)

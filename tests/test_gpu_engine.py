@@ -163,7 +163,7 @@ def test_attention_full_size_sampled_rows(gpu):
         M.call("mk_heads", X.p, B, T, 3 * D, T * 3 * D, col0, H, 128, w_.p if w_ else None, 1e-6,
                None if tr else csd.p, 0 if tr else 2, out.p, pad, 0, tr, None)
     O = M.Dev(B * T * D * 2)
-    M.call("mk_attention", Q.p, K.p, V.p, O.p, B, H, 128, T, q_pad, T, k_pad, D, T * D, 0, 0,
+    M.call("mk_attention", Q.p, K.p, V.p, O.p, B, H, H, 128, T, q_pad, T, k_pad, D, T * D, 0, 0,
            float(1 / np.sqrt(128)), None)
     M.sync()
     got = M.bf16_to_f32(O.to_array(np.uint16, (B, T, D)))

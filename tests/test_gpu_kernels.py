@@ -326,6 +326,95 @@ def test_gemm_stream_k_matches_oracle_and_repeats(gpu, rng, epi, cdt, w8):
             assert np.abs(outs[0][i] - want).max() <= 2 ** -8 * np.abs(want).max() + 1e-6
 
 
+def _sk_problem(rng, K=6144):
+    """A grouped gated-residual GEMM that runs stream-K: 8192 + 512 rows x 3072 x K (408 tiles of 256 x 256, 1.6 waves
+    on 256 compute units, K of 96 k steps)."""
+    N = 3072
+    shapes = (8192, 512)
+    A = [R.bf16_round(rng.standard_normal((Mr, K)).astype(np.float32)) for Mr in shapes]
+    W = R.bf16_round(rng.standard_normal((N, K)).astype(np.float32) * 0.02)
+    b = rng.standard_normal(N).astype(np.float32)
+    gt = rng.standard_normal(N).astype(np.float32)
+    X = [rng.standard_normal((Mr, N)).astype(np.float32) for Mr in shapes]
+    return dict(N=N, K=K, shapes=shapes, A=A, W=W, b=b, gt=gt, X=X, Ad=[bdev(a) for a in A], Wd=bdev(W), bd=dev(b),
+                gd=dev(gt))
+
+
+def _sk_launch(P, stream=None):
+    cs = [dev(x) for x in P["X"]]
+    args = [gemm_args(a, P["Wd"], bias=P["bd"], c=c, epi=M.EPI_GATE_ADD, M_=(Mr, P["N"], P["K"]), lda=P["K"],
+                      ldc=P["N"], gate=P["gd"]) for a, c, Mr in zip(P["Ad"], cs, P["shapes"])]
+    arr = (M.GemmArgs * 2)(*args)
+    _live.append(arr)
+    M.call("mk_gemm_grouped", C.cast(arr, C.c_void_p), 2, stream)
+    return cs
+
+
+def test_gemm_stream_k_long_k_matches_oracle_and_repeats(gpu, rng):
+    P = _sk_problem(rng)
+    outs = []
+    for _ in range(2):
+        cs = _sk_launch(P)
+        M.sync()
+        outs.append([fetch(c, (Mr, P["N"])) for c, Mr in zip(cs, P["shapes"])])
+    for i, Mr in enumerate(P["shapes"]):
+        assert np.array_equal(outs[0][i], outs[1][i])  # the fixed reduction order repeats bit for bit
+        rows = np.sort(rng.choice(Mr, 48, replace=False))
+        want = P["X"][i][rows].astype(np.float64) + P["gt"] * R.gemm(P["A"][i][rows], P["W"], P["b"])
+        assert maxrel(outs[0][i][rows], want) < 1e-5
+
+
+def test_gemm_stream_k_on_two_streams_at_once(gpu, rng):
+    # two streams issue stream-K launches concurrently (each its own workspace): every result equals the same
+    # launch run alone
+    P = [_sk_problem(np.random.default_rng(s)) for s in (21, 22)]
+    alone = []
+    for p in P:
+        cs = _sk_launch(p)
+        M.sync()
+        alone.append([fetch(c, (Mr, p["N"])) for c, Mr in zip(cs, p["shapes"])])
+    streams = []
+    for _ in range(2):
+        h = C.c_void_p()
+        M.call("mk_stream_create", C.byref(h))
+        streams.append(h.value)
+    try:
+        runs = []
+        for _ in range(3):
+            for p, st in zip(P, streams):
+                runs.append((p, _sk_launch(p, st), len(runs) % 2))
+        for st in streams:
+            M.call("mk_stream_synchronize", st)
+        for p, cs, j in runs:
+            for i, (c, Mr) in enumerate(zip(cs, p["shapes"])):
+                assert np.array_equal(fetch(c, (Mr, p["N"])), alone[j][i])
+    finally:
+        M.sync()
+        for st in streams:
+            M.call("mk_stream_destroy", st)
+
+
+def test_gemm_stream_k_gave_up_wait_is_reported(gpu, rng):
+    # a zero wait bound makes every owner of a split tile give up at once (the kernel still completes, from whatever
+    # the partial slots hold); the next synchronisation reports it, once, and the default bound restores results
+    P = _sk_problem(rng)
+    ref = _sk_launch(P)
+    M.sync()
+    want = [fetch(c, (Mr, P["N"])) for c, Mr in zip(ref, P["shapes"])]
+    M.call("mk_gemm_set_wait_limit", 0)
+    try:
+        _sk_launch(P)
+        assert M.lib().mk_synchronize() == 3  # MK_ERR_DEVICE
+        assert b"gave up" in M.lib().mk_last_error()
+    finally:
+        M.call("mk_gemm_set_wait_limit", 1 << 26)
+    M.sync()  # reported once
+    cs = _sk_launch(P)
+    M.sync()
+    for c, Mr, w in zip(cs, P["shapes"], want):
+        assert np.array_equal(fetch(c, (Mr, P["N"])), w)
+
+
 def test_gemm_stream_k_heads(gpu, rng):
     # the QKV heads epilogue on 4.5 waves of tiles: 2 x 4096 rows, 24 heads
     B, Mr, H, K_ = 2, 4096, 24, 256
@@ -378,19 +467,20 @@ def test_gemm_rejects_bad_shapes(gpu):
 # ---------------------------------------------------------------------------------------------------------------
 
 def run_attention(q, k, v, scale, q_pos0=0, block=0):
-    """q [B][H][Tq][d], k, v [B][H][Tk][d] (bf16-exact floats) through mk_attention; returns [B][Tq][H*d]."""
+    """q [B][H][Tq][d], k, v [B][Hkv][Tk][d] (bf16-exact floats, Hkv dividing H) through mk_attention; returns
+    [B][Tq][H*d]."""
     B, H, Tq, d = q.shape
-    Tk = k.shape[2]
+    Hkv, Tk = k.shape[1], k.shape[2]
     q_pad = (Tq + 255) // 256 * 256
     k_pad = (Tk + 63) // 64 * 64
     qp = np.zeros((B, H, q_pad, d), np.float32)
     qp[:, :, :Tq] = q
-    kp = np.zeros((B, H, k_pad, d), np.float32)
+    kp = np.zeros((B, Hkv, k_pad, d), np.float32)
     kp[:, :, :Tk] = k
-    vt = np.zeros((B, H, d, k_pad), np.float32)
+    vt = np.zeros((B, Hkv, d, k_pad), np.float32)
     vt[:, :, :, M.vt_col(np.arange(Tk))] = v.transpose(0, 1, 3, 2)
-    out = M.Dev(B * Tq * H * d * 2)
-    M.call("mk_attention", bdev(qp).p, bdev(kp).p, bdev(vt).p, out.p, B, H, d, Tq, q_pad, Tk, k_pad, H * d,
+    out = dev(np.zeros(B * Tq * H * d, np.uint16))
+    M.call("mk_attention", bdev(qp).p, bdev(kp).p, bdev(vt).p, out.p, B, H, Hkv, d, Tq, q_pad, Tk, k_pad, H * d,
            Tq * H * d, q_pos0, block, scale, None)
     M.sync()
     return fetch_bf16(out, (B, Tq, H * d))
@@ -638,3 +728,64 @@ def test_quantize_fp8_matches_oracle(gpu):
     M.sync()
     assert np.array_equal(fetch(sc, (rows,)), scale)
     assert np.array_equal(R.e4m3_table()[fetch(codes, (rows, cols), np.uint8)], q)
+
+
+def test_quantize_fp8_every_bf16_value_and_zeros(gpu):
+    # Every finite bf16 value of magnitude <= 448 (both zeros included), in rows that start with 448 so the row
+    # scale is exactly 1 and each code is the encoder's own rounding of the value; then an all-zero row (scale 1,
+    # zero codes: exact zeros once came out as code 0xF8, -256 x the scale).
+    v = M.bf16_to_f32(np.arange(0x10000, dtype=np.uint32).astype(np.uint16))
+    vals = v[np.isfinite(v) & (np.abs(v) <= 448.0)]
+    cols = 512
+    rows = -(-vals.size // (cols - 1))
+    body = np.zeros(rows * (cols - 1), np.float32)
+    body[:vals.size] = vals
+    mat = np.concatenate([np.full((rows, 1), 448.0, np.float32), body.reshape(rows, cols - 1)], axis=1)
+    mat = np.concatenate([mat, np.zeros((1, cols), np.float32)])
+    rows += 1
+    codes, sc = M.Dev(rows * cols), M.Dev(rows * 4)
+    M.call("mk_quantize_fp8_rows", bdev(mat).p, rows, cols, codes.p, sc.p, None)
+    M.sync()
+    assert np.array_equal(fetch(sc, (rows,)), np.ones(rows, np.float32))
+    enc = R.lib().mkref_f32_to_e4m3
+    want = np.array([enc(float(x)) for x in mat.ravel()], dtype=np.uint8).reshape(rows, cols)
+    got = fetch(codes, (rows, cols), np.uint8)
+    assert np.array_equal(got, want), np.argwhere(got != want)[:8]
+    assert not got[-1].any()
+
+
+@pytest.mark.parametrize("d,H,Hkv,scale", [(128, 8, 2, 0.0), (64, 6, 3, 0.125), (128, 4, 1, 0.0)])
+def test_attention_grouped_kv_heads(gpu, rng, d, H, Hkv, scale):
+    # grouped-query attention (the reference's AttnArgs kv_heads): query head h reads key / value head h / (H / Hkv);
+    # the oracle runs plain attention on K / V repeated to every query head
+    B, Tq, Tk = 2, 200, 333
+    q = R.bf16_round(rng.standard_normal((B, H, Tq, d)).astype(np.float32))
+    k = rng.standard_normal((B, Hkv, Tk, d)).astype(np.float32)
+    if scale == 0.0:  # K carries the softmax scale in log2 units: softmax(q K'^T ln 2)
+        k = k / np.sqrt(d) * np.log2(np.e)
+    k = R.bf16_round(k)
+    v = R.bf16_round(rng.standard_normal((B, Hkv, Tk, d)).astype(np.float32))
+    got = run_attention(q, k, v, scale)
+    rep = H // Hkv
+    want = R.attention(q, np.repeat(k, rep, axis=1), np.repeat(v, rep, axis=1),
+                       float(np.log(2.0)) if scale == 0.0 else scale)
+    dd = R.diff(got, want, d)
+    assert dd["min_cos"] > 0.9999 and dd["max_rel"] < 1e-2, dd
+
+
+def test_attention_rejects_kv_heads_not_dividing(gpu):
+    z = dev(np.zeros(4096, np.uint16))
+    st = M.lib().mk_attention(z.p, z.p, z.p, z.p, 1, 6, 4, 64, 16, 256, 16, 64, 384, 0, 0, 0, 0.125, None)
+    assert st == 1 and b"kv_heads" in M.lib().mk_last_error()
+
+
+def test_binding_keeps_dropped_buffers_until_sync(gpu, rng):
+    # the pointer of a temporary Dev passed straight to a call stays valid: dropped buffers are freed only after the
+    # next device-wide synchronisation
+    x = rng.standard_normal(1 << 16).astype(np.float32)
+    out = dev(np.zeros(1 << 16, np.uint16))
+    M.call("mk_f32_to_bf16", M.Dev.from_array(x).p, x.size, out.p, None)
+    assert len(M._pending) >= 1
+    M.sync()
+    assert not M._pending
+    assert np.array_equal(out.to_array(np.uint16, x.shape), M.bf16_bits(x))
