@@ -209,6 +209,14 @@ mk_status mk_layer_norm(const float* x, uint32_t rows, uint32_t n, const float* 
 /* group_norm over channels-last [batch][rows][c], `groups` groups, affine; y bf16 */
 mk_status mk_group_norm(const float* x, uint32_t batch, uint32_t rows, uint32_t c, uint32_t groups, const float* g,
                         const float* b, float eps, void* y, void* stream);
+/* mk_group_norm without allocating: no counterpart in the reference; for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). Same arguments and results
+ * (bit-identical); the partial sums live in a fixed 4 MiB array of the library on each device instead of a per-call
+ * allocation: 16 bytes for each of batch x ceil(rows / 16) x groups partials plus 8 for each of batch x groups
+ * statistics must fit (e.g. batch 2, 4096 rows, 32 groups: 264 KiB), else MK_ERR_ARG. Every call on a device shares
+ * that device's array: calls that overlap on one device (different streams, or threads) race and must not be made. */
+mk_status mk_group_norm_noalloc(const float* x, uint32_t batch, uint32_t rows, uint32_t c, uint32_t groups,
+                                const float* g, const float* b, float eps, void* y, void* stream);
 /* x_out = x + dt * (neg + guidance * (pos - neg)) over n floats (engine.cpp:476-502); guidance 1 / neg NULL:
  * x + dt * pos. */
 mk_status mk_cfg_euler(const float* x, const float* pos, const float* neg, size_t n, float guidance, float dt,

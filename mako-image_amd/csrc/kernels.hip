@@ -4,6 +4,7 @@
 #include "common.hpp"
 
 #include <cmath>
+#include <mutex>
 
 namespace mk {
 
@@ -759,6 +760,35 @@ mk_status ln_modulate_group(const LnArgs* a, int count, uint32_t n, float eps, v
 
 using namespace mk;
 
+// Scratch of mk_group_norm_noalloc, the entry point that allocates nothing: the per-chunk partial sums and the
+// per-(sample, group) statistics of one call, 4 MiB a device for the life of the process. Host code never passes the
+// array's name to a kernel (on the host it is a stand-in, not the device address): it takes each device's address once
+// with hipGetSymbolAddress and uses that.
+static __device__ __align__(256) double2 scratch[1 << 18];
+
+namespace {
+constexpr int kScratchDevices = 64;
+std::mutex g_scratch_mutex;
+char* g_scratch[kScratchDevices] = {};
+
+// The current device's copy of `scratch`, its address looked up on the device's first call.
+mk_status scratch_of_device(char** out)
+{
+    int dev = 0;
+    MK_HIP(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kScratchDevices)
+        return fail(MK_ERR_DEVICE, "scratch: device index out of range");
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (!g_scratch[dev]) {
+        void* p = nullptr;
+        MK_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        g_scratch[dev] = static_cast<char*>(p);
+    }
+    *out = g_scratch[dev];
+    return MK_OK;
+}
+} // namespace
+
 extern "C" {
 
 mk_status mk_ln_modulate(const float* x, uint32_t rows, uint32_t n, const float* scale, const float* shift,
@@ -793,30 +823,67 @@ mk_status mk_layer_norm(const float* x, uint32_t rows, uint32_t n, const float* 
     return MK_OK;
 }
 
-mk_status mk_group_norm(const float* x, uint32_t batch, uint32_t rows, uint32_t c, uint32_t groups, const float* g,
-                        const float* b, float eps, void* y, void* stream)
+// Both group norm entry points: arguments checked, then the three kernels over the scratch `ws` (the per-chunk
+// partials, then the (mean, 1 / std) pairs; group_norm_scratch bytes).
+static mk_status group_norm_check(const float* x, uint32_t batch, uint32_t c, uint32_t groups, const float* g,
+                                  const float* b, void* y)
 {
     if (!x || !g || !b || !y || !groups || c % groups || !batch)
         return fail(MK_ERR_ARG, "group_norm: null pointer or channels not a multiple of groups");
     if (c > 4096 || groups > 1024)
         return fail(MK_ERR_ARG, "group_norm: at most 4096 channels and 1024 groups");
-    if (!rows)
-        return MK_OK;
+    return MK_OK;
+}
+static size_t group_norm_part_bytes(uint32_t batch, uint32_t rows, uint32_t groups)
+{
+    return sizeof(double2) * batch * cdiv(rows, kGnRows) * groups;
+}
+static size_t group_norm_scratch(uint32_t batch, uint32_t rows, uint32_t groups)
+{
+    return group_norm_part_bytes(batch, rows, groups) + sizeof(float2) * batch * groups;
+}
+static mk_status group_norm_run(const float* x, uint32_t batch, uint32_t rows, uint32_t c, uint32_t groups,
+                                const float* g, const float* b, float eps, void* y, char* ws, hipStream_t s)
+{
     const uint32_t chunks = cdiv(rows, kGnRows);
-    // one allocation: the partials, then the (mean, 1 / std) pairs
-    const size_t part_bytes = sizeof(double2) * batch * chunks * groups;
-    char* ws = nullptr;
-    MK_HIP(hipMallocAsync(reinterpret_cast<void**>(&ws), part_bytes + sizeof(float2) * batch * groups, S(stream)));
     double2* part = reinterpret_cast<double2*>(ws);
-    float2* stats = reinterpret_cast<float2*>(ws + part_bytes);
-    group_partial_kernel<<<dim3(chunks, batch), 256, 0, S(stream)>>>(x, rows, c, groups, part);
-    group_final_kernel<<<dim3(groups, batch), 64, 0, S(stream)>>>(part, chunks, groups,
-                                                                 double(rows) * double(c / groups), eps, stats);
-    group_apply_kernel<<<dim3(std::min<uint32_t>(cdiv(uint64_t(rows) * c, 256), 4096), batch), 256, 0, S(stream)>>>(
+    float2* stats = reinterpret_cast<float2*>(ws + group_norm_part_bytes(batch, rows, groups));
+    group_partial_kernel<<<dim3(chunks, batch), 256, 0, s>>>(x, rows, c, groups, part);
+    group_final_kernel<<<dim3(groups, batch), 64, 0, s>>>(part, chunks, groups, double(rows) * double(c / groups), eps,
+                                                          stats);
+    group_apply_kernel<<<dim3(std::min<uint32_t>(cdiv(uint64_t(rows) * c, 256), 4096), batch), 256, 0, s>>>(
         x, rows, c, groups, stats, g, b, static_cast<uint16_t*>(y));
     MK_LAUNCH_CHECK("group_norm");
-    MK_HIP(hipFreeAsync(ws, S(stream)));
     return MK_OK;
+}
+
+mk_status mk_group_norm(const float* x, uint32_t batch, uint32_t rows, uint32_t c, uint32_t groups, const float* g,
+                        const float* b, float eps, void* y, void* stream)
+{
+    MK_TRY(group_norm_check(x, batch, c, groups, g, b, y));
+    if (!rows)
+        return MK_OK;
+    char* ws = nullptr;
+    MK_HIP(hipMallocAsync(reinterpret_cast<void**>(&ws), group_norm_scratch(batch, rows, groups), S(stream)));
+    const mk_status st = group_norm_run(x, batch, rows, c, groups, g, b, eps, y, ws, S(stream));
+    MK_HIP(hipFreeAsync(ws, S(stream)));
+    return st;
+}
+
+mk_status mk_group_norm_noalloc(const float* x, uint32_t batch, uint32_t rows, uint32_t c, uint32_t groups,
+                                const float* g, const float* b, float eps, void* y, void* stream)
+{
+    MK_TRY(group_norm_check(x, batch, c, groups, g, b, y));
+    if (!rows)
+        return MK_OK;
+    const size_t need = group_norm_scratch(batch, rows, groups);
+    if (need > sizeof(scratch))
+        return fail(MK_ERR_ARG, "group_norm_noalloc: needs " + std::to_string(need) + " bytes of scratch, more than its " +
+                                    std::to_string(sizeof(scratch)) + " (16 bytes for each of batch x ceil(rows / 16) "
+                                    "x groups partials, 8 for each of batch x groups statistics)");
+    char* ws = nullptr;
+    MK_TRY(scratch_of_device(&ws));
+    return group_norm_run(x, batch, rows, c, groups, g, b, eps, y, ws, S(stream));
 }
 
 mk_status mk_gate_add(float* x, const void* y, uint32_t y_dtype, uint32_t rows, uint32_t n, const float* gate,

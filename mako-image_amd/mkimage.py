@@ -100,6 +100,7 @@ _SIGS = {
     "mk_rms_norm": (_i, [_vp, _u32, _u32, _vp, _f, _f, _vp, _vp]),
     "mk_layer_norm": (_i, [_vp, _u32, _u32, _vp, _vp, _f, _vp, _vp]),
     "mk_group_norm": (_i, [_vp, _u32, _u32, _u32, _u32, _vp, _vp, _f, _vp, _vp]),
+    "mk_group_norm_noalloc": (_i, [_vp, _u32, _u32, _u32, _u32, _vp, _vp, _f, _vp, _vp]),
     "mk_cfg_euler": (_i, [_vp, _vp, _vp, _sz, _f, _f, _vp, _vp]),
     "mk_rope_table": (_i, [_u32, _u32, _u32, _vp]),
     "mk_patchify": (_i, [_vp, _u32, _u32, _u32, _u32, _vp, _vp]),
