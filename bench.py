@@ -201,8 +201,9 @@ def bench_sdxl(args):
     kernels = {k: {"ms_per_pass": round(v["ms"] / args.steps, 3), "launches_per_pass": v["launches"] // args.steps,
                    **({"tflops": round(v["flops"] / (v["ms"] / 1e3) / 1e12, 1)} if v["flops"] else {})}
                for k, v in sorted(per.items(), key=lambda kv: -kv[1]["ms"])}
-    g = per.get("gemm")
-    gemm_tf = g["flops"] / (g["ms"] / 1e3) / 1e12 if g and g["flops"] else None
+    g = {"ms": sum(v["ms"] for k, v in per.items() if k.startswith("gemm")),
+         "flops": sum(v["flops"] for k, v in per.items() if k.startswith("gemm"))}
+    gemm_tf = g["flops"] / (g["ms"] / 1e3) / 1e12 if g["flops"] else None
     line = {
         "metric": SDXL_METRIC, "value": round(tot_s, 5), "unit": "s/pass", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(tot_s * 1e3, 3), "higher_is_better": False, "scaling": "weak",
@@ -246,6 +247,155 @@ def cpu_baseline_sdxl(seconds_target, pass_flops):
             "sample": f"oracle (C++/OpenMP, fp32 over bf16 weights): {reps} x one stage-A block of one sample at "
                       f"{n_side * n_side} tokens ({flops / 1e9:.1f} GFLOP each, {t_total:.1f} s, "
                       f"{rate / 1e9:.1f} GFLOP/s), scaled by FLOPs to the whole batch-2 pass"}
+
+
+# Qwen-Image 2.1 as the reference runs it (qwen_image.hpp:38; its published numbers, docs/performance.md:5): 32
+# blocks of width 4096, 32 heads x 128, SwiGLU 12288, one weight set for text and image rows, 4096 image tokens at
+# 1024x1024 and a prompt of 256 rows of width 4096; guidance as two passes (each slot keeps its text K / V).
+Q21_CFG = dict(blocks=32, dim=4096, heads=32, head_dim=128, ffn=12288, text_dim=4096)
+Q21_METRIC = ("s/denoise-step Qwen-Image 2.1 graph (reference's own model) 1024² bf16, CFG as two passes; "
+              "attention+GEMM % of MFMA peak")
+
+
+def q21_flops(first, N=4096, S=256, blocks=32, D=4096, F=12288, H=32):
+    """Algorithmic FLOPs of one guided 2.1 step (two passes): per block the q|k|v, o, gate|up and down projections
+    (2 T D (4 D + 3 F)) over T rows (text + image on the first step, image only after) and the attention over
+    N (S + N) image query-key pairs plus S (S + 1) / 2 causal text pairs on the first step (4 d per pair a head)."""
+    T = N + S if first else N
+    lin = 2 * T * D * (4 * D + 3 * F)
+    attn = 4 * (N * (N + S) + (S * (S + 1) // 2 if first else 0)) * 128 * H
+    return 2 * blocks * (lin + attn), 2 * blocks * lin, 2 * blocks * attn
+
+
+def bench_q21(args):
+    """The 2.1 graph: step 1 (text and image rows, the text K / V kept per slot) and the later steps (image rows
+    against the cached K / V), guidance as two passes, each timed with HIP events on the engine's stream."""
+    import numpy as np
+
+    import mkimage as M
+
+    M.call("mk_set_device", 0)
+    side, S = 64, 256
+    N = side * side
+    eng = M.Engine(M.FAMILY_Q21, **Q21_CFG)
+    eng.init_random(0)
+    rng = np.random.default_rng(0)
+    prompts = [rng.standard_normal((S, Q21_CFG["text_dim"])).astype(np.float32) for _ in range(2)]
+    lat = [M.Dev.from_array(rng.standard_normal((N, 64)).astype(np.float32)), M.Dev(N * 64 * 4)]
+    stream = eng.stream()
+
+    def begin():
+        for s in (0, 1):
+            eng.begin(prompts[s], side, side, s)
+
+    def run(i):
+        eng.step_cfg_device(lat[i % 2], 1.0 - 0.02 * i, 0.98 - 0.02 * i, 4.0, lat[(i + 1) % 2], stream)
+
+    def timed(n, first):
+        e0, e1 = M.Event(), M.Event()
+        tot = 0.0
+        for i in range(n):
+            if first:
+                begin()
+            M.call("mk_stream_synchronize", stream)
+            e0.record(stream)
+            run(i)
+            e1.record(stream)
+            M.call("mk_stream_synchronize", stream)
+            tot += e0.elapsed_ms(e1)
+        return tot / n / 1e3
+
+    begin()
+    for i in range(args.warmup):
+        run(i)
+    first_s = timed(max(2, args.steps // 4), True)
+    begin()
+    run(0)  # step 1 of this generation
+    M.call("mk_stream_synchronize", stream)
+    e0, e1 = M.Event(), M.Event()
+    e0.record(stream)
+    for i in range(args.steps):
+        run(1 + i)
+    e1.record(stream)
+    M.call("mk_stream_synchronize", stream)
+    later_s = e0.elapsed_ms(e1) / 1e3 / args.steps
+    if not np.isfinite(lat[(1 + args.steps) % 2].to_array(np.float32, (N, 64))).all():
+        raise RuntimeError("non-finite latents")
+    # per-kernel pass over later steps
+    eng.set_timing(True)
+    per = {}
+    for i in range(args.steps):
+        run(1 + args.steps + i)
+        for k, v in eng.timing().items():
+            acc = per.setdefault(k, {"ms": 0.0, "launches": 0, "flops": 0.0})
+            for f in ("ms", "launches", "flops"):
+                acc[f] += v[f]
+    eng.set_timing(False)
+    tot, lin, attn = q21_flops(False, N, S)
+    tot1 = q21_flops(True, N, S)[0]
+    g = {f: sum(v[f] for k, v in per.items() if k.startswith("gemm")) for f in ("ms", "flops")}
+    a = per["attention"]
+    both = (g["flops"] + a["flops"]) / ((g["ms"] + a["ms"]) / 1e3)
+    dom = max((k for k, v in per.items() if v["flops"] and (k.startswith("gemm.") or k == "attention")),
+              key=lambda k: per[k]["ms"])
+    dv = per[dom]
+    dl = dv["ms"] / 1e3 / dv["launches"]
+    kernels = {k: {"ms_per_step": round(v["ms"] / args.steps, 3), "launches_per_step": v["launches"] // args.steps,
+                   **({"tflops": round(v["flops"] / (v["ms"] / 1e3) / 1e12, 1)} if v["flops"] else {})}
+               for k, v in sorted(per.items(), key=lambda kv: -kv[1]["ms"])}
+    line = {
+        "metric": Q21_METRIC, "value": round(later_s, 5), "unit": "s/step", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(later_s * 1e3, 3), "higher_is_better": False, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "weight_dtype": "bf16",
+        "data": "synthetic (random-init N(0,0.02) weights, N(0,1) latents and prompts)",
+        "config": {"workload": "Qwen-Image 2.1 graph (one weight set, SwiGLU, causal text prefix, text K/V cached "
+                               "after step 1), 1024x1024, CFG as two passes", **Q21_CFG, "image_tokens": N,
+                   "text_tokens": S, "heads_dtype": "f16"},
+        "step1_s": round(first_s, 5), "step1_tflop": round(tot1 / 1e12, 2), "step_tflop": round(tot / 1e12, 2),
+        "step_mfma_frac": round(tot / later_s / PEAK_BF16, 4),
+        "attention_gemm_mfma_frac": round(both / PEAK_BF16, 4),
+        "roofline": {"bound": "mfma", "kernel": f"{dom}: {KERNEL_OF_Q21.get(dom, dom)}",
+                     "achieved": round(dv["flops"] / dv["launches"] / dl / 1e12, 1), "peak": PEAK_BF16 / 1e12,
+                     "unit": "TFLOP/s", "frac": round(dv["flops"] / dv["launches"] / dl / PEAK_BF16, 4),
+                     "flops_per_launch": dv["flops"] / dv["launches"], "launch_us": round(dl * 1e6, 1),
+                     "traffic": None},
+        "kernels": kernels,
+        "reference_published": "1.28 s/step at step 2 on an Apple M5 GPU (docs/performance.md:5), other hardware",
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline_q21(args.cpu_seconds, tot)
+    print(json.dumps(line), flush=True)
+
+
+def cpu_baseline_q21(seconds_target, step_flops_):
+    """The oracle's 2.1 graph (one block, one pass, 32 x 32 image tokens and the 256-row prompt) timed on this host,
+    scaled by FLOPs to the 32-block guided step."""
+    import numpy as np
+
+    import mkref as R
+
+    m = R.Model(R.Q21, **{**Q21_CFG, "blocks": 1}, seed=0)
+    rng = np.random.default_rng(0)
+    side, S = 32, 256
+    prompt = rng.standard_normal((S, Q21_CFG["text_dim"])).astype(np.float32)
+    lat = rng.standard_normal((side * side, 64)).astype(np.float32)
+    flops = q21_flops(True, side * side, S, blocks=1)[0] / 2
+    reps, t_total = 0, 0.0
+    while t_total < seconds_target and reps < 50:
+        t0 = time.perf_counter()
+        m.q21_step(prompt, lat, side, side, 0.7)
+        t_total += time.perf_counter() - t0
+        reps += 1
+    rate = flops * reps / t_total
+    return {"value": step_flops_ / rate, "unit": "s/step", "cores": R.lib().mkref_threads(), "kind": "port",
+            "sample": f"oracle (C++/OpenMP, fp32 over bf16 weights): {reps} x one 2.1 block, one pass, {side * side} "
+                      f"image + {S} text tokens ({flops / 1e9:.0f} GFLOP each, {t_total:.1f} s, {rate / 1e9:.1f} "
+                      f"GFLOP/s), scaled by FLOPs to the 32-block two-pass step at 4096 image tokens (cached text)"}
+
+
+KERNEL_OF_Q21 = {"gemm.ff1": "gemm_kernel<256, 256, false, 4, 8> (SwiGLU epilogue)",
+                 "gemm.ff2": "gemm_sk_kernel<256, 256, false, 2, 8>", "gemm.qkv": "gemm_kernel<256, 256, false, 3, 8>",
+                 "gemm.o": "gemm_kernel<256, 256, false, 2, 8>", "attention": "attn2_kernel<128, true, true> (f16)"}
 
 
 # The kernel each timing class of the step launches (rocprofv3's name for it), for the traffic figure.
@@ -317,15 +467,15 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--workload", choices=sorted(WORKLOADS) + ["sdxl-1024-bf16", "vae-1024-decode"],
-                    default="mmdit-1024-bf16")
+    extra = {"sdxl-1024-bf16": bench_sdxl, "vae-1024-decode": bench_vae, "q21-1024": bench_q21}
+    ap.add_argument("--workload", choices=sorted(WORKLOADS) + sorted(extra), default="mmdit-1024-bf16")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
-    if args.workload in ("sdxl-1024-bf16", "vae-1024-decode"):
+    if args.workload in extra:
         if args.gpus != 1 or world != 1:
             print("bench.py measures one GPU: run it with --gpus 1", file=sys.stderr)
             sys.exit(2)
-        (bench_sdxl if args.workload == "sdxl-1024-bf16" else bench_vae)(args)
+        extra[args.workload](args)
         return
     wl = WORKLOADS[args.workload]
     global H, W, S

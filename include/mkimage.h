@@ -75,7 +75,11 @@ enum mk_epilogue {
     MK_EPI_GATE_TANH = 3,  /* X += tanh(gate[n]) * acc (gate_add, image.metal:55-65) */
     MK_EPI_SILU = 4,       /* C = silu(acc) */
     MK_EPI_ADD = 5,        /* X += acc (plain residual) */
-    MK_EPI_HEADS = 6       /* q|k|v columns scattered to heads with per-head RMSNorm + RoPE (see mk_heads_args) */
+    MK_EPI_HEADS = 6,      /* q|k|v columns scattered to heads with per-head RMSNorm + RoPE (see mk_heads_args) */
+    /* Gated linear units fused into the projection: W holds N = 2F rows [first part; second part] (the fused
+     * gate|up matrix as upload_rows stacks it), C is [M][F] (ldc >= F): */
+    MK_EPI_SWIGLU = 7,     /* C[r][i] = silu(acc[r][i]) * acc[r][F + i] (swiglu_rows, qwen_image.cpp:275-280) */
+    MK_EPI_GEGLU = 8       /* C[r][i] = acc[r][i] * gelu_erf(acc[r][F + i]) (geglu_rows, image.metal:475-484) */
 };
 
 typedef struct mk_heads_args {
@@ -93,6 +97,10 @@ typedef struct mk_heads_args {
     uint32_t rope_mode;   /* 0 none, 1 half-split pairs (i, i + d/2), 2 interleaved pairs (2i, 2i+1) */
     float eps;
     float k_scale;        /* K rows times this (0: 1), e.g. the softmax scale times log2(e) for mk_attention's scale 0 */
+    uint32_t dtype;       /* element type of Q, K, V^T: 0 or MK_BF16 bf16; MK_F16 IEEE half (the reference's
+                             heads_norm_half / heads_half, qwen_image.cpp:226-250) */
+    int64_t rope_stride;  /* floats between the RoPE tables of consecutive batch items (0: one table for all): a
+                             guidance batch whose prompts differ in length has one table per prompt */
 } mk_heads_args;
 
 typedef struct mk_gemm_args {
@@ -172,26 +180,31 @@ mk_status mk_gate_add(float* x, const void* y, uint32_t y_dtype, uint32_t rows, 
 
 /* heads_norm_half / heads_half (qwen_image.cpp:226-250, sdxl.cpp:439-448): per (row, head) of x bf16
  * [batch][rows][ld] at column col0 + head * d: optional RMSNorm * w, RoPE from table rows rope[row0 + r], written
- * bf16 to out [batch][heads][n_pad][d] at row0 + r (transpose = 0), or to out [batch][heads][d][n_pad] at column
- * MK_VT_COL(row0 + r) (transpose = 1: the V^T layout the attention reads). */
+ * to out [batch][heads][n_pad][d] at row0 + r (transpose = 0), or to out [batch][heads][d][n_pad] at column
+ * MK_VT_COL(row0 + r) (transpose = 1: the V^T layout the attention reads), as out_dtype: MK_BF16 or MK_F16 (the
+ * reference's half; rounded to nearest even). */
 mk_status mk_heads(const void* x, uint32_t batch, uint32_t rows, int64_t ld, int64_t stride_x, uint32_t col0,
                    uint32_t heads, uint32_t d, const float* w, float eps, const float* rope, uint32_t rope_mode,
-                   void* out, uint32_t n_pad, uint32_t row0, int transpose, void* stream);
+                   void* out, uint32_t n_pad, uint32_t row0, int transpose, uint32_t out_dtype, void* stream);
 
 /* V^T key order: within each group of 16 keys, key k sits at column k with bits 2 and 3 swapped (the order in which
  * a lane of the P V matrix product reads 8 keys as one 16-byte load). */
 #define MK_VT_COL(k) (((k) & ~12u) | (((k) & 4u) << 1) | (((k) & 8u) >> 1))
 
 /* attention (qwen_image.cpp:271 and the AttnArgs it fills, sdxl.cpp:24-27, 450-457): softmax(Q K^T scale) V, fp32
- * online softmax on bf16 MFMA. q [batch][heads][q_pad][d], k [batch][kv_heads][k_pad][d], vt
- * [batch][kv_heads][d][k_pad] bf16 with keys in the MK_VT_COL order (padding keys zero); query head h reads key /
+ * online softmax on MFMA in the inputs' type `dtype`: MK_BF16, or MK_F16 (the reference's half heads; the
+ * probabilities then enter P V as half too). q [batch][heads][q_pad][d], k [batch][kv_heads][k_pad][d], vt
+ * [batch][kv_heads][d][k_pad] with keys in the MK_VT_COL order (padding keys zero); query head h reads key /
  * value head h / (heads / kv_heads) (grouped-query attention; kv_heads == heads for every graph here).
  * out bf16 [batch][n_q][ldo] at column head * d. Query row i (absolute q_pos0 + i) sees key c < n_k iff
- * q_pos0 + i >= block or c <= q_pos0 + i (block 0: no mask; UINT32_MAX: causal; S: causal text prefix).
- * d in {64, 128}; kv_heads divides heads; q_pad % 128 == 0; k_pad % 64 == 0. */
-mk_status mk_attention(const void* q, const void* k, const void* vt, void* out, uint32_t batch, uint32_t heads,
-                       uint32_t kv_heads, uint32_t d, uint32_t n_q, uint32_t q_pad, uint32_t n_k, uint32_t k_pad,
-                       int64_t ldo, int64_t stride_o, uint32_t q_pos0, uint32_t block, float scale, void* stream);
+ * q_pos0 + i >= block or c <= q_pos0 + i (block 0: no mask; UINT32_MAX: causal; S: causal text prefix), and c lies
+ * outside its batch item's masked range: key_hole NULL, or a host array of batch pairs (lo, hi) (batch <= 8): keys
+ * [lo, hi) of item b are masked (a classifier-free-guidance batch whose shorter prompt is padded to the longer one's
+ * rows; lo >= 1). d in {64, 128}; kv_heads divides heads; q_pad % 128 == 0; k_pad % 64 == 0. */
+mk_status mk_attention(const void* q, const void* k, const void* vt, void* out, uint32_t dtype, uint32_t batch,
+                       uint32_t heads, uint32_t kv_heads, uint32_t d, uint32_t n_q, uint32_t q_pad, uint32_t n_k,
+                       uint32_t k_pad, int64_t ldo, int64_t stride_o, uint32_t q_pos0, uint32_t block, float scale,
+                       const uint32_t* key_hole, void* stream);
 
 /* Elementwise and norms (fp32 unless stated). */
 mk_status mk_silu(float* x, size_t n, void* stream);

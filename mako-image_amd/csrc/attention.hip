@@ -1,4 +1,5 @@
-// attention: joint softmax(Q K^T scale) V on gfx950 bf16 MFMA (v_mfma_f32_32x32x16_bf16), online softmax in fp32.
+// attention: joint softmax(Q K^T scale) V on gfx950 MFMA (v_mfma_f32_32x32x16_bf16, or _f16 for half inputs),
+// online softmax in fp32.
 //
 // Each wave owns 32 queries and computes S^T = K Q^T: the MFMA's A operand is a K tile (rows = keys), its B operand
 // the wave's Q held in registers for the whole pass (cols = queries). A lane then holds 16 scores of one query per
@@ -23,12 +24,16 @@ namespace mk {
 
 namespace {
 
+constexpr int kMaxHoleBatch = 8; // batch items that can carry a masked key range
+
 struct AttnP {
     const uint16_t *q, *k, *vt;
     uint16_t* out;
     uint32_t heads, group, batch, n_q, q_pad, n_k, k_pad, q_pos0, block; // group: query heads a key / value head
     int64_t ldo, so;
     float c; // scale * log2(e)
+    // keys [hole[b][0], hole[b][1]) of batch item b are masked (a shorter prompt's padding rows); empty: none
+    uint32_t hole[kMaxHoleBatch][2];
 };
 
 constexpr int kKT = 64; // keys per tile
@@ -48,14 +53,54 @@ __device__ inline uint32_t cvt_bf16x2(float a, float b)
     return __builtin_bit_cast(uint32_t, v);
 }
 
+// The element type of Q, K, V^T and the probabilities: bf16, or IEEE half (the reference's half heads). The same
+// kernel over either: the 32 x 32 x 16 MFMA, the packed conversion (v_cvt_pk_bf16_f32 / v_cvt_pk_f16_f32, both
+// round to nearest even), the two-deep dot product the row sums use, and the rounding that keeps the running max
+// exactly representable.
+typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 f16x8;
+typedef __attribute__((__vector_size__(2 * sizeof(_Float16)))) _Float16 f16x2;
+template <bool F16> struct Elem;
+template <> struct Elem<false> {
+    typedef bf16x8 v8;
+    typedef __bf16 e;
+    static __device__ f32x16 mfma(v8 a, v8 b, f32x16 c, int, int, int)
+    {
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+    }
+    static __device__ uint32_t pack(float a, float b) { return cvt_bf16x2(a, b); }
+    // acc + the two values of p (a packed pair) times 1
+    static __device__ float sum2(uint32_t p, float acc)
+    {
+        const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
+        return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, p), ones, acc, false);
+    }
+};
+template <> struct Elem<true> {
+    typedef f16x8 v8;
+    typedef _Float16 e;
+    static __device__ f32x16 mfma(v8 a, v8 b, f32x16 c, int, int, int)
+    {
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+    }
+    static __device__ uint32_t pack(float a, float b) { return pack_f16x2(a, b); }
+    static __device__ float sum2(uint32_t p, float acc)
+    {
+        const f16x2 ones = {(_Float16)1.0f, (_Float16)1.0f};
+        return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, p), ones, acc, false);
+    }
+};
+
 // U: K carries the softmax scale in log2 units (scale 0 at the API). The running max then enters the S^T MFMAs as
 // one more 16-deep product, a constant fragment of ones (K side, dim 0) times a fragment holding -m (Q side), so
 // S - m comes out of the matrix core: the softmax needs no per-score multiply-add, and the row sums are taken on the
 // bf16 probabilities the P V product uses (v_dot2 against ones), which halves those adds too. m is kept
 // bf16-representable so the product subtracts it exactly.
-template <int D, bool U>
+template <int D, bool U, bool F16, bool HOLE>
 __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn2_kernel(AttnP p)
 {
+    typedef Elem<F16> X;
+    typedef typename X::v8 V8;
+    typedef typename X::e E;
     constexpr int DS = D / 16, DT = D / 32, KC = D / 8;
     constexpr int RK = kKT * KC / 256, RV = D * 8 / 256;
     constexpr int NB = 2;
@@ -72,18 +117,31 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     if (total % 8 == 0)
         item = (item % 8) * (total / 8) + item / 8;
     const uint32_t qb = item % nqb, head = (item / nqb) % p.heads, bi = item / (nqb * p.heads);
+    // HOLE: the batch item's masked key range (a shorter prompt padded to the batch's text rows); a variant of its
+    // own, so the launches without one carry none of its registers
+    int hole_lo = 0, hole_hi = 0;
+    if constexpr (HOLE) {
+        hole_lo = bi < uint32_t(kMaxHoleBatch) ? int(p.hole[bi][0]) : 0;
+        hole_hi = bi < uint32_t(kMaxHoleBatch) ? int(p.hole[bi][1]) : 0;
+    }
+    auto in_hole = [&](int key) { return HOLE && key >= hole_lo && key < hole_hi; };
+    // keys [k0, k0 + n) reach into the hole (the general path masks them score by score; the scale-0 path through
+    // the matrix core, below)
+    auto hits_hole = [&](int k0, int n) {
+        return HOLE && !U && hole_lo < hole_hi && k0 < hole_hi && k0 + n > hole_lo;
+    };
     const int64_t bh = int64_t(bi) * p.heads + head, bkv = int64_t(bi) * (p.heads / p.group) + head / p.group;
     const uint16_t* Q = p.q + bh * p.q_pad * D;
     const uint16_t* K = p.k + bkv * p.k_pad * D;
     const uint16_t* VT = p.vt + bkv * int64_t(D) * p.k_pad;
     const int q0 = int(qb) * 128 + wave * 32;
 
-    bf16x8 qf[DS];
+    V8 qf[DS];
     {
         const int qi = min(q0 + r32, int(p.n_q) - 1);
 #pragma unroll
         for (int ds = 0; ds < DS; ++ds)
-            qf[ds] = *reinterpret_cast<const bf16x8*>(Q + int64_t(qi) * D + ds * 16 + hk * 8);
+            qf[ds] = *reinterpret_cast<const V8*>(Q + int64_t(qi) * D + ds * 16 + hk * 8);
     }
     // K / V^T tiles go to LDS by buffer loads (resources over the head's rows; lane byte offsets select key / dim and
     // chunk, the tile's key offset is a scalar): unlike the global form they leave the LDS counter alone.
@@ -118,9 +176,19 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
             buf_load_lds16(rsV, (lds_void*)&sV[buf][(i * 4 + wave) * 512], ov[i], k0 * 2);
     };
     // S^T of a 32-key half of a tile: value r <-> key 8(r/4) + 4hk + r%4 of the half
-    bf16x8 kone = {}, qm = {}; // U: ones at dim 0 (K side); -m at dim 0 (Q side), lanes of the first k half
+    V8 kone = {}, qm = {}; // U: ones at dim 0 (K side); -m at dim 0 (Q side), lanes of the first k half
     if (hk == 0)
-        kone[0] = (__bf16)1.0f;
+        kone[0] = (E)1.0f;
+    // U with a masked key range: the same product also adds bias(key) x 1 at dim 1, bias -inf for the masked keys
+    // (0 otherwise), so their scores leave the matrix core as -inf (lanes of the first k half hold dims 0 .. 7)
+    if (HOLE && U && hk == 0)
+        qm[1] = (E)1.0f;
+    auto kbias = [&](int key) {
+        V8 kb = kone;
+        if (hk == 0 && key >= hole_lo && key < hole_hi)
+            kb[1] = (E)(-__builtin_inff());
+        return kb;
+    };
     f32x16 oacc[DT];
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
@@ -131,22 +199,22 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     // U: the scores arrive as S - m; the first half-tile sets m to its max (every query sees key 0), later ones move
     // it lazily as below.
     auto softmax_u = [&](f32x16& sacc, int k0, u32x4 (&pb)[2], bool first, f32x16* other) {
-        if (k0 + 32 > int(p.n_k) || (wave_causal && k0 + 31 > int(p.q_pos0) + q0)) {
+        if (k0 + 32 > int(p.n_k) || (wave_causal && k0 + 31 > int(p.q_pos0) + q0) || hits_hole(k0, 32)) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int key = k0 + 8 * (r / 4) + 4 * hk + (r % 4);
-                if (key >= int(p.n_k) || (uint32_t(qpos) < p.block && key > qpos))
+                if (key >= int(p.n_k) || (uint32_t(qpos) < p.block && key > qpos) || in_hole(key))
                     sacc[r] = -__builtin_inff();
             }
         }
         const float mx = max_xor32(max16(sacc));
         if (first || __any(mx > kLazy)) {
-            const float mn = float((__bf16)(m + (first ? mx : fmaxf(mx, 0.0f))));
+            const float mn = float((E)(m + (first ? mx : fmaxf(mx, 0.0f))));
             const float dm = mn - m;
             const float alpha = first ? 1.0f : __builtin_amdgcn_exp2f(-dm);
             m = mn;
             if (hk == 0)
-                qm[0] = (__bf16)(-m);
+                qm[0] = (E)(-m);
             l *= alpha;
 #pragma unroll
             for (int r = 0; r < 16; ++r)
@@ -162,8 +230,7 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
                     oacc[dt][r] *= alpha;
         }
         // row sums as four two-deep dot2 chains (one chain of eight serialises on the accumulator)
-        const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
-        float ls[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+                float ls[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int st = 0; st < 2; ++st) {
             const int o = 8 * st;
@@ -171,21 +238,21 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 // (bit-cast from a scalar: this compiler miscompiles a bit-cast of a vector element here)
-                const uint32_t pj = cvt_bf16x2(__builtin_amdgcn_exp2f(sacc[o + 2 * j]),
+                const uint32_t pj = X::pack(__builtin_amdgcn_exp2f(sacc[o + 2 * j]),
                                                __builtin_amdgcn_exp2f(sacc[o + 2 * j + 1]));
                 v[j] = pj;
-                ls[j] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pj), ones, ls[j], false);
+                ls[j] = X::sum2(pj, ls[j]);
             }
             pb[st] = v;
         }
         l += (ls[0] + ls[1]) + (ls[2] + ls[3]);
     };
     auto softmax = [&](f32x16& sacc, int k0, u32x4 (&pb)[2]) {
-        if (k0 + 32 > int(p.n_k) || (wave_causal && k0 + 31 > int(p.q_pos0) + q0)) {
+        if (k0 + 32 > int(p.n_k) || (wave_causal && k0 + 31 > int(p.q_pos0) + q0) || hits_hole(k0, 32)) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int key = k0 + 8 * (r / 4) + 4 * hk + (r % 4);
-                if (key >= int(p.n_k) || (uint32_t(qpos) < p.block && key > qpos))
+                if (key >= int(p.n_k) || (uint32_t(qpos) < p.block && key > qpos) || in_hole(key))
                     sacc[r] = -__builtin_inff();
             }
         }
@@ -212,8 +279,8 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
 #pragma unroll
         for (int st = 0; st < 2; ++st) {
             const int o = 8 * st;
-            pb[st] = u32x4{cvt_bf16x2(sacc[o], sacc[o + 1]), cvt_bf16x2(sacc[o + 2], sacc[o + 3]),
-                           cvt_bf16x2(sacc[o + 4], sacc[o + 5]), cvt_bf16x2(sacc[o + 6], sacc[o + 7])};
+            pb[st] = u32x4{X::pack(sacc[o], sacc[o + 1]), X::pack(sacc[o + 2], sacc[o + 3]),
+                           X::pack(sacc[o + 4], sacc[o + 5]), X::pack(sacc[o + 6], sacc[o + 7])};
         }
     };
     issue(0, 0);
@@ -231,16 +298,16 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
         __builtin_amdgcn_s_waitcnt(0); // tile t resident
         __syncthreads();               // ... for every wave, and every wave done with tile t - 1's buffer
         issue(t + 1, buf ^ 1);         // past the end: the last tile again (discarded)
-        bf16x8 fk[2 * DS], fv[4 * DT];
+        V8 fk[2 * DS], fv[4 * DT];
         // read g: K fragments g < 2 DS as (ds, half) pairs, then V fragments of half 0, then half 1
         auto rd = [&](int g) {
             if (g < 2 * DS) {
                 const int ds = g / 2, kt = g % 2, key = kt * 32 + r32, c = kswz(key, ds * 2 + hk);
-                fk[g] = *reinterpret_cast<const bf16x8*>(&sK[buf][key * D + c * 8]);
+                fk[g] = *reinterpret_cast<const V8*>(&sK[buf][key * D + c * 8]);
             } else if (g < 2 * DS + 4 * DT) {
                 const int j = g - 2 * DS, kt = j / (2 * DT), dt = (j % (2 * DT)) % DT, st = (j % (2 * DT)) / DT;
                 const int d = dt * 32 + r32, s2 = 2 * kt + st;
-                fv[j] = *reinterpret_cast<const bf16x8*>(&sV[buf][d * kKT + (((2 * s2 + hk) ^ ((d >> 1) & 7)) << 3)]);
+                fv[j] = *reinterpret_cast<const V8*>(&sV[buf][d * kKT + (((2 * s2 + hk) ^ ((d >> 1) & 7)) << 3)]);
             }
         };
 #pragma unroll
@@ -250,14 +317,14 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
         s_a = f32x16{};
         s_b = f32x16{};
         if constexpr (U) {
-            s_a = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kone, qm, s_a, 0, 0, 0);
-            s_b = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kone, qm, s_b, 0, 0, 0);
+            s_a = X::mfma(kone, qm, s_a, 0, 0, 0);
+            s_b = X::mfma(kone, qm, s_b, 0, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
         }
 #pragma unroll
         for (int g = 0; g < 2 * DS; ++g) {
             f32x16& acc = g % 2 ? s_b : s_a;
-            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fk[g], qf[g / 2], acc, 0, 0, 0);
+            acc = X::mfma(fk[g], qf[g / 2], acc, 0, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
             rd(g + LA);
             __builtin_amdgcn_sched_barrier(0);
@@ -267,7 +334,7 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
 #pragma unroll
             for (int j = 0; j < 2 * DT; ++j) {
                 const int dt = j % DT, st = j / DT;
-                oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fv[kt * 2 * DT + j], __builtin_bit_cast(bf16x8, pb[st]),
+                oacc[dt] = X::mfma(fv[kt * 2 * DT + j], __builtin_bit_cast(V8, pb[st]),
                                                                    oacc[dt], 0, 0, 0);
                 __builtin_amdgcn_sched_barrier(0);
                 rd(2 * DS + kt * 2 * DT + j + LA);
@@ -290,27 +357,28 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     // needs whenever no score exceeds m by more than kLazy. The exponentials, conversions and row sums of half a then
     // run in chunks between the S^T MFMAs of half b, those of half b between the P V MFMAs of half a, and the row max
     // only decides afterwards whether a half is redone against a new m (the first half of the pass, and the rare
-    // tiles whose max jumps). EDGE tiles (ragged key end, causal diagonal) mask scores in the chunks.
+    // tiles whose max jumps). EDGE tiles (ragged key end, causal diagonal, a masked key range) mask scores in the
+    // chunks.
     constexpr int CH = 16 / DS;                  // scores per chunk: DS S^T MFMAs (= 2 DT P V MFMAs) per half
     auto tile_u = [&](int t, auto buf_c, auto edge_c) {
         constexpr int buf = decltype(buf_c)::value;
         constexpr bool EDGE = decltype(edge_c)::value;
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
-        bf16x8 fk[2 * DS], fv[4 * DT];
+        V8 fk[2 * DS], fv[4 * DT];
         // read g: K fragments of half a, of half b, then V fragments of half a, of half b
         auto rd = [&](int g) {
             if (g < 2 * DS) {
                 const int kt = g / DS, ds = g % DS, key = kt * 32 + r32, c = kswz(key, ds * 2 + hk);
-                fk[g] = *reinterpret_cast<const bf16x8*>(&sK[buf][key * D + c * 8]);
+                fk[g] = *reinterpret_cast<const V8*>(&sK[buf][key * D + c * 8]);
             } else if (g < 2 * DS + 4 * DT) {
                 const int j = g - 2 * DS, kt = j / (2 * DT), dt = (j % (2 * DT)) % DT, st = (j % (2 * DT)) / DT;
                 const int d = dt * 32 + r32, s2 = 2 * kt + st;
-                fv[j] = *reinterpret_cast<const bf16x8*>(&sV[buf][d * kKT + (((2 * s2 + hk) ^ ((d >> 1) & 7)) << 3)]);
+                fv[j] = *reinterpret_cast<const V8*>(&sV[buf][d * kKT + (((2 * s2 + hk) ^ ((d >> 1) & 7)) << 3)]);
             }
         };
-        const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
-        // chunk c of a half: scores 2j, 2j + 1 for pairs j of the chunk -> bf16 pair pw[j], row-sum partials, pair max
+        // chunk c of a half: scores 2j, 2j + 1 for pairs j of the chunk -> a packed pair pw[j], row-sum partials,
+        // pair max
         auto chunk = [&](f32x16& sc, int k0, uint32_t (&pw)[8], float (&ls)[4], float (&mp)[8], int c) {
 #pragma unroll
             for (int i = 0; i < CH / 2; ++i) {
@@ -326,8 +394,8 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
                     sc[2 * j] = x0;
                     sc[2 * j + 1] = x1;
                 }
-                pw[j] = cvt_bf16x2(__builtin_amdgcn_exp2f(x0), __builtin_amdgcn_exp2f(x1));
-                ls[j % 4] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pw[j]), ones, ls[j % 4], false);
+                pw[j] = X::pack(__builtin_amdgcn_exp2f(x0), __builtin_amdgcn_exp2f(x1));
+                ls[j % 4] = X::sum2(pw[j], ls[j % 4]);
                 mp[j] = max2(x0, x1);
                 // pinned here: the redo path overwrites them, so the compiler would otherwise sink the
                 // speculative work out of the MFMA shadow into the path that keeps it
@@ -342,12 +410,12 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
         // moves m to cover the half's max (the pass's first half: to its max), rescales what was accumulated against
         // the old m, and redoes the half's probabilities and row sum
         auto redo = [&](f32x16& sc, uint32_t (&pw)[8], float& lh, float mx, bool first, f32x16* other) {
-            const float mn = float((__bf16)(m + (first ? mx : fmaxf(mx, 0.0f))));
+            const float mn = float((E)(m + (first ? mx : fmaxf(mx, 0.0f))));
             const float dm = mn - m;
             const float alpha = first ? 1.0f : __builtin_amdgcn_exp2f(-dm);
             m = mn;
             if (hk == 0)
-                qm[0] = (__bf16)(-m);
+                qm[0] = (E)(-m);
             l *= alpha;
 #pragma unroll
             for (int r = 0; r < 16; ++r)
@@ -364,8 +432,8 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
             float ls[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                pw[j] = cvt_bf16x2(__builtin_amdgcn_exp2f(sc[2 * j]), __builtin_amdgcn_exp2f(sc[2 * j + 1]));
-                ls[j % 4] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pw[j]), ones, ls[j % 4], false);
+                pw[j] = X::pack(__builtin_amdgcn_exp2f(sc[2 * j]), __builtin_amdgcn_exp2f(sc[2 * j + 1]));
+                ls[j % 4] = X::sum2(pw[j], ls[j % 4]);
             }
             lh = (ls[0] + ls[1]) + (ls[2] + ls[3]);
         };
@@ -374,14 +442,14 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
         for (int g = 0; g < LA; ++g)
             rd(g);
         __builtin_amdgcn_sched_barrier(0);
-        s_a = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kone, qm, f32x16{}, 0, 0, 0);
+        s_a = X::mfma(HOLE ? kbias(k0 + r32) : kone, qm, f32x16{}, 0, 0, 0);
         __builtin_amdgcn_sched_barrier(0);
         // the next tile's direct loads (past the end: the last tile again, discarded) go out one after each S^T
         // MFMA of half a, not as one burst after the barrier (a burst from every wave stalls their issue)
         constexpr int ND = RK + RV, PER = (ND + DS - 1) / DS;
 #pragma unroll
         for (int ds = 0; ds < DS; ++ds) {
-            s_a = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fk[ds], qf[ds], s_a, 0, 0, 0);
+            s_a = X::mfma(fk[ds], qf[ds], s_a, 0, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
             rd(ds + LA);
             __builtin_amdgcn_sched_barrier(0);
@@ -390,14 +458,14 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
                 dma1(t + 1, buf ^ 1, i);
             __builtin_amdgcn_sched_barrier(0);
         }
-        s_b = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kone, qm, f32x16{}, 0, 0, 0);
+        s_b = X::mfma(HOLE ? kbias(k0 + 32 + r32) : kone, qm, f32x16{}, 0, 0, 0);
         __builtin_amdgcn_sched_barrier(0);
         uint32_t pa[8], pbw[8];
         float lsa[4] = {0.0f, 0.0f, 0.0f, 0.0f}, lsb[4] = {0.0f, 0.0f, 0.0f, 0.0f}, mpa[8], mpb[8];
         // S^T of half b || softmax of half a
 #pragma unroll
         for (int ds = 0; ds < DS; ++ds) {
-            s_b = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fk[DS + ds], qf[ds], s_b, 0, 0, 0);
+            s_b = X::mfma(fk[DS + ds], qf[ds], s_b, 0, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
             rd(DS + ds + LA);
             __builtin_amdgcn_sched_barrier(0);
@@ -417,7 +485,7 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
 #pragma unroll
         for (int j = 0; j < 2 * DT; ++j) {
             const int dt = j % DT, st = j / DT;
-            oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fv[j], __builtin_bit_cast(bf16x8, pA[st]), oacc[dt], 0, 0, 0);
+            oacc[dt] = X::mfma(fv[j], __builtin_bit_cast(V8, pA[st]), oacc[dt], 0, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
             rd(2 * DS + j + LA);
             __builtin_amdgcn_sched_barrier(0);
@@ -436,7 +504,7 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
 #pragma unroll
         for (int j = 0; j < 2 * DT; ++j) {
             const int dt = j % DT, st = j / DT;
-            oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fv[2 * DT + j], __builtin_bit_cast(bf16x8, pB[st]),
+            oacc[dt] = X::mfma(fv[2 * DT + j], __builtin_bit_cast(V8, pB[st]),
                                                                oacc[dt], 0, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
             rd(2 * DS + 2 * DT + j + LA);
@@ -449,7 +517,7 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
         // first query
         auto run = [&](int tt, auto buf_c) {
             const int e = tt * kKT + kKT - 1;
-            if (e >= int(p.n_k) || (wave_causal && e > int(p.q_pos0) + q0))
+            if (e >= int(p.n_k) || (wave_causal && e > int(p.q_pos0) + q0) || hits_hole(tt * kKT, kKT))
                 tile_u(tt, buf_c, std::true_type{});
             else
                 tile_u(tt, buf_c, std::false_type{});
@@ -491,13 +559,16 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
 
 using namespace mk;
 
-extern "C" mk_status mk_attention(const void* q, const void* k, const void* vt, void* out, uint32_t batch,
-                                  uint32_t heads, uint32_t kv_heads, uint32_t d, uint32_t n_q, uint32_t q_pad,
-                                  uint32_t n_k, uint32_t k_pad, int64_t ldo, int64_t stride_o, uint32_t q_pos0,
-                                  uint32_t block, float scale, void* stream)
+extern "C" mk_status mk_attention(const void* q, const void* k, const void* vt, void* out, uint32_t dtype,
+                                  uint32_t batch, uint32_t heads, uint32_t kv_heads, uint32_t d, uint32_t n_q,
+                                  uint32_t q_pad, uint32_t n_k, uint32_t k_pad, int64_t ldo, int64_t stride_o,
+                                  uint32_t q_pos0, uint32_t block, float scale, const uint32_t* key_hole,
+                                  void* stream)
 {
     if (!q || !k || !vt || !out)
         return fail(MK_ERR_ARG, "attention: null pointer");
+    if (dtype != MK_BF16 && dtype != MK_F16)
+        return fail(MK_ERR_ARG, "attention: q, k, v must be bf16 or f16");
     if (!heads || !kv_heads || heads % kv_heads)
         return fail(MK_ERR_ARG, "attention: kv_heads must divide heads");
     if (d != 64 && d != 128)
@@ -506,17 +577,47 @@ extern "C" mk_status mk_attention(const void* q, const void* k, const void* vt, 
         return fail(MK_ERR_ARG, "attention: need 0 < n_q <= q_pad, 0 < n_k <= k_pad, k_pad a multiple of 64");
     if (ldo % 4 || (reinterpret_cast<uintptr_t>(out) & 7))
         return fail(MK_ERR_ARG, "attention: output rows must be 8-byte aligned");
+    if (key_hole && batch > uint32_t(kMaxHoleBatch))
+        return fail(MK_ERR_ARG, "attention: masked key ranges for at most 8 batch items");
     AttnP p{static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(vt),
             static_cast<uint16_t*>(out), heads, heads / kv_heads, batch, n_q, q_pad, n_k, k_pad, q_pos0, block, ldo,
             stride_o,
-            scale * 1.4426950408889634f};
+            scale * 1.4426950408889634f, {}};
+    if (key_hole)
+        for (uint32_t b = 0; b < batch; ++b) {
+            p.hole[b][0] = key_hole[2 * b];
+            p.hole[b][1] = key_hole[2 * b + 1];
+            // the first key stays visible (every query row needs one finite score in the first tile)
+            if (p.hole[b][0] == 0 && p.hole[b][1] > 0)
+                return fail(MK_ERR_ARG, "attention: a masked key range must leave key 0 visible");
+        }
     const dim3 grid(cdiv(n_q, 128) * heads * batch);
     hipStream_t s = static_cast<hipStream_t>(stream);
     const bool unit = scale == 0.0f;
-    if (d == 128)
-        unit ? attn2_kernel<128, true><<<grid, 256, 0, s>>>(p) : attn2_kernel<128, false><<<grid, 256, 0, s>>>(p);
-    else
-        unit ? attn2_kernel<64, true><<<grid, 256, 0, s>>>(p) : attn2_kernel<64, false><<<grid, 256, 0, s>>>(p);
+#define MK_ATTN(F16, HOLE)                                                                                         \
+    if (d == 128)                                                                                                  \
+        unit ? attn2_kernel<128, true, F16, HOLE><<<grid, 256, 0, s>>>(p)                                          \
+             : attn2_kernel<128, false, F16, HOLE><<<grid, 256, 0, s>>>(p);                                        \
+    else                                                                                                           \
+        unit ? attn2_kernel<64, true, F16, HOLE><<<grid, 256, 0, s>>>(p)                                           \
+             : attn2_kernel<64, false, F16, HOLE><<<grid, 256, 0, s>>>(p)
+    bool hole = false;
+    for (uint32_t b = 0; key_hole && b < batch; ++b)
+        hole = hole || key_hole[2 * b] < key_hole[2 * b + 1];
+    if (dtype == MK_F16) {
+        if (hole) {
+            MK_ATTN(true, true);
+        } else {
+            MK_ATTN(true, false);
+        }
+    } else {
+        if (hole) {
+            MK_ATTN(false, true);
+        } else {
+            MK_ATTN(false, false);
+        }
+    }
+#undef MK_ATTN
     MK_LAUNCH_CHECK("attention");
     return MK_OK;
 }

@@ -79,6 +79,10 @@ struct LnArgs {
 // count 1 or 2 problems of width n (the mk_ln_modulate arguments each); one launch when n is 2048, 3072 or 4096
 mk_status ln_modulate_group(const LnArgs* a, int count, uint32_t n, float eps, void* stream);
 
+// Zero `bytes` (a multiple of 4, 4-byte aligned) of device memory on a stream with a kernel (kernels.hip): a fill node
+// a caller's graph capture can replay, unlike a memset node.
+mk_status fill_zero(void* p, size_t bytes, void* stream);
+
 // ---- error state (thread-local, read by mk_last_error) ----
 void set_error(const std::string& msg);
 mk_status fail(mk_status s, const std::string& msg);
@@ -131,6 +135,23 @@ __host__ __device__ inline float bf2f_bits(uint16_t b) { return __builtin_bit_ca
 __device__ inline uint32_t pack_bf16x2(float a, float b)
 {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2v{a, b}, bf16x2cv));
+}
+
+// ---- IEEE half (the reference's heads and attention precision, `half` in image.metal): round to nearest even,
+// subnormals kept, overflow to infinity. On the device gfx950's v_cvt_pk_f16_f32. ----
+typedef _Float16 f16x2cv __attribute__((ext_vector_type(2)));
+__device__ inline uint32_t pack_f16x2(float a, float b)
+{
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2v{a, b}, f16x2cv));
+}
+__device__ inline uint16_t f2h_bits(float x) { return __builtin_bit_cast(uint16_t, _Float16(x)); }
+__device__ inline float h2f_bits(uint16_t h) { return float(__builtin_bit_cast(_Float16, h)); }
+// A pair in the heads' element type: bf16 or half.
+__device__ inline uint32_t pack_x2(float a, float b, bool f16) { return f16 ? pack_f16x2(a, b) : pack_bf16x2(a, b); }
+// bf16 pair -> half pair (exact scaling aside, rounded to nearest even)
+__device__ inline uint32_t bf16x2_to_f16x2(uint32_t v)
+{
+    return pack_f16x2(__builtin_bit_cast(float, v << 16), __builtin_bit_cast(float, v & 0xffff0000u));
 }
 
 // ---- OCP fp8 e4m3 -> float (exact) ----

@@ -174,13 +174,12 @@ struct mk_engine {
     } slots[2];
     uint32_t gh = 0, gw = 0;
     std::vector<float> rope_host;
-    Buf rope;                     // [S + N][64][2]
-    uint32_t rope_S = 0xffffffffu;
+    Buf rope;                     // [tables][S + N][64][2]
+    std::vector<uint32_t> rope_key; // (S, h, w, the samples' prompt rows) the table was built for
 
     // ---- scratch ----
-    Buf x_img, x_txt, xn_img, xn_txt, q, k, vt, att, hid, out, lat, lat_bf, tn, tproj, temb_h, temb, mod, omod, qkv,
-        gu;
-    Buf xo; // SDXL
+    Buf x_img, x_txt, xn_img, xn_txt, q, k, vt, att, hid, out, lat, lat_bf, tn, tproj, temb_h, temb, mod, omod, qkv;
+    Buf vpos; // the positive pass's velocity when guidance runs as two passes
 
     // ---- probe / timing ----
     mk_probe_fn probe = nullptr;
@@ -453,17 +452,36 @@ struct mk_engine {
         return MK_OK;
     }
 
-    mk_status make_rope(uint32_t S)
+    // The RoPE table(s) of a step: one table of S + h w rows (mk_rope_table) when n = 1; n tables for samples whose
+    // prompts have Sb[b] <= S rows, all padded to S text rows: table b holds the text positions 0 .. S - 1 and, from
+    // row S on, its image rows at frame Sb[b].
+    mk_status make_rope(const uint32_t* Sb, uint32_t n, uint32_t S)
     {
-        if (S == rope_S && !rope_host.empty())
+        std::vector<uint32_t> key{S, gh, gw};
+        key.insert(key.end(), Sb, Sb + n);
+        if (key == rope_key)
             return MK_OK;
-        rope_host.assign((uint64_t(S) + uint64_t(gh) * gw) * 128, 0.0f);
-        MK_TRY(mk_rope_table(S, gh, gw, rope_host.data()));
+        const uint64_t N = uint64_t(gh) * gw, rows = S + N;
+        std::vector<float> base(rows * 128), t;
+        MK_TRY(mk_rope_table(S, gh, gw, base.data()));
+        rope_host.assign(n * rows * 128, 0.0f);
+        for (uint32_t b = 0; b < n; ++b) {
+            float* tab = rope_host.data() + b * rows * 128;
+            if (Sb[b] == S) {
+                std::copy(base.begin(), base.end(), tab);
+            } else {
+                std::copy(base.begin(), base.begin() + S * 128, tab); // the text positions 0 .. S - 1
+                t.assign((Sb[b] + N) * 128, 0.0f);
+                MK_TRY(mk_rope_table(Sb[b], gh, gw, t.data()));
+                std::copy(t.begin() + Sb[b] * 128, t.end(), tab + S * 128); // the image rows at frame Sb[b]
+            }
+        }
         MK_TRY(rope.ensure(rope_host.size() * 4));
         MK_HIP(hipMemcpy(rope.p, rope_host.data(), rope_host.size() * 4, hipMemcpyHostToDevice));
-        rope_S = S;
+        rope_key = key;
         return MK_OK;
     }
+    mk_status make_rope(uint32_t S) { return make_rope(&S, 1, S); }
 
     // Sinusoidal embedding, cos half first (qwen_image.cpp:179-187), of v (= 1000 sigma) for each row.
     static void sinusoid(float v, float* out)
@@ -481,10 +499,16 @@ struct mk_engine {
     mk_status dual_step(const float* lat_dev, float sigma, const uint32_t* slot_of, uint32_t nb)
     {
         const uint32_t D = cfg.dim, H = cfg.heads, F = cfg.ffn, E = cfg.text_dim, L = cfg.latent;
-        const uint32_t S = slots[slot_of[0]].S, N = gh * gw, T = S + N;
+        // a guidance batch whose prompts differ in length: every sample's text takes S = the longest prompt's rows,
+        // a shorter prompt's rows [S_b, S) are zero on input and masked as keys; sample b's image rows keep their
+        // RoPE frame S_b (one table a sample)
+        uint32_t Sb[2] = {slots[slot_of[0]].S, nb > 1 ? slots[slot_of[1]].S : 0};
+        const uint32_t S = nb > 1 ? std::max(Sb[0], Sb[1]) : Sb[0], N = gh * gw, T = S + N;
+        const bool ragged = nb > 1 && Sb[0] != Sb[1];
         const uint32_t q_pad = uint32_t(round_up(T, 256)), k_pad = uint32_t(round_up(T, 64));
         const float eps = 1e-6f;
-        MK_TRY(make_rope(S));
+        MK_TRY(make_rope(Sb, ragged ? nb : 1, S));
+        uint32_t hole[4] = {Sb[0], S, Sb[1], S}; // keys [S_b, S) of sample b
         // scratch
         MK_TRY(x_img.ensure(size_t(nb) * N * D * 4));
         MK_TRY(x_txt.ensure(size_t(nb) * S * D * 4));
@@ -534,11 +558,14 @@ struct mk_engine {
         }
         MK_TRY(timed("gemv", 2.0 * 2 * D * D, [&] { return mk_gemv(temb.f(), 1, D, norm_out.w, norm_out.bias, 2 * D, omod.f(), 1, stream); }));
         // text in: RMSNorm(w) -> Linear; image in: Linear
-        for (uint32_t b = 0; b < nb; ++b)
+        for (uint32_t b = 0; b < nb; ++b) {
             MK_TRY(timed("norm", 0, [&] {
-                return mk_rms_norm(slots[slot_of[b]].prompt.f(), S, E, txt_norm, 0.0f, eps,
+                return mk_rms_norm(slots[slot_of[b]].prompt.f(), Sb[b], E, txt_norm, 0.0f, eps,
                                    tn.h() + size_t(b) * S * E, stream);
             }));
+            if (Sb[b] < S)
+                MK_TRY(fill_zero(tn.h() + (size_t(b) * S + Sb[b]) * E, size_t(S - Sb[b]) * E * 2, stream));
+        }
         MK_TRY(gemm(txt_in, tn.p, E, 0, nb * S, 1, x_txt.p, D, 0, MK_EPI_STORE, MK_F32));
         MK_TRY(timed("convert", 0, [&] { return mk_f32_to_bf16(lat_dev, size_t(nb) * N * L, lat_bf.p, stream); }));
         MK_TRY(gemm(img_in, lat_bf.p, L, 0, nb * N, 1, x_img.p, D, 0, MK_EPI_STORE, MK_F32));
@@ -586,6 +613,7 @@ struct mk_engine {
                 ha[j].norm_q = B.nq[s.which];
                 ha[j].norm_k = B.nk[s.which];
                 ha[j].rope = rope.f();
+                ha[j].rope_stride = ragged ? int64_t(T) * 128 : 0;
                 ha[j].rope_mode = 2;
                 ha[j].eps = eps;
                 ha[j].k_scale = kScaleLog2; // K carries the softmax scale: attention runs with scale 0
@@ -594,8 +622,8 @@ struct mk_engine {
             }
             MK_TRY(gemm2(g, "gemm.qkv"));
             MK_TRY(timed("attention", attn_flops, [&] {
-                return mk_attention(q.p, k.p, vt.p, att.p, nb, H, H, 128, T, q_pad, T, k_pad, D, int64_t(T) * D, 0, 0,
-                                    0.0f, stream);
+                return mk_attention(q.p, k.p, vt.p, att.p, MK_BF16, nb, H, H, 128, T, q_pad, T, k_pad, D,
+                                    int64_t(T) * D, 0, 0, 0.0f, ragged ? hole : nullptr, stream);
             }));
             for (int j = 0; j < 2; ++j) {
                 const St& s = st[j];
@@ -652,7 +680,6 @@ struct mk_engine {
         MK_TRY(k.ensure(size_t(H) * k_pad * 128 * 2));
         MK_TRY(vt.ensure(size_t(H) * 128 * k_pad * 2));
         MK_TRY(att.ensure(size_t(T) * D * 2));
-        MK_TRY(gu.ensure(size_t(T) * 2 * F * 2));
         MK_TRY(hid.ensure(size_t(T) * F * 2));
         MK_TRY(out.ensure(size_t(T) * L * 4));
         MK_TRY(lat_bf.ensure(size_t(N) * L * 2));
@@ -716,6 +743,7 @@ struct mk_engine {
             ha.rope_mode = 2;
             ha.eps = eps;
             ha.k_scale = kScaleLog2;
+            ha.dtype = MK_F16; // the reference's heads_norm_half / heads_half
             // the text's keys and values (heads_rows): kept after the first step's q/k/v, restored before the later
             // steps'. V^T keeps whole groups of 16 keys (its columns permute keys within a group); a group shared
             // with image keys is rewritten by the image rows' q/k/v that follow the restore.
@@ -727,7 +755,8 @@ struct mk_engine {
                 MK_HIP(hipMemcpy2DAsync(vt.p, size_t(k_pad) * 2, vc, size_t(S16) * 2, size_t(S16) * 2,
                                         size_t(H) * 128, hipMemcpyDeviceToDevice, stream));
             }
-            MK_TRY(gemm(B.qkv[0], xn_img.p, D, 0, T, 1, nullptr, 0, 0, MK_EPI_HEADS, MK_BF16, nullptr, 0, 0, 0, &ha));
+            MK_TRY(gemm(B.qkv[0], xn_img.p, D, 0, T, 1, nullptr, 0, 0, MK_EPI_HEADS, MK_BF16, nullptr, 0, 0, 0, &ha,
+                        "gemm.qkv"));
             if (first) {
                 MK_HIP(hipMemcpy2DAsync(kc, size_t(S) * 256, k.p, size_t(k_pad) * 256, size_t(S) * 256, H,
                                         hipMemcpyDeviceToDevice, stream));
@@ -735,19 +764,20 @@ struct mk_engine {
                                         size_t(H) * 128, hipMemcpyDeviceToDevice, stream));
             }
             MK_TRY(timed("attention", 4.0 * pairs * 128 * H, [&] {
-                return mk_attention(q.p, k.p, vt.p, att.p, 1, H, H, 128, T, q_pad, n_k, k_pad, D, 0, row0, S, 0.0f,
-                                    stream);
+                return mk_attention(q.p, k.p, vt.p, att.p, MK_F16, 1, H, H, 128, T, q_pad, n_k, k_pad, D, 0, row0, S, 0.0f,
+                                    nullptr, stream);
             }));
             MK_TRY(gemm(B.o[0], att.p, D, 0, T, 1, x_img.p, D, 0, MK_EPI_GATE_TANH, MK_F32, mod.f() + D, 4 * D, split,
-                        T));
+                        T, nullptr, "gemm.o"));
             MK_TRY(timed("ln_modulate", 0, [&] {
                 return mk_ln_modulate(x_img.f(), T, D, mod.f() + 2 * D, nullptr, 4 * D, split, T, eps, xn_img.p,
                                       stream);
             }));
-            MK_TRY(gemm(B.ff1[0], xn_img.p, D, 0, T, 1, gu.p, 2 * F, 0, MK_EPI_STORE, MK_BF16));
-            MK_TRY(timed("swiglu", 0, [&] { return mk_swiglu(gu.p, MK_BF16, T, F, hid.p, stream); }));
+            // gate|up -> swiglu_rows fused: the GEMM's epilogue takes silu(gate) up on the fp32 accumulators
+            MK_TRY(gemm(B.ff1[0], xn_img.p, D, 0, T, 1, hid.p, F, 0, MK_EPI_SWIGLU, MK_BF16, nullptr, 0, 0, 0, nullptr,
+                        "gemm.ff1"));
             MK_TRY(gemm(B.ff2[0], hid.p, F, 0, T, 1, x_img.p, D, 0, MK_EPI_GATE_TANH, MK_F32, mod.f() + 3 * D, 4 * D,
-                        split, T));
+                        split, T, nullptr, "gemm.ff2"));
             MK_TRY(probe_f32("block", int(i), x_img.f(), size_t(T) * D));
         }
         MK_TRY(timed("ln_modulate", 0, [&] {
@@ -776,8 +806,11 @@ struct mk_engine {
             MK_TRY(gemm(blocks[i].kv2, tn.p, E, 0, S, 1, qkv.p, 2 * c, 0, MK_EPI_STORE, MK_BF16));
             uint16_t* kd = slots[0].ck.h() + (size_t(i) * 2 + slot) * H * s_pad * 64;
             uint16_t* vd = slots[0].cvt.h() + (size_t(i) * 2 + slot) * H * 64 * s_pad;
-            MK_TRY(mk_heads(qkv.p, 1, S, 2 * c, 0, 0, H, 64, nullptr, 0, nullptr, 0, kd, s_pad, 0, 0, stream));
-            MK_TRY(mk_heads(qkv.p, 1, S, 2 * c, 0, c, H, 64, nullptr, 0, nullptr, 0, vd, s_pad, 0, 1, stream));
+            // the reference's half heads (heads_half, sdxl.cpp:439-448)
+            MK_TRY(mk_heads(qkv.p, 1, S, 2 * c, 0, 0, H, 64, nullptr, 0, nullptr, 0, kd, s_pad, 0, 0, MK_F16,
+                            stream));
+            MK_TRY(mk_heads(qkv.p, 1, S, 2 * c, 0, c, H, 64, nullptr, 0, nullptr, 0, vd, s_pad, 0, 1, MK_F16,
+                            stream));
         }
         return MK_OK;
     }
@@ -795,7 +828,6 @@ struct mk_engine {
         MK_TRY(k.ensure(size_t(nb) * H * k_pad * 64 * 2));
         MK_TRY(vt.ensure(size_t(nb) * H * 64 * k_pad * 2));
         MK_TRY(att.ensure(size_t(nb) * n * c * 2));
-        MK_TRY(gu.ensure(size_t(nb) * n * 2 * F * 2));
         MK_TRY(hid.ensure(size_t(nb) * n * F * 2));
         if (k_pad_last != k_pad) {
             MK_HIP(hipMemsetAsync(k.p, 0, k.bytes, stream));
@@ -810,39 +842,47 @@ struct mk_engine {
         for (uint32_t i = 0; i < cfg.blocks; ++i) {
             const Block& B = blocks[i];
             MK_TRY(timed("norm", 0, [&] { return mk_layer_norm(hs, nb * n, c, B.n1g, B.n1b, 1e-5f, xn_img.p, stream); }));
-            MK_TRY(gemm(B.qkv[0], xn_img.p, c, 0, nb * n, 1, qkv.p, 3 * c, 0, MK_EPI_STORE, MK_BF16));
+            MK_TRY(gemm(B.qkv[0], xn_img.p, c, 0, nb * n, 1, qkv.p, 3 * c, 0, MK_EPI_STORE, MK_BF16, nullptr, 0, 0, 0,
+                        nullptr, "gemm.qkv"));
             MK_TRY(timed("heads", 0, [&] {
                 mk_status s = mk_heads(qkv.p, nb, n, 3 * c, int64_t(n) * 3 * c, 0, H, 64, nullptr, 0, nullptr, 0, q.p,
-                                       q_pad, 0, 0, stream);
+                                       q_pad, 0, 0, MK_F16, stream);
                 if (s == MK_OK)
                     s = mk_heads(qkv.p, nb, n, 3 * c, int64_t(n) * 3 * c, c, H, 64, nullptr, 0, nullptr, 0, k.p, k_pad,
-                                 0, 0, stream);
+                                 0, 0, MK_F16, stream);
                 if (s == MK_OK)
                     s = mk_heads(qkv.p, nb, n, 3 * c, int64_t(n) * 3 * c, 2 * c, H, 64, nullptr, 0, nullptr, 0, vt.p,
-                                 k_pad, 0, 1, stream);
+                                 k_pad, 0, 1, MK_F16, stream);
                 return s;
             }));
             MK_TRY(timed("attention", 4.0 * double(n) * n * 64 * H * nb, [&] {
-                return mk_attention(q.p, k.p, vt.p, att.p, nb, H, H, 64, n, q_pad, n, k_pad, c, nc, 0, 0, scale, stream);
+                return mk_attention(q.p, k.p, vt.p, att.p, MK_F16, nb, H, H, 64, n, q_pad, n, k_pad, c, nc, 0, 0, scale, nullptr,
+                                    stream);
             }));
-            MK_TRY(gemm(B.o[0], att.p, c, 0, nb * n, 1, hs, c, 0, MK_EPI_ADD, MK_F32));
+            MK_TRY(gemm(B.o[0], att.p, c, 0, nb * n, 1, hs, c, 0, MK_EPI_ADD, MK_F32, nullptr, 0, 0, 0, nullptr,
+                        "gemm.o"));
             MK_TRY(timed("norm", 0, [&] { return mk_layer_norm(hs, nb * n, c, B.n2g, B.n2b, 1e-5f, xn_img.p, stream); }));
-            MK_TRY(gemm(B.q2, xn_img.p, c, 0, nb * n, 1, qkv.p, c, 0, MK_EPI_STORE, MK_BF16));
+            MK_TRY(gemm(B.q2, xn_img.p, c, 0, nb * n, 1, qkv.p, c, 0, MK_EPI_STORE, MK_BF16, nullptr, 0, 0, 0, nullptr,
+                        "gemm.q2"));
             MK_TRY(timed("heads", 0, [&] {
                 return mk_heads(qkv.p, nb, n, c, int64_t(n) * c, 0, H, 64, nullptr, 0, nullptr, 0, q.p, q_pad, 0, 0,
-                                stream);
+                                MK_F16, stream);
             }));
             // cross attention: batch b reads slot b's context keys (consecutive in the cache)
             const uint16_t* kc = slots[0].ck.h() + size_t(i) * 2 * H * s_pad * 64;
             const uint16_t* vc = slots[0].cvt.h() + size_t(i) * 2 * H * 64 * s_pad;
             MK_TRY(timed("attention", 4.0 * double(n) * S * 64 * H * nb, [&] {
-                return mk_attention(q.p, kc, vc, att.p, nb, H, H, 64, n, q_pad, S, s_pad, c, nc, 0, 0, scale, stream);
+                return mk_attention(q.p, kc, vc, att.p, MK_F16, nb, H, H, 64, n, q_pad, S, s_pad, c, nc, 0, 0, scale, nullptr,
+                                    stream);
             }));
-            MK_TRY(gemm(B.o[1], att.p, c, 0, nb * n, 1, hs, c, 0, MK_EPI_ADD, MK_F32));
+            MK_TRY(gemm(B.o[1], att.p, c, 0, nb * n, 1, hs, c, 0, MK_EPI_ADD, MK_F32, nullptr, 0, 0, 0, nullptr,
+                        "gemm.o2"));
             MK_TRY(timed("norm", 0, [&] { return mk_layer_norm(hs, nb * n, c, B.n3g, B.n3b, 1e-5f, xn_img.p, stream); }));
-            MK_TRY(gemm(B.ff1[0], xn_img.p, c, 0, nb * n, 1, gu.p, 2 * F, 0, MK_EPI_STORE, MK_BF16));
-            MK_TRY(timed("geglu", 0, [&] { return mk_geglu(gu.p, MK_BF16, nb * n, F, hid.p, stream); }));
-            MK_TRY(gemm(B.ff2[0], hid.p, F, 0, nb * n, 1, hs, c, 0, MK_EPI_ADD, MK_F32));
+            // ff.net.0 -> geglu_rows fused into the GEMM's epilogue
+            MK_TRY(gemm(B.ff1[0], xn_img.p, c, 0, nb * n, 1, hid.p, F, 0, MK_EPI_GEGLU, MK_BF16, nullptr, 0, 0, 0,
+                        nullptr, "gemm.ff1"));
+            MK_TRY(gemm(B.ff2[0], hid.p, F, 0, nb * n, 1, hs, c, 0, MK_EPI_ADD, MK_F32, nullptr, 0, 0, 0, nullptr,
+                        "gemm.ff2"));
         }
         // proj_out + bias + the transformer's input
         MK_HIP(hipMemcpyAsync(y, x, size_t(nb) * nc * 4, hipMemcpyDeviceToDevice, stream));
@@ -1004,7 +1044,7 @@ mk_status mk_begin(mk_engine* e, const float* prompt, size_t rows, uint32_t h, u
         return fail(MK_ERR_ARG, "begin: empty latent grid");
     auto& g = e->slots[slot];
     if (e->gh != h || e->gw != w)
-        e->rope_S = 0xffffffffu;
+        e->rope_key.clear();
     e->gh = h;
     e->gw = w;
     g.S = uint32_t(rows);
@@ -1065,8 +1105,8 @@ mk_status mk_step_cfg_device(mk_engine* e, const float* lat, float sigma, float 
         MK_HIP(hipEventDestroy(ev));
     }
     const float dt = sigma_next - sigma;
-    if (e->cfg.family == MK_FAMILY_DUAL && e->slots[0].S == e->slots[1].S) {
-        // both guidance passes as one batch of 2
+    if (e->cfg.family == MK_FAMILY_DUAL) {
+        // both guidance passes as one batch of 2 (prompts of different lengths padded to the longer one)
         MK_TRY(e->lat.ensure(2 * N * L * 4));
         MK_HIP(hipMemcpyAsync(e->lat.p, lat, N * L * 4, hipMemcpyDeviceToDevice, e->stream));
         MK_HIP(hipMemcpyAsync(e->lat.f() + N * L, lat, N * L * 4, hipMemcpyDeviceToDevice, e->stream));
@@ -1076,25 +1116,20 @@ mk_status mk_step_cfg_device(mk_engine* e, const float* lat, float sigma, float 
             return mk_cfg_euler(lat, e->out.f(), e->out.f() + N * L, N * L, guidance, dt, lat_out, e->stream);
         }));
     } else {
-        // two passes (different text lengths, or the 2.1 graph whose slots keep their own K / V)
-        Buf pos;
+        // two passes (the 2.1 graph, whose slots keep their own K / V): the positive velocity waits in a buffer of
+        // the engine's
+        Buf& pos = e->vpos;
         MK_TRY(pos.ensure(N * L * 4));
         MK_TRY(e->lat.ensure(N * L * 4));
         MK_HIP(hipMemcpyAsync(e->lat.p, lat, N * L * 4, hipMemcpyDeviceToDevice, e->stream));
         for (uint32_t s = 0; s < 2; ++s) {
-            if (e->cfg.family == MK_FAMILY_DUAL) {
-                const uint32_t so[1] = {s};
-                MK_TRY(e->dual_step(e->lat.f(), sigma, so, 1));
-            } else {
-                MK_TRY(e->q21_step(e->lat.f(), sigma, s));
-            }
+            MK_TRY(e->q21_step(e->lat.f(), sigma, s));
             if (s == 0)
                 MK_HIP(hipMemcpyAsync(pos.p, e->out.p, N * L * 4, hipMemcpyDeviceToDevice, e->stream));
         }
         MK_TRY(e->timed("cfg_euler", 0, [&] {
             return mk_cfg_euler(lat, pos.f(), e->out.f(), N * L, guidance, dt, lat_out, e->stream);
         }));
-        MK_HIP(hipStreamSynchronize(e->stream)); // `pos` is freed on return
     }
     if (stream && stream != e->stream) {
         hipEvent_t ev;

@@ -29,6 +29,8 @@ struct HeadsP {
     uint32_t heads, q_pad, k_pad, row0, q_row0, rope_mode, dim;
     const float *norm_q, *norm_k, *rope;
     float eps, k_scale;
+    uint32_t f16;     // Q, K, V^T as IEEE half (else bf16)
+    int64_t rope_bs;  // floats between the batch items' RoPE tables
 };
 
 struct GemmP {
@@ -47,6 +49,8 @@ struct GemmP {
     // 3 x 3 convolution (EK_CONV): the padded grid's row width w + 2, k tiles a tap (channels / 64), and
     // ceil(2^16 / conv_tpt) for the tap index by multiply-shift
     uint32_t conv_pw, conv_tpt, conv_inv;
+    // gated linear unit (EK_GLU): the weights' rows are [first part F; second part F], the output [M][F]
+    uint32_t glu_f;
 };
 
 // One launch of up to two GEMMs of equal N, K and epilogue kind (the dual-stream blocks' image and text
@@ -83,8 +87,9 @@ __device__ inline void f8x16_to_bf16(const u32x4& v, u32x4& lo, u32x4& hi)
     hi = u32x4{o[4], o[5], o[6], o[7]};
 }
 
-// Epilogue kinds (template): a plain store, an activation, a read-modify-write of the fp32 residual, the q/k/v heads.
-enum { EK_STORE = 0, EK_ACT = 1, EK_RMW = 2, EK_HEADS = 3 };
+// Epilogue kinds (template): a plain store, an activation, a read-modify-write of the fp32 residual, the q/k/v heads,
+// a gated linear unit (SwiGLU / GEGLU: each output channel from two weight rows F apart).
+enum { EK_STORE = 0, EK_ACT = 1, EK_RMW = 2, EK_HEADS = 3, EK_GLU = 4 };
 // Flag on the epilogue kind: the A operand is a 3 x 3 convolution's input (implicit im2col, see conv_koff).
 constexpr int EK_CONV = 8;
 
@@ -232,15 +237,15 @@ __device__ inline void epi_heads(const GemmP& p, const float* st, int ld, int to
                     // physical columns 16g + 0..15 hold keys 16g + {0..3, 8..11, 4..7, 12..15}
                     const int j0 = 16 * g;
                     *reinterpret_cast<u32x4*>(dst + k0 + j0) =
-                        u32x4{pack_bf16x2(v(j0 + 0), v(j0 + 1)), pack_bf16x2(v(j0 + 2), v(j0 + 3)),
-                              pack_bf16x2(v(j0 + 8), v(j0 + 9)), pack_bf16x2(v(j0 + 10), v(j0 + 11))};
+                        u32x4{pack_x2(v(j0 + 0), v(j0 + 1), h.f16), pack_x2(v(j0 + 2), v(j0 + 3), h.f16),
+                              pack_x2(v(j0 + 8), v(j0 + 9), h.f16), pack_x2(v(j0 + 10), v(j0 + 11), h.f16)};
                     *reinterpret_cast<u32x4*>(dst + k0 + j0 + 8) =
-                        u32x4{pack_bf16x2(v(j0 + 4), v(j0 + 5)), pack_bf16x2(v(j0 + 6), v(j0 + 7)),
-                              pack_bf16x2(v(j0 + 12), v(j0 + 13)), pack_bf16x2(v(j0 + 14), v(j0 + 15))};
+                        u32x4{pack_x2(v(j0 + 4), v(j0 + 5), h.f16), pack_x2(v(j0 + 6), v(j0 + 7), h.f16),
+                              pack_x2(v(j0 + 12), v(j0 + 13), h.f16), pack_x2(v(j0 + 14), v(j0 + 15), h.f16)};
                 }
             } else {
                 for (int t = 0; t < 32 && tok0 + t < int(p.M); ++t)
-                    dst[vt_col(k0 + t)] = f2bf_bits(v(t));
+                    dst[vt_col(k0 + t)] = h.f16 ? f2h_bits(v(t)) : f2bf_bits(v(t));
             }
         }
         return;
@@ -261,12 +266,13 @@ __device__ inline void epi_heads(const GemmP& p, const float* st, int ld, int to
     // the lane's 4 channels; mode 1, channel d and d + 64 pair at angle d -> cos / sin of angles 4 (c % 16) .. + 3
     auto rope_lo = [&](int i) {
         const int t = min(tok0 + r0 + 2 * i, last);
-        const float* cs = h.rope + (int64_t(h.row0) + t) * 128;
+        const float* cs = h.rope + int64_t(z) * h.rope_bs + (int64_t(h.row0) + t) * 128;
         return *reinterpret_cast<const f32x4*>(cs + (mode == 2 ? ch : 8 * (c & 15)));
     };
     auto rope_hi = [&](int i) {
         const int t = min(tok0 + r0 + 2 * i, last);
-        return *reinterpret_cast<const f32x4*>(h.rope + (int64_t(h.row0) + t) * 128 + 8 * (c & 15) + 4);
+        return *reinterpret_cast<const f32x4*>(h.rope + int64_t(z) * h.rope_bs + (int64_t(h.row0) + t) * 128 +
+                                               8 * (c & 15) + 4);
     };
     auto val = [&](int i) {
         f32x4 x = *reinterpret_cast<const f32x4*>(st + (r0 + 2 * i) * ld + ch);
@@ -331,7 +337,7 @@ __device__ inline void epi_heads(const GemmP& p, const float* st, int ld, int to
         const int t = tok0 + r0 + 2 * i;
         if (t <= last)
             *reinterpret_cast<u32x2*>(base + int64_t(t) * 128) =
-                u32x2{pack_bf16x2(x[0], x[1]), pack_bf16x2(x[2], x[3])};
+                u32x2{pack_x2(x[0], x[1], h.f16), pack_x2(x[2], x[3], h.f16)};
     };
 #pragma unroll
     for (int i = 0; i < 8; ++i)
@@ -418,7 +424,8 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
                                           uint16_t* smem, const SkP* sk, int publish, int fix_lo = 0,
                                           int fix_hi = -1, int self = -1, uint64_t tt = 0)
 {
-    static_assert((EK & 7) != EK_HEADS || !(EK & EK_CONV), "a convolution has no heads epilogue");
+    static_assert(((EK & 7) != EK_HEADS && (EK & 7) != EK_GLU) || !(EK & EK_CONV),
+                  "a convolution has no heads or GLU epilogue");
     constexpr bool kConv = (EK & EK_CONV) != 0;
     constexpr int EKE = EK & 7;                 // the epilogue kind
     constexpr int NT = 64 * NW;                 // threads
@@ -448,7 +455,18 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
     // spans the tile's rows (base = its first row), the lane's 32-bit byte offset selects row and chunk, the k
     // offset is a scalar; activation rows past M read the last row.
     const char* gA = reinterpret_cast<const char*>(p.a + int64_t(z) * p.sa + int64_t(m0) * p.lda);
-    const char* gW = static_cast<const char*>(p.w) + int64_t(n0) * p.K * (kF8 ? 1 : 2);
+    // GLU: the tile computes output channels tn BN/2 .. + BN/2; each wave's WC rows are WC/2 rows of the first part
+    // and the same channels' rows of the second part (F rows further on), so one lane's accumulator blocks cb and
+    // cb + CB/2 hold the two operands of the same output. wrow: the tile's local weight row -> row offset from gW.
+    constexpr bool kGlu = EKE == EK_GLU;
+    const int nw0 = kGlu ? int(tn) * (BN / 2) : n0;
+    const char* gW = static_cast<const char*>(p.w) + int64_t(nw0) * p.K * (kF8 ? 1 : 2);
+    auto wrow = [&](int r) -> int {
+        if constexpr (kGlu)
+            return (r / WC) * (WC / 2) + (r % WC) % (WC / 2) + ((r % WC) >= WC / 2 ? int(p.glu_f) : 0);
+        else
+            return r;
+    };
     // a convolution's tile reads up to 2 (w + 2) + 2 rows past its own (the taps' shifts), all inside the input
     const BufRes rsA = buf_res(
         gA, uint32_t(kConv ? (min(int(p.M) - m0, BM) + 2 * int64_t(p.conv_pw) + 2) * p.lda * 2
@@ -466,7 +484,7 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
             return uint32_t(kt * BK * 2);
         }
     };
-    const BufRes rsW = buf_res(gW, uint32_t(int64_t(BN) * p.K * 2));
+    const BufRes rsW = buf_res(gW, uint32_t((kGlu ? int64_t(p.glu_f) + BN / 2 : int64_t(BN)) * p.K * 2));
     uint32_t oa[RA];
 #pragma unroll
     for (int i = 0; i < RA; ++i) {
@@ -479,13 +497,13 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
 #pragma unroll
         for (int i = 0; i < RW; ++i) {
             const int P = (i * NW + wave) * 64 + lane, row = P >> 3, kc = swz_chunk(row, P & 7);
-            ow[i] = uint32_t(row * int(p.K) + kc * 8) * 2;
+            ow[i] = uint32_t(wrow(row) * int(p.K) + kc * 8) * 2;
         }
     } else {
 #pragma unroll
         for (int i = 0; i < LW; ++i) {
             const int c = tid + NT * i, row = c >> 2, kc = c & 3;
-            gw8[i] = reinterpret_cast<const uint8_t*>(gW) + int64_t(row) * p.K + kc * 16;
+            gw8[i] = reinterpret_cast<const uint8_t*>(gW) + int64_t(wrow(row)) * p.K + kc * 16;
         }
     }
     u32x4 rw[kF8 ? LW : 1];
@@ -851,6 +869,55 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
         }
     };
     constexpr int NS = WM / 32, RB = TB / NS; // 32-token slices of a wave, MFMA token blocks a slice
+    if constexpr (EKE == EK_GLU) {
+        // out = silu(first) second (SwiGLU, swiglu_rows) or first gelu_erf(second) (GEGLU, geglu_rows), computed
+        // into blocks cb < CB/2 from blocks cb and cb + CB/2 (each with its rows' scale and bias), then stored as a
+        // slice of WC/2 channels
+        constexpr int CH2 = CB / 2, NQ = M16 ? 1 : 4; // groups of 4 consecutive channels a lane holds in a block
+        const int oc0 = int(tn) * (BN / 2) + wn * (WC / 2);
+        const bool swi = p.epi == MK_EPI_SWIGLU;
+#pragma unroll
+        for (int cb = 0; cb < CH2; ++cb)
+#pragma unroll
+            for (int q = 0; q < NQ; ++q) {
+                const int c1 = oc0 + cb * MB + (M16 ? 4 * g4 : 8 * q + 4 * hk), c2 = c1 + int(p.glu_f);
+                const f32x4 s1 = p.wscale ? *reinterpret_cast<const f32x4*>(p.wscale + c1) : f32x4{1, 1, 1, 1};
+                const f32x4 s2 = p.wscale ? *reinterpret_cast<const f32x4*>(p.wscale + c2) : f32x4{1, 1, 1, 1};
+                const f32x4 b1 = p.bias ? *reinterpret_cast<const f32x4*>(p.bias + c1) : f32x4{0, 0, 0, 0};
+                const f32x4 b2 = p.bias ? *reinterpret_cast<const f32x4*>(p.bias + c2) : f32x4{0, 0, 0, 0};
+#pragma unroll
+                for (int tb = 0; tb < TB; ++tb)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float a = acc[cb][tb][4 * q + e] * s1[e] + b1[e];
+                        const float g = acc[cb + CH2][tb][4 * q + e] * s2[e] + b2[e];
+                        acc[cb][tb][4 * q + e] =
+                            swi ? silu_f(a) * g : a * (0.5f * g * (1.0f + erf_fit(g * 0.70710678f)));
+                    }
+            }
+        constexpr int WH = WC / 2, LDH = WH + 4;
+        float* sh = reinterpret_cast<float*>(smem) + wave * 32 * LDH;
+        const EpiCh unit{f32x4{1, 1, 1, 1}, f32x4{0, 0, 0, 0}, f32x4{}, f32x4{}};
+#pragma unroll
+        for (int s2 = 0; s2 < NS; ++s2) {
+#pragma unroll
+            for (int cb = 0; cb < CH2; ++cb) {
+                if constexpr (M16) {
+#pragma unroll
+                    for (int h = 0; h < 2; ++h)
+                        *reinterpret_cast<f32x4*>(sh + (16 * h + r16) * LDH + cb * 16 + 4 * g4) = acc[cb][2 * s2 + h];
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        *reinterpret_cast<f32x4*>(sh + r32 * LDH + cb * 32 + 8 * i + 4 * hk) =
+                            f32x4{acc[cb][s2][4 * i], acc[cb][s2][4 * i + 1], acc[cb][s2][4 * i + 2],
+                                  acc[cb][s2][4 * i + 3]};
+                }
+            }
+            epi_slice<EK_STORE, WH>(p, sh, LDH, m0 + wm * WM + s2 * 32, oc0, lane, zc, unit);
+        }
+        return;
+    }
     if constexpr (EKE == EK_HEADS) {
         // the heads epilogue is large: one copy of it in a rolled loop over the 32-token slices, which always
         // stages slice 0 of the accumulators and then rotates the next slice into its place (static register
@@ -1084,9 +1151,10 @@ mk_status launch(GemmP* p, uint32_t count, const GemmPlan& plan, hipStream_t s)
 // The epilogue kind of an mk_epilogue.
 int epi_kind(uint32_t e)
 {
-    return e == MK_EPI_HEADS ? EK_HEADS
-           : e == MK_EPI_STORE ? EK_STORE
+    return e == MK_EPI_HEADS                             ? EK_HEADS
+           : e == MK_EPI_STORE                           ? EK_STORE
            : (e == MK_EPI_GELU_TANH || e == MK_EPI_SILU) ? EK_ACT
+           : (e == MK_EPI_SWIGLU || e == MK_EPI_GEGLU)   ? EK_GLU
                                                          : EK_RMW;
 }
 
@@ -1104,8 +1172,11 @@ mk_status prepare(const mk_gemm_args* a, GemmP& p)
         return fail(MK_ERR_ARG, "gemm: A and W must be 16-byte aligned with lda a multiple of 8");
     if (a->lda >= (1u << 23) || a->K >= (1u << 23))
         return fail(MK_ERR_ARG, "gemm: lda and K must be below 2^23 (32-bit byte offsets within a tile)");
-    if (a->epilogue > MK_EPI_HEADS)
+    if (a->epilogue > MK_EPI_GEGLU)
         return fail(MK_ERR_ARG, "gemm: unknown epilogue");
+    const bool glu = a->epilogue == MK_EPI_SWIGLU || a->epilogue == MK_EPI_GEGLU;
+    if (glu && (a->N % 128 || (a->N / 2) % 4))
+        return fail(MK_ERR_ARG, "gemm: a gated linear unit needs N = 2 F a multiple of 128");
     const bool gated = a->epilogue == MK_EPI_GATE_ADD || a->epilogue == MK_EPI_GATE_TANH;
     if (gated && !a->gate)
         return fail(MK_ERR_ARG, "gemm: gated epilogue without a gate");
@@ -1131,16 +1202,20 @@ mk_status prepare(const mk_gemm_args* a, GemmP& p)
     p.epi = a->epilogue;
     p.c_bf16 = a->c_dtype == MK_BF16;
     p.batch = a->batch;
+    p.glu_f = glu ? a->N / 2 : 0;
     if (a->epilogue == MK_EPI_HEADS) {
         const mk_heads_args* h = a->heads;
         if (!h || !h->q || !h->k || !h->vt || h->head_dim != 128 || a->N % 256 || (a->N / 3) % 128 ||
             a->N / 3 != h->heads * 128 || h->rope_mode > 2 || (h->rope_mode && !h->rope) || h->k_pad % 16 ||
-            uint64_t(h->row0) + a->M > h->k_pad || uint64_t(h->q_row0) + a->M > h->q_pad)
+            uint64_t(h->row0) + a->M > h->k_pad || uint64_t(h->q_row0) + a->M > h->q_pad ||
+            (h->dtype != 0 && h->dtype != MK_BF16 && h->dtype != MK_F16))
             return fail(MK_ERR_ARG, "gemm heads epilogue: needs q, k, vt, head_dim 128, N = 3 * heads * 128 a multiple "
-                                    "of 256, k_pad a multiple of 16, and row0 + M within the padded rows");
+                                    "of 256, k_pad a multiple of 16, row0 + M within the padded rows, and dtype bf16 "
+                                    "or f16");
         p.hp = HeadsP{static_cast<uint16_t*>(h->q), static_cast<uint16_t*>(h->k), static_cast<uint16_t*>(h->vt),
                       h->heads, h->q_pad, h->k_pad, h->row0, h->q_row0, h->rope_mode, a->N / 3, h->norm_q, h->norm_k,
-                      h->rope, h->eps, h->k_scale == 0.0f ? 1.0f : h->k_scale};
+                      h->rope, h->eps, h->k_scale == 0.0f ? 1.0f : h->k_scale, h->dtype == MK_F16 ? 1u : 0u,
+                      h->rope_stride};
     }
     return MK_OK;
 }
@@ -1223,8 +1298,8 @@ extern "C" mk_status mk_gemm_grouped(const mk_gemm_args* a, uint32_t count, void
             live[j++] = a[i];
     const GemmPlan plan = gemm_plan(live, n, uint32_t(cus > 0 ? cus : 1));
     const int bn = plan.bn;
-    if (bn == 64 && ek == EK_ACT)
-        return fail(MK_ERR_UNSUPPORTED, "gemm: activation epilogues need N a multiple of 128");
+    if (bn == 64 && (ek == EK_ACT || ek == EK_GLU))
+        return fail(MK_ERR_UNSUPPORTED, "gemm: activation and GLU epilogues need N a multiple of 128");
     hipStream_t s = static_cast<hipStream_t>(stream);
     mk_status e;
     // 256-wide tiles: 8 waves (two a SIMD, 64 x 128 wave tiles), so one wave's waits (barrier, loads) leave the
@@ -1239,6 +1314,8 @@ extern "C" mk_status mk_gemm_grouped(const mk_gemm_args* a, uint32_t count, void
             MK_GEMM_EK(256, EK_STORE);
         else if (ek == EK_ACT)
             MK_GEMM_EK(256, EK_ACT);
+        else if (ek == EK_GLU)
+            MK_GEMM_EK(256, EK_GLU);
         else
             MK_GEMM_EK(256, EK_RMW);
     } else if (bn == 128) {
@@ -1246,6 +1323,8 @@ extern "C" mk_status mk_gemm_grouped(const mk_gemm_args* a, uint32_t count, void
             MK_GEMM_EK(128, EK_STORE);
         else if (ek == EK_ACT)
             MK_GEMM_EK(128, EK_ACT);
+        else if (ek == EK_GLU)
+            MK_GEMM_EK(128, EK_GLU);
         else
             MK_GEMM_EK(128, EK_RMW);
     } else {

@@ -281,7 +281,8 @@ __global__ __launch_bounds__(256) void heads_kernel(const uint16_t* __restrict__
                                                     int64_t stride_x, uint32_t col0, uint32_t heads, uint32_t d,
                                                     const float* __restrict__ w, float eps,
                                                     const float* __restrict__ rope, uint32_t mode,
-                                                    uint16_t* __restrict__ out, uint32_t n_pad, uint32_t row0)
+                                                    uint16_t* __restrict__ out, uint32_t n_pad, uint32_t row0,
+                                                    bool f16)
 {
     const uint32_t lane = threadIdx.x & 63, bi = blockIdx.y;
     const uint64_t idx = uint64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
@@ -308,23 +309,29 @@ __global__ __launch_bounds__(256) void heads_kernel(const uint16_t* __restrict__
     }
     if (act) {
         uint16_t* o = out + ((uint64_t(bi) * heads + h) * n_pad + row0 + r) * d;
-        o[i0] = f2bf_bits(a);
-        o[i1] = f2bf_bits(b);
+        o[i0] = f16 ? f2h_bits(a) : f2bf_bits(a);
+        o[i1] = f16 ? f2h_bits(b) : f2bf_bits(b);
     }
 }
 
 // The layout alone (no norm, no rope): 16 bytes a thread, 32-bit indexing (rows * heads * d / 8 < 2^31; ld, col0,
-// stride_x multiples of 8; 16-byte aligned buffers). out [batch][heads][n_pad][d] row row0 + r = x's row r.
+// stride_x multiples of 8; 16-byte aligned buffers). out [batch][heads][n_pad][d] row row0 + r = x's row r (as half
+// when f16).
 __global__ __launch_bounds__(256) void heads_copy_kernel(const uint16_t* __restrict__ x, uint32_t rows, int64_t ld,
                                                          int64_t stride_x, uint32_t col0, uint32_t heads, uint32_t d,
-                                                         uint16_t* __restrict__ out, uint32_t n_pad, uint32_t row0)
+                                                         uint16_t* __restrict__ out, uint32_t n_pad, uint32_t row0,
+                                                         bool f16)
 {
     const uint32_t i = blockIdx.x * 256 + threadIdx.x, q = d / 8, bi = blockIdx.y;
     if (i >= rows * heads * q)
         return;
     const uint32_t c = (i % q) * 8, p = i / q, r = p / heads, h = p - r * heads;
-    const u32x4 v =
+    u32x4 v =
         *reinterpret_cast<const u32x4*>(x + uint64_t(bi) * stride_x + uint64_t(r) * ld + col0 + uint64_t(h) * d + c);
+    if (f16)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            v[j] = bf16x2_to_f16x2(v[j]);
     *reinterpret_cast<u32x4*>(out + ((uint64_t(bi) * heads + h) * n_pad + row0 + r) * d + c) = v;
 }
 
@@ -334,7 +341,8 @@ __global__ __launch_bounds__(256) void heads_copy_kernel(const uint16_t* __restr
 template <int kD>
 __global__ __launch_bounds__(256) void heads_t_kernel(const uint16_t* __restrict__ x, uint32_t rows, int64_t ld,
                                                       int64_t stride_x, uint32_t col0, uint32_t heads,
-                                                      uint16_t* __restrict__ out, uint32_t n_pad, uint32_t row0)
+                                                      uint16_t* __restrict__ out, uint32_t n_pad, uint32_t row0,
+                                                      bool f16)
 {
     __shared__ uint16_t t[64][kD + 2];
     const uint32_t r0 = blockIdx.x * 64, h = blockIdx.y, bi = blockIdx.z, tid = threadIdx.x;
@@ -345,6 +353,8 @@ __global__ __launch_bounds__(256) void heads_t_kernel(const uint16_t* __restrict
         if (r0 + r < rows)
             v = *reinterpret_cast<const uint32_t*>(x + uint64_t(bi) * stride_x + uint64_t(r0 + r) * ld + col0 +
                                                    uint64_t(h) * kD + c);
+        if (f16)
+            v = bf16x2_to_f16x2(v);
         t[r][c] = uint16_t(v);
         t[r][c + 1] = uint16_t(v >> 16);
     }
@@ -717,6 +727,23 @@ inline hipStream_t S(void* s) { return static_cast<hipStream_t>(s); }
 
 } // namespace
 
+__global__ __launch_bounds__(256) void zero_kernel(uint32_t* __restrict__ p, uint64_t n)
+{
+    for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < n; i += uint64_t(gridDim.x) * 256)
+        p[i] = 0;
+}
+
+mk_status fill_zero(void* p, size_t bytes, void* stream)
+{
+    if (bytes % 4 || (reinterpret_cast<uintptr_t>(p) & 3))
+        return fail(MK_ERR_ARG, "fill_zero: bytes and address must be multiples of 4");
+    if (!bytes)
+        return MK_OK;
+    zero_kernel<<<grid_for(bytes / 4), 256, 0, S(stream)>>>(static_cast<uint32_t*>(p), bytes / 4);
+    MK_LAUNCH_CHECK("fill_zero");
+    return MK_OK;
+}
+
 mk_status ln_modulate_group(const LnArgs* a, int count, uint32_t n, float eps, void* stream)
 {
     if (count < 1 || count > 2 || n % 4 || n > 4u * 64 * kMaxVec)
@@ -913,11 +940,13 @@ mk_status mk_gate_add(float* x, const void* y, uint32_t y_dtype, uint32_t rows, 
 
 mk_status mk_heads(const void* x, uint32_t batch, uint32_t rows, int64_t ld, int64_t stride_x, uint32_t col0,
                    uint32_t heads, uint32_t d, const float* w, float eps, const float* rope, uint32_t rope_mode,
-                   void* out, uint32_t n_pad, uint32_t row0, int transpose, void* stream)
+                   void* out, uint32_t n_pad, uint32_t row0, int transpose, uint32_t out_dtype, void* stream)
 {
     if (!x || !out || !batch || (d != 64 && d != 128) || rope_mode > 2 || (rope_mode && !rope) ||
-        uint64_t(row0) + rows > n_pad)
-        return fail(MK_ERR_ARG, "heads: null pointer, d not 64 / 128, bad rope mode, or rows past n_pad");
+        uint64_t(row0) + rows > n_pad || (out_dtype != MK_BF16 && out_dtype != MK_F16))
+        return fail(MK_ERR_ARG, "heads: null pointer, d not 64 / 128, bad rope mode, rows past n_pad, or an output "
+                                "dtype other than bf16 / f16");
+    const bool f16 = out_dtype == MK_F16;
     if (!rows)
         return MK_OK;
     if (transpose) {
@@ -928,20 +957,20 @@ mk_status mk_heads(const void* x, uint32_t batch, uint32_t rows, int64_t ld, int
         const dim3 grid(cdiv(rows, 64), heads, batch);
         if (d == 128)
             heads_t_kernel<128><<<grid, 256, 0, S(stream)>>>(static_cast<const uint16_t*>(x), rows, ld, stride_x, col0,
-                                                             heads, static_cast<uint16_t*>(out), n_pad, row0);
+                                                             heads, static_cast<uint16_t*>(out), n_pad, row0, f16);
         else
             heads_t_kernel<64><<<grid, 256, 0, S(stream)>>>(static_cast<const uint16_t*>(x), rows, ld, stride_x, col0,
-                                                            heads, static_cast<uint16_t*>(out), n_pad, row0);
+                                                            heads, static_cast<uint16_t*>(out), n_pad, row0, f16);
     } else if (!w && !(rope && rope_mode) && ld % 8 == 0 && col0 % 8 == 0 && stride_x % 8 == 0 &&
                !(reinterpret_cast<uintptr_t>(x) & 15) && !(reinterpret_cast<uintptr_t>(out) & 15) &&
                uint64_t(rows) * heads * d / 8 < (uint64_t(1) << 31)) {
         heads_copy_kernel<<<dim3(cdiv(uint64_t(rows) * heads * d / 8, 256), batch), 256, 0, S(stream)>>>(
             static_cast<const uint16_t*>(x), rows, ld, stride_x, col0, heads, d, static_cast<uint16_t*>(out), n_pad,
-            row0);
+            row0, f16);
     } else {
         heads_kernel<<<dim3(cdiv(uint64_t(rows) * heads, 4), batch), 256, 0, S(stream)>>>(
             static_cast<const uint16_t*>(x), rows, ld, stride_x, col0, heads, d, w, eps, rope, rope_mode,
-            static_cast<uint16_t*>(out), n_pad, row0);
+            static_cast<uint16_t*>(out), n_pad, row0, f16);
     }
     MK_LAUNCH_CHECK("heads");
     return MK_OK;

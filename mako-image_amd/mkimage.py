@@ -14,7 +14,7 @@ HERE = pathlib.Path(__file__).resolve().parent
 LIB_PATH = HERE / "libmkimage.so"
 
 F32, BF16, FP8, F16, DTYPE_OTHER = 0, 1, 2, 3, 255
-EPI_STORE, EPI_GELU_TANH, EPI_GATE_ADD, EPI_GATE_TANH, EPI_SILU, EPI_ADD, EPI_HEADS = range(7)
+EPI_STORE, EPI_GELU_TANH, EPI_GATE_ADD, EPI_GATE_TANH, EPI_SILU, EPI_ADD, EPI_HEADS, EPI_SWIGLU, EPI_GEGLU = range(9)
 FAMILY_DUAL, FAMILY_Q21, FAMILY_SDXL = 0, 1, 2
 
 _vp, _sz, _u32, _u64, _i64, _f, _d, _i = (C.c_void_p, C.c_size_t, C.c_uint32, C.c_uint64, C.c_int64, C.c_float,
@@ -29,7 +29,7 @@ class MkError(RuntimeError):
 class HeadsArgs(C.Structure):
     _fields_ = [("q", _vp), ("k", _vp), ("vt", _vp), ("heads", _u32), ("head_dim", _u32), ("q_pad", _u32),
                 ("k_pad", _u32), ("row0", _u32), ("q_row0", _u32), ("norm_q", _vp), ("norm_k", _vp), ("rope", _vp),
-                ("rope_mode", _u32), ("eps", _f), ("k_scale", _f)]
+                ("rope_mode", _u32), ("eps", _f), ("k_scale", _f), ("dtype", _u32), ("rope_stride", _i64)]
 
 
 class GemmArgs(C.Structure):
@@ -90,9 +90,10 @@ _SIGS = {
     "mk_gemv": (_i, [_vp, _u32, _u32, _vp, _vp, _u32, _vp, _i, _vp]),
     "mk_ln_modulate": (_i, [_vp, _u32, _u32, _vp, _vp, _i64, _u32, _u32, _f, _vp, _vp]),
     "mk_gate_add": (_i, [_vp, _vp, _u32, _u32, _u32, _vp, _i64, _u32, _u32, _i, _vp]),
-    "mk_heads": (_i, [_vp, _u32, _u32, _i64, _i64, _u32, _u32, _u32, _vp, _f, _vp, _u32, _vp, _u32, _u32, _i, _vp]),
-    "mk_attention": (_i, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _i64, _i64, _u32, _u32,
-                          _f, _vp]),
+    "mk_heads": (_i, [_vp, _u32, _u32, _i64, _i64, _u32, _u32, _u32, _vp, _f, _vp, _u32, _vp, _u32, _u32, _i, _u32,
+                      _vp]),
+    "mk_attention": (_i, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _i64, _i64, _u32,
+                          _u32, _f, _vp, _vp]),
     "mk_silu": (_i, [_vp, _sz, _vp]),
     "mk_gelu_tanh": (_i, [_vp, _sz, _vp]),
     "mk_swiglu": (_i, [_vp, _u32, _u32, _u32, _vp, _vp]),
@@ -316,6 +317,15 @@ def bf16_bits(a):
 
 def bf16_to_f32(b):
     return (np.asarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def f16_bits(a):
+    """float32 -> IEEE half bit patterns, round to nearest even."""
+    return np.ascontiguousarray(a, dtype=np.float32).astype(np.float16).view(np.uint16)
+
+
+def f16_to_f32(b):
+    return np.asarray(b, dtype=np.uint16).view(np.float16).astype(np.float32)
 
 
 class SafeTensors:

@@ -42,6 +42,23 @@ inline uint16_t to_bf16(float x)
 }
 inline float bf16(float x) { return from_bits(uint32_t(to_bf16(x)) << 16); }
 
+// Round-to-nearest-even to IEEE binary16 (`half`, the reference's heads and attention precision: heads_norm_half /
+// heads_half, qwen_image.cpp:165-167, 226-250, sdxl.cpp:439-448), as the float it stands for: 11 significant bits,
+// subnormals below 2^-14 on the grid of 2^-24, overflow (at or past the midpoint 65520) to infinity, NaN kept.
+inline float f16(float x)
+{
+    if (std::isnan(x))
+        return x;
+    const float a = std::fabs(x);
+    if (a >= 65520.0f)
+        return std::copysign(INFINITY, x);
+    int e;
+    std::frexp(a, &e);                       // a = f 2^e, f in [0.5, 1): binade 2^(e - 1)
+    const int b = std::max(e - 1, -14);      // subnormals share the step of binade -14
+    const float step = std::ldexp(1.0f, b - 10);
+    return std::copysign(std::nearbyint(a / step) * step, x); // exact scaling; ties to even in the default mode
+}
+
 // OCP fp8 e4m3 ("fn"): bias 7, no infinities, 0x7f / 0xff NaN, max 448; saturating round-to-nearest-even.
 inline float e4m3_decode(uint8_t b)
 {
@@ -403,6 +420,11 @@ void mkref_round_bf16(float* x, size_t n)
 {
     for (size_t i = 0; i < n; ++i)
         x[i] = bf16(x[i]);
+}
+void mkref_round_f16(float* x, size_t n)
+{
+    for (size_t i = 0; i < n; ++i)
+        x[i] = f16(x[i]);
 }
 uint8_t mkref_f32_to_e4m3(float x) { return e4m3_encode(x); }
 float mkref_e4m3_to_f32(uint8_t b) { return e4m3_decode(b); }
@@ -934,9 +956,10 @@ int mkref_q21_step(const mkref_model* mp, const float* prompt, int64_t S, const 
             heads_norm_rope(q.data(), T, D, 0, H, hd, m.vec(b + "attn.norm_q.weight"), eps, cs.data(), 2, Q.data(), T, 0);
             heads_norm_rope(k.data(), T, D, 0, H, hd, m.vec(b + "attn.norm_k.weight"), eps, cs.data(), 2, K.data(), T, 0);
             heads_norm_rope(v.data(), T, D, 0, H, hd, nullptr, eps, nullptr, 0, V.data(), T, 0);
-            mkref_round_bf16(Q.data(), Q.size());
-            mkref_round_bf16(K.data(), K.size());
-            mkref_round_bf16(V.data(), V.size());
+            // q, k, v (and the text's cached keys / values) are half (heads_norm_half / heads_half)
+            mkref_round_f16(Q.data(), Q.size());
+            mkref_round_f16(K.data(), K.size());
+            mkref_round_f16(V.data(), V.size());
             attention(Q.data(), K.data(), V.data(), 1, H, T, T, hd, 1.0f / std::sqrt(float(hd)), 0, uint32_t(S),
                       att.data());
             m.linear(b + "attn.to_out.0", att.data(), D, T, o.data(), D, false);
@@ -990,9 +1013,10 @@ int mkref_sdxl_trans(const mkref_model* mp, const float* x, int64_t n, const flo
             heads_norm_rope(q.data(), n, c, 0, H, 64, nullptr, 0, nullptr, 0, Q.data(), n, 0);
             heads_norm_rope(k.data(), n, c, 0, H, 64, nullptr, 0, nullptr, 0, K.data(), n, 0);
             heads_norm_rope(v.data(), n, c, 0, H, 64, nullptr, 0, nullptr, 0, V.data(), n, 0);
-            mkref_round_bf16(Q.data(), Q.size());
-            mkref_round_bf16(K.data(), K.size());
-            mkref_round_bf16(V.data(), V.size());
+            // half heads (heads64 -> heads_half, sdxl.cpp:439-448)
+            mkref_round_f16(Q.data(), Q.size());
+            mkref_round_f16(K.data(), K.size());
+            mkref_round_f16(V.data(), V.size());
             attention(Q.data(), K.data(), V.data(), 1, H, n, n, 64, scale, 0, 0, att.data());
             m.linear(b + "attn1.to_out.0", att.data(), c, n, o.data(), c);
             add(hs, o);
@@ -1003,9 +1027,9 @@ int mkref_sdxl_trans(const mkref_model* mp, const float* x, int64_t n, const flo
             m.linear(b + "attn2.to_v", ctx, E, S, cv.data(), c, false);
             heads_norm_rope(ck.data(), S, c, 0, H, 64, nullptr, 0, nullptr, 0, CK.data(), S, 0);
             heads_norm_rope(cv.data(), S, c, 0, H, 64, nullptr, 0, nullptr, 0, CV.data(), S, 0);
-            mkref_round_bf16(Q.data(), Q.size());
-            mkref_round_bf16(CK.data(), CK.size());
-            mkref_round_bf16(CV.data(), CV.size());
+            mkref_round_f16(Q.data(), Q.size());
+            mkref_round_f16(CK.data(), CK.size());
+            mkref_round_f16(CV.data(), CV.size());
             attention(Q.data(), CK.data(), CV.data(), 1, H, n, S, 64, scale, 0, 0, att.data());
             m.linear(b + "attn2.to_out.0", att.data(), c, n, o.data(), c);
             add(hs, o);

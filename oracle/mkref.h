@@ -7,15 +7,17 @@
  * Arithmetic model (mirrors the reference: bf16 storage, fp32 accumulation, fp32 residual stream):
  *  - matrix weights hold bf16 values (or OCP fp8-e4m3 values with a per-output-channel fp32 scale);
  *  - every GEMM rounds its activation operand to bf16 (round-to-nearest-even), accumulates in fp32;
- *  - attention operands Q, K, V are rounded to bf16; the softmax is fp32;
+ *  - attention operands Q, K, V are rounded to bf16 in the dual-stream graph, and to IEEE half in the reference's own
+ *    graphs (Qwen-Image 2.1 and SDXL, whose heads kernels write `half`: qwen_image.cpp:165-167, 226-250,
+ *    sdxl.cpp:439-448), the 2.1 graph's cached text keys / values with them; the softmax is fp32;
  *  - norms reduce in double (more exact than any kernel), elementwise math is fp32.
  *
  * Parity unpinned: the reference's GEMM / attention / heads kernels live in an un-vendored submodule
  * (external/mako-common, no source or pinned commit in the tree) and the reference holds no vectors for this path,
  * so these choices are inferred, not pinned to the reference: the GEMM's bf16 rounding of its activation operand;
  * RoPE mode 2 as interleaved pairs (2i, 2i+1); the causal-prefix rule of attention(block = S); the textbook
- * gelu_tanh and swiglu forms; the precision of P in P V (fp32 here; a kernel may round it to bf16 within the
- * tolerance). Everything else is pinned by tests/test_oracle.py and
+ * gelu_tanh and swiglu forms; the precision of P in P V (fp32 here; a kernel may round it to the operands' type
+ * within the tolerance). Everything else is pinned by tests/test_oracle.py and
  * tests/test_oracle_graph.py (library routines in float64, closed forms, invariants).
  *
  * Reference files restated (see each function in mkref.cpp for its file:line):
@@ -37,6 +39,7 @@ extern "C" {
 uint16_t mkref_f32_to_bf16(float x);
 float mkref_bf16_to_f32(uint16_t b);
 void mkref_round_bf16(float* x, size_t n);
+void mkref_round_f16(float* x, size_t n); /* IEEE half, nearest even */
 uint8_t mkref_f32_to_e4m3(float x);
 float mkref_e4m3_to_f32(uint8_t b);
 

@@ -40,6 +40,7 @@ def lib():
         L.mkref_bf16_to_f32.restype = C.c_float
         L.mkref_bf16_to_f32.argtypes = [C.c_uint16]
         L.mkref_round_bf16.argtypes = [_F, C.c_size_t]
+        L.mkref_round_f16.argtypes = [_F, C.c_size_t]
         L.mkref_f32_to_e4m3.restype = C.c_uint8
         L.mkref_f32_to_e4m3.argtypes = [C.c_float]
         L.mkref_e4m3_to_f32.restype = C.c_float
@@ -128,6 +129,13 @@ def bf16_bits(a):
 
 def bf16_round(a):
     return (bf16_bits(a).astype(np.uint32) << 16).view(np.float32)
+
+
+def f16_round(a):
+    """IEEE half rounding (nearest even) of float32 values, the oracle's rule."""
+    x = np.array(a, dtype=np.float32, copy=True, order="C")
+    lib().mkref_round_f16(fp(x), x.size)
+    return x
 
 
 def bf16_to_f32(bits):

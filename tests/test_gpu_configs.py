@@ -45,7 +45,8 @@ def test_fp8_2048_attention_sampled_rows(gpu):
     Q, K, V = (M.Dev.from_array(M.bf16_bits(a)) for a in (q, k, vt))
     del vt
     O = M.Dev(B * T5 * D * 2)
-    M.call("mk_attention", Q.p, K.p, V.p, O.p, B, H, H, 128, T5, q_pad, T5, k_pad, D, T5 * D, 0, 0, 0.0, None)
+    M.call("mk_attention", Q.p, K.p, V.p, O.p, M.BF16, B, H, H, 128, T5, q_pad, T5, k_pad, D, T5 * D, 0, 0, 0.0, None,
+           None)
     M.sync()
     got = M.bf16_to_f32(O.to_array(np.uint16, (B, T5, D)))
     rows = np.sort(rng.choice(T5, 48, replace=False))

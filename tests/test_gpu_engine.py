@@ -74,6 +74,32 @@ def test_dual_cfg_batch_matches_two_oracle_passes(gpu):
     within(got - x, (sig_next - sig) * (neg + g * (pos - neg)), 64, cos=0.99999, max_rel=1e-3)
 
 
+@pytest.mark.parametrize("S0,S1", [(64, 41), (23, 64)])
+def test_dual_cfg_batch_ragged_prompts_matches_two_oracle_passes(gpu, S0, S1):
+    # prompts of different lengths (the reference runs each slot with its own S, engine.cpp:475-477) still run as one
+    # batch of 2: the shorter prompt padded, its padding rows masked as keys, each sample's RoPE at its own frame
+    m, e = make_pair(M.FAMILY_DUAL)
+    rng = np.random.default_rng(9)
+    p = [rng.standard_normal((S0, 512)).astype(np.float32), rng.standard_normal((S1, 512)).astype(np.float32)]
+    x = rng.standard_normal((H_ * W_, 64)).astype(np.float32)
+    for s in (0, 1):
+        e.begin(p[s], H_, W_, s)
+    sig, sig_next, g = 0.7, 0.55, 3.5
+    got = e.step_cfg(x, sig, sig_next, g)
+    v = [m.dual_step(p[s][None], x[None], H_, W_, sig)[0] for s in (0, 1)]
+    want = x + (sig_next - sig) * (v[1] + g * (v[0] - v[1]))
+    within(got - x, want - x, 64)
+    # each sample's velocity in the padded batch (guidance 1: the positive's, 0: the negative's) against its own
+    # single-slot step: the padded sample's keys sit at other tile positions, so its attention sums run in another
+    # order and a few bf16 roundings of the attention output flip (2^-9 each): within 5e-3, cosine 0.99999
+    dt = sig_next - sig
+    for gg, slot in ((1.0, 0), (0.0, 1)):
+        v_b = (e.step_cfg(x, sig, sig_next, gg) - x) / dt
+        within(v_b, e.step(x, sig, slot), 64, cos=0.99999, max_rel=5e-3)
+    # the padded batch repeats bit for bit
+    assert np.array_equal(e.step_cfg(x, sig, sig_next, g), got)
+
+
 def test_init_random_equals_uploaded_oracle_weights(gpu):
     # the device RNG reproduces the CPU reference's weights bit for bit: the same step, the same bits
     m, e = make_pair(M.FAMILY_DUAL, seed=3)
@@ -161,10 +187,10 @@ def test_attention_full_size_sampled_rows(gpu):
         M.Dev.from_array(nk)
     for col0, w_, out, pad, tr in ((0, nqd, Q, q_pad, 0), (D, nkd, K, k_pad, 0), (2 * D, None, V, k_pad, 1)):
         M.call("mk_heads", X.p, B, T, 3 * D, T * 3 * D, col0, H, 128, w_.p if w_ else None, 1e-6,
-               None if tr else csd.p, 0 if tr else 2, out.p, pad, 0, tr, None)
+               None if tr else csd.p, 0 if tr else 2, out.p, pad, 0, tr, M.BF16, None)
     O = M.Dev(B * T * D * 2)
-    M.call("mk_attention", Q.p, K.p, V.p, O.p, B, H, H, 128, T, q_pad, T, k_pad, D, T * D, 0, 0,
-           float(1 / np.sqrt(128)), None)
+    M.call("mk_attention", Q.p, K.p, V.p, O.p, M.BF16, B, H, H, 128, T, q_pad, T, k_pad, D, T * D, 0, 0,
+           float(1 / np.sqrt(128)), None, None)
     M.sync()
     got = M.bf16_to_f32(O.to_array(np.uint16, (B, T, D)))
     rows = np.sort(rng.choice(T, 48, replace=False))

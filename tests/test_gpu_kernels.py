@@ -159,9 +159,10 @@ def test_gemm_fp8_every_code(gpu):
     assert np.array_equal(fetch(out, (K, N)), want)
 
 
-@pytest.mark.parametrize("mode,row0,q_row0,k_scale", [(2, 40, 40, 0.0), (1, 0, 0, 0.0), (0, 17, 0, 0.0),
-                                                      (2, 40, 40, 0.3)])
-def test_gemm_heads_epilogue(gpu, rng, mode, row0, q_row0, k_scale):
+@pytest.mark.parametrize("mode,row0,q_row0,k_scale,odt", [(2, 40, 40, 0.0, M.BF16), (1, 0, 0, 0.0, M.BF16),
+                                                          (0, 17, 0, 0.0, M.BF16), (2, 40, 40, 0.3, M.BF16),
+                                                          (2, 40, 0, 0.3, M.F16), (0, 0, 0, 0.0, M.F16)])
+def test_gemm_heads_epilogue(gpu, rng, mode, row0, q_row0, k_scale, odt):
     # q | k | v columns -> per-head RMSNorm + RoPE -> Q, K [b][h][pad][128] and V^T [b][h][128][pad]
     B, Mr, H = 2, 150, 2
     D = H * 128
@@ -174,15 +175,17 @@ def test_gemm_heads_epilogue(gpu, rng, mode, row0, q_row0, k_scale):
     nk = (1 + 0.1 * rng.standard_normal(128)).astype(np.float32)
     cs = R.rope_table(row0, 14, 14)[: row0 + Mr] if row0 else R.rope_table(0, 15, 10)[:Mr]
     Q, Kd, Vt = M.Dev(B * H * q_pad * 256), M.Dev(B * H * k_pad * 256), M.Dev(B * H * k_pad * 256)
-    ha = M.HeadsArgs(Q.p, Kd.p, Vt.p, H, 128, q_pad, k_pad, row0, q_row0, None, None, None, mode, 1e-6, k_scale)
+    ha = M.HeadsArgs(Q.p, Kd.p, Vt.p, H, 128, q_pad, k_pad, row0, q_row0, None, None, None, mode, 1e-6, k_scale,
+                     odt)
     nqd, nkd, csd = dev(nq), dev(nk), dev(cs)
     ha.norm_q, ha.norm_k, ha.rope = nqd.p, nkd.p, csd.p
     Ad = bdev(A)
     gemm(Ad, bdev(W), bias=dev(b), epi=M.EPI_HEADS, c_dtype=M.BF16, M_=(Mr, 3 * D, K_), batch=B, lda=K_,
          sa=Mr * K_, heads=ha)
-    gq = fetch_bf16(Q, (B, H, q_pad, 128))
-    gk = fetch_bf16(Kd, (B, H, k_pad, 128))
-    gv = fetch_bf16(Vt, (B, H, 128, k_pad))
+    get = (lambda d, sh: M.f16_to_f32(d.to_array(np.uint16, sh))) if odt == M.F16 else fetch_bf16
+    gq = get(Q, (B, H, q_pad, 128))
+    gk = get(Kd, (B, H, k_pad, 128))
+    gv = get(Vt, (B, H, 128, k_pad))
     for bi in range(B):
         y = R.gemm(A[bi], W, b)
         tab = cs[row0:]
@@ -466,9 +469,16 @@ def test_gemm_rejects_bad_shapes(gpu):
 # attention
 # ---------------------------------------------------------------------------------------------------------------
 
-def run_attention(q, k, v, scale, q_pos0=0, block=0):
-    """q [B][H][Tq][d], k, v [B][Hkv][Tk][d] (bf16-exact floats, Hkv dividing H) through mk_attention; returns
-    [B][Tq][H*d]."""
+def hdev(a):
+    """IEEE half device copy of a float array."""
+    d = M.Dev.from_array(M.f16_bits(a))
+    _live.append(d)
+    return d
+
+
+def run_attention(q, k, v, scale, q_pos0=0, block=0, dtype=M.BF16, hole=None):
+    """q [B][H][Tq][d], k, v [B][Hkv][Tk][d] (floats exact in `dtype`, bf16 or f16; Hkv dividing H) through
+    mk_attention; returns [B][Tq][H*d]."""
     B, H, Tq, d = q.shape
     Hkv, Tk = k.shape[1], k.shape[2]
     q_pad = (Tq + 255) // 256 * 256
@@ -480,8 +490,10 @@ def run_attention(q, k, v, scale, q_pos0=0, block=0):
     vt = np.zeros((B, Hkv, d, k_pad), np.float32)
     vt[:, :, :, M.vt_col(np.arange(Tk))] = v.transpose(0, 1, 3, 2)
     out = dev(np.zeros(B * Tq * H * d, np.uint16))
-    M.call("mk_attention", bdev(qp).p, bdev(kp).p, bdev(vt).p, out.p, B, H, Hkv, d, Tq, q_pad, Tk, k_pad, H * d,
-           Tq * H * d, q_pos0, block, scale, None)
+    up = hdev if dtype == M.F16 else bdev
+    kh = None if hole is None else np.ascontiguousarray(np.array(hole, dtype=np.uint32).reshape(-1))
+    M.call("mk_attention", up(qp).p, up(kp).p, up(vt).p, out.p, dtype, B, H, Hkv, d, Tq, q_pad, Tk, k_pad, H * d,
+           Tq * H * d, q_pos0, block, scale, None if kh is None else kh.ctypes.data, None)
     M.sync()
     return fetch_bf16(out, (B, Tq, H * d))
 
@@ -500,6 +512,26 @@ def test_attention_matches_oracle(gpu, rng, d, Tq, Tk, block, q_pos0):
     want = R.attention(q, k, v, 1 / np.sqrt(d), q_pos0, block)
     dd = R.diff(got, want, d)
     # P is rounded to bf16 for the MFMA, the output stored bf16
+    assert dd["min_cos"] > 0.9999 and dd["max_rel"] < 1e-2, dd
+
+
+# the reference's half heads (its 2.1 graph and SDXL): half Q, K, V and probabilities, the scale-0 path (K carrying
+# the softmax scale in log2 units) as the engine runs it, with the causal text prefix and offset queries
+@pytest.mark.parametrize("d,Tq,Tk,block,q_pos0,scale", [(128, 300, 300, 0, 0, 0.0), (128, 200, 460, 60, 260, 0.0),
+                                                        (128, 260, 260, 60, 0, 0.0), (64, 333, 77, 0, 0, 0.125),
+                                                        (64, 256, 1000, 0, 0, 0.125), (128, 300, 2000, 0, 0, 0.0)])
+def test_attention_half_matches_oracle(gpu, rng, d, Tq, Tk, block, q_pos0, scale):
+    B, H = 2, 3
+    q = R.f16_round(rng.standard_normal((B, H, Tq, d)).astype(np.float32))
+    k = rng.standard_normal((B, H, Tk, d)).astype(np.float32)
+    if scale == 0.0:
+        k = k / np.sqrt(d) * np.log2(np.e)
+    k = R.f16_round(k)
+    v = R.f16_round(rng.standard_normal((B, H, Tk, d)).astype(np.float32))
+    eff = float(np.log(2.0)) if scale == 0.0 else scale
+    got = run_attention(q, k, v, scale, q_pos0, block, dtype=M.F16)
+    want = R.attention(q, k, v, eff, q_pos0, block)
+    dd = R.diff(got, want, d)
     assert dd["min_cos"] > 0.9999 and dd["max_rel"] < 1e-2, dd
 
 
@@ -565,8 +597,10 @@ def test_gate_add_tanh_bf16(gpu, rng):
     assert maxrel(fetch(xd, (rows, n)), want) < 1e-6
 
 
-@pytest.mark.parametrize("d,mode,transpose", [(128, 2, 0), (128, 1, 0), (64, 0, 0), (128, 0, 1), (64, 0, 1)])
-def test_heads(gpu, rng, d, mode, transpose):
+@pytest.mark.parametrize("d,mode,transpose,odt", [(128, 2, 0, M.BF16), (128, 1, 0, M.BF16), (64, 0, 0, M.BF16),
+                                                  (128, 0, 1, M.BF16), (64, 0, 1, M.BF16), (128, 2, 0, M.F16),
+                                                  (64, 0, 0, M.F16), (128, 0, 1, M.F16), (64, 0, 1, M.F16)])
+def test_heads(gpu, rng, d, mode, transpose, odt):
     B, rows, H = 2, 90, 3
     ld = 3 * H * d
     x = R.bf16_round(rng.standard_normal((B, rows, ld)).astype(np.float32))
@@ -577,9 +611,10 @@ def test_heads(gpu, rng, d, mode, transpose):
     wd = dev(w) if w is not None else None
     csd = dev(cs)
     M.call("mk_heads", bdev(x).p, B, rows, ld, rows * ld, H * d, H, d, wd.p if wd else None, 1e-6,
-           csd.p if mode else None, mode, out.p, n_pad, row0, transpose, None)
+           csd.p if mode else None, mode, out.p, n_pad, row0, transpose, odt, None)
     M.sync()
-    got = fetch_bf16(out, (B, H, d, n_pad) if transpose else (B, H, n_pad, d))
+    shape = (B, H, d, n_pad) if transpose else (B, H, n_pad, d)
+    got = M.f16_to_f32(out.to_array(np.uint16, shape)) if odt == M.F16 else fetch_bf16(out, shape)
     for bi in range(B):
         want = R.heads_norm_rope(x[bi], H, d, col0=H * d, w=w, cs=cs[row0:] if mode else None, rope=mode)
         if transpose:
@@ -589,18 +624,21 @@ def test_heads(gpu, rng, d, mode, transpose):
         assert np.abs(g - want).max() <= 2 ** -8 * np.abs(want).max() + 1e-6
 
 
-@pytest.mark.parametrize("d", [64, 128])
-def test_heads_plain_layout_is_an_exact_copy(gpu, rng, d):
-    # no norm, no rope: the 16-byte copy path; every value lands bit for bit at [batch][head][row0 + r]
+@pytest.mark.parametrize("d,odt", [(64, M.BF16), (128, M.BF16), (64, M.F16), (128, M.F16)])
+def test_heads_plain_layout_is_an_exact_copy(gpu, rng, d, odt):
+    # no norm, no rope: the 16-byte copy path; every value lands bit for bit at [batch][head][row0 + r] (as half: the
+    # bf16 value rounded to nearest even, as numpy rounds it)
     B, rows, H, row0, n_pad = 2, 77, 5, 3, 96
     ld = 3 * H * d
-    x = M.bf16_bits(rng.standard_normal((B, rows, ld)).astype(np.float32))
+    x = M.bf16_bits(rng.standard_normal((B, rows, ld)).astype(np.float32) * 3.0)
     out = M.Dev(B * H * n_pad * d * 2)
     M.call("mk_heads", M.Dev.from_array(x).p, B, rows, ld, rows * ld, H * d, H, d, None, 1e-6, None, 0, out.p, n_pad,
-           row0, 0, None)
+           row0, 0, odt, None)
     M.sync()
     got = out.to_array(np.uint16, (B, H, n_pad, d))[:, :, row0:row0 + rows]
     want = x[:, :, H * d:2 * H * d].reshape(B, rows, H, d).transpose(0, 2, 1, 3)
+    if odt == M.F16:
+        want = M.f16_bits(M.bf16_to_f32(want))
     assert np.array_equal(got, want)
 
 
@@ -775,7 +813,8 @@ def test_attention_grouped_kv_heads(gpu, rng, d, H, Hkv, scale):
 
 def test_attention_rejects_kv_heads_not_dividing(gpu):
     z = dev(np.zeros(4096, np.uint16))
-    st = M.lib().mk_attention(z.p, z.p, z.p, z.p, 1, 6, 4, 64, 16, 256, 16, 64, 384, 0, 0, 0, 0.125, None)
+    st = M.lib().mk_attention(z.p, z.p, z.p, z.p, M.BF16, 1, 6, 4, 64, 16, 256, 16, 64, 384, 0, 0, 0, 0.125, None,
+                              None)
     assert st == 1 and b"kv_heads" in M.lib().mk_last_error()
 
 
@@ -789,3 +828,75 @@ def test_binding_keeps_dropped_buffers_until_sync(gpu, rng):
     M.sync()
     assert not M._pending
     assert np.array_equal(out.to_array(np.uint16, x.shape), M.bf16_bits(x))
+
+
+# Gated linear units in the projection's epilogue: W = [first F rows; second F rows] (the fused gate|up matrix),
+# C [M][F] = silu(first) second (SwiGLU) or first gelu_erf(second) (GEGLU), from the fp32 accumulators. Shapes that
+# take 256-wide tiles (8 waves) and 128-wide ones (4 waves); bf16 and fp8 weights; with and without bias.
+@pytest.mark.parametrize("epi,Mr,F,K,w8,bias", [(M.EPI_SWIGLU, 4352, 3072, 512, False, False),
+                                                (M.EPI_GEGLU, 2048, 2560, 320, False, True),
+                                                (M.EPI_SWIGLU, 300, 640, 256, False, True),
+                                                (M.EPI_GEGLU, 77, 192, 128, False, True),
+                                                (M.EPI_SWIGLU, 1100, 1536, 384, True, False)])
+def test_gemm_glu_epilogue(gpu, rng, epi, Mr, F, K, w8, bias):
+    N = 2 * F
+    A = rng.standard_normal((Mr, K)).astype(np.float32)
+    Wf = rng.standard_normal((N, K)).astype(np.float32) * 0.08
+    if w8:
+        scale = (np.abs(Wf).max(1) / 448).astype(np.float32)
+        table = R.e4m3_table()
+        mags, a = table[:127], np.abs(Wf / scale[:, None])
+        i = np.clip(np.searchsorted(mags, a), 1, 126)
+        codes = np.where(a - mags[i - 1] <= mags[i] - a, i - 1, i).astype(np.uint8) | \
+            np.where(Wf < 0, 0x80, 0).astype(np.uint8)
+        Wv, Wd, sd = table[codes], dev(codes), dev(scale)
+    else:
+        Wv, Wd, sd, scale = R.bf16_round(Wf), None, None, None
+        Wd = bdev(Wv)
+    b = rng.standard_normal(N).astype(np.float32) * 0.3 if bias else None
+    out = dev(np.zeros(Mr * F, np.uint16))
+    gemm(bdev(A), Wd, bias=dev(b) if bias else None, wscale=sd, c=out, c_dtype=M.BF16, epi=epi, M_=(Mr, N, K),
+         lda=K, ldc=F, w_dtype=M.FP8 if w8 else M.BF16)
+    y = R.gemm(A, Wv, b, wscale=scale)
+    want = R.swiglu(y) if epi == M.EPI_SWIGLU else R.geglu(y)
+    got = fetch_bf16(out, (Mr, F))
+    assert np.abs(got - want).max() <= 2 ** -8 * np.abs(want).max() + 1e-6
+
+
+def test_gemm_glu_equals_separate_glu_kernel(gpu, rng):
+    # the fused epilogue against the two-step form (fp32 GEMM output, then mk_swiglu on it): within one bf16 rounding
+    Mr, F, K = 512, 1024, 256
+    A, W = bdev(rng.standard_normal((Mr, K)).astype(np.float32)), bdev(rng.standard_normal((2 * F, K)) * 0.05)
+    fused = dev(np.zeros(Mr * F, np.uint16))
+    gemm(A, W, c=fused, c_dtype=M.BF16, epi=M.EPI_SWIGLU, M_=(Mr, 2 * F, K), lda=K, ldc=F)
+    gu, m = M.Dev(Mr * 2 * F * 4), dev(np.zeros(Mr * F, np.uint16))
+    _live.append(gu)
+    gemm(A, W, c=gu, c_dtype=M.F32, M_=(Mr, 2 * F, K), lda=K, ldc=2 * F)
+    M.call("mk_swiglu", gu.p, M.F32, Mr, F, m.p, None)
+    M.sync()
+    a, b = fetch_bf16(fused, (Mr, F)), fetch_bf16(m, (Mr, F))
+    assert np.abs(a - b).max() <= 2 ** -8 * np.abs(b).max()
+    assert np.mean(a == b) > 0.95
+
+
+@pytest.mark.parametrize("d,Tq,Tk,holes,scale", [(128, 300, 300, ((41, 64), (64, 64)), 0.0),
+                                                 (128, 300, 700, ((5, 200), (100, 101)), 0.0),
+                                                 (64, 120, 333, ((1, 64), (30, 97)), 0.125)])
+def test_attention_masked_key_range(gpu, rng, d, Tq, Tk, holes, scale):
+    # a guidance batch whose shorter prompt is padded: keys [lo, hi) of each batch item are masked; equal to attention
+    # over the remaining keys (ranges inside a tile, across tiles, empty, a single key)
+    B, H = 2, 3
+    q = R.bf16_round(rng.standard_normal((B, H, Tq, d)).astype(np.float32))
+    k = rng.standard_normal((B, H, Tk, d)).astype(np.float32)
+    if scale == 0.0:
+        k = k / np.sqrt(d) * np.log2(np.e)
+    k = R.bf16_round(k)
+    v = R.bf16_round(rng.standard_normal((B, H, Tk, d)).astype(np.float32))
+    got = run_attention(q, k, v, scale, hole=holes)
+    eff = float(np.log(2.0)) if scale == 0.0 else scale
+    for b, (lo, hi) in enumerate(holes):
+        keep = np.r_[0:lo, hi:Tk]
+        want = R.attention(q[b:b + 1], np.ascontiguousarray(k[b:b + 1, :, keep]),
+                           np.ascontiguousarray(v[b:b + 1, :, keep]), eff)
+        dd = R.diff(got[b], want[0], d)
+        assert dd["min_cos"] > 0.9999 and dd["max_rel"] < 1e-2, dd

@@ -209,3 +209,17 @@ def test_patchify_round_trip_and_layout():
     assert np.array_equal(R.unpatchify(tok, 16, 4, 3), lat)
     # token (y/2, x/2), feature c*4 + (y%2)*2 + x%2 (the reference's unpack layout)
     assert tok[1 * 3 + 2, 5 * 4 + 1 * 2 + 0] == lat[5, 3, 4]
+
+
+def test_f16_rounding_matches_numpy_half():
+    # the oracle's IEEE half rounding against numpy's float32 -> float16 conversion (nearest even): random values over
+    # every binade a half holds, the subnormal range, the overflow edge, and every midpoint between adjacent halves
+    rng = np.random.default_rng(0)
+    x = (rng.standard_normal(200000) * np.exp2(rng.uniform(-30, 17, 200000))).astype(np.float32)
+    h = np.arange(0, 0x7BFF, dtype=np.uint16).view(np.float16).astype(np.float32)
+    mids = ((h[:-1].astype(np.float64) + h[1:]) / 2).astype(np.float32)  # exact in float32
+    special = np.array([0.0, -0.0, 65504.0, 65519.9, 65520.0, 7e4, 2.0 ** -24, 2.0 ** -25, 2.0 ** -25 * 1.0001,
+                        6.0e-8, np.inf, -np.inf], dtype=np.float32)
+    for a in (x, mids, -mids, special):
+        want = a.astype(np.float16).astype(np.float32)
+        assert np.array_equal(R.f16_round(a).view(np.uint32), want.view(np.uint32))
