@@ -10,6 +10,7 @@
 //   - the guided Euler step of the sampler loop (engine.cpp:471-503) with both guidance passes as one batch of 2.
 #include "common.hpp"
 
+#include <algorithm>
 #include <cmath>
 #include <map>
 #include <string>
@@ -78,6 +79,7 @@ struct Timing {
         int cls;
         double flops;
     };
+    hipEvent_t ref = nullptr; // recorded on the engine's stream before the step's first timed launch
     std::vector<Ev> evs;
     std::vector<std::string> names;
     std::vector<float> ms;
@@ -328,23 +330,30 @@ struct mk_engine {
     }
 
     // ---------------------------------------------------------------------------------------------------------
-    // launches with optional timing
+    // launches with optional timing: events around the launch on its stream (the engine's, or `on`)
     template <typename F>
-    mk_status timed(const char* cls, double flops, F&& f)
+    mk_status timed(const char* cls, double flops, F&& f, hipStream_t on = nullptr)
     {
         if (!timing.on)
             return f();
+        if (timing.evs.empty()) {
+            if (!timing.ref)
+                MK_HIP(hipEventCreate(&timing.ref));
+            MK_HIP(hipEventRecord(timing.ref, stream));
+        }
         Timing::Ev ev{};
         MK_HIP(hipEventCreate(&ev.a));
         MK_HIP(hipEventCreate(&ev.b));
         ev.cls = timing.cls(cls);
         ev.flops = flops;
-        MK_HIP(hipEventRecord(ev.a, stream));
+        MK_HIP(hipEventRecord(ev.a, on ? on : stream));
         mk_status s = f();
-        MK_HIP(hipEventRecord(ev.b, stream));
+        MK_HIP(hipEventRecord(ev.b, on ? on : stream));
         timing.evs.push_back(ev);
         return s;
     }
+    // Per class: the summed launch durations; and the step's attention and GEMM time as the union of their launches'
+    // intervals (class "union:attention+gemm"): the summed durations less any overlap of launches on other streams.
     mk_status finish_timing()
     {
         if (!timing.on)
@@ -355,16 +364,41 @@ struct mk_engine {
             timing.launches[i] = 0;
             timing.flops[i] = 0;
         }
+        std::vector<std::pair<float, float>> iv;
+        double uflops = 0;
         for (auto& e : timing.evs) {
-            float ms = 0;
+            float ms = 0, t0 = 0, t1 = 0;
             MK_HIP(hipEventElapsedTime(&ms, e.a, e.b));
             timing.ms[e.cls] += ms;
             timing.launches[e.cls] += 1;
             timing.flops[e.cls] += e.flops;
+            const std::string& n = timing.names[e.cls];
+            if (n == "attention" || n.compare(0, 4, "gemm") == 0) {
+                MK_HIP(hipEventElapsedTime(&t0, timing.ref, e.a));
+                MK_HIP(hipEventElapsedTime(&t1, timing.ref, e.b));
+                iv.emplace_back(t0, t1);
+                uflops += e.flops;
+            }
             (void)hipEventDestroy(e.a);
             (void)hipEventDestroy(e.b);
         }
         timing.evs.clear();
+        std::sort(iv.begin(), iv.end());
+        double uni = 0, lo = 0, hi = -1;
+        for (const auto& [a, b] : iv) {
+            if (a > hi) {
+                uni += hi > lo ? hi - lo : 0;
+                lo = a;
+                hi = b;
+            } else if (b > hi) {
+                hi = b;
+            }
+        }
+        uni += hi > lo ? hi - lo : 0;
+        const int u = timing.cls("union:attention+gemm");
+        timing.ms[u] = float(uni);
+        timing.launches[u] = uint32_t(iv.size());
+        timing.flops[u] = uflops;
         return MK_OK;
     }
 
@@ -976,6 +1010,8 @@ mk_status mk_engine_destroy(mk_engine* e)
         (void)hipEventDestroy(ev);
     if (e->temb_ready)
         (void)hipEventDestroy(e->temb_ready);
+    if (e->timing.ref)
+        (void)hipEventDestroy(e->timing.ref);
     if (e->side)
         (void)hipStreamDestroy(e->side);
     (void)hipStreamDestroy(e->stream);
