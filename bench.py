@@ -462,6 +462,24 @@ def cpu_baseline(seconds_target=12.0, fp8=False):
                       f"{rate / 1e9:.1f} GFLOP/s), scaled by FLOPs to the 60-block batch-2 step at {H * W} + {S} tokens"}
 
 
+def copy_calibration(args):
+    """The traffic counters' calibration: a conversion kernel of known HBM traffic (fp32 -> bf16 over 64 Mi elements:
+    reads 256 MiB, writes 128 MiB a launch), three launches. FETCH_SIZE / WRITE_SIZE per dispatch of this kernel give
+    the counters' scale."""
+    import mkimage as M
+
+    M.call("mk_set_device", 0)
+    n = 64 << 20
+    x, y = M.Dev(n * 4), M.Dev(n * 2)
+    M.call("mk_fill_normal", x.p, n, M.F32, 1, 0.0, 1.0, None)
+    M.sync()
+    for _ in range(3):
+        M.call("mk_f32_to_bf16", x.p, n, y.p, None)
+    M.sync()
+    print(json.dumps({"calibration": "mk_f32_to_bf16", "elements": n, "read_bytes": 4 * n, "written_bytes": 2 * n}),
+          flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -469,7 +487,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    extra = {"sdxl-1024-bf16": bench_sdxl, "vae-1024-decode": bench_vae, "q21-1024": bench_q21}
+    extra = {"sdxl-1024-bf16": bench_sdxl, "vae-1024-decode": bench_vae, "q21-1024": bench_q21,
+             "copy-calibration": copy_calibration}
     ap.add_argument("--workload", choices=sorted(WORKLOADS) + sorted(extra), default="mmdit-1024-bf16")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -502,7 +521,7 @@ def main():
     for s in (0, 1):
         eng.begin(rng.standard_normal((S, 3584)).astype(np.float32), H, W, s)
     lat = [M.Dev.from_array(rng.standard_normal((H * W, 64)).astype(np.float32)), M.Dev(H * W * 64 * 4)]
-    sigmas = [1.0 - 0.02 * i for i in range(args.warmup + args.steps + 2)]
+    sigmas = [1.0 - 0.02 * i for i in range(args.warmup + max(args.steps, 4) + 2)]  # (the ragged run takes 4)
     stream = eng.stream()
 
     def run(i):
