@@ -54,13 +54,16 @@ __device__ inline u32x4 buf_load16(BufRes, uint32_t, uint32_t) { return u32x4{};
 
 // ---- GEMM dispatch plan (gemm.hip), shared with the engine's launch-grouping cost model ----
 struct GemmPlan {
-    int bn;          // tile width in channels (256, 128 or 64); tiles are 256 tokens
+    int bm;          // tile height in tokens (256, or 128 for launches of few tiles)
+    int bn;          // tile width in channels (256, 128 or 64)
     uint64_t tiles;  // tiles of the launch
     bool sk;         // stream-K: whole waves round robin, the last partial wave split by k steps
     uint64_t dp;     // tiles done whole (stream-K)
+    double cost;     // estimated duration in units of one k step of a 256 x 256 tile
 };
-// The plan of a launch of n grouped problems (equal N, K, weight type, epilogue kind) on `cus` compute units.
-GemmPlan gemm_plan(const mk_gemm_args* a, uint32_t n, uint32_t cus);
+// The plan of a launch of n grouped problems (equal N, K, weight type, epilogue kind) on `cus` compute units;
+// `conv`: a 3 x 3 convolution (256-token tiles only).
+GemmPlan gemm_plan(const mk_gemm_args* a, uint32_t n, uint32_t cus, bool conv = false);
 // Its estimated duration in units of one 256-channel k step.
 double gemm_cost(const mk_gemm_args* a, uint32_t n, uint32_t cus);
 // MK_ERR_DEVICE when a stream-K launch on any device gave up waiting for a partial tile since the last check (the

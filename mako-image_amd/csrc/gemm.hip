@@ -951,8 +951,13 @@ constexpr int gemm_smem()
 }
 
 // One tile a workgroup.
+// Waves a SIMD: 8-wave tiles two (one workgroup a CU), 4-wave 128 x 128 tiles two (two workgroups a CU, 64 KB of LDS
+// each), other 4-wave tiles one.
+template <int BM, int NW> constexpr int gemm_waves_per_eu() { return NW == 8 || BM == 128 ? 2 : 1; }
+
 template <int BM, int BN, bool kF8, int EK, int NW>
-__global__ __launch_bounds__(64 * NW, 1) __attribute__((amdgpu_waves_per_eu(NW / 4, NW / 4))) void gemm_kernel(GemmG G)
+__global__ __launch_bounds__(64 * NW, BM == 128 ? 2 : 1) __attribute__((
+    amdgpu_waves_per_eu(gemm_waves_per_eu<BM, NW>(), gemm_waves_per_eu<BM, NW>()))) void gemm_kernel(GemmG G)
 {
     __shared__ __attribute__((aligned(16))) uint16_t smem[gemm_smem<BM, BN, NW>() / 2];
     uint32_t z, tm, tn;
@@ -1106,7 +1111,7 @@ mk_status launch(GemmP* p, uint32_t count, const GemmPlan& plan, hipStream_t s)
     }
     G.tiles0 = count > 1 ? p[0].tiles_m * p[0].tiles_n * p[0].batch : tiles;
     const uint32_t kt = p[0].K / BK;
-    if constexpr (BN == 256) {
+    if constexpr (BN == 256 && BM == 256) {
         int dev = 0;
         MK_HIP(hipGetDevice(&dev));
         if (dev < 0 || dev >= kMaxDevices)
@@ -1231,36 +1236,63 @@ mk_status gemm_take_error()
     return MK_OK;
 }
 
-// Tile width: 256 x 256 tiles once there is a wave of them, else 256 x 128, else 256 x 64 (N = 64: stores, residuals);
-// heads epilogues always 256. Stream-K for 256-wide tiles when the last partial wave would leave a twentieth or more
-// of the launch idle and a tile is long (K of 6144 or more; measured, the partials' exchange costs about 24 k steps
-// of a tile, more than the balance saves on shorter tiles): the whole waves go round robin, the rest is split by k
-// steps (at least 4 a workgroup).
-GemmPlan gemm_plan(const mk_gemm_args* a, uint32_t n, uint32_t cus)
+// The tile shape of a launch, by its estimated duration: waves of tiles (rounded up) x k steps x the duration of one
+// k step of the tile relative to a 256 x 256 one, measured on MI355X (kt = 20-80, the SDXL and step shapes): 256 x 128
+// 0.66, 256 x 64 0.62, 128 x 128 0.67 for a pair of tiles (two workgroups share a CU: 64 KB of LDS each), so a wave of
+// 128 x 128 tiles is 2 per CU and an odd last tile costs half a pair; ties keep the larger tile. The heads epilogue
+// takes 256 x 256 tiles only; fp8 weights and convolutions 256-token tiles. 256 x 256 tiles use stream-K when whole waves leave at least 5% of the last wave's workgroups idle and
+// a tile is long (K of 6144 or more; measured, the partials' exchange costs about 24 k steps of a tile, more than the
+// balance saves on shorter tiles): the whole waves go round robin, the rest is split by k steps (at least 4 a
+// workgroup).
+GemmPlan gemm_plan(const mk_gemm_args* a, uint32_t n, uint32_t cus, bool conv)
 {
-    GemmPlan pl{};
-    uint64_t t256 = 0;
-    for (uint32_t i = 0; i < n; ++i)
-        t256 += uint64_t((a[i].M + 255) / 256) * a[i].batch * (a[0].N / 256);
-    pl.bn = a[0].epilogue == MK_EPI_HEADS || (a[0].N % 256 == 0 && t256 >= cus) ? 256 : a[0].N % 128 == 0 ? 128 : 64;
-    for (uint32_t i = 0; i < n; ++i)
-        pl.tiles += uint64_t((a[i].M + 255) / 256) * a[i].batch * (a[0].N / pl.bn);
-    const uint64_t waves = pl.tiles / cus, rounds = (pl.tiles + cus - 1) / cus, idle = rounds * cus - pl.tiles;
     const uint64_t kt = a[0].K / gemm_detail::BK;
-    pl.dp = waves * cus;
-    pl.sk = pl.bn == 256 && waves >= 1 && idle * 20 >= rounds * cus && kt >= 96 &&
-            (pl.tiles - pl.dp) * kt >= uint64_t(4) * cus;
-    return pl;
+    const uint32_t N = a[0].N;
+    const bool heads = a[0].epilogue == MK_EPI_HEADS;
+    const bool narrow_ok = a[0].epilogue != MK_EPI_GELU_TANH && a[0].epilogue != MK_EPI_SILU &&
+                           a[0].epilogue != MK_EPI_SWIGLU && a[0].epilogue != MK_EPI_GEGLU; // 64-wide tiles
+    const bool short_ok = !heads && !conv && a[0].w_dtype == MK_BF16;                     // 128-token tiles
+    auto tiles_of = [&](int bm, int bn) {
+        uint64_t t = 0;
+        for (uint32_t i = 0; i < n; ++i)
+            t += uint64_t((a[i].M + bm - 1) / bm) * a[i].batch * (N / bn);
+        return t;
+    };
+    GemmPlan best{};
+    best.cost = -1.0;
+    auto consider = [&](int bm, int bn, double c) {
+        if (N % bn)
+            return;
+        GemmPlan pl{};
+        pl.bm = bm;
+        pl.bn = bn;
+        pl.tiles = tiles_of(bm, bn);
+        const uint64_t rounds = (pl.tiles + cus - 1) / cus;
+        pl.cost = (bm == 128 ? 0.5 * double(rounds) : double(rounds)) * double(kt) * c;
+        if (bm == 256 && bn == 256) {
+            const uint64_t waves = pl.tiles / cus, idle = rounds * cus - pl.tiles;
+            pl.dp = waves * cus;
+            pl.sk = waves >= 1 && idle * 20 >= rounds * cus && kt >= 96 && (pl.tiles - pl.dp) * kt >= uint64_t(4) * cus;
+            if (pl.sk)
+                pl.cost = (double(pl.tiles) / cus + 24.0 / double(kt)) * double(kt);
+        }
+        if (best.cost < 0 || pl.cost < best.cost)
+            best = pl;
+    };
+    consider(256, 256, 1.0);
+    if (heads)
+        return best;
+    consider(256, 128, 0.66);
+    if (narrow_ok)
+        consider(256, 64, 0.62);
+    if (short_ok)
+        consider(128, 128, 0.67);
+    if (best.cost < 0) // N not a multiple of 128 with an activation or GLU: the dispatch rejects it
+        consider(256, 64, 0.62);
+    return best;
 }
 
-double gemm_cost(const mk_gemm_args* a, uint32_t n, uint32_t cus)
-{
-    const GemmPlan pl = gemm_plan(a, n, cus);
-    const double kt = double(a[0].K / gemm_detail::BK), w = pl.bn / 256.0;
-    if (pl.sk)
-        return (double(pl.tiles) / cus + 24.0 / kt) * kt * w;
-    return double((pl.tiles + cus - 1) / cus) * kt * w;
-}
+double gemm_cost(const mk_gemm_args* a, uint32_t n, uint32_t cus) { return gemm_plan(a, n, cus).cost; }
 } // namespace mk
 
 using namespace mk;
@@ -1307,7 +1339,17 @@ extern "C" mk_status mk_gemm_grouped(const mk_gemm_args* a, uint32_t count, void
 #define MK_GEMM_EK(BN, EK)                                                                                        \
     e = f8 ? launch<256, BN, true, EK, BN == 256 ? 8 : 4>(p, n, plan, s)                                           \
            : launch<256, BN, false, EK, BN == 256 ? 8 : 4>(p, n, plan, s)
-    if (ek == EK_HEADS) {
+    if (plan.bm == 128) {
+        // 128 x 128 tiles (bf16 weights; launches of few tiles): two workgroups a CU
+        if (ek == EK_STORE)
+            e = launch<128, 128, false, EK_STORE, 4>(p, n, plan, s);
+        else if (ek == EK_ACT)
+            e = launch<128, 128, false, EK_ACT, 4>(p, n, plan, s);
+        else if (ek == EK_GLU)
+            e = launch<128, 128, false, EK_GLU, 4>(p, n, plan, s);
+        else
+            e = launch<128, 128, false, EK_RMW, 4>(p, n, plan, s);
+    } else if (ek == EK_HEADS) {
         MK_GEMM_EK(256, EK_HEADS);
     } else if (bn == 256) {
         if (ek == EK_STORE)
@@ -1384,7 +1426,7 @@ extern "C" mk_status mk_conv3x3(const mk_conv_args* a, void* stream)
     int cus = 0, dev = 0;
     MK_HIP(hipGetDevice(&dev));
     MK_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
-    GemmPlan plan = gemm_plan(&g, 1, uint32_t(cus > 0 ? cus : 1));
+    GemmPlan plan = gemm_plan(&g, 1, uint32_t(cus > 0 ? cus : 1), true);
     plan.sk = false;
     hipStream_t s = static_cast<hipStream_t>(stream);
     const bool add = a->epilogue == MK_EPI_ADD;

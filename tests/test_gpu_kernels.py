@@ -900,3 +900,58 @@ def test_attention_masked_key_range(gpu, rng, d, Tq, Tk, holes, scale):
                            np.ascontiguousarray(v[b:b + 1, :, keep]), eff)
         dd = R.diff(got[b], want[0], d)
         assert dd["min_cos"] > 0.9999 and dd["max_rel"] < 1e-2, dd
+
+
+# Launches of few tiles take 128 x 128 tiles (two workgroups a CU): the SDXL stage-B shapes (2 x 1024 tokens, 1280
+# channels) and a row count that leaves a partial 128-row tile, each epilogue kind against the oracle. The same
+# products through 256-row tiles (a grouped launch with an empty second problem plans the same way, so instead the
+# rows are split: rows [0, 1024) and [1024, Mr) as two launches) must give the same bits: a tile's k order does not
+# depend on its height.
+@pytest.mark.parametrize("Mr,N,K,epi", [(2048, 1280, 1280, M.EPI_ADD), (2048, 1280, 5120, M.EPI_GATE_ADD),
+                                        (2000, 3840, 1280, M.EPI_STORE), (2048, 2 * 5120, 1280, M.EPI_GEGLU),
+                                        (1900, 1280, 640, M.EPI_GELU_TANH)])
+def test_gemm_short_tiles_match_oracle(gpu, rng, Mr, N, K, epi):
+    A = rng.standard_normal((Mr, K)).astype(np.float32)
+    W = R.bf16_round(rng.standard_normal((N, K)).astype(np.float32) * 0.03)
+    b = rng.standard_normal(N).astype(np.float32) * 0.3
+    glu = epi == M.EPI_GEGLU
+    F = N // 2 if glu else N
+    resid = epi in (M.EPI_ADD, M.EPI_GATE_ADD)
+    bf16_out = epi in (M.EPI_GEGLU, M.EPI_GELU_TANH)
+    X = rng.standard_normal((Mr, F)).astype(np.float32) if resid else None
+    gate = rng.standard_normal(N).astype(np.float32) if epi == M.EPI_GATE_ADD else None
+    out = dev(X) if resid else dev(np.zeros(Mr * F, np.uint16 if bf16_out else np.float32))
+    gemm(bdev(A), bdev(W), bias=dev(b), c=out, c_dtype=M.BF16 if bf16_out else M.F32, epi=epi, M_=(Mr, N, K),
+         lda=K, ldc=F, gate=dev(gate) if gate is not None else None)
+    got = fetch_bf16(out, (Mr, F)) if bf16_out else fetch(out, (Mr, F))
+    rows = np.sort(rng.choice(Mr, 96, replace=False))
+    rows[-1] = Mr - 1  # the partial tile's last row
+    y = R.gemm(np.ascontiguousarray(A[rows]), W, b)
+    if epi == M.EPI_ADD:
+        want = X[rows].astype(np.float64) + y
+    elif epi == M.EPI_GATE_ADD:
+        want = X[rows].astype(np.float64) + gate * y
+    elif glu:
+        want = R.geglu(y)
+    elif epi == M.EPI_GELU_TANH:
+        want = R.gelu_tanh(y)
+    else:
+        want = y
+    if bf16_out:
+        assert np.abs(got[rows] - want).max() <= 2 ** -8 * np.abs(want).max() + 1e-6
+    elif resid:
+        assert maxrel(got[rows] - X[rows], want - X[rows]) < 1e-5
+    else:
+        assert maxrel(got[rows], want) < 1e-5
+    # the same rows as two launches of a different plan (1024 rows: 256-row tiles where the whole launch took
+    # 128-row ones, or the reverse): bit-identical
+    out2 = dev(X) if resid else dev(np.zeros(Mr * F, np.uint16 if bf16_out else np.float32))
+    esz = 2 if bf16_out else 4
+    for r0, r1 in ((0, 1024), (1024, Mr)):
+        g = gemm_args(bdev(A[r0:r1]), bdev(W), bias=dev(b), c=out2, c_dtype=M.BF16 if bf16_out else M.F32, epi=epi,
+                      M_=(r1 - r0, N, K), lda=K, ldc=F, gate=dev(gate) if gate is not None else None)
+        g.c = out2.p + r0 * F * esz
+        M.call("mk_gemm", C.byref(g), None)
+    M.sync()
+    got2 = fetch_bf16(out2, (Mr, F)) if bf16_out else fetch(out2, (Mr, F))
+    assert np.array_equal(got, got2)
