@@ -563,8 +563,8 @@ struct mk_engine {
         MK_TRY(omod.ensure(size_t(2) * D * 4));
         if (k_pad_last != k_pad) {
             // a new key padding: the padded keys / values must be zero
-            MK_HIP(hipMemsetAsync(k.p, 0, k.bytes, stream));
-            MK_HIP(hipMemsetAsync(vt.p, 0, vt.bytes, stream));
+            MK_TRY(fill_zero(k.p, k.bytes, stream));
+            MK_TRY(fill_zero(vt.p, vt.bytes, stream));
             k_pad_last = k_pad;
         }
         // time embedding -> every block's modulation (silu(temb) feeds them all) and the output norm's
@@ -723,9 +723,9 @@ struct mk_engine {
         MK_TRY(temb.ensure(size_t(2) * D * 4));
         MK_TRY(mod.ensure(size_t(2) * 4 * D * 4));
         MK_TRY(omod.ensure(size_t(2) * D * 4));
-        if (k_pad_last != k_pad) {
-            MK_HIP(hipMemsetAsync(k.p, 0, k.bytes, stream));
-            MK_HIP(hipMemsetAsync(vt.p, 0, vt.bytes, stream));
+        if (k_pad_last != k_pad) { // padding keys zero (the heads epilogue writes rows < n only)
+            MK_TRY(fill_zero(k.p, k.bytes, stream));
+            MK_TRY(fill_zero(vt.p, vt.bytes, stream));
             k_pad_last = k_pad;
         }
         const uint32_t S16 = uint32_t(round_up(S, 16)); // V^T cache columns: whole groups of 16 keys
@@ -857,17 +857,28 @@ struct mk_engine {
         const uint32_t q_pad = uint32_t(round_up(n, 256)), k_pad = uint32_t(round_up(n, 64)), s_pad = sdxl_spad;
         MK_TRY(xn_img.ensure(size_t(nb) * n * c * 2));
         MK_TRY(x_img.ensure(size_t(nb) * n * c * 4));
-        MK_TRY(qkv.ensure(size_t(nb) * n * 3 * c * 2));
         MK_TRY(q.ensure(size_t(nb) * H * q_pad * 64 * 2));
         MK_TRY(k.ensure(size_t(nb) * H * k_pad * 64 * 2));
         MK_TRY(vt.ensure(size_t(nb) * H * 64 * k_pad * 2));
         MK_TRY(att.ensure(size_t(nb) * n * c * 2));
         MK_TRY(hid.ensure(size_t(nb) * n * F * 2));
-        if (k_pad_last != k_pad) {
-            MK_HIP(hipMemsetAsync(k.p, 0, k.bytes, stream));
-            MK_HIP(hipMemsetAsync(vt.p, 0, vt.bytes, stream));
+        if (k_pad_last != k_pad) { // padding keys zero (the heads epilogue writes rows < n only)
+            MK_TRY(fill_zero(k.p, k.bytes, stream));
+            MK_TRY(fill_zero(vt.p, vt.bytes, stream));
             k_pad_last = k_pad;
         }
+        // Q, K, V^T as half (the reference's heads_half, sdxl.cpp:439-448), written by the projections' epilogue
+        mk_heads_args ha{};
+        ha.q = q.p;
+        ha.k = k.p;
+        ha.vt = vt.p;
+        ha.heads = H;
+        ha.head_dim = 64;
+        ha.q_pad = q_pad;
+        ha.k_pad = k_pad;
+        ha.dtype = MK_F16;
+        mk_heads_args hq = ha; // the cross attention's Q alone
+        hq.k = hq.vt = nullptr;
         float* hs = x_img.f();
         const int64_t nc = int64_t(n) * c;
         MK_TRY(timed("norm", 0, [&] { return mk_group_norm(x, nb, n, c, 32, gn_g, gn_b, 1e-6f, xn_img.p, stream); }));
@@ -876,19 +887,8 @@ struct mk_engine {
         for (uint32_t i = 0; i < cfg.blocks; ++i) {
             const Block& B = blocks[i];
             MK_TRY(timed("norm", 0, [&] { return mk_layer_norm(hs, nb * n, c, B.n1g, B.n1b, 1e-5f, xn_img.p, stream); }));
-            MK_TRY(gemm(B.qkv[0], xn_img.p, c, 0, nb * n, 1, qkv.p, 3 * c, 0, MK_EPI_STORE, MK_BF16, nullptr, 0, 0, 0,
-                        nullptr, "gemm.qkv"));
-            MK_TRY(timed("heads", 0, [&] {
-                mk_status s = mk_heads(qkv.p, nb, n, 3 * c, int64_t(n) * 3 * c, 0, H, 64, nullptr, 0, nullptr, 0, q.p,
-                                       q_pad, 0, 0, MK_F16, stream);
-                if (s == MK_OK)
-                    s = mk_heads(qkv.p, nb, n, 3 * c, int64_t(n) * 3 * c, c, H, 64, nullptr, 0, nullptr, 0, k.p, k_pad,
-                                 0, 0, MK_F16, stream);
-                if (s == MK_OK)
-                    s = mk_heads(qkv.p, nb, n, 3 * c, int64_t(n) * 3 * c, 2 * c, H, 64, nullptr, 0, nullptr, 0, vt.p,
-                                 k_pad, 0, 1, MK_F16, stream);
-                return s;
-            }));
+            MK_TRY(gemm(B.qkv[0], xn_img.p, c, nc, n, nb, nullptr, 0, 0, MK_EPI_HEADS, MK_BF16, nullptr, 0, 0, 0, &ha,
+                        "gemm.qkv"));
             MK_TRY(timed("attention", 4.0 * double(n) * n * 64 * H * nb, [&] {
                 return mk_attention(q.p, k.p, vt.p, att.p, MK_F16, nb, H, H, 64, n, q_pad, n, k_pad, c, nc, 0, 0, scale, nullptr,
                                     stream);
@@ -896,12 +896,8 @@ struct mk_engine {
             MK_TRY(gemm(B.o[0], att.p, c, 0, nb * n, 1, hs, c, 0, MK_EPI_ADD, MK_F32, nullptr, 0, 0, 0, nullptr,
                         "gemm.o"));
             MK_TRY(timed("norm", 0, [&] { return mk_layer_norm(hs, nb * n, c, B.n2g, B.n2b, 1e-5f, xn_img.p, stream); }));
-            MK_TRY(gemm(B.q2, xn_img.p, c, 0, nb * n, 1, qkv.p, c, 0, MK_EPI_STORE, MK_BF16, nullptr, 0, 0, 0, nullptr,
+            MK_TRY(gemm(B.q2, xn_img.p, c, nc, n, nb, nullptr, 0, 0, MK_EPI_HEADS, MK_BF16, nullptr, 0, 0, 0, &hq,
                         "gemm.q2"));
-            MK_TRY(timed("heads", 0, [&] {
-                return mk_heads(qkv.p, nb, n, c, int64_t(n) * c, 0, H, 64, nullptr, 0, nullptr, 0, q.p, q_pad, 0, 0,
-                                MK_F16, stream);
-            }));
             // cross attention: batch b reads slot b's context keys (consecutive in the cache)
             const uint16_t* kc = slots[0].ck.h() + size_t(i) * 2 * H * s_pad * 64;
             const uint16_t* vc = slots[0].cvt.h() + size_t(i) * 2 * H * 64 * s_pad;

@@ -31,6 +31,7 @@ struct HeadsP {
     float eps, k_scale;
     uint32_t f16;     // Q, K, V^T as IEEE half (else bf16)
     int64_t rope_bs;  // floats between the batch items' RoPE tables
+    uint32_t hd;      // head dim: 128 (a wave slice of 128 channels is one head) or 64 (128-channel tiles)
 };
 
 struct GemmP {
@@ -352,6 +353,58 @@ __device__ inline void epi_heads(const GemmP& p, const float* st, int ld, int to
 #pragma unroll
     for (int i = 0; i < 8; ++i)
         emit(8 + i, ra[i], rb[i]);
+}
+
+// The heads epilogue for 64-dim heads (the SDXL form: no norm, no RoPE) on 128-channel tiles, whose wave slice of
+// 32 tokens x 64 channels is one head: Q / K rows [bh][row][64] (16 lanes a row, 4 channels each), V^T rows
+// [bh][d][k_pad] (a lane per dim, 32 keys in the vt_col order). Q-only launches (k == NULL) write Q alone.
+__device__ inline void epi_heads64(const GemmP& p, const float* st, int ld, int tok0, int nw0, int lane, uint32_t z)
+{
+    const HeadsP& h = p.hp;
+    const int which = nw0 / int(h.dim), head = (nw0 % int(h.dim)) / 64;
+    const int64_t bh = int64_t(z) * h.heads + head;
+    const int last = int(p.M) - 1;
+    if (which == 2) {
+        const int d = lane;
+        const float sc = p.wscale ? p.wscale[nw0 + d] : 1.0f, bi = p.bias ? p.bias[nw0 + d] : 0.0f;
+        const uint32_t k0 = h.row0 + tok0;
+        uint16_t* dst = h.vt + (bh * 64 + d) * int64_t(h.k_pad);
+        auto v = [&](int j) { return st[j * ld + d] * sc + bi; };
+        if (k0 % 16 == 0 && tok0 + 32 <= int(p.M)) {
+#pragma unroll
+            for (int g = 0; g < 2; ++g) {
+                // physical columns 16g + 0..15 hold keys 16g + {0..3, 8..11, 4..7, 12..15}
+                const int j0 = 16 * g;
+                *reinterpret_cast<u32x4*>(dst + k0 + j0) =
+                    u32x4{pack_x2(v(j0 + 0), v(j0 + 1), h.f16), pack_x2(v(j0 + 2), v(j0 + 3), h.f16),
+                          pack_x2(v(j0 + 8), v(j0 + 9), h.f16), pack_x2(v(j0 + 10), v(j0 + 11), h.f16)};
+                *reinterpret_cast<u32x4*>(dst + k0 + j0 + 8) =
+                    u32x4{pack_x2(v(j0 + 4), v(j0 + 5), h.f16), pack_x2(v(j0 + 6), v(j0 + 7), h.f16),
+                          pack_x2(v(j0 + 12), v(j0 + 13), h.f16), pack_x2(v(j0 + 14), v(j0 + 15), h.f16)};
+            }
+        } else {
+            for (int t = 0; t < 32 && tok0 + t <= last; ++t)
+                dst[vt_col(k0 + t)] = h.f16 ? f2h_bits(v(t)) : f2bf_bits(v(t));
+        }
+        return;
+    }
+    const int c = lane & 15, r0 = lane >> 4, ch = 4 * c;
+    const f32x4 sc = p.wscale ? *reinterpret_cast<const f32x4*>(p.wscale + nw0 + ch) : f32x4{1, 1, 1, 1};
+    const f32x4 bi = p.bias ? *reinterpret_cast<const f32x4*>(p.bias + nw0 + ch) : f32x4{0, 0, 0, 0};
+    const float ks = which == 1 ? h.k_scale : 1.0f;
+    const int64_t pad = which == 0 ? h.q_pad : h.k_pad;
+    uint16_t* base = (which == 0 ? h.q : h.k) + (bh * pad + (which == 0 ? h.q_row0 : h.row0)) * 64 + ch;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int r = r0 + 4 * i, t = tok0 + r;
+        f32x4 x = *reinterpret_cast<const f32x4*>(st + r * ld + ch);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            x[e] = (x[e] * sc[e] + bi[e]) * ks;
+        if (t <= last)
+            *reinterpret_cast<u32x2*>(base + int64_t(t) * 64) =
+                u32x2{pack_x2(x[0], x[1], h.f16), pack_x2(x[2], x[3], h.f16)};
+    }
 }
 
 // Stream-K state of a persistent launch: the tail tiles are split into k ranges over the whole grid; a workgroup
@@ -925,7 +978,10 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
 #pragma unroll 1
         for (int s = 0; s < NS; ++s) {
             stage(0);
-            epi_heads(p, st, LDW, m0 + wm * WM + s * 32, n0 + wn * WC, lane, z);
+            if constexpr (WC == 64)
+                epi_heads64(p, st, LDW, m0 + wm * WM + s * 32, n0 + wn * WC, lane, z);
+            else
+                epi_heads(p, st, LDW, m0 + wm * WM + s * 32, n0 + wn * WC, lane, z);
 #pragma unroll
             for (int cb = 0; cb < CB; ++cb)
 #pragma unroll
@@ -1209,18 +1265,28 @@ mk_status prepare(const mk_gemm_args* a, GemmP& p)
     p.batch = a->batch;
     p.glu_f = glu ? a->N / 2 : 0;
     if (a->epilogue == MK_EPI_HEADS) {
+        // q|k|v columns (N = 3 heads d), or q alone (k and vt NULL: N = heads d); d = 128 on 256-channel tiles
+        // (per-head RMSNorm and RoPE optional), d = 64 on 128-channel tiles (no norm, no RoPE)
         const mk_heads_args* h = a->heads;
-        if (!h || !h->q || !h->k || !h->vt || h->head_dim != 128 || a->N % 256 || (a->N / 3) % 128 ||
-            a->N / 3 != h->heads * 128 || h->rope_mode > 2 || (h->rope_mode && !h->rope) || h->k_pad % 16 ||
-            uint64_t(h->row0) + a->M > h->k_pad || uint64_t(h->q_row0) + a->M > h->q_pad ||
-            (h->dtype != 0 && h->dtype != MK_BF16 && h->dtype != MK_F16))
-            return fail(MK_ERR_ARG, "gemm heads epilogue: needs q, k, vt, head_dim 128, N = 3 * heads * 128 a multiple "
-                                    "of 256, k_pad a multiple of 16, row0 + M within the padded rows, and dtype bf16 "
-                                    "or f16");
+        const bool qonly = h && !h->k && !h->vt;
+        const uint32_t parts = qonly ? 1 : 3, d = h ? h->head_dim : 0;
+        bool ok = h && h->q && (qonly || (h->k && h->vt)) && (d == 128 || d == 64) && h->heads &&
+                  uint64_t(a->N) == uint64_t(parts) * h->heads * d && h->k_pad % 16 == 0 &&
+                  (qonly || uint64_t(h->row0) + a->M <= h->k_pad) && uint64_t(h->q_row0) + a->M <= h->q_pad &&
+                  (h->dtype == 0 || h->dtype == MK_BF16 || h->dtype == MK_F16);
+        if (d == 128)
+            ok = ok && a->N % 256 == 0 && h->rope_mode <= 2 && (!h->rope_mode || h->rope);
+        else
+            ok = ok && a->N % 128 == 0 && h->rope_mode == 0 && !h->norm_q && !h->norm_k;
+        if (!ok)
+            return fail(MK_ERR_ARG, "gemm heads epilogue: needs q (and k, vt, or neither: Q only), N = 3 (or 1) x "
+                                    "heads x head_dim, head_dim 128 with N a multiple of 256 or head_dim 64 with N a "
+                                    "multiple of 128 and no norm or RoPE, k_pad a multiple of 16, row0 + M within "
+                                    "the padded rows, and dtype bf16 or f16");
         p.hp = HeadsP{static_cast<uint16_t*>(h->q), static_cast<uint16_t*>(h->k), static_cast<uint16_t*>(h->vt),
-                      h->heads, h->q_pad, h->k_pad, h->row0, h->q_row0, h->rope_mode, a->N / 3, h->norm_q, h->norm_k,
-                      h->rope, h->eps, h->k_scale == 0.0f ? 1.0f : h->k_scale, h->dtype == MK_F16 ? 1u : 0u,
-                      h->rope_stride};
+                      h->heads, h->q_pad, h->k_pad, h->row0, h->q_row0, h->rope_mode, a->N / parts, h->norm_q,
+                      h->norm_k, h->rope, h->eps, h->k_scale == 0.0f ? 1.0f : h->k_scale, h->dtype == MK_F16 ? 1u : 0u,
+                      h->rope_stride, d};
     }
     return MK_OK;
 }
@@ -1240,7 +1306,8 @@ mk_status gemm_take_error()
 // k step of the tile relative to a 256 x 256 one, measured on MI355X (kt = 20-80, the SDXL and step shapes): 256 x 128
 // 0.66, 256 x 64 0.62, 128 x 128 0.67 for a pair of tiles (two workgroups share a CU: 64 KB of LDS each), so a wave of
 // 128 x 128 tiles is 2 per CU and an odd last tile costs half a pair; ties keep the larger tile. The heads epilogue
-// takes 256 x 256 tiles only; fp8 weights and convolutions 256-token tiles. 256 x 256 tiles use stream-K when whole waves leave at least 5% of the last wave's workgroups idle and
+// takes 256 x 256 tiles for 128-dim heads and 128-channel tiles for 64-dim heads; fp8 weights and convolutions
+// 256-token tiles. 256 x 256 tiles use stream-K when whole waves leave at least 5% of the last wave's workgroups idle and
 // a tile is long (K of 6144 or more; measured, the partials' exchange costs about 24 k steps of a tile, more than the
 // balance saves on shorter tiles): the whole waves go round robin, the rest is split by k steps (at least 4 a
 // workgroup).
@@ -1251,7 +1318,7 @@ GemmPlan gemm_plan(const mk_gemm_args* a, uint32_t n, uint32_t cus, bool conv)
     const bool heads = a[0].epilogue == MK_EPI_HEADS;
     const bool narrow_ok = a[0].epilogue != MK_EPI_GELU_TANH && a[0].epilogue != MK_EPI_SILU &&
                            a[0].epilogue != MK_EPI_SWIGLU && a[0].epilogue != MK_EPI_GEGLU; // 64-wide tiles
-    const bool short_ok = !heads && !conv && a[0].w_dtype == MK_BF16;                     // 128-token tiles
+    const bool short_ok = !heads && !conv && a[0].w_dtype == MK_BF16; // 128-token tiles
     auto tiles_of = [&](int bm, int bn) {
         uint64_t t = 0;
         for (uint32_t i = 0; i < n; ++i)
@@ -1279,6 +1346,12 @@ GemmPlan gemm_plan(const mk_gemm_args* a, uint32_t n, uint32_t cus, bool conv)
         if (best.cost < 0 || pl.cost < best.cost)
             best = pl;
     };
+    if (heads && a[0].heads && a[0].heads->head_dim == 64) {
+        consider(256, 128, 0.66);
+        if (a[0].w_dtype == MK_BF16)
+            consider(128, 128, 0.67);
+        return best;
+    }
     consider(256, 256, 1.0);
     if (heads)
         return best;
@@ -1343,6 +1416,8 @@ extern "C" mk_status mk_gemm_grouped(const mk_gemm_args* a, uint32_t count, void
         // 128 x 128 tiles (bf16 weights; launches of few tiles): two workgroups a CU
         if (ek == EK_STORE)
             e = launch<128, 128, false, EK_STORE, 4>(p, n, plan, s);
+        else if (ek == EK_HEADS)
+            e = launch<128, 128, false, EK_HEADS, 4>(p, n, plan, s);
         else if (ek == EK_ACT)
             e = launch<128, 128, false, EK_ACT, 4>(p, n, plan, s);
         else if (ek == EK_GLU)
@@ -1350,7 +1425,10 @@ extern "C" mk_status mk_gemm_grouped(const mk_gemm_args* a, uint32_t count, void
         else
             e = launch<128, 128, false, EK_RMW, 4>(p, n, plan, s);
     } else if (ek == EK_HEADS) {
-        MK_GEMM_EK(256, EK_HEADS);
+        if (bn == 256)
+            MK_GEMM_EK(256, EK_HEADS);
+        else
+            MK_GEMM_EK(128, EK_HEADS);
     } else if (bn == 256) {
         if (ek == EK_STORE)
             MK_GEMM_EK(256, EK_STORE);

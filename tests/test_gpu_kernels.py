@@ -200,6 +200,50 @@ def test_gemm_heads_epilogue(gpu, rng, mode, row0, q_row0, k_scale, odt):
     assert not gk[:, :, :row0].any() and not gk[:, :, row0 + Mr:].any()
 
 
+# 64-dim heads (the SDXL form: half, no norm, no RoPE) on 128-channel tiles: q | k | v and Q alone, batch 2, row
+# counts that end inside a tile and inside a 16-key group; each value within one rounding (half or bf16) of the
+# oracle's GEMM, padding rows untouched (zero)
+@pytest.mark.parametrize("Mr,H,qonly,odt,k_scale", [(1024, 20, False, M.F16, 0.0), (300, 10, False, M.F16, 0.5),
+                                                    (77, 4, False, M.BF16, 0.0), (1024, 20, True, M.F16, 0.0),
+                                                    (130, 2, True, M.BF16, 0.0)])
+def test_gemm_heads64_epilogue(gpu, rng, Mr, H, qonly, odt, k_scale):
+    B, d, K_ = 2, 64, 320
+    D = H * d
+    parts = 1 if qonly else 3
+    q_pad, k_pad = -(-Mr // 256) * 256, -(-Mr // 64) * 64
+    A = rng.standard_normal((B, Mr, K_)).astype(np.float32)
+    W = R.bf16_round(rng.standard_normal((parts * D, K_)).astype(np.float32) * 0.05)
+    b = rng.standard_normal(parts * D).astype(np.float32) * 0.1
+    Q = dev(np.zeros(B * H * q_pad * d, np.uint16))
+    Kd = None if qonly else dev(np.zeros(B * H * k_pad * d, np.uint16))
+    Vt = None if qonly else dev(np.zeros(B * H * k_pad * d, np.uint16))
+    ha = M.HeadsArgs(Q.p, None if qonly else Kd.p, None if qonly else Vt.p, H, d, q_pad, k_pad, 0, 0, None, None,
+                     None, 0, 0.0, k_scale, odt)
+    gemm(bdev(A), bdev(W), bias=dev(b), epi=M.EPI_HEADS, c_dtype=M.BF16, M_=(Mr, parts * D, K_), batch=B, lda=K_,
+         sa=Mr * K_, heads=ha)
+    get = (lambda t, sh: M.f16_to_f32(t.to_array(np.uint16, sh))) if odt == M.F16 else fetch_bf16
+    rnd = R.f16_round if odt == M.F16 else R.bf16_round
+    ulp = 2 ** -10 if odt == M.F16 else 2 ** -7
+    gq = get(Q, (B, H, q_pad, d))
+    outs = [(gq, 0)]
+    if not qonly:
+        outs += [(get(Kd, (B, H, k_pad, d)), D), (get(Vt, (B, H, d, k_pad)), 2 * D)]
+    for bi in range(B):
+        y = R.gemm(A[bi], W, b)
+        for j, (g, col0) in enumerate(outs):
+            want = y[:, col0:col0 + D].reshape(Mr, H, d).transpose(1, 0, 2)  # [H][Mr][d]
+            if j == 1:
+                want = want * (k_scale or 1.0)
+            if j == 2:
+                got = g[bi][:, :, M.vt_col(np.arange(Mr))].transpose(0, 2, 1)
+                pad = g[bi][:, :, M.vt_col(np.arange(Mr, k_pad))] if Mr < k_pad else np.zeros(1)
+            else:
+                got = g[bi][:, :Mr]
+                pad = g[bi][:, Mr:]
+            assert np.abs(got - rnd(want)).max() <= ulp * np.abs(want).max()
+            assert not pad.any()
+
+
 def test_gemm_grouped_residual_equals_separate_launches(gpu, rng):
     # an image-like and a text-like problem (own A, W, bias, gate, residual, M and strides) in one launch give the
     # bits of two launches, and match the oracle
