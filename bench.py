@@ -9,7 +9,8 @@ Synthetic inputs: prompts and latents N(0, 1), resident on the device when the t
 Prints one JSON line. `roofline` is the dominant kernel (the launch shape with the most time a step: the grouped
 FFN-down GEMM): its algorithmic FLOPs per launch divided by its average launch duration, from HIP events recorded
 around each launch on the engine's stream in a separate timed pass of the same steps; `gemm_class` is the same over
-every GEMM launch, `attention_gemm_mfma_frac` over every GEMM and attention launch. `cpu_baseline` is the oracle (CPU restatement of the same step) on a bounded sample of one
+every GEMM launch, `attention_gemm_mfma_frac` over every GEMM and attention launch (their FLOPs over the union of
+their launch intervals). `cpu_baseline` is the oracle (CPU restatement of the same step) on a bounded sample of one
 block, timed on this host's cores and scaled by FLOPs to a whole step.
 """
 import argparse
