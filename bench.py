@@ -432,15 +432,16 @@ def step_bytes_ff2(N=4096, S=256, B=2, D=3072, F=12288):
 
 
 def cpu_baseline(seconds_target=12.0, fp8=False):
-    """The oracle on one dual-stream block of one sample at a reduced image size (32 x 32 tokens + the workload's text
-    tokens), timed on this host; throughput scaled to the full step's FLOPs."""
+    """The oracle on one dual-stream block of one sample, timed on this host. At 1024x1024 the block runs at the
+    step's own sequence (64 x 64 image tokens + the text tokens), so the step is exactly 60 blocks x 2 samples of it;
+    larger workloads sample a 64 x 64 block and scale by FLOPs (their attention share differs)."""
     import numpy as np
 
     import mkref as R
 
     m = R.Model(R.DUAL, **{**CFG, "blocks": 1}, fp8=fp8, seed=0)
     rng = np.random.default_rng(0)
-    n_side = 32
+    n_side = min(H, 64)
     N = n_side * n_side
     img = rng.standard_normal((N, 3072)).astype(np.float32)
     txt = rng.standard_normal((S, 3072)).astype(np.float32)
@@ -460,7 +461,9 @@ def cpu_baseline(seconds_target=12.0, fp8=False):
             "sample": f"oracle (C++/OpenMP, fp32 over {'fp8' if fp8 else 'bf16'} weights): {reps} x one dual-stream "
                       f"block of one sample at "
                       f"{N} image + {S} text tokens ({flops / 1e9:.0f} GFLOP each, {t_total:.1f} s, "
-                      f"{rate / 1e9:.1f} GFLOP/s), scaled by FLOPs to the 60-block batch-2 step at {H * W} + {S} tokens"}
+                      f"{rate / 1e9:.1f} GFLOP/s), "
+                      + (f"x 60 blocks x 2 samples (the step's own shape)" if N == H * W else
+                         f"scaled by FLOPs to the 60-block batch-2 step at {H * W} + {S} tokens")}
 
 
 def copy_calibration(args):
