@@ -55,7 +55,7 @@ __device__ inline u32x4 buf_load16(BufRes, uint32_t, uint32_t) { return u32x4{};
 // ---- GEMM dispatch plan (gemm.hip), shared with the engine's launch-grouping cost model ----
 struct GemmPlan {
     int bm;          // tile height in tokens (256, or 128 for launches of few tiles)
-    int bn;          // tile width in channels (256, 128 or 64)
+    int bn;          // tile width in channels (256, 192 (convolutions), 128 or 64)
     uint64_t tiles;  // tiles of the launch
     bool sk;         // stream-K: whole waves round robin, the last partial wave split by k steps
     uint64_t dp;     // tiles done whole (stream-K)

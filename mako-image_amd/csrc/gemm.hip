@@ -990,11 +990,27 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
         }
         return;
     }
-    EpiCh kch = epi_channels(p, n0 + wn * WC + 4 * (lane % (WC / 4)));
+    if constexpr (WC == 96) {
+        // 192-channel tiles: the wave's 96 staged channels go out as three 32-channel slices
+        EpiCh kch[3];
 #pragma unroll
-    for (int s = 0; s < NS; ++s) {
-        stage(s);
-        epi_slice<EKE, WC>(p, st, LDW, m0 + wm * WM + s * 32, n0 + wn * WC, lane, zc, kch);
+        for (int j = 0; j < 3; ++j)
+            kch[j] = epi_channels(p, n0 + wn * WC + 32 * j + 4 * (lane % 8));
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            stage(s);
+#pragma unroll
+            for (int j = 0; j < 3; ++j)
+                epi_slice<EKE, 32>(p, st + 32 * j, LDW, m0 + wm * WM + s * 32, n0 + wn * WC + 32 * j, lane, zc,
+                                   kch[j]);
+        }
+    } else {
+        EpiCh kch = epi_channels(p, n0 + wn * WC + 4 * (lane % (WC / 4)));
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            stage(s);
+            epi_slice<EKE, WC>(p, st, LDW, m0 + wm * WM + s * 32, n0 + wn * WC, lane, zc, kch);
+        }
     }
 }
 
@@ -1305,7 +1321,8 @@ mk_status gemm_take_error()
 // The tile shape of a launch, by its estimated duration: waves of tiles (rounded up) x k steps x the duration of one
 // k step of the tile relative to a 256 x 256 one, measured on MI355X (kt = 20-80, the SDXL and step shapes): 256 x 128
 // 0.66, 256 x 64 0.62, 128 x 128 0.67 for a pair of tiles (two workgroups share a CU: 64 KB of LDS each), so a wave of
-// 128 x 128 tiles is 2 per CU and an odd last tile costs half a pair; ties keep the larger tile. The heads epilogue
+// 128 x 128 tiles is 2 per CU and an odd last tile costs half a pair; ties keep the larger tile. Convolutions also
+// have 256 x 192 tiles (8 waves, 0.78), for their 192- and 384-channel layers. The heads epilogue
 // takes 256 x 256 tiles for 128-dim heads and 128-channel tiles for 64-dim heads; fp8 weights and convolutions
 // 256-token tiles. 256 x 256 tiles use stream-K when whole waves leave at least 5% of the last wave's workgroups idle and
 // a tile is long (K of 6144 or more; measured, the partials' exchange costs about 24 k steps of a tile, more than the
@@ -1356,6 +1373,8 @@ GemmPlan gemm_plan(const mk_gemm_args* a, uint32_t n, uint32_t cus, bool conv)
     if (heads)
         return best;
     consider(256, 128, 0.66);
+    if (conv)
+        consider(256, 192, 0.78);
     if (narrow_ok)
         consider(256, 64, 0.62);
     if (short_ok)
@@ -1511,6 +1530,9 @@ extern "C" mk_status mk_conv3x3(const mk_conv_args* a, void* stream)
     if (plan.bn == 256)
         return add ? launch<256, 256, false, EK_RMW | EK_CONV, 8>(&p, 1, plan, s)
                    : launch<256, 256, false, EK_STORE | EK_CONV, 8>(&p, 1, plan, s);
+    if (plan.bn == 192)
+        return add ? launch<256, 192, false, EK_RMW | EK_CONV, 8>(&p, 1, plan, s)
+                   : launch<256, 192, false, EK_STORE | EK_CONV, 8>(&p, 1, plan, s);
     if (plan.bn == 128)
         return add ? launch<256, 128, false, EK_RMW | EK_CONV, 4>(&p, 1, plan, s)
                    : launch<256, 128, false, EK_STORE | EK_CONV, 4>(&p, 1, plan, s);

@@ -237,19 +237,70 @@ __global__ __launch_bounds__(256) void vae_compact_kernel(const float* __restric
     y[i] = x[g.row_of(uint32_t(p / g.w), uint32_t(p % g.w)) * cs + i % c];
 }
 
-// conv_out's first 3 channels -> RGBA in [-1, 1], alpha 1 (engine.cpp:948-953). One thread a pixel.
-__global__ __launch_bounds__(256) void vae_out_kernel(const float* __restrict__ x, uint32_t cs, GridDims g,
-                                                      float* __restrict__ rgba)
+// conv_out (3 x 3, c -> 3 channels, engine.cpp:940-946) fused with the clamp to RGBA (engine.cpp:948-953). Three
+// output channels are too few for the matrix cores (a 64-channel tile computes 61 zero channels), so: a workgroup
+// takes a 16 x 16 pixel tile, stages its 18 x 18 input neighbourhood (c channels, rows padded by 8 so the 16 lanes of a
+// pixel row read distinct banks) and the 3 x 9 x c weights in LDS with whole-row loads, then each thread sums its
+// pixel's 9 taps from LDS (weights: broadcasts), bf16 pairs by v_dot2_f32_bf16 with fp32 accumulation. x: the bf16
+// grid (cs channels a row, zero ring and zero channels past the input's); c: the input's channels rounded up to 8
+// (<= cs <= 128); w: the packed weight rows [3][9][cs]; pre (may be NULL): the unclamped values into the fp32 grid
+// rows (stride ps), for probes.
+constexpr int kCoTile = 16;
+struct alignas(16) Bf16Quad { // 4 bf16 pairs: one 16-byte LDS access
+    bf16x2cv v[4];
+};
+__global__ __launch_bounds__(256) void vae_conv_out_kernel(const uint16_t* __restrict__ x, uint32_t cs, uint32_t c,
+                                                           GridDims g, const uint16_t* __restrict__ w,
+                                                           const float* __restrict__ bias, float* __restrict__ rgba,
+                                                           float* __restrict__ pre, uint32_t ps)
 {
-    const uint64_t p = uint64_t(blockIdx.x) * 256 + threadIdx.x;
-    if (p >= uint64_t(g.h) * g.w)
+    // (operands are read as bf16 pairs: no bit casts of vector elements, which this compiler gets wrong)
+    constexpr int NB = kCoTile + 2;
+    __shared__ Bf16Quad sw[3][9][16];
+    extern __shared__ __attribute__((aligned(16))) uint16_t sx[]; // NB x NB pixels x (c + 8): the launch's size
+    const uint32_t pst = c + 8; // LDS pixel stride (elements)
+    const uint32_t tid = threadIdx.x, cq = c / 8;
+    const uint32_t ty0 = blockIdx.y * kCoTile, tx0 = blockIdx.x * kCoTile;
+    for (uint32_t i = tid; i < 3 * 9 * cq; i += 256) {
+        const uint32_t o = i / (9 * cq), r = i - o * 9 * cq, tap = r / cq, j = r - tap * cq;
+        sw[o][tap][j] = *reinterpret_cast<const Bf16Quad*>(w + (uint64_t(o) * 9 + tap) * cs + 8 * j);
+    }
+    // neighbourhood pixel (qy, qx) is grid pixel (ty0 + qy - 1, tx0 + qx - 1): grid row slack + (ty0 + qy) (w + 2) +
+    // tx0 + qx, inside the grid while ty0 + qy <= h + 1 and tx0 + qx <= w + 1
+    for (uint32_t i = tid; i < NB * NB * cq; i += 256) {
+        const uint32_t q = i / cq, k = i - q * cq, qy = q / NB, qx = q - qy * NB;
+        u32x4 v = u32x4{0, 0, 0, 0};
+        if (ty0 + qy <= g.h + 1 && tx0 + qx <= g.w + 1)
+            v = *reinterpret_cast<const u32x4*>(x + (g.slack() + uint64_t(ty0 + qy) * g.pw() + tx0 + qx) * cs + 8 * k);
+        *reinterpret_cast<u32x4*>(sx + q * pst + 8 * k) = v;
+    }
+    __syncthreads();
+    const uint32_t ly = tid / kCoTile, lx = tid - ly * kCoTile, py = ty0 + ly, px = tx0 + lx;
+    if (py >= g.h || px >= g.w)
         return;
-    const float* xr = x + g.row_of(uint32_t(p / g.w), uint32_t(p % g.w)) * cs;
-    f32x4 o;
-    for (int k = 0; k < 3; ++k)
-        o[k] = fminf(1.0f, fmaxf(-1.0f, xr[k]));
-    o[3] = 1.0f;
-    *reinterpret_cast<f32x4*>(rgba + 4 * p) = o;
+    float acc[3] = {bias[0], bias[1], bias[2]};
+#pragma unroll
+    for (int tap = 0; tap < 9; ++tap) {
+        const int dy = tap / 3, dx = tap - 3 * dy;
+        const Bf16Quad* xq = reinterpret_cast<const Bf16Quad*>(sx + ((ly + dy) * NB + lx + dx) * pst);
+        for (uint32_t j = 0; j < cq; ++j) {
+            const Bf16Quad a = xq[j];
+#pragma unroll
+            for (int o = 0; o < 3; ++o) {
+                const Bf16Quad wq = sw[o][tap][j];
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    acc[o] = __builtin_amdgcn_fdot2_f32_bf16(a.v[e], wq.v[e], acc[o], false);
+            }
+        }
+    }
+    if (pre)
+#pragma unroll
+        for (int o = 0; o < 3; ++o)
+            pre[g.row_of(py, px) * ps + o] = acc[o];
+    const uint64_t p = uint64_t(py) * g.w + px;
+    *reinterpret_cast<f32x4*>(rgba + 4 * p) = f32x4{fminf(1.0f, fmaxf(-1.0f, acc[0])), fminf(1.0f, fmaxf(-1.0f, acc[1])),
+                                                    fminf(1.0f, fmaxf(-1.0f, acc[2])), 1.0f};
 }
 
 // A PyTorch conv weight [parts * co][ci][kt][k][k] (bf16; kt time taps of a causal 3-D conv, the last one used: a
@@ -710,10 +761,15 @@ struct mk_vae {
             MK_TRY(probe_grid("vae_up", i, xp, cs, g, u.up ? u.conv.co : u.cout));
         }
         MK_TRY(norm(xp, cs, g, b, out_g, 0, a.p, conv_out.cip()));
-        MK_TRY(conv3(conv_out, a.p, g, yp, conv_out.cop(), false));
+        // (base <= 128: conv_out's input takes at most 128 padded channels)
+        const dim3 cog((g.w + kCoTile - 1) / kCoTile, (g.h + kCoTile - 1) / kCoTile);
+        const uint32_t c8 = (conv_out.ci + 7) / 8 * 8;
+        const size_t lds = size_t(kCoTile + 2) * (kCoTile + 2) * (c8 + 8) * 2;
+        vae_conv_out_kernel<<<cog, 256, lds, stream>>>(static_cast<const uint16_t*>(a.p), conv_out.cip(), c8, g,
+                                                       conv_out.w, conv_out.b, out,
+            probe ? yp : nullptr, conv_out.cop());
+        MK_LAUNCH_CHECK("vae_conv_out");
         MK_TRY(probe_grid("vae_out", -1, yp, conv_out.cop(), g, 3));
-        vae_out_kernel<<<blocks_for(uint64_t(g.h) * g.w), 256, 0, stream>>>(yp, conv_out.cop(), g, out);
-        MK_LAUNCH_CHECK("vae_out");
         return MK_OK;
     }
 };

@@ -48,9 +48,11 @@ def from_grid(g, h, w, c):
     return np.stack([g[S + (y + 1) * (w + 2) + 1:S + (y + 1) * (w + 2) + 1 + w, :c] for y in range(h)])
 
 
+# (the 150 x 150 grids take 192-channel tiles: more than a wave of 64- or 128-channel ones)
 @pytest.mark.parametrize("h, w, c, n, add", [(5, 7, 64, 64, False), (16, 16, 128, 192, False),
                                              (9, 33, 192, 64, True), (32, 40, 384, 384, True),
-                                             (1, 1, 64, 128, False), (64, 3, 64, 256, False)])
+                                             (1, 1, 64, 128, False), (64, 3, 64, 256, False),
+                                             (150, 150, 64, 192, True), (150, 150, 64, 384, False)])
 def test_conv3x3_matches_torch(gpu, h, w, c, n, add):
     rng = np.random.default_rng(h * 1000 + w)
     x = M.bf16_bits(rng.standard_normal((h, w, c)).astype(np.float32))
