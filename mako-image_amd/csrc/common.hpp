@@ -85,6 +85,9 @@ mk_status ln_modulate_group(const LnArgs* a, int count, uint32_t n, float eps, v
 // Zero `bytes` (a multiple of 4, 4-byte aligned) of device memory on a stream with a kernel (kernels.hip): a fill node
 // a caller's graph capture can replay, unlike a memset node.
 mk_status fill_zero(void* p, size_t bytes, void* stream);
+// mk_conv3x3 for c (a multiple of 8, not of 64, <= 512) input channels in rows of stride lda, with dense weights
+// [n][K], K = 9 c rounded up to 64 (k = tap c + channel, zero past 9 c) (gemm.hip).
+mk_status conv3x3_dense(const mk_conv_args* a, uint32_t lda, void* stream);
 
 // ---- error state (thread-local, read by mk_last_error) ----
 void set_error(const std::string& msg);

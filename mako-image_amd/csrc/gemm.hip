@@ -48,7 +48,7 @@ struct GemmP {
     uint32_t tiles_m, tiles_n, batch;
     HeadsP hp;
     // 3 x 3 convolution (EK_CONV): the padded grid's row width w + 2, k tiles a tap (channels / 64), and
-    // ceil(2^16 / conv_tpt) for the tap index by multiply-shift
+    // ceil(2^16 / conv_tpt) for the tap index by multiply-shift; with EK_CONVQ conv_tpt counts 8-channel chunks
     uint32_t conv_pw, conv_tpt, conv_inv;
     // gated linear unit (EK_GLU): the weights' rows are [first part F; second part F], the output [M][F]
     uint32_t glu_f;
@@ -93,6 +93,9 @@ __device__ inline void f8x16_to_bf16(const u32x4& v, u32x4& lo, u32x4& hi)
 enum { EK_STORE = 0, EK_ACT = 1, EK_RMW = 2, EK_HEADS = 3, EK_GLU = 4 };
 // Flag on the epilogue kind: the A operand is a 3 x 3 convolution's input (implicit im2col, see conv_koff).
 constexpr int EK_CONV = 8;
+// With EK_CONV: input channels not a multiple of 64 (dense K = 9 c rounded up to 64, k = tap c + channel): a k step
+// spans taps, so each 16-byte chunk (8 channels) takes its own tap's row shift (conv3x3_dense).
+constexpr int EK_CONVQ = 32;
 
 // Per-tile channel constants of a lane's 4 channels (the same for every token row it writes).
 struct EpiCh {
@@ -479,7 +482,7 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
 {
     static_assert(((EK & 7) != EK_HEADS && (EK & 7) != EK_GLU) || !(EK & EK_CONV),
                   "a convolution has no heads or GLU epilogue");
-    constexpr bool kConv = (EK & EK_CONV) != 0;
+    constexpr bool kConv = (EK & EK_CONV) != 0, kConvQ = (EK & EK_CONVQ) != 0;
     constexpr int EKE = EK & 7;                 // the epilogue kind
     constexpr int NT = 64 * NW;                 // threads
     constexpr int WM = BM / (NW / 2);           // tokens per wave (waves: 2 along channels x NW/2 along tokens)
@@ -538,12 +541,25 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
         }
     };
     const BufRes rsW = buf_res(gW, uint32_t((kGlu ? int64_t(p.glu_f) + BN / 2 : int64_t(BN)) * p.K * 2));
-    uint32_t oa[RA];
+    uint32_t oa[RA], kq[kConvQ ? RA : 1];
 #pragma unroll
     for (int i = 0; i < RA; ++i) {
         const int P = (i * NW + wave) * 64 + lane, row = P >> 3, kc = swz_chunk(row, P & 7);
-        oa[i] = uint32_t(min(row, int(p.M) - 1 - m0) * int(p.lda) + kc * 8) * 2;
+        oa[i] = uint32_t(min(row, int(p.M) - 1 - m0) * int(p.lda) + (kConvQ ? 0 : kc * 8)) * 2;
+        if constexpr (kConvQ)
+            kq[i] = uint32_t(kc);
     }
+    // EK_CONVQ: the lane's A byte offset (beyond its row) for chunk kq[i] of k step kt: global chunk q = 8 kt + kc,
+    // tap = q / cq, channel chunk q - tap cq (multiply-shift, exact for q < 2^16 / cq: cq <= 64); the tail past
+    // 9 cq (zero weights) reads tap 8's rows
+    auto koffq = [&](int kt, int i) -> uint32_t {
+        const uint32_t q = uint32_t(kt) * 8 + kq[i];
+        uint32_t tap = (q * p.conv_inv) >> 16;
+        const uint32_t ch8 = q - tap * p.conv_tpt;
+        tap = min(tap, 8u);
+        const uint32_t dy = (tap * 21846u) >> 16, dx = tap - 3 * dy;
+        return ((dy * p.conv_pw + dx) * uint32_t(p.lda) + ch8 * 8) * 2;
+    };
     uint32_t ow[kF8 ? 1 : RW];
     const uint8_t* gw8[kF8 ? LW : 1];
     if constexpr (!kF8) {
@@ -562,8 +578,12 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
     u32x4 rw[kF8 ? LW : 1];
     // direct load i (activation rounds first, then bf16 weight rounds) of k step kt into buffer buf
     auto dma1 = [&](int kt, int buf, int i) {
-        if (i < RA)
-            buf_load_lds16(rsA, (lds_void*)&sA[buf][(i * NW + wave) * 64 * 8], oa[i], koffA(kt));
+        if (i < RA) {
+            if constexpr (kConvQ)
+                buf_load_lds16(rsA, (lds_void*)&sA[buf][(i * NW + wave) * 64 * 8], oa[i] + koffq(kt, i), 0);
+            else
+                buf_load_lds16(rsA, (lds_void*)&sA[buf][(i * NW + wave) * 64 * 8], oa[i], koffA(kt));
+        }
         else if constexpr (!kF8)
             buf_load_lds16(rsW, (lds_void*)&sW[buf][((i - RA) * NW + wave) * 64 * 8], ow[i - RA],
                            uint32_t(kt * BK * 2));
@@ -634,7 +654,7 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
     auto gload = [&](int kt, int i) {
         if constexpr (kStage) {
             if (i < RA)
-                stg[i] = buf_load16(rsA, oa[i], koffA(kt));
+                stg[i] = kConvQ ? buf_load16(rsA, oa[i] + koffq(kt, i), 0) : buf_load16(rsA, oa[i], koffA(kt));
             else
                 stg[i] = buf_load16(rsW, ow[i - RA], uint32_t(kt * BK * 2));
         }
@@ -1323,8 +1343,7 @@ mk_status gemm_take_error()
 // 0.66, 256 x 64 0.62, 128 x 128 0.67 for a pair of tiles (two workgroups share a CU: 64 KB of LDS each), so a wave of
 // 128 x 128 tiles is 2 per CU and an odd last tile costs half a pair; ties keep the larger tile. Convolutions also
 // have 256 x 192 tiles (8 waves, 0.78), for their 192- and 384-channel layers. The heads epilogue
-// takes 256 x 256 tiles for 128-dim heads and 128-channel tiles for 64-dim heads; fp8 weights and convolutions
-// 256-token tiles. 256 x 256 tiles use stream-K when whole waves leave at least 5% of the last wave's workgroups idle and
+// takes 256 x 256 tiles for 128-dim heads and 128-channel tiles for 64-dim heads; fp8 weights 256-token tiles. 256 x 256 tiles use stream-K when whole waves leave at least 5% of the last wave's workgroups idle and
 // a tile is long (K of 6144 or more; measured, the partials' exchange costs about 24 k steps of a tile, more than the
 // balance saves on shorter tiles): the whole waves go round robin, the rest is split by k steps (at least 4 a
 // workgroup).
@@ -1335,7 +1354,7 @@ GemmPlan gemm_plan(const mk_gemm_args* a, uint32_t n, uint32_t cus, bool conv)
     const bool heads = a[0].epilogue == MK_EPI_HEADS;
     const bool narrow_ok = a[0].epilogue != MK_EPI_GELU_TANH && a[0].epilogue != MK_EPI_SILU &&
                            a[0].epilogue != MK_EPI_SWIGLU && a[0].epilogue != MK_EPI_GEGLU; // 64-wide tiles
-    const bool short_ok = !heads && !conv && a[0].w_dtype == MK_BF16; // 128-token tiles
+    const bool short_ok = !heads && a[0].w_dtype == MK_BF16; // 128-token tiles
     auto tiles_of = [&](int bm, int bn) {
         uint64_t t = 0;
         for (uint32_t i = 0; i < n; ++i)
@@ -1527,6 +1546,9 @@ extern "C" mk_status mk_conv3x3(const mk_conv_args* a, void* stream)
     plan.sk = false;
     hipStream_t s = static_cast<hipStream_t>(stream);
     const bool add = a->epilogue == MK_EPI_ADD;
+    if (plan.bm == 128)
+        return add ? launch<128, 128, false, EK_RMW | EK_CONV, 4>(&p, 1, plan, s)
+                   : launch<128, 128, false, EK_STORE | EK_CONV, 4>(&p, 1, plan, s);
     if (plan.bn == 256)
         return add ? launch<256, 256, false, EK_RMW | EK_CONV, 8>(&p, 1, plan, s)
                    : launch<256, 256, false, EK_STORE | EK_CONV, 8>(&p, 1, plan, s);
@@ -1539,3 +1561,65 @@ extern "C" mk_status mk_conv3x3(const mk_conv_args* a, void* stream)
     return add ? launch<256, 64, false, EK_RMW | EK_CONV, 4>(&p, 1, plan, s)
                : launch<256, 64, false, EK_STORE | EK_CONV, 4>(&p, 1, plan, s);
 }
+
+namespace mk {
+// mk_conv3x3 for inputs whose channel count c is a multiple of 8 but not of 64 (at most 512), rows of stride lda (a
+// multiple of 8, >= c): the weight w is dense [n][K], K = 9 c rounded up to 64, k = tap c + channel for k < 9 c and
+// zero beyond, so no MFMA work goes to channel padding (the VAE's 96-channel level: K 864 -> 896 instead of 1152).
+mk_status conv3x3_dense(const mk_conv_args* a, uint32_t lda, void* stream)
+{
+    if (!a || !a->x || !a->w || !a->y)
+        return fail(MK_ERR_ARG, "conv3x3_dense: null argument");
+    if (!a->h || !a->width || !a->c || a->c % 8 || a->c % 64 == 0 || a->c > 512 || lda < a->c || lda % 8 ||
+        a->n % 64 || !a->n)
+        return fail(MK_ERR_ARG, "conv3x3_dense: channels in a multiple of 8 (not of 64) up to 512, lda >= c a "
+                                "multiple of 8, channels out a nonzero multiple of 64");
+    if ((a->epilogue != MK_EPI_STORE && a->epilogue != MK_EPI_ADD) ||
+        (a->epilogue == MK_EPI_ADD && a->y_dtype != MK_F32) || (a->y_dtype != MK_F32 && a->y_dtype != MK_BF16))
+        return fail(MK_ERR_ARG, "conv3x3_dense: epilogue STORE (fp32 or bf16) or ADD (fp32)");
+    const uint64_t pw = uint64_t(a->width) + 2, rows = (uint64_t(a->h) + 2) * pw;
+    if (rows >= (1u << 31) || (256 + 2 * pw + 2) * lda * 2 >= (uint64_t(1) << 32) || a->ldy < a->n)
+        return fail(MK_ERR_ARG, "conv3x3_dense: image too large or ldy < n");
+    mk_gemm_args g{};
+    g.a = a->x;
+    g.w = a->w;
+    g.bias = a->bias;
+    g.c = a->y;
+    g.M = uint32_t(rows);
+    g.N = a->n;
+    g.K = (9 * a->c + 63) / 64 * 64;
+    g.lda = lda;
+    g.ldc = a->ldy;
+    g.batch = 1;
+    g.w_dtype = MK_BF16;
+    g.c_dtype = a->y_dtype;
+    g.epilogue = a->epilogue;
+    GemmP p;
+    MK_TRY(prepare(&g, p));
+    p.conv_pw = uint32_t(pw);
+    p.conv_tpt = a->c / 8;
+    p.conv_inv = (65536u + p.conv_tpt - 1) / p.conv_tpt;
+    int cus = 0, dev = 0;
+    MK_HIP(hipGetDevice(&dev));
+    MK_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    GemmPlan plan = gemm_plan(&g, 1, uint32_t(cus > 0 ? cus : 1), true);
+    plan.sk = false;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const bool add = a->epilogue == MK_EPI_ADD;
+    constexpr int Q = EK_CONV | EK_CONVQ;
+    if (plan.bm == 128)
+        return add ? launch<128, 128, false, EK_RMW | Q, 4>(&p, 1, plan, s)
+                   : launch<128, 128, false, EK_STORE | Q, 4>(&p, 1, plan, s);
+    if (plan.bn == 256)
+        return add ? launch<256, 256, false, EK_RMW | Q, 8>(&p, 1, plan, s)
+                   : launch<256, 256, false, EK_STORE | Q, 8>(&p, 1, plan, s);
+    if (plan.bn == 192)
+        return add ? launch<256, 192, false, EK_RMW | Q, 8>(&p, 1, plan, s)
+                   : launch<256, 192, false, EK_STORE | Q, 8>(&p, 1, plan, s);
+    if (plan.bn == 128)
+        return add ? launch<256, 128, false, EK_RMW | Q, 4>(&p, 1, plan, s)
+                   : launch<256, 128, false, EK_STORE | Q, 4>(&p, 1, plan, s);
+    return add ? launch<256, 64, false, EK_RMW | Q, 4>(&p, 1, plan, s)
+               : launch<256, 64, false, EK_STORE | Q, 4>(&p, 1, plan, s);
+}
+} // namespace mk

@@ -324,6 +324,24 @@ __global__ __launch_bounds__(256) void vae_pack_kernel(const uint16_t* __restric
     dst[i] = v;
 }
 
+// A 3 x 3 conv weight packed dense for conv3x3_dense: dst [cop][kp], k = tap ci + c for k < 9 ci, zero beyond and
+// for rows past co (source as vae_pack_kernel's, one part).
+__global__ __launch_bounds__(256) void vae_pack_dense_kernel(const uint16_t* __restrict__ src, uint32_t co,
+                                                             uint32_t ci, uint32_t kt, uint32_t cop, uint32_t kp,
+                                                             uint16_t* __restrict__ dst)
+{
+    const uint64_t i = uint64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= uint64_t(cop) * kp)
+        return;
+    const uint32_t o = uint32_t(i / kp), k = uint32_t(i - uint64_t(o) * kp);
+    uint16_t v = 0;
+    if (o < co && k < 9 * ci) {
+        const uint32_t tap = k / ci, c = k - tap * ci;
+        v = src[((uint64_t(o) * ci + c) * kt + (kt - 1)) * 9 + tap];
+    }
+    dst[i] = v;
+}
+
 // fp32 vector [parts * n] -> [parts][np] zero-padded.
 __global__ __launch_bounds__(256) void vae_pack_vec_kernel(const float* __restrict__ src, uint32_t parts, uint32_t n,
                                                            uint32_t np, float* __restrict__ dst)
@@ -351,8 +369,10 @@ struct mk_vae {
         uint16_t* w = nullptr;
         float* b = nullptr;
         uint32_t co = 0, ci = 0, k = 0, parts = 1;
+        bool dense = false; // 3 x 3 weights packed [cop][kp] for conv3x3_dense (ci not a multiple of 64)
         uint32_t cop() const { return cpad(co); }
         uint32_t cip() const { return cpad(ci); }
+        uint32_t kp() const { return (9 * ci + 63) / 64 * 64; }
     };
     struct Res {
         float *g1 = nullptr, *g2 = nullptr;
@@ -431,12 +451,15 @@ struct mk_vae {
         return MK_OK;
     }
 
-    mk_status conv(Conv& c, const std::string& name, uint32_t co, uint32_t ci, uint32_t k, uint32_t parts = 1)
+    // dense_ok: a 3 x 3 conv run by conv3 may take dense weights (not conv_out, whose kernel reads [3][9][cip])
+    mk_status conv(Conv& c, const std::string& name, uint32_t co, uint32_t ci, uint32_t k, uint32_t parts = 1,
+                   bool dense_ok = true)
     {
         c.co = co;
         c.ci = ci;
         c.k = k;
         c.parts = parts;
+        c.dense = dense_ok && k == 3 && parts == 1 && ci % 64 && ci % 8 == 0 && ci <= 512;
         MK_TRY(alloc(size_t(parts) * c.cop() * k * k * c.cip() * 2, reinterpret_cast<void**>(&c.w)));
         MK_TRY(alloc(size_t(parts) * c.cop() * 4, reinterpret_cast<void**>(&c.b)));
         Slot w{Slot::CONV_W, &c, nullptr, 0, {int64_t(parts) * co, ci, k, k}};
@@ -494,7 +517,7 @@ struct mk_vae {
                 MK_TRY(conv(u.conv, p + ".upsamplers.0.resample.1", outs[i] / 2, outs[i], 3));
         }
         MK_TRY(vec(&out_g, "decoder.norm_out.gamma", b));
-        MK_TRY(conv(conv_out, "decoder.conv_out", 3, b, 3));
+        MK_TRY(conv(conv_out, "decoder.conv_out", 3, b, 3, 1, false));
         return MK_OK;
     }
 
@@ -505,6 +528,12 @@ struct mk_vae {
         switch (s.kind) {
         case Slot::CONV_W: {
             const Conv& c = *s.conv;
+            if (c.dense) {
+                const uint64_t n = uint64_t(c.cop()) * c.kp();
+                vae_pack_dense_kernel<<<blocks_for(n), 256, 0, stream>>>(static_cast<const uint16_t*>(src), c.co,
+                                                                         c.ci, kt, c.cop(), c.kp(), c.w);
+                break;
+            }
             const uint64_t n = uint64_t(c.parts) * c.cop() * c.k * c.k * c.cip();
             vae_pack_kernel<<<blocks_for(n), 256, 0, stream>>>(static_cast<const uint16_t*>(src), c.parts, c.co, c.ci,
                                                               kt, c.k * c.k, c.cop(), c.cip(), c.w);
@@ -541,6 +570,10 @@ struct mk_vae {
         a.ldy = ldo;
         a.y_dtype = MK_F32;
         a.epilogue = add ? MK_EPI_ADD : MK_EPI_STORE;
+        if (c.dense) {
+            a.c = c.ci;
+            return conv3x3_dense(&a, c.cip(), stream);
+        }
         return mk_conv3x3(&a, stream);
     }
     // 1 x 1 conv over rows (grid or compact): y[rows][ldo] (fp32 or bf16) = a[rows][cip] W^T + b (or +=)
