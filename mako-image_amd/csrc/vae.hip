@@ -175,6 +175,59 @@ __device__ inline void ms_merge(float& m, float& s, float m2, float s2)
     m = mm;
 }
 
+// The same softmax with the row held in registers (NV float4 a thread, rows up to 1024 NV): one read of the scores
+// instead of two. Out-of-row columns (n .. ld) get probability 0.
+template <int NV>
+__global__ __launch_bounds__(256) void vae_softmax1_kernel(const float* __restrict__ s, uint32_t n, uint32_t ld,
+                                                           float scale, uint16_t* __restrict__ p)
+{
+    __shared__ float red[2][4];
+    const float* sr = s + uint64_t(blockIdx.x) * ld;
+    uint16_t* pr = p + uint64_t(blockIdx.x) * ld;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    f32x4 v[NV];
+    float m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const uint32_t j = 4 * (tid + 256 * i);
+        v[i] = j < ld ? *reinterpret_cast<const f32x4*>(sr + j) : f32x4{0, 0, 0, 0};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            v[i][e] = j + e < n ? scale * v[i][e] : -INFINITY;
+            m = fmaxf(m, v[i][e]);
+        }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1)
+        m = fmaxf(m, __shfl_xor(m, o));
+    if (lane == 0)
+        red[0][wave] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
+    float sum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            v[i][e] = __expf(v[i][e] - m);
+            sum += v[i][e];
+        }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1)
+        sum += __shfl_xor(sum, o);
+    if (lane == 0)
+        red[1][wave] = sum;
+    __syncthreads();
+    const float inv = 1.0f / (red[1][0] + red[1][1] + red[1][2] + red[1][3]);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const uint32_t j = 4 * (tid + 256 * i);
+        if (j < ld)
+            *reinterpret_cast<u32x2*>(pr + j) = u32x2{pack_bf16x2(v[i][0] * inv, v[i][1] * inv),
+                                                      pack_bf16x2(v[i][2] * inv, v[i][3] * inv)};
+    }
+}
+
 __global__ __launch_bounds__(256) void vae_softmax_kernel(const float* __restrict__ s, uint32_t n, uint32_t ld,
                                                           float scale, uint16_t* __restrict__ p)
 {
@@ -717,8 +770,17 @@ struct mk_vae {
             s.c_dtype = MK_F32;
             s.epilogue = MK_EPI_STORE;
             MK_TRY(mk_gemm(&s, stream));
-            vae_softmax_kernel<<<uint32_t(m), 256, 0, stream>>>(static_cast<float*>(sb.p), uint32_t(n), uint32_t(np),
-                                                                scale, static_cast<uint16_t*>(pb.p));
+            float* sp = static_cast<float*>(sb.p);
+            uint16_t* pp = static_cast<uint16_t*>(pb.p);
+            // rows that fit the registers (up to 16384 columns) in one read, longer ones in two
+            if (np <= 1024)
+                vae_softmax1_kernel<1><<<uint32_t(m), 256, 0, stream>>>(sp, uint32_t(n), uint32_t(np), scale, pp);
+            else if (np <= 4096)
+                vae_softmax1_kernel<4><<<uint32_t(m), 256, 0, stream>>>(sp, uint32_t(n), uint32_t(np), scale, pp);
+            else if (np <= 16384)
+                vae_softmax1_kernel<16><<<uint32_t(m), 256, 0, stream>>>(sp, uint32_t(n), uint32_t(np), scale, pp);
+            else
+                vae_softmax_kernel<<<uint32_t(m), 256, 0, stream>>>(sp, uint32_t(n), uint32_t(np), scale, pp);
             MK_LAUNCH_CHECK("vae_softmax");
             mk_gemm_args o{};
             o.a = pb.p;

@@ -115,6 +115,23 @@ def test_vae_decode_matches_oracle(gpu, base, h, w):
     assert np.array_equal(vae.decode(tokens, h, w), got)
 
 
+def test_vae_mid_attention_over_256_pixels(gpu):
+    # 8 x 8 tokens: 256 pixels in the mid block, whose one-head attention (scores, softmax, P V) runs over all of them;
+    # the mid block's output against the oracle's exact softmax. (Further
+    # down, the 128 x 128 image's last layers add bf16 noise beyond this file's tolerance at its largest pixel:
+    # max-rel 2.2e-2 at rel 6.7e-3; the smaller decodes above check the whole path.)
+    ref = R.Vae(16, seed=7, mean=MEAN, std=STD)
+    vae = M.Vae(16, mean=MEAN, std=STD)
+    vae.init_random(7)
+    tokens = np.random.default_rng(88).standard_normal((64, 64)).astype(np.float32)
+    want_p, got_p = {}, {}
+    ref.decode(tokens, 8, 8, want_p)
+    vae.set_probe(got_p)
+    vae.decode(tokens, 8, 8)
+    for k in (("vae_conv_in", -1), ("vae_mid", -1)):
+        within(got_p[k], want_p[k], 64)
+
+
 def test_vae_checkpoint_with_causal_3d_convs(gpu, tmp_path):
     base, h, w = 16, 2, 2
     ref = R.Vae(base, seed=9, mean=MEAN, std=STD)
