@@ -225,29 +225,34 @@ def bench_sdxl(args):
 
 
 def cpu_baseline_sdxl(seconds_target, pass_flops):
-    """The oracle's SDXL transformer (one stage-A block, one sample, 1024 tokens) timed on this host, scaled by FLOPs
-    to the whole pass."""
+    """The oracle's SDXL transformer timed on this host on one block of each stage at its own shape (stage A: 4096
+    tokens x 640 channels; stage B: 1024 x 1280), one sample each; the pass's time at their combined FLOP rate."""
     import numpy as np
 
     import mkref as R
 
-    n_side, C = 32, 640
-    m = R.Model(R.SDXL, blocks=1, dim=C, heads=C // 64, head_dim=64, ffn=4 * C, text_dim=SDXL_CTX_DIM, seed=0)
     rng = np.random.default_rng(0)
-    x = rng.standard_normal((n_side * n_side, C)).astype(np.float32)
     ctx = rng.standard_normal((SDXL_CTX, SDXL_CTX_DIM)).astype(np.float32)
-    flops = sdxl_flops(n_side * n_side, C, 1, B=1)[0] + 2 * 2 * C * SDXL_CTX_DIM * SDXL_CTX  # + the context K / V
-    reps, t_total = 0, 0.0
+    cases = []
+    for _name, side, C, _depth in SDXL_STAGES:
+        m = R.Model(R.SDXL, blocks=1, dim=C, heads=C // 64, head_dim=64, ffn=4 * C, text_dim=SDXL_CTX_DIM, seed=0)
+        x = rng.standard_normal((side * side, C)).astype(np.float32)
+        fl = sdxl_flops(side * side, C, 1, B=1)[0] + 2 * 2 * C * SDXL_CTX_DIM * SDXL_CTX  # + the context K / V
+        cases.append((m, x, fl, side, C))
+    reps, t_total, done = 0, 0.0, 0.0
     while t_total < seconds_target and reps < 50:
-        t0 = time.perf_counter()
-        m.sdxl_trans(x, ctx)
-        t_total += time.perf_counter() - t0
+        for m, x, fl, _side, _C in cases:
+            t0 = time.perf_counter()
+            m.sdxl_trans(x, ctx)
+            t_total += time.perf_counter() - t0
+            done += fl
         reps += 1
-    rate = flops * reps / t_total
+    rate = done / t_total
+    shapes = " and ".join(f"{side * side} tokens x {C}" for _m, _x, _fl, side, C in cases)
     return {"value": pass_flops / rate, "unit": "s/pass", "cores": R.lib().mkref_threads(), "kind": "port",
-            "sample": f"oracle (C++/OpenMP, fp32 over bf16 weights): {reps} x one stage-A block of one sample at "
-                      f"{n_side * n_side} tokens ({flops / 1e9:.1f} GFLOP each, {t_total:.1f} s, "
-                      f"{rate / 1e9:.1f} GFLOP/s), scaled by FLOPs to the whole batch-2 pass"}
+            "sample": f"oracle (C++/OpenMP, fp32 over bf16 weights): {reps} x one block of each stage ({shapes}), one "
+                      f"sample ({done / reps / 1e9:.1f} GFLOP a round, {t_total:.1f} s, {rate / 1e9:.1f} GFLOP/s), "
+                      f"scaled by FLOPs to the whole batch-2 pass"}
 
 
 # Qwen-Image 2.1 as the reference runs it (qwen_image.hpp:38; its published numbers, docs/performance.md:5): 32
@@ -370,15 +375,15 @@ def bench_q21(args):
 
 
 def cpu_baseline_q21(seconds_target, step_flops_):
-    """The oracle's 2.1 graph (one block, one pass, 32 x 32 image tokens and the 256-row prompt) timed on this host,
-    scaled by FLOPs to the 32-block guided step."""
+    """The oracle's 2.1 graph (one block, one pass, at the step's own 64 x 64 image tokens and 256-row prompt: a first
+    step, text rows included) timed on this host, scaled by FLOPs to the 32-block guided step with cached text."""
     import numpy as np
 
     import mkref as R
 
     m = R.Model(R.Q21, **{**Q21_CFG, "blocks": 1}, seed=0)
     rng = np.random.default_rng(0)
-    side, S = 32, 256
+    side, S = 64, 256
     prompt = rng.standard_normal((S, Q21_CFG["text_dim"])).astype(np.float32)
     lat = rng.standard_normal((side * side, 64)).astype(np.float32)
     flops = q21_flops(True, side * side, S, blocks=1)[0] / 2
@@ -397,7 +402,7 @@ def cpu_baseline_q21(seconds_target, step_flops_):
 
 KERNEL_OF_Q21 = {"gemm.ff1": "gemm_kernel<256, 256, false, 4, 8> (SwiGLU epilogue)",
                  "gemm.ff2": "gemm_sk_kernel<256, 256, false, 2, 8>", "gemm.qkv": "gemm_kernel<256, 256, false, 3, 8>",
-                 "gemm.o": "gemm_kernel<256, 256, false, 2, 8>", "attention": "attn2_kernel<128, true, true> (f16)"}
+                 "gemm.o": "gemm_kernel<256, 256, false, 2, 8>", "attention": "attn2_kernel<128, true, true, false> (half)"}
 
 
 # The kernel each timing class of the step launches (rocprofv3's name for it), for the traffic figure.
