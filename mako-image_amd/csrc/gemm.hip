@@ -208,6 +208,47 @@ __device__ inline void epi_slice(const GemmP& p, const float* st, int ld, int to
     }
 }
 
+// The residual epilogue in two halves, so a tile's slices can overlap: rmw_load issues the loads of a slice's x rows
+// (rows past M read the last valid row), rmw_finish adds gate * (acc scale + bias) to them and stores the rows; the
+// next slice's loads go out before this slice's stores (epi_slice's lane mapping: WC / 4 lanes a row).
+template <int WC>
+__device__ inline void rmw_load(const GemmP& p, int tok0, int chw, int lane, int64_t zc, f32x4 (&x)[WC / 8])
+{
+    constexpr int LPR = WC / 4, RPI = 64 / LPR, NI = 32 / RPI;
+    const int c = lane % LPR, r0 = lane / LPR;
+    const float* cp = static_cast<const float*>(p.c) + zc + chw + 4 * c;
+#pragma unroll
+    for (int i = 0; i < NI; ++i)
+        x[i] = *reinterpret_cast<const f32x4*>(cp + int64_t(min(tok0 + r0 + RPI * i, int(p.M) - 1)) * p.ldc);
+}
+template <int WC>
+__device__ inline void rmw_finish(const GemmP& p, const float* st, int ld, int tok0, int chw, int lane, int64_t zc,
+                                  const EpiCh& k, f32x4 (&x)[WC / 8])
+{
+    constexpr int LPR = WC / 4, RPI = 64 / LPR, NI = 32 / RPI;
+    const int c = lane % LPR, r0 = lane / LPR;
+    const bool add = p.epi == MK_EPI_ADD;
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(st + (r0 + RPI * i) * ld + 4 * c);
+        const int t = tok0 + r0 + RPI * i;
+        const f32x4& g = (uint32_t(t) % p.seg_rows) < p.split ? k.g1 : k.g0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            x[i][e] += (add ? 1.0f : g[e]) * (v[e] * k.scale[e] + k.bias[e]);
+    }
+    float* c0 = static_cast<float*>(p.c) + zc + chw + 4 * c + int64_t(tok0 + r0) * p.ldc;
+    const int64_t step = int64_t(RPI) * p.ldc;
+    if (tok0 + 32 <= int(p.M)) {
+#pragma unroll
+        for (int i = 0; i < NI; ++i)
+            *reinterpret_cast<f32x4*>(c0 + i * step) = x[i];
+    } else {
+        for (int i = 0; i < NI && tok0 + r0 + RPI * i < int(p.M); ++i)
+            *reinterpret_cast<f32x4*>(c0 + i * step) = x[i];
+    }
+}
+
 // The q / k / v epilogue from a wave's staged slice: 32 tokens x 128 channels (one head of q, k or v) in LDS, row
 // stride ld floats, tokens tok0 .. tok0 + 31 (GEMM rows).
 //  - q, k: lanes along the head's channels (4 each, 32 lanes a row, rows r0 + 2i for i < 16): per-head RMSNorm * w
@@ -1026,10 +1067,23 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
         }
     } else {
         EpiCh kch = epi_channels(p, n0 + wn * WC + 4 * (lane % (WC / 4)));
+        if constexpr (EKE == EK_RMW) {
+            // the residual rows of slice s + 1 load while slice s is staged, added and stored
+            f32x4 xr[2][WC / 8];
+            rmw_load<WC>(p, m0 + wm * WM, n0 + wn * WC, lane, zc, xr[0]);
 #pragma unroll
-        for (int s = 0; s < NS; ++s) {
-            stage(s);
-            epi_slice<EKE, WC>(p, st, LDW, m0 + wm * WM + s * 32, n0 + wn * WC, lane, zc, kch);
+            for (int s = 0; s < NS; ++s) {
+                stage(s);
+                if (s + 1 < NS)
+                    rmw_load<WC>(p, m0 + wm * WM + (s + 1) * 32, n0 + wn * WC, lane, zc, xr[(s + 1) & 1]);
+                rmw_finish<WC>(p, st, LDW, m0 + wm * WM + s * 32, n0 + wn * WC, lane, zc, kch, xr[s & 1]);
+            }
+        } else {
+#pragma unroll
+            for (int s = 0; s < NS; ++s) {
+                stage(s);
+                epi_slice<EKE, WC>(p, st, LDW, m0 + wm * WM + s * 32, n0 + wn * WC, lane, zc, kch);
+            }
         }
     }
 }
