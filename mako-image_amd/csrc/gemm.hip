@@ -326,14 +326,18 @@ __device__ inline void epi_heads(const GemmP& p, const float* st, int ld, int to
             x[e] = x[e] * sc[e] + bi[e];
         return x;
     };
-    // the first half's RoPE factors go out before anything else
-    f32x4 ra[8], rb[8];
-    if (mode)
+    // the RoPE factors go out before anything else: mode 2 all 16 rows' (one f32x4 a row), mode 1 the first half's
+    // (two a row; the second half's after the first half is written)
+    f32x4 ra[16], rb[8];
+    if (mode == 2)
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+            ra[i] = rope_lo(i);
+    else if (mode == 1)
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             ra[i] = rope_lo(i);
-            if (mode == 1)
-                rb[i] = rope_hi(i);
+            rb[i] = rope_hi(i);
         }
     // per-row 1 / rms over the head: partial sums of squares, then a reduce across the row's 32 lanes
     float inv[16];
@@ -387,16 +391,15 @@ __device__ inline void epi_heads(const GemmP& p, const float* st, int ld, int to
 #pragma unroll
     for (int i = 0; i < 8; ++i)
         emit(i, ra[i], rb[i]);
-    if (mode)
+    if (mode == 1)
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             ra[i] = rope_lo(8 + i);
-            if (mode == 1)
-                rb[i] = rope_hi(8 + i);
+            rb[i] = rope_hi(8 + i);
         }
 #pragma unroll
     for (int i = 0; i < 8; ++i)
-        emit(8 + i, ra[i], rb[i]);
+        emit(8 + i, mode == 2 ? ra[8 + i] : ra[i], rb[i]);
 }
 
 // The heads epilogue for 64-dim heads (the SDXL form: no norm, no RoPE) on 128-channel tiles, whose wave slice of
