@@ -150,7 +150,7 @@ mk_status mk_gemm_set_wait_limit(uint32_t polls);
  *   y: (h + 2)(w + 2) rows of ldy values from its first grid row (a padded-grid buffer + S rows): every grid row is
  *      written (ring rows hold values the next layer must not read as pixels);
  *   epilogue MK_EPI_STORE (y = acc + bias, fp32 or bf16) or MK_EPI_ADD (y += acc + bias, fp32).
- * c and n are multiples of 64 (c <= 4096); pad channels with zeros. */
+ * c is a multiple of 64 (c <= 4096), n a multiple of 64 or 96; pad channels with zeros. */
 typedef struct mk_conv_args {
     const void* x;
     const void* w;

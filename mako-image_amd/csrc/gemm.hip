@@ -533,8 +533,9 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
     constexpr int WC = BN / 2;                  // channels per wave
     // 8-wave tiles run v_mfma_f32_16x16x32_bf16 (16 x 16 output blocks, 32-deep substeps: 3-4% faster than the
     // 32 x 32 x 16 form on the step's shapes, where the matrix cores are held by the power limit; bit-identical
-    // results), 4-wave tiles v_mfma_f32_32x32x16_bf16.
-    constexpr bool M16 = NW == 8;
+    // results), 4-wave tiles v_mfma_f32_32x32x16_bf16, except the 96-channel ones (48 channels a wave: three
+    // 16-row blocks).
+    constexpr bool M16 = NW == 8 || BN == 96;
     constexpr int MB = M16 ? 16 : 32;
     constexpr int TB = WM / MB, CB = WC / MB;   // MFMA blocks per wave along tokens / channels
     constexpr int RA = BM * 8 / NT;             // direct-load rounds for the activation tile (64 chunks per wave)
@@ -1054,7 +1055,21 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
         }
         return;
     }
-    if constexpr (WC == 96) {
+    if constexpr (WC == 48) {
+        // 96-channel tiles: the wave's 48 staged channels go out as three 16-channel slices
+        EpiCh kch[3];
+#pragma unroll
+        for (int j = 0; j < 3; ++j)
+            kch[j] = epi_channels(p, n0 + wn * WC + 16 * j + 4 * (lane % 4));
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            stage(s);
+#pragma unroll
+            for (int j = 0; j < 3; ++j)
+                epi_slice<EKE, 16>(p, st + 16 * j, LDW, m0 + wm * WM + s * 32, n0 + wn * WC + 16 * j, lane, zc,
+                                   kch[j]);
+        }
+    } else if constexpr (WC == 96) {
         // 192-channel tiles: the wave's 96 staged channels go out as three 32-channel slices
         EpiCh kch[3];
 #pragma unroll
@@ -1313,11 +1328,12 @@ int epi_kind(uint32_t e)
 }
 
 // Checks one problem's arguments and fills its kernel parameters.
-mk_status prepare(const mk_gemm_args* a, GemmP& p)
+// conv: a 3 x 3 convolution's GEMM, whose N may also be a multiple of 96 (128 x 96 tiles)
+mk_status prepare(const mk_gemm_args* a, GemmP& p, bool conv = false)
 {
     if (!a || !a->a || !a->w || (!a->c && a->epilogue != MK_EPI_HEADS))
         return fail(MK_ERR_ARG, "gemm: null argument");
-    if (a->K % 64 || a->N % 64 || a->K == 0 || a->N == 0)
+    if (a->K % 64 || (a->N % 64 && !(conv && a->N % 96 == 0)) || a->K == 0 || a->N == 0)
         return fail(MK_ERR_ARG, "gemm: K and N must be nonzero multiples of 64 (K " + std::to_string(a->K) + ", N " +
                                     std::to_string(a->N) + ")");
     if (a->w_dtype != MK_BF16 && a->w_dtype != MK_FP8_E4M3)
@@ -1399,7 +1415,8 @@ mk_status gemm_take_error()
 // k step of the tile relative to a 256 x 256 one, measured on MI355X (kt = 20-80, the SDXL and step shapes): 256 x 128
 // 0.66, 256 x 64 0.62, 128 x 128 0.67 for a pair of tiles (two workgroups share a CU: 64 KB of LDS each), so a wave of
 // 128 x 128 tiles is 2 per CU and an odd last tile costs half a pair; ties keep the larger tile. Convolutions also
-// have 256 x 192 tiles (8 waves, 0.78), for their 192- and 384-channel layers. The heads epilogue
+// have 256 x 192 tiles (8 waves, 0.78), for their 192- and 384-channel layers, and 128 x 96 tiles (4 waves on
+// 16 x 16 x 32, two workgroups a CU) for output channels that are an odd multiple of 96. The heads epilogue
 // takes 256 x 256 tiles for 128-dim heads and 128-channel tiles for 64-dim heads; fp8 weights 256-token tiles. 256 x 256 tiles use stream-K when whole waves leave at least 5% of the last wave's workgroups idle and
 // a tile is long (K of 6144 or more; measured, the partials' exchange costs about 24 k steps of a tile, more than the
 // balance saves on shorter tiles): the whole waves go round robin, the rest is split by k steps (at least 4 a
@@ -1451,6 +1468,8 @@ GemmPlan gemm_plan(const mk_gemm_args* a, uint32_t n, uint32_t cus, bool conv)
     consider(256, 128, 0.66);
     if (conv)
         consider(256, 192, 0.78);
+    if (conv && N % 64) // 96 output channels (and odd multiples of 96) take 128 x 96 tiles, nothing else
+        consider(128, 96, 0.5);
     if (narrow_ok)
         consider(256, 64, 0.62);
     if (short_ok)
@@ -1569,8 +1588,9 @@ extern "C" mk_status mk_conv3x3(const mk_conv_args* a, void* stream)
 {
     if (!a || !a->x || !a->w || !a->y)
         return fail(MK_ERR_ARG, "conv3x3: null argument");
-    if (!a->h || !a->width || a->c % 64 || !a->c || a->c > 4096 || a->n % 64 || !a->n)
-        return fail(MK_ERR_ARG, "conv3x3: needs h, w >= 1 and channels in, out nonzero multiples of 64 (in <= 4096)");
+    if (!a->h || !a->width || a->c % 64 || !a->c || a->c > 4096 || (a->n % 64 && a->n % 96) || !a->n)
+        return fail(MK_ERR_ARG, "conv3x3: needs h, w >= 1, channels in a nonzero multiple of 64 (<= 4096) and channels "
+                                "out a nonzero multiple of 64 or 96");
     if ((a->epilogue != MK_EPI_STORE && a->epilogue != MK_EPI_ADD) ||
         (a->epilogue == MK_EPI_ADD && a->y_dtype != MK_F32) || (a->y_dtype != MK_F32 && a->y_dtype != MK_BF16))
         return fail(MK_ERR_ARG, "conv3x3: epilogue STORE (fp32 or bf16) or ADD (fp32)");
@@ -1592,7 +1612,7 @@ extern "C" mk_status mk_conv3x3(const mk_conv_args* a, void* stream)
     g.c_dtype = a->y_dtype;
     g.epilogue = a->epilogue;
     GemmP p;
-    MK_TRY(prepare(&g, p));
+    MK_TRY(prepare(&g, p, true));
     p.conv_pw = uint32_t(pw);
     p.conv_tpt = a->c / 64;
     p.conv_inv = (65536u + p.conv_tpt - 1) / p.conv_tpt;
@@ -1603,6 +1623,9 @@ extern "C" mk_status mk_conv3x3(const mk_conv_args* a, void* stream)
     plan.sk = false;
     hipStream_t s = static_cast<hipStream_t>(stream);
     const bool add = a->epilogue == MK_EPI_ADD;
+    if (plan.bn == 96)
+        return add ? launch<128, 96, false, EK_RMW | EK_CONV, 4>(&p, 1, plan, s)
+                   : launch<128, 96, false, EK_STORE | EK_CONV, 4>(&p, 1, plan, s);
     if (plan.bm == 128)
         return add ? launch<128, 128, false, EK_RMW | EK_CONV, 4>(&p, 1, plan, s)
                    : launch<128, 128, false, EK_STORE | EK_CONV, 4>(&p, 1, plan, s);
@@ -1628,9 +1651,9 @@ mk_status conv3x3_dense(const mk_conv_args* a, uint32_t lda, void* stream)
     if (!a || !a->x || !a->w || !a->y)
         return fail(MK_ERR_ARG, "conv3x3_dense: null argument");
     if (!a->h || !a->width || !a->c || a->c % 8 || a->c % 64 == 0 || a->c > 512 || lda < a->c || lda % 8 ||
-        a->n % 64 || !a->n)
+        (a->n % 64 && a->n % 96) || !a->n)
         return fail(MK_ERR_ARG, "conv3x3_dense: channels in a multiple of 8 (not of 64) up to 512, lda >= c a "
-                                "multiple of 8, channels out a nonzero multiple of 64");
+                                "multiple of 8, channels out a nonzero multiple of 64 or 96");
     if ((a->epilogue != MK_EPI_STORE && a->epilogue != MK_EPI_ADD) ||
         (a->epilogue == MK_EPI_ADD && a->y_dtype != MK_F32) || (a->y_dtype != MK_F32 && a->y_dtype != MK_BF16))
         return fail(MK_ERR_ARG, "conv3x3_dense: epilogue STORE (fp32 or bf16) or ADD (fp32)");
@@ -1652,7 +1675,7 @@ mk_status conv3x3_dense(const mk_conv_args* a, uint32_t lda, void* stream)
     g.c_dtype = a->y_dtype;
     g.epilogue = a->epilogue;
     GemmP p;
-    MK_TRY(prepare(&g, p));
+    MK_TRY(prepare(&g, p, true));
     p.conv_pw = uint32_t(pw);
     p.conv_tpt = a->c / 8;
     p.conv_inv = (65536u + p.conv_tpt - 1) / p.conv_tpt;
@@ -1664,6 +1687,9 @@ mk_status conv3x3_dense(const mk_conv_args* a, uint32_t lda, void* stream)
     hipStream_t s = static_cast<hipStream_t>(stream);
     const bool add = a->epilogue == MK_EPI_ADD;
     constexpr int Q = EK_CONV | EK_CONVQ;
+    if (plan.bn == 96)
+        return add ? launch<128, 96, false, EK_RMW | Q, 4>(&p, 1, plan, s)
+                   : launch<128, 96, false, EK_STORE | Q, 4>(&p, 1, plan, s);
     if (plan.bm == 128)
         return add ? launch<128, 128, false, EK_RMW | Q, 4>(&p, 1, plan, s)
                    : launch<128, 128, false, EK_STORE | Q, 4>(&p, 1, plan, s);

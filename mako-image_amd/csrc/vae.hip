@@ -423,7 +423,8 @@ struct mk_vae {
         float* b = nullptr;
         uint32_t co = 0, ci = 0, k = 0, parts = 1;
         bool dense = false; // 3 x 3 weights packed [cop][kp] for conv3x3_dense (ci not a multiple of 64)
-        uint32_t cop() const { return cpad(co); }
+        bool narrow = false; // a 3 x 3 conv whose output channels, an odd multiple of 96, stay unpadded (128 x 96 tiles)
+        uint32_t cop() const { return narrow ? co : cpad(co); }
         uint32_t cip() const { return cpad(ci); }
         uint32_t kp() const { return (9 * ci + 63) / 64 * 64; }
     };
@@ -504,15 +505,18 @@ struct mk_vae {
         return MK_OK;
     }
 
-    // dense_ok: a 3 x 3 conv run by conv3 may take dense weights (not conv_out, whose kernel reads [3][9][cip])
+    // dense_ok: a 3 x 3 conv run by conv3 may take dense weights (not conv_out, whose kernel reads [3][9][cip]);
+    // narrow_ok: its output may keep 96 channels unpadded (not where a 1 x 1 shortcut, padded to 64, writes the same
+    // rows)
     mk_status conv(Conv& c, const std::string& name, uint32_t co, uint32_t ci, uint32_t k, uint32_t parts = 1,
-                   bool dense_ok = true)
+                   bool dense_ok = true, bool narrow_ok = true)
     {
         c.co = co;
         c.ci = ci;
         c.k = k;
         c.parts = parts;
         c.dense = dense_ok && k == 3 && parts == 1 && ci % 64 && ci % 8 == 0 && ci <= 512;
+        c.narrow = narrow_ok && dense_ok && k == 3 && parts == 1 && co % 64 && co % 96 == 0;
         MK_TRY(alloc(size_t(parts) * c.cop() * k * k * c.cip() * 2, reinterpret_cast<void**>(&c.w)));
         MK_TRY(alloc(size_t(parts) * c.cop() * 4, reinterpret_cast<void**>(&c.b)));
         Slot w{Slot::CONV_W, &c, nullptr, 0, {int64_t(parts) * co, ci, k, k}};
@@ -532,8 +536,8 @@ struct mk_vae {
         MK_TRY(vec(&r.g1, p + ".norm1.gamma", ci));
         MK_TRY(conv(r.c1, p + ".conv1", co, ci, 3));
         MK_TRY(vec(&r.g2, p + ".norm2.gamma", co));
-        MK_TRY(conv(r.c2, p + ".conv2", co, co, 3));
         r.shortcut = ci != co;
+        MK_TRY(conv(r.c2, p + ".conv2", co, co, 3, 1, true, !r.shortcut));
         if (r.shortcut)
             MK_TRY(conv(r.sc, p + ".conv_shortcut", co, ci, 1));
         return MK_OK;
@@ -693,7 +697,7 @@ struct mk_vae {
         return MK_OK;
     }
 
-    // res_block (engine.cpp:732-746): x (fp32 grid, stride cs = cpad(cout) after) <- conv2(silu(norm2(conv1(
+    // res_block (engine.cpp:732-746): x (fp32 grid, stride cs = c2.cop() after) <- conv2(silu(norm2(conv1(
     // silu(norm1(x)))))) + shortcut(x). x and the result may differ in channels; xs is x's stride.
     mk_status res_block(const Res& r, GridDims g, float*& xp, uint32_t xs, float*& yp)
     {

@@ -48,11 +48,14 @@ def from_grid(g, h, w, c):
     return np.stack([g[S + (y + 1) * (w + 2) + 1:S + (y + 1) * (w + 2) + 1 + w, :c] for y in range(h)])
 
 
-# (the 150 x 150 grids take 192-channel tiles: more than a wave of 64- or 128-channel ones)
+# (the 150 x 150 grids take 192-channel tiles: more than a wave of 64- or 128-channel ones; 96 and 288 output
+# channels take 128 x 96 tiles)
 @pytest.mark.parametrize("h, w, c, n, add", [(5, 7, 64, 64, False), (16, 16, 128, 192, False),
                                              (9, 33, 192, 64, True), (32, 40, 384, 384, True),
                                              (1, 1, 64, 128, False), (64, 3, 64, 256, False),
-                                             (150, 150, 64, 192, True), (150, 150, 64, 384, False)])
+                                             (150, 150, 64, 192, True), (150, 150, 64, 384, False),
+                                             (40, 37, 192, 96, False), (150, 150, 64, 96, True),
+                                             (5, 7, 128, 288, True), (1, 2, 64, 96, False)])
 def test_conv3x3_matches_torch(gpu, h, w, c, n, add):
     rng = np.random.default_rng(h * 1000 + w)
     x = M.bf16_bits(rng.standard_normal((h, w, c)).astype(np.float32))
@@ -86,13 +89,15 @@ def test_conv3x3_rejects_bad_shapes(gpu):
     assert M.lib().mk_conv3x3(ctypes.byref(a), None) == 1
     a = M.ConvArgs(16, 16, 0, 16, 4, 4, 64, 64, 64, M.BF16, M.EPI_ADD)  # accumulate into bf16
     assert M.lib().mk_conv3x3(ctypes.byref(a), None) == 1
+    a = M.ConvArgs(16, 16, 0, 16, 4, 4, 64, 160, 160, M.F32, M.EPI_STORE)  # 160 outputs: not of 64 or 96
+    assert M.lib().mk_conv3x3(ctypes.byref(a), None) == 1
 
 
 MEAN = np.linspace(-0.3, 0.3, 16).astype(np.float32)
 STD = np.linspace(0.5, 2.0, 16).astype(np.float32)
 
 
-# base 96 is Qwen-Image's: 384 / 192 / 96 channels (96 padded to 128, 192-wide layers on 64-wide tiles)
+# base 96 is Qwen-Image's: 384 / 192 / 96 channels (96-channel inputs dense, 96-channel outputs unpadded)
 @pytest.mark.parametrize("base, h, w", [(16, 2, 2), (16, 2, 3), (32, 4, 4), (96, 4, 4)])
 def test_vae_decode_matches_oracle(gpu, base, h, w):
     ref = R.Vae(base, seed=5, mean=MEAN, std=STD)
