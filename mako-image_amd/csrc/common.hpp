@@ -87,7 +87,9 @@ mk_status ln_modulate_group(const LnArgs* a, int count, uint32_t n, float eps, v
 mk_status fill_zero(void* p, size_t bytes, void* stream);
 // mk_conv3x3 for c (a multiple of 8, not of 64, <= 512) input channels in rows of stride lda, with dense weights
 // [n][K], K = 9 c rounded up to 64 (k = tap c + channel, zero past 9 c) (gemm.hip).
-mk_status conv3x3_dense(const mk_conv_args* a, uint32_t lda, void* stream);
+// With norm_g (96 output channels, bf16 STORE only): the output row is the RMS norm of the conv's row times norm_g,
+// then SiLU (the VAE's norm_silu), and ring rows are written as zeros, so y is the next conv's input grid.
+mk_status conv3x3_dense(const mk_conv_args* a, uint32_t lda, void* stream, const float* norm_g = nullptr);
 
 // ---- error state (thread-local, read by mk_last_error) ----
 void set_error(const std::string& msg);

@@ -52,6 +52,8 @@ struct GemmP {
     uint32_t conv_pw, conv_tpt, conv_inv;
     // gated linear unit (EK_GLU): the weights' rows are [first part F; second part F], the output [M][F]
     uint32_t glu_f;
+    // EK_NORM: the RMS norm's per-channel gain
+    const float* norm_g;
 };
 
 // One launch of up to two GEMMs of equal N, K and epilogue kind (the dual-stream blocks' image and text
@@ -90,7 +92,8 @@ __device__ inline void f8x16_to_bf16(const u32x4& v, u32x4& lo, u32x4& hi)
 
 // Epilogue kinds (template): a plain store, an activation, a read-modify-write of the fp32 residual, the q/k/v heads,
 // a gated linear unit (SwiGLU / GEGLU: each output channel from two weight rows F apart).
-enum { EK_STORE = 0, EK_ACT = 1, EK_RMW = 2, EK_HEADS = 3, EK_GLU = 4 };
+// EK_NORM: a 96-channel convolution's rows RMS-normed and SiLU-ed into the next convolution's bf16 input grid.
+enum { EK_STORE = 0, EK_ACT = 1, EK_RMW = 2, EK_HEADS = 3, EK_GLU = 4, EK_NORM = 5 };
 // Flag on the epilogue kind: the A operand is a 3 x 3 convolution's input (implicit im2col, see conv_koff).
 constexpr int EK_CONV = 8;
 // With EK_CONV: input channels not a multiple of 64 (dense K = 9 c rounded up to 64, k = tap c + channel): a k step
@@ -516,6 +519,57 @@ constexpr int fixup_groups(int qn, int cap)
     return q;
 }
 
+// EK_NORM epilogue of a wave's staged slice (32 rows x 96 channels, row stride ld floats; rows tok0 .. of the
+// padded grid, M = (h + 2) pw of them): y = silu(v rsqrt(mean(v^2) + 1e-24 / 96) g), v = the conv's value + bias,
+// as the VAE's RMS norm + SiLU (engine.cpp:725-727); ring rows zero. 8 lanes a row (4 channels of each 32-channel
+// third), 8 rows an instruction, 4 rows a lane; the row's sum of squares over its 8 lanes by xor shuffles.
+__device__ inline void epi_norm_silu(const GemmP& p, const float* st, int ld, int tok0, int lane)
+{
+    const int c = lane % 8, r0 = lane / 8;
+    f32x4 bias[3], gm[3];
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+        bias[j] = p.bias ? *reinterpret_cast<const f32x4*>(p.bias + 32 * j + 4 * c) : f32x4{0, 0, 0, 0};
+        gm[j] = *reinterpret_cast<const f32x4*>(p.norm_g + 32 * j + 4 * c);
+    }
+    const uint32_t pw = p.conv_pw, gh = p.M / pw;
+    uint16_t* y = static_cast<uint16_t*>(p.c);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int row = r0 + 8 * i, t = tok0 + row;
+        f32x4 v[3];
+        float ss = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+            v[j] = *reinterpret_cast<const f32x4*>(st + row * ld + 32 * j + 4 * c);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                v[j][e] += bias[j][e];
+                ss = fmaf(v[j][e], v[j][e], ss);
+            }
+        }
+        ss += __shfl_xor(ss, 1, 8);
+        ss += __shfl_xor(ss, 2, 8);
+        ss += __shfl_xor(ss, 4, 8);
+        const float sc = rsqrtf(ss / 96.0f + 1e-24f / 96.0f);
+        const uint32_t gy = uint32_t(t) / pw, gx = uint32_t(t) - gy * pw;
+        const bool on = gy >= 1 && gy + 1 < gh && gx >= 1 && gx + 1 < pw;
+        if (t < int(p.M)) {
+#pragma unroll
+            for (int j = 0; j < 3; ++j) {
+                float o[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float u = v[j][e] * sc * gm[j][e];
+                    o[e] = on ? u / (1.0f + __expf(-u)) : 0.0f;
+                }
+                *reinterpret_cast<u32x2*>(y + int64_t(t) * p.ldc + 32 * j + 4 * c) =
+                    u32x2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+            }
+        }
+    }
+}
+
 // One tile's k steps [kb, ke): the pipelined main loop, then either the partial published to stream-K slot
 // `publish`, or the partials of the tile's other ranges (virtual indices fix_lo .. fix_hi except `self`, tail tile
 // tt) added in index order, and the epilogue.
@@ -529,12 +583,13 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
     constexpr bool kConv = (EK & EK_CONV) != 0, kConvQ = (EK & EK_CONVQ) != 0;
     constexpr int EKE = EK & 7;                 // the epilogue kind
     constexpr int NT = 64 * NW;                 // threads
-    constexpr int WM = BM / (NW / 2);           // tokens per wave (waves: 2 along channels x NW/2 along tokens)
-    constexpr int WC = BN / 2;                  // channels per wave
+    // waves: 2 along channels x NW/2 along tokens; the 96-channel tiles 1 x NW (a wave holds whole rows)
+    constexpr int WCH = BN == 96 ? 1 : 2;
+    constexpr int WM = BM / (NW / WCH);         // tokens per wave
+    constexpr int WC = BN / WCH;                // channels per wave
     // 8-wave tiles run v_mfma_f32_16x16x32_bf16 (16 x 16 output blocks, 32-deep substeps: 3-4% faster than the
     // 32 x 32 x 16 form on the step's shapes, where the matrix cores are held by the power limit; bit-identical
-    // results), 4-wave tiles v_mfma_f32_32x32x16_bf16, except the 96-channel ones (48 channels a wave: three
-    // 16-row blocks).
+    // results), 4-wave tiles v_mfma_f32_32x32x16_bf16, except the 96-channel ones (six 16-row blocks a wave).
     constexpr bool M16 = NW == 8 || BN == 96;
     constexpr int MB = M16 ? 16 : 32;
     constexpr int TB = WM / MB, CB = WC / MB;   // MFMA blocks per wave along tokens / channels
@@ -548,7 +603,7 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
 
     // the wave index is uniform: readfirstlane keeps it (and the LDS bases of the direct loads) in scalar registers
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wn = wave & 1, wm = wave >> 1;
+    const int wn = WCH == 2 ? wave & 1 : 0, wm = WCH == 2 ? wave >> 1 : wave;
     const int m0 = int(tm) * BM, n0 = int(tn) * BN;
 
     // Direct loads: wave w's round i fills LDS chunks P = (i * NW + w) * 64 + lane of the tile; chunk P holds
@@ -1036,6 +1091,12 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
         }
         return;
     }
+    if constexpr (EKE == EK_NORM) {
+        static_assert(WC == 96 && NS == 1 && M16, "the norm epilogue takes whole 96-channel rows, one slice a wave");
+        stage(0);
+        epi_norm_silu(p, st, LDW, m0 + wm * WM, lane);
+        return;
+    }
     if constexpr (EKE == EK_HEADS) {
         // the heads epilogue is large: one copy of it in a rolled loop over the 32-token slices, which always
         // stages slice 0 of the accumulators and then rotates the next slice into its place (static register
@@ -1055,22 +1116,8 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
         }
         return;
     }
-    if constexpr (WC == 48) {
-        // 96-channel tiles: the wave's 48 staged channels go out as three 16-channel slices
-        EpiCh kch[3];
-#pragma unroll
-        for (int j = 0; j < 3; ++j)
-            kch[j] = epi_channels(p, n0 + wn * WC + 16 * j + 4 * (lane % 4));
-#pragma unroll
-        for (int s = 0; s < NS; ++s) {
-            stage(s);
-#pragma unroll
-            for (int j = 0; j < 3; ++j)
-                epi_slice<EKE, 16>(p, st + 16 * j, LDW, m0 + wm * WM + s * 32, n0 + wn * WC + 16 * j, lane, zc,
-                                   kch[j]);
-        }
-    } else if constexpr (WC == 96) {
-        // 192-channel tiles: the wave's 96 staged channels go out as three 32-channel slices
+    if constexpr (WC == 96) {
+        // 192- and 96-channel tiles: the wave's 96 staged channels go out as three 32-channel slices
         EpiCh kch[3];
 #pragma unroll
         for (int j = 0; j < 3; ++j)
@@ -1646,7 +1693,7 @@ namespace mk {
 // mk_conv3x3 for inputs whose channel count c is a multiple of 8 but not of 64 (at most 512), rows of stride lda (a
 // multiple of 8, >= c): the weight w is dense [n][K], K = 9 c rounded up to 64, k = tap c + channel for k < 9 c and
 // zero beyond, so no MFMA work goes to channel padding (the VAE's 96-channel level: K 864 -> 896 instead of 1152).
-mk_status conv3x3_dense(const mk_conv_args* a, uint32_t lda, void* stream)
+mk_status conv3x3_dense(const mk_conv_args* a, uint32_t lda, void* stream, const float* norm_g)
 {
     if (!a || !a->x || !a->w || !a->y)
         return fail(MK_ERR_ARG, "conv3x3_dense: null argument");
@@ -1657,6 +1704,8 @@ mk_status conv3x3_dense(const mk_conv_args* a, uint32_t lda, void* stream)
     if ((a->epilogue != MK_EPI_STORE && a->epilogue != MK_EPI_ADD) ||
         (a->epilogue == MK_EPI_ADD && a->y_dtype != MK_F32) || (a->y_dtype != MK_F32 && a->y_dtype != MK_BF16))
         return fail(MK_ERR_ARG, "conv3x3_dense: epilogue STORE (fp32 or bf16) or ADD (fp32)");
+    if (norm_g && (a->n != 96 || a->y_dtype != MK_BF16 || a->epilogue != MK_EPI_STORE))
+        return fail(MK_ERR_ARG, "conv3x3_dense: the norm epilogue needs 96 output channels stored as bf16");
     const uint64_t pw = uint64_t(a->width) + 2, rows = (uint64_t(a->h) + 2) * pw;
     if (rows >= (1u << 31) || (256 + 2 * pw + 2) * lda * 2 >= (uint64_t(1) << 32) || a->ldy < a->n)
         return fail(MK_ERR_ARG, "conv3x3_dense: image too large or ldy < n");
@@ -1687,6 +1736,10 @@ mk_status conv3x3_dense(const mk_conv_args* a, uint32_t lda, void* stream)
     hipStream_t s = static_cast<hipStream_t>(stream);
     const bool add = a->epilogue == MK_EPI_ADD;
     constexpr int Q = EK_CONV | EK_CONVQ;
+    if (norm_g) {
+        p.norm_g = norm_g;
+        return launch<128, 96, false, EK_NORM | Q, 4>(&p, 1, plan, s);
+    }
     if (plan.bn == 96)
         return add ? launch<128, 96, false, EK_RMW | Q, 4>(&p, 1, plan, s)
                    : launch<128, 96, false, EK_STORE | Q, 4>(&p, 1, plan, s);

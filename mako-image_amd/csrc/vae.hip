@@ -613,24 +613,30 @@ struct mk_vae {
     }
 
     // ---- the decoder ----
-    mk_status conv3(const Conv& c, const void* in, GridDims g, void* out, uint32_t ldo, bool add)
+    // lda: the input rows' stride (0: c.cip()); norm_g: the output RMS-normed (gain norm_g) and SiLU-ed into a bf16
+    // grid of ldo = 96 channels (a dense 96-channel conv only)
+    mk_status conv3(const Conv& c, const void* in, GridDims g, void* out, uint32_t ldo, bool add, uint32_t lda = 0,
+                    const float* norm_g = nullptr)
     {
         mk_conv_args a{};
         a.x = in;
         a.w = c.w;
         a.bias = c.b;
-        a.y = static_cast<float*>(out) + uint64_t(g.slack()) * ldo;
+        a.y = norm_g ? static_cast<void*>(static_cast<uint16_t*>(out) + uint64_t(g.slack()) * ldo)
+                     : static_cast<void*>(static_cast<float*>(out) + uint64_t(g.slack()) * ldo);
         a.h = g.h;
         a.width = g.w;
         a.c = c.cip();
         a.n = c.cop();
         a.ldy = ldo;
-        a.y_dtype = MK_F32;
+        a.y_dtype = norm_g ? MK_BF16 : MK_F32;
         a.epilogue = add ? MK_EPI_ADD : MK_EPI_STORE;
         if (c.dense) {
             a.c = c.ci;
-            return conv3x3_dense(&a, c.cip(), stream);
+            return conv3x3_dense(&a, lda ? lda : c.cip(), stream, norm_g);
         }
+        if (norm_g || lda)
+            return fail(MK_ERR_ARG, "vae: a fused norm or an input stride needs a dense conv");
         return mk_conv3x3(&a, stream);
     }
     // 1 x 1 conv over rows (grid or compact): y[rows][ldo] (fp32 or bf16) = a[rows][cip] W^T + b (or +=)
@@ -703,17 +709,32 @@ struct mk_vae {
     {
         const Conv &c1 = r.c1, &c2 = r.c2;
         MK_TRY(norm(xp, xs, g, c1.ci, r.g1, 0, a.p, c1.cip()));
-        MK_TRY(conv3(c1, a.p, g, t.p, c1.cop(), false));
-        MK_TRY(norm(t.p, c1.cop(), g, c1.co, r.g2, 0, a.p, c2.cip()));
+        // 96 channels (one 128 x 96 tile spans a row): conv1 writes norm2 + SiLU of its rows straight into t as the
+        // bf16 grid conv2 reads (rows of 96; its slack rows zeroed here, the ring by the epilogue)
+        const bool fused = c1.dense && c1.narrow && c1.co == 96 && c2.dense && c2.ci == 96;
+        const void* c2_in = a.p;
+        uint32_t c2_lda = 0;
+        if (fused) {
+            uint16_t* tn = static_cast<uint16_t*>(t.p);
+            const size_t slack_bytes = size_t(g.slack()) * 96 * 2;
+            MK_TRY(fill_zero(tn, slack_bytes, stream));
+            MK_TRY(fill_zero(tn + (g.slack() + g.grid_rows()) * 96, slack_bytes, stream));
+            MK_TRY(conv3(c1, a.p, g, tn, 96, false, 0, r.g2));
+            c2_in = tn;
+            c2_lda = 96;
+        } else {
+            MK_TRY(conv3(c1, a.p, g, t.p, c1.cop(), false));
+            MK_TRY(norm(t.p, c1.cop(), g, c1.co, r.g2, 0, a.p, c2.cip()));
+        }
         if (r.shortcut) {
             // y = shortcut(x) over the grid rows, then y += conv2
             MK_TRY(norm(xp, xs, g, r.sc.ci, nullptr, 2, sc.p, r.sc.cip()));
             MK_TRY(conv1(r.sc, 0, static_cast<uint16_t*>(sc.p) + uint64_t(g.slack()) * r.sc.cip(), g.grid_rows(),
                          yp + uint64_t(g.slack()) * r.sc.cop(), r.sc.cop(), MK_F32, MK_EPI_STORE));
-            MK_TRY(conv3(c2, a.p, g, yp, c2.cop(), true));
+            MK_TRY(conv3(c2, c2_in, g, yp, c2.cop(), true, c2_lda));
             std::swap(xp, yp);
         } else {
-            MK_TRY(conv3(c2, a.p, g, xp, c2.cop(), true));
+            MK_TRY(conv3(c2, c2_in, g, xp, c2.cop(), true, c2_lda));
         }
         return MK_OK;
     }
