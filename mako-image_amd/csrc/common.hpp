@@ -85,11 +85,20 @@ mk_status ln_modulate_group(const LnArgs* a, int count, uint32_t n, float eps, v
 // Zero `bytes` (a multiple of 4, 4-byte aligned) of device memory on a stream with a kernel (kernels.hip): a fill node
 // a caller's graph capture can replay, unlike a memset node.
 mk_status fill_zero(void* p, size_t bytes, void* stream);
+// A 96-output-channel conv's rows RMS-normed (mean of squares over the 96 channels, + 1e-24 / 96), times the gain g,
+// then SiLU (the VAE's norm_silu): with out NULL they are the conv's output (y bf16, STORE); otherwise y takes the
+// conv's fp32 rows (STORE or ADD) and out (bf16 rows of stride ld, from its first grid row) the normed ones. Ring rows
+// of the normed output are written as zeros, so it is the next conv's input grid (its slack rows are the caller's).
+struct ConvNorm {
+    const float* g = nullptr;
+    uint16_t* out = nullptr;
+    uint32_t ld = 0;
+};
 // mk_conv3x3 for c (a multiple of 8, not of 64, <= 512) input channels in rows of stride lda, with dense weights
-// [n][K], K = 9 c rounded up to 64 (k = tap c + channel, zero past 9 c) (gemm.hip).
-// With norm_g (96 output channels, bf16 STORE only): the output row is the RMS norm of the conv's row times norm_g,
-// then SiLU (the VAE's norm_silu), and ring rows are written as zeros, so y is the next conv's input grid.
-mk_status conv3x3_dense(const mk_conv_args* a, uint32_t lda, void* stream, const float* norm_g = nullptr);
+// [n][K], K = 9 c rounded up to 64 (k = tap c + channel, zero past 9 c); optionally a norm epilogue (gemm.hip).
+mk_status conv3x3_dense(const mk_conv_args* a, uint32_t lda, void* stream, const ConvNorm* nm = nullptr);
+// mk_conv3x3 with a norm epilogue
+mk_status conv3x3_fused(const mk_conv_args* a, const ConvNorm& nm, void* stream);
 
 // ---- error state (thread-local, read by mk_last_error) ----
 void set_error(const std::string& msg);

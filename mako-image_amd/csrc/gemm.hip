@@ -52,8 +52,10 @@ struct GemmP {
     uint32_t conv_pw, conv_tpt, conv_inv;
     // gated linear unit (EK_GLU): the weights' rows are [first part F; second part F], the output [M][F]
     uint32_t glu_f;
-    // EK_NORM: the RMS norm's per-channel gain
+    // EK_NORM / EK_RMWN: the RMS norm's per-channel gain; EK_RMWN: the normed rows' bf16 output and its row stride
     const float* norm_g;
+    uint16_t* norm_out;
+    uint32_t norm_ld;
 };
 
 // One launch of up to two GEMMs of equal N, K and epilogue kind (the dual-stream blocks' image and text
@@ -92,8 +94,9 @@ __device__ inline void f8x16_to_bf16(const u32x4& v, u32x4& lo, u32x4& hi)
 
 // Epilogue kinds (template): a plain store, an activation, a read-modify-write of the fp32 residual, the q/k/v heads,
 // a gated linear unit (SwiGLU / GEGLU: each output channel from two weight rows F apart).
-// EK_NORM: a 96-channel convolution's rows RMS-normed and SiLU-ed into the next convolution's bf16 input grid.
-enum { EK_STORE = 0, EK_ACT = 1, EK_RMW = 2, EK_HEADS = 3, EK_GLU = 4, EK_NORM = 5 };
+// EK_NORM: a 96-channel convolution's rows RMS-normed and SiLU-ed into the next convolution's bf16 input grid;
+// EK_RMWN: the rows stored (or added into the fp32 residual) and their RMS norm + SiLU written besides.
+enum { EK_STORE = 0, EK_ACT = 1, EK_RMW = 2, EK_HEADS = 3, EK_GLU = 4, EK_NORM = 5, EK_RMWN = 6 };
 // Flag on the epilogue kind: the A operand is a 3 x 3 convolution's input (implicit im2col, see conv_koff).
 constexpr int EK_CONV = 8;
 // With EK_CONV: input channels not a multiple of 64 (dense K = 9 c rounded up to 64, k = tap c + channel): a k step
@@ -519,10 +522,12 @@ constexpr int fixup_groups(int qn, int cap)
     return q;
 }
 
-// EK_NORM epilogue of a wave's staged slice (32 rows x 96 channels, row stride ld floats; rows tok0 .. of the
-// padded grid, M = (h + 2) pw of them): y = silu(v rsqrt(mean(v^2) + 1e-24 / 96) g), v = the conv's value + bias,
-// as the VAE's RMS norm + SiLU (engine.cpp:725-727); ring rows zero. 8 lanes a row (4 channels of each 32-channel
-// third), 8 rows an instruction, 4 rows a lane; the row's sum of squares over its 8 lanes by xor shuffles.
+// The norm epilogues of a wave's staged slice (32 rows x 96 channels, row stride ld floats; rows tok0 .. of the padded
+// grid, M = (h + 2) pw of them). v = the conv's value + bias; EK_NORM: y = n(v) (bf16) where n(v) = silu(v rsqrt(
+// mean(v^2) + 1e-24 / 96) g), the VAE's RMS norm + SiLU (engine.cpp:725-727); EK_RMWN: y = v or y += v (fp32) and
+// norm_out = n(y) (bf16). Normed ring rows are zero. 8 lanes a row (4 channels of each 32-channel third), 8 rows an
+// instruction, 4 rows a lane; a row's sum of squares over its 8 lanes by xor shuffles.
+template <int EKE>
 __device__ inline void epi_norm_silu(const GemmP& p, const float* st, int ld, int tok0, int lane)
 {
     const int c = lane % 8, r0 = lane / 8;
@@ -533,19 +538,29 @@ __device__ inline void epi_norm_silu(const GemmP& p, const float* st, int ld, in
         gm[j] = *reinterpret_cast<const f32x4*>(p.norm_g + 32 * j + 4 * c);
     }
     const uint32_t pw = p.conv_pw, gh = p.M / pw;
-    uint16_t* y = static_cast<uint16_t*>(p.c);
+    const bool add = EKE == EK_RMWN && p.epi == MK_EPI_ADD;
+    f32x4 v[4][3];
+    if (add) {
+        // the residual rows first, all in flight together (rows past M read the last row and are not stored)
+        const float* x = static_cast<const float*>(p.c);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 3; ++j)
+                v[i][j] = *reinterpret_cast<const f32x4*>(x + int64_t(min(tok0 + r0 + 8 * i, int(p.M) - 1)) * p.ldc +
+                                                          32 * j + 4 * c);
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int row = r0 + 8 * i, t = tok0 + row;
-        f32x4 v[3];
         float ss = 0.0f;
 #pragma unroll
         for (int j = 0; j < 3; ++j) {
-            v[j] = *reinterpret_cast<const f32x4*>(st + row * ld + 32 * j + 4 * c);
+            const f32x4 a = *reinterpret_cast<const f32x4*>(st + row * ld + 32 * j + 4 * c);
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                v[j][e] += bias[j][e];
-                ss = fmaf(v[j][e], v[j][e], ss);
+                v[i][j][e] = add ? v[i][j][e] + (a[e] + bias[j][e]) : a[e] + bias[j][e];
+                ss = fmaf(v[i][j][e], v[i][j][e], ss);
             }
         }
         ss += __shfl_xor(ss, 1, 8);
@@ -555,16 +570,19 @@ __device__ inline void epi_norm_silu(const GemmP& p, const float* st, int ld, in
         const uint32_t gy = uint32_t(t) / pw, gx = uint32_t(t) - gy * pw;
         const bool on = gy >= 1 && gy + 1 < gh && gx >= 1 && gx + 1 < pw;
         if (t < int(p.M)) {
+            uint16_t* y = EKE == EK_RMWN ? p.norm_out + int64_t(t) * p.norm_ld
+                                         : static_cast<uint16_t*>(p.c) + int64_t(t) * p.ldc;
 #pragma unroll
             for (int j = 0; j < 3; ++j) {
+                if constexpr (EKE == EK_RMWN)
+                    *reinterpret_cast<f32x4*>(static_cast<float*>(p.c) + int64_t(t) * p.ldc + 32 * j + 4 * c) = v[i][j];
                 float o[4];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const float u = v[j][e] * sc * gm[j][e];
+                    const float u = v[i][j][e] * sc * gm[j][e];
                     o[e] = on ? u / (1.0f + __expf(-u)) : 0.0f;
                 }
-                *reinterpret_cast<u32x2*>(y + int64_t(t) * p.ldc + 32 * j + 4 * c) =
-                    u32x2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+                *reinterpret_cast<u32x2*>(y + 32 * j + 4 * c) = u32x2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
             }
         }
     }
@@ -1091,10 +1109,10 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
         }
         return;
     }
-    if constexpr (EKE == EK_NORM) {
-        static_assert(WC == 96 && NS == 1 && M16, "the norm epilogue takes whole 96-channel rows, one slice a wave");
+    if constexpr (EKE == EK_NORM || EKE == EK_RMWN) {
+        static_assert(WC == 96 && NS == 1 && M16, "the norm epilogues take whole 96-channel rows, one slice a wave");
         stage(0);
-        epi_norm_silu(p, st, LDW, m0 + wm * WM, lane);
+        epi_norm_silu<EKE>(p, st, LDW, m0 + wm * WM, lane);
         return;
     }
     if constexpr (EKE == EK_HEADS) {
@@ -1627,88 +1645,37 @@ extern "C" mk_status mk_gemm_set_wait_limit(uint32_t polls)
     return MK_OK;
 }
 
+namespace mk {
 // 3 x 3 convolution as one GEMM over the padded pixel grid: output row r (grid pixel r of (h + 2) x (w + 2)) and tap
 // (dy, dx) read input row r + dy (w + 2) + dx of x, whose w + 3 slack rows before the grid make every shift
-// non-negative; K = 9 c runs tap-major, each 64-wide k step inside one tap, so the tap is a scalar offset of the
-// k step (koffA). The ring's output rows are computed like the others and are the caller's to ignore.
-extern "C" mk_status mk_conv3x3(const mk_conv_args* a, void* stream)
+// non-negative. K = 9 c runs tap-major: with c a multiple of 64 each 64-wide k step lies inside one tap, so the tap
+// is a scalar offset of the k step (koffA); with dense weights (c a multiple of 8, not of 64, K = 9 c rounded up to
+// 64, k = tap c + channel, zero past 9 c) each 16-byte chunk takes its own tap's row shift (koffq), so no MFMA work
+// goes to channel padding (the VAE's 96-channel level: K 864 -> 896 instead of 1152). The ring's output rows are
+// computed like the others and are the caller's to ignore (the norm epilogues write them as zeros).
+mk_status conv3x3_run(const mk_conv_args* a, uint32_t lda, bool dense, const ConvNorm* nm, void* stream)
 {
+    const char* who = dense ? "conv3x3_dense" : "conv3x3";
     if (!a || !a->x || !a->w || !a->y)
-        return fail(MK_ERR_ARG, "conv3x3: null argument");
-    if (!a->h || !a->width || a->c % 64 || !a->c || a->c > 4096 || (a->n % 64 && a->n % 96) || !a->n)
-        return fail(MK_ERR_ARG, "conv3x3: needs h, w >= 1, channels in a nonzero multiple of 64 (<= 4096) and channels "
-                                "out a nonzero multiple of 64 or 96");
+        return fail(MK_ERR_ARG, std::string(who) + ": null argument");
+    if (!a->h || !a->width || !a->c || (a->n % 64 && a->n % 96) || !a->n)
+        return fail(MK_ERR_ARG, std::string(who) + ": needs h, w >= 1 and channels out a nonzero multiple of 64 or 96");
+    if (dense ? (a->c % 8 || a->c % 64 == 0 || a->c > 512 || lda < a->c || lda % 8)
+              : (a->c % 64 || a->c > 4096 || lda != a->c))
+        return fail(MK_ERR_ARG, dense ? "conv3x3_dense: channels in a multiple of 8 (not of 64) up to 512, lda >= c a "
+                                        "multiple of 8"
+                                      : "conv3x3: channels in a nonzero multiple of 64 (<= 4096)");
     if ((a->epilogue != MK_EPI_STORE && a->epilogue != MK_EPI_ADD) ||
         (a->epilogue == MK_EPI_ADD && a->y_dtype != MK_F32) || (a->y_dtype != MK_F32 && a->y_dtype != MK_BF16))
-        return fail(MK_ERR_ARG, "conv3x3: epilogue STORE (fp32 or bf16) or ADD (fp32)");
-    const uint64_t pw = uint64_t(a->width) + 2, rows = (uint64_t(a->h) + 2) * pw;
-    if (rows >= (1u << 31) || (256 + 2 * pw + 2) * a->c * 2 >= (uint64_t(1) << 32) || a->ldy < a->n)
-        return fail(MK_ERR_ARG, "conv3x3: image too large or ldy < n");
-    mk_gemm_args g{};
-    g.a = a->x;
-    g.w = a->w;
-    g.bias = a->bias;
-    g.c = a->y;
-    g.M = uint32_t(rows);
-    g.N = a->n;
-    g.K = 9 * a->c;
-    g.lda = a->c;
-    g.ldc = a->ldy;
-    g.batch = 1;
-    g.w_dtype = MK_BF16;
-    g.c_dtype = a->y_dtype;
-    g.epilogue = a->epilogue;
-    GemmP p;
-    MK_TRY(prepare(&g, p, true));
-    p.conv_pw = uint32_t(pw);
-    p.conv_tpt = a->c / 64;
-    p.conv_inv = (65536u + p.conv_tpt - 1) / p.conv_tpt;
-    int cus = 0, dev = 0;
-    MK_HIP(hipGetDevice(&dev));
-    MK_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
-    GemmPlan plan = gemm_plan(&g, 1, uint32_t(cus > 0 ? cus : 1), true);
-    plan.sk = false;
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    const bool add = a->epilogue == MK_EPI_ADD;
-    if (plan.bn == 96)
-        return add ? launch<128, 96, false, EK_RMW | EK_CONV, 4>(&p, 1, plan, s)
-                   : launch<128, 96, false, EK_STORE | EK_CONV, 4>(&p, 1, plan, s);
-    if (plan.bm == 128)
-        return add ? launch<128, 128, false, EK_RMW | EK_CONV, 4>(&p, 1, plan, s)
-                   : launch<128, 128, false, EK_STORE | EK_CONV, 4>(&p, 1, plan, s);
-    if (plan.bn == 256)
-        return add ? launch<256, 256, false, EK_RMW | EK_CONV, 8>(&p, 1, plan, s)
-                   : launch<256, 256, false, EK_STORE | EK_CONV, 8>(&p, 1, plan, s);
-    if (plan.bn == 192)
-        return add ? launch<256, 192, false, EK_RMW | EK_CONV, 8>(&p, 1, plan, s)
-                   : launch<256, 192, false, EK_STORE | EK_CONV, 8>(&p, 1, plan, s);
-    if (plan.bn == 128)
-        return add ? launch<256, 128, false, EK_RMW | EK_CONV, 4>(&p, 1, plan, s)
-                   : launch<256, 128, false, EK_STORE | EK_CONV, 4>(&p, 1, plan, s);
-    return add ? launch<256, 64, false, EK_RMW | EK_CONV, 4>(&p, 1, plan, s)
-               : launch<256, 64, false, EK_STORE | EK_CONV, 4>(&p, 1, plan, s);
-}
-
-namespace mk {
-// mk_conv3x3 for inputs whose channel count c is a multiple of 8 but not of 64 (at most 512), rows of stride lda (a
-// multiple of 8, >= c): the weight w is dense [n][K], K = 9 c rounded up to 64, k = tap c + channel for k < 9 c and
-// zero beyond, so no MFMA work goes to channel padding (the VAE's 96-channel level: K 864 -> 896 instead of 1152).
-mk_status conv3x3_dense(const mk_conv_args* a, uint32_t lda, void* stream, const float* norm_g)
-{
-    if (!a || !a->x || !a->w || !a->y)
-        return fail(MK_ERR_ARG, "conv3x3_dense: null argument");
-    if (!a->h || !a->width || !a->c || a->c % 8 || a->c % 64 == 0 || a->c > 512 || lda < a->c || lda % 8 ||
-        (a->n % 64 && a->n % 96) || !a->n)
-        return fail(MK_ERR_ARG, "conv3x3_dense: channels in a multiple of 8 (not of 64) up to 512, lda >= c a "
-                                "multiple of 8, channels out a nonzero multiple of 64 or 96");
-    if ((a->epilogue != MK_EPI_STORE && a->epilogue != MK_EPI_ADD) ||
-        (a->epilogue == MK_EPI_ADD && a->y_dtype != MK_F32) || (a->y_dtype != MK_F32 && a->y_dtype != MK_BF16))
-        return fail(MK_ERR_ARG, "conv3x3_dense: epilogue STORE (fp32 or bf16) or ADD (fp32)");
-    if (norm_g && (a->n != 96 || a->y_dtype != MK_BF16 || a->epilogue != MK_EPI_STORE))
-        return fail(MK_ERR_ARG, "conv3x3_dense: the norm epilogue needs 96 output channels stored as bf16");
+        return fail(MK_ERR_ARG, std::string(who) + ": epilogue STORE (fp32 or bf16) or ADD (fp32)");
+    if (nm && (!nm->g || a->n != 96 ||
+               (nm->out ? (a->y_dtype != MK_F32 || nm->ld < 96 || nm->ld % 4)
+                        : (a->y_dtype != MK_BF16 || a->epilogue != MK_EPI_STORE))))
+        return fail(MK_ERR_ARG, std::string(who) + ": the norm epilogues need 96 output channels and a gain, and "
+                                                   "either a bf16 store or an fp32 output plus a normed one");
     const uint64_t pw = uint64_t(a->width) + 2, rows = (uint64_t(a->h) + 2) * pw;
     if (rows >= (1u << 31) || (256 + 2 * pw + 2) * lda * 2 >= (uint64_t(1) << 32) || a->ldy < a->n)
-        return fail(MK_ERR_ARG, "conv3x3_dense: image too large or ldy < n");
+        return fail(MK_ERR_ARG, std::string(who) + ": image too large or ldy < n");
     mk_gemm_args g{};
     g.a = a->x;
     g.w = a->w;
@@ -1716,7 +1683,7 @@ mk_status conv3x3_dense(const mk_conv_args* a, uint32_t lda, void* stream, const
     g.c = a->y;
     g.M = uint32_t(rows);
     g.N = a->n;
-    g.K = (9 * a->c + 63) / 64 * 64;
+    g.K = dense ? (9 * a->c + 63) / 64 * 64 : 9 * a->c;
     g.lda = lda;
     g.ldc = a->ldy;
     g.batch = 1;
@@ -1726,7 +1693,7 @@ mk_status conv3x3_dense(const mk_conv_args* a, uint32_t lda, void* stream, const
     GemmP p;
     MK_TRY(prepare(&g, p, true));
     p.conv_pw = uint32_t(pw);
-    p.conv_tpt = a->c / 8;
+    p.conv_tpt = dense ? a->c / 8 : a->c / 64;
     p.conv_inv = (65536u + p.conv_tpt - 1) / p.conv_tpt;
     int cus = 0, dev = 0;
     MK_HIP(hipGetDevice(&dev));
@@ -1735,27 +1702,66 @@ mk_status conv3x3_dense(const mk_conv_args* a, uint32_t lda, void* stream, const
     plan.sk = false;
     hipStream_t s = static_cast<hipStream_t>(stream);
     const bool add = a->epilogue == MK_EPI_ADD;
-    constexpr int Q = EK_CONV | EK_CONVQ;
-    if (norm_g) {
-        p.norm_g = norm_g;
-        return launch<128, 96, false, EK_NORM | Q, 4>(&p, 1, plan, s);
+    constexpr int C = EK_CONV, Q = EK_CONV | EK_CONVQ;
+    if (nm) {
+        p.norm_g = nm->g;
+        p.norm_out = nm->out;
+        p.norm_ld = nm->ld;
+        if (nm->out)
+            return dense ? launch<128, 96, false, EK_RMWN | Q, 4>(&p, 1, plan, s)
+                         : launch<128, 96, false, EK_RMWN | C, 4>(&p, 1, plan, s);
+        return dense ? launch<128, 96, false, EK_NORM | Q, 4>(&p, 1, plan, s)
+                     : launch<128, 96, false, EK_NORM | C, 4>(&p, 1, plan, s);
     }
-    if (plan.bn == 96)
-        return add ? launch<128, 96, false, EK_RMW | Q, 4>(&p, 1, plan, s)
-                   : launch<128, 96, false, EK_STORE | Q, 4>(&p, 1, plan, s);
-    if (plan.bm == 128)
-        return add ? launch<128, 128, false, EK_RMW | Q, 4>(&p, 1, plan, s)
-                   : launch<128, 128, false, EK_STORE | Q, 4>(&p, 1, plan, s);
-    if (plan.bn == 256)
-        return add ? launch<256, 256, false, EK_RMW | Q, 8>(&p, 1, plan, s)
-                   : launch<256, 256, false, EK_STORE | Q, 8>(&p, 1, plan, s);
-    if (plan.bn == 192)
-        return add ? launch<256, 192, false, EK_RMW | Q, 8>(&p, 1, plan, s)
-                   : launch<256, 192, false, EK_STORE | Q, 8>(&p, 1, plan, s);
-    if (plan.bn == 128)
-        return add ? launch<256, 128, false, EK_RMW | Q, 4>(&p, 1, plan, s)
-                   : launch<256, 128, false, EK_STORE | Q, 4>(&p, 1, plan, s);
-    return add ? launch<256, 64, false, EK_RMW | Q, 4>(&p, 1, plan, s)
-               : launch<256, 64, false, EK_STORE | Q, 4>(&p, 1, plan, s);
+    // (the tile shapes a convolution's plan may take, each with the implicit-GEMM flags of its K layout)
+    auto go = [&](auto f) -> mk_status {
+        if (plan.bn == 96)
+            return add ? f(std::integral_constant<int, 0>{}) : f(std::integral_constant<int, 1>{});
+        if (plan.bm == 128)
+            return add ? f(std::integral_constant<int, 2>{}) : f(std::integral_constant<int, 3>{});
+        if (plan.bn == 256)
+            return add ? f(std::integral_constant<int, 4>{}) : f(std::integral_constant<int, 5>{});
+        if (plan.bn == 192)
+            return add ? f(std::integral_constant<int, 6>{}) : f(std::integral_constant<int, 7>{});
+        if (plan.bn == 128)
+            return add ? f(std::integral_constant<int, 8>{}) : f(std::integral_constant<int, 9>{});
+        return add ? f(std::integral_constant<int, 10>{}) : f(std::integral_constant<int, 11>{});
+    };
+    auto shape = [&](auto sel, auto flags) -> mk_status {
+        constexpr int i = decltype(sel)::value, F = decltype(flags)::value;
+        constexpr int EK = (i % 2 ? EK_STORE : EK_RMW) | F;
+        if constexpr (i / 2 == 0)
+            return launch<128, 96, false, EK, 4>(&p, 1, plan, s);
+        else if constexpr (i / 2 == 1)
+            return launch<128, 128, false, EK, 4>(&p, 1, plan, s);
+        else if constexpr (i / 2 == 2)
+            return launch<256, 256, false, EK, 8>(&p, 1, plan, s);
+        else if constexpr (i / 2 == 3)
+            return launch<256, 192, false, EK, 8>(&p, 1, plan, s);
+        else if constexpr (i / 2 == 4)
+            return launch<256, 128, false, EK, 4>(&p, 1, plan, s);
+        else
+            return launch<256, 64, false, EK, 4>(&p, 1, plan, s);
+    };
+    if (dense)
+        return go([&](auto sel) { return shape(sel, std::integral_constant<int, Q>{}); });
+    return go([&](auto sel) { return shape(sel, std::integral_constant<int, C>{}); });
+}
+
+mk_status conv3x3_dense(const mk_conv_args* a, uint32_t lda, void* stream, const ConvNorm* nm)
+{
+    return conv3x3_run(a, lda, true, nm, stream);
+}
+} // namespace mk
+
+extern "C" mk_status mk_conv3x3(const mk_conv_args* a, void* stream)
+{
+    return conv3x3_run(a, a ? a->c : 0, false, nullptr, stream);
+}
+
+namespace mk {
+mk_status conv3x3_fused(const mk_conv_args* a, const ConvNorm& nm, void* stream)
+{
+    return conv3x3_run(a, a ? a->c : 0, false, &nm, stream);
 }
 } // namespace mk

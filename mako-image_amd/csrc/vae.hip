@@ -295,14 +295,15 @@ __global__ __launch_bounds__(256) void vae_compact_kernel(const float* __restric
 // takes a 16 x 16 pixel tile, stages its 18 x 18 input neighbourhood (c channels, rows padded by 8 so the 16 lanes of a
 // pixel row read distinct banks) and the 3 x 9 x c weights in LDS with whole-row loads, then each thread sums its
 // pixel's 9 taps from LDS (weights: broadcasts), bf16 pairs by v_dot2_f32_bf16 with fp32 accumulation. x: the bf16
-// grid (cs channels a row, zero ring and zero channels past the input's); c: the input's channels rounded up to 8
-// (<= cs <= 128); w: the packed weight rows [3][9][cs]; pre (may be NULL): the unclamped values into the fp32 grid
+// grid (rows of stride xs, zero ring and zero channels past the input's); c: the input's channels rounded up to 8
+// (<= xs, cs <= 128); w: the packed weight rows [3][9][cs]; pre (may be NULL): the unclamped values into the fp32 grid
 // rows (stride ps), for probes.
 constexpr int kCoTile = 16;
 struct alignas(16) Bf16Quad { // 4 bf16 pairs: one 16-byte LDS access
     bf16x2cv v[4];
 };
-__global__ __launch_bounds__(256) void vae_conv_out_kernel(const uint16_t* __restrict__ x, uint32_t cs, uint32_t c,
+__global__ __launch_bounds__(256) void vae_conv_out_kernel(const uint16_t* __restrict__ x, uint32_t xs, uint32_t cs,
+                                                           uint32_t c,
                                                            GridDims g, const uint16_t* __restrict__ w,
                                                            const float* __restrict__ bias, float* __restrict__ rgba,
                                                            float* __restrict__ pre, uint32_t ps)
@@ -324,7 +325,7 @@ __global__ __launch_bounds__(256) void vae_conv_out_kernel(const uint16_t* __res
         const uint32_t q = i / cq, k = i - q * cq, qy = q / NB, qx = q - qy * NB;
         u32x4 v = u32x4{0, 0, 0, 0};
         if (ty0 + qy <= g.h + 1 && tx0 + qx <= g.w + 1)
-            v = *reinterpret_cast<const u32x4*>(x + (g.slack() + uint64_t(ty0 + qy) * g.pw() + tx0 + qx) * cs + 8 * k);
+            v = *reinterpret_cast<const u32x4*>(x + (g.slack() + uint64_t(ty0 + qy) * g.pw() + tx0 + qx) * xs + 8 * k);
         *reinterpret_cast<u32x4*>(sx + q * pst + 8 * k) = v;
     }
     __syncthreads();
@@ -415,6 +416,13 @@ inline mk_status hip_ok(hipError_t e, const char* what) { return e == hipSuccess
 } // namespace mk
 
 using namespace mk;
+
+// A norm + SiLU that a 96-channel conv's epilogue applies to its rows: gain g, into the bf16 grid buf (rows of 96; its
+// slack rows zeroed by mk_vae::conv3)
+struct NormTo {
+    const float* g = nullptr;
+    uint16_t* buf = nullptr;
+};
 
 struct mk_vae {
     // A convolution's packed weight [parts][cop][k * k][cip] and bias [parts][cop] (fp32).
@@ -613,31 +621,50 @@ struct mk_vae {
     }
 
     // ---- the decoder ----
-    // lda: the input rows' stride (0: c.cip()); norm_g: the output RMS-normed (gain norm_g) and SiLU-ed into a bf16
-    // grid of ldo = 96 channels (a dense 96-channel conv only)
+    mk_status zero_slack(uint16_t* buf, GridDims g, uint32_t ld)
+    {
+        const size_t bytes = size_t(g.slack()) * ld * 2;
+        MK_TRY(fill_zero(buf, bytes, stream));
+        return fill_zero(buf + (g.slack() + g.grid_rows()) * ld, bytes, stream);
+    }
+    // Whether conv c's epilogue can norm its rows (96 output channels unpadded: one 128 x 96 tile spans a row).
+    static bool norm_fusable(const Conv& c) { return c.narrow && c.co == 96; }
+    // lda: the input rows' stride (0: c.cip()). only: the output is only the normed rows (bf16 grid out, ldo = 96);
+    // else, with nt.g set, out gets the conv's fp32 rows (store or add) and nt.buf their norm.
     mk_status conv3(const Conv& c, const void* in, GridDims g, void* out, uint32_t ldo, bool add, uint32_t lda = 0,
-                    const float* norm_g = nullptr)
+                    NormTo nt = {}, bool only = false)
     {
         mk_conv_args a{};
         a.x = in;
         a.w = c.w;
         a.bias = c.b;
-        a.y = norm_g ? static_cast<void*>(static_cast<uint16_t*>(out) + uint64_t(g.slack()) * ldo)
-                     : static_cast<void*>(static_cast<float*>(out) + uint64_t(g.slack()) * ldo);
+        a.y = only ? static_cast<void*>(static_cast<uint16_t*>(out) + uint64_t(g.slack()) * ldo)
+                   : static_cast<void*>(static_cast<float*>(out) + uint64_t(g.slack()) * ldo);
         a.h = g.h;
         a.width = g.w;
         a.c = c.cip();
         a.n = c.cop();
         a.ldy = ldo;
-        a.y_dtype = norm_g ? MK_BF16 : MK_F32;
+        a.y_dtype = only ? MK_BF16 : MK_F32;
         a.epilogue = add ? MK_EPI_ADD : MK_EPI_STORE;
+        ConvNorm nm;
+        if (nt.g) {
+            if (!norm_fusable(c))
+                return fail(MK_ERR_ARG, "vae: a fused norm needs a conv with 96 unpadded output channels");
+            MK_TRY(zero_slack(only ? static_cast<uint16_t*>(out) : nt.buf, g, 96));
+            nm.g = nt.g;
+            if (!only) {
+                nm.out = nt.buf + uint64_t(g.slack()) * 96;
+                nm.ld = 96;
+            }
+        }
         if (c.dense) {
             a.c = c.ci;
-            return conv3x3_dense(&a, lda ? lda : c.cip(), stream, norm_g);
+            return conv3x3_dense(&a, lda ? lda : c.cip(), stream, nt.g ? &nm : nullptr);
         }
-        if (norm_g || lda)
-            return fail(MK_ERR_ARG, "vae: a fused norm or an input stride needs a dense conv");
-        return mk_conv3x3(&a, stream);
+        if (lda)
+            return fail(MK_ERR_ARG, "vae: an input stride needs a dense conv");
+        return nt.g ? conv3x3_fused(&a, nm, stream) : mk_conv3x3(&a, stream);
     }
     // 1 x 1 conv over rows (grid or compact): y[rows][ldo] (fp32 or bf16) = a[rows][cip] W^T + b (or +=)
     mk_status conv1(const Conv& c, uint32_t part, const void* a, uint64_t rows, void* out, uint32_t ldo,
@@ -704,26 +731,31 @@ struct mk_vae {
     }
 
     // res_block (engine.cpp:732-746): x (fp32 grid, stride cs = c2.cop() after) <- conv2(silu(norm2(conv1(
-    // silu(norm1(x)))))) + shortcut(x). x and the result may differ in channels; xs is x's stride.
-    mk_status res_block(const Res& r, GridDims g, float*& xp, uint32_t xs, float*& yp)
+    // silu(norm1(x)))))) + shortcut(x). x and the result may differ in channels; xs is x's stride. At 96 channels the
+    // norms come from the convs' epilogues: normed_in (rows of 96) already holds silu(norm1(x)), conv1 writes
+    // silu(norm2(.)) straight into t as conv2's bf16 input, and with next.g conv2 also writes the norm the next layer
+    // takes of the result into next.buf (which conv2 does not read).
+    mk_status res_block(const Res& r, GridDims g, float*& xp, uint32_t xs, float*& yp, const uint16_t* normed_in = nullptr,
+                        NormTo next = {})
     {
         const Conv &c1 = r.c1, &c2 = r.c2;
-        MK_TRY(norm(xp, xs, g, c1.ci, r.g1, 0, a.p, c1.cip()));
-        // 96 channels (one 128 x 96 tile spans a row): conv1 writes norm2 + SiLU of its rows straight into t as the
-        // bf16 grid conv2 reads (rows of 96; its slack rows zeroed here, the ring by the epilogue)
-        const bool fused = c1.dense && c1.narrow && c1.co == 96 && c2.dense && c2.ci == 96;
+        const void* c1_in = a.p;
+        uint32_t c1_lda = 0;
+        if (normed_in) {
+            c1_in = normed_in;
+            c1_lda = 96;
+        } else {
+            MK_TRY(norm(xp, xs, g, c1.ci, r.g1, 0, a.p, c1.cip()));
+        }
         const void* c2_in = a.p;
         uint32_t c2_lda = 0;
-        if (fused) {
+        if (norm_fusable(c1) && c2.dense && c2.ci == 96) {
             uint16_t* tn = static_cast<uint16_t*>(t.p);
-            const size_t slack_bytes = size_t(g.slack()) * 96 * 2;
-            MK_TRY(fill_zero(tn, slack_bytes, stream));
-            MK_TRY(fill_zero(tn + (g.slack() + g.grid_rows()) * 96, slack_bytes, stream));
-            MK_TRY(conv3(c1, a.p, g, tn, 96, false, 0, r.g2));
+            MK_TRY(conv3(c1, c1_in, g, tn, 96, false, c1_lda, NormTo{r.g2, nullptr}, true));
             c2_in = tn;
             c2_lda = 96;
         } else {
-            MK_TRY(conv3(c1, a.p, g, t.p, c1.cop(), false));
+            MK_TRY(conv3(c1, c1_in, g, t.p, c1.cop(), false, c1_lda));
             MK_TRY(norm(t.p, c1.cop(), g, c1.co, r.g2, 0, a.p, c2.cip()));
         }
         if (r.shortcut) {
@@ -731,10 +763,10 @@ struct mk_vae {
             MK_TRY(norm(xp, xs, g, r.sc.ci, nullptr, 2, sc.p, r.sc.cip()));
             MK_TRY(conv1(r.sc, 0, static_cast<uint16_t*>(sc.p) + uint64_t(g.slack()) * r.sc.cip(), g.grid_rows(),
                          yp + uint64_t(g.slack()) * r.sc.cop(), r.sc.cop(), MK_F32, MK_EPI_STORE));
-            MK_TRY(conv3(c2, c2_in, g, yp, c2.cop(), true, c2_lda));
+            MK_TRY(conv3(c2, c2_in, g, yp, c2.cop(), true, c2_lda, next));
             std::swap(xp, yp);
         } else {
-            MK_TRY(conv3(c2, c2_in, g, xp, c2.cop(), true, c2_lda));
+            MK_TRY(conv3(c2, c2_in, g, xp, c2.cop(), true, c2_lda, next));
         }
         return MK_OK;
     }
@@ -862,32 +894,53 @@ struct mk_vae {
         MK_TRY(res_block(mid1, g, xp, cpad(d0), yp));
         MK_TRY(probe_grid("vae_mid", -1, xp, cpad(d0), g, d0));
         uint32_t cs = cpad(d0);
+        // At 96 channels each conv that produces x also writes the norm + SiLU its consumer takes of x (the next res
+        // block's norm1, or norm_out before conv_out): `normed` is that grid (rows of 96) when the last conv wrote it.
+        // A res block's conv2 writes it into a (conv2 reads t), the upsampling conv into sc (it reads a).
+        auto takes_normed = [](const Res& r) { return r.c1.dense && r.c1.ci == 96; };
+        uint16_t* const na = static_cast<uint16_t*>(a.p);
+        uint16_t* const ns = static_cast<uint16_t*>(sc.p);
+        const uint16_t* normed = nullptr;
         for (int i = 0; i < 4; ++i) {
             Up& u = ups[i];
             for (int j = 0; j < 3; ++j) {
-                MK_TRY(res_block(u.res[j], g, xp, cs, yp));
-                cs = u.res[j].c2.cop();
+                const Res& r = u.res[j];
+                NormTo next{};
+                if (norm_fusable(r.c2) && !r.shortcut) {
+                    if (j < 2 && takes_normed(u.res[j + 1]))
+                        next = NormTo{u.res[j + 1].g1, na};
+                    else if (j == 2 && i == 3 && conv_out.ci == 96)
+                        next = NormTo{out_g, na};
+                }
+                MK_TRY(res_block(r, g, xp, cs, yp, normed, next));
+                normed = next.g ? next.buf : nullptr;
+                cs = r.c2.cop();
             }
             if (u.up) {
                 const GridDims g2{2 * g.h, 2 * g.w};
                 vae_up_kernel<<<blocks_for(g2.rows() * u.conv.cip() / 4), 256, 0, stream>>>(
-                    xp, cs, g, u.cout, g2, u.conv.cip(), static_cast<uint16_t*>(a.p));
+                    xp, cs, g, u.cout, g2, u.conv.cip(), na);
                 MK_LAUNCH_CHECK("vae_up");
-                MK_TRY(conv3(u.conv, a.p, g2, yp, u.conv.cop(), false));
+                NormTo next{};
+                if (norm_fusable(u.conv) && i + 1 < 4 && takes_normed(ups[i + 1].res[0]))
+                    next = NormTo{ups[i + 1].res[0].g1, ns};
+                MK_TRY(conv3(u.conv, na, g2, yp, u.conv.cop(), false, 0, next));
+                normed = next.g ? next.buf : nullptr;
                 std::swap(xp, yp);
                 g = g2;
                 cs = u.conv.cop();
             }
             MK_TRY(probe_grid("vae_up", i, xp, cs, g, u.up ? u.conv.co : u.cout));
         }
-        MK_TRY(norm(xp, cs, g, b, out_g, 0, a.p, conv_out.cip()));
+        if (!normed)
+            MK_TRY(norm(xp, cs, g, b, out_g, 0, na, conv_out.cip()));
         // (base <= 128: conv_out's input takes at most 128 padded channels)
         const dim3 cog((g.w + kCoTile - 1) / kCoTile, (g.h + kCoTile - 1) / kCoTile);
         const uint32_t c8 = (conv_out.ci + 7) / 8 * 8;
         const size_t lds = size_t(kCoTile + 2) * (kCoTile + 2) * (c8 + 8) * 2;
-        vae_conv_out_kernel<<<cog, 256, lds, stream>>>(static_cast<const uint16_t*>(a.p), conv_out.cip(), c8, g,
-                                                       conv_out.w, conv_out.b, out,
-            probe ? yp : nullptr, conv_out.cop());
+        vae_conv_out_kernel<<<cog, 256, lds, stream>>>(normed ? normed : na, normed ? 96 : conv_out.cip(),
+                                                       conv_out.cip(), c8, g, conv_out.w, conv_out.b, out,
+                                                       probe ? yp : nullptr, conv_out.cop());
         MK_LAUNCH_CHECK("vae_conv_out");
         MK_TRY(probe_grid("vae_out", -1, yp, conv_out.cop(), g, 3));
         return MK_OK;
