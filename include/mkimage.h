@@ -147,8 +147,8 @@ mk_status mk_gemm_set_wait_limit(uint32_t polls);
  * holds pixel (y, x), S = w + 3, each row c channels.
  *   x: bf16 padded grid, c channels (ring and slack rows zero);
  *   w: bf16 [n][9][c], tap = 3 dy + dx (the PyTorch weight [n][c][3][3] with its taps moved in front of c);
- *   y: (h + 2)(w + 2) rows of ldy values from its first grid row (a padded-grid buffer + S rows): every grid row is
- *      written (ring rows hold values the next layer must not read as pixels);
+ *   y: (h + 2)(w + 2) rows of ldy values from its first grid row (a padded-grid buffer + S rows): the pixel rows are
+ *      written; ring rows are left as they were or hold values the next layer must not read as pixels;
  *   epilogue MK_EPI_STORE (y = acc + bias, fp32 or bf16) or MK_EPI_ADD (y += acc + bias, fp32).
  * c is a multiple of 64 (c <= 4096), n a multiple of 64 or 96; pad channels with zeros. */
 typedef struct mk_conv_args {

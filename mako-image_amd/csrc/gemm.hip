@@ -50,6 +50,10 @@ struct GemmP {
     // 3 x 3 convolution (EK_CONV): the padded grid's row width w + 2, k tiles a tap (channels / 64), and
     // ceil(2^16 / conv_tpt) for the tap index by multiply-shift; with EK_CONVQ conv_tpt counts 8-channel chunks
     uint32_t conv_pw, conv_tpt, conv_inv;
+    // With conv_w (the image width, a multiple of BM) the tiles cover the conv_pix = h w pixels only, BM of one image
+    // row each (tile tm: pixel tm BM, grid row (y + 1) pw + x + 1), so no tile is spent on ring rows and the launch
+    // holds whole rounds where h w does; the ring's output rows are then not written.
+    uint32_t conv_w, conv_pix;
     // gated linear unit (EK_GLU): the weights' rows are [first part F; second part F], the output [M][F]
     uint32_t glu_f;
     // EK_NORM / EK_RMWN: the RMS norm's per-channel gain; EK_RMWN: the normed rows' bf16 output and its row stride
@@ -622,7 +626,14 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
     // the wave index is uniform: readfirstlane keeps it (and the LDS bases of the direct loads) in scalar registers
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wn = WCH == 2 ? wave & 1 : 0, wm = WCH == 2 ? wave >> 1 : wave;
-    const int m0 = int(tm) * BM, n0 = int(tn) * BN;
+    int m0 = int(tm) * BM;
+    if constexpr (kConv) {
+        if (p.conv_w) {
+            const int y = m0 / int(p.conv_w), x = m0 - y * int(p.conv_w);
+            m0 = (y + 1) * int(p.conv_pw) + x + 1;
+        }
+    }
+    const int n0 = int(tn) * BN;
 
     // Direct loads: wave w's round i fills LDS chunks P = (i * NW + w) * 64 + lane of the tile; chunk P holds
     // row P / 8 and logical k-chunk swz_chunk(row, P % 8), so the lane loads that one. Buffer loads: the resource
@@ -1333,7 +1344,7 @@ mk_status launch(GemmP* p, uint32_t count, const GemmPlan& plan, hipStream_t s)
     GemmG G{};
     uint32_t tiles = 0;
     for (uint32_t i = 0; i < count; ++i) {
-        p[i].tiles_m = cdiv(p[i].M, BM);
+        p[i].tiles_m = p[i].conv_w ? p[i].conv_pix / BM : cdiv(p[i].M, BM);
         p[i].tiles_n = p[i].N / BN;
         G.g[i] = p[i];
         tiles += p[i].tiles_m * p[i].tiles_n * p[i].batch;
@@ -1698,7 +1709,16 @@ mk_status conv3x3_run(const mk_conv_args* a, uint32_t lda, bool dense, const Con
     int cus = 0, dev = 0;
     MK_HIP(hipGetDevice(&dev));
     MK_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
-    GemmPlan plan = gemm_plan(&g, 1, uint32_t(cus > 0 ? cus : 1), true);
+    // tiles over the pixels when the plan for h w rows has a tile height dividing w, else over the padded rows
+    mk_gemm_args gp = g;
+    gp.M = a->h * a->width;
+    GemmPlan plan = gemm_plan(&gp, 1, uint32_t(cus > 0 ? cus : 1), true);
+    if (a->width % plan.bm == 0) {
+        p.conv_w = a->width;
+        p.conv_pix = gp.M;
+    } else {
+        plan = gemm_plan(&g, 1, uint32_t(cus > 0 ? cus : 1), true);
+    }
     plan.sk = false;
     hipStream_t s = static_cast<hipStream_t>(stream);
     const bool add = a->epilogue == MK_EPI_ADD;

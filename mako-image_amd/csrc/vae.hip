@@ -149,6 +149,28 @@ __global__ __launch_bounds__(256) void vae_norm_kernel(const float* __restrict__
     }
 }
 
+// Zeroes the rows of a bf16 padded grid (ld channels a row, a multiple of 8) that hold no pixel: the slack rows, the
+// top and bottom ring rows and each image row's two ring pixels, 2 (w + 3) + 2 (w + 2) + 2 h rows in all. One thread a
+// (row, 8 channels).
+__global__ __launch_bounds__(256) void vae_ring_zero_kernel(uint16_t* __restrict__ y, GridDims g, uint32_t ld)
+{
+    const uint32_t q = ld / 8, i = blockIdx.x * 256 + threadIdx.x;
+    const uint32_t edge = g.slack() + g.pw(), n = 2 * edge + 2 * g.h; // rows
+    if (i >= n * q)
+        return;
+    const uint32_t k = i / q, j = i - k * q;
+    uint64_t r;
+    if (k < edge) // slack before, top ring row
+        r = k;
+    else if (k < 2 * edge) // bottom ring row, slack after
+        r = g.rows() - 2 * edge + k;
+    else { // image row y's left or right ring pixel
+        const uint32_t y = (k - 2 * edge) / 2, right = (k - 2 * edge) % 2;
+        r = g.slack() + uint64_t(y + 1) * g.pw() + (right ? g.pw() - 1 : 0);
+    }
+    *reinterpret_cast<u32x4*>(y + r * ld + 8 * j) = u32x4{0, 0, 0, 0};
+}
+
 // Nearest 2x: the bf16 padded grid of the 2h x 2w image (cp channels) from the fp32 grid of the h x w one (c
 // channels, a multiple of 4, stride cs). One thread a (output row, 4 channels); 32-bit indexing.
 __global__ __launch_bounds__(256) void vae_up_kernel(const float* __restrict__ x, uint32_t cs, GridDims gi,
@@ -418,7 +440,7 @@ inline mk_status hip_ok(hipError_t e, const char* what) { return e == hipSuccess
 using namespace mk;
 
 // A norm + SiLU that a 96-channel conv's epilogue applies to its rows: gain g, into the bf16 grid buf (rows of 96; its
-// slack rows zeroed by mk_vae::conv3)
+// slack and ring rows zeroed by mk_vae::conv3)
 struct NormTo {
     const float* g = nullptr;
     uint16_t* buf = nullptr;
@@ -621,11 +643,13 @@ struct mk_vae {
     }
 
     // ---- the decoder ----
-    mk_status zero_slack(uint16_t* buf, GridDims g, uint32_t ld)
+    // the rows of a bf16 grid that hold no pixel (a conv whose tiles cover pixels only leaves them unwritten)
+    mk_status zero_ring(uint16_t* buf, GridDims g, uint32_t ld)
     {
-        const size_t bytes = size_t(g.slack()) * ld * 2;
-        MK_TRY(fill_zero(buf, bytes, stream));
-        return fill_zero(buf + (g.slack() + g.grid_rows()) * ld, bytes, stream);
+        const uint64_t n = (2ull * (g.slack() + g.pw()) + 2ull * g.h) * (ld / 8);
+        vae_ring_zero_kernel<<<blocks_for(n), 256, 0, stream>>>(buf, g, ld);
+        MK_LAUNCH_CHECK("vae_ring_zero");
+        return MK_OK;
     }
     // Whether conv c's epilogue can norm its rows (96 output channels unpadded: one 128 x 96 tile spans a row).
     static bool norm_fusable(const Conv& c) { return c.narrow && c.co == 96; }
@@ -651,7 +675,7 @@ struct mk_vae {
         if (nt.g) {
             if (!norm_fusable(c))
                 return fail(MK_ERR_ARG, "vae: a fused norm needs a conv with 96 unpadded output channels");
-            MK_TRY(zero_slack(only ? static_cast<uint16_t*>(out) : nt.buf, g, 96));
+            MK_TRY(zero_ring(only ? static_cast<uint16_t*>(out) : nt.buf, g, 96));
             nm.g = nt.g;
             if (!only) {
                 nm.out = nt.buf + uint64_t(g.slack()) * 96;
