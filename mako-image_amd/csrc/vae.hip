@@ -830,10 +830,11 @@ struct mk_vae {
             v.epilogue = MK_EPI_STORE;
             MK_TRY(mk_gemm(&v, stream));
         }
-        // queries in chunks whose scores stay near 1 GiB
-        const uint64_t qc = std::min<uint64_t>(n, std::max<uint64_t>(256, (uint64_t(1) << 28) / np / 256 * 256));
+        // Queries in chunks whose fp32 scores (near 128 MB) stay in the memory-side cache between the score GEMM that
+        // writes them and the softmax that reads them; P (bf16) for all queries, then one P V product.
+        const uint64_t qc = std::min<uint64_t>(n, std::max<uint64_t>(256, (uint64_t(1) << 25) / np / 256 * 256));
         MK_TRY(ensure(sb, qc * np * 4));
-        MK_TRY(ensure(pb, qc * np * 2));
+        MK_TRY(ensure(pb, n * np * 2));
         const float scale = 1.0f / std::sqrt(float(c));
         for (uint64_t q0 = 0; q0 < n; q0 += qc) {
             const uint64_t m = std::min(qc, n - q0);
@@ -852,7 +853,7 @@ struct mk_vae {
             s.epilogue = MK_EPI_STORE;
             MK_TRY(mk_gemm(&s, stream));
             float* sp = static_cast<float*>(sb.p);
-            uint16_t* pp = static_cast<uint16_t*>(pb.p);
+            uint16_t* pp = static_cast<uint16_t*>(pb.p) + q0 * np;
             // rows that fit the registers (up to 16384 columns) in one read, longer ones in two
             if (np <= 1024)
                 vae_softmax1_kernel<1><<<uint32_t(m), 256, 0, stream>>>(sp, uint32_t(n), uint32_t(np), scale, pp);
@@ -863,12 +864,14 @@ struct mk_vae {
             else
                 vae_softmax_kernel<<<uint32_t(m), 256, 0, stream>>>(sp, uint32_t(n), uint32_t(np), scale, pp);
             MK_LAUNCH_CHECK("vae_softmax");
+        }
+        {
             mk_gemm_args o{};
             o.a = pb.p;
             o.w = vtb.p;
             o.bias = qkv.b + size_t(2) * cp;
-            o.c = static_cast<uint16_t*>(ob.p) + q0 * cp;
-            o.M = uint32_t(m);
+            o.c = ob.p;
+            o.M = uint32_t(n);
             o.N = cp;
             o.K = uint32_t(np);
             o.lda = int64_t(np);
