@@ -230,7 +230,15 @@ __device__ inline float wave_max(float v)
 {
     return wave_reduce(v, [](float a, float b) { return fmaxf(a, b); });
 }
+// sum over each 8 consecutive lanes: the two quad permutations, then the half-row mirror (lane i <-> 7 - i)
+__device__ inline float oct_sum(float v)
+{
+    v += dpp_f<0xB1>(v);
+    v += dpp_f<0x4E>(v);
+    return v + dpp_f<0x141>(v);
+}
 #else
+__device__ inline float oct_sum(float v) { return v; }
 __device__ inline float wave_sum(float v) { return v; }
 __device__ inline float half_sum(float v) { return v; }
 __device__ inline float wave_max(float v) { return v; }

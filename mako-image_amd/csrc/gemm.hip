@@ -567,26 +567,34 @@ __device__ inline void epi_norm_silu(const GemmP& p, const float* st, int ld, in
                 ss = fmaf(v[i][j][e], v[i][j][e], ss);
             }
         }
-        ss += __shfl_xor(ss, 1, 8);
-        ss += __shfl_xor(ss, 2, 8);
-        ss += __shfl_xor(ss, 4, 8);
-        const float sc = rsqrtf(ss / 96.0f + 1e-24f / 96.0f);
-        const uint32_t gy = uint32_t(t) / pw, gx = uint32_t(t) - gy * pw;
-        const bool on = gy >= 1 && gy + 1 < gh && gx >= 1 && gx + 1 < pw;
+        // (v_rsq_f32: ss is a sum of squares plus 1e-24, never a denormal)
+        const float sc = __builtin_amdgcn_rsqf(oct_sum(ss) * (1.0f / 96.0f) + 1e-24f / 96.0f);
+        // (tiles over the pixels hold pixel rows only; else the row's ring test, an integer division). Ring rows are
+        // zeroed by a mask on the bits, so a ring value that is not finite still comes out 0.
+        uint32_t keep = ~0u;
+        if (!p.conv_w) {
+            const uint32_t gy = uint32_t(t) / pw, gx = uint32_t(t) - gy * pw;
+            keep = gy >= 1 && gy + 1 < gh && gx >= 1 && gx + 1 < pw ? ~0u : 0u;
+        }
+        uint32_t o[3][2];
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+            float u[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                u[e] = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, silu_f(v[i][j][e] * sc * gm[j][e])) & keep);
+            o[j][0] = pack_bf16x2(u[0], u[1]);
+            o[j][1] = pack_bf16x2(u[2], u[3]);
+        }
         if (t < int(p.M)) {
-            uint16_t* y = EKE == EK_RMWN ? p.norm_out + int64_t(t) * p.norm_ld
-                                         : static_cast<uint16_t*>(p.c) + int64_t(t) * p.ldc;
+            uint16_t* y = EKE == EK_RMWN ? p.norm_out + int64_t(t) * p.norm_ld + 4 * c
+                                         : static_cast<uint16_t*>(p.c) + int64_t(t) * p.ldc + 4 * c;
+            float* x = static_cast<float*>(p.c) + int64_t(t) * p.ldc + 4 * c;
 #pragma unroll
             for (int j = 0; j < 3; ++j) {
                 if constexpr (EKE == EK_RMWN)
-                    *reinterpret_cast<f32x4*>(static_cast<float*>(p.c) + int64_t(t) * p.ldc + 32 * j + 4 * c) = v[i][j];
-                float o[4];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float u = v[i][j][e] * sc * gm[j][e];
-                    o[e] = on ? u / (1.0f + __expf(-u)) : 0.0f;
-                }
-                *reinterpret_cast<u32x2*>(y + 32 * j + 4 * c) = u32x2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+                    *reinterpret_cast<f32x4*>(x + 32 * j) = v[i][j];
+                *reinterpret_cast<u32x2*>(y + 32 * j) = u32x2{o[j][0], o[j][1]};
             }
         }
     }
