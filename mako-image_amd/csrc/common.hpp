@@ -85,7 +85,7 @@ mk_status ln_modulate_group(const LnArgs* a, int count, uint32_t n, float eps, v
 // Zero `bytes` (a multiple of 4, 4-byte aligned) of device memory on a stream with a kernel (kernels.hip): a fill node
 // a caller's graph capture can replay, unlike a memset node.
 mk_status fill_zero(void* p, size_t bytes, void* stream);
-// A 96-output-channel conv's rows RMS-normed (mean of squares over the 96 channels, + 1e-24 / 96), times the gain g,
+// A 96- or 192-output-channel conv's rows RMS-normed (mean of squares over the C channels, + 1e-24 / C), times the gain g,
 // then SiLU (the VAE's norm_silu): with out NULL they are the conv's output (y bf16, STORE); otherwise y takes the
 // conv's fp32 rows (STORE or ADD) and out (bf16 rows of stride ld, from its first grid row) the normed ones. Ring rows
 // of the normed output are written as zeros, so it is the next conv's input grid (its slack rows are the caller's).

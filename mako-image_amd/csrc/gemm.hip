@@ -526,27 +526,31 @@ constexpr int fixup_groups(int qn, int cap)
     return q;
 }
 
-// The norm epilogues of a wave's staged slice (32 rows x 96 channels, row stride ld floats; rows tok0 .. of the padded
-// grid, M = (h + 2) pw of them). v = the conv's value + bias; EK_NORM: y = n(v) (bf16) where n(v) = silu(v rsqrt(
-// mean(v^2) + 1e-24 / 96) g), the VAE's RMS norm + SiLU (engine.cpp:725-727); EK_RMWN: y = v or y += v (fp32) and
-// norm_out = n(y) (bf16). Normed ring rows are zero. 8 lanes a row (4 channels of each 32-channel third), 8 rows an
-// instruction, 4 rows a lane; a row's sum of squares over its 8 lanes by xor shuffles.
-template <int EKE>
-__device__ inline void epi_norm_silu(const GemmP& p, const float* st, int ld, int tok0, int lane)
+// The norm epilogues of a wave's staged slice (32 rows x 96 channels from chw, row stride ld floats; rows tok0 .. of
+// the padded grid, M = (h + 2) pw of them). v = the conv's value + bias; EK_NORM: y = n(v) (bf16) where n(v) =
+// silu(v rsqrt(mean(v^2) + 1e-24 / C) g) over the row's C channels, the VAE's RMS norm + SiLU (engine.cpp:725-727);
+// EK_RMWN: y = v or y += v (fp32) and norm_out = n(y) (bf16). Normed ring rows are zero. 8 lanes a row (4 channels of
+// each 32-channel third), 8 rows an instruction, 4 rows a lane; a row's sum of squares over its 8 lanes by DPP. With
+// C = 192 (PAIR) the row's other 96 channels are the partner wave's (wave ^ 1): the partial sums meet in xch (32
+// floats a wave) across one barrier that waits for LDS operations only, not for the stores in flight.
+template <int EKE, bool PAIR>
+__device__ inline void epi_norm_silu(const GemmP& p, const float* st, int ld, int tok0, int chw, int lane, float* xch,
+                                     int wave)
 {
+    constexpr float kInvC = PAIR ? 1.0f / 192.0f : 1.0f / 96.0f;
     const int c = lane % 8, r0 = lane / 8;
     f32x4 bias[3], gm[3];
 #pragma unroll
     for (int j = 0; j < 3; ++j) {
-        bias[j] = p.bias ? *reinterpret_cast<const f32x4*>(p.bias + 32 * j + 4 * c) : f32x4{0, 0, 0, 0};
-        gm[j] = *reinterpret_cast<const f32x4*>(p.norm_g + 32 * j + 4 * c);
+        bias[j] = p.bias ? *reinterpret_cast<const f32x4*>(p.bias + chw + 32 * j + 4 * c) : f32x4{0, 0, 0, 0};
+        gm[j] = *reinterpret_cast<const f32x4*>(p.norm_g + chw + 32 * j + 4 * c);
     }
     const uint32_t pw = p.conv_pw, gh = p.M / pw;
     const bool add = EKE == EK_RMWN && p.epi == MK_EPI_ADD;
     f32x4 v[4][3];
     if (add) {
         // the residual rows first, all in flight together (rows past M read the last row and are not stored)
-        const float* x = static_cast<const float*>(p.c);
+        const float* x = static_cast<const float*>(p.c) + chw;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -554,21 +558,40 @@ __device__ inline void epi_norm_silu(const GemmP& p, const float* st, int ld, in
                 v[i][j] = *reinterpret_cast<const f32x4*>(x + int64_t(min(tok0 + r0 + 8 * i, int(p.M) - 1)) * p.ldc +
                                                           32 * j + 4 * c);
     }
+    float ss[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const int row = r0 + 8 * i, t = tok0 + row;
-        float ss = 0.0f;
+        const int row = r0 + 8 * i;
+        ss[i] = 0.0f;
 #pragma unroll
         for (int j = 0; j < 3; ++j) {
             const f32x4 a = *reinterpret_cast<const f32x4*>(st + row * ld + 32 * j + 4 * c);
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 v[i][j][e] = add ? v[i][j][e] + (a[e] + bias[j][e]) : a[e] + bias[j][e];
-                ss = fmaf(v[i][j][e], v[i][j][e], ss);
+                ss[i] = fmaf(v[i][j][e], v[i][j][e], ss[i]);
             }
         }
-        // (v_rsq_f32: ss is a sum of squares plus 1e-24, never a denormal)
-        const float sc = __builtin_amdgcn_rsqf(oct_sum(ss) * (1.0f / 96.0f) + 1e-24f / 96.0f);
+        ss[i] = oct_sum(ss[i]);
+    }
+    if constexpr (PAIR) {
+        if (c == 0)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                xch[wave * 32 + r0 + 8 * i] = ss[i];
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_waitcnt(0xc07f); // lgkmcnt(0): this wave's LDS writes done
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            ss[i] += xch[(wave ^ 1) * 32 + r0 + 8 * i];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int row = r0 + 8 * i, t = tok0 + row;
+        // (v_rsq_f32: the mean of squares plus 1e-24 / C is never a denormal)
+        const float sc = __builtin_amdgcn_rsqf(ss[i] * kInvC + 1e-24f * kInvC);
         // (tiles over the pixels hold pixel rows only; else the row's ring test, an integer division). Ring rows are
         // zeroed by a mask on the bits, so a ring value that is not finite still comes out 0.
         uint32_t keep = ~0u;
@@ -587,9 +610,9 @@ __device__ inline void epi_norm_silu(const GemmP& p, const float* st, int ld, in
             o[j][1] = pack_bf16x2(u[2], u[3]);
         }
         if (t < int(p.M)) {
-            uint16_t* y = EKE == EK_RMWN ? p.norm_out + int64_t(t) * p.norm_ld + 4 * c
-                                         : static_cast<uint16_t*>(p.c) + int64_t(t) * p.ldc + 4 * c;
-            float* x = static_cast<float*>(p.c) + int64_t(t) * p.ldc + 4 * c;
+            uint16_t* y = EKE == EK_RMWN ? p.norm_out + int64_t(t) * p.norm_ld + chw + 4 * c
+                                         : static_cast<uint16_t*>(p.c) + int64_t(t) * p.ldc + chw + 4 * c;
+            float* x = static_cast<float*>(p.c) + int64_t(t) * p.ldc + chw + 4 * c;
 #pragma unroll
             for (int j = 0; j < 3; ++j) {
                 if constexpr (EKE == EK_RMWN)
@@ -1129,9 +1152,17 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
         return;
     }
     if constexpr (EKE == EK_NORM || EKE == EK_RMWN) {
-        static_assert(WC == 96 && NS == 1 && M16, "the norm epilogues take whole 96-channel rows, one slice a wave");
-        stage(0);
-        epi_norm_silu<EKE>(p, st, LDW, m0 + wm * WM, lane);
+        // 96-channel tiles: a wave holds whole rows; 192-channel tiles: a row's channels are a wave pair's
+        static_assert(WC == 96 && M16 && (BN == 96 || BN == 192), "the norm epilogues take 96- or 192-channel rows");
+        constexpr bool PAIR = BN == 192;
+        // the exchange of partial sums (192: two slices' worth, by parity) after the staging regions
+        static_assert(!PAIR || (NW * 32 * LDW + 2 * NW * 32) * 4 <= 2 * (BN + BM) * 64 * 2, "exchange area in LDS");
+        float* xch = reinterpret_cast<float*>(smem) + NW * 32 * LDW;
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            stage(s);
+            epi_norm_silu<EKE, PAIR>(p, st, LDW, m0 + wm * WM + s * 32, wn * WC, lane, xch + (s & 1) * NW * 32, wave);
+        }
         return;
     }
     if constexpr (EKE == EK_HEADS) {
@@ -1687,11 +1718,11 @@ mk_status conv3x3_run(const mk_conv_args* a, uint32_t lda, bool dense, const Con
     if ((a->epilogue != MK_EPI_STORE && a->epilogue != MK_EPI_ADD) ||
         (a->epilogue == MK_EPI_ADD && a->y_dtype != MK_F32) || (a->y_dtype != MK_F32 && a->y_dtype != MK_BF16))
         return fail(MK_ERR_ARG, std::string(who) + ": epilogue STORE (fp32 or bf16) or ADD (fp32)");
-    if (nm && (!nm->g || a->n != 96 ||
-               (nm->out ? (a->y_dtype != MK_F32 || nm->ld < 96 || nm->ld % 4)
+    if (nm && (!nm->g || (a->n != 96 && a->n != 192) ||
+               (nm->out ? (a->y_dtype != MK_F32 || nm->ld < a->n || nm->ld % 4)
                         : (a->y_dtype != MK_BF16 || a->epilogue != MK_EPI_STORE))))
-        return fail(MK_ERR_ARG, std::string(who) + ": the norm epilogues need 96 output channels and a gain, and "
-                                                   "either a bf16 store or an fp32 output plus a normed one");
+        return fail(MK_ERR_ARG, std::string(who) + ": the norm epilogues need 96 or 192 output channels and a gain, "
+                                                   "and either a bf16 store or an fp32 output plus a normed one");
     const uint64_t pw = uint64_t(a->width) + 2, rows = (uint64_t(a->h) + 2) * pw;
     if (rows >= (1u << 31) || (256 + 2 * pw + 2) * lda * 2 >= (uint64_t(1) << 32) || a->ldy < a->n)
         return fail(MK_ERR_ARG, std::string(who) + ": image too large or ldy < n");
@@ -1721,10 +1752,14 @@ mk_status conv3x3_run(const mk_conv_args* a, uint32_t lda, bool dense, const Con
     mk_gemm_args gp = g;
     gp.M = a->h * a->width;
     GemmPlan plan = gemm_plan(&gp, 1, uint32_t(cus > 0 ? cus : 1), true);
+    if (nm) { // the norm epilogues' tiles span the row: 128 x 96 or 256 x 192
+        plan.bm = a->n == 96 ? 128 : 256;
+        plan.bn = a->n;
+    }
     if (a->width % plan.bm == 0) {
         p.conv_w = a->width;
         p.conv_pix = gp.M;
-    } else {
+    } else if (!nm) {
         plan = gemm_plan(&g, 1, uint32_t(cus > 0 ? cus : 1), true);
     }
     plan.sk = false;
@@ -1735,6 +1770,13 @@ mk_status conv3x3_run(const mk_conv_args* a, uint32_t lda, bool dense, const Con
         p.norm_g = nm->g;
         p.norm_out = nm->out;
         p.norm_ld = nm->ld;
+        if (a->n == 192) {
+            if (nm->out)
+                return dense ? launch<256, 192, false, EK_RMWN | Q, 8>(&p, 1, plan, s)
+                             : launch<256, 192, false, EK_RMWN | C, 8>(&p, 1, plan, s);
+            return dense ? launch<256, 192, false, EK_NORM | Q, 8>(&p, 1, plan, s)
+                         : launch<256, 192, false, EK_NORM | C, 8>(&p, 1, plan, s);
+        }
         if (nm->out)
             return dense ? launch<128, 96, false, EK_RMWN | Q, 4>(&p, 1, plan, s)
                          : launch<128, 96, false, EK_RMWN | C, 4>(&p, 1, plan, s);

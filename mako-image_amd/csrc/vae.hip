@@ -651,9 +651,15 @@ struct mk_vae {
         MK_LAUNCH_CHECK("vae_ring_zero");
         return MK_OK;
     }
-    // Whether conv c's epilogue can norm its rows (96 output channels unpadded: one 128 x 96 tile spans a row).
-    static bool norm_fusable(const Conv& c) { return c.narrow && c.co == 96; }
-    // lda: the input rows' stride (0: c.cip()). only: the output is only the normed rows (bf16 grid out, ldo = 96);
+    // Whether conv c's epilogue can norm its rows: 96 output channels unpadded (one 128 x 96 tile spans a row) or 192
+    // (a 256 x 192 tile). The normed grid has rows of c.co channels.
+    static bool norm_fusable(const Conv& c)
+    {
+        return c.k == 3 && c.parts == 1 && ((c.narrow && c.co == 96) || (c.co == 192 && c.cop() == 192));
+    }
+    // Whether a conv reads a normed grid of rows of C channels as its input: dense K over 96, or 192 channels.
+    static bool reads_normed(const Conv& c, uint32_t C) { return c.ci == C && (c.dense || c.cip() == C); }
+    // lda: the input rows' stride (0: c.cip()). only: the output is only the normed rows (bf16 grid out, ldo = c.co);
     // else, with nt.g set, out gets the conv's fp32 rows (store or add) and nt.buf their norm.
     mk_status conv3(const Conv& c, const void* in, GridDims g, void* out, uint32_t ldo, bool add, uint32_t lda = 0,
                     NormTo nt = {}, bool only = false)
@@ -674,12 +680,12 @@ struct mk_vae {
         ConvNorm nm;
         if (nt.g) {
             if (!norm_fusable(c))
-                return fail(MK_ERR_ARG, "vae: a fused norm needs a conv with 96 unpadded output channels");
-            MK_TRY(zero_ring(only ? static_cast<uint16_t*>(out) : nt.buf, g, 96));
+                return fail(MK_ERR_ARG, "vae: a fused norm needs a conv with 96 or 192 unpadded output channels");
+            MK_TRY(zero_ring(only ? static_cast<uint16_t*>(out) : nt.buf, g, c.co));
             nm.g = nt.g;
             if (!only) {
-                nm.out = nt.buf + uint64_t(g.slack()) * 96;
-                nm.ld = 96;
+                nm.out = nt.buf + uint64_t(g.slack()) * c.co;
+                nm.ld = c.co;
             }
         }
         if (c.dense) {
@@ -767,17 +773,17 @@ struct mk_vae {
         uint32_t c1_lda = 0;
         if (normed_in) {
             c1_in = normed_in;
-            c1_lda = 96;
+            c1_lda = c1.dense ? c1.ci : 0;
         } else {
             MK_TRY(norm(xp, xs, g, c1.ci, r.g1, 0, a.p, c1.cip()));
         }
         const void* c2_in = a.p;
         uint32_t c2_lda = 0;
-        if (norm_fusable(c1) && c2.dense && c2.ci == 96) {
+        if (norm_fusable(c1) && reads_normed(c2, c1.co)) {
             uint16_t* tn = static_cast<uint16_t*>(t.p);
-            MK_TRY(conv3(c1, c1_in, g, tn, 96, false, c1_lda, NormTo{r.g2, nullptr}, true));
+            MK_TRY(conv3(c1, c1_in, g, tn, c1.co, false, c1_lda, NormTo{r.g2, nullptr}, true));
             c2_in = tn;
-            c2_lda = 96;
+            c2_lda = c2.dense ? c2.ci : 0;
         } else {
             MK_TRY(conv3(c1, c1_in, g, t.p, c1.cop(), false, c1_lda));
             MK_TRY(norm(t.p, c1.cop(), g, c1.co, r.g2, 0, a.p, c2.cip()));
@@ -924,7 +930,7 @@ struct mk_vae {
         // At 96 channels each conv that produces x also writes the norm + SiLU its consumer takes of x (the next res
         // block's norm1, or norm_out before conv_out): `normed` is that grid (rows of 96) when the last conv wrote it.
         // A res block's conv2 writes it into a (conv2 reads t), the upsampling conv into sc (it reads a).
-        auto takes_normed = [](const Res& r) { return r.c1.dense && r.c1.ci == 96; };
+        auto takes_normed = [](const Res& r, const Conv& from) { return reads_normed(r.c1, from.co); };
         uint16_t* const na = static_cast<uint16_t*>(a.p);
         uint16_t* const ns = static_cast<uint16_t*>(sc.p);
         const uint16_t* normed = nullptr;
@@ -934,9 +940,9 @@ struct mk_vae {
                 const Res& r = u.res[j];
                 NormTo next{};
                 if (norm_fusable(r.c2) && !r.shortcut) {
-                    if (j < 2 && takes_normed(u.res[j + 1]))
+                    if (j < 2 && takes_normed(u.res[j + 1], r.c2))
                         next = NormTo{u.res[j + 1].g1, na};
-                    else if (j == 2 && i == 3 && conv_out.ci == 96)
+                    else if (j == 2 && i == 3 && r.c2.co == 96 && conv_out.ci == 96)
                         next = NormTo{out_g, na};
                 }
                 MK_TRY(res_block(r, g, xp, cs, yp, normed, next));
@@ -949,7 +955,7 @@ struct mk_vae {
                     xp, cs, g, u.cout, g2, u.conv.cip(), na);
                 MK_LAUNCH_CHECK("vae_up");
                 NormTo next{};
-                if (norm_fusable(u.conv) && i + 1 < 4 && takes_normed(ups[i + 1].res[0]))
+                if (norm_fusable(u.conv) && i + 1 < 4 && takes_normed(ups[i + 1].res[0], u.conv))
                     next = NormTo{ups[i + 1].res[0].g1, ns};
                 MK_TRY(conv3(u.conv, na, g2, yp, u.conv.cop(), false, 0, next));
                 normed = next.g ? next.buf : nullptr;
