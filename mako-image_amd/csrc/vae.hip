@@ -439,8 +439,8 @@ inline mk_status hip_ok(hipError_t e, const char* what) { return e == hipSuccess
 
 using namespace mk;
 
-// A norm + SiLU that a 96-channel conv's epilogue applies to its rows: gain g, into the bf16 grid buf (rows of 96; its
-// slack and ring rows zeroed by mk_vae::conv3)
+// A norm + SiLU that a 96- or 192-channel conv's epilogue applies to its rows: gain g, into the bf16 grid buf (rows of
+// the conv's channels; its slack and ring rows zeroed by mk_vae::conv3)
 struct NormTo {
     const float* g = nullptr;
     uint16_t* buf = nullptr;
@@ -761,10 +761,10 @@ struct mk_vae {
     }
 
     // res_block (engine.cpp:732-746): x (fp32 grid, stride cs = c2.cop() after) <- conv2(silu(norm2(conv1(
-    // silu(norm1(x)))))) + shortcut(x). x and the result may differ in channels; xs is x's stride. At 96 channels the
-    // norms come from the convs' epilogues: normed_in (rows of 96) already holds silu(norm1(x)), conv1 writes
-    // silu(norm2(.)) straight into t as conv2's bf16 input, and with next.g conv2 also writes the norm the next layer
-    // takes of the result into next.buf (which conv2 does not read).
+    // silu(norm1(x)))))) + shortcut(x). x and the result may differ in channels; xs is x's stride. At 96 and 192
+    // channels the norms come from the convs' epilogues: normed_in (rows of the channels) already holds silu(norm1(x)),
+    // conv1 writes silu(norm2(.)) straight into t as conv2's bf16 input, and with next.g conv2 also writes the norm the
+    // next layer takes of the result into next.buf (which conv2 does not read).
     mk_status res_block(const Res& r, GridDims g, float*& xp, uint32_t xs, float*& yp, const uint16_t* normed_in = nullptr,
                         NormTo next = {})
     {
@@ -836,48 +836,51 @@ struct mk_vae {
             v.epilogue = MK_EPI_STORE;
             MK_TRY(mk_gemm(&v, stream));
         }
-        // Queries in chunks whose fp32 scores (near 128 MB) stay in the memory-side cache between the score GEMM that
-        // writes them and the softmax that reads them; P (bf16) for all queries, then one P V product.
-        const uint64_t qc = std::min<uint64_t>(n, std::max<uint64_t>(256, (uint64_t(1) << 25) / np / 256 * 256));
+        // Queries in groups whose bf16 P stays within 512 MB (one P V product each), and within a group in chunks
+        // whose fp32 scores (near 128 MB) stay in the memory-side cache between the score GEMM that writes them and
+        // the softmax that reads them. (At 128 x 128 pixels: one group, 8 chunks of 2048 queries.)
+        const uint64_t qg = std::min<uint64_t>(n, std::max<uint64_t>(256, (uint64_t(1) << 28) / np / 256 * 256));
+        const uint64_t qc = std::min<uint64_t>(qg, std::max<uint64_t>(256, (uint64_t(1) << 25) / np / 256 * 256));
         MK_TRY(ensure(sb, qc * np * 4));
-        MK_TRY(ensure(pb, n * np * 2));
+        MK_TRY(ensure(pb, qg * np * 2));
         const float scale = 1.0f / std::sqrt(float(c));
-        for (uint64_t q0 = 0; q0 < n; q0 += qc) {
-            const uint64_t m = std::min(qc, n - q0);
-            mk_gemm_args s{};
-            s.a = static_cast<uint16_t*>(qb.p) + q0 * cp;
-            s.w = kb.p;
-            s.c = sb.p;
-            s.M = uint32_t(m);
-            s.N = uint32_t(np);
-            s.K = cp;
-            s.lda = cp;
-            s.ldc = int64_t(np);
-            s.batch = 1;
-            s.w_dtype = MK_BF16;
-            s.c_dtype = MK_F32;
-            s.epilogue = MK_EPI_STORE;
-            MK_TRY(mk_gemm(&s, stream));
-            float* sp = static_cast<float*>(sb.p);
-            uint16_t* pp = static_cast<uint16_t*>(pb.p) + q0 * np;
-            // rows that fit the registers (up to 16384 columns) in one read, longer ones in two
-            if (np <= 1024)
-                vae_softmax1_kernel<1><<<uint32_t(m), 256, 0, stream>>>(sp, uint32_t(n), uint32_t(np), scale, pp);
-            else if (np <= 4096)
-                vae_softmax1_kernel<4><<<uint32_t(m), 256, 0, stream>>>(sp, uint32_t(n), uint32_t(np), scale, pp);
-            else if (np <= 16384)
-                vae_softmax1_kernel<16><<<uint32_t(m), 256, 0, stream>>>(sp, uint32_t(n), uint32_t(np), scale, pp);
-            else
-                vae_softmax_kernel<<<uint32_t(m), 256, 0, stream>>>(sp, uint32_t(n), uint32_t(np), scale, pp);
-            MK_LAUNCH_CHECK("vae_softmax");
-        }
-        {
+        for (uint64_t g0 = 0; g0 < n; g0 += qg) {
+            const uint64_t gm = std::min(qg, n - g0);
+            for (uint64_t q0 = g0; q0 < g0 + gm; q0 += qc) {
+                const uint64_t m = std::min(qc, g0 + gm - q0);
+                mk_gemm_args s{};
+                s.a = static_cast<uint16_t*>(qb.p) + q0 * cp;
+                s.w = kb.p;
+                s.c = sb.p;
+                s.M = uint32_t(m);
+                s.N = uint32_t(np);
+                s.K = cp;
+                s.lda = cp;
+                s.ldc = int64_t(np);
+                s.batch = 1;
+                s.w_dtype = MK_BF16;
+                s.c_dtype = MK_F32;
+                s.epilogue = MK_EPI_STORE;
+                MK_TRY(mk_gemm(&s, stream));
+                float* sp = static_cast<float*>(sb.p);
+                uint16_t* pp = static_cast<uint16_t*>(pb.p) + (q0 - g0) * np;
+                // rows that fit the registers (up to 16384 columns) in one read, longer ones in two
+                if (np <= 1024)
+                    vae_softmax1_kernel<1><<<uint32_t(m), 256, 0, stream>>>(sp, uint32_t(n), uint32_t(np), scale, pp);
+                else if (np <= 4096)
+                    vae_softmax1_kernel<4><<<uint32_t(m), 256, 0, stream>>>(sp, uint32_t(n), uint32_t(np), scale, pp);
+                else if (np <= 16384)
+                    vae_softmax1_kernel<16><<<uint32_t(m), 256, 0, stream>>>(sp, uint32_t(n), uint32_t(np), scale, pp);
+                else
+                    vae_softmax_kernel<<<uint32_t(m), 256, 0, stream>>>(sp, uint32_t(n), uint32_t(np), scale, pp);
+                MK_LAUNCH_CHECK("vae_softmax");
+            }
             mk_gemm_args o{};
             o.a = pb.p;
             o.w = vtb.p;
             o.bias = qkv.b + size_t(2) * cp;
-            o.c = ob.p;
-            o.M = uint32_t(n);
+            o.c = static_cast<uint16_t*>(ob.p) + g0 * cp;
+            o.M = uint32_t(gm);
             o.N = cp;
             o.K = uint32_t(np);
             o.lda = int64_t(np);
