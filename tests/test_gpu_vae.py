@@ -86,6 +86,31 @@ def test_conv3x3_matches_torch(gpu, h, w, c, n, add):
     assert np.array_equal(out[:S], y0[:S]) and np.array_equal(out[-S:], y0[-S:])
 
 
+# bf16 output (STORE): the 96-wide tile's 32-channel slices, a 192-wide tile, pixel-tiled and padded-row widths
+@pytest.mark.parametrize("h, w, c, n", [(4, 128, 64, 96), (7, 9, 128, 96), (8, 256, 64, 192), (5, 6, 64, 128)])
+def test_conv3x3_bf16_output(gpu, h, w, c, n):
+    rng = np.random.default_rng(h * 100 + w + n)
+    x = M.bf16_bits(rng.standard_normal((h, w, c)).astype(np.float32))
+    wb = M.bf16_bits((rng.standard_normal((n, c, 3, 3)) / np.sqrt(9 * c)).astype(np.float32))
+    bias = rng.standard_normal(n).astype(np.float32) * 0.1
+    packed = np.ascontiguousarray(wb.transpose(0, 2, 3, 1).reshape(n, 9 * c))
+    y0 = np.full((grid_rows(h, w), n), 0x7FC0, dtype=np.uint16)  # NaN patterns: rows the conv must not write
+    dx, dw, db = M.Dev.from_array(to_grid(x, c)), M.Dev.from_array(packed), M.Dev.from_array(bias)
+    dy = M.Dev.from_array(y0)
+    S = w + 3
+    a = M.ConvArgs(int(dx), int(dw), int(db), int(dy) + S * n * 2, h, w, c, n, n, M.BF16, M.EPI_STORE)
+    M.check(M.lib().mk_conv3x3(ctypes.byref(a), None), "mk_conv3x3")
+    M.sync()
+    out = dy.to_array(np.uint16, y0.shape)
+    got = M.bf16_to_f32(from_grid(out, h, w, n))
+    xt = torch.from_numpy(M.bf16_to_f32(x)).double().permute(2, 0, 1)[None]
+    want = F.conv2d(xt, torch.from_numpy(M.bf16_to_f32(wb)).double(), torch.from_numpy(bias).double(), padding=1)
+    want = want[0].permute(1, 2, 0).numpy()
+    # one bf16 rounding of the fp32 result: within 2^-8 relative of the largest value
+    assert np.abs(got - want).max() <= np.abs(want).max() * 2.0 ** -8, np.abs(got - want).max()
+    assert np.array_equal(out[:S], y0[:S]) and np.array_equal(out[-S:], y0[-S:])
+
+
 def test_conv3x3_rejects_bad_shapes(gpu):
     a = M.ConvArgs(16, 16, 0, 16, 4, 4, 96, 64, 64, M.F32, M.EPI_STORE)  # 96 channels: not a multiple of 64
     assert M.lib().mk_conv3x3(ctypes.byref(a), None) == 1
