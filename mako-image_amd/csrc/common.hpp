@@ -99,6 +99,14 @@ struct ConvNorm {
 mk_status conv3x3_dense(const mk_conv_args* a, uint32_t lda, void* stream, const ConvNorm* nm = nullptr);
 // mk_conv3x3 with a norm epilogue
 mk_status conv3x3_fused(const mk_conv_args* a, const ConvNorm& nm, void* stream);
+// mk_conv3x3 (ADD, output channels a multiple of 192, width a multiple of 256) whose sums y + conv go, as bf16, to the
+// four pixels each becomes in the nearest-2x padded grid at out (its first buffer row, rows of ld channels), instead
+// of back into y; the 2x grid's ring and slack rows are the caller's.
+struct ConvUp {
+    uint16_t* out = nullptr;
+    uint32_t ld = 0;
+};
+mk_status conv3x3_up(const mk_conv_args* a, const ConvUp& up, void* stream);
 
 // ---- error state (thread-local, read by mk_last_error) ----
 void set_error(const std::string& msg);

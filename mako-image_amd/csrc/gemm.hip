@@ -57,9 +57,12 @@ struct GemmP {
     // gated linear unit (EK_GLU): the weights' rows are [first part F; second part F], the output [M][F]
     uint32_t glu_f;
     // EK_NORM / EK_RMWN: the RMS norm's per-channel gain; EK_RMWN: the normed rows' bf16 output and its row stride
+    // (EK_RMWUP: the 2x grid's bf16 buffer, from its first row, and row stride)
     const float* norm_g;
     uint16_t* norm_out;
     uint32_t norm_ld;
+    // EK_RMWUP: the 2x grid's row width (2 w + 2) and slack rows (2 w + 3)
+    uint32_t up_pw, up_slack;
 };
 
 // One launch of up to two GEMMs of equal N, K and epilogue kind (the dual-stream blocks' image and text
@@ -99,8 +102,9 @@ __device__ inline void f8x16_to_bf16(const u32x4& v, u32x4& lo, u32x4& hi)
 // Epilogue kinds (template): a plain store, an activation, a read-modify-write of the fp32 residual, the q/k/v heads,
 // a gated linear unit (SwiGLU / GEGLU: each output channel from two weight rows F apart).
 // EK_NORM: a 96-channel convolution's rows RMS-normed and SiLU-ed into the next convolution's bf16 input grid;
-// EK_RMWN: the rows stored (or added into the fp32 residual) and their RMS norm + SiLU written besides.
-enum { EK_STORE = 0, EK_ACT = 1, EK_RMW = 2, EK_HEADS = 3, EK_GLU = 4, EK_NORM = 5, EK_RMWN = 6 };
+// EK_RMWN: the rows stored (or added into the fp32 residual) and their RMS norm + SiLU written besides; EK_RMWUP: the
+// rows added into the residual and written, as bf16, to the four pixels each becomes in the nearest 2x grid.
+enum { EK_STORE = 0, EK_ACT = 1, EK_RMW = 2, EK_HEADS = 3, EK_GLU = 4, EK_NORM = 5, EK_RMWN = 6, EK_RMWUP = 7 };
 // Flag on the epilogue kind: the A operand is a 3 x 3 convolution's input (implicit im2col, see conv_koff).
 constexpr int EK_CONV = 8;
 // With EK_CONV: input channels not a multiple of 64 (dense K = 9 c rounded up to 64, k = tap c + channel): a k step
@@ -150,6 +154,33 @@ __device__ inline void epi_slice(const GemmP& p, const float* st, int ld, int to
 #pragma unroll
         for (int e = 0; e < 4; ++e)
             v[i][e] = v[i][e] * k.scale[e] + k.bias[e];
+    }
+    if constexpr (EK == EK_RMWUP) {
+        // x + v (the convolution's ADD) goes to the four pixels (2 y + dy, 2 x + dx) of the nearest 2x grid as bf16;
+        // the residual itself is not stored (its next reader is the upsampling). Tiles over the pixels only: every
+        // row of the slice is a pixel of image row y.
+        const float* c = static_cast<const float*>(p.c) + ch;
+        const uint32_t pw = p.conv_pw, y = uint32_t(tok0) / pw - 1, ld2 = p.norm_ld;
+        uint16_t* up = p.norm_out + ch;
+        f32x4 xs[NI];
+#pragma unroll
+        for (int i = 0; i < NI; ++i)
+            xs[i] = *reinterpret_cast<const f32x4*>(c + int64_t(min(tok0 + r0 + RPI * i, int(p.M) - 1)) * p.ldc);
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const int t = tok0 + r0 + RPI * i;
+            const f32x4& x = xs[i];
+            if (t < int(p.M)) {
+                const uint32_t xx = uint32_t(t) - (y + 1) * pw - 1;
+                const uint64_t r = p.up_slack + uint64_t(2 * y + 1) * p.up_pw + 2 * xx + 1;
+                const u32x2 o{pack_bf16x2(x[0] + v[i][0], x[1] + v[i][1]), pack_bf16x2(x[2] + v[i][2], x[3] + v[i][3])};
+                *reinterpret_cast<u32x2*>(up + r * ld2) = o;
+                *reinterpret_cast<u32x2*>(up + (r + 1) * ld2) = o;
+                *reinterpret_cast<u32x2*>(up + (r + p.up_pw) * ld2) = o;
+                *reinterpret_cast<u32x2*>(up + (r + p.up_pw + 1) * ld2) = o;
+            }
+        }
+        return;
     }
     if constexpr (EK == EK_RMW) {
         // rows past M read (and leave) the last valid row
@@ -1703,7 +1734,8 @@ namespace mk {
 // 64, k = tap c + channel, zero past 9 c) each 16-byte chunk takes its own tap's row shift (koffq), so no MFMA work
 // goes to channel padding (the VAE's 96-channel level: K 864 -> 896 instead of 1152). The ring's output rows are
 // computed like the others and are the caller's to ignore (the norm epilogues write them as zeros).
-mk_status conv3x3_run(const mk_conv_args* a, uint32_t lda, bool dense, const ConvNorm* nm, void* stream)
+mk_status conv3x3_run(const mk_conv_args* a, uint32_t lda, bool dense, const ConvNorm* nm, void* stream,
+                      const ConvUp* up = nullptr)
 {
     const char* who = dense ? "conv3x3_dense" : "conv3x3";
     if (!a || !a->x || !a->w || !a->y)
@@ -1723,6 +1755,10 @@ mk_status conv3x3_run(const mk_conv_args* a, uint32_t lda, bool dense, const Con
                         : (a->y_dtype != MK_BF16 || a->epilogue != MK_EPI_STORE))))
         return fail(MK_ERR_ARG, std::string(who) + ": the norm epilogues need 96 or 192 output channels and a gain, "
                                                    "and either a bf16 store or an fp32 output plus a normed one");
+    if (up && (nm || dense || !up->out || a->epilogue != MK_EPI_ADD || a->n % 192 || a->width % 256 || up->ld < a->n ||
+               up->ld % 4 || a->h > (1u << 14) || a->width > (1u << 14)))
+        return fail(MK_ERR_ARG, std::string(who) + ": the 2x-grid epilogue needs an ADD over 192-channel multiples, "
+                                                   "an image width of a multiple of 256 and no norm epilogue");
     const uint64_t pw = uint64_t(a->width) + 2, rows = (uint64_t(a->h) + 2) * pw;
     if (rows >= (1u << 31) || (256 + 2 * pw + 2) * lda * 2 >= (uint64_t(1) << 32) || a->ldy < a->n)
         return fail(MK_ERR_ARG, std::string(who) + ": image too large or ldy < n");
@@ -1756,6 +1792,10 @@ mk_status conv3x3_run(const mk_conv_args* a, uint32_t lda, bool dense, const Con
         plan.bm = a->n == 96 ? 128 : 256;
         plan.bn = a->n;
     }
+    if (up) { // 256 x 192 tiles over the pixels: a tile's rows lie in one image row
+        plan.bm = 256;
+        plan.bn = 192;
+    }
     if (a->width % plan.bm == 0) {
         p.conv_w = a->width;
         p.conv_pix = gp.M;
@@ -1766,6 +1806,13 @@ mk_status conv3x3_run(const mk_conv_args* a, uint32_t lda, bool dense, const Con
     hipStream_t s = static_cast<hipStream_t>(stream);
     const bool add = a->epilogue == MK_EPI_ADD;
     constexpr int C = EK_CONV, Q = EK_CONV | EK_CONVQ;
+    if (up) {
+        p.norm_out = up->out;
+        p.norm_ld = up->ld;
+        p.up_pw = 2 * a->width + 2;
+        p.up_slack = 2 * a->width + 3;
+        return launch<256, 192, false, EK_RMWUP | C, 8>(&p, 1, plan, s);
+    }
     if (nm) {
         p.norm_g = nm->g;
         p.norm_out = nm->out;
@@ -1833,5 +1880,9 @@ namespace mk {
 mk_status conv3x3_fused(const mk_conv_args* a, const ConvNorm& nm, void* stream)
 {
     return conv3x3_run(a, a ? a->c : 0, false, &nm, stream);
+}
+mk_status conv3x3_up(const mk_conv_args* a, const ConvUp& up, void* stream)
+{
+    return conv3x3_run(a, a ? a->c : 0, false, nullptr, stream, &up);
 }
 } // namespace mk

@@ -661,8 +661,9 @@ struct mk_vae {
     static bool reads_normed(const Conv& c, uint32_t C) { return c.ci == C && (c.dense || c.cip() == C); }
     // lda: the input rows' stride (0: c.cip()). only: the output is only the normed rows (bf16 grid out, ldo = c.co);
     // else, with nt.g set, out gets the conv's fp32 rows (store or add) and nt.buf their norm.
+    // up: the sums go to the nearest-2x grid up->out instead of back into out (an ADD; see conv3x3_up)
     mk_status conv3(const Conv& c, const void* in, GridDims g, void* out, uint32_t ldo, bool add, uint32_t lda = 0,
-                    NormTo nt = {}, bool only = false)
+                    NormTo nt = {}, bool only = false, const ConvUp* up = nullptr)
     {
         mk_conv_args a{};
         a.x = in;
@@ -694,6 +695,8 @@ struct mk_vae {
         }
         if (lda)
             return fail(MK_ERR_ARG, "vae: an input stride needs a dense conv");
+        if (up)
+            return nt.g ? fail(MK_ERR_ARG, "vae: a 2x-grid output has no norm") : conv3x3_up(&a, *up, stream);
         return nt.g ? conv3x3_fused(&a, nm, stream) : mk_conv3x3(&a, stream);
     }
     // 1 x 1 conv over rows (grid or compact): y[rows][ldo] (fp32 or bf16) = a[rows][cip] W^T + b (or +=)
@@ -765,8 +768,9 @@ struct mk_vae {
     // channels the norms come from the convs' epilogues: normed_in (rows of the channels) already holds silu(norm1(x)),
     // conv1 writes silu(norm2(.)) straight into t as conv2's bf16 input, and with next.g conv2 also writes the norm the
     // next layer takes of the result into next.buf (which conv2 does not read).
+    // With up, conv2's sums go to the nearest-2x grid (see conv3x3_up) and x is left as it was.
     mk_status res_block(const Res& r, GridDims g, float*& xp, uint32_t xs, float*& yp, const uint16_t* normed_in = nullptr,
-                        NormTo next = {})
+                        NormTo next = {}, const ConvUp* up = nullptr)
     {
         const Conv &c1 = r.c1, &c2 = r.c2;
         const void* c1_in = a.p;
@@ -793,10 +797,12 @@ struct mk_vae {
             MK_TRY(norm(xp, xs, g, r.sc.ci, nullptr, 2, sc.p, r.sc.cip()));
             MK_TRY(conv1(r.sc, 0, static_cast<uint16_t*>(sc.p) + uint64_t(g.slack()) * r.sc.cip(), g.grid_rows(),
                          yp + uint64_t(g.slack()) * r.sc.cop(), r.sc.cop(), MK_F32, MK_EPI_STORE));
+            if (up)
+                return fail(MK_ERR_ARG, "vae: a 2x-grid output after a shortcut");
             MK_TRY(conv3(c2, c2_in, g, yp, c2.cop(), true, c2_lda, next));
             std::swap(xp, yp);
         } else {
-            MK_TRY(conv3(c2, c2_in, g, xp, c2.cop(), true, c2_lda, next));
+            MK_TRY(conv3(c2, c2_in, g, xp, c2.cop(), true, c2_lda, next, false, up));
         }
         return MK_OK;
     }
@@ -939,6 +945,13 @@ struct mk_vae {
         const uint16_t* normed = nullptr;
         for (int i = 0; i < 4; ++i) {
             Up& u = ups[i];
+            // the last res block's conv2 can write the nearest-2x grid the upsampling conv reads (into sc, since its
+            // input may be a): whole 192-channel tiles over the pixels of one image row each
+            const Res& rl = u.res[2];
+            const bool up_fused = u.up && !rl.shortcut && !rl.c2.dense && rl.c2.co % 192 == 0 &&
+                                  rl.c2.cop() == rl.c2.co && u.cout == rl.c2.co && u.conv.cip() == rl.c2.co &&
+                                  g.w % 256 == 0;
+            uint16_t* const upbuf = up_fused ? ns : na;
             for (int j = 0; j < 3; ++j) {
                 const Res& r = u.res[j];
                 NormTo next{};
@@ -948,19 +961,28 @@ struct mk_vae {
                     else if (j == 2 && i == 3 && r.c2.co == 96 && conv_out.ci == 96)
                         next = NormTo{out_g, na};
                 }
-                MK_TRY(res_block(r, g, xp, cs, yp, normed, next));
+                ConvUp cu;
+                if (j == 2 && up_fused) {
+                    const GridDims g2{2 * g.h, 2 * g.w};
+                    MK_TRY(zero_ring(ns, g2, u.conv.cip()));
+                    cu = ConvUp{ns, u.conv.cip()};
+                }
+                MK_TRY(res_block(r, g, xp, cs, yp, normed, next, cu.out ? &cu : nullptr));
                 normed = next.g ? next.buf : nullptr;
                 cs = r.c2.cop();
             }
             if (u.up) {
                 const GridDims g2{2 * g.h, 2 * g.w};
-                vae_up_kernel<<<blocks_for(g2.rows() * u.conv.cip() / 4), 256, 0, stream>>>(
-                    xp, cs, g, u.cout, g2, u.conv.cip(), na);
-                MK_LAUNCH_CHECK("vae_up");
+                if (!up_fused) {
+                    vae_up_kernel<<<blocks_for(g2.rows() * u.conv.cip() / 4), 256, 0, stream>>>(
+                        xp, cs, g, u.cout, g2, u.conv.cip(), na);
+                    MK_LAUNCH_CHECK("vae_up");
+                }
+                // the conv's norm output goes to whichever of a and sc it does not read
                 NormTo next{};
                 if (norm_fusable(u.conv) && i + 1 < 4 && takes_normed(ups[i + 1].res[0], u.conv))
-                    next = NormTo{ups[i + 1].res[0].g1, ns};
-                MK_TRY(conv3(u.conv, na, g2, yp, u.conv.cop(), false, 0, next));
+                    next = NormTo{ups[i + 1].res[0].g1, upbuf == na ? ns : na};
+                MK_TRY(conv3(u.conv, upbuf, g2, yp, u.conv.cop(), false, 0, next));
                 normed = next.g ? next.buf : nullptr;
                 std::swap(xp, yp);
                 g = g2;
