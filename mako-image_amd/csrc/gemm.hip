@@ -4,9 +4,10 @@
 // N = tokens), so each lane's accumulators hold 4 consecutive channels of one token: the epilogues stage a wave's
 // 32-token slice through LDS and write whole row segments.
 //
-// Tiling: BM = 256 tokens x BN channels x 64 k per workgroup; 256-wide tiles run 8 waves (two a SIMD: 2 along
-// channels x 4 along tokens, 128 x 64 per wave) on v_mfma_f32_16x16x32_bf16, narrower ones 4 waves (2 x 2) on
-// v_mfma_f32_32x32x16_bf16. Both tiles are K-contiguous and staged in LDS with a 16-byte-chunk XOR swizzle
+// Tiling: BM = 256 (or 128) tokens x BN channels x 64 k per workgroup; 256- and 192-wide tiles run 8 waves (two a
+// SIMD: 2 along channels x 4 along tokens) on v_mfma_f32_16x16x32_bf16, 128- and 64-wide ones 4 waves (2 x 2) on
+// v_mfma_f32_32x32x16_bf16, 96-wide ones (convolutions) 4 waves of whole 96-channel rows on 16x16x32; 128-token tiles
+// run two workgroups a CU. Both tiles are K-contiguous and staged in LDS with a 16-byte-chunk XOR swizzle
 // (chunk ^ ((row >> 1) & 7)) so the fragment reads of 16 or 32 rows at one k offset are bank-conflict free. Two LDS
 // buffers, one barrier per k step: buffer loads write a later k step straight into LDS while the current one's
 // MFMAs run (128-channel tiles stage it through registers instead). The main loop's instruction order is fixed by
