@@ -93,6 +93,7 @@ struct ConvNorm {
     const float* g = nullptr;
     uint16_t* out = nullptr;
     uint32_t ld = 0;
+    bool skip_y = false; // with out: the fp32 rows are not stored (nothing reads them after the norm)
 };
 // mk_conv3x3 for c (a multiple of 8, not of 64, <= 512) input channels in rows of stride lda, with dense weights
 // [n][K], K = 9 c rounded up to 64 (k = tap c + channel, zero past 9 c); optionally a norm epilogue (gemm.hip).

@@ -64,6 +64,8 @@ struct GemmP {
     uint32_t norm_ld;
     // EK_RMWUP: the 2x grid's row width (2 w + 2) and slack rows (2 w + 3)
     uint32_t up_pw, up_slack;
+    // EK_RMWN: the fp32 rows are not stored, only their norm
+    uint32_t norm_only;
 };
 
 // One launch of up to two GEMMs of equal N, K and epilogue kind (the dual-stream blocks' image and text
@@ -647,7 +649,7 @@ __device__ inline void epi_norm_silu(const GemmP& p, const float* st, int ld, in
             float* x = static_cast<float*>(p.c) + int64_t(t) * p.ldc + chw + 4 * c;
 #pragma unroll
             for (int j = 0; j < 3; ++j) {
-                if constexpr (EKE == EK_RMWN)
+                if (EKE == EK_RMWN && !p.norm_only)
                     *reinterpret_cast<f32x4*>(x + 32 * j) = v[i][j];
                 *reinterpret_cast<u32x2*>(y + 32 * j) = u32x2{o[j][0], o[j][1]};
             }
@@ -1818,6 +1820,7 @@ mk_status conv3x3_run(const mk_conv_args* a, uint32_t lda, bool dense, const Con
         p.norm_g = nm->g;
         p.norm_out = nm->out;
         p.norm_ld = nm->ld;
+        p.norm_only = nm->out && nm->skip_y ? 1u : 0u;
         if (a->n == 192) {
             if (nm->out)
                 return dense ? launch<256, 192, false, EK_RMWN | Q, 8>(&p, 1, plan, s)

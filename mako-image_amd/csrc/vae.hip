@@ -444,6 +444,7 @@ using namespace mk;
 struct NormTo {
     const float* g = nullptr;
     uint16_t* buf = nullptr;
+    bool only = false; // the conv's own fp32 rows are not needed (the decode's last residual, without probes)
 };
 
 struct mk_vae {
@@ -687,6 +688,7 @@ struct mk_vae {
             if (!only) {
                 nm.out = nt.buf + uint64_t(g.slack()) * c.co;
                 nm.ld = c.co;
+                nm.skip_y = nt.only;
             }
         }
         if (c.dense) {
@@ -959,7 +961,7 @@ struct mk_vae {
                     if (j < 2 && takes_normed(u.res[j + 1], r.c2))
                         next = NormTo{u.res[j + 1].g1, na};
                     else if (j == 2 && i == 3 && r.c2.co == 96 && conv_out.ci == 96)
-                        next = NormTo{out_g, na};
+                        next = NormTo{out_g, na, !probe}; // x itself is read only by the probe
                 }
                 ConvUp cu;
                 if (j == 2 && up_fused) {
