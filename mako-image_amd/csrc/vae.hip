@@ -379,6 +379,85 @@ __global__ __launch_bounds__(256) void vae_conv_out_kernel(const uint16_t* __res
                                                     fminf(1.0f, fmaxf(-1.0f, acc[2])), 1.0f};
 }
 
+// conv_out over 96 input channels on the matrix cores (v_mfma_f32_16x16x32_bf16). The weights are the A operand: its
+// 16 rows are the 3 output channels and 13 zero rows, and a tap's 96 channels are three 32-deep k chunks, so the 27
+// fragments stay in registers. 16 pixels of one tile row are the B operand, one 16-byte LDS read a lane from the
+// neighbourhood (pixel stride 208 B: the 16 pixels of a read fall on distinct bank groups). A lane of the product
+// holds outputs 4 g4 .. 4 g4 + 3 of pixel r16, so the lanes with g4 = 0 hold each pixel's (r, g, b) for one
+// 16-byte RGBA store. Wave w takes tile rows 4 w .. 4 w + 3: four independent accumulator chains of 27 products.
+__global__ __launch_bounds__(256) void vae_conv_out96_kernel(const uint16_t* __restrict__ x, uint32_t xs, uint32_t cs,
+                                                             GridDims g, const uint16_t* __restrict__ w,
+                                                             const float* __restrict__ bias,
+                                                             float* __restrict__ rgba, float* __restrict__ pre,
+                                                             uint32_t ps)
+{
+    constexpr uint32_t NB = kCoTile + 2, C = 96, PST = C + 8, CQ = C / 8;
+    static_assert(kCoTile == 16, "a tile row is one 16-pixel B operand, four rows a wave");
+    __shared__ __attribute__((aligned(16))) uint16_t sx[NB * NB * PST];
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, r16 = lane & 15, g4 = lane >> 4;
+    const uint32_t ty0 = blockIdx.y * kCoTile, tx0 = blockIdx.x * kCoTile;
+    // the weight fragments (rows past the 3 outputs zero), loaded while the neighbourhood comes in
+    bf16x8 wf[9][3];
+#pragma unroll
+    for (int tap = 0; tap < 9; ++tap)
+#pragma unroll
+        for (int j = 0; j < 3; ++j)
+            wf[tap][j] = r16 < 3 ? *reinterpret_cast<const bf16x8*>(w + (uint64_t(r16) * 9 + tap) * cs + 32 * j + 8 * g4)
+                                 : bf16x8{};
+    // neighbourhood pixel (qy, qx) is grid pixel (ty0 + qy - 1, tx0 + qx - 1): grid row slack + (ty0 + qy) (w + 2) +
+    // tx0 + qx, inside the grid while ty0 + qy <= h + 1 and tx0 + qx <= w + 1 (zeros beyond). All of a thread's
+    // loads go out before its LDS stores (a load-store loop would wait for each load in turn).
+    constexpr uint32_t NF = NB * NB * CQ, NL = (NF + 255) / 256;
+    u32x4 v[NL];
+#pragma unroll
+    for (uint32_t n = 0; n < NL; ++n) {
+        const uint32_t i = tid + 256 * n, q = i / CQ, k = i - q * CQ, qy = q / NB, qx = q - qy * NB;
+        v[n] = u32x4{0, 0, 0, 0};
+        if (i < NF && ty0 + qy <= g.h + 1 && tx0 + qx <= g.w + 1)
+            v[n] = *reinterpret_cast<const u32x4*>(x + (g.slack() + uint64_t(ty0 + qy) * g.pw() + tx0 + qx) * xs +
+                                                   8 * k);
+    }
+#pragma unroll
+    for (uint32_t n = 0; n < NL; ++n) {
+        const uint32_t i = tid + 256 * n;
+        if (i < NF)
+            *reinterpret_cast<u32x4*>(sx + i / CQ * PST + 8 * (i % CQ)) = v[n];
+    }
+    __syncthreads();
+    f32x4 acc[4] = {};
+#pragma unroll
+    for (int tap = 0; tap < 9; ++tap) {
+        const uint32_t dy = tap / 3, dx = tap - 3 * dy;
+#pragma unroll
+        for (int j = 0; j < 3; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const bf16x8 b = *reinterpret_cast<const bf16x8*>(
+                    sx + ((4 * wave + r + dy) * NB + r16 + dx) * PST + 32 * j + 8 * g4);
+                acc[r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[tap][j], b, acc[r], 0, 0, 0);
+            }
+    }
+    if (g4 != 0)
+        return;
+    const uint32_t px = tx0 + r16;
+    const float b0 = bias[0], b1 = bias[1], b2 = bias[2];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const uint32_t py = ty0 + 4 * wave + r;
+        if (py < g.h && px < g.w) {
+            const float o0 = acc[r][0] + b0, o1 = acc[r][1] + b1, o2 = acc[r][2] + b2;
+            if (pre) {
+                float* q = pre + g.row_of(py, px) * ps;
+                q[0] = o0;
+                q[1] = o1;
+                q[2] = o2;
+            }
+            *reinterpret_cast<f32x4*>(rgba + 4 * (uint64_t(py) * g.w + px)) =
+                f32x4{fminf(1.0f, fmaxf(-1.0f, o0)), fminf(1.0f, fmaxf(-1.0f, o1)), fminf(1.0f, fmaxf(-1.0f, o2)), 1.0f};
+        }
+    }
+}
+
 // A PyTorch conv weight [parts * co][ci][kt][k][k] (bf16; kt time taps of a causal 3-D conv, the last one used: a
 // single frame sees only it) -> [parts][cop][k * k][cip] bf16, tap-major, zero-padded. One thread an output value.
 __global__ __launch_bounds__(256) void vae_pack_kernel(const uint16_t* __restrict__ src, uint32_t parts, uint32_t co,
@@ -998,9 +1077,14 @@ struct mk_vae {
         const dim3 cog((g.w + kCoTile - 1) / kCoTile, (g.h + kCoTile - 1) / kCoTile);
         const uint32_t c8 = (conv_out.ci + 7) / 8 * 8;
         const size_t lds = size_t(kCoTile + 2) * (kCoTile + 2) * (c8 + 8) * 2;
-        vae_conv_out_kernel<<<cog, 256, lds, stream>>>(normed ? normed : na, normed ? 96 : conv_out.cip(),
-                                                       conv_out.cip(), c8, g, conv_out.w, conv_out.b, out,
-                                                       probe ? yp : nullptr, conv_out.cop());
+        if (c8 == 96)
+            vae_conv_out96_kernel<<<cog, 256, 0, stream>>>(normed ? normed : na, normed ? 96 : conv_out.cip(),
+                                                           conv_out.cip(), g, conv_out.w, conv_out.b, out,
+                                                           probe ? yp : nullptr, conv_out.cop());
+        else
+            vae_conv_out_kernel<<<cog, 256, lds, stream>>>(normed ? normed : na, normed ? 96 : conv_out.cip(),
+                                                           conv_out.cip(), c8, g, conv_out.w, conv_out.b, out,
+                                                           probe ? yp : nullptr, conv_out.cop());
         MK_LAUNCH_CHECK("vae_conv_out");
         MK_TRY(probe_grid("vae_out", -1, yp, conv_out.cop(), g, 3));
         return MK_OK;
