@@ -39,7 +39,7 @@ struct AttnP {
 constexpr int kKT = 64; // keys per tile
 // Lazy rescaling: the running max the exponentials use moves only when a row max exceeds it by more than 2^8, so
 // P <= 256 (exact enough in bf16, far from fp32 overflow) and the output is rescaled on few tiles.
-constexpr float kLazy = 8.0f;
+constexpr float kLazy = 8.0f, kLazyP = 256.0f; // kLazyP = 2^kLazy
 
 typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2;
 
@@ -355,9 +355,9 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     // U: one 64-key tile with the softmax work in the matrix core's shadow. The scores arrive as S - m, so each
     // half's probabilities are computed speculatively, before its row max is known: P = 2^(S - m) is what the tile
     // needs whenever no score exceeds m by more than kLazy. The exponentials, conversions and row sums of half a then
-    // run in chunks between the S^T MFMAs of half b, those of half b between the P V MFMAs of half a, and the row max
-    // only decides afterwards whether a half is redone against a new m (the first half of the pass, and the rare
-    // tiles whose max jumps). EDGE tiles (ragged key end, causal diagonal, a masked key range) mask scores in the
+    // run in chunks between the S^T MFMAs of half b, those of half b between the P V MFMAs of half a, and the lane's
+    // part of the row sum only decides afterwards whether a half is redone against a new m (the first half of the
+    // pass, and the rare tiles whose max jumps: a score more than kLazy above m puts that sum above 2^kLazy). EDGE tiles (ragged key end, causal diagonal, a masked key range) mask scores in the
     // chunks.
     constexpr int CH = 16 / DS;                  // scores per chunk: DS S^T MFMAs (= 2 DT P V MFMAs) per half
     auto tile_u = [&](int t, auto buf_c, auto edge_c) {
@@ -379,7 +379,7 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
         };
         // chunk c of a half: scores 2j, 2j + 1 for pairs j of the chunk -> a packed pair pw[j], row-sum partials,
         // pair max
-        auto chunk = [&](f32x16& sc, int k0, uint32_t (&pw)[8], float (&ls)[4], float (&mp)[8], int c) {
+        auto chunk = [&](f32x16& sc, int k0, uint32_t (&pw)[8], float (&ls)[4], int c) {
 #pragma unroll
             for (int i = 0; i < CH / 2; ++i) {
                 const int j = c * (CH / 2) + i;
@@ -396,20 +396,15 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
                 }
                 pw[j] = X::pack(__builtin_amdgcn_exp2f(x0), __builtin_amdgcn_exp2f(x1));
                 ls[j % 4] = X::sum2(pw[j], ls[j % 4]);
-                mp[j] = max2(x0, x1);
                 // pinned here: the redo path overwrites them, so the compiler would otherwise sink the
                 // speculative work out of the MFMA shadow into the path that keeps it
                 asm volatile("" : "+v"(pw[j]), "+v"(ls[j % 4]));
             }
         };
-        auto half_max = [&](const float (&mp)[8]) {
-            const float a = max2(max2(mp[0], mp[1]), max2(mp[2], mp[3]));
-            const float b = max2(max2(mp[4], mp[5]), max2(mp[6], mp[7]));
-            return max_xor32(max2(a, b));
-        };
         // moves m to cover the half's max (the pass's first half: to its max), rescales what was accumulated against
         // the old m, and redoes the half's probabilities and row sum
-        auto redo = [&](f32x16& sc, uint32_t (&pw)[8], float& lh, float mx, bool first, f32x16* other) {
+        auto redo = [&](f32x16& sc, uint32_t (&pw)[8], float& lh, bool first, f32x16* other) {
+            const float mx = max_xor32(max16(sc));
             const float mn = float((E)(m + (first ? mx : fmaxf(mx, 0.0f))));
             const float dm = mn - m;
             const float alpha = first ? 1.0f : __builtin_amdgcn_exp2f(-dm);
@@ -461,7 +456,7 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
         s_b = X::mfma(HOLE ? kbias(k0 + 32 + r32) : kone, qm, f32x16{}, 0, 0, 0);
         __builtin_amdgcn_sched_barrier(0);
         uint32_t pa[8], pbw[8];
-        float lsa[4] = {0.0f, 0.0f, 0.0f, 0.0f}, lsb[4] = {0.0f, 0.0f, 0.0f, 0.0f}, mpa[8], mpb[8];
+        float lsa[4] = {0.0f, 0.0f, 0.0f, 0.0f}, lsb[4] = {0.0f, 0.0f, 0.0f, 0.0f};
         // S^T of half b || softmax of half a
 #pragma unroll
         for (int ds = 0; ds < DS; ++ds) {
@@ -469,15 +464,14 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
             __builtin_amdgcn_sched_barrier(0);
             rd(DS + ds + LA);
             __builtin_amdgcn_sched_barrier(0);
-            chunk(s_a, k0, pa, lsa, mpa, ds);
+            chunk(s_a, k0, pa, lsa, ds);
             __builtin_amdgcn_sched_barrier(0);
         }
+        // a score more than kLazy above m makes its P, and so the lane's row-sum part, exceed 2^kLazy (P >= 0, and
+        // an overflow is +inf); a larger sum of smaller P only redoes a half that needed none
         float la = (lsa[0] + lsa[1]) + (lsa[2] + lsa[3]);
-        {
-            const float mx = half_max(mpa);
-            if (t == 0 || __any(mx > kLazy))
-                redo(s_a, pa, la, mx, t == 0, &s_b);
-        }
+        if (t == 0 || __any(la > kLazyP))
+            redo(s_a, pa, la, t == 0, &s_b);
         l += la;
         __builtin_amdgcn_sched_barrier(0);
         const u32x4 pA[2] = {u32x4{pa[0], pa[1], pa[2], pa[3]}, u32x4{pa[4], pa[5], pa[6], pa[7]}};
@@ -489,15 +483,12 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
             __builtin_amdgcn_sched_barrier(0);
             rd(2 * DS + j + LA);
             __builtin_amdgcn_sched_barrier(0);
-            chunk(s_b, k0 + 32, pbw, lsb, mpb, j);
+            chunk(s_b, k0 + 32, pbw, lsb, j);
             __builtin_amdgcn_sched_barrier(0);
         }
         float lb = (lsb[0] + lsb[1]) + (lsb[2] + lsb[3]);
-        {
-            const float mx = half_max(mpb);
-            if (__any(mx > kLazy))
-                redo(s_b, pbw, lb, mx, false, nullptr);
-        }
+        if (__any(lb > kLazyP))
+            redo(s_b, pbw, lb, false, nullptr);
         l += lb;
         __builtin_amdgcn_sched_barrier(0);
         const u32x4 pB[2] = {u32x4{pbw[0], pbw[1], pbw[2], pbw[3]}, u32x4{pbw[4], pbw[5], pbw[6], pbw[7]}};
