@@ -377,9 +377,9 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
                 fv[j] = *reinterpret_cast<const V8*>(&sV[buf][d * kKT + (((2 * s2 + hk) ^ ((d >> 1) & 7)) << 3)]);
             }
         };
-        // chunk c of a half: scores 2j, 2j + 1 for pairs j of the chunk -> a packed pair pw[j], row-sum partials,
-        // pair max
-        auto chunk = [&](f32x16& sc, int k0, uint32_t (&pw)[8], float (&ls)[4], int c) {
+        // chunk c of a half: scores 2j, 2j + 1 for pairs j of the chunk -> a packed pair pw[j], added to the lane's
+        // row-sum part ls (one chain: its links sit an MFMA apart, and one accumulator needs no zeroing or final adds)
+        auto chunk = [&](f32x16& sc, int k0, uint32_t (&pw)[8], float& ls, int c) {
 #pragma unroll
             for (int i = 0; i < CH / 2; ++i) {
                 const int j = c * (CH / 2) + i;
@@ -395,10 +395,10 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
                     sc[2 * j + 1] = x1;
                 }
                 pw[j] = X::pack(__builtin_amdgcn_exp2f(x0), __builtin_amdgcn_exp2f(x1));
-                ls[j % 4] = X::sum2(pw[j], ls[j % 4]);
+                ls = X::sum2(pw[j], ls);
                 // pinned here: the redo path overwrites them, so the compiler would otherwise sink the
                 // speculative work out of the MFMA shadow into the path that keeps it
-                asm volatile("" : "+v"(pw[j]), "+v"(ls[j % 4]));
+                asm volatile("" : "+v"(pw[j]), "+v"(ls));
             }
         };
         // moves m to cover the half's max (the pass's first half: to its max), rescales what was accumulated against
@@ -424,13 +424,13 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
 #pragma unroll
                 for (int r = 0; r < 16; ++r)
                     oacc[dt][r] *= alpha;
-            float ls[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            float ls = 0.0f;
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 pw[j] = X::pack(__builtin_amdgcn_exp2f(sc[2 * j]), __builtin_amdgcn_exp2f(sc[2 * j + 1]));
-                ls[j % 4] = X::sum2(pw[j], ls[j % 4]);
+                ls = X::sum2(pw[j], ls);
             }
-            lh = (ls[0] + ls[1]) + (ls[2] + ls[3]);
+            lh = ls;
         };
         const int k0 = t * kKT;
 #pragma unroll
@@ -456,7 +456,7 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
         s_b = X::mfma(HOLE ? kbias(k0 + 32 + r32) : kone, qm, f32x16{}, 0, 0, 0);
         __builtin_amdgcn_sched_barrier(0);
         uint32_t pa[8], pbw[8];
-        float lsa[4] = {0.0f, 0.0f, 0.0f, 0.0f}, lsb[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        float la = 0.0f, lb = 0.0f;
         // S^T of half b || softmax of half a
 #pragma unroll
         for (int ds = 0; ds < DS; ++ds) {
@@ -464,12 +464,11 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
             __builtin_amdgcn_sched_barrier(0);
             rd(DS + ds + LA);
             __builtin_amdgcn_sched_barrier(0);
-            chunk(s_a, k0, pa, lsa, ds);
+            chunk(s_a, k0, pa, la, ds);
             __builtin_amdgcn_sched_barrier(0);
         }
         // a score more than kLazy above m makes its P, and so the lane's row-sum part, exceed 2^kLazy (P >= 0, and
         // an overflow is +inf); a larger sum of smaller P only redoes a half that needed none
-        float la = (lsa[0] + lsa[1]) + (lsa[2] + lsa[3]);
         if (t == 0 || __any(la > kLazyP))
             redo(s_a, pa, la, t == 0, &s_b);
         l += la;
@@ -483,10 +482,9 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
             __builtin_amdgcn_sched_barrier(0);
             rd(2 * DS + j + LA);
             __builtin_amdgcn_sched_barrier(0);
-            chunk(s_b, k0 + 32, pbw, lsb, j);
+            chunk(s_b, k0 + 32, pbw, lb, j);
             __builtin_amdgcn_sched_barrier(0);
         }
-        float lb = (lsb[0] + lsb[1]) + (lsb[2] + lsb[3]);
         if (__any(lb > kLazyP))
             redo(s_b, pbw, lb, false, nullptr);
         l += lb;
