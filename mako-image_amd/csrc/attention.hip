@@ -103,11 +103,16 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     typedef typename X::e E;
     constexpr int DS = D / 16, DT = D / 32, KC = D / 8;
     constexpr int RK = kKT * KC / 256, RV = D * 8 / 256;
-    constexpr int NB = 2;
-    __shared__ __attribute__((aligned(16))) uint16_t sK[NB][kKT * D];
-    __shared__ __attribute__((aligned(16))) uint16_t sV[NB][D * kKT];
+    // the two buffers are separate objects, so the compiler can tell a direct load into one from the fragment reads
+    // of the other (with one array indexed by the buffer it waits for the loads before each read)
+    __shared__ __attribute__((aligned(16))) uint16_t sK0[kKT * D], sK1[kKT * D];
+    __shared__ __attribute__((aligned(16))) uint16_t sV0[D * kKT], sV1[D * kKT];
+    auto sK = [&](int b) { return b ? sK1 : sK0; };
+    auto sV = [&](int b) { return b ? sV1 : sV0; };
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, r32 = lane & 31, hk = lane >> 5;
+    // (the direct loads' LDS bases from a uniform copy of the wave index: scalar, no v_readfirstlane before a load)
+    const int wave_s = __builtin_amdgcn_readfirstlane(wave);
     auto kswz = [](int key, int c) { return KC == 16 ? c ^ (key & 15) : c ^ ((key >> 1) & 7); };
     // XCD-aware order: workgroup i runs on XCD i % 8 (round-robin dispatch), so give each XCD a contiguous run of
     // (batch, head, query block) items: the query blocks of one head then share its K / V in that XCD's L2, instead
@@ -162,18 +167,18 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     auto dma1 = [&](int t, int buf, int i) {
         const uint32_t k0 = uint32_t(min(t, ntiles - 1) * kKT);
         if (i < RK)
-            buf_load_lds16(rsK, (lds_void*)&sK[buf][(i * 4 + wave) * 512], ok[i], k0 * D * 2);
+            buf_load_lds16(rsK, (lds_void*)&sK(buf)[(i * 4 + wave_s) * 512], ok[i], k0 * D * 2);
         else if (i < RK + RV)
-            buf_load_lds16(rsV, (lds_void*)&sV[buf][((i - RK) * 4 + wave) * 512], ov[i - RK], k0 * 2);
+            buf_load_lds16(rsV, (lds_void*)&sV(buf)[((i - RK) * 4 + wave_s) * 512], ov[i - RK], k0 * 2);
     };
     auto issue = [&](int t, int buf) {
         const uint32_t k0 = uint32_t(min(t, ntiles - 1) * kKT);
 #pragma unroll
         for (int i = 0; i < RK; ++i)
-            buf_load_lds16(rsK, (lds_void*)&sK[buf][(i * 4 + wave) * 512], ok[i], k0 * D * 2);
+            buf_load_lds16(rsK, (lds_void*)&sK(buf)[(i * 4 + wave_s) * 512], ok[i], k0 * D * 2);
 #pragma unroll
         for (int i = 0; i < RV; ++i)
-            buf_load_lds16(rsV, (lds_void*)&sV[buf][(i * 4 + wave) * 512], ov[i], k0 * 2);
+            buf_load_lds16(rsV, (lds_void*)&sV(buf)[(i * 4 + wave_s) * 512], ov[i], k0 * 2);
     };
     // S^T of a 32-key half of a tile: value r <-> key 8(r/4) + 4hk + r%4 of the half
     V8 kone = {}, qm = {}; // U: ones at dim 0 (K side); -m at dim 0 (Q side), lanes of the first k half
@@ -303,11 +308,11 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
         auto rd = [&](int g) {
             if (g < 2 * DS) {
                 const int ds = g / 2, kt = g % 2, key = kt * 32 + r32, c = kswz(key, ds * 2 + hk);
-                fk[g] = *reinterpret_cast<const V8*>(&sK[buf][key * D + c * 8]);
+                fk[g] = *reinterpret_cast<const V8*>(&sK(buf)[key * D + c * 8]);
             } else if (g < 2 * DS + 4 * DT) {
                 const int j = g - 2 * DS, kt = j / (2 * DT), dt = (j % (2 * DT)) % DT, st = (j % (2 * DT)) / DT;
                 const int d = dt * 32 + r32, s2 = 2 * kt + st;
-                fv[j] = *reinterpret_cast<const V8*>(&sV[buf][d * kKT + (((2 * s2 + hk) ^ ((d >> 1) & 7)) << 3)]);
+                fv[j] = *reinterpret_cast<const V8*>(&sV(buf)[d * kKT + (((2 * s2 + hk) ^ ((d >> 1) & 7)) << 3)]);
             }
         };
 #pragma unroll
@@ -370,11 +375,11 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
         auto rd = [&](int g) {
             if (g < 2 * DS) {
                 const int kt = g / DS, ds = g % DS, key = kt * 32 + r32, c = kswz(key, ds * 2 + hk);
-                fk[g] = *reinterpret_cast<const V8*>(&sK[buf][key * D + c * 8]);
+                fk[g] = *reinterpret_cast<const V8*>(&sK(buf)[key * D + c * 8]);
             } else if (g < 2 * DS + 4 * DT) {
                 const int j = g - 2 * DS, kt = j / (2 * DT), dt = (j % (2 * DT)) % DT, st = (j % (2 * DT)) / DT;
                 const int d = dt * 32 + r32, s2 = 2 * kt + st;
-                fv[j] = *reinterpret_cast<const V8*>(&sV[buf][d * kKT + (((2 * s2 + hk) ^ ((d >> 1) & 7)) << 3)]);
+                fv[j] = *reinterpret_cast<const V8*>(&sV(buf)[d * kKT + (((2 * s2 + hk) ^ ((d >> 1) & 7)) << 3)]);
             }
         };
         // chunk c of a half: scores 2j, 2j + 1 for pairs j of the chunk -> a packed pair pw[j], added to the lane's
