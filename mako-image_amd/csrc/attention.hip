@@ -37,8 +37,9 @@ struct AttnP {
 };
 
 constexpr int kKT = 64; // keys per tile
-// Lazy rescaling: the running max the exponentials use moves only when a row max exceeds it by more than 2^8, so
-// P <= 256 (exact enough in bf16, far from fp32 overflow) and the output is rescaled on few tiles.
+// Lazy rescaling: the running max m the exponentials use moves only when a score exceeds it by more than kLazy (log2
+// units; the unit-scale path notices it as a row-sum part above 2^kLazy), so P stays near or below 256 (exact enough
+// in bf16, far from fp32 overflow) and the output is rescaled on few tiles.
 constexpr float kLazy = 8.0f, kLazyP = 256.0f; // kLazyP = 2^kLazy
 
 typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2;
@@ -362,8 +363,8 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     // needs whenever no score exceeds m by more than kLazy. The exponentials, conversions and row sums of half a then
     // run in chunks between the S^T MFMAs of half b, those of half b between the P V MFMAs of half a, and the lane's
     // part of the row sum only decides afterwards whether a half is redone against a new m (the first half of the
-    // pass, and the rare tiles whose max jumps: a score more than kLazy above m puts that sum above 2^kLazy). EDGE tiles (ragged key end, causal diagonal, a masked key range) mask scores in the
-    // chunks.
+    // pass, and the rare tiles whose max jumps: a score more than kLazy above m puts that sum above 2^kLazy). EDGE
+    // tiles (ragged key end, causal diagonal, a masked key range) mask scores in the chunks.
     constexpr int CH = 16 / DS;                  // scores per chunk: DS S^T MFMAs (= 2 DT P V MFMAs) per half
     auto tile_u = [&](int t, auto buf_c, auto edge_c) {
         constexpr int buf = decltype(buf_c)::value;

@@ -1566,7 +1566,8 @@ mk_status gemm_take_error()
 // 128 x 128 tiles is 2 per CU and an odd last tile costs half a pair; ties keep the larger tile. Convolutions also
 // have 256 x 192 tiles (8 waves, 0.78), for their 192- and 384-channel layers, and 128 x 96 tiles (4 waves on
 // 16 x 16 x 32, two workgroups a CU) for output channels that are an odd multiple of 96. The heads epilogue
-// takes 256 x 256 tiles for 128-dim heads and 128-channel tiles for 64-dim heads; fp8 weights 256-token tiles. 256 x 256 tiles use stream-K when whole waves leave at least 5% of the last wave's workgroups idle and
+// takes 256 x 256 tiles for 128-dim heads and 128-channel tiles for 64-dim heads; fp8 weights 256-token tiles.
+// 256 x 256 tiles use stream-K when whole waves leave at least 5% of the last wave's workgroups idle and
 // a tile is long (K of 6144 or more; measured, the partials' exchange costs about 24 k steps of a tile, more than the
 // balance saves on shorter tiles): the whole waves go round robin, the rest is split by k steps (at least 4 a
 // workgroup).

@@ -402,8 +402,9 @@ __global__ __launch_bounds__(256) void vae_conv_out96_kernel(const uint16_t* __r
     for (int tap = 0; tap < 9; ++tap)
 #pragma unroll
         for (int j = 0; j < 3; ++j)
-            wf[tap][j] = r16 < 3 ? *reinterpret_cast<const bf16x8*>(w + (uint64_t(r16) * 9 + tap) * cs + 32 * j + 8 * g4)
-                                 : bf16x8{};
+            wf[tap][j] = r16 < 3
+                             ? *reinterpret_cast<const bf16x8*>(w + (uint64_t(r16) * 9 + tap) * cs + 32 * j + 8 * g4)
+                             : bf16x8{};
     // neighbourhood pixel (qy, qx) is grid pixel (ty0 + qy - 1, tx0 + qx - 1): grid row slack + (ty0 + qy) (w + 2) +
     // tx0 + qx, inside the grid while ty0 + qy <= h + 1 and tx0 + qx <= w + 1 (zeros beyond). All of a thread's
     // loads go out before its LDS stores (a load-store loop would wait for each load in turn).
