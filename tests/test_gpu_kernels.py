@@ -597,6 +597,29 @@ def test_attention_unit_scale(gpu, rng, d, Tq, Tk, block, q_pos0, kscale):
     assert dd["min_cos"] > 0.9999 and dd["max_rel"] < 1e-2, dd
 
 
+# Scores that jump late in the key range (unit scale, bf16 and half): keys [s, s + 40) carry a logit some 30 log2
+# units above every earlier score, so the running max moves by far more than the lazy-rescale margin on a tile that
+# is not the first. Before that tile's redo its speculative probabilities reach 2^30 (+inf in half), and the lane's
+# row-sum part that decides the redo has to catch it.
+@pytest.mark.parametrize("dtype", [M.BF16, M.F16])
+@pytest.mark.parametrize("s", [600, 984])
+def test_attention_late_score_jump(gpu, rng, dtype, s):
+    B, H, Tq, Tk, d = 1, 2, 256, 1024, 128
+    rnd = R.f16_round if dtype == M.F16 else R.bf16_round
+    q = rng.standard_normal((B, H, Tq, d)).astype(np.float32)
+    q[..., 0] = 1.0
+    q = rnd(q)
+    kp = rng.standard_normal((B, H, Tk, d)).astype(np.float32) / np.sqrt(d) * np.log2(np.e)
+    kp[:, :, s:s + 40, 0] = 30.0
+    kp = rnd(kp)
+    v = rnd(rng.standard_normal((B, H, Tk, d)).astype(np.float32))
+    got = run_attention(q, kp, v, 0.0, dtype=dtype)
+    want = R.attention(q, kp, v, float(np.log(2.0)), 0, 0)
+    assert np.all(np.isfinite(got))
+    dd = R.diff(got, want, d)
+    assert dd["min_cos"] > 0.9999 and dd["max_rel"] < 1e-2, dd
+
+
 def test_attention_golden(gpu):
     import pathlib
     G = np.load(pathlib.Path(__file__).resolve().parent / "golden" / "golden.npz")
