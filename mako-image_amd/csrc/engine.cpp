@@ -879,6 +879,9 @@ struct mk_engine {
         ha.dtype = MK_F16;
         mk_heads_args hq = ha; // the cross attention's Q alone
         hq.k = hq.vt = nullptr;
+        // the self attention's K carries its softmax scale in log2 units (1 / sqrt(64) * log2(e)), so it runs the
+        // unit-scale attention (scores arrive as S - m from the matrix core; the softmax in the MFMAs' shadow)
+        ha.k_scale = 0.18033688011112042f;
         float* hs = x_img.f();
         const int64_t nc = int64_t(n) * c;
         MK_TRY(timed("norm", 0, [&] { return mk_group_norm(x, nb, n, c, 32, gn_g, gn_b, 1e-6f, xn_img.p, stream); }));
@@ -890,8 +893,8 @@ struct mk_engine {
             MK_TRY(gemm(B.qkv[0], xn_img.p, c, nc, n, nb, nullptr, 0, 0, MK_EPI_HEADS, MK_BF16, nullptr, 0, 0, 0, &ha,
                         "gemm.qkv"));
             MK_TRY(timed("attention", 4.0 * double(n) * n * 64 * H * nb, [&] {
-                return mk_attention(q.p, k.p, vt.p, att.p, MK_F16, nb, H, H, 64, n, q_pad, n, k_pad, c, nc, 0, 0, scale, nullptr,
-                                    stream);
+                return mk_attention(q.p, k.p, vt.p, att.p, MK_F16, nb, H, H, 64, n, q_pad, n, k_pad, c, nc, 0, 0, 0.0f,
+                                    nullptr, stream);
             }));
             MK_TRY(gemm(B.o[0], att.p, c, 0, nb * n, 1, hs, c, 0, MK_EPI_ADD, MK_F32, nullptr, 0, 0, 0, nullptr,
                         "gemm.o"));
