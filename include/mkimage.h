@@ -367,6 +367,12 @@ mk_status mk_engine_load(mk_engine* e, const char* name, const void* data, uint3
  * name + ".scale". A missing tensor, a wrong shape or a checkpoint with more blocks than the engine is MK_ERR_ARG
  * (the reference throws); other tensors in the files are ignored. `loaded` (may be NULL): tensors read. */
 mk_status mk_engine_load_safetensors(mk_engine* e, const char* path, uint64_t* loaded);
+/* mk_engine_load_safetensors with each name looked up under `prefix` first (NULL or "": none), then under the default
+ * prefixes: an SDXL spatial transformer inside a whole UNet checkpoint, as Sdxl::load_trans reads it under
+ * kUnet + its path (sdxl.cpp:264-306), e.g. prefix "model.diffusion_model.input_blocks.4.1." finds
+ * "...input_blocks.4.1.transformer_blocks.0.attn1.to_q.weight"; the block-count check then counts the blocks under
+ * the prefix only. */
+mk_status mk_engine_load_safetensors_at(mk_engine* e, const char* path, const char* prefix, uint64_t* loaded);
 /* Merge a LoRA file into the weights for good (the reference's add_lora with merging, engine.hpp:195-197; targets as
  * QwenImage::lora_target gives them, qwen_image.cpp:295-331: a module's rows inside the fused tensor that holds it).
  * Pairs <module>.lora_A.weight / .lora_B.weight or .lora_down.weight / .lora_up.weight, with an optional scalar
@@ -423,6 +429,11 @@ mk_status mk_sigmas(uint32_t steps, uint32_t tokens, const mk_schedule* sched, f
  * latents are copied to latents_out (host). Slot 0 (and slot 1 when guidance != 1) must have been begun. */
 mk_status mk_generate(mk_engine* e, const float* noise, size_t n, const float* sigmas, uint32_t steps, float guidance,
                       float* latents_out);
+/* The start noise Engine::generate draws when a request brings none (engine.cpp:398-408): out[i] =
+ * std::normal_distribution<float>{}(rng) in order over std::mt19937_64 rng(seed). Host arithmetic only. The engine
+ * is fixed by the C++ standard; the normal distribution's algorithm is the C++ library's, so the values equal the
+ * reference's where both are built against the same standard library (this build: libstdc++). */
+mk_status mk_noise(uint64_t seed, float* out, size_t n);
 
 /* Probe of intermediates (the reference's set_probe, tests/image_ref_test.cpp:133-136): called synchronously on the
  * host after a stage with its name ("temb", "modulation", "txt_in", "img_in", "block", "norm_out"), its layer

@@ -13,6 +13,7 @@
 #include <algorithm>
 #include <cmath>
 #include <map>
+#include <random>
 #include <string>
 #include <unordered_map>
 #include <memory>
@@ -182,6 +183,9 @@ struct mk_engine {
     // ---- scratch ----
     Buf x_img, x_txt, xn_img, xn_txt, q, k, vt, att, hid, out, lat, lat_bf, tn, tproj, temb_h, temb, mod, omod, qkv;
     Buf vpos; // the positive pass's velocity when guidance runs as two passes
+    Buf host_in, host_out; // mk_step_cfg's device copies of the caller's latents (kept: no allocation a step)
+    // ordering against a caller's stream (mk_step_cfg_device with another stream): created once, reused
+    hipEvent_t ord_in = nullptr, ord_out = nullptr;
 
     // ---- probe / timing ----
     mk_probe_fn probe = nullptr;
@@ -1011,6 +1015,10 @@ mk_status mk_engine_destroy(mk_engine* e)
         (void)hipEventDestroy(e->temb_ready);
     if (e->timing.ref)
         (void)hipEventDestroy(e->timing.ref);
+    if (e->ord_in)
+        (void)hipEventDestroy(e->ord_in);
+    if (e->ord_out)
+        (void)hipEventDestroy(e->ord_out);
     if (e->side)
         (void)hipStreamDestroy(e->side);
     (void)hipStreamDestroy(e->stream);
@@ -1133,11 +1141,10 @@ mk_status mk_step_cfg_device(mk_engine* e, const float* lat, float sigma, float 
     const size_t N = size_t(e->gh) * e->gw, L = e->cfg.latent;
     if (stream && stream != e->stream) {
         // order after the caller's stream
-        hipEvent_t ev;
-        MK_HIP(hipEventCreate(&ev));
-        MK_HIP(hipEventRecord(ev, static_cast<hipStream_t>(stream)));
-        MK_HIP(hipStreamWaitEvent(e->stream, ev, 0));
-        MK_HIP(hipEventDestroy(ev));
+        if (!e->ord_in)
+            MK_HIP(hipEventCreateWithFlags(&e->ord_in, hipEventDisableTiming));
+        MK_HIP(hipEventRecord(e->ord_in, static_cast<hipStream_t>(stream)));
+        MK_HIP(hipStreamWaitEvent(e->stream, e->ord_in, 0));
     }
     const float dt = sigma_next - sigma;
     if (e->cfg.family == MK_FAMILY_DUAL) {
@@ -1167,11 +1174,10 @@ mk_status mk_step_cfg_device(mk_engine* e, const float* lat, float sigma, float 
         }));
     }
     if (stream && stream != e->stream) {
-        hipEvent_t ev;
-        MK_HIP(hipEventCreate(&ev));
-        MK_HIP(hipEventRecord(ev, e->stream));
-        MK_HIP(hipStreamWaitEvent(static_cast<hipStream_t>(stream), ev, 0));
-        MK_HIP(hipEventDestroy(ev));
+        if (!e->ord_out)
+            MK_HIP(hipEventCreateWithFlags(&e->ord_out, hipEventDisableTiming));
+        MK_HIP(hipEventRecord(e->ord_out, e->stream));
+        MK_HIP(hipStreamWaitEvent(static_cast<hipStream_t>(stream), e->ord_out, 0));
     }
     if (e->timing.on)
         MK_TRY(e->finish_timing());
@@ -1186,14 +1192,26 @@ mk_status mk_step_cfg(mk_engine* e, const float* latents, size_t n, float sigma,
     const size_t N = size_t(e->gh) * e->gw, L = e->cfg.latent;
     if (n != N * L)
         return fail(MK_ERR_ARG, "latents must be [h * w][" + std::to_string(L) + "]");
-    Buf in, out;
-    MK_TRY(in.ensure(n * 4));
-    MK_TRY(out.ensure(n * 4));
-    MK_HIP(hipMemcpy(in.p, latents, n * 4, hipMemcpyHostToDevice));
-    MK_TRY(mk_step_cfg_device(e, in.f(), sigma, sigma_next, guidance, out.f(), nullptr));
+    // the engine's buffers (grown once, then reused: a steady-state call allocates nothing)
+    MK_TRY(e->host_in.ensure(n * 4));
+    MK_TRY(e->host_out.ensure(n * 4));
+    MK_HIP(hipMemcpyAsync(e->host_in.p, latents, n * 4, hipMemcpyHostToDevice, e->stream));
+    MK_TRY(mk_step_cfg_device(e, e->host_in.f(), sigma, sigma_next, guidance, e->host_out.f(), nullptr));
+    MK_HIP(hipMemcpyAsync(latents_out, e->host_out.p, n * 4, hipMemcpyDeviceToHost, e->stream));
     MK_HIP(hipStreamSynchronize(e->stream));
     MK_TRY(gemm_take_error());
-    MK_HIP(hipMemcpy(latents_out, out.p, n * 4, hipMemcpyDeviceToHost));
+    return MK_OK;
+}
+
+mk_status mk_noise(uint64_t seed, float* out, size_t n)
+{
+    if (!out && n)
+        return fail(MK_ERR_ARG, "noise: null");
+    // the reference's two lines (engine.cpp:399-400, 406-407): one engine, one distribution, the values in order
+    std::mt19937_64 rng(seed);
+    std::normal_distribution<float> nd;
+    for (size_t i = 0; i < n; ++i)
+        out[i] = nd(rng);
     return MK_OK;
 }
 
@@ -1441,8 +1459,11 @@ bool float_dtype(uint32_t dt) { return dt == MK_F32 || dt == MK_BF16 || dt == MK
 // Checkpoint name under the prefixes single-file checkpoints use.
 const char* const kPrefixes[] = {"", "model.diffusion_model.", "transformer."};
 
-bool find_prefixed(const mk_st* st, const std::string& name, mk_st_tensor* t)
+bool find_prefixed(const mk_st* st, const std::string& name, mk_st_tensor* t, const std::string& first = "")
 {
+    // a caller-given prefix (an SDXL spatial transformer's place in its UNet) first, then the defaults
+    if (!first.empty() && mk_st_find(st, (first + name).c_str(), t) == MK_OK)
+        return true;
     for (const char* p : kPrefixes) {
         const std::string n = p + name;
         if (mk_st_find(st, n.c_str(), t) == MK_OK)
@@ -1462,18 +1483,29 @@ extern "C" {
 
 mk_status mk_engine_load_safetensors(mk_engine* e, const char* path, uint64_t* loaded)
 {
+    return mk_engine_load_safetensors_at(e, path, nullptr, loaded);
+}
+
+mk_status mk_engine_load_safetensors_at(mk_engine* e, const char* path, const char* prefix, uint64_t* loaded)
+{
     if (!e || !path)
         return fail(MK_ERR_ARG, "engine_load_safetensors: null");
+    const std::string pre = prefix ? prefix : "";
     mk_st* raw_st = nullptr;
     MK_TRY(mk_st_open(path, &raw_st));
     std::unique_ptr<mk_st, StClose> st(raw_st);
-    // a checkpoint with more blocks than the engine was made for
+    // a checkpoint with more blocks than the engine was made for (with a prefix: the blocks under it)
     size_t count = 0;
     MK_TRY(mk_st_count(st.get(), &count, nullptr));
     for (size_t i = 0; i < count; ++i) {
         mk_st_tensor t;
         MK_TRY(mk_st_at(st.get(), i, &t));
         std::string n = t.name;
+        if (!pre.empty()) {
+            if (n.rfind(pre, 0) != 0)
+                continue;
+            n = n.substr(pre.size());
+        }
         for (const char* p : kPrefixes)
             if (*p && n.rfind(p, 0) == 0)
                 n = n.substr(strlen(p));
@@ -1494,8 +1526,8 @@ mk_status mk_engine_load_safetensors(mk_engine* e, const char* path, uint64_t* l
     std::vector<Job> jobs;
     for (const auto& [name, d] : e->dests) {
         Job j{&d, {}, {}};
-        if (!find_prefixed(st.get(), name, &j.t))
-            return fail(MK_ERR_ARG, "load_safetensors: the checkpoint has no tensor " + name);
+        if (!find_prefixed(st.get(), name, &j.t, pre))
+            return fail(MK_ERR_ARG, "load_safetensors: the checkpoint has no tensor " + pre + name);
         const mk_st_tensor& t = j.t;
         const bool matrix = d.cols > 1;
         const bool shape_ok = matrix ? t.ndim == 2 && t.dims[0] == d.cols && t.dims[1] == d.rows
@@ -1512,7 +1544,7 @@ mk_status mk_engine_load_safetensors(mk_engine* e, const char* path, uint64_t* l
             if (d.dtype != MK_FP8_E4M3)
                 return fail(MK_ERR_ARG, "load_safetensors: " + name + " is F8_E4M3 but the engine stores it as " +
                                             dtype_label(d.dtype));
-            if (!find_prefixed(st.get(), name + ".scale", &j.scale) || numel(j.scale) != d.rows ||
+            if (!find_prefixed(st.get(), name + ".scale", &j.scale, pre) || numel(j.scale) != d.rows ||
                 !float_dtype(j.scale.dtype))
                 return fail(MK_ERR_ARG, "load_safetensors: F8_E4M3 " + name + " needs its per-row scale " + name +
                                             ".scale (" + std::to_string(d.rows) + " values)");

@@ -4,7 +4,9 @@
 #include "common.hpp"
 
 #include <cmath>
+#include <algorithm>
 #include <mutex>
+#include <vector>
 
 namespace mk {
 
@@ -884,16 +886,52 @@ static mk_status group_norm_run(const float* x, uint32_t batch, uint32_t rows, u
     return MK_OK;
 }
 
+// mk_group_norm's partial sums: one buffer a device, grown (stream-ordered) when a call needs more and kept, so a
+// steady-state call allocates nothing. A call's stream first waits for the event of the buffer's previous user (any
+// stream), and records it after its own kernels: calls on different streams take turns on the buffer.
+struct GnScratch {
+    int dev = -1;
+    char* p = nullptr;
+    size_t bytes = 0;
+    hipEvent_t last = nullptr;
+};
+static std::mutex g_gn_mutex;
+static std::vector<GnScratch> g_gn;
+
 mk_status mk_group_norm(const float* x, uint32_t batch, uint32_t rows, uint32_t c, uint32_t groups, const float* g,
                         const float* b, float eps, void* y, void* stream)
 {
     MK_TRY(group_norm_check(x, batch, c, groups, g, b, y));
     if (!rows)
         return MK_OK;
-    char* ws = nullptr;
-    MK_HIP(hipMallocAsync(reinterpret_cast<void**>(&ws), group_norm_scratch(batch, rows, groups), S(stream)));
-    const mk_status st = group_norm_run(x, batch, rows, c, groups, g, b, eps, y, ws, S(stream));
-    MK_HIP(hipFreeAsync(ws, S(stream)));
+    int dev = 0;
+    MK_HIP(hipGetDevice(&dev));
+    const hipStream_t s = S(stream);
+    std::lock_guard<std::mutex> lock(g_gn_mutex);
+    GnScratch* w = nullptr;
+    for (GnScratch& e : g_gn)
+        if (e.dev == dev)
+            w = &e;
+    if (!w) {
+        g_gn.push_back(GnScratch{});
+        w = &g_gn.back();
+        w->dev = dev;
+        MK_HIP(hipEventCreateWithFlags(&w->last, hipEventDisableTiming));
+        MK_HIP(hipEventRecord(w->last, s));
+    }
+    MK_HIP(hipStreamWaitEvent(s, w->last, 0));
+    const size_t need = group_norm_scratch(batch, rows, groups);
+    if (need > w->bytes) {
+        if (w->p)
+            MK_HIP(hipFreeAsync(w->p, s));
+        w->p = nullptr;
+        w->bytes = 0;
+        const size_t bytes = std::max(need, size_t(1) << 20);
+        MK_HIP(hipMallocAsync(reinterpret_cast<void**>(&w->p), bytes, s));
+        w->bytes = bytes;
+    }
+    const mk_status st = group_norm_run(x, batch, rows, c, groups, g, b, eps, y, w->p, s);
+    MK_HIP(hipEventRecord(w->last, s));
     return st;
 }
 

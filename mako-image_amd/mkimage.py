@@ -5,6 +5,7 @@ library must be built (`make -C mako-image_amd`); nothing here falls back to a C
 """
 from __future__ import annotations
 
+import bisect
 import ctypes as C
 import pathlib
 
@@ -121,6 +122,7 @@ _SIGS = {
     "mk_step_cfg": (_i, [_vp, _vp, _sz, _f, _f, _f, _vp]),
     "mk_step_cfg_device": (_i, [_vp, _vp, _f, _f, _f, _vp, _vp]),
     "mk_engine_stream": (_i, [_vp, C.POINTER(_vp)]),
+    "mk_noise": (_i, [_u64, _vp, _sz]),
     "mk_sigmas": (_i, [_u32, _u32, C.POINTER(Schedule), _vp]),
     "mk_generate": (_i, [_vp, _vp, _sz, _vp, _u32, _f, _vp]),
     "mk_engine_set_probe": (_i, [_vp, PROBE, _vp]),
@@ -136,6 +138,7 @@ _SIGS = {
     "mk_st_find": (_i, [_vp, C.c_char_p, C.POINTER(StTensor)]),
     "mk_st_read": (_i, [_vp, C.c_char_p, _vp, _sz]),
     "mk_engine_load_safetensors": (_i, [_vp, C.c_char_p, C.POINTER(_u64)]),
+    "mk_engine_load_safetensors_at": (_i, [_vp, C.c_char_p, C.c_char_p, C.POINTER(_u64)]),
     "mk_engine_add_lora": (_i, [_vp, C.c_char_p, _f, C.POINTER(_u64), C.POINTER(_u64)]),
     "mk_engine_tensor_count": (_i, [_vp, C.POINTER(_sz)]),
     "mk_engine_tensor_at": (_i, [_vp, _sz, C.POINTER(C.c_char_p), C.POINTER(_u32), C.POINTER(_u64),
@@ -178,6 +181,9 @@ def check(status, what=""):
 
 
 def call(name, *args):
+    chk = _EXTENT_CHECKS.get(name)
+    if chk is not None:
+        chk(*args)
     check(getattr(lib(), name)(*args), name)
 
 
@@ -205,6 +211,7 @@ def _free_pending():
 
 def _release(p, nbytes):
     global _pending_bytes, _pending_status
+    unregister(p)
     _pending.append(p)
     _pending_bytes += nbytes
     if _pending_bytes >= _PENDING_LIMIT:
@@ -216,6 +223,120 @@ def _release(p, nbytes):
             _free_pending()
 
 
+# ---------------------------------------------------------------------------------------------------------------
+# operand extents: call() checks every device operand of a GEMM, convolution or attention launch against the
+# allocation it points into before the launch, so an undersized buffer is refused (MkError) instead of overrun
+# ---------------------------------------------------------------------------------------------------------------
+
+_starts = []      # sorted start addresses of the known allocations
+_extent = {}      # start -> bytes
+STRICT = False    # True: an operand outside every known allocation is refused as well (the tests set it)
+
+
+def register(p, nbytes):
+    """Makes device memory not allocated through Dev (e.g. another library's tensor) known to the checks."""
+    p, nbytes = int(p), int(nbytes)
+    if p not in _extent:
+        bisect.insort(_starts, p)
+    _extent[p] = nbytes
+
+
+def unregister(p):
+    p = int(p)
+    if _extent.pop(p, None) is not None:
+        del _starts[bisect.bisect_left(_starts, p)]
+
+
+def check_extent(p, nbytes, what):
+    """Raises MkError unless bytes [p, p + nbytes) lie inside one known allocation (p None/0 or nbytes <= 0: nothing
+    to check; an unknown p passes unless STRICT)."""
+    if not p or nbytes <= 0:
+        return
+    p = int(p)
+    i = bisect.bisect_right(_starts, p) - 1
+    if i < 0 or p >= _starts[i] + _extent[_starts[i]]:
+        if STRICT:
+            raise MkError(f"{what}: {p:#x} is not inside any known device allocation")
+        return
+    end = _starts[i] + _extent[_starts[i]]
+    if p + nbytes > end:
+        raise MkError(f"{what}: needs {nbytes} bytes from {p:#x}, its allocation holds {end - p}")
+
+
+def _struct(arg, cls):
+    """The structure a byref() / pointer() / address argument points at."""
+    if isinstance(arg, cls):
+        return arg
+    obj = getattr(arg, "_obj", None)   # C.byref(x)
+    if isinstance(obj, cls):
+        return obj
+    if hasattr(arg, "contents"):       # C.pointer(x)
+        return arg.contents
+    addr = arg.value if isinstance(arg, C.c_void_p) else int(arg)
+    return cls.from_address(addr)
+
+
+def gemm_extents(g, what="mk_gemm"):
+    """The bytes each operand of one mk_gemm_args problem spans, checked (include/mkimage.h)."""
+    if g.M == 0 or g.N == 0:
+        return
+    b = max(int(g.batch), 1)
+    glu = g.epilogue in (EPI_SWIGLU, EPI_GEGLU)
+    check_extent(g.a, ((b - 1) * g.stride_a + (g.M - 1) * g.lda + g.K) * 2, what + ": A")
+    check_extent(g.w, g.N * g.K * (1 if g.w_dtype == FP8 else 2), what + ": W")
+    check_extent(g.wscale, g.N * 4, what + ": wscale")
+    check_extent(g.bias, g.N * 4, what + ": bias")
+    if g.epilogue in (EPI_GATE_ADD, EPI_GATE_TANH):
+        check_extent(g.gate, (g.N + (max(int(g.gate_alt), 0) if g.split else 0)) * 4, what + ": gate")
+    if g.epilogue == EPI_HEADS:
+        if not g.heads:
+            return
+        h = g.heads.contents
+        d = h.head_dim
+        check_extent(h.q, b * h.heads * h.q_pad * d * 2, what + ": heads q")
+        check_extent(h.k, b * h.heads * h.k_pad * d * 2, what + ": heads k")
+        check_extent(h.vt, b * h.heads * d * h.k_pad * 2, what + ": heads vt")
+        check_extent(h.norm_q, d * 4, what + ": norm_q")
+        check_extent(h.norm_k, d * 4, what + ": norm_k")
+        if h.rope_mode:
+            check_extent(h.rope, ((b - 1) * h.rope_stride + (h.row0 + g.M) * 128) * 4, what + ": rope")
+    else:
+        cols = g.N // 2 if glu else g.N
+        check_extent(g.c, ((b - 1) * g.stride_c + (g.M - 1) * g.ldc + cols) * (4 if g.c_dtype == F32 else 2),
+                     what + ": C")
+
+
+def _check_gemm(args, stream=None):
+    gemm_extents(_struct(args, GemmArgs))
+
+
+def _check_gemm_grouped(args, count, stream=None):
+    addr = args.value if isinstance(args, C.c_void_p) else int(C.cast(args, C.c_void_p).value)
+    for i, g in enumerate((GemmArgs * int(count)).from_address(addr)):
+        gemm_extents(g, f"mk_gemm_grouped[{i}]")
+
+
+def _check_conv(args, stream=None):
+    a = _struct(args, ConvArgs)
+    grid = (a.h + 2) * (a.width + 2)
+    check_extent(a.x, (grid + 2 * (a.width + 3)) * a.c * 2, "mk_conv3x3: x (padded grid with slack rows)")
+    check_extent(a.w, a.n * 9 * a.c * 2, "mk_conv3x3: w")
+    check_extent(a.bias, a.n * 4, "mk_conv3x3: bias")
+    check_extent(a.y, ((grid - 1) * a.ldy + a.n) * (4 if a.y_dtype == F32 else 2), "mk_conv3x3: y")
+
+
+def _check_attention(q, k, vt, out, dtype, batch, heads, kv_heads, d, n_q, q_pad, n_k, k_pad, ldo, stride_o, *rest):
+    check_extent(q, batch * heads * q_pad * d * 2, "mk_attention: q")
+    check_extent(k, batch * kv_heads * k_pad * d * 2, "mk_attention: k")
+    check_extent(vt, batch * kv_heads * d * k_pad * 2, "mk_attention: vt")
+    if n_q:
+        check_extent(out, ((batch - 1) * stride_o + (n_q - 1) * ldo + heads * d) * 2, "mk_attention: out")
+
+
+_EXTENT_CHECKS = {"mk_gemm": _check_gemm, "mk_gemm_grouped": _check_gemm_grouped, "mk_conv3x3": _check_conv,
+                  "mk_attention": _check_attention}
+
+
 class Dev:
     """A device allocation (zero-filled). Dropping the object releases it after the next device-wide
     synchronisation (sync()), never before work already queued on it has run."""
@@ -225,6 +346,7 @@ class Dev:
         call("mk_malloc", C.byref(p), max(int(nbytes), 16))
         self.p = p.value
         self.nbytes = int(nbytes)
+        register(self.p, self.nbytes)
 
     @classmethod
     def from_array(cls, a):
@@ -467,10 +589,14 @@ class Engine:
     def init_random(self, seed):
         call("mk_engine_init_random", self.h, seed)
 
-    def load_safetensors(self, path):
-        """Every weight from a safetensors file or shard directory; returns the number of tensors read."""
+    def load_safetensors(self, path, prefix=None):
+        """Every weight from a safetensors file or shard directory; returns the number of tensors read. `prefix`: the
+        names are looked up under it first (an SDXL spatial transformer's path inside a UNet checkpoint)."""
         n = _u64()
-        call("mk_engine_load_safetensors", self.h, str(path).encode(), C.byref(n))
+        if prefix:
+            call("mk_engine_load_safetensors_at", self.h, str(path).encode(), prefix.encode(), C.byref(n))
+        else:
+            call("mk_engine_load_safetensors", self.h, str(path).encode(), C.byref(n))
         return n.value
 
     def add_lora(self, path, scale=1.0):
@@ -573,6 +699,14 @@ def sigmas(steps, tokens, terminal=0.0, mu=None, base_seq=256.0, max_seq=4096.0,
     sc = Schedule(base_seq, max_seq, base_shift, max_shift, terminal, mu is not None, 0.0 if mu is None else mu)
     out = np.empty(steps + 1, np.float32)
     call("mk_sigmas", steps, tokens, C.byref(sc), out.ctypes.data)
+    return out
+
+
+def noise(seed, n):
+    """The start noise Engine::generate draws for a seed (engine.cpp:398-408): n floats of
+    std::normal_distribution<float> over std::mt19937_64(seed) (mk_noise)."""
+    out = np.empty(int(n), np.float32)
+    call("mk_noise", int(seed), out.ctypes.data, int(n))
     return out
 
 

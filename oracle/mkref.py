@@ -282,6 +282,76 @@ def sigmas(steps, tokens, base_seq=256, max_seq=4096, base_shift=0.5, max_shift=
     return out
 
 
+_MASK64 = (1 << 64) - 1
+
+
+def mt19937_64(seed):
+    """std::mt19937_64 (the C++ standard's [rand.predef] parameters: w 64, n 312, m 156, r 31, a 0xB5026F5AA96619E9,
+    u 29 d 0x5555555555555555, s 17 b 0x71D67FFFEDA60000, t 37 c 0xFFF7EEE000000000, l 43, f 6364136223846793005):
+    a generator of its outputs, pure Python."""
+    n, m = 312, 156
+    mt = [seed & _MASK64]
+    for i in range(1, n):
+        mt.append((6364136223846793005 * (mt[-1] ^ (mt[-1] >> 62)) + i) & _MASK64)
+    upper, lower = _MASK64 ^ 0x7FFFFFFF, 0x7FFFFFFF
+    while True:
+        for i in range(n):
+            x = (mt[i] & upper) | (mt[(i + 1) % n] & lower)
+            xa = (x >> 1) ^ (0xB5026F5AA96619E9 if x & 1 else 0)
+            mt[i] = mt[(i + m) % n] ^ xa
+        for i in range(n):
+            y = mt[i]
+            y ^= (y >> 29) & 0x5555555555555555
+            y ^= (y << 17) & 0x71D67FFFEDA60000
+            y ^= (y << 37) & 0xFFF7EEE000000000
+            y ^= y >> 43
+            yield y
+
+
+def _u64_to_f32(v):
+    """An unsigned 64-bit integer rounded to the nearest float32 (ties to even), exactly as a C++ conversion does."""
+    if v.bit_length() <= 24:
+        return np.float32(v)
+    sh = v.bit_length() - 24
+    mant, rem, half = v >> sh, v & ((1 << sh) - 1), 1 << (sh - 1)
+    if rem > half or (rem == half and mant & 1):
+        mant += 1
+    return np.float32(float(mant) * 2.0 ** sh)
+
+
+def noise(seed, n):
+    """The start noise of Engine::generate (engine.cpp:398-408): n draws of std::normal_distribution<float> over
+    std::mt19937_64(seed), as libstdc++ computes them: generate_canonical<float, 24> is one 64-bit draw rounded to
+    float over 2^64 (a result of 1 becomes the float below 1), then Marsaglia's polar method: x, y = 2 u - 1
+    (float(2) u in float, minus the double 1.0, back to float), r2 = x x + y y in float, redrawn while r2 > 1 or
+    r2 == 0, mult = sqrt(-2 logf(r2) / r2); the call returns y mult and keeps x mult for the next call."""
+    logf = C.CDLL("libm.so.6").logf
+    logf.restype, logf.argtypes = C.c_float, [C.c_float]
+    gen = mt19937_64(seed)
+    one_below = np.nextafter(np.float32(1), np.float32(0))
+
+    def canonical():
+        u = _u64_to_f32(next(gen)) / np.float32(2.0 ** 64)
+        return one_below if u >= 1 else u
+
+    out = np.empty(n, np.float32)
+    saved = None
+    for i in range(n):
+        if saved is not None:
+            out[i], saved = saved, None
+            continue
+        while True:
+            x = np.float32(float(np.float32(2) * canonical()) - 1.0)
+            y = np.float32(float(np.float32(2) * canonical()) - 1.0)
+            r2 = x * x + y * y
+            if not (r2 > 1.0 or r2 == 0.0):
+                break
+        mult = np.sqrt(np.float32(-2) * np.float32(logf(r2)) / r2)
+        saved = x * mult
+        out[i] = y * mult
+    return out
+
+
 def patchify(lat, h, w):
     lat = f32(lat)
     C_ = lat.shape[0]

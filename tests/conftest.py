@@ -26,6 +26,8 @@ def gpu():
     if n < 1:
         pytest.fail("no GPU visible to the HIP runtime")
     mkimage.call("mk_set_device", 0)
+    # every GEMM / convolution / attention operand must lie inside a known allocation of the extent it needs
+    mkimage.STRICT = True
     return mkimage
 
 

@@ -114,6 +114,30 @@ def test_sharded_f32_checkpoint_with_prefix_round_trips(gpu, tmp_path, family, d
     same_state(state(e2), st)
 
 
+def test_sdxl_transformer_at_its_unet_path(gpu, tmp_path):
+    # a UNet checkpoint holding two spatial transformers (sdxl.cpp:264-306 reads each under kUnet + its path): the
+    # engine takes the one its prefix names, and the other's (deeper) blocks do not count against the engine's
+    e_a = M.Engine(M.FAMILY_SDXL, **SDXL)
+    e_a.init_random(21)
+    e_b = M.Engine(M.FAMILY_SDXL, **SDXL)
+    e_b.init_random(22)
+    ts = {}
+    for path, e in (("input_blocks.4.1.", e_a), ("output_blocks.2.1.", e_b)):
+        for k, (a, dt) in state(e).items():
+            ts["model.diffusion_model." + path + k] = torch.from_numpy(
+                M.bf16_to_f32(a) if dt == M.BF16 else a.astype(np.float32))
+    # a deeper transformer elsewhere in the UNet: more blocks than the engine holds
+    ts["model.diffusion_model.middle_block.1.transformer_blocks.9.norm1.weight"] = torch.zeros(8)
+    save_file(ts, str(tmp_path / "unet.safetensors"))
+    e = M.Engine(M.FAMILY_SDXL, **SDXL)
+    n = e.load_safetensors(tmp_path / "unet.safetensors", prefix="model.diffusion_model.output_blocks.2.1.")
+    assert n == len(state(e_b))
+    same_state(state(e), state(e_b))
+    # without the prefix the names are not found
+    with pytest.raises(M.MkError, match="no tensor"):
+        M.Engine(M.FAMILY_SDXL, **SDXL).load_safetensors(tmp_path / "unet.safetensors")
+
+
 def test_f16_checkpoint_rounds_like_torch(gpu, tmp_path):
     e = M.Engine(M.FAMILY_DUAL, **TINY)
     e.init_random(9)

@@ -141,6 +141,39 @@ def test_q21_steps_with_text_cache_match_oracle(gpu):
             within(got_p[("block", i)].reshape(-1, 512)[-N:], want_p[("block", i)].reshape(-1, 512)[-N:], 512)
 
 
+# The reference's own model at its own shape (qwen_image.hpp:37-38, the 2.1 graph of qwen_image.cpp:144-293): one block
+# of width 4096 (32 heads x 128, SwiGLU 12288, f16 heads, causal text prefix), a 64 x 64 latent grid (1024 x 1024
+# pixels) and 256 prompt rows of width 4096.
+Q21_FULL = dict(blocks=1, dim=4096, heads=32, head_dim=128, ffn=12288, text_dim=4096)
+
+
+def test_q21_full_shape_steps_with_text_cache_match_oracle(gpu):
+    # step 1 over [text; image], then step 2 over the image rows against the cached text K / V; the probes
+    # image_ref_test dit compares (tests/image_ref_test.cpp:127-164), each against the oracle's
+    m, e = make_pair(M.FAMILY_Q21, dims=Q21_FULL, seed=5)
+    h = w = 64
+    N, D = h * w, Q21_FULL["dim"]
+    prompt, lat = inputs(5, B=1, S=256, h=h, w=w, E=Q21_FULL["text_dim"])
+    e.begin(prompt[0], h, w, 0)
+    for step, sig in enumerate((0.9, 0.7)):
+        print(f"q21 full shape: step {step + 1}, sigma {sig}", flush=True)
+        got_p, want_p = {}, {}
+        e.set_probe(got_p)
+        got = e.step(lat[0], sig, 0)
+        e.set_probe(None)
+        want = m.q21_step(prompt[0], lat[0], h, w, sig, want_p)
+        d = within(got, want, 64)
+        print("  velocity", d, flush=True)
+        for name in ("temb", "modulation"):
+            within(got_p[(name, -1)], want_p[(name, -1)], D, cos=0.99999, max_rel=1e-3)
+        if ("txt_in", -1) in got_p:  # step 1 only: later steps reuse the cached text
+            within(got_p[("txt_in", -1)], want_p[("txt_in", -1)], D)
+        within(got_p[("img_in", -1)], want_p[("img_in", -1)], D)
+        for name, layer in (("block", 0), ("norm_out", -1)):  # the image rows (step 2 runs only those)
+            d = within(got_p[(name, layer)].reshape(-1, D)[-N:], want_p[(name, layer)].reshape(-1, D)[-N:], D)
+            print(f"  {name}", d, flush=True)
+
+
 def test_q21_step_errors(gpu):
     e = M.Engine(M.FAMILY_Q21, **Q21)
     with pytest.raises(M.MkError, match="before begin"):

@@ -71,7 +71,7 @@ def test_conv3x3_matches_torch(gpu, h, w, c, n, add):
     S = w + 3
     a = M.ConvArgs(int(dx), int(dw), int(db), int(dy) + S * n * 4, h, w, c, n, n, M.F32,
                    M.EPI_ADD if add else M.EPI_STORE)
-    M.check(M.lib().mk_conv3x3(ctypes.byref(a), None), "mk_conv3x3")
+    M.call("mk_conv3x3", ctypes.byref(a), None)
     M.sync()
     got = from_grid(dy.to_array(np.float32, y0.shape), h, w, n)
     xt = torch.from_numpy(M.bf16_to_f32(x)).double().permute(2, 0, 1)[None]
@@ -99,7 +99,7 @@ def test_conv3x3_bf16_output(gpu, h, w, c, n):
     dy = M.Dev.from_array(y0)
     S = w + 3
     a = M.ConvArgs(int(dx), int(dw), int(db), int(dy) + S * n * 2, h, w, c, n, n, M.BF16, M.EPI_STORE)
-    M.check(M.lib().mk_conv3x3(ctypes.byref(a), None), "mk_conv3x3")
+    M.call("mk_conv3x3", ctypes.byref(a), None)
     M.sync()
     out = dy.to_array(np.uint16, y0.shape)
     got = M.bf16_to_f32(from_grid(out, h, w, n))
