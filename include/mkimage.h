@@ -79,7 +79,9 @@ enum mk_epilogue {
     /* Gated linear units fused into the projection: W holds N = 2F rows [first part; second part] (the fused
      * gate|up matrix as upload_rows stacks it), C is [M][F] (ldc >= F): */
     MK_EPI_SWIGLU = 7,     /* C[r][i] = silu(acc[r][i]) * acc[r][F + i] (swiglu_rows, qwen_image.cpp:275-280) */
-    MK_EPI_GEGLU = 8       /* C[r][i] = acc[r][i] * gelu_erf(acc[r][F + i]) (geglu_rows, image.metal:475-484) */
+    MK_EPI_GEGLU = 8,      /* C[r][i] = acc[r][i] * gelu_erf(acc[r][F + i]) (geglu_rows, image.metal:475-484) */
+    MK_EPI_PAIR_SUM = 9    /* C[r][i] = acc[r][i] + acc[r][F + i]: an fp32 operand split into two halves (hi, lo)
+                            * stacked as the weight's two row halves, summed (the VAE attention's F32 V^T) */
 };
 
 typedef struct mk_heads_args {
@@ -106,11 +108,12 @@ typedef struct mk_heads_args {
 } mk_heads_args;
 
 typedef struct mk_gemm_args {
-    const void* a;        /* bf16 [batch][M][lda] */
-    const void* w;        /* [N][K] bf16 or fp8 */
+    const void* a;        /* [batch][M][lda] bf16 (f16 with f16 weights) */
+    const void* w;        /* [N][K] bf16, fp8, or f16 (then A is f16 too: the products of F16 weights and half
+                             activations, as the reference's VAE runs them) */
     const float* wscale;  /* [N] per-output-channel scale (fp8), or NULL */
     const float* bias;    /* [N] or NULL */
-    void* c;              /* output [batch][M][ldc] (f32 or bf16), or the fp32 residual X for GATE/ADD */
+    void* c;              /* output [batch][M][ldc] (f32, bf16 or f16), or the fp32 residual X for GATE/ADD */
     const float* gate;    /* [N] gate row (GATE_ADD / GATE_TANH); rows r % seg_rows < split read gate + gate_alt */
     int64_t gate_alt;
     uint32_t split, seg_rows;
@@ -118,8 +121,8 @@ typedef struct mk_gemm_args {
     int64_t lda, ldc;
     int64_t stride_a, stride_c; /* between batches, in elements */
     uint32_t batch;
-    uint32_t w_dtype;     /* MK_BF16 or MK_FP8_E4M3 */
-    uint32_t c_dtype;     /* MK_F32 or MK_BF16 */
+    uint32_t w_dtype;     /* MK_BF16, MK_FP8_E4M3 or MK_F16 (f16: epilogues STORE, ADD / GATE, PAIR_SUM) */
+    uint32_t c_dtype;     /* MK_F32, MK_BF16 or MK_F16 */
     uint32_t epilogue;    /* mk_epilogue */
     const mk_heads_args* heads; /* MK_EPI_HEADS only */
 } mk_gemm_args;
@@ -142,14 +145,15 @@ mk_status mk_gemm_grouped(const mk_gemm_args* a, uint32_t count, void* stream);
 mk_status mk_gemm_set_wait_limit(uint32_t polls);
 
 /* 3x3 convolution, stride 1, zero padding 1 (the VAE decoder's conv, src/image/engine.cpp:732-746, 907-947), as one
- * GEMM over the padded pixel grid (implicit im2col on MFMA). Layout "padded grid": an h x w image is stored as the
+ * GEMM over the padded pixel grid (implicit im2col on MFMA) in IEEE half operands with fp32 sums, as the reference
+ * runs it (F16 weights, docs/performance.md:13). Layout "padded grid": an h x w image is stored as the
  * (h + 2) x (w + 2) grid with a zero ring, preceded and followed by w + 3 zero rows: row S + (y + 1)(w + 2) + x + 1
  * holds pixel (y, x), S = w + 3, each row c channels.
- *   x: bf16 padded grid, c channels (ring and slack rows zero);
- *   w: bf16 [n][9][c], tap = 3 dy + dx (the PyTorch weight [n][c][3][3] with its taps moved in front of c);
+ *   x: f16 padded grid, c channels (ring and slack rows zero);
+ *   w: f16 [n][9][c], tap = 3 dy + dx (the PyTorch weight [n][c][3][3] with its taps moved in front of c);
  *   y: (h + 2)(w + 2) rows of ldy values from its first grid row (a padded-grid buffer + S rows): the pixel rows are
  *      written; ring rows are left as they were or hold values the next layer must not read as pixels;
- *   epilogue MK_EPI_STORE (y = acc + bias, fp32 or bf16) or MK_EPI_ADD (y += acc + bias, fp32).
+ *   epilogue MK_EPI_STORE (y = acc + bias, fp32 or f16) or MK_EPI_ADD (y += acc + bias, fp32).
  * c is a multiple of 64 (c <= 4096), n a multiple of 64 or 96; pad channels with zeros. */
 typedef struct mk_conv_args {
     const void* x;

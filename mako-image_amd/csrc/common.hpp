@@ -170,8 +170,8 @@ __device__ inline uint32_t pack_f16x2(float a, float b)
 {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2v{a, b}, f16x2cv));
 }
-__device__ inline uint16_t f2h_bits(float x) { return __builtin_bit_cast(uint16_t, _Float16(x)); }
-__device__ inline float h2f_bits(uint16_t h) { return float(__builtin_bit_cast(_Float16, h)); }
+__host__ __device__ inline uint16_t f2h_bits(float x) { return __builtin_bit_cast(uint16_t, _Float16(x)); }
+__host__ __device__ inline float h2f_bits(uint16_t h) { return float(__builtin_bit_cast(_Float16, h)); }
 // A pair in the heads' element type: bf16 or half.
 __device__ inline uint32_t pack_x2(float a, float b, bool f16) { return f16 ? pack_f16x2(a, b) : pack_bf16x2(a, b); }
 // bf16 pair -> half pair (exact scaling aside, rounded to nearest even)

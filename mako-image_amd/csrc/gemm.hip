@@ -45,7 +45,7 @@ struct GemmP {
     int64_t gate_alt;
     uint32_t split, seg_rows, M, N, K;
     int64_t lda, ldc, sa, sc;
-    uint32_t epi, c_bf16;
+    uint32_t epi, c_bf16, c_f16; // 16-bit outputs (c_bf16), as IEEE half (c_f16) rather than bf16
     uint32_t tiles_m, tiles_n, batch;
     HeadsP hp;
     // 3 x 3 convolution (EK_CONV): the padded grid's row width w + 2, k tiles a tap (channels / 64), and
@@ -57,8 +57,8 @@ struct GemmP {
     uint32_t conv_w, conv_pix;
     // gated linear unit (EK_GLU): the weights' rows are [first part F; second part F], the output [M][F]
     uint32_t glu_f;
-    // EK_NORM / EK_RMWN: the RMS norm's per-channel gain; EK_RMWN: the normed rows' bf16 output and its row stride
-    // (EK_RMWUP: the 2x grid's bf16 buffer, from its first row, and row stride)
+    // EK_NORM / EK_RMWN: the RMS norm's per-channel gain; EK_RMWN: the normed rows' 16-bit output and its row stride
+    // (EK_RMWUP: the 2x grid's 16-bit buffer, from its first row, and row stride)
     const float* norm_g;
     uint16_t* norm_out;
     uint32_t norm_ld;
@@ -104,15 +104,23 @@ __device__ inline void f8x16_to_bf16(const u32x4& v, u32x4& lo, u32x4& hi)
 
 // Epilogue kinds (template): a plain store, an activation, a read-modify-write of the fp32 residual, the q/k/v heads,
 // a gated linear unit (SwiGLU / GEGLU: each output channel from two weight rows F apart).
-// EK_NORM: a 96-channel convolution's rows RMS-normed and SiLU-ed into the next convolution's bf16 input grid;
+// EK_NORM: a 96-channel convolution's rows RMS-normed and SiLU-ed into the next convolution's 16-bit input grid;
 // EK_RMWN: the rows stored (or added into the fp32 residual) and their RMS norm + SiLU written besides; EK_RMWUP: the
-// rows added into the residual and written, as bf16, to the four pixels each becomes in the nearest 2x grid.
+// rows added into the residual and written, 16-bit, to the four pixels each becomes in the nearest 2x grid. (A
+// convolution's 16-bit grids are IEEE half, like its operands.)
 enum { EK_STORE = 0, EK_ACT = 1, EK_RMW = 2, EK_HEADS = 3, EK_GLU = 4, EK_NORM = 5, EK_RMWN = 6, EK_RMWUP = 7 };
 // Flag on the epilogue kind: the A operand is a 3 x 3 convolution's input (implicit im2col, see conv_koff).
 constexpr int EK_CONV = 8;
 // With EK_CONV: input channels not a multiple of 64 (dense K = 9 c rounded up to 64, k = tap c + channel): a k step
 // spans taps, so each 16-byte chunk (8 channels) takes its own tap's row shift (conv3x3_dense).
 constexpr int EK_CONVQ = 32;
+// Flag on the epilogue kind: the operands are IEEE half (v_mfma_f32_*_f16): the VAE's convolutions and products, whose
+// reference multiplies F16 weights with half activations (docs/performance.md:13, engine.cpp:766-773).
+constexpr int EK_F16 = 64;
+typedef _Float16 f16x8v __attribute__((ext_vector_type(8)));
+
+// A pair of 16-bit outputs: IEEE half or bf16, round to nearest even either way.
+__device__ inline uint32_t pack16(float a, float b, bool half) { return half ? pack_f16x2(a, b) : pack_bf16x2(a, b); }
 
 // Per-tile channel constants of a lane's 4 channels (the same for every token row it writes).
 struct EpiCh {
@@ -159,7 +167,7 @@ __device__ inline void epi_slice(const GemmP& p, const float* st, int ld, int to
             v[i][e] = v[i][e] * k.scale[e] + k.bias[e];
     }
     if constexpr (EK == EK_RMWUP) {
-        // x + v (the convolution's ADD) goes to the four pixels (2 y + dy, 2 x + dx) of the nearest 2x grid as bf16;
+        // x + v (the convolution's ADD) goes to the four pixels (2 y + dy, 2 x + dx) of the nearest 2x grid, 16-bit;
         // the residual itself is not stored (its next reader is the upsampling). Tiles over the pixels only: every
         // row of the slice is a pixel of image row y.
         const float* c = static_cast<const float*>(p.c) + ch;
@@ -176,7 +184,7 @@ __device__ inline void epi_slice(const GemmP& p, const float* st, int ld, int to
             if (t < int(p.M)) {
                 const uint32_t xx = uint32_t(t) - (y + 1) * pw - 1;
                 const uint64_t r = p.up_slack + uint64_t(2 * y + 1) * p.up_pw + 2 * xx + 1;
-                const u32x2 o{pack_bf16x2(x[0] + v[i][0], x[1] + v[i][1]), pack_bf16x2(x[2] + v[i][2], x[3] + v[i][3])};
+                const u32x2 o{pack16(x[0] + v[i][0], x[1] + v[i][1], p.c_f16), pack16(x[2] + v[i][2], x[3] + v[i][3], p.c_f16)};
                 *reinterpret_cast<u32x2*>(up + r * ld2) = o;
                 *reinterpret_cast<u32x2*>(up + (r + 1) * ld2) = o;
                 *reinterpret_cast<u32x2*>(up + (r + p.up_pw) * ld2) = o;
@@ -229,7 +237,7 @@ __device__ inline void epi_slice(const GemmP& p, const float* st, int ld, int to
         u32x2 o[NI];
 #pragma unroll
         for (int i = 0; i < NI; ++i)
-            o[i] = u32x2{pack_bf16x2(v[i][0], v[i][1]), pack_bf16x2(v[i][2], v[i][3])};
+            o[i] = u32x2{pack16(v[i][0], v[i][1], p.c_f16), pack16(v[i][2], v[i][3], p.c_f16)};
         uint16_t* c = static_cast<uint16_t*>(p.c) + off0;
         if (whole) {
 #pragma unroll
@@ -561,9 +569,9 @@ constexpr int fixup_groups(int qn, int cap)
 }
 
 // The norm epilogues of a wave's staged slice (32 rows x 96 channels from chw, row stride ld floats; rows tok0 .. of
-// the padded grid, M = (h + 2) pw of them). v = the conv's value + bias; EK_NORM: y = n(v) (bf16) where n(v) =
+// the padded grid, M = (h + 2) pw of them). v = the conv's value + bias; EK_NORM: y = n(v) (16-bit) where n(v) =
 // silu(v rsqrt(mean(v^2) + 1e-24 / C) g) over the row's C channels, the VAE's RMS norm + SiLU (engine.cpp:725-727);
-// EK_RMWN: y = v or y += v (fp32) and norm_out = n(y) (bf16). Normed ring rows are zero. 8 lanes a row (4 channels of
+// EK_RMWN: y = v or y += v (fp32) and norm_out = n(y) (16-bit). Normed ring rows are zero. 8 lanes a row (4 channels of
 // each 32-channel third), 8 rows an instruction, 4 rows a lane; a row's sum of squares over its 8 lanes by DPP. With
 // C = 192 (PAIR) the row's other 96 channels are the partner wave's (wave ^ 1): the partial sums meet in xch (32
 // floats a wave) across one barrier that waits for LDS operations only, not for the stores in flight.
@@ -640,8 +648,8 @@ __device__ inline void epi_norm_silu(const GemmP& p, const float* st, int ld, in
 #pragma unroll
             for (int e = 0; e < 4; ++e)
                 u[e] = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, silu_f(v[i][j][e] * sc * gm[j][e])) & keep);
-            o[j][0] = pack_bf16x2(u[0], u[1]);
-            o[j][1] = pack_bf16x2(u[2], u[3]);
+            o[j][0] = pack16(u[0], u[1], p.c_f16);
+            o[j][1] = pack16(u[2], u[3], p.c_f16);
         }
         if (t < int(p.M)) {
             uint16_t* y = EKE == EK_RMWN ? p.norm_out + int64_t(t) * p.norm_ld + chw + 4 * c
@@ -667,7 +675,7 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
 {
     static_assert(((EK & 7) != EK_HEADS && (EK & 7) != EK_GLU) || !(EK & EK_CONV),
                   "a convolution has no heads or GLU epilogue");
-    constexpr bool kConv = (EK & EK_CONV) != 0, kConvQ = (EK & EK_CONVQ) != 0;
+    constexpr bool kConv = (EK & EK_CONV) != 0, kConvQ = (EK & EK_CONVQ) != 0, kF16 = (EK & EK_F16) != 0;
     constexpr int EKE = EK & 7;                 // the epilogue kind
     constexpr int NT = 64 * NW;                 // threads
     // waves: 2 along channels x NW/2 along tokens; the 96-channel tiles 1 x NW (a wave holds whole rows)
@@ -822,6 +830,21 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
     const int r32 = lane & 31, hk = lane >> 5, r16 = lane & 15, g4 = lane >> 4;
     // fragment j of a substep in first-use order (the MFMAs run channel-block-major): weight block 0, the token
     // blocks, then weight blocks 1 ..
+    // the matrix-core products in the operands' type (the fragments are 16-bit lanes either way)
+    auto mfma16 = [](const bf16x8& w, const bf16x8& a, const f32x4& c) -> f32x4 {
+        if constexpr (kF16)
+            return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8v, w), __builtin_bit_cast(f16x8v, a),
+                                                          c, 0, 0, 0);
+        else
+            return __builtin_amdgcn_mfma_f32_16x16x32_bf16(w, a, c, 0, 0, 0);
+    };
+    auto mfma32 = [](const bf16x8& w, const bf16x8& a, const f32x16& c) -> f32x16 {
+        if constexpr (kF16)
+            return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8v, w), __builtin_bit_cast(f16x8v, a),
+                                                          c, 0, 0, 0);
+        else
+            return __builtin_amdgcn_mfma_f32_32x32x16_bf16(w, a, c, 0, 0, 0);
+    };
     auto frag = [&](int buf, int ks, int j, bf16x8(&wf)[CB], bf16x8(&af)[TB]) {
         const int kc = ks * 2 + hk;
         if (j == 0 || j > TB) {
@@ -887,7 +910,7 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
         for (int i = 0; i < CB * TB; ++i) {
             const int cb = i / TB, tb = i % TB;
             if constexpr (!M16)
-                acc[cb][tb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[cb], af[tb], acc[cb][tb], 0, 0, 0);
+                acc[cb][tb] = mfma32(wf[cb], af[tb], acc[cb][tb]);
             __builtin_amdgcn_sched_barrier(0);
             if (nks >= 0 && i < CB + TB) {
                 frag(nbuf, nks, i, nwf, naf);
@@ -917,7 +940,7 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
         for (int i = 0; i < CB * TB; ++i) {
             const int cb = i / TB, tb = i % TB;
             if constexpr (M16)
-                acc[cb][tb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[cb], af[tb], acc[cb][tb], 0, 0, 0);
+                acc[cb][tb] = mfma16(wf[cb], af[tb], acc[cb][tb]);
             __builtin_amdgcn_sched_barrier(0);
             if (nks >= 0 && cb == 0) {
                 rda(nbuf, nks, tb, naf);
@@ -1137,12 +1160,13 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
     };
     constexpr int NS = WM / 32, RB = TB / NS; // 32-token slices of a wave, MFMA token blocks a slice
     if constexpr (EKE == EK_GLU) {
-        // out = silu(first) second (SwiGLU, swiglu_rows) or first gelu_erf(second) (GEGLU, geglu_rows), computed
+        // out = silu(first) second (SwiGLU, swiglu_rows), first gelu_erf(second) (GEGLU, geglu_rows) or first +
+        // second (a product split in two weight halves, MK_EPI_PAIR_SUM), computed
         // into blocks cb < CB/2 from blocks cb and cb + CB/2 (each with its rows' scale and bias), then stored as a
         // slice of WC/2 channels
         constexpr int CH2 = CB / 2, NQ = M16 ? 1 : 4; // groups of 4 consecutive channels a lane holds in a block
         const int oc0 = int(tn) * (BN / 2) + wn * (WC / 2);
-        const bool swi = p.epi == MK_EPI_SWIGLU;
+        const bool swi = p.epi == MK_EPI_SWIGLU, sum = p.epi == MK_EPI_PAIR_SUM;
 #pragma unroll
         for (int cb = 0; cb < CH2; ++cb)
 #pragma unroll
@@ -1158,8 +1182,9 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
                     for (int e = 0; e < 4; ++e) {
                         const float a = acc[cb][tb][4 * q + e] * s1[e] + b1[e];
                         const float g = acc[cb + CH2][tb][4 * q + e] * s2[e] + b2[e];
-                        acc[cb][tb][4 * q + e] =
-                            swi ? silu_f(a) * g : a * (0.5f * g * (1.0f + erf_fit(g * 0.70710678f)));
+                        acc[cb][tb][4 * q + e] = sum ? a + g
+                                                 : swi ? silu_f(a) * g
+                                                       : a * (0.5f * g * (1.0f + erf_fit(g * 0.70710678f)));
                     }
             }
         constexpr int WH = WC / 2, LDH = WH + 4;
@@ -1472,7 +1497,7 @@ int epi_kind(uint32_t e)
     return e == MK_EPI_HEADS                             ? EK_HEADS
            : e == MK_EPI_STORE                           ? EK_STORE
            : (e == MK_EPI_GELU_TANH || e == MK_EPI_SILU) ? EK_ACT
-           : (e == MK_EPI_SWIGLU || e == MK_EPI_GEGLU)   ? EK_GLU
+           : (e == MK_EPI_SWIGLU || e == MK_EPI_GEGLU || e == MK_EPI_PAIR_SUM) ? EK_GLU
                                                          : EK_RMW;
 }
 
@@ -1485,15 +1510,17 @@ mk_status prepare(const mk_gemm_args* a, GemmP& p, bool conv = false)
     if (a->K % 64 || (a->N % 64 && !(conv && a->N % 96 == 0)) || a->K == 0 || a->N == 0)
         return fail(MK_ERR_ARG, "gemm: K and N must be nonzero multiples of 64 (K " + std::to_string(a->K) + ", N " +
                                     std::to_string(a->N) + ")");
-    if (a->w_dtype != MK_BF16 && a->w_dtype != MK_FP8_E4M3)
-        return fail(MK_ERR_ARG, "gemm: weights must be bf16 or fp8-e4m3");
+    if (a->w_dtype != MK_BF16 && a->w_dtype != MK_FP8_E4M3 && a->w_dtype != MK_F16)
+        return fail(MK_ERR_ARG, "gemm: weights must be bf16, fp8-e4m3 or f16 (then A is f16 too)");
+    if (a->c_dtype != MK_F32 && a->c_dtype != MK_BF16 && a->c_dtype != MK_F16 && a->epilogue != MK_EPI_HEADS)
+        return fail(MK_ERR_ARG, "gemm: C must be f32, bf16 or f16");
     if (a->lda % 8 || (reinterpret_cast<uintptr_t>(a->a) & 15) || (reinterpret_cast<uintptr_t>(a->w) & 15))
         return fail(MK_ERR_ARG, "gemm: A and W must be 16-byte aligned with lda a multiple of 8");
     if (a->lda >= (1u << 23) || a->K >= (1u << 23))
         return fail(MK_ERR_ARG, "gemm: lda and K must be below 2^23 (32-bit byte offsets within a tile)");
-    if (a->epilogue > MK_EPI_GEGLU)
+    if (a->epilogue > MK_EPI_PAIR_SUM)
         return fail(MK_ERR_ARG, "gemm: unknown epilogue");
-    const bool glu = a->epilogue == MK_EPI_SWIGLU || a->epilogue == MK_EPI_GEGLU;
+    const bool glu = a->epilogue == MK_EPI_SWIGLU || a->epilogue == MK_EPI_GEGLU || a->epilogue == MK_EPI_PAIR_SUM;
     if (glu && (a->N % 128 || (a->N / 2) % 4))
         return fail(MK_ERR_ARG, "gemm: a gated linear unit needs N = 2 F a multiple of 128");
     const bool gated = a->epilogue == MK_EPI_GATE_ADD || a->epilogue == MK_EPI_GATE_TANH;
@@ -1519,7 +1546,8 @@ mk_status prepare(const mk_gemm_args* a, GemmP& p, bool conv = false)
     p.sa = a->stride_a;
     p.sc = a->stride_c;
     p.epi = a->epilogue;
-    p.c_bf16 = a->c_dtype == MK_BF16;
+    p.c_bf16 = a->c_dtype == MK_BF16 || a->c_dtype == MK_F16;
+    p.c_f16 = a->c_dtype == MK_F16;
     p.batch = a->batch;
     p.glu_f = glu ? a->N / 2 : 0;
     if (a->epilogue == MK_EPI_HEADS) {
@@ -1577,7 +1605,8 @@ GemmPlan gemm_plan(const mk_gemm_args* a, uint32_t n, uint32_t cus, bool conv)
     const uint32_t N = a[0].N;
     const bool heads = a[0].epilogue == MK_EPI_HEADS;
     const bool narrow_ok = a[0].epilogue != MK_EPI_GELU_TANH && a[0].epilogue != MK_EPI_SILU &&
-                           a[0].epilogue != MK_EPI_SWIGLU && a[0].epilogue != MK_EPI_GEGLU; // 64-wide tiles
+                           a[0].epilogue != MK_EPI_SWIGLU && a[0].epilogue != MK_EPI_GEGLU &&
+                           a[0].epilogue != MK_EPI_PAIR_SUM; // 64-wide tiles
     const bool short_ok = !heads && a[0].w_dtype == MK_BF16; // 128-token tiles
     auto tiles_of = [&](int bm, int bn) {
         uint64_t t = 0;
@@ -1671,6 +1700,29 @@ extern "C" mk_status mk_gemm_grouped(const mk_gemm_args* a, uint32_t count, void
         return fail(MK_ERR_UNSUPPORTED, "gemm: activation and GLU epilogues need N a multiple of 128");
     hipStream_t s = static_cast<hipStream_t>(stream);
     mk_status e;
+    if (a[0].w_dtype == MK_F16) {
+        // half operands (the VAE's 1 x 1 convolutions and attention products): plain, residual and pair-sum epilogues
+        if (ek != EK_STORE && ek != EK_RMW && !(ek == EK_GLU && a[0].epilogue == MK_EPI_PAIR_SUM))
+            return fail(MK_ERR_UNSUPPORTED, "gemm: f16 operands take the STORE, ADD / GATE and PAIR_SUM epilogues");
+        auto f16 = [&](auto ek_c) -> mk_status {
+            constexpr int E = decltype(ek_c)::value | EK_F16;
+            if (plan.bm == 128)
+                return launch<128, 128, false, E, 4>(p, n, plan, s);
+            if (bn == 256)
+                return launch<256, 256, false, E, 8>(p, n, plan, s);
+            if (bn == 128)
+                return launch<256, 128, false, E, 4>(p, n, plan, s);
+            if constexpr (decltype(ek_c)::value == EK_GLU)
+                return fail(MK_ERR_UNSUPPORTED, "gemm: a pair sum needs N a multiple of 128");
+            else
+                return launch<256, 64, false, E, 4>(p, n, plan, s);
+        };
+        if (ek == EK_STORE)
+            return f16(std::integral_constant<int, EK_STORE>{});
+        if (ek == EK_RMW)
+            return f16(std::integral_constant<int, EK_RMW>{});
+        return f16(std::integral_constant<int, EK_GLU>{});
+    }
     // 256-wide tiles: 8 waves (two a SIMD, 64 x 128 wave tiles), so one wave's waits (barrier, loads) leave the
     // other's MFMAs running
 #define MK_GEMM_EK(BN, EK)                                                                                        \
@@ -1752,13 +1804,13 @@ mk_status conv3x3_run(const mk_conv_args* a, uint32_t lda, bool dense, const Con
                                         "multiple of 8"
                                       : "conv3x3: channels in a nonzero multiple of 64 (<= 4096)");
     if ((a->epilogue != MK_EPI_STORE && a->epilogue != MK_EPI_ADD) ||
-        (a->epilogue == MK_EPI_ADD && a->y_dtype != MK_F32) || (a->y_dtype != MK_F32 && a->y_dtype != MK_BF16))
-        return fail(MK_ERR_ARG, std::string(who) + ": epilogue STORE (fp32 or bf16) or ADD (fp32)");
+        (a->epilogue == MK_EPI_ADD && a->y_dtype != MK_F32) || (a->y_dtype != MK_F32 && a->y_dtype != MK_F16))
+        return fail(MK_ERR_ARG, std::string(who) + ": epilogue STORE (fp32 or f16) or ADD (fp32)");
     if (nm && (!nm->g || (a->n != 96 && a->n != 192) ||
                (nm->out ? (a->y_dtype != MK_F32 || nm->ld < a->n || nm->ld % 4)
-                        : (a->y_dtype != MK_BF16 || a->epilogue != MK_EPI_STORE))))
+                        : (a->y_dtype != MK_F16 || a->epilogue != MK_EPI_STORE))))
         return fail(MK_ERR_ARG, std::string(who) + ": the norm epilogues need 96 or 192 output channels and a gain, "
-                                                   "and either a bf16 store or an fp32 output plus a normed one");
+                                                   "and either an f16 store or an fp32 output plus a normed one");
     if (up && (nm || dense || !up->out || a->epilogue != MK_EPI_ADD || a->n % 192 || a->width % 256 || up->ld < a->n ||
                up->ld % 4 || a->h > (1u << 14) || a->width > (1u << 14)))
         return fail(MK_ERR_ARG, std::string(who) + ": the 2x-grid epilogue needs an ADD over 192-channel multiples, "
@@ -1777,11 +1829,12 @@ mk_status conv3x3_run(const mk_conv_args* a, uint32_t lda, bool dense, const Con
     g.lda = lda;
     g.ldc = a->ldy;
     g.batch = 1;
-    g.w_dtype = MK_BF16;
+    g.w_dtype = MK_F16;
     g.c_dtype = a->y_dtype;
     g.epilogue = a->epilogue;
     GemmP p;
     MK_TRY(prepare(&g, p, true));
+    p.c_f16 = 1; // every 16-bit grid a convolution writes (its output, a normed or a 2x grid) is half
     p.conv_pw = uint32_t(pw);
     p.conv_tpt = dense ? a->c / 8 : a->c / 64;
     p.conv_inv = (65536u + p.conv_tpt - 1) / p.conv_tpt;
@@ -1809,7 +1862,7 @@ mk_status conv3x3_run(const mk_conv_args* a, uint32_t lda, bool dense, const Con
     plan.sk = false;
     hipStream_t s = static_cast<hipStream_t>(stream);
     const bool add = a->epilogue == MK_EPI_ADD;
-    constexpr int C = EK_CONV, Q = EK_CONV | EK_CONVQ;
+    constexpr int C = EK_CONV | EK_F16, Q = EK_CONV | EK_CONVQ | EK_F16;
     if (up) {
         p.norm_out = up->out;
         p.norm_ld = up->ld;

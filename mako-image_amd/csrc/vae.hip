@@ -2,12 +2,13 @@
 // Wan-2.1-layout decoder Qwen-Image uses, one frame. Every 3 x 3 convolution is one implicit-GEMM launch on the matrix
 // cores (mk_conv3x3 over the padded pixel grid), 1 x 1 convolutions are plain GEMMs over the same rows, and the kernels
 // here do the rest: token unpacking with the latent denormalisation and post_quant_conv, RMS norms (+ SiLU) that write
-// the next convolution's bf16 input with its zero ring, nearest 2x upsampling into the next grid, the mid block's
-// softmax, and the clamp to RGBA.
+// the next convolution's input with its zero ring, nearest 2x upsampling into the next grid, the mid block's softmax,
+// and the clamp to RGBA. Every convolution multiplies IEEE half weights with half activations in fp32 sums, as the
+// reference does (its convolution weights F16, docs/performance.md:13): the 16-bit grids here hold half values.
 //
 // Image layout "padded grid" (h x w, c channels, row stride cs): (h + 2)(w + 2) grid rows with a one-pixel ring, and
 // S = w + 3 slack rows before and after; pixel (y, x) is row S + (y + 1)(w + 2) + x + 1. fp32 activations use it as
-// written by the convolutions (ring rows hold values nobody reads as pixels); bf16 convolution inputs keep ring and
+// written by the convolutions (ring rows hold values nobody reads as pixels); half convolution inputs keep ring and
 // slack rows zero, and channels past c zero.
 #include "common.hpp"
 
@@ -57,10 +58,12 @@ struct GridDims {
 };
 
 inline uint32_t cpad(uint32_t c) { return (c + 63) / 64 * 64; }
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
 // tokens [th][tw][4 z] -> the latent image (2 th x 2 tw, z channels: value (c * 2 + py) * 2 + px of a token is channel
-// c of pixel (2 y + py, 2 x + px)), denormalised (v * std + mean, engine.cpp:887-898), post_quant_conv in fp32
-// (w [z][z], b [z]), written as the bf16 padded grid with cp channels. One thread a (buffer row, channel).
+// c of pixel (2 y + py, 2 x + px)), denormalised (v * std + mean, engine.cpp:887-898), then post_quant_conv as the
+// reference's 1 x 1 conv computes it: half inputs times half weights (w [z][z] holds half values as floats, b [z]) in
+// fp32, written as the half padded grid with cp channels (conv_in's input). One thread a (buffer row, channel).
 __global__ __launch_bounds__(256) void vae_in_kernel(const float* __restrict__ tok, uint32_t tw, GridDims g, uint32_t z,
                                                      uint32_t cp, const float* __restrict__ mean,
                                                      const float* __restrict__ sd, const float* __restrict__ w,
@@ -77,15 +80,15 @@ __global__ __launch_bounds__(256) void vae_in_kernel(const float* __restrict__ t
         const float* t = tok + (uint64_t(y / 2) * tw + x / 2) * 4 * z + (y % 2) * 2 + (x % 2);
         float acc = b[c];
         for (uint32_t ch = 0; ch < z; ++ch)
-            acc = fmaf(w[c * z + ch], t[4 * ch] * sd[ch] + mean[ch], acc);
+            acc = fmaf(w[c * z + ch], h2f_bits(f2h_bits(t[4 * ch] * sd[ch] + mean[ch])), acc);
         v = acc;
     }
-    out[i] = f2bf_bits(v);
+    out[i] = f2h_bits(v);
 }
 
 // RMS norm over a pixel's c channels (x / sqrt(mean(x^2) + 1e-24 / c) * gamma, engine.cpp:725-727), then SiLU (mode
-// 0), or not (mode 1), or a plain bf16 copy (mode 2). 16 lanes a row, J = cp / 64 chunks of 4 channels a lane; x fp32
-// rows of stride cs (c a multiple of 4); y bf16 rows of stride cp. Grid output (compact = 0): every buffer row of y,
+// 0), or not (mode 1), or a plain half copy (mode 2). 16 lanes a row, J = cp / 64 chunks of 4 channels a lane; x fp32
+// rows of stride cs (c a multiple of 4); y half rows of stride cp. Grid output (compact = 0): every buffer row of y,
 // ring and slack rows and channels past c zero. Compact output: y row p = pixel p (y * w + x), p < rows.
 template <int J>
 __global__ __launch_bounds__(256) void vae_norm_kernel(const float* __restrict__ xg, uint32_t cs, GridDims g,
@@ -145,11 +148,11 @@ __global__ __launch_bounds__(256) void vae_norm_kernel(const float* __restrict__
                 o[e] = t;
             }
         }
-        *reinterpret_cast<u32x2*>(yr + k) = u32x2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+        *reinterpret_cast<u32x2*>(yr + k) = u32x2{pack_f16x2(o[0], o[1]), pack_f16x2(o[2], o[3])};
     }
 }
 
-// Zeroes the rows of a bf16 padded grid (ld channels a row, a multiple of 8) that hold no pixel: the slack rows, the
+// Zeroes the rows of a 16-bit padded grid (ld channels a row, a multiple of 8) that hold no pixel: the slack rows, the
 // top and bottom ring rows and each image row's two ring pixels, 2 (w + 3) + 2 (w + 2) + 2 h rows in all. One thread a
 // (row, 8 channels).
 __global__ __launch_bounds__(256) void vae_ring_zero_kernel(uint16_t* __restrict__ y, GridDims g, uint32_t ld)
@@ -171,7 +174,7 @@ __global__ __launch_bounds__(256) void vae_ring_zero_kernel(uint16_t* __restrict
     *reinterpret_cast<u32x4*>(y + r * ld + 8 * j) = u32x4{0, 0, 0, 0};
 }
 
-// Nearest 2x: the bf16 padded grid of the 2h x 2w image (cp channels) from the fp32 grid of the h x w one (c
+// Nearest 2x: the half padded grid of the 2h x 2w image (cp channels) from the fp32 grid of the h x w one (c
 // channels, a multiple of 4, stride cs). One thread a (output row, 4 channels); 32-bit indexing.
 __global__ __launch_bounds__(256) void vae_up_kernel(const float* __restrict__ x, uint32_t cs, GridDims gi,
                                                      uint32_t c, GridDims go, uint32_t cp, uint16_t* __restrict__ y)
@@ -184,10 +187,11 @@ __global__ __launch_bounds__(256) void vae_up_kernel(const float* __restrict__ x
     f32x4 v{0, 0, 0, 0};
     if (k < c && go.pixel32(r, py, px))
         v = *reinterpret_cast<const f32x4*>(x + gi.row_of(py / 2, px / 2) * cs + k);
-    *reinterpret_cast<u32x2*>(y + uint64_t(i) * 4) = u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+    *reinterpret_cast<u32x2*>(y + uint64_t(i) * 4) = u32x2{pack_f16x2(v[0], v[1]), pack_f16x2(v[2], v[3])};
 }
 
-// Row softmax for the mid block's attention: p[j] = exp(scale (s[j] - max)) / sum over the n real columns, bf16, 0
+// Row softmax for the mid block's attention: p[j] = exp(scale (s[j] - max)) / sum over the n real columns, as half
+// (the reference's halves() of P, engine.cpp:773), 0
 // for the padding columns up to ld. One block a row: one read for the max and the sum together (each thread keeps a
 // running max and a sum rescaled to it; pairs merge the same way), one more to write P.
 __device__ inline void ms_merge(float& m, float& s, float m2, float s2)
@@ -245,8 +249,8 @@ __global__ __launch_bounds__(256) void vae_softmax1_kernel(const float* __restri
     for (int i = 0; i < NV; ++i) {
         const uint32_t j = 4 * (tid + 256 * i);
         if (j < ld)
-            *reinterpret_cast<u32x2*>(pr + j) = u32x2{pack_bf16x2(v[i][0] * inv, v[i][1] * inv),
-                                                      pack_bf16x2(v[i][2] * inv, v[i][3] * inv)};
+            *reinterpret_cast<u32x2*>(pr + j) = u32x2{pack_f16x2(v[i][0] * inv, v[i][1] * inv),
+                                                      pack_f16x2(v[i][2] * inv, v[i][3] * inv)};
     }
 }
 
@@ -285,7 +289,7 @@ __global__ __launch_bounds__(256) void vae_softmax_kernel(const float* __restric
 #pragma unroll
         for (int e = 0; e < 4; ++e)
             o[e] = j + e < n ? __expf(scale * v[e] - m) * inv : 0.0f;
-        *reinterpret_cast<u32x2*>(pr + j) = u32x2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+        *reinterpret_cast<u32x2*>(pr + j) = u32x2{pack_f16x2(o[0], o[1]), pack_f16x2(o[2], o[3])};
     }
 }
 
@@ -316,13 +320,13 @@ __global__ __launch_bounds__(256) void vae_compact_kernel(const float* __restric
 // output channels are too few for the matrix cores (a 64-channel tile computes 61 zero channels), so: a workgroup
 // takes a 16 x 16 pixel tile, stages its 18 x 18 input neighbourhood (c channels, rows padded by 8 so the 16 lanes of a
 // pixel row read distinct banks) and the 3 x 9 x c weights in LDS with whole-row loads, then each thread sums its
-// pixel's 9 taps from LDS (weights: broadcasts), bf16 pairs by v_dot2_f32_bf16 with fp32 accumulation. x: the bf16
+// pixel's 9 taps from LDS (weights: broadcasts), half pairs by v_dot2_f32_f16 with fp32 accumulation. x: the half
 // grid (rows of stride xs, zero ring and zero channels past the input's); c: the input's channels rounded up to 8
 // (<= xs, cs <= 128); w: the packed weight rows [3][9][cs]; pre (may be NULL): the unclamped values into the fp32 grid
 // rows (stride ps), for probes.
 constexpr int kCoTile = 16;
-struct alignas(16) Bf16Quad { // 4 bf16 pairs: one 16-byte LDS access
-    bf16x2cv v[4];
+struct alignas(16) HalfQuad { // 4 half pairs: one 16-byte LDS access
+    f16x2cv v[4];
 };
 __global__ __launch_bounds__(256) void vae_conv_out_kernel(const uint16_t* __restrict__ x, uint32_t xs, uint32_t cs,
                                                            uint32_t c,
@@ -330,16 +334,16 @@ __global__ __launch_bounds__(256) void vae_conv_out_kernel(const uint16_t* __res
                                                            const float* __restrict__ bias, float* __restrict__ rgba,
                                                            float* __restrict__ pre, uint32_t ps)
 {
-    // (operands are read as bf16 pairs: no bit casts of vector elements, which this compiler gets wrong)
+    // (operands are read as half pairs: no bit casts of vector elements, which this compiler gets wrong)
     constexpr int NB = kCoTile + 2;
-    __shared__ Bf16Quad sw[3][9][16];
+    __shared__ HalfQuad sw[3][9][16];
     extern __shared__ __attribute__((aligned(16))) uint16_t sx[]; // NB x NB pixels x (c + 8): the launch's size
     const uint32_t pst = c + 8; // LDS pixel stride (elements)
     const uint32_t tid = threadIdx.x, cq = c / 8;
     const uint32_t ty0 = blockIdx.y * kCoTile, tx0 = blockIdx.x * kCoTile;
     for (uint32_t i = tid; i < 3 * 9 * cq; i += 256) {
         const uint32_t o = i / (9 * cq), r = i - o * 9 * cq, tap = r / cq, j = r - tap * cq;
-        sw[o][tap][j] = *reinterpret_cast<const Bf16Quad*>(w + (uint64_t(o) * 9 + tap) * cs + 8 * j);
+        sw[o][tap][j] = *reinterpret_cast<const HalfQuad*>(w + (uint64_t(o) * 9 + tap) * cs + 8 * j);
     }
     // neighbourhood pixel (qy, qx) is grid pixel (ty0 + qy - 1, tx0 + qx - 1): grid row slack + (ty0 + qy) (w + 2) +
     // tx0 + qx, inside the grid while ty0 + qy <= h + 1 and tx0 + qx <= w + 1
@@ -358,15 +362,15 @@ __global__ __launch_bounds__(256) void vae_conv_out_kernel(const uint16_t* __res
 #pragma unroll
     for (int tap = 0; tap < 9; ++tap) {
         const int dy = tap / 3, dx = tap - 3 * dy;
-        const Bf16Quad* xq = reinterpret_cast<const Bf16Quad*>(sx + ((ly + dy) * NB + lx + dx) * pst);
+        const HalfQuad* xq = reinterpret_cast<const HalfQuad*>(sx + ((ly + dy) * NB + lx + dx) * pst);
         for (uint32_t j = 0; j < cq; ++j) {
-            const Bf16Quad a = xq[j];
+            const HalfQuad a = xq[j];
 #pragma unroll
             for (int o = 0; o < 3; ++o) {
-                const Bf16Quad wq = sw[o][tap][j];
+                const HalfQuad wq = sw[o][tap][j];
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
-                    acc[o] = __builtin_amdgcn_fdot2_f32_bf16(a.v[e], wq.v[e], acc[o], false);
+                    acc[o] = __builtin_amdgcn_fdot2(a.v[e], wq.v[e], acc[o], false);
             }
         }
     }
@@ -379,7 +383,7 @@ __global__ __launch_bounds__(256) void vae_conv_out_kernel(const uint16_t* __res
                                                     fminf(1.0f, fmaxf(-1.0f, acc[2])), 1.0f};
 }
 
-// conv_out over 96 input channels on the matrix cores (v_mfma_f32_16x16x32_bf16). The weights are the A operand: its
+// conv_out over 96 input channels on the matrix cores (v_mfma_f32_16x16x32_f16). The weights are the A operand: its
 // 16 rows are the 3 output channels and 13 zero rows, and a tap's 96 channels are three 32-deep k chunks, so the 27
 // fragments stay in registers. 16 pixels of one tile row are the B operand, one 16-byte LDS read a lane from the
 // neighbourhood (pixel stride 208 B: the 16 pixels of a read fall on distinct bank groups). A lane of the product
@@ -435,7 +439,8 @@ __global__ __launch_bounds__(256) void vae_conv_out96_kernel(const uint16_t* __r
             for (int r = 0; r < 4; ++r) {
                 const bf16x8 b = *reinterpret_cast<const bf16x8*>(
                     sx + ((4 * wave + r + dy) * NB + r16 + dx) * PST + 32 * j + 8 * g4);
-                acc[r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[tap][j], b, acc[r], 0, 0, 0);
+                acc[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, wf[tap][j]),
+                                                                 __builtin_bit_cast(f16x8, b), acc[r], 0, 0, 0);
             }
     }
     if (g4 != 0)
@@ -459,11 +464,15 @@ __global__ __launch_bounds__(256) void vae_conv_out96_kernel(const uint16_t* __r
     }
 }
 
-// A PyTorch conv weight [parts * co][ci][kt][k][k] (bf16; kt time taps of a causal 3-D conv, the last one used: a
-// single frame sees only it) -> [parts][cop][k * k][cip] bf16, tap-major, zero-padded. One thread an output value.
-__global__ __launch_bounds__(256) void vae_pack_kernel(const uint16_t* __restrict__ src, uint32_t parts, uint32_t co,
-                                                       uint32_t ci, uint32_t kt, uint32_t kk, uint32_t cop,
-                                                       uint32_t cip, uint16_t* __restrict__ dst)
+// A weight's 16-bit source value as IEEE half: bf16 rounded to the nearest half, or a half as it is.
+__device__ inline uint16_t w_half(uint16_t v, bool src_f16) { return src_f16 ? v : f2h_bits(bf2f_bits(v)); }
+
+// A PyTorch conv weight [parts * co][ci][kt][k][k] (bf16 or half; kt time taps of a causal 3-D conv, the last one
+// used: a single frame sees only it) -> [parts][cop][k * k][cip] half, tap-major, zero-padded. One thread an output
+// value.
+__global__ __launch_bounds__(256) void vae_pack_kernel(const uint16_t* __restrict__ src, int src_f16, uint32_t parts,
+                                                       uint32_t co, uint32_t ci, uint32_t kt, uint32_t kk,
+                                                       uint32_t cop, uint32_t cip, uint16_t* __restrict__ dst)
 {
     const uint64_t i = uint64_t(blockIdx.x) * 256 + threadIdx.x;
     const uint64_t n = uint64_t(parts) * cop * kk * cip;
@@ -476,15 +485,15 @@ __global__ __launch_bounds__(256) void vae_pack_kernel(const uint16_t* __restric
     const uint32_t o = uint32_t(po % cop), part = uint32_t(po / cop);
     uint16_t v = 0;
     if (o < co && c < ci)
-        v = src[((uint64_t(part * co + o) * ci + c) * kt + (kt - 1)) * kk + tap];
+        v = w_half(src[((uint64_t(part * co + o) * ci + c) * kt + (kt - 1)) * kk + tap], src_f16);
     dst[i] = v;
 }
 
 // A 3 x 3 conv weight packed dense for conv3x3_dense: dst [cop][kp], k = tap ci + c for k < 9 ci, zero beyond and
 // for rows past co (source as vae_pack_kernel's, one part).
-__global__ __launch_bounds__(256) void vae_pack_dense_kernel(const uint16_t* __restrict__ src, uint32_t co,
-                                                             uint32_t ci, uint32_t kt, uint32_t cop, uint32_t kp,
-                                                             uint16_t* __restrict__ dst)
+__global__ __launch_bounds__(256) void vae_pack_dense_kernel(const uint16_t* __restrict__ src, int src_f16,
+                                                             uint32_t co, uint32_t ci, uint32_t kt, uint32_t cop,
+                                                             uint32_t kp, uint16_t* __restrict__ dst)
 {
     const uint64_t i = uint64_t(blockIdx.x) * 256 + threadIdx.x;
     if (i >= uint64_t(cop) * kp)
@@ -493,7 +502,7 @@ __global__ __launch_bounds__(256) void vae_pack_dense_kernel(const uint16_t* __r
     uint16_t v = 0;
     if (o < co && k < 9 * ci) {
         const uint32_t tap = k / ci, c = k - tap * ci;
-        v = src[((uint64_t(o) * ci + c) * kt + (kt - 1)) * 9 + tap];
+        v = w_half(src[((uint64_t(o) * ci + c) * kt + (kt - 1)) * 9 + tap], src_f16);
     }
     dst[i] = v;
 }
@@ -509,6 +518,33 @@ __global__ __launch_bounds__(256) void vae_pack_vec_kernel(const float* __restri
     dst[i] = k < n ? src[part * n + k] : 0.0f;
 }
 
+// post_quant_conv's weight [z][z] from its 16-bit source to the half values it multiplies with, held as floats.
+__global__ __launch_bounds__(256) void vae_w16_to_f32_kernel(const uint16_t* __restrict__ src, int src_f16, uint32_t n,
+                                                             float* __restrict__ dst)
+{
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n)
+        dst[i] = h2f_bits(w_half(src[i], src_f16));
+}
+
+// An fp32 operand of the attention's products as two half planes, hi = half(v) and lo = half(v - hi) (the sum holds
+// v to about 22 bits: the reference keeps K and V^T in fp32, engine.cpp:764-773): rows [rows][cols] (stride ld) plus
+// an optional per-row bias (V^T's value bias) -> hi at dst + r * dld + c, lo at that + lo_off. One thread a value.
+__global__ __launch_bounds__(256) void vae_split_kernel(const float* __restrict__ x, uint32_t rows, uint32_t cols,
+                                                        uint32_t ld, const float* __restrict__ bias,
+                                                        uint16_t* __restrict__ dst, uint32_t dld, uint64_t lo_off)
+{
+    const uint64_t i = uint64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= uint64_t(rows) * cols)
+        return;
+    const uint32_t r = uint32_t(i / cols), c = uint32_t(i - uint64_t(r) * cols);
+    const float v = x[uint64_t(r) * ld + c] + (bias ? bias[r] : 0.0f);
+    const uint16_t hi = f2h_bits(v);
+    uint16_t* d = dst + uint64_t(r) * dld + c;
+    d[0] = hi;
+    d[lo_off] = f2h_bits(v - h2f_bits(hi));
+}
+
 inline uint32_t blocks_for(uint64_t n) { return uint32_t((n + 255) / 256); }
 
 // MK_OK, or the HIP error as a status (hip_check records a failure; it is only called on one)
@@ -519,7 +555,7 @@ inline mk_status hip_ok(hipError_t e, const char* what) { return e == hipSuccess
 
 using namespace mk;
 
-// A norm + SiLU that a 96- or 192-channel conv's epilogue applies to its rows: gain g, into the bf16 grid buf (rows of
+// A norm + SiLU that a 96- or 192-channel conv's epilogue applies to its rows: gain g, into the half grid buf (rows of
 // the conv's channels; its slack and ring rows zeroed by mk_vae::conv3)
 struct NormTo {
     const float* g = nullptr;
@@ -577,7 +613,7 @@ struct mk_vae {
         void* p = nullptr;
         size_t bytes = 0;
     };
-    Buf x, y, t, a, sc, qb, kb, vtb, sb, pb, ob, pj, tok, rgba, probe_buf;
+    Buf x, y, t, a, sc, qb, kb, vtb, kf, sb, pb, ob, pj, tok, rgba, probe_buf;
     mk_probe_fn probe = nullptr;
     void* probe_user = nullptr;
 
@@ -587,7 +623,7 @@ struct mk_vae {
             (void)hipStreamSynchronize(stream);
         for (void* p : allocs)
             (void)hipFree(p);
-        for (Buf* b : {&x, &y, &t, &a, &sc, &qb, &kb, &vtb, &sb, &pb, &ob, &pj, &tok, &rgba, &probe_buf})
+        for (Buf* b : {&x, &y, &t, &a, &sc, &qb, &kb, &vtb, &kf, &sb, &pb, &ob, &pj, &tok, &rgba, &probe_buf})
             if (b->p)
                 (void)hipFree(b->p);
         if (stream)
@@ -689,22 +725,22 @@ struct mk_vae {
         return MK_OK;
     }
 
-    // One tensor from device memory in PyTorch layout: conv weights bf16 [parts * co][ci][kt][k][k] (kt >= 1),
-    // everything else fp32.
-    mk_status put(const Slot& s, const void* src, uint32_t kt)
+    // One tensor from device memory in PyTorch layout: conv weights 16-bit [parts * co][ci][kt][k][k] (kt >= 1; half,
+    // or bf16 when src_f16 is false), everything else fp32. Convolution weights are stored as half.
+    mk_status put(const Slot& s, const void* src, uint32_t kt, bool src_f16)
     {
         switch (s.kind) {
         case Slot::CONV_W: {
             const Conv& c = *s.conv;
             if (c.dense) {
                 const uint64_t n = uint64_t(c.cop()) * c.kp();
-                vae_pack_dense_kernel<<<blocks_for(n), 256, 0, stream>>>(static_cast<const uint16_t*>(src), c.co,
-                                                                         c.ci, kt, c.cop(), c.kp(), c.w);
+                vae_pack_dense_kernel<<<blocks_for(n), 256, 0, stream>>>(static_cast<const uint16_t*>(src), src_f16,
+                                                                         c.co, c.ci, kt, c.cop(), c.kp(), c.w);
                 break;
             }
             const uint64_t n = uint64_t(c.parts) * c.cop() * c.k * c.k * c.cip();
-            vae_pack_kernel<<<blocks_for(n), 256, 0, stream>>>(static_cast<const uint16_t*>(src), c.parts, c.co, c.ci,
-                                                              kt, c.k * c.k, c.cop(), c.cip(), c.w);
+            vae_pack_kernel<<<blocks_for(n), 256, 0, stream>>>(static_cast<const uint16_t*>(src), src_f16, c.parts,
+                                                              c.co, c.ci, kt, c.k * c.k, c.cop(), c.cip(), c.w);
             break;
         }
         case Slot::CONV_B: {
@@ -713,8 +749,10 @@ struct mk_vae {
                 static_cast<const float*>(src), c.parts, c.co, c.cop(), c.b);
             break;
         }
-        case Slot::PQ_W: // bf16 [z][z] -> fp32
-            return mk_bf16_to_f32(src, s.n, s.vec, stream);
+        case Slot::PQ_W: // 16-bit [z][z] -> its half values as fp32
+            vae_w16_to_f32_kernel<<<blocks_for(s.n), 256, 0, stream>>>(static_cast<const uint16_t*>(src), src_f16,
+                                                                       s.n, s.vec);
+            break;
         case Slot::VEC:
             MK_HIP(hipMemcpyAsync(s.vec, src, size_t(s.n) * 4, hipMemcpyDeviceToDevice, stream));
             return MK_OK;
@@ -724,7 +762,7 @@ struct mk_vae {
     }
 
     // ---- the decoder ----
-    // the rows of a bf16 grid that hold no pixel (a conv whose tiles cover pixels only leaves them unwritten)
+    // the rows of a half grid that hold no pixel (a conv whose tiles cover pixels only leaves them unwritten)
     mk_status zero_ring(uint16_t* buf, GridDims g, uint32_t ld)
     {
         const uint64_t n = (2ull * (g.slack() + g.pw()) + 2ull * g.h) * (ld / 8);
@@ -740,7 +778,7 @@ struct mk_vae {
     }
     // Whether a conv reads a normed grid of rows of C channels as its input: dense K over 96, or 192 channels.
     static bool reads_normed(const Conv& c, uint32_t C) { return c.ci == C && (c.dense || c.cip() == C); }
-    // lda: the input rows' stride (0: c.cip()). only: the output is only the normed rows (bf16 grid out, ldo = c.co);
+    // lda: the input rows' stride (0: c.cip()). only: the output is only the normed rows (half grid out, ldo = c.co);
     // else, with nt.g set, out gets the conv's fp32 rows (store or add) and nt.buf their norm.
     // up: the sums go to the nearest-2x grid up->out instead of back into out (an ADD; see conv3x3_up)
     mk_status conv3(const Conv& c, const void* in, GridDims g, void* out, uint32_t ldo, bool add, uint32_t lda = 0,
@@ -757,7 +795,7 @@ struct mk_vae {
         a.c = c.cip();
         a.n = c.cop();
         a.ldy = ldo;
-        a.y_dtype = only ? MK_BF16 : MK_F32;
+        a.y_dtype = only ? MK_F16 : MK_F32;
         a.epilogue = add ? MK_EPI_ADD : MK_EPI_STORE;
         ConvNorm nm;
         if (nt.g) {
@@ -781,7 +819,7 @@ struct mk_vae {
             return nt.g ? fail(MK_ERR_ARG, "vae: a 2x-grid output has no norm") : conv3x3_up(&a, *up, stream);
         return nt.g ? conv3x3_fused(&a, nm, stream) : mk_conv3x3(&a, stream);
     }
-    // 1 x 1 conv over rows (grid or compact): y[rows][ldo] (fp32 or bf16) = a[rows][cip] W^T + b (or +=)
+    // 1 x 1 conv over rows (grid or compact), half operands: y[rows][ldo] (fp32 or half) = a[rows][cip] W^T + b (or +=)
     mk_status conv1(const Conv& c, uint32_t part, const void* a, uint64_t rows, void* out, uint32_t ldo,
                     uint32_t out_dtype, uint32_t epi)
     {
@@ -796,7 +834,7 @@ struct mk_vae {
         g.lda = c.cip();
         g.ldc = ldo;
         g.batch = 1;
-        g.w_dtype = MK_BF16;
+        g.w_dtype = MK_F16;
         g.c_dtype = out_dtype;
         g.epilogue = epi;
         return mk_gemm(&g, stream);
@@ -848,7 +886,7 @@ struct mk_vae {
     // res_block (engine.cpp:732-746): x (fp32 grid, stride cs = c2.cop() after) <- conv2(silu(norm2(conv1(
     // silu(norm1(x)))))) + shortcut(x). x and the result may differ in channels; xs is x's stride. At 96 and 192
     // channels the norms come from the convs' epilogues: normed_in (rows of the channels) already holds silu(norm1(x)),
-    // conv1 writes silu(norm2(.)) straight into t as conv2's bf16 input, and with next.g conv2 also writes the norm the
+    // conv1 writes silu(norm2(.)) straight into t as conv2's half input, and with next.g conv2 also writes the norm the
     // next layer takes of the result into next.buf (which conv2 does not read).
     // With up, conv2's sums go to the nearest-2x grid (see conv3x3_up) and x is left as it was.
     mk_status res_block(const Res& r, GridDims g, float*& xp, uint32_t xs, float*& yp, const uint16_t* normed_in = nullptr,
@@ -889,42 +927,59 @@ struct mk_vae {
         return MK_OK;
     }
 
-    // vae_attention (engine.cpp:748-777): one head over the n pixels, d = c
+    // vae_attention (engine.cpp:748-777): one head over the n pixels, d = c, in the reference's precision: the scores
+    // are half queries times fp32 keys, the output half probabilities times fp32 values (its gemm_->encode with F32
+    // K / V^T and halves() of Q and P, engine.cpp:764-773). The matrix cores multiply halves, so each fp32 operand
+    // goes in as two half planes hi + lo (vae_split_kernel): scores = [Q | Q] [K_hi | K_lo]^T (a GEMM over 2 c), the
+    // output = P [V^T_hi ; V^T_lo]^T with the two c-wide halves summed in the epilogue (MK_EPI_PAIR_SUM).
     mk_status attention(GridDims g, float* xp)
     {
         const uint32_t c = qkv.co, cp = qkv.cip();
         const uint64_t n = uint64_t(g.h) * g.w, np = (n + 63) / 64 * 64;
-        // q [np][cp], k [np][cp] (rows past n zero), v^T [cp][np], the normed pixels [np][cp] (rows past n zero)
-        MK_TRY(ensure(qb, np * cp * 2));
-        MK_TRY(ensure(kb, np * cp * 2));
-        MK_TRY(ensure(vtb, np * cp * 2));
+        // q2 [np][2 cp] = [Q | Q], k2 [np][2 cp] = [K_hi | K_lo], vt2 [2 cp][np] = [V^T_hi ; V^T_lo] (halves); kf the
+        // fp32 projections (K [np][cp], then V^T [cp][np]); the normed pixels [np][cp] (rows past n zero)
+        MK_TRY(ensure(qb, np * cp * 4));
+        MK_TRY(ensure(kb, np * cp * 4));
+        MK_TRY(ensure(vtb, np * cp * 4));
+        MK_TRY(ensure(kf, np * cp * 4));
         MK_TRY(ensure(ob, np * cp * 2));
         MK_TRY(ensure(pj, np * cp * 4));
         MK_TRY(ensure(sc, np * cp * 2));
-        MK_HIP(hipMemsetAsync(kb.p, 0, np * cp * 2, stream));
         MK_HIP(hipMemsetAsync(sc.p, 0, np * cp * 2, stream));
         uint16_t* xn = static_cast<uint16_t*>(sc.p);
         MK_TRY(norm(xp, cp, g, c, attn_g, 1, xn, cp, 1, n));
-        MK_TRY(conv1(qkv, 0, xn, n, qb.p, cp, MK_BF16, MK_EPI_STORE));
-        MK_TRY(conv1(qkv, 1, xn, n, kb.p, cp, MK_BF16, MK_EPI_STORE));
+        // Q (with its bias) rounded to half, twice side by side; K (with its bias) in fp32, split
+        uint16_t* q2 = static_cast<uint16_t*>(qb.p);
+        MK_TRY(conv1(qkv, 0, xn, np, q2, 2 * cp, MK_F16, MK_EPI_STORE));
+        MK_TRY(conv1(qkv, 0, xn, np, q2 + cp, 2 * cp, MK_F16, MK_EPI_STORE));
+        float* kfp = static_cast<float*>(kf.p);
+        MK_TRY(conv1(qkv, 1, xn, np, kfp, cp, MK_F32, MK_EPI_STORE));
+        vae_split_kernel<<<blocks_for(np * cp), 256, 0, stream>>>(kfp, uint32_t(np), cp, cp, nullptr,
+                                                                  static_cast<uint16_t*>(kb.p), 2 * cp, cp);
+        MK_LAUNCH_CHECK("vae_split k");
         {
-            // v^T = W_v xn^T, no bias (added after the weighted sum: each softmax row sums to 1)
+            // V^T [cp][np] = W_v xn^T in fp32, then + the value bias and split into rows [0, cp) and [cp, 2 cp)
             mk_gemm_args v{};
             v.a = qkv.w + size_t(2) * cp * cp;
             v.w = xn;
-            v.c = vtb.p;
+            v.c = kfp;
             v.M = cp;
             v.N = uint32_t(np);
             v.K = cp;
             v.lda = cp;
             v.ldc = int64_t(np);
             v.batch = 1;
-            v.w_dtype = MK_BF16;
-            v.c_dtype = MK_BF16;
+            v.w_dtype = MK_F16;
+            v.c_dtype = MK_F32;
             v.epilogue = MK_EPI_STORE;
             MK_TRY(mk_gemm(&v, stream));
+            vae_split_kernel<<<blocks_for(np * cp), 256, 0, stream>>>(kfp, cp, uint32_t(np), uint32_t(np),
+                                                                      qkv.b + size_t(2) * cp,
+                                                                      static_cast<uint16_t*>(vtb.p), uint32_t(np),
+                                                                      uint64_t(cp) * np);
+            MK_LAUNCH_CHECK("vae_split vt");
         }
-        // Queries in groups whose bf16 P stays within 512 MB (one P V product each), and within a group in chunks
+        // Queries in groups whose half P stays within 512 MB (one P V product each), and within a group in chunks
         // whose fp32 scores (near 128 MB) stay in the memory-side cache between the score GEMM that writes them and
         // the softmax that reads them. (At 128 x 128 pixels: one group, 8 chunks of 2048 queries.)
         const uint64_t qg = std::min<uint64_t>(n, std::max<uint64_t>(256, (uint64_t(1) << 28) / np / 256 * 256));
@@ -937,16 +992,16 @@ struct mk_vae {
             for (uint64_t q0 = g0; q0 < g0 + gm; q0 += qc) {
                 const uint64_t m = std::min(qc, g0 + gm - q0);
                 mk_gemm_args s{};
-                s.a = static_cast<uint16_t*>(qb.p) + q0 * cp;
+                s.a = q2 + q0 * 2 * cp;
                 s.w = kb.p;
                 s.c = sb.p;
                 s.M = uint32_t(m);
                 s.N = uint32_t(np);
-                s.K = cp;
-                s.lda = cp;
+                s.K = 2 * cp;
+                s.lda = 2 * cp;
                 s.ldc = int64_t(np);
                 s.batch = 1;
-                s.w_dtype = MK_BF16;
+                s.w_dtype = MK_F16;
                 s.c_dtype = MK_F32;
                 s.epilogue = MK_EPI_STORE;
                 MK_TRY(mk_gemm(&s, stream));
@@ -966,17 +1021,16 @@ struct mk_vae {
             mk_gemm_args o{};
             o.a = pb.p;
             o.w = vtb.p;
-            o.bias = qkv.b + size_t(2) * cp;
             o.c = static_cast<uint16_t*>(ob.p) + g0 * cp;
             o.M = uint32_t(gm);
-            o.N = cp;
+            o.N = 2 * cp;
             o.K = uint32_t(np);
             o.lda = int64_t(np);
             o.ldc = cp;
             o.batch = 1;
-            o.w_dtype = MK_BF16;
-            o.c_dtype = MK_BF16;
-            o.epilogue = MK_EPI_STORE;
+            o.w_dtype = MK_F16;
+            o.c_dtype = MK_F16;
+            o.epilogue = MK_EPI_PAIR_SUM;
             MK_TRY(mk_gemm(&o, stream));
         }
         MK_TRY(conv1(proj, 0, ob.p, n, pj.p, cp, MK_F32, MK_EPI_STORE));
@@ -1157,19 +1211,20 @@ mk_status mk_vae_load(mk_vae* v, const char* name, const float* data, const int6
     for (uint32_t i = 0; i < ndim; ++i)
         n *= uint64_t(dims[i]);
     const bool mat = it->second.kind == mk_vae::Slot::CONV_W || it->second.kind == mk_vae::Slot::PQ_W;
+    // convolution weights go in as half (rounded to nearest even: an F16 checkpoint's values exactly)
     std::vector<uint16_t> hb;
     const void* host = data;
     if (mat) {
         hb.resize(n);
         for (uint64_t i = 0; i < n; ++i)
-            hb[i] = f2bf_bits(data[i]);
+            hb[i] = f2h_bits(data[i]);
         host = hb.data();
     }
     void* tmp = nullptr;
     MK_HIP(hipMalloc(&tmp, n * (mat ? 2 : 4)));
     mk_status st = hip_ok(hipMemcpy(tmp, host, n * (mat ? 2 : 4), hipMemcpyHostToDevice), "vae_load copy");
     if (st == MK_OK)
-        st = v->put(it->second, tmp, kt);
+        st = v->put(it->second, tmp, kt, true);
     if (st == MK_OK)
         st = hip_ok(hipStreamSynchronize(v->stream), "vae_load sync");
     (void)hipFree(tmp);
@@ -1192,7 +1247,7 @@ mk_status mk_vae_init_random(mk_vae* v, uint64_t seed)
         mk_status st = mk_fill_normal(tmp, n, mat ? MK_BF16 : MK_F32, tensor_key(seed, name.c_str()),
                                       gamma ? 1.0 : 0.0, sd, v->stream);
         if (st == MK_OK)
-            st = v->put(s, tmp, 1);
+            st = v->put(s, tmp, 1, false); // bf16 draws, stored as the nearest halves
         if (st == MK_OK)
             st = hip_ok(hipStreamSynchronize(v->stream), "vae_init_random sync");
         (void)hipFree(tmp);

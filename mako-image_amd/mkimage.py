@@ -15,7 +15,8 @@ HERE = pathlib.Path(__file__).resolve().parent
 LIB_PATH = HERE / "libmkimage.so"
 
 F32, BF16, FP8, F16, DTYPE_OTHER = 0, 1, 2, 3, 255
-EPI_STORE, EPI_GELU_TANH, EPI_GATE_ADD, EPI_GATE_TANH, EPI_SILU, EPI_ADD, EPI_HEADS, EPI_SWIGLU, EPI_GEGLU = range(9)
+EPI_STORE, EPI_GELU_TANH, EPI_GATE_ADD, EPI_GATE_TANH, EPI_SILU, EPI_ADD, EPI_HEADS, EPI_SWIGLU, EPI_GEGLU, \
+    EPI_PAIR_SUM = range(10)
 FAMILY_DUAL, FAMILY_Q21, FAMILY_SDXL = 0, 1, 2
 
 _vp, _sz, _u32, _u64, _i64, _f, _d, _i = (C.c_void_p, C.c_size_t, C.c_uint32, C.c_uint64, C.c_int64, C.c_float,
@@ -281,7 +282,7 @@ def gemm_extents(g, what="mk_gemm"):
     if g.M == 0 or g.N == 0:
         return
     b = max(int(g.batch), 1)
-    glu = g.epilogue in (EPI_SWIGLU, EPI_GEGLU)
+    glu = g.epilogue in (EPI_SWIGLU, EPI_GEGLU, EPI_PAIR_SUM)
     check_extent(g.a, ((b - 1) * g.stride_a + (g.M - 1) * g.lda + g.K) * 2, what + ": A")
     check_extent(g.w, g.N * g.K * (1 if g.w_dtype == FP8 else 2), what + ": W")
     check_extent(g.wscale, g.N * 4, what + ": wscale")

@@ -1054,8 +1054,11 @@ int mkref_sdxl_trans(const mkref_model* mp, const float* x, int64_t n, const flo
 // VAE decoder: src/image/engine.cpp:589-628 (the weights it loads), 722-746 (norm_silu, res_block), 748-777
 // (vae_attention), 862-954 (decode: latent denormalisation over 2x2 patches, post_quant_conv, conv_in, mid block,
 // up blocks with nearest 2x upsampling, norm_out + SiLU, conv_out, clamp to [-1, 1], alpha 1). Images are
-// [pixels][channels] fp32; every conv input is rounded to bf16 (the device feeds bf16 to its matrix cores), sums in
-// double. The RMS norm is x / sqrt(sum x^2 + 1e-24) * sqrt(c) * gamma (engine.cpp:725-727).
+// [pixels][channels] fp32. Precision points as the reference runs them: every convolution multiplies F16 weights with
+// its input rounded to half (docs/performance.md:13: "the VAE's convolution weights in F16 on that GEMM"; its GEMM
+// takes half activations), sums in double here; the mid block's attention multiplies half queries with fp32 keys and
+// half probabilities with fp32 values (engine.cpp:764-773: gemm_->encode with F32 kc / vt and halves() of Q and P).
+// The RMS norm is x / sqrt(sum x^2 + 1e-24) * sqrt(c) * gamma (engine.cpp:725-727).
 // =====================================================================================================================
 
 struct mkref_vae {
@@ -1092,16 +1095,17 @@ void vae_add(mkref_vae* m, const std::string& name, std::vector<int64_t> dims, u
     m->t[name] = {std::move(v), std::move(dims)};
 }
 
-// y = conv(bf16(x)) + bias, k = 1 or 3, zero padding; or y += that (accumulate).
+// y = conv(half(x)) with half(W) + bias, k = 1 or 3, zero padding; or y += that (accumulate).
 void vae_conv(const mkref_vae* m, const std::string& p, const Img& x, Img& y, bool accumulate)
 {
-    const std::vector<float>& W = m->w(p + ".weight");
+    std::vector<float> W(m->w(p + ".weight"));
+    mkref_round_f16(W.data(), W.size());
     const std::vector<float>& b = m->w(p + ".bias");
     const int64_t co = m->dim(p + ".weight", 0), ci = m->dim(p + ".weight", 1), k = m->dim(p + ".weight", 2);
     if (ci != x.c)
         throw std::runtime_error("vae_conv: channels");
     std::vector<float> xb(x.v);
-    mkref_round_bf16(xb.data(), xb.size());
+    mkref_round_f16(xb.data(), xb.size());
     if (!accumulate)
         y = Img(x.h, x.w, uint32_t(co));
     const int H = int(x.h), Wd = int(x.w), r = int(k / 2);
@@ -1130,7 +1134,8 @@ void vae_conv(const mkref_vae* m, const std::string& p, const Img& x, Img& y, bo
             }
 }
 
-// RMS norm over each pixel's channels with gamma, then SiLU (silu = true); the result as bf16 values.
+// RMS norm over each pixel's channels with gamma, then SiLU (silu = true); the result as half values (the next
+// convolution's input).
 Img vae_norm(const Img& x, const std::vector<float>& g, bool silu)
 {
     Img y(x.h, x.w, x.c);
@@ -1146,7 +1151,7 @@ Img vae_norm(const Img& x, const std::vector<float>& g, bool silu)
             float v = a[c] * r * g[c];
             if (silu)
                 v = v / (1.0f + std::exp(-v));
-            y.v[i * x.c + c] = bf16(v);
+            y.v[i * x.c + c] = f16(v);
         }
     }
     return y;
@@ -1165,8 +1170,9 @@ void vae_res(const mkref_vae* m, const std::string& p, Img& x)
     x = std::move(y);
 }
 
-// One-head attention over the pixels (engine.cpp:748-777): q, k, v from the 1x1 to_qkv conv of the normed image,
-// softmax(q k^T / sqrt(c)) v with q, k, v and P rounded to bf16, then proj and the residual.
+// One-head attention over the pixels (engine.cpp:748-777): q, k, v (with their biases) from the 1x1 to_qkv conv of
+// the normed image, softmax(q k^T / sqrt(c)) v with q and P rounded to half and k, v in fp32, then proj and the
+// residual.
 void vae_attn(const mkref_vae* m, Img& x)
 {
     const std::string a = "decoder.mid_block.attentions.0.";
@@ -1174,21 +1180,10 @@ void vae_attn(const mkref_vae* m, Img& x)
     Img xn = vae_norm(x, m->w(a + "norm.gamma"), false);
     Img qkv;
     vae_conv(m, a + "to_qkv", xn, qkv, false);
-    mkref_round_bf16(qkv.v.data(), qkv.v.size());
-    // the value bias is added after the weighted sum (the weights of a row sum to 1)
-    const std::vector<float>& bq = m->w(a + "to_qkv.bias");
-    std::vector<float> vraw(size_t(n) * c);
-    {
-        // v without its bias, rounded to bf16 as the device stores V^T
-        const std::vector<float>& W = m->w(a + "to_qkv.weight");
-        for (uint32_t i = 0; i < n; ++i)
-            for (uint32_t o = 0; o < c; ++o) {
-                double acc = 0.0;
-                for (uint32_t k = 0; k < c; ++k)
-                    acc += double(xn.v[size_t(i) * c + k]) * W[size_t(2 * c + o) * c + k];
-                vraw[size_t(i) * c + o] = bf16(float(acc));
-            }
-    }
+    // q -> half; k, v stay fp32
+    for (uint32_t i = 0; i < n; ++i)
+        for (uint32_t k = 0; k < c; ++k)
+            qkv.v[size_t(i) * 3 * c + k] = f16(qkv.v[size_t(i) * 3 * c + k]);
     Img o(x.h, x.w, c);
     const double scale = 1.0 / std::sqrt(double(c));
 #pragma omp parallel for schedule(dynamic)
@@ -1208,8 +1203,8 @@ void vae_attn(const mkref_vae* m, Img& x)
         for (uint32_t k = 0; k < c; ++k) {
             double acc = 0.0;
             for (uint32_t j = 0; j < n; ++j)
-                acc += double(bf16(float(s[j] / sum))) * vraw[size_t(j) * c + k];
-            o.v[size_t(i) * c + k] = bf16(float(acc) + bq[2 * c + k]);
+                acc += double(f16(float(s[j] / sum))) * qkv.v[size_t(j) * 3 * c + 2 * c + k];
+            o.v[size_t(i) * c + k] = float(acc);
         }
     }
     vae_conv(m, a + "proj", o, x, true);
@@ -1301,19 +1296,9 @@ int mkref_vae_decode(const mkref_vae* m, const float* tokens, uint32_t h, uint32
                         for (uint32_t px = 0; px < 2; ++px)
                             lat.v[((size_t(2 * y + py)) * 2 * w + 2 * x + px) * z + c] =
                                 tokens[(size_t(y) * w + x) * L + (c * 2 + py) * 2 + px] * m->std_[c] + m->mean[c];
-        // post_quant_conv in fp32 (the device applies it while unpacking the tokens), then conv_in
-        Img pq(lat.h, lat.w, z);
-        {
-            const std::vector<float>& W = m->w("post_quant_conv.weight");
-            const std::vector<float>& b = m->w("post_quant_conv.bias");
-            for (size_t i = 0; i < size_t(lat.h) * lat.w; ++i)
-                for (uint32_t o = 0; o < z; ++o) {
-                    double acc = 0.0;
-                    for (uint32_t c = 0; c < z; ++c)
-                        acc += double(lat.v[i * z + c]) * W[size_t(o) * z + c];
-                    pq.v[i * z + o] = float(acc) + b[o];
-                }
-        }
+        // post_quant_conv (a 1x1 convolution: half inputs, half weights), then conv_in
+        Img pq;
+        vae_conv(m, "post_quant_conv", lat, pq, false);
         Img x;
         vae_conv(m, "decoder.conv_in", pq, x, false);
         pr("vae_conv_in", -1, x);

@@ -78,6 +78,49 @@ def gemm_grouped(*args):
 
 # ---------------------------------------------------------------------------------------------------------------
 # GEMM
+
+def hdev(a):
+    """IEEE half device copy of a float array."""
+    d = M.Dev.from_array(M.f16_bits(a))
+    _live.append(d)
+    return d
+
+
+# f16 operands (the VAE's products): STORE into fp32 and half, ADD into fp32, and the pair sum of a weight stacked as
+# two halves, over the tile shapes the plan takes (few rows: 128 x 128; 64-, 128- and 256-wide tiles)
+@pytest.mark.parametrize("Mr, N, K", [(100, 256, 128), (700, 256, 192), (600, 128, 256), (1000, 64, 320),
+                                      (3000, 512, 128)])
+def test_gemm_half_operands_match_float64(gpu, rng, Mr, N, K):
+    A = rng.standard_normal((Mr, K)).astype(np.float32)
+    W = (rng.standard_normal((N, K)) / np.sqrt(K)).astype(np.float32)
+    b = rng.standard_normal(N).astype(np.float32) * 0.1
+    Ah, Wh = M.f16_to_f32(M.f16_bits(A)).astype(np.float64), M.f16_to_f32(M.f16_bits(W)).astype(np.float64)
+    want = Ah @ Wh.T + b
+    dA, dW, db = hdev(A), hdev(W), dev(b)
+    c32 = dev(np.zeros((Mr, N), np.float32))
+    gemm(dA, dW, bias=db, c=c32, c_dtype=M.F32, M_=(Mr, N, K), lda=K, ldc=N, w_dtype=M.F16)
+    assert maxrel(fetch(c32, (Mr, N)), want) <= 1e-5
+    c16 = dev(np.zeros((Mr, N), np.uint16))
+    gemm(dA, dW, bias=db, c=c16, c_dtype=M.F16, M_=(Mr, N, K), lda=K, ldc=N, w_dtype=M.F16)
+    assert maxrel(M.f16_to_f32(c16.to_array(np.uint16, (Mr, N))), want) <= 2.0 ** -11
+    x0 = rng.standard_normal((Mr, N)).astype(np.float32)
+    cx = dev(x0)
+    gemm(dA, dW, bias=db, c=cx, c_dtype=M.F32, M_=(Mr, N, K), lda=K, ldc=N, w_dtype=M.F16, epi=M.EPI_ADD)
+    assert maxrel(fetch(cx, (Mr, N)), x0 + want) <= 1e-5
+    if N % 128 == 0:
+        # an fp32 weight as hi + lo halves stacked along the rows: C = A (W_hi + W_lo)^T, half output
+        F_ = N // 2
+        Wf = (rng.standard_normal((F_, K)) / np.sqrt(K)).astype(np.float32)
+        hi = M.f16_to_f32(M.f16_bits(Wf))
+        lo = M.f16_to_f32(M.f16_bits(Wf - hi))
+        cp = dev(np.zeros((Mr, F_), np.float32))
+        gemm(dA, hdev(np.concatenate([hi, lo])), c=cp, c_dtype=M.F32, M_=(Mr, N, K), lda=K, ldc=F_, w_dtype=M.F16,
+             epi=M.EPI_PAIR_SUM)
+        got = fetch(cp, (Mr, F_))
+        # hi + lo holds the fp32 weight to ~2^-22: the product matches the fp32 weight's, not only its half rounding
+        assert maxrel(got, Ah @ Wf.astype(np.float64).T) <= 1e-5
+        assert maxrel(Ah @ hi.astype(np.float64).T, Ah @ Wf.astype(np.float64).T) > 1e-5
+
 # ---------------------------------------------------------------------------------------------------------------
 
 @pytest.mark.parametrize("Mr,N,K", [(300, 256, 192), (512, 1024, 256), (77, 128, 64), (1000, 64, 128), (5, 640, 2560)])

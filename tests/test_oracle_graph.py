@@ -235,20 +235,22 @@ def test_sdxl_trans_matches_torch():
 
 
 # ---- VAE decoder (src/image/engine.cpp:862-954), written in the idiom of the public Wan-2.1 decoder: conv2d with
-# padding 1, RMS norm over channels, nearest interpolation, one-head scaled_dot_product_attention ----
+# padding 1, RMS norm over channels, nearest interpolation, one-head attention; at the reference's precision points:
+# half weights and half inputs for every convolution (docs/performance.md:13), half queries and probabilities against
+# fp32 keys and values in the attention (engine.cpp:764-773) ----
 
-def vae_reference(vae, tokens, h, w):
+def vae_reference(vae, tokens, h, w, rnd=hf):
     t = {n: torch.from_numpy(a).double() for n, a in vae.tensors()}
     z = vae.z
 
-    def conv(x, name):  # x [1][c][H][W]; the conv input rounded to bf16
+    def conv(x, name):  # x [1][c][H][W]; the input and the weights rounded to half
         W = t[name + ".weight"]
-        return F.conv2d(bf(x), W, t[name + ".bias"], padding=W.shape[-1] // 2)
+        return F.conv2d(rnd(x), rnd(W), t[name + ".bias"], padding=W.shape[-1] // 2)
 
     def rms(x, g, silu=True):
         c = x.shape[1]
         y = x / torch.sqrt((x * x).sum(1, keepdim=True) + 1e-24) * (c ** 0.5) * g[None, :, None, None]
-        return bf(F.silu(y) if silu else y)
+        return rnd(F.silu(y) if silu else y)
 
     def res(x, p):
         hh = conv(rms(x, t[p + ".norm1.gamma"]), p + ".conv1")
@@ -259,23 +261,21 @@ def vae_reference(vae, tokens, h, w):
         a = "decoder.mid_block.attentions.0."
         _, c, H, W_ = x.shape
         xn = rms(x, t[a + "norm.gamma"], silu=False)
-        Wq = t[a + "to_qkv.weight"][:, :, 0, 0]
+        Wq = rnd(t[a + "to_qkv.weight"][:, :, 0, 0])
         bq = t[a + "to_qkv.bias"]
         seq = xn.flatten(2).transpose(1, 2)[0]  # [n][c]
-        q = bf(F.linear(seq, Wq[:c], bq[:c]))
-        k = bf(F.linear(seq, Wq[c:2 * c], bq[c:2 * c]))
-        v = bf(F.linear(seq, Wq[2 * c:]))  # the value bias joins after the weighted sum
-        p = bf(torch.softmax((q @ k.T).float().double() / c ** 0.5, dim=-1))  # scores fp32, P bf16
-        o = bf(p @ v + bq[2 * c:])
-        o = o.T.reshape(1, c, H, W_)
+        q = hf(F.linear(seq, Wq[:c], bq[:c]))  # half queries
+        k = F.linear(seq, Wq[c:2 * c], bq[c:2 * c])  # fp32 keys and values
+        v = F.linear(seq, Wq[2 * c:], bq[2 * c:])
+        p = hf(torch.softmax((q @ k.T).float().double() / c ** 0.5, dim=-1))  # scores fp32, P half
+        o = (p @ v).T.reshape(1, c, H, W_)
         return x + conv(o, a + "proj")
 
     tok = torch.from_numpy(np.asarray(tokens, np.float64)).reshape(h, w, z, 2, 2)
     lat = tok.permute(2, 0, 3, 1, 4).reshape(1, z, 2 * h, 2 * w)  # channel c of pixel (2y + py, 2x + px)
     lat = lat * torch.from_numpy(vae.std).double()[None, :, None, None] + \
         torch.from_numpy(vae.mean).double()[None, :, None, None]
-    Wp = t["post_quant_conv.weight"]
-    x = F.conv2d(lat, Wp, t["post_quant_conv.bias"])  # fp32 on both sides, no bf16 rounding of its input
+    x = conv(lat, "post_quant_conv")  # a 1x1 convolution like the others
     x = conv(x, "decoder.conv_in")
     x = res(x, "decoder.mid_block.resnets.0")
     x = attn(x)
@@ -299,4 +299,7 @@ def test_vae_decode_matches_torch(h, w):
     got = vae.decode(tokens, h, w)
     want = vae_reference(vae, tokens, h, w)
     assert got.shape == (16 * h, 16 * w, 4) and np.all(got[..., 3] == 1)
-    agree(got[..., :3], want[..., :3])
+    agree(got[..., :3], want[..., :3], tol_rel=1.5e-3)
+    # the precision points matter at that tolerance: the same graph with bf16 convolution operands is 4x outside it
+    d = R.diff(got[..., :3], vae_reference(vae, tokens, h, w, rnd=bf)[..., :3], 3)
+    assert d["rel"] > 4e-3, d
