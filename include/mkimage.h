@@ -88,7 +88,8 @@ typedef struct mk_heads_args {
     /* Destination of the fused q/k/v epilogue: Q, K [batch][heads][n_pad][d] bf16 and V^T [batch][heads][d][k_pad]
      * bf16 (keys in the MK_VT_COL order), written at rows row0 + r (r the GEMM row within the batch). The GEMM's N
      * columns are q|k|v (N = 3 heads d), or Q alone when k and vt are NULL (N = heads d: a cross attention's query,
-     * sdxl.cpp:778-779). head_dim 128 (norm and RoPE optional) or 64 (the SDXL heads: no norm, no RoPE). */
+     * sdxl.cpp:778-779), or, for head_dim 64, K and V^T alone when q is NULL (N = 2 heads d: a cross attention's
+     * context, sdxl.cpp:697-708). head_dim 128 (norm and RoPE optional) or 64 (the SDXL heads: no norm, no RoPE). */
     void* q;
     void* k;
     void* vt;

@@ -841,14 +841,16 @@ struct mk_engine {
         sdxl_spad = s_pad;
         MK_TRY(timed("convert", 0, [&] { return mk_f32_to_bf16(g.prompt.f(), size_t(S) * E, tn.p, stream); }));
         for (uint32_t i = 0; i < cfg.blocks; ++i) {
-            MK_TRY(gemm(blocks[i].kv2, tn.p, E, 0, S, 1, qkv.p, 2 * c, 0, MK_EPI_STORE, MK_BF16));
-            uint16_t* kd = slots[0].ck.h() + (size_t(i) * 2 + slot) * H * s_pad * 64;
-            uint16_t* vd = slots[0].cvt.h() + (size_t(i) * 2 + slot) * H * 64 * s_pad;
-            // the reference's half heads (heads_half, sdxl.cpp:439-448)
-            MK_TRY(mk_heads(qkv.p, 1, S, 2 * c, 0, 0, H, 64, nullptr, 0, nullptr, 0, kd, s_pad, 0, 0, MK_F16,
-                            stream));
-            MK_TRY(mk_heads(qkv.p, 1, S, 2 * c, 0, c, H, 64, nullptr, 0, nullptr, 0, vd, s_pad, 0, 1, MK_F16,
-                            stream));
+            // the reference's half heads of the fp32 projection (heads_half, sdxl.cpp:697-708): the k|v GEMM's
+            // epilogue rounds its accumulators to half once, straight into K and V^T
+            mk_heads_args ha{};
+            ha.k = slots[0].ck.h() + (size_t(i) * 2 + slot) * H * s_pad * 64;
+            ha.vt = slots[0].cvt.h() + (size_t(i) * 2 + slot) * H * 64 * s_pad;
+            ha.heads = H;
+            ha.head_dim = 64;
+            ha.k_pad = s_pad;
+            ha.dtype = MK_F16;
+            MK_TRY(gemm(blocks[i].kv2, tn.p, E, 0, S, 1, nullptr, 0, 0, MK_EPI_HEADS, MK_BF16, nullptr, 0, 0, 0, &ha));
         }
         return MK_OK;
     }

@@ -456,11 +456,14 @@ __device__ inline void epi_heads(const GemmP& p, const float* st, int ld, int to
 
 // The heads epilogue for 64-dim heads (the SDXL form: no norm, no RoPE) on 128-channel tiles, whose wave slice of
 // 32 tokens x 64 channels is one head: Q / K rows [bh][row][64] (16 lanes a row, 4 channels each), V^T rows
-// [bh][d][k_pad] (a lane per dim, 32 keys in the vt_col order). Q-only launches (k == NULL) write Q alone.
+// [bh][d][k_pad] (a lane per dim, 32 keys in the vt_col order). Q-only launches (k == NULL) write Q alone, k|v-only
+// launches (q == NULL: the cross attention's context, heads_half from the fp32 projection, sdxl.cpp:697-708) K and
+// V^T, each rounded once from the fp32 accumulators.
 __device__ inline void epi_heads64(const GemmP& p, const float* st, int ld, int tok0, int nw0, int lane, uint32_t z)
 {
     const HeadsP& h = p.hp;
-    const int which = nw0 / int(h.dim), head = (nw0 % int(h.dim)) / 64;
+    // 0 q, 1 k, 2 v (a k|v-only launch, q NULL, starts at k)
+    const int which = nw0 / int(h.dim) + (h.q ? 0 : 1), head = (nw0 % int(h.dim)) / 64;
     const int64_t bh = int64_t(z) * h.heads + head;
     const int last = int(p.M) - 1;
     if (which == 2) {
@@ -1554,21 +1557,23 @@ mk_status prepare(const mk_gemm_args* a, GemmP& p, bool conv = false)
         // q|k|v columns (N = 3 heads d), or q alone (k and vt NULL: N = heads d); d = 128 on 256-channel tiles
         // (per-head RMSNorm and RoPE optional), d = 64 on 128-channel tiles (no norm, no RoPE)
         const mk_heads_args* h = a->heads;
-        const bool qonly = h && !h->k && !h->vt;
-        const uint32_t parts = qonly ? 1 : 3, d = h ? h->head_dim : 0;
-        bool ok = h && h->q && (qonly || (h->k && h->vt)) && (d == 128 || d == 64) && h->heads &&
-                  uint64_t(a->N) == uint64_t(parts) * h->heads * d && h->k_pad % 16 == 0 &&
-                  (qonly || uint64_t(h->row0) + a->M <= h->k_pad) && uint64_t(h->q_row0) + a->M <= h->q_pad &&
+        // q|k|v, q alone (k, vt NULL), or, for 64-dim heads, k|v alone (q NULL: a cross attention's context)
+        const bool qonly = h && h->q && !h->k && !h->vt, kvonly = h && !h->q && h->k && h->vt;
+        const uint32_t parts = qonly ? 1 : kvonly ? 2 : 3, d = h ? h->head_dim : 0;
+        bool ok = h && (h->q || kvonly) && (qonly || (h->k && h->vt)) && (d == 128 || d == 64) && h->heads &&
+                  (!kvonly || d == 64) && uint64_t(a->N) == uint64_t(parts) * h->heads * d && h->k_pad % 16 == 0 &&
+                  (qonly || uint64_t(h->row0) + a->M <= h->k_pad) &&
+                  (kvonly || uint64_t(h->q_row0) + a->M <= h->q_pad) &&
                   (h->dtype == 0 || h->dtype == MK_BF16 || h->dtype == MK_F16);
         if (d == 128)
             ok = ok && a->N % 256 == 0 && h->rope_mode <= 2 && (!h->rope_mode || h->rope);
         else
             ok = ok && a->N % 128 == 0 && h->rope_mode == 0 && !h->norm_q && !h->norm_k;
         if (!ok)
-            return fail(MK_ERR_ARG, "gemm heads epilogue: needs q (and k, vt, or neither: Q only), N = 3 (or 1) x "
-                                    "heads x head_dim, head_dim 128 with N a multiple of 256 or head_dim 64 with N a "
-                                    "multiple of 128 and no norm or RoPE, k_pad a multiple of 16, row0 + M within "
-                                    "the padded rows, and dtype bf16 or f16");
+            return fail(MK_ERR_ARG, "gemm heads epilogue: needs q, k, vt (N = 3 x heads x head_dim), q alone (1 x) "
+                                    "or, for head_dim 64, k and vt alone (2 x), head_dim 128 with N a multiple of "
+                                    "256 or head_dim 64 with N a multiple of 128 and no norm or RoPE, k_pad a "
+                                    "multiple of 16, row0 + M within the padded rows, and dtype bf16 or f16");
         p.hp = HeadsP{static_cast<uint16_t*>(h->q), static_cast<uint16_t*>(h->k), static_cast<uint16_t*>(h->vt),
                       h->heads, h->q_pad, h->k_pad, h->row0, h->q_row0, h->rope_mode, a->N / parts, h->norm_q,
                       h->norm_k, h->rope, h->eps, h->k_scale == 0.0f ? 1.0f : h->k_scale, h->dtype == MK_F16 ? 1u : 0u,

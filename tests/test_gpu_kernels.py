@@ -86,6 +86,31 @@ def hdev(a):
     return d
 
 
+# the cross attention's context K and V^T from one k|v GEMM (q NULL), as half from the fp32 accumulators
+# (sdxl.cpp:697-708: heads_half of the fp32 projection): within one half rounding of the float64 product, where a bf16
+# intermediate (bf16 store, then half) is not
+def test_gemm_heads64_kv_only_rounds_once(gpu, rng):
+    S, E, H = 77, 2048, 4
+    s_pad = 80
+    A = rng.standard_normal((S, E)).astype(np.float32)
+    W = R.bf16_round((rng.standard_normal((2 * H * 64, E)) / np.sqrt(E)).astype(np.float32))
+    b = rng.standard_normal(2 * H * 64).astype(np.float32) * 0.1
+    Kd, Vt = M.Dev(H * s_pad * 64 * 2), M.Dev(H * 64 * s_pad * 2)
+    _live.extend([Kd, Vt])
+    ha = M.HeadsArgs(None, Kd.p, Vt.p, H, 64, 0, s_pad, 0, 0, None, None, None, 0, 1e-6, 0.0, M.F16)
+    gemm(bdev(A), bdev(W), bias=dev(b), epi=M.EPI_HEADS, c_dtype=M.BF16, M_=(S, 2 * H * 64, E), lda=E, heads=ha)
+    y = R.bf16_round(A).astype(np.float64) @ W.astype(np.float64).T + b
+    k_want = y[:, :H * 64].reshape(S, H, 64).transpose(1, 0, 2)
+    v_want = y[:, H * 64:].reshape(S, H, 64).transpose(1, 2, 0)
+    k_got = M.f16_to_f32(Kd.to_array(np.uint16, (H, s_pad, 64)))[:, :S]
+    v_got = M.f16_to_f32(Vt.to_array(np.uint16, (H, 64, s_pad)))[:, :, M.vt_col(np.arange(S))]
+    for got, want in ((k_got, k_want), (v_got, v_want)):
+        tol = np.abs(want) * (2.0 ** -11 + 1e-5) + 1e-6
+        assert np.all(np.abs(got - want) <= tol)
+        twice = M.f16_to_f32(M.f16_bits(R.bf16_round(want.astype(np.float32))))
+        assert np.any(np.abs(twice - want) > tol)
+
+
 # f16 operands (the VAE's products): STORE into fp32 and half, ADD into fp32, and the pair sum of a weight stacked as
 # two halves, over the tile shapes the plan takes (few rows: 128 x 128; 64-, 128- and 256-wide tiles)
 @pytest.mark.parametrize("Mr, N, K", [(100, 256, 128), (700, 256, 192), (600, 128, 256), (1000, 64, 320),
