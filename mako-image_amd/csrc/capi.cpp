@@ -119,7 +119,7 @@ mk_status mk_memset(void* p, int v, size_t bytes)
 mk_status mk_synchronize(void)
 {
     MK_HIP(hipDeviceSynchronize());
-    return gemm_take_error();
+    return gemm_take_error(nullptr, true);
 }
 
 mk_status mk_stream_create(void** s)
@@ -142,7 +142,7 @@ mk_status mk_stream_destroy(void* s)
 mk_status mk_stream_synchronize(void* s)
 {
     MK_HIP(hipStreamSynchronize(static_cast<hipStream_t>(s)));
-    return gemm_take_error();
+    return gemm_take_error(s);
 }
 
 mk_status mk_event_create(void** e)

@@ -66,9 +66,9 @@ struct GemmPlan {
 GemmPlan gemm_plan(const mk_gemm_args* a, uint32_t n, uint32_t cus, bool conv = false);
 // Its estimated duration in units of one 256-channel k step.
 double gemm_cost(const mk_gemm_args* a, uint32_t n, uint32_t cus);
-// MK_ERR_DEVICE when a stream-K launch on any device gave up waiting for a partial tile since the last check (the
-// check clears it); called after synchronisations.
-mk_status gemm_take_error();
+// MK_ERR_DEVICE when a stream-K launch on `stream` (all: on any stream of any device) gave up waiting for a partial
+// tile since the last check (the check clears it); called after synchronisations of that stream (all: of the device).
+mk_status gemm_take_error(const void* stream, bool all = false);
 
 // ---- ln_modulate over one or two problems in one launch (kernels.hip; the engine groups the two streams) ----
 struct LnArgs {

@@ -1126,7 +1126,7 @@ mk_status mk_step(mk_engine* e, const float* latents, size_t n, float sigma, uin
     }
     MK_HIP(hipMemcpyAsync(out, e->out.p, N * L * 4, hipMemcpyDeviceToHost, e->stream));
     MK_HIP(hipStreamSynchronize(e->stream));
-    MK_TRY(gemm_take_error());
+    MK_TRY(gemm_take_error(e->stream));
     MK_TRY(e->finish_timing());
     return MK_OK;
 }
@@ -1201,7 +1201,7 @@ mk_status mk_step_cfg(mk_engine* e, const float* latents, size_t n, float sigma,
     MK_TRY(mk_step_cfg_device(e, e->host_in.f(), sigma, sigma_next, guidance, e->host_out.f(), nullptr));
     MK_HIP(hipMemcpyAsync(latents_out, e->host_out.p, n * 4, hipMemcpyDeviceToHost, e->stream));
     MK_HIP(hipStreamSynchronize(e->stream));
-    MK_TRY(gemm_take_error());
+    MK_TRY(gemm_take_error(e->stream));
     return MK_OK;
 }
 
@@ -1284,7 +1284,7 @@ mk_status mk_generate(mk_engine* e, const float* noise, size_t n, const float* s
     }
     MK_HIP(hipMemcpyAsync(latents_out, x[steps % 2].p, n * 4, hipMemcpyDeviceToHost, e->stream));
     MK_HIP(hipStreamSynchronize(e->stream));
-    return gemm_take_error();
+    return gemm_take_error(e->stream);
 }
 
 mk_status mk_engine_stream(mk_engine* e, void** stream)
@@ -1341,7 +1341,7 @@ mk_status mk_sdxl_forward(mk_engine* e, const float* x, uint32_t batch, uint32_t
     (void)stream;
     MK_TRY(e->sdxl_forward(x, batch, n, y));
     MK_HIP(hipStreamSynchronize(e->stream));
-    MK_TRY(gemm_take_error());
+    MK_TRY(gemm_take_error(e->stream));
     MK_TRY(e->finish_timing());
     return MK_OK;
 }

@@ -1365,14 +1365,15 @@ __global__ __launch_bounds__(64 * NW, 1) __attribute__((amdgpu_waves_per_eu(NW /
 // stream waits for that launch's event). Streams of one device thus never share partials in flight.
 // The memory is uncached: a partial written by a CU of one XCD is read by a CU of another, whose L2 is not coherent
 // with the writer's for ordinary allocations. Allocated at the full size and never freed (uncached memory a kernel has
-// read stays allocated until the process ends). The error word is pinned host memory the kernel writes when a wait
-// gives up; the host checks it at every launch and synchronisation (sk_take_error).
+// read stays allocated until the process ends). A launch that gives up a wait sets its stream's error word (pinned host
+// memory, one a stream: the error belongs to the launch's stream, whichever workspace it used); a stream's word is
+// checked and cleared when that stream is synchronised through the library or launches again, every word by a
+// device-wide synchronisation.
 struct SkWork {
     float* ws = nullptr;
     size_t ws_bytes = 0;
     uint32_t* flags = nullptr;
     uint32_t nflags = 0, epoch = 0;
-    uint32_t* err = nullptr;
     hipStream_t last = nullptr;
     hipEvent_t done = nullptr;
     uint64_t used = 0; // launch counter at its last use (least recently used first)
@@ -1381,6 +1382,8 @@ struct SkDevice {
     uint32_t cus = 0;
     uint64_t launches = 0;
     std::vector<std::unique_ptr<SkWork>> pool;
+    // the error words of the streams that launched stream-K work on this device (kept until the process ends)
+    std::vector<std::pair<hipStream_t, uint32_t*>> errs;
 };
 constexpr int kMaxDevices = 64;
 constexpr size_t kSkPool = 4;
@@ -1411,8 +1414,6 @@ mk_status sk_acquire(SkDevice& D, hipStream_t s, size_t need, uint32_t nflags, S
         MK_HIP(hipMemset(w->flags, 0, nflags * sizeof(uint32_t)));
         MK_HIP(hipStreamSynchronize(nullptr)); // cleared before the launch's stream reads them
         w->nflags = nflags;
-        MK_HIP(hipHostMalloc(reinterpret_cast<void**>(&w->err), sizeof(uint32_t), hipHostMallocCoherent));
-        *w->err = 0;
         MK_HIP(hipEventCreateWithFlags(&w->done, hipEventDisableTiming));
         pick = w.get();
         D.pool.push_back(std::move(w));
@@ -1429,11 +1430,28 @@ mk_status sk_acquire(SkDevice& D, hipStream_t s, size_t need, uint32_t nflags, S
     return MK_OK;
 }
 
-// A stream-K wait that gave up on a device (g_sk_mutex held): MK_ERR_DEVICE once, then cleared.
-mk_status sk_check(SkDevice& D)
+// The error word of stream s on a device (g_sk_mutex held), made on its first stream-K launch.
+mk_status sk_err_word(SkDevice& D, hipStream_t s, uint32_t*& out)
 {
-    for (auto& w : D.pool)
-        if (__atomic_exchange_n(w->err, 0u, __ATOMIC_RELAXED))
+    for (auto& e : D.errs)
+        if (e.first == s) {
+            out = e.second;
+            return MK_OK;
+        }
+    uint32_t* w = nullptr;
+    MK_HIP(hipHostMalloc(reinterpret_cast<void**>(&w), sizeof(uint32_t), hipHostMallocCoherent));
+    *w = 0;
+    D.errs.emplace_back(s, w);
+    out = w;
+    return MK_OK;
+}
+
+// A stream-K wait that gave up in a launch on stream s (all: on any stream) of a device (g_sk_mutex held):
+// MK_ERR_DEVICE once, then cleared.
+mk_status sk_check(SkDevice& D, hipStream_t s, bool all)
+{
+    for (auto& e : D.errs)
+        if ((all || e.first == s) && __atomic_exchange_n(e.second, 0u, __ATOMIC_RELAXED))
             return fail(MK_ERR_DEVICE, "gemm: a stream-K launch gave up waiting for a partial tile; its output is wrong");
     return MK_OK;
 }
@@ -1466,7 +1484,7 @@ mk_status launch(GemmP* p, uint32_t count, const GemmPlan& plan, hipStream_t s)
         }
         const uint32_t grid = D.cus;
         if (plan.sk && plan.dp % grid == 0 && plan.dp < tiles) {
-            MK_TRY(sk_check(D));
+            MK_TRY(sk_check(D, s, false));
             SkP sk{};
             sk.total = tiles;
             sk.dp = uint32_t(plan.dp);
@@ -1478,7 +1496,7 @@ mk_status launch(GemmP* p, uint32_t count, const GemmPlan& plan, hipStream_t s)
                 W->epoch = 1;
             sk.ws = W->ws;
             sk.flags = W->flags;
-            sk.err = W->err;
+            MK_TRY(sk_err_word(D, s, sk.err));
             sk.epoch = W->epoch;
             sk.polls = g_sk_polls;
             gemm_sk_kernel<BM, BN, kF8, EK, NW><<<grid, NT, 0, s>>>(G, sk);
@@ -1584,12 +1602,12 @@ mk_status prepare(const mk_gemm_args* a, GemmP& p, bool conv = false)
 
 } // namespace gemm_detail
 
-mk_status gemm_take_error()
+mk_status gemm_take_error(const void* stream, bool all)
 {
     using namespace gemm_detail;
     std::lock_guard<std::mutex> lock(g_sk_mutex);
     for (SkDevice& D : g_sk)
-        MK_TRY(sk_check(D));
+        MK_TRY(sk_check(D, static_cast<hipStream_t>(const_cast<void*>(stream)), all));
     return MK_OK;
 }
 
