@@ -1659,7 +1659,9 @@ GemmPlan gemm_plan(const mk_gemm_args* a, uint32_t n, uint32_t cus, bool conv)
             best = pl;
     };
     if (heads && a[0].heads && a[0].heads->head_dim == 64) {
-        consider(256, 128, 0.66);
+        // the 64-dim heads epilogue on 256-token tiles: 0.8 (measured on the SDXL shapes, 2048-8192 tokens x 1280 or
+        // 640 channels: 256 x 128 tiles took 10-25% longer than pairs of 128 x 128 at the 0.66 estimate's ties)
+        consider(256, 128, 0.8);
         if (a[0].w_dtype == MK_BF16)
             consider(128, 128, 0.67);
         return best;
@@ -1721,6 +1723,9 @@ extern "C" mk_status mk_gemm_grouped(const mk_gemm_args* a, uint32_t count, void
     const int bn = plan.bn;
     if (bn == 64 && (ek == EK_ACT || ek == EK_GLU))
         return fail(MK_ERR_UNSUPPORTED, "gemm: activation and GLU epilogues need N a multiple of 128");
+    // the heads epilogue writes one head per wave slice: 128-dim heads on 256-channel tiles, 64-dim on 128-channel
+    if (ek == EK_HEADS && !((bn == 256 && p[0].hp.hd == 128) || (bn == 128 && p[0].hp.hd == 64)))
+        return fail(MK_ERR_UNSUPPORTED, "gemm: heads epilogue tile width does not match the head dim");
     hipStream_t s = static_cast<hipStream_t>(stream);
     mk_status e;
     if (a[0].w_dtype == MK_F16) {

@@ -130,8 +130,10 @@ __global__ __launch_bounds__(256) void ln_modulate_nv_kernel(LnG g, float eps)
     }
 }
 
-// Layer norm with gamma / beta (sdxl.cpp:425-437), or RMSNorm * (w + w_offset) (rms = 1): bf16 out.
-template <bool kRms>
+// Layer norm with gamma / beta (sdxl.cpp:425-437), or RMSNorm * (w + w_offset) (rms = 1): bf16 out. One row a wave,
+// NV float4s a lane (the row's n floats, rounded up to 256): the row, gamma and beta are all requested before the
+// first reduction, so the launch waits on memory once.
+template <bool kRms, int NV>
 __global__ __launch_bounds__(256) void norm_kernel(const float* __restrict__ x, uint32_t rows, uint32_t n,
                                                    const float* __restrict__ g, const float* __restrict__ b,
                                                    float w_offset, float eps, uint16_t* __restrict__ y)
@@ -141,15 +143,23 @@ __global__ __launch_bounds__(256) void norm_kernel(const float* __restrict__ x, 
         return;
     const f32x4* xr = reinterpret_cast<const f32x4*>(x + uint64_t(row) * n);
     const uint32_t nv = n / 4;
-    f32x4 v[kMaxVec];
-    float s = 0.0f;
+    f32x4 v[NV], gg[NV], bb[NV];
 #pragma unroll
-    for (int i = 0; i < kMaxVec; ++i) {
+    for (int i = 0; i < NV; ++i) {
         const uint32_t c = lane + 64u * i;
         v[i] = c < nv ? xr[c] : f32x4{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const uint32_t c = lane + 64u * i;
+        gg[i] = c < nv ? reinterpret_cast<const f32x4*>(g)[c] : f32x4{0, 0, 0, 0};
+        bb[i] = !kRms && c < nv ? reinterpret_cast<const f32x4*>(b)[c] : f32x4{0, 0, 0, 0};
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
         s += kRms ? v[i][0] * v[i][0] + v[i][1] * v[i][1] + v[i][2] * v[i][2] + v[i][3] * v[i][3]
                   : v[i][0] + v[i][1] + v[i][2] + v[i][3];
-    }
     float mean = 0.0f, inv;
     if (kRms) {
         inv = rsqrtf(wave_sum(s) / float(n) + eps);
@@ -157,7 +167,7 @@ __global__ __launch_bounds__(256) void norm_kernel(const float* __restrict__ x, 
         mean = wave_sum(s) / float(n);
         float q = 0.0f;
 #pragma unroll
-        for (int i = 0; i < kMaxVec; ++i)
+        for (int i = 0; i < NV; ++i)
             if (lane + 64u * i < nv)
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
@@ -166,18 +176,28 @@ __global__ __launch_bounds__(256) void norm_kernel(const float* __restrict__ x, 
     }
     u32x2* yr = reinterpret_cast<u32x2*>(y + uint64_t(row) * n);
 #pragma unroll
-    for (int i = 0; i < kMaxVec; ++i) {
+    for (int i = 0; i < NV; ++i) {
         const uint32_t c = lane + 64u * i;
         if (c < nv) {
-            const f32x4 gg = reinterpret_cast<const f32x4*>(g)[c];
-            const f32x4 bb = kRms ? f32x4{0, 0, 0, 0} : reinterpret_cast<const f32x4*>(b)[c];
             float o[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j)
-                o[j] = kRms ? v[i][j] * inv * (gg[j] + w_offset) : (v[i][j] - mean) * inv * gg[j] + bb[j];
+                o[j] = kRms ? v[i][j] * inv * (gg[i][j] + w_offset) : (v[i][j] - mean) * inv * gg[i][j] + bb[i][j];
             yr[c] = u32x2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
         }
     }
+}
+
+// norm_kernel with the smallest NV >= nvec (1 .. kMaxVec float4s a lane)
+template <bool kRms, int NV = 1>
+void launch_norm(uint32_t nvec, const float* x, uint32_t rows, uint32_t n, const float* g, const float* b,
+                 float w_offset, float eps, uint16_t* y, hipStream_t stream)
+{
+    if constexpr (NV < kMaxVec) {
+        if (nvec > uint32_t(NV))
+            return launch_norm<kRms, NV + 1>(nvec, x, rows, n, g, b, w_offset, eps, y, stream);
+    }
+    norm_kernel<kRms, NV><<<cdiv(rows, 4), 256, 0, stream>>>(x, rows, n, g, b, w_offset, eps, y);
 }
 
 // Group norm statistics (sdxl.cpp:425-437), two kernels: 16-row chunks of a sample, one workgroup each, sum x and
@@ -834,8 +854,7 @@ mk_status mk_rms_norm(const float* x, uint32_t rows, uint32_t n, const float* w,
         return fail(MK_ERR_ARG, "rms_norm: null pointer, or n not a multiple of 4 up to 4096");
     if (!rows)
         return MK_OK;
-    norm_kernel<true><<<cdiv(rows, 4), 256, 0, S(stream)>>>(x, rows, n, w, nullptr, w_offset, eps,
-                                                             static_cast<uint16_t*>(y));
+    launch_norm<true>(cdiv(n / 4, 64), x, rows, n, w, nullptr, w_offset, eps, static_cast<uint16_t*>(y), S(stream));
     MK_LAUNCH_CHECK("rms_norm");
     return MK_OK;
 }
@@ -847,7 +866,7 @@ mk_status mk_layer_norm(const float* x, uint32_t rows, uint32_t n, const float* 
         return fail(MK_ERR_ARG, "layer_norm: null pointer, or n not a multiple of 4 up to 4096");
     if (!rows)
         return MK_OK;
-    norm_kernel<false><<<cdiv(rows, 4), 256, 0, S(stream)>>>(x, rows, n, g, b, 0.0f, eps, static_cast<uint16_t*>(y));
+    launch_norm<false>(cdiv(n / 4, 64), x, rows, n, g, b, 0.0f, eps, static_cast<uint16_t*>(y), S(stream));
     MK_LAUNCH_CHECK("layer_norm");
     return MK_OK;
 }
