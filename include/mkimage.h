@@ -138,8 +138,8 @@ mk_status mk_gemm(const mk_gemm_args* a, void* stream);
 mk_status mk_gemm_grouped(const mk_gemm_args* a, uint32_t count, void* stream);
 /* Long GEMMs whose last wave of tiles would leave compute units idle split that wave's k steps over the chip
  * (stream-K); the tile's owner waits, bounded, for the other ranges' partials. A wait that gives up finishes the tile
- * from what is there and is reported as MK_ERR_DEVICE by the next mk_synchronize / mk_stream_synchronize / mk_gemm /
- * engine step. This sets the bound in polls (an uncached load and a 128-cycle sleep each; default MK_GEMM_WAIT_LIMIT,
+ * from what is there and is reported as MK_ERR_DEVICE to its own stream: by that stream's next stream-K launch,
+ * mk_stream_synchronize on it, or the engine call that launched it (mk_synchronize reports any stream's). This sets the bound in polls (an uncached load and a 128-cycle sleep each; default MK_GEMM_WAIT_LIMIT,
  * tens of seconds); a test hook: 0 gives up at once. Stream-K launches on different streams use different workspaces,
  * so they may run concurrently. No counterpart in the reference. */
 #define MK_GEMM_WAIT_LIMIT (1u << 26)
