@@ -169,7 +169,7 @@ def bench_sdxl(args):
 
     M.call("mk_set_device", 0)
     rng = np.random.default_rng(0)
-    stages, per, tot_s, tot_f, tot_attn = {}, {}, 0.0, 0.0, 0.0
+    stages, per, tot_s, tot_f, tot_attn, tot_h = {}, {}, 0.0, 0.0, 0.0, 0.0
     for name, side, C, depth in SDXL_STAGES:
         n = side * side
         eng = M.Engine(M.FAMILY_SDXL, blocks=depth, dim=C, heads=C // 64, head_dim=64, ffn=4 * C,
@@ -198,9 +198,25 @@ def bench_sdxl(args):
         eng.set_timing(False)
         eng.close()
         fl, fa = sdxl_flops(n, C, depth)
+        # the same stage with half matrices (an F16 checkpoint, as SDXL's are: Engine::matrix keeps them F16)
+        eh = M.Engine(M.FAMILY_SDXL, blocks=depth, dim=C, heads=C // 64, head_dim=64, ffn=4 * C,
+                      text_dim=SDXL_CTX_DIM, weight_dtype=M.F16)
+        eh.init_random(0)
+        for s in (0, 1):
+            eh.begin(rng.standard_normal((SDXL_CTX, SDXL_CTX_DIM)).astype(np.float32), side, side, s)
+        for _ in range(args.warmup):
+            eh.sdxl_forward(x, 2, n, y)
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            eh.sdxl_forward(x, 2, n, y)
+        sec_h = (time.perf_counter() - t0) / args.steps
+        if not np.isfinite(y.to_array(np.float32, (2, n, C))).all():
+            raise RuntimeError("non-finite SDXL output (half matrices)")
+        eh.close()
         stages[name] = {"tokens": n, "channels": C, "heads": C // 64, "depth": depth, "ms": round(sec * 1e3, 3),
-                        "tflop": round(fl / 1e12, 3), "tflops": round(fl / sec / 1e12, 1)}
-        tot_s, tot_f, tot_attn = tot_s + sec, tot_f + fl, tot_attn + fa
+                        "tflop": round(fl / 1e12, 3), "tflops": round(fl / sec / 1e12, 1),
+                        "ms_f16_matrices": round(sec_h * 1e3, 3)}
+        tot_s, tot_f, tot_attn, tot_h = tot_s + sec, tot_f + fl, tot_attn + fa, tot_h + sec_h
     kernels = {k: {"ms_per_pass": round(v["ms"] / args.steps, 3), "launches_per_pass": v["launches"] // args.steps,
                    **({"tflops": round(v["flops"] / (v["ms"] / 1e3) / 1e12, 1)} if v["flops"] else {})}
                for k, v in sorted(per.items(), key=lambda kv: -kv[1]["ms"])}
@@ -219,6 +235,9 @@ def bench_sdxl(args):
                      "frac": round(gemm_tf * 1e12 / PEAK_BF16, 4) if gemm_tf else None, "traffic": None},
         "pass_tflops": round(tot_f / tot_s / 1e12, 1),
         "pass_mfma_frac": round(tot_f / tot_s / PEAK_BF16, 4),
+        "f16_matrices": {"ms_per_pass": round(tot_h * 1e3, 3), "pass_mfma_frac": round(tot_f / tot_h / PEAK_BF16, 4),
+                         "note": "weight_dtype F16: proj_in/out, to_out, attn2.to_q and ff as half (half inputs), "
+                                 "q|k|v and the context k|v bf16"},
         "kernels": kernels,
     }
     if not args.no_cpu:

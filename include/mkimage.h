@@ -252,7 +252,7 @@ mk_status mk_patchify(const float* lat, uint32_t batch, uint32_t C, uint32_t h, 
 mk_status mk_unpatchify(const float* tokens, uint32_t batch, uint32_t C, uint32_t h, uint32_t w, float* lat,
                         void* stream);
 /* Counter RNG fill (synthetic weights and inputs): value i = mean + std * N(0,1)[key, i], stored as dtype
- * (bf16 rounded to nearest even). */
+ * (MK_F32, or MK_BF16 / MK_F16 rounded to nearest even). */
 mk_status mk_fill_normal(void* p, size_t n, uint32_t dtype, uint64_t key, double mean, double std, void* stream);
 uint64_t mk_tensor_key(uint64_t seed, const char* name);
 /* Per-output-row fp8 quantisation: scale[r] = max|W[r]| / 448 (1 for a zero row), dst[r][c] = e4m3(W[r][c] /
@@ -264,7 +264,7 @@ mk_status mk_bf16_to_f32(const void* x, size_t n, float* y, void* stream);
 
 /* LoRA merge into a weight matrix on the device: W[r][c] += factor * sum_j B[r][j] A[j][c] for rows x cols, A fp32
  * [rank][cols], B fp32 [rows][rank] (rank <= 1024), the sum in fp32 in ascending j, the result rounded to W's dtype:
- * bf16 (nearest even), or e4m3 with W's per-row scale recomputed from the merged row (max / 448, cols <= 32768), the
+ * bf16 or IEEE half (nearest even), or e4m3 with W's per-row scale recomputed from the merged row (max / 448, cols <= 32768), the
  * rule mk_quantize_fp8_rows applies. The merge of a LoRA added for good (TransformerRuntime::add_lora, called from
  * src/image/h3_image.cpp:136; targets from QwenImage::lora_target, src/image/qwen_image.cpp:295-331). */
 mk_status mk_lora_merge(void* w, uint32_t w_dtype, float* w_scale, uint64_t rows, uint64_t cols, const float* a,
@@ -350,7 +350,10 @@ typedef struct mk_config {
     uint32_t ffn;        /* FFN inner width (SwiGLU / GEGLU inner) */
     uint32_t text_dim;   /* prompt embedding width */
     uint32_t latent;     /* token latent width (64) */
-    uint32_t weight_dtype; /* MK_BF16 or MK_FP8_E4M3 for the block linears */
+    uint32_t weight_dtype; /* MK_BF16 or MK_FP8_E4M3 for the block linears; MK_SDXL also MK_F16: the matrices
+                              Sdxl::load_trans reads through Engine::matrix (proj_in, proj_out, to_out, attn2.to_q, ff)
+                              are kept half, as that keeps an F16 checkpoint's (engine.cpp:292-302, sdxl.cpp:267-306),
+                              and their GEMMs take half inputs; q|k|v and the context's k|v stay bf16 */
     uint32_t max_batch;  /* 1 or 2 (CFG) */
 } mk_config;
 

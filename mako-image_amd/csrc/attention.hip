@@ -34,6 +34,7 @@ struct AttnP {
     float c; // scale * log2(e)
     // keys [hole[b][0], hole[b][1]) of batch item b are masked (a shorter prompt's padding rows); empty: none
     uint32_t hole[kMaxHoleBatch][2];
+    uint32_t out_f16; // the output as IEEE half (the input of a GEMM over half weights), else bf16
 };
 
 constexpr int kKT = 64; // keys per tile
@@ -43,10 +44,6 @@ constexpr int kKT = 64; // keys per tile
 constexpr float kLazy = 8.0f, kLazyP = 256.0f; // kLazyP = 2^kLazy
 
 typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2;
-
-// max of two scores: this file is built without NaN semantics (scores are finite or -inf), so it is one v_max_f32
-// (with NaNs honoured, each operand that comes from a matrix product is first canonicalized: two more VALU ops)
-__device__ inline float max2(float a, float b) { return fmaxf(a, b); }
 
 __device__ inline uint32_t cvt_bf16x2(float a, float b)
 {
@@ -539,13 +536,15 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     if (qi >= int(p.n_q))
         return;
     uint16_t* o = p.out + int64_t(bi) * p.so + int64_t(qi) * p.ldo + int64_t(head) * D;
+    const bool of16 = p.out_f16 != 0;
+    auto pk = [&](float a, float b) { return of16 ? pack_f16x2(a, b) : cvt_bf16x2(a, b); };
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const f32x16& a = oacc[dt];
             *reinterpret_cast<u32x2*>(o + dt * 32 + 8 * i + 4 * hk) =
-                u32x2{cvt_bf16x2(a[4 * i] * inv, a[4 * i + 1] * inv), cvt_bf16x2(a[4 * i + 2] * inv, a[4 * i + 3] * inv)};
+                u32x2{pk(a[4 * i] * inv, a[4 * i + 1] * inv), pk(a[4 * i + 2] * inv, a[4 * i + 3] * inv)};
         }
 }
 
@@ -554,14 +553,16 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
 
 using namespace mk;
 
-extern "C" mk_status mk_attention(const void* q, const void* k, const void* vt, void* out, uint32_t dtype,
-                                  uint32_t batch, uint32_t heads, uint32_t kv_heads, uint32_t d, uint32_t n_q,
-                                  uint32_t q_pad, uint32_t n_k, uint32_t k_pad, int64_t ldo, int64_t stride_o,
-                                  uint32_t q_pos0, uint32_t block, float scale, const uint32_t* key_hole,
-                                  void* stream)
+namespace mk {
+mk_status attention_to(const void* q, const void* k, const void* vt, void* out, uint32_t dtype, uint32_t batch,
+                       uint32_t heads, uint32_t kv_heads, uint32_t d, uint32_t n_q, uint32_t q_pad, uint32_t n_k,
+                       uint32_t k_pad, int64_t ldo, int64_t stride_o, uint32_t q_pos0, uint32_t block, float scale,
+                       const uint32_t* key_hole, uint32_t out_dtype, void* stream)
 {
     if (!q || !k || !vt || !out)
         return fail(MK_ERR_ARG, "attention: null pointer");
+    if (out_dtype != MK_BF16 && out_dtype != MK_F16)
+        return fail(MK_ERR_ARG, "attention: output bf16 or f16");
     if (dtype != MK_BF16 && dtype != MK_F16)
         return fail(MK_ERR_ARG, "attention: q, k, v must be bf16 or f16");
     if (!heads || !kv_heads || heads % kv_heads)
@@ -577,7 +578,7 @@ extern "C" mk_status mk_attention(const void* q, const void* k, const void* vt, 
     AttnP p{static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(vt),
             static_cast<uint16_t*>(out), heads, heads / kv_heads, batch, n_q, q_pad, n_k, k_pad, q_pos0, block, ldo,
             stride_o,
-            scale * 1.4426950408889634f, {}};
+            scale * 1.4426950408889634f, {}, out_dtype == MK_F16 ? 1u : 0u};
     if (key_hole)
         for (uint32_t b = 0; b < batch; ++b) {
             p.hole[b][0] = key_hole[2 * b];
@@ -615,4 +616,15 @@ extern "C" mk_status mk_attention(const void* q, const void* k, const void* vt, 
 #undef MK_ATTN
     MK_LAUNCH_CHECK("attention");
     return MK_OK;
+}
+} // namespace mk
+
+extern "C" mk_status mk_attention(const void* q, const void* k, const void* vt, void* out, uint32_t dtype,
+                                  uint32_t batch, uint32_t heads, uint32_t kv_heads, uint32_t d, uint32_t n_q,
+                                  uint32_t q_pad, uint32_t n_k, uint32_t k_pad, int64_t ldo, int64_t stride_o,
+                                  uint32_t q_pos0, uint32_t block, float scale, const uint32_t* key_hole,
+                                  void* stream)
+{
+    return attention_to(q, k, vt, out, dtype, batch, heads, kv_heads, d, n_q, q_pad, n_k, k_pad, ldo, stride_o, q_pos0,
+                        block, scale, key_hole, MK_BF16, stream);
 }

@@ -82,6 +82,19 @@ struct LnArgs {
 // count 1 or 2 problems of width n (the mk_ln_modulate arguments each); one launch when n is 2048, 3072 or 4096
 mk_status ln_modulate_group(const LnArgs* a, int count, uint32_t n, float eps, void* stream);
 
+// mk_layer_norm / mk_group_norm with the output in y_dtype (MK_BF16, or MK_F16: the input of a GEMM over half
+// weights), and fp32 -> IEEE half (nearest even) (kernels.hip)
+mk_status layer_norm_to(const float* x, uint32_t rows, uint32_t n, const float* g, const float* b, float eps, void* y,
+                        uint32_t y_dtype, void* stream);
+mk_status group_norm_to(const float* x, uint32_t batch, uint32_t rows, uint32_t c, uint32_t groups, const float* g,
+                        const float* b, float eps, void* y, uint32_t y_dtype, void* stream);
+mk_status f32_to_f16(const float* x, size_t n, void* y, void* stream);
+// mk_attention with the output in out_dtype (MK_BF16, or MK_F16: the input of a GEMM over half weights) (attention.hip)
+mk_status attention_to(const void* q, const void* k, const void* vt, void* out, uint32_t dtype, uint32_t batch,
+                       uint32_t heads, uint32_t kv_heads, uint32_t d, uint32_t n_q, uint32_t q_pad, uint32_t n_k,
+                       uint32_t k_pad, int64_t ldo, int64_t stride_o, uint32_t q_pos0, uint32_t block, float scale,
+                       const uint32_t* key_hole, uint32_t out_dtype, void* stream);
+
 // Zero `bytes` (a multiple of 4, 4-byte aligned) of device memory on a stream with a kernel (kernels.hip): a fill node
 // a caller's graph capture can replay, unlike a memset node.
 mk_status fill_zero(void* p, size_t bytes, void* stream);

@@ -202,7 +202,7 @@ struct mk_engine {
         weight_bytes += bytes;
         return MK_OK;
     }
-    static size_t esize(uint32_t dt) { return dt == MK_F32 ? 4 : dt == MK_BF16 ? 2 : 1; }
+    static size_t esize(uint32_t dt) { return dt == MK_F32 ? 4 : (dt == MK_BF16 || dt == MK_F16) ? 2 : 1; }
 
     // A fused linear layer from `parts` checkpoint names stacked along output rows (upload_rows).
     mk_status linear(Linear& L, const std::vector<std::string>& parts, uint32_t rows_each, uint32_t in, bool bias,
@@ -306,10 +306,14 @@ struct mk_engine {
                 MK_TRY(linear(B.ff2[0], {b + "img_mlp.out"}, D, F, false, wdt));
             }
         } else if (cfg.family == MK_FAMILY_SDXL) {
+            // weight_dtype F16: the matrices Sdxl::load_trans reads through Engine::matrix (sdxl.cpp:267-306) are
+            // half, as that keeps an F16 checkpoint's (engine.cpp:292-302); q|k|v and the context's k|v (upload_rows)
+            // stay bf16
+            const uint32_t mdt = wdt == MK_F16 ? MK_F16 : wdt, rdt = wdt == MK_F16 ? MK_BF16 : wdt;
             MK_TRY(vec(&gn_g, "norm.weight", D, 1.0));
             MK_TRY(vec(&gn_b, "norm.bias", D, 0.0));
-            MK_TRY(linear(proj_in, {"proj_in"}, D, D, true));
-            MK_TRY(linear(proj_out, {"proj_out"}, D, D, true));
+            MK_TRY(linear(proj_in, {"proj_in"}, D, D, true, wdt == MK_F16 ? MK_F16 : MK_BF16));
+            MK_TRY(linear(proj_out, {"proj_out"}, D, D, true, wdt == MK_F16 ? MK_F16 : MK_BF16));
             for (uint32_t i = 0; i < cfg.blocks; ++i) {
                 const std::string b = "transformer_blocks." + std::to_string(i) + ".";
                 Block& B = blocks[i];
@@ -319,13 +323,13 @@ struct mk_engine {
                 MK_TRY(vec(&B.n2b, b + "norm2.bias", D, 0.0));
                 MK_TRY(vec(&B.n3g, b + "norm3.weight", D, 1.0));
                 MK_TRY(vec(&B.n3b, b + "norm3.bias", D, 0.0));
-                MK_TRY(linear(B.qkv[0], {b + "attn1.to_q", b + "attn1.to_k", b + "attn1.to_v"}, D, D, false, wdt));
-                MK_TRY(linear(B.o[0], {b + "attn1.to_out.0"}, D, D, true, wdt));
-                MK_TRY(linear(B.q2, {b + "attn2.to_q"}, D, D, false, wdt));
-                MK_TRY(linear(B.kv2, {b + "attn2.to_k", b + "attn2.to_v"}, D, E, false, wdt));
-                MK_TRY(linear(B.o[1], {b + "attn2.to_out.0"}, D, D, true, wdt));
-                MK_TRY(linear(B.ff1[0], {b + "ff.net.0.proj"}, 2 * F, D, true, wdt));
-                MK_TRY(linear(B.ff2[0], {b + "ff.net.2"}, D, F, true, wdt));
+                MK_TRY(linear(B.qkv[0], {b + "attn1.to_q", b + "attn1.to_k", b + "attn1.to_v"}, D, D, false, rdt));
+                MK_TRY(linear(B.o[0], {b + "attn1.to_out.0"}, D, D, true, mdt));
+                MK_TRY(linear(B.q2, {b + "attn2.to_q"}, D, D, false, mdt));
+                MK_TRY(linear(B.kv2, {b + "attn2.to_k", b + "attn2.to_v"}, D, E, false, rdt));
+                MK_TRY(linear(B.o[1], {b + "attn2.to_out.0"}, D, D, true, mdt));
+                MK_TRY(linear(B.ff1[0], {b + "ff.net.0.proj"}, 2 * F, D, true, mdt));
+                MK_TRY(linear(B.ff2[0], {b + "ff.net.2"}, D, F, true, mdt));
             }
         } else {
             return fail(MK_ERR_ARG, "engine: unknown family");
@@ -890,42 +894,56 @@ struct mk_engine {
         ha.k_scale = 0.18033688011112042f;
         float* hs = x_img.f();
         const int64_t nc = int64_t(n) * c;
-        MK_TRY(timed("norm", 0, [&] { return mk_group_norm(x, nb, n, c, 32, gn_g, gn_b, 1e-6f, xn_img.p, stream); }));
+        // the type of a GEMM's input: half for a half matrix (both matrix-core operands take one type), else bf16;
+        // the norms, the attention and the GEGLU epilogue write their outputs in the type of the GEMM they feed
+        auto in_dt = [](const Linear& L) { return L.dtype == MK_F16 ? uint32_t(MK_F16) : uint32_t(MK_BF16); };
+        MK_TRY(timed("norm", 0, [&] {
+            return group_norm_to(x, nb, n, c, 32, gn_g, gn_b, 1e-6f, xn_img.p, in_dt(proj_in), stream);
+        }));
         MK_TRY(gemm(proj_in, xn_img.p, c, 0, nb * n, 1, hs, c, 0, MK_EPI_STORE, MK_F32));
         const float scale = 0.125f;
         for (uint32_t i = 0; i < cfg.blocks; ++i) {
             const Block& B = blocks[i];
-            MK_TRY(timed("norm", 0, [&] { return mk_layer_norm(hs, nb * n, c, B.n1g, B.n1b, 1e-5f, xn_img.p, stream); }));
+            MK_TRY(timed("norm", 0, [&] {
+                return layer_norm_to(hs, nb * n, c, B.n1g, B.n1b, 1e-5f, xn_img.p, in_dt(B.qkv[0]), stream);
+            }));
             MK_TRY(gemm(B.qkv[0], xn_img.p, c, nc, n, nb, nullptr, 0, 0, MK_EPI_HEADS, MK_BF16, nullptr, 0, 0, 0, &ha,
                         "gemm.qkv"));
             MK_TRY(timed("attention", 4.0 * double(n) * n * 64 * H * nb, [&] {
-                return mk_attention(q.p, k.p, vt.p, att.p, MK_F16, nb, H, H, 64, n, q_pad, n, k_pad, c, nc, 0, 0, 0.0f,
-                                    nullptr, stream);
+                return attention_to(q.p, k.p, vt.p, att.p, MK_F16, nb, H, H, 64, n, q_pad, n, k_pad, c, nc, 0, 0, 0.0f,
+                                    nullptr, in_dt(B.o[0]), stream);
             }));
             MK_TRY(gemm(B.o[0], att.p, c, 0, nb * n, 1, hs, c, 0, MK_EPI_ADD, MK_F32, nullptr, 0, 0, 0, nullptr,
                         "gemm.o"));
-            MK_TRY(timed("norm", 0, [&] { return mk_layer_norm(hs, nb * n, c, B.n2g, B.n2b, 1e-5f, xn_img.p, stream); }));
+            MK_TRY(timed("norm", 0, [&] {
+                return layer_norm_to(hs, nb * n, c, B.n2g, B.n2b, 1e-5f, xn_img.p, in_dt(B.q2), stream);
+            }));
             MK_TRY(gemm(B.q2, xn_img.p, c, nc, n, nb, nullptr, 0, 0, MK_EPI_HEADS, MK_BF16, nullptr, 0, 0, 0, &hq,
                         "gemm.q2"));
             // cross attention: batch b reads slot b's context keys (consecutive in the cache)
             const uint16_t* kc = slots[0].ck.h() + size_t(i) * 2 * H * s_pad * 64;
             const uint16_t* vc = slots[0].cvt.h() + size_t(i) * 2 * H * 64 * s_pad;
             MK_TRY(timed("attention", 4.0 * double(n) * S * 64 * H * nb, [&] {
-                return mk_attention(q.p, kc, vc, att.p, MK_F16, nb, H, H, 64, n, q_pad, S, s_pad, c, nc, 0, 0, scale, nullptr,
-                                    stream);
+                return attention_to(q.p, kc, vc, att.p, MK_F16, nb, H, H, 64, n, q_pad, S, s_pad, c, nc, 0, 0, scale,
+                                    nullptr, in_dt(B.o[1]), stream);
             }));
             MK_TRY(gemm(B.o[1], att.p, c, 0, nb * n, 1, hs, c, 0, MK_EPI_ADD, MK_F32, nullptr, 0, 0, 0, nullptr,
                         "gemm.o2"));
-            MK_TRY(timed("norm", 0, [&] { return mk_layer_norm(hs, nb * n, c, B.n3g, B.n3b, 1e-5f, xn_img.p, stream); }));
+            MK_TRY(timed("norm", 0, [&] {
+                return layer_norm_to(hs, nb * n, c, B.n3g, B.n3b, 1e-5f, xn_img.p, in_dt(B.ff1[0]), stream);
+            }));
             // ff.net.0 -> geglu_rows fused into the GEMM's epilogue
-            MK_TRY(gemm(B.ff1[0], xn_img.p, c, 0, nb * n, 1, hid.p, F, 0, MK_EPI_GEGLU, MK_BF16, nullptr, 0, 0, 0,
-                        nullptr, "gemm.ff1"));
+            MK_TRY(gemm(B.ff1[0], xn_img.p, c, 0, nb * n, 1, hid.p, F, 0, MK_EPI_GEGLU, in_dt(B.ff2[0]), nullptr, 0, 0,
+                        0, nullptr, "gemm.ff1"));
             MK_TRY(gemm(B.ff2[0], hid.p, F, 0, nb * n, 1, hs, c, 0, MK_EPI_ADD, MK_F32, nullptr, 0, 0, 0, nullptr,
                         "gemm.ff2"));
         }
         // proj_out + bias + the transformer's input
         MK_HIP(hipMemcpyAsync(y, x, size_t(nb) * nc * 4, hipMemcpyDeviceToDevice, stream));
-        MK_TRY(timed("convert", 0, [&] { return mk_f32_to_bf16(hs, size_t(nb) * nc, xn_img.p, stream); }));
+        MK_TRY(timed("convert", 0, [&] {
+            return in_dt(proj_out) == MK_F16 ? f32_to_f16(hs, size_t(nb) * nc, xn_img.p, stream)
+                                             : mk_f32_to_bf16(hs, size_t(nb) * nc, xn_img.p, stream);
+        }));
         MK_TRY(gemm(proj_out, xn_img.p, c, 0, nb * n, 1, y, c, 0, MK_EPI_ADD, MK_F32));
         return MK_OK;
     }
@@ -979,8 +997,9 @@ mk_status mk_engine_create(const mk_config* cfg, mk_engine** out)
         c.text_dim > 4096)
         return fail(MK_ERR_ARG, "engine_create: dim a multiple of 256 (SDXL: 64) up to 4096, ffn and text_dim "
                                 "multiples of 64");
-    if (c.weight_dtype != MK_BF16 && c.weight_dtype != MK_FP8_E4M3)
-        return fail(MK_ERR_ARG, "engine_create: weights bf16 or fp8-e4m3");
+    if (c.weight_dtype != MK_BF16 && c.weight_dtype != MK_FP8_E4M3 &&
+        !(c.weight_dtype == MK_F16 && c.family == MK_FAMILY_SDXL))
+        return fail(MK_ERR_ARG, "engine_create: weights bf16 or fp8-e4m3 (SDXL: also f16)");
     auto e = std::make_unique<mk_engine>();
     e->cfg = c;
     if (!e->cfg.max_batch)
@@ -1364,7 +1383,7 @@ const char* dtype_label(uint32_t dt)
     return dt == MK_F32 ? "F32" : dt == MK_BF16 ? "BF16" : dt == MK_F16 ? "F16" : dt == MK_FP8_E4M3 ? "F8_E4M3" : "?";
 }
 
-// n values of dtype `from` (F32, BF16 or F16) as `to` (F32 or BF16, nearest even).
+// n values of dtype `from` (F32, BF16 or F16) as `to` (F32, BF16 or F16, nearest even).
 void convert_host(const void* src, uint32_t from, void* dst, uint32_t to, size_t n)
 {
     for (size_t i = 0; i < n; ++i) {
@@ -1374,7 +1393,7 @@ void convert_host(const void* src, uint32_t from, void* dst, uint32_t to, size_t
         if (to == MK_F32)
             static_cast<float*>(dst)[i] = v;
         else
-            static_cast<uint16_t*>(dst)[i] = f2bf_bits(v);
+            static_cast<uint16_t*>(dst)[i] = to == MK_F16 ? f2h_bits(v) : f2bf_bits(v);
     }
 }
 

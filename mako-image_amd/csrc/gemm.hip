@@ -1617,7 +1617,8 @@ mk_status gemm_take_error(const void* stream, bool all)
 // 128 x 128 tiles is 2 per CU and an odd last tile costs half a pair; ties keep the larger tile. Convolutions also
 // have 256 x 192 tiles (8 waves, 0.78), for their 192- and 384-channel layers, and 128 x 96 tiles (4 waves on
 // 16 x 16 x 32, two workgroups a CU) for output channels that are an odd multiple of 96. The heads epilogue
-// takes 256 x 256 tiles for 128-dim heads and 128-channel tiles for 64-dim heads; fp8 weights 256-token tiles.
+// takes 256 x 256 tiles for 128-dim heads and 128-channel tiles for 64-dim heads; fp8 weights 256-token tiles, and so
+// do half-weight convolutions.
 // 256 x 256 tiles use stream-K when whole waves leave at least 5% of the last wave's workgroups idle and
 // a tile is long (K of 6144 or more; measured, the partials' exchange costs about 24 k steps of a tile, more than the
 // balance saves on shorter tiles): the whole waves go round robin, the rest is split by k steps (at least 4 a
@@ -1630,7 +1631,8 @@ GemmPlan gemm_plan(const mk_gemm_args* a, uint32_t n, uint32_t cus, bool conv)
     const bool narrow_ok = a[0].epilogue != MK_EPI_GELU_TANH && a[0].epilogue != MK_EPI_SILU &&
                            a[0].epilogue != MK_EPI_SWIGLU && a[0].epilogue != MK_EPI_GEGLU &&
                            a[0].epilogue != MK_EPI_PAIR_SUM; // 64-wide tiles
-    const bool short_ok = !heads && a[0].w_dtype == MK_BF16; // 128-token tiles
+    // 128-token tiles: bf16 or half weights (convolutions: bf16 only, as their plans were measured)
+    const bool short_ok = !heads && (conv ? a[0].w_dtype == MK_BF16 : a[0].w_dtype != MK_FP8_E4M3);
     auto tiles_of = [&](int bm, int bn) {
         uint64_t t = 0;
         for (uint32_t i = 0; i < n; ++i)
@@ -1662,7 +1664,7 @@ GemmPlan gemm_plan(const mk_gemm_args* a, uint32_t n, uint32_t cus, bool conv)
         // the 64-dim heads epilogue on 256-token tiles: 0.8 (measured on the SDXL shapes, 2048-8192 tokens x 1280 or
         // 640 channels: 256 x 128 tiles took 10-25% longer than pairs of 128 x 128 at the 0.66 estimate's ties)
         consider(256, 128, 0.8);
-        if (a[0].w_dtype == MK_BF16)
+        if (a[0].w_dtype != MK_FP8_E4M3)
             consider(128, 128, 0.67);
         return best;
     }
@@ -1729,19 +1731,21 @@ extern "C" mk_status mk_gemm_grouped(const mk_gemm_args* a, uint32_t count, void
     hipStream_t s = static_cast<hipStream_t>(stream);
     mk_status e;
     if (a[0].w_dtype == MK_F16) {
-        // half operands (the VAE's 1 x 1 convolutions and attention products): plain, residual and pair-sum epilogues
-        if (ek != EK_STORE && ek != EK_RMW && !(ek == EK_GLU && a[0].epilogue == MK_EPI_PAIR_SUM))
-            return fail(MK_ERR_UNSUPPORTED, "gemm: f16 operands take the STORE, ADD / GATE and PAIR_SUM epilogues");
+        // half operands (the VAE's 1 x 1 convolutions and attention products; SDXL's F16 matrices): plain, residual,
+        // GLU / pair-sum and heads epilogues
+        if (ek == EK_ACT)
+            return fail(MK_ERR_UNSUPPORTED, "gemm: f16 operands take the STORE, ADD / GATE, GLU, PAIR_SUM and HEADS "
+                                            "epilogues");
         auto f16 = [&](auto ek_c) -> mk_status {
-            constexpr int E = decltype(ek_c)::value | EK_F16;
+            constexpr int K = decltype(ek_c)::value, E = K | EK_F16;
             if (plan.bm == 128)
                 return launch<128, 128, false, E, 4>(p, n, plan, s);
             if (bn == 256)
                 return launch<256, 256, false, E, 8>(p, n, plan, s);
             if (bn == 128)
                 return launch<256, 128, false, E, 4>(p, n, plan, s);
-            if constexpr (decltype(ek_c)::value == EK_GLU)
-                return fail(MK_ERR_UNSUPPORTED, "gemm: a pair sum needs N a multiple of 128");
+            if constexpr (K == EK_GLU || K == EK_HEADS)
+                return fail(MK_ERR_UNSUPPORTED, "gemm: GLU, pair-sum and heads epilogues need N a multiple of 128");
             else
                 return launch<256, 64, false, E, 4>(p, n, plan, s);
         };
@@ -1749,6 +1753,8 @@ extern "C" mk_status mk_gemm_grouped(const mk_gemm_args* a, uint32_t count, void
             return f16(std::integral_constant<int, EK_STORE>{});
         if (ek == EK_RMW)
             return f16(std::integral_constant<int, EK_RMW>{});
+        if (ek == EK_HEADS)
+            return f16(std::integral_constant<int, EK_HEADS>{});
         return f16(std::integral_constant<int, EK_GLU>{});
     }
     // 256-wide tiles: 8 waves (two a SIMD, 64 x 128 wave tiles), so one wave's waits (barrier, loads) leave the
@@ -1757,7 +1763,7 @@ extern "C" mk_status mk_gemm_grouped(const mk_gemm_args* a, uint32_t count, void
     e = f8 ? launch<256, BN, true, EK, BN == 256 ? 8 : 4>(p, n, plan, s)                                           \
            : launch<256, BN, false, EK, BN == 256 ? 8 : 4>(p, n, plan, s)
     if (plan.bm == 128) {
-        // 128 x 128 tiles (bf16 weights; launches of few tiles): two workgroups a CU
+        // 128 x 128 tiles (bf16 weights; launches of few tiles): two workgroups a CU (half weights: above)
         if (ek == EK_STORE)
             e = launch<128, 128, false, EK_STORE, 4>(p, n, plan, s);
         else if (ek == EK_HEADS)

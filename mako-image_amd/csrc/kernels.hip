@@ -130,13 +130,14 @@ __global__ __launch_bounds__(256) void ln_modulate_nv_kernel(LnG g, float eps)
     }
 }
 
-// Layer norm with gamma / beta (sdxl.cpp:425-437), or RMSNorm * (w + w_offset) (rms = 1): bf16 out. One row a wave,
+// Layer norm with gamma / beta (sdxl.cpp:425-437), or RMSNorm * (w + w_offset) (rms = 1): bf16 or half out (f16: the
+// input of a GEMM over half weights). One row a wave,
 // NV float4s a lane (the row's n floats, rounded up to 256): the row, gamma and beta are all requested before the
 // first reduction, so the launch waits on memory once.
 template <bool kRms, int NV>
 __global__ __launch_bounds__(256) void norm_kernel(const float* __restrict__ x, uint32_t rows, uint32_t n,
                                                    const float* __restrict__ g, const float* __restrict__ b,
-                                                   float w_offset, float eps, uint16_t* __restrict__ y)
+                                                   float w_offset, float eps, uint16_t* __restrict__ y, bool f16)
 {
     const uint32_t lane = threadIdx.x & 63, row = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= rows)
@@ -183,7 +184,7 @@ __global__ __launch_bounds__(256) void norm_kernel(const float* __restrict__ x, 
 #pragma unroll
             for (int j = 0; j < 4; ++j)
                 o[j] = kRms ? v[i][j] * inv * (gg[i][j] + w_offset) : (v[i][j] - mean) * inv * gg[i][j] + bb[i][j];
-            yr[c] = u32x2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+            yr[c] = u32x2{pack_x2(o[0], o[1], f16), pack_x2(o[2], o[3], f16)};
         }
     }
 }
@@ -191,13 +192,13 @@ __global__ __launch_bounds__(256) void norm_kernel(const float* __restrict__ x, 
 // norm_kernel with the smallest NV >= nvec (1 .. kMaxVec float4s a lane)
 template <bool kRms, int NV = 1>
 void launch_norm(uint32_t nvec, const float* x, uint32_t rows, uint32_t n, const float* g, const float* b,
-                 float w_offset, float eps, uint16_t* y, hipStream_t stream)
+                 float w_offset, float eps, uint16_t* y, bool f16, hipStream_t stream)
 {
     if constexpr (NV < kMaxVec) {
         if (nvec > uint32_t(NV))
-            return launch_norm<kRms, NV + 1>(nvec, x, rows, n, g, b, w_offset, eps, y, stream);
+            return launch_norm<kRms, NV + 1>(nvec, x, rows, n, g, b, w_offset, eps, y, f16, stream);
     }
-    norm_kernel<kRms, NV><<<cdiv(rows, 4), 256, 0, stream>>>(x, rows, n, g, b, w_offset, eps, y);
+    norm_kernel<kRms, NV><<<cdiv(rows, 4), 256, 0, stream>>>(x, rows, n, g, b, w_offset, eps, y, f16);
 }
 
 // Group norm statistics (sdxl.cpp:425-437), two kernels: 16-row chunks of a sample, one workgroup each, sum x and
@@ -265,14 +266,15 @@ __global__ __launch_bounds__(64) void group_final_kernel(const double2* __restri
 __global__ __launch_bounds__(256) void group_apply_kernel(const float* __restrict__ x, uint32_t rows, uint32_t c,
                                                           uint32_t groups, const float2* __restrict__ stats,
                                                           const float* __restrict__ g, const float* __restrict__ b,
-                                                          uint16_t* __restrict__ y)
+                                                          uint16_t* __restrict__ y, bool f16)
 {
     const uint64_t n = uint64_t(rows) * c;
     const uint32_t bi = blockIdx.y;
     for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < n; i += uint64_t(gridDim.x) * 256) {
         const uint32_t ch = uint32_t(i % c);
         const float2 st = stats[bi * groups + ch / (c / groups)];
-        y[uint64_t(bi) * n + i] = f2bf_bits((x[uint64_t(bi) * n + i] - st.x) * st.y * g[ch] + b[ch]);
+        const float v = (x[uint64_t(bi) * n + i] - st.x) * st.y * g[ch] + b[ch];
+        y[uint64_t(bi) * n + i] = f16 ? f2h_bits(v) : f2bf_bits(v);
     }
 }
 
@@ -596,7 +598,7 @@ __global__ __launch_bounds__(256) void fill_normal_kernel(void* __restrict__ p, 
         if (dtype == MK_F32)
             static_cast<float*>(p)[i] = v;
         else
-            static_cast<uint16_t*>(p)[i] = f2bf_bits(v);
+            static_cast<uint16_t*>(p)[i] = dtype == MK_F16 ? f2h_bits(v) : f2bf_bits(v);
     }
 }
 
@@ -604,6 +606,11 @@ __global__ __launch_bounds__(256) void f2bf_kernel(const float* __restrict__ x, 
 {
     for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < n; i += uint64_t(gridDim.x) * 256)
         y[i] = f2bf_bits(x[i]);
+}
+__global__ __launch_bounds__(256) void f2h_kernel(const float* __restrict__ x, uint64_t n, uint16_t* __restrict__ y)
+{
+    for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < n; i += uint64_t(gridDim.x) * 256)
+        y[i] = f2h_bits(x[i]);
 }
 __global__ __launch_bounds__(256) void bf2f_kernel(const uint16_t* __restrict__ x, uint64_t n, float* __restrict__ y)
 {
@@ -672,11 +679,11 @@ __device__ inline float e4m3_decode(uint8_t v)
     return v & 0x80 ? -a : a;
 }
 
-// LoRA merge into bf16 rows: RB rows a block share each A value they load; B's RB rows sit in LDS.
+// LoRA merge into bf16 (or half: f16) rows: RB rows a block share each A value they load; B's RB rows sit in LDS.
 template <int RB>
 __global__ __launch_bounds__(256) void lora_bf16_kernel(uint16_t* __restrict__ w, uint64_t rows, uint64_t cols,
                                                         const float* __restrict__ a, const float* __restrict__ b,
-                                                        uint32_t rank, float factor)
+                                                        uint32_t rank, float factor, bool f16)
 {
     extern __shared__ float bs[]; // [RB][rank]
     const uint64_t r0 = uint64_t(blockIdx.x) * RB;
@@ -699,7 +706,7 @@ __global__ __launch_bounds__(256) void lora_bf16_kernel(uint16_t* __restrict__ w
     for (int t = 0; t < RB; ++t)
         if (r0 + t < rows) {
             uint16_t* x = w + (r0 + t) * cols + c;
-            *x = f2bf_bits(bf2f_bits(*x) + factor * acc[t]);
+            *x = f16 ? f2h_bits(h2f_bits(*x) + factor * acc[t]) : f2bf_bits(bf2f_bits(*x) + factor * acc[t]);
         }
 }
 
@@ -854,7 +861,8 @@ mk_status mk_rms_norm(const float* x, uint32_t rows, uint32_t n, const float* w,
         return fail(MK_ERR_ARG, "rms_norm: null pointer, or n not a multiple of 4 up to 4096");
     if (!rows)
         return MK_OK;
-    launch_norm<true>(cdiv(n / 4, 64), x, rows, n, w, nullptr, w_offset, eps, static_cast<uint16_t*>(y), S(stream));
+    launch_norm<true>(cdiv(n / 4, 64), x, rows, n, w, nullptr, w_offset, eps, static_cast<uint16_t*>(y), false,
+                      S(stream));
     MK_LAUNCH_CHECK("rms_norm");
     return MK_OK;
 }
@@ -862,13 +870,7 @@ mk_status mk_rms_norm(const float* x, uint32_t rows, uint32_t n, const float* w,
 mk_status mk_layer_norm(const float* x, uint32_t rows, uint32_t n, const float* g, const float* b, float eps, void* y,
                         void* stream)
 {
-    if (!x || !g || !b || !y || n % 4 || n > 4u * 64 * kMaxVec)
-        return fail(MK_ERR_ARG, "layer_norm: null pointer, or n not a multiple of 4 up to 4096");
-    if (!rows)
-        return MK_OK;
-    launch_norm<false>(cdiv(n / 4, 64), x, rows, n, g, b, 0.0f, eps, static_cast<uint16_t*>(y), S(stream));
-    MK_LAUNCH_CHECK("layer_norm");
-    return MK_OK;
+    return mk::layer_norm_to(x, rows, n, g, b, eps, y, MK_BF16, stream);
 }
 
 // Both group norm entry points: arguments checked, then the three kernels over the scratch `ws` (the per-chunk
@@ -891,7 +893,8 @@ static size_t group_norm_scratch(uint32_t batch, uint32_t rows, uint32_t groups)
     return group_norm_part_bytes(batch, rows, groups) + sizeof(float2) * batch * groups;
 }
 static mk_status group_norm_run(const float* x, uint32_t batch, uint32_t rows, uint32_t c, uint32_t groups,
-                                const float* g, const float* b, float eps, void* y, char* ws, hipStream_t s)
+                                const float* g, const float* b, float eps, void* y, char* ws, hipStream_t s,
+                                bool f16 = false)
 {
     const uint32_t chunks = cdiv(rows, kGnRows);
     double2* part = reinterpret_cast<double2*>(ws);
@@ -900,7 +903,7 @@ static mk_status group_norm_run(const float* x, uint32_t batch, uint32_t rows, u
     group_final_kernel<<<dim3(groups, batch), 64, 0, s>>>(part, chunks, groups, double(rows) * double(c / groups), eps,
                                                           stats);
     group_apply_kernel<<<dim3(std::min<uint32_t>(cdiv(uint64_t(rows) * c, 256), 4096), batch), 256, 0, s>>>(
-        x, rows, c, groups, stats, g, b, static_cast<uint16_t*>(y));
+        x, rows, c, groups, stats, g, b, static_cast<uint16_t*>(y), f16);
     MK_LAUNCH_CHECK("group_norm");
     return MK_OK;
 }
@@ -920,7 +923,17 @@ static std::vector<GnScratch> g_gn;
 mk_status mk_group_norm(const float* x, uint32_t batch, uint32_t rows, uint32_t c, uint32_t groups, const float* g,
                         const float* b, float eps, void* y, void* stream)
 {
+    return mk::group_norm_to(x, batch, rows, c, groups, g, b, eps, y, MK_BF16, stream);
+}
+} // extern "C"
+
+namespace mk {
+mk_status group_norm_to(const float* x, uint32_t batch, uint32_t rows, uint32_t c, uint32_t groups, const float* g,
+                        const float* b, float eps, void* y, uint32_t y_dtype, void* stream)
+{
     MK_TRY(group_norm_check(x, batch, c, groups, g, b, y));
+    if (y_dtype != MK_BF16 && y_dtype != MK_F16)
+        return fail(MK_ERR_ARG, "group_norm: output bf16 or f16");
     if (!rows)
         return MK_OK;
     int dev = 0;
@@ -949,10 +962,37 @@ mk_status mk_group_norm(const float* x, uint32_t batch, uint32_t rows, uint32_t 
         MK_HIP(hipMallocAsync(reinterpret_cast<void**>(&w->p), bytes, s));
         w->bytes = bytes;
     }
-    const mk_status st = group_norm_run(x, batch, rows, c, groups, g, b, eps, y, w->p, s);
+    const mk_status st = group_norm_run(x, batch, rows, c, groups, g, b, eps, y, w->p, s, y_dtype == MK_F16);
     MK_HIP(hipEventRecord(w->last, s));
     return st;
 }
+
+mk_status layer_norm_to(const float* x, uint32_t rows, uint32_t n, const float* g, const float* b, float eps, void* y,
+                        uint32_t y_dtype, void* stream)
+{
+    if (!x || !g || !b || !y || n % 4 || n > 4u * 64 * kMaxVec || (y_dtype != MK_BF16 && y_dtype != MK_F16))
+        return fail(MK_ERR_ARG, "layer_norm: null pointer, n not a multiple of 4 up to 4096, or output not bf16 / f16");
+    if (!rows)
+        return MK_OK;
+    launch_norm<false>(cdiv(n / 4, 64), x, rows, n, g, b, 0.0f, eps, static_cast<uint16_t*>(y), y_dtype == MK_F16,
+                       S(stream));
+    MK_LAUNCH_CHECK("layer_norm");
+    return MK_OK;
+}
+
+mk_status f32_to_f16(const float* x, size_t n, void* y, void* stream)
+{
+    if (!x || !y)
+        return fail(MK_ERR_ARG, "f32_to_f16: null pointer");
+    if (!n)
+        return MK_OK;
+    f2h_kernel<<<grid_for(n), 256, 0, S(stream)>>>(x, n, static_cast<uint16_t*>(y));
+    MK_LAUNCH_CHECK("f32_to_f16");
+    return MK_OK;
+}
+} // namespace mk
+
+extern "C" {
 
 mk_status mk_group_norm_noalloc(const float* x, uint32_t batch, uint32_t rows, uint32_t c, uint32_t groups,
                                 const float* g, const float* b, float eps, void* y, void* stream)
@@ -1146,8 +1186,8 @@ mk_status mk_unpatchify(const float* tokens, uint32_t batch, uint32_t C, uint32_
 
 mk_status mk_fill_normal(void* p, size_t n, uint32_t dtype, uint64_t key, double mean, double std, void* stream)
 {
-    if (!p || (dtype != MK_F32 && dtype != MK_BF16))
-        return fail(MK_ERR_ARG, "fill_normal: null pointer or dtype not f32 / bf16");
+    if (!p || (dtype != MK_F32 && dtype != MK_BF16 && dtype != MK_F16))
+        return fail(MK_ERR_ARG, "fill_normal: null pointer or dtype not f32 / bf16 / f16");
     fill_normal_kernel<<<grid_for(n), 256, 0, S(stream)>>>(p, n, dtype, key, mean, std);
     MK_LAUNCH_CHECK("fill_normal");
     return MK_OK;
@@ -1170,19 +1210,19 @@ mk_status mk_lora_merge(void* w, uint32_t w_dtype, float* w_scale, uint64_t rows
 {
     if (!w || !a || !b || (w_dtype == MK_FP8_E4M3 && !w_scale))
         return fail(MK_ERR_ARG, "lora_merge: null pointer");
-    if (w_dtype != MK_BF16 && w_dtype != MK_FP8_E4M3)
-        return fail(MK_ERR_ARG, "lora_merge: weights bf16 or fp8-e4m3");
+    if (w_dtype != MK_BF16 && w_dtype != MK_F16 && w_dtype != MK_FP8_E4M3)
+        return fail(MK_ERR_ARG, "lora_merge: weights bf16, f16 or fp8-e4m3");
     if (!rank || rank > 1024)
         return fail(MK_ERR_ARG, "lora_merge: rank " + std::to_string(rank) + " not in 1..1024");
     if (!rows || !cols)
         return MK_OK;
-    if (w_dtype == MK_BF16) {
+    if (w_dtype != MK_FP8_E4M3) {
         constexpr int RB = 8;
         const uint64_t gx = (rows + RB - 1) / RB, gy = (cols + 255) / 256;
         if (gx > 0x7fffffffu || gy > 65535)
             return fail(MK_ERR_ARG, "lora_merge: matrix too large");
         lora_bf16_kernel<RB><<<dim3(uint32_t(gx), uint32_t(gy)), 256, RB * rank * 4, S(stream)>>>(
-            static_cast<uint16_t*>(w), rows, cols, a, b, rank, factor);
+            static_cast<uint16_t*>(w), rows, cols, a, b, rank, factor, w_dtype == MK_F16);
     } else {
         if (rows > 0x7fffffffu)
             return fail(MK_ERR_ARG, "lora_merge: too many rows");

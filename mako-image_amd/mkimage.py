@@ -192,7 +192,7 @@ def call(name, *args):
 # device memory
 # ---------------------------------------------------------------------------------------------------------------
 
-_NP = {F32: np.float32, BF16: np.uint16, FP8: np.uint8}
+_NP = {F32: np.float32, BF16: np.uint16, FP8: np.uint8, F16: np.uint16}
 
 
 # Device memory of dropped Dev objects: freed only after a device-wide synchronisation, so a pointer taken from a
@@ -618,7 +618,8 @@ class Engine:
         return out
 
     def fetch(self, name, dtype, rows, cols):
-        """A weight as stored (float32, bf16 bits as uint16, e4m3 codes as uint8); name + ".scale": fp32 scales."""
+        """A weight as stored (float32, bf16 or half bits as uint16, e4m3 codes as uint8); name + ".scale": fp32
+        scales."""
         if name.endswith(".scale"):
             a = np.empty(rows, dtype=np.float32)
         else:
@@ -720,13 +721,15 @@ def rope_table(S, h, w):
 
 def upload_model(engine, tensors):
     """Upload (name, float32 array, kind) triples (kind 0 vector, 1 bf16 matrix, 2 fp8 matrix whose values are exact
-    e4m3 and whose scale is the tensor name + '.scale')."""
+    e4m3 and whose scale is the tensor name + '.scale', 3 half matrix)."""
     table = None
     for name, a, kind in tensors:
         if kind == 0:
             engine.load(name, a, F32)
         elif kind == 1:
             engine.load(name, bf16_bits(a), BF16)
+        elif kind == 3:
+            engine.load(name, f16_bits(a), F16)
         else:
             if table is None:
                 table = _e4m3_table()

@@ -114,13 +114,14 @@ inline double normal_at(uint64_t key, uint64_t i)
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// GEMM: C = bf16(A) W^T (* scale) + bias, blocked for the cache, OpenMP over 64x64 tiles.
+// GEMM: C = r(A) W^T (* scale) + bias with r = bf16 rounding (half rounding for half weights), blocked for the
+// cache, OpenMP over 64x64 tiles.
 // ---------------------------------------------------------------------------------------------------------------
 
 typedef float v8 __attribute__((vector_size(32)));
 
 void gemm(const float* A, int64_t lda, int64_t M, int64_t K, const float* W, int64_t N, const float* wscale,
-          const float* bias, float* C, int64_t ldc)
+          const float* bias, float* C, int64_t ldc, bool half_a = false)
 {
     if (M <= 0 || N <= 0)
         return;
@@ -136,13 +137,14 @@ void gemm(const float* A, int64_t lda, int64_t M, int64_t K, const float* W, int
             for (int64_t k = 0; k < K; ++k)
                 Wp[(size_t(s) * K + k) * 16 + c] = W[size_t(n) * K + k];
         }
-    // A rounded to bf16 (the GEMM's activation operand), rows padded to a multiple of 4.
+    // A rounded to bf16 (the GEMM's activation operand; half for half weights: the matrix-core operands share a
+    // type), rows padded to a multiple of 4.
     const int64_t Mp = (M + 3) / 4 * 4;
     std::vector<float> Ap(size_t(Mp) * K, 0.0f);
 #pragma omp parallel for schedule(static)
     for (int64_t m = 0; m < M; ++m)
         for (int64_t k = 0; k < K; ++k)
-            Ap[size_t(m) * K + k] = bf16(A[size_t(m) * lda + k]);
+            Ap[size_t(m) * K + k] = half_a ? f16(A[size_t(m) * lda + k]) : bf16(A[size_t(m) * lda + k]);
     const int64_t TM = 64, TS = 4, KC = 512; // 64 rows x 4 strips (64 columns) per task, K in chunks
     const int64_t mt = (Mp + TM - 1) / TM, st = (NS + TS - 1) / TS;
 #pragma omp parallel for collapse(2) schedule(dynamic)
@@ -561,7 +563,7 @@ struct mkref_model {
         std::string name;
         std::vector<float> v;
         int64_t rows, cols;
-        int kind; // 0 vector, 1 bf16 matrix, 2 fp8 matrix
+        int kind; // 0 vector, 1 bf16 matrix, 2 fp8 matrix, 3 half matrix
     };
     std::vector<T> ts;
     std::map<std::string, size_t> index;
@@ -584,15 +586,20 @@ struct mkref_model {
     void add(const std::string& n, int64_t rows, int64_t cols, int kind, double mean, double std)
     {
         T t{n, std::vector<float>(size_t(rows) * cols), rows, cols, kind};
-        mkref_fill_normal(t.v.data(), t.v.size(), mkref_tensor_key(seed, n.c_str()), mean, std, kind != 0);
+        mkref_fill_normal(t.v.data(), t.v.size(), mkref_tensor_key(seed, n.c_str()), mean, std, kind == 1);
+        if (kind == 3)
+            mkref_round_f16(t.v.data(), t.v.size());
         index[n] = ts.size();
         ts.push_back(std::move(t));
     }
     // A matrix [rows][cols] of N(0, 0.02); in fp8 mode (block linears only) stored e4m3 with a per-row scale
     // max|W_row| / 448.
-    void mat(const std::string& n, int64_t rows, int64_t cols, bool quant = false)
+    // half: a matrix Engine::matrix keeps F16 (SDXL with dims.f16), N(0, wstd) rounded to half, not bf16.
+    void mat(const std::string& n, int64_t rows, int64_t cols, bool quant = false, bool half = false)
     {
-        add(n, rows, cols, 1, 0.0, wstd);
+        add(n, rows, cols, half ? 3 : 1, 0.0, wstd);
+        if (half)
+            return;
         if (quant && dims.fp8) {
             T& t = ts[index[n]];
             t.kind = 2;
@@ -621,7 +628,7 @@ struct mkref_model {
     {
         const T& W = get(n + ".weight");
         const float* sc = W.kind == 2 ? vec(n + ".weight.scale") : nullptr;
-        gemm(x, lda, M, W.cols, W.v.data(), W.rows, sc, has_bias ? opt(n + ".bias") : nullptr, y, ldy);
+        gemm(x, lda, M, W.cols, W.v.data(), W.rows, sc, has_bias ? opt(n + ".bias") : nullptr, y, ldy, W.kind == 3);
     }
     int64_t out_dim(const std::string& n) const { return get(n + ".weight").rows; }
 };
@@ -692,12 +699,16 @@ mkref_model* mkref_model_create(const mkref_dims* d, uint64_t seed, double wstd)
             m->mat(b + "img_mlp.out.weight", D, F, true);
         }
     } else if (d->kind == MKREF_SDXL) {
-        // One spatial transformer (sdxl.cpp:264-310): C channels, GEGLU inner F, context E.
+        // One spatial transformer (sdxl.cpp:264-310): C channels, GEGLU inner F, context E. With dims.f16 the
+        // matrices Sdxl::load_trans reads through Engine::matrix (proj_in, proj_out, to_out, attn2.to_q, ff;
+        // sdxl.cpp:267-306) are half, as that keeps an F16 checkpoint's (engine.cpp:292-302); q|k|v and the
+        // context's k|v go through upload_rows and stay bf16.
+        const bool h = d->f16 != 0;
         m->normw("norm.weight", D);
         m->bias("norm.bias", D);
-        m->mat("proj_in.weight", D, D);
+        m->mat("proj_in.weight", D, D, false, h);
         m->bias("proj_in.bias", D);
-        m->mat("proj_out.weight", D, D);
+        m->mat("proj_out.weight", D, D, false, h);
         m->bias("proj_out.bias", D);
         for (uint32_t i = 0; i < d->blocks; ++i) {
             const std::string b = "transformer_blocks." + std::to_string(i) + ".";
@@ -705,17 +716,18 @@ mkref_model* mkref_model_create(const mkref_dims* d, uint64_t seed, double wstd)
                 m->normw(b + s + ".weight", D);
                 m->bias(b + s + ".bias", D);
             }
-            for (const char* s : {"attn1.to_q", "attn1.to_k", "attn1.to_v", "attn2.to_q"})
+            for (const char* s : {"attn1.to_q", "attn1.to_k", "attn1.to_v"})
                 m->mat(b + s + ".weight", D, D, true);
+            m->mat(b + "attn2.to_q.weight", D, D, true, h);
             m->mat(b + "attn2.to_k.weight", D, E, true);
             m->mat(b + "attn2.to_v.weight", D, E, true);
             for (const char* s : {"attn1.to_out.0", "attn2.to_out.0"}) {
-                m->mat(b + s + ".weight", D, D, true);
+                m->mat(b + s + ".weight", D, D, true, h);
                 m->bias(b + s + ".bias", D);
             }
-            m->mat(b + "ff.net.0.proj.weight", 2 * F, D, true);
+            m->mat(b + "ff.net.0.proj.weight", 2 * F, D, true, h);
             m->bias(b + "ff.net.0.proj.bias", 2 * F);
-            m->mat(b + "ff.net.2.weight", D, F, true);
+            m->mat(b + "ff.net.2.weight", D, F, true, h);
             m->bias(b + "ff.net.2.bias", D);
         }
     } else {

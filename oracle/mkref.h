@@ -5,8 +5,10 @@
  * (mako-image_amd/libmkimage.so) never links, loads or calls it.
  *
  * Arithmetic model (mirrors the reference: bf16 storage, fp32 accumulation, fp32 residual stream):
- *  - matrix weights hold bf16 values (or OCP fp8-e4m3 values with a per-output-channel fp32 scale);
- *  - every GEMM rounds its activation operand to bf16 (round-to-nearest-even), accumulates in fp32;
+ *  - matrix weights hold bf16 values (or OCP fp8-e4m3 values with a per-output-channel fp32 scale; or, for the SDXL
+ *    matrices Engine::matrix keeps F16 when the checkpoint's are, engine.cpp:292-302 and sdxl.cpp:267-306, half);
+ *  - every GEMM rounds its activation operand to bf16 (half for half weights: both matrix-core operands take one
+ *    type) with round-to-nearest-even, accumulates in fp32;
  *  - attention operands Q, K, V are rounded to bf16 in the dual-stream graph, and to IEEE half in the reference's own
  *    graphs (Qwen-Image 2.1 and SDXL, whose heads kernels write `half`: qwen_image.cpp:165-167, 226-250,
  *    sdxl.cpp:439-448), the 2.1 graph's cached text keys / values with them; the softmax is fp32;
@@ -99,14 +101,15 @@ typedef struct mkref_dims {
     uint32_t text_dim;   /* prompt width */
     uint32_t latent;     /* 64 */
     uint32_t fp8;        /* block linears stored fp8-e4m3 with per-row scales */
+    uint32_t f16;        /* SDXL: the matrices Engine::matrix keeps F16 are half, their GEMMs take half inputs */
 } mkref_dims;
 typedef struct mkref_model mkref_model;
 /* weights N(0, wstd) (biases too), norm scales 1 + N(0, wstd); wstd 0.02 is the synthetic checkpoint's */
 mkref_model* mkref_model_create(const mkref_dims* dims, uint64_t seed, double wstd);
 void mkref_model_destroy(mkref_model* m);
 size_t mkref_model_count(const mkref_model* m);
-/* tensor i: its name, its fp32 values (bf16- or e4m3-exact for matrices), rows x cols, and kind
- * (0 fp32 vector, 1 bf16 matrix, 2 fp8 matrix whose scale is the tensor named name + ".scale") */
+/* tensor i: its name, its fp32 values (bf16-, e4m3- or half-exact for matrices), rows x cols, and kind
+ * (0 fp32 vector, 1 bf16 matrix, 2 fp8 matrix whose scale is the tensor named name + ".scale", 3 half matrix) */
 const char* mkref_model_name(const mkref_model* m, size_t i);
 const float* mkref_model_tensor(const mkref_model* m, size_t i, int64_t* rows, int64_t* cols, int* kind);
 int64_t mkref_model_find(const mkref_model* m, const char* name);

@@ -19,7 +19,7 @@ DUAL, Q21, SDXL = 0, 1, 2
 
 class Dims(C.Structure):
     _fields_ = [(n, C.c_uint32) for n in ("kind", "blocks", "dim", "heads", "head_dim", "ffn", "text_dim", "latent",
-                                           "fp8")]
+                                           "fp8", "f16")]
 
 
 PROBE = C.CFUNCTYPE(None, C.c_void_p, C.c_char_p, C.c_int, C.POINTER(C.c_float), C.c_size_t)
@@ -372,8 +372,9 @@ def unpatchify(tokens, C_, h, w):
 class Model:
     """Synthetic weights by name (counter RNG), and the oracle's graphs over them."""
 
-    def __init__(self, kind, blocks, dim, heads, head_dim, ffn, text_dim, latent=64, fp8=False, seed=0, wstd=0.02):
-        self.dims = Dims(kind, blocks, dim, heads, head_dim, ffn, text_dim, latent, int(bool(fp8)))
+    def __init__(self, kind, blocks, dim, heads, head_dim, ffn, text_dim, latent=64, fp8=False, seed=0, wstd=0.02,
+                 f16=False):
+        self.dims = Dims(kind, blocks, dim, heads, head_dim, ffn, text_dim, latent, int(bool(fp8)), int(bool(f16)))
         self.seed = seed
         self.h = lib().mkref_model_create(C.byref(self.dims), seed, wstd)
         if not self.h:

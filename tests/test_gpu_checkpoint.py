@@ -156,6 +156,56 @@ def test_f16_checkpoint_rounds_like_torch(gpu, tmp_path):
                            want.view(torch.int16) if dt == M.BF16 else want), k
 
 
+def test_sdxl_f16_matrices_kept_half(gpu, tmp_path):
+    # an SDXL engine with F16 weights keeps the matrices Engine::matrix keeps F16 (proj_in / proj_out, to_out,
+    # attn2.to_q, ff: engine.cpp:292-302, sdxl.cpp:267-306) as half, q|k|v and the context's k|v as bf16: its random
+    # init is the oracle's half model bit for bit, an F16 checkpoint of it loads back bit for bit, and a bf16 engine
+    # reading the same file rounds the half matrices to bf16 as torch does
+    m = R.Model(R.SDXL, **SDXL, f16=True, seed=13)
+    e = M.Engine(M.FAMILY_SDXL, **SDXL, weight_dtype=M.F16)
+    e.init_random(13)
+    st = state(e)
+    kinds = {}
+    for name, a, kind in m.tensors():
+        got, dt = st[name]
+        kinds[name] = kind
+        if kind == 3:
+            assert dt == M.F16 and np.array_equal(got, M.f16_bits(a)), name
+        elif kind == 1:
+            assert dt == M.BF16 and np.array_equal(got, M.bf16_bits(a)), name
+        else:
+            assert dt == M.F32 and np.array_equal(got, a), name
+    assert sum(k == 3 for k in kinds.values()) == 7 and sum(k == 1 for k in kinds.values()) == 5  # q, k, v; k2, v2
+    ts = {k: torch.from_numpy(a.view(np.float16).copy()) if dt == M.F16 else as_torch(a, dt)
+          for k, (a, dt) in st.items()}
+    save_file(ts, str(tmp_path / "sdxl_f16.safetensors"))
+    e2 = M.Engine(M.FAMILY_SDXL, **SDXL, weight_dtype=M.F16)
+    assert e2.load_safetensors(tmp_path / "sdxl_f16.safetensors") == len(st)
+    same_state(state(e2), st)
+    e3 = M.Engine(M.FAMILY_SDXL, **SDXL)
+    e3.load_safetensors(tmp_path / "sdxl_f16.safetensors")
+    for k, (a, dt) in state(e3).items():
+        if kinds[k] == 3:
+            assert dt == M.BF16
+            assert torch.equal(as_torch(a, dt).view(torch.int16), ts[k].to(torch.bfloat16).view(torch.int16)), k
+    # a LoRA merges into a half matrix within one half unit in the last place of the float64 merge
+    rng = np.random.default_rng(5)
+    D, Fd = SDXL["dim"], SDXL["ffn"]
+    lw = {}
+    a1, b1 = lora_pair(rng, D, Fd, 8)
+    lw["transformer_blocks.0.ff.net.2.lora_A.weight"], lw["transformer_blocks.0.ff.net.2.lora_B.weight"] = a1, b1
+    save_file(lw, str(tmp_path / "lora.safetensors"))
+    before = st["transformer_blocks.0.ff.net.2.weight"][0]
+    assert e.add_lora(tmp_path / "lora.safetensors", 0.7) == (1, 0)
+    after, dt = state(e)["transformer_blocks.0.ff.net.2.weight"]
+    assert dt == M.F16
+    want = M.f16_to_f32(before).astype(np.float64) + 0.7 * (b1.double().numpy() @ a1.double().numpy())
+    got = M.f16_to_f32(after).astype(np.float64)
+    ulp = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(want), 2.0 ** -14))) - 10)
+    assert (np.abs(got - want) <= ulp * 1.0001 + 1e-8).all()
+    assert np.mean(after == M.f16_bits(want.astype(np.float32))) >= 0.99
+
+
 def test_checkpoint_errors(gpu, tmp_path):
     e = M.Engine(M.FAMILY_DUAL, **TINY)
     e.init_random(1)

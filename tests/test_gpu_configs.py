@@ -137,11 +137,12 @@ SDXL_B = dict(blocks=1, dim=1280, heads=20, head_dim=64, ffn=5120, text_dim=2048
 SDXL_A = dict(blocks=1, dim=640, heads=10, head_dim=64, ffn=2560, text_dim=2048)
 
 
+@pytest.mark.parametrize("f16", [False, True])
 @pytest.mark.parametrize("dims,side", [(SDXL_B, 32), (SDXL_A, 64)])
-def test_sdxl_stage_block_matches_oracle(gpu, dims, side):
+def test_sdxl_stage_block_matches_oracle(gpu, dims, side, f16):
     # stage B: 1024 tokens x 1280 channels, 20 heads; stage A at its full 4096 tokens; batch 2 (CFG) with 77-token
-    # contexts of width 2048
-    m, e = make_pair(M.FAMILY_SDXL, dims=dims, wstd=0.05)
+    # contexts of width 2048; f16: the matrices Engine::matrix keeps F16 as half, their GEMMs on half inputs
+    m, e = make_pair(M.FAMILY_SDXL, dims=dims, wstd=0.05, f16=f16)
     rng = np.random.default_rng(43)
     n, S, c = side * side, 77, dims["dim"]
     x = rng.standard_normal((2, n, c)).astype(np.float32)
@@ -153,4 +154,6 @@ def test_sdxl_stage_block_matches_oracle(gpu, dims, side):
     got = yd.to_array(np.float32, x.shape)
     for b in range(2):
         want = m.sdxl_trans(x[b], ctx[b])
-        within(got[b] - x[b], want - x[b], c)
+        # measured: rel 1.5e-3 (stage B) and 7.5e-4 (stage A) with half matrices, 6.2e-3 and 4.2e-3 with bf16 ones
+        d = within(got[b] - x[b], want - x[b], c, max_rel=5e-3 if f16 else 2e-2)
+        print(f"sdxl c={c} f16={f16} sample {b}: {d}", flush=True)

@@ -24,10 +24,10 @@ def within(got, want, width, cos=0.9995, max_rel=2e-2):
     return d
 
 
-def make_pair(family, fp8=False, seed=0, wstd=0.02, dims=TINY):
+def make_pair(family, fp8=False, seed=0, wstd=0.02, dims=TINY, f16=False):
     m = R.Model({M.FAMILY_DUAL: R.DUAL, M.FAMILY_Q21: R.Q21, M.FAMILY_SDXL: R.SDXL}[family], **dims, fp8=fp8,
-                seed=seed, wstd=wstd)
-    e = M.Engine(family, **dims, weight_dtype=M.FP8 if fp8 else M.BF16)
+                seed=seed, wstd=wstd, f16=f16)
+    e = M.Engine(family, **dims, weight_dtype=M.FP8 if fp8 else M.F16 if f16 else M.BF16)
     M.upload_model(e, m.tensors())
     return m, e
 

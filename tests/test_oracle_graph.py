@@ -24,7 +24,9 @@ def hf(x):
 
 class Weights:
     def __init__(self, model):
-        self.t = {n: torch.from_numpy(a).double() for n, a, _ in model.tensors()}
+        self.t, self.kind = {}, {}
+        for n, a, k in model.tensors():
+            self.t[n], self.kind[n] = torch.from_numpy(a).double(), k
 
     def w(self, name):
         W = self.t[name + ".weight"]
@@ -36,7 +38,8 @@ class Weights:
         if self.t.get(name + ".weight.scale") is not None:  # fp8: scale after the product, as stored
             y = F.linear(bf(x), self.t[name + ".weight"]) * self.t[name + ".weight.scale"]
             return y + b if b is not None else y
-        return F.linear(bf(x), self.w(name), b)
+        # a half matrix (kind 3) takes its input in half, the others in bf16
+        return F.linear(hf(x) if self.kind[name + ".weight"] == 3 else bf(x), self.w(name), b)
 
     def __getitem__(self, k):
         return self.t[k]
@@ -224,14 +227,36 @@ def test_q21_step_matches_torch():
     agree(m.q21_step(prompt, lat, h, w, 0.8), q21_reference(m, dims, prompt, lat, h, w, 0.8), 8e-4)
 
 
-def test_sdxl_trans_matches_torch():
-    # agrees to 2.3e-3 with half heads; bf16 heads would be off by 5.8e-3
+@pytest.mark.parametrize("f16", [False, True])
+def test_sdxl_trans_matches_torch(f16):
+    # agrees to 2.3e-3 with half heads; bf16 heads would be off by 5.8e-3. With half matrices: 7.8e-4, and inputs
+    # to them rounded to bf16 instead of half would be off by 4.6e-3
     dims = dict(kind=R.SDXL, blocks=2, dim=128, heads=2, head_dim=64, ffn=256, text_dim=192)
-    m = R.Model(**dims, seed=5, wstd=WSTD)
+    m = R.Model(**dims, seed=5, wstd=WSTD, f16=f16)
     rng = np.random.default_rng(6)
     x = rng.standard_normal((40, 128)).astype(np.float32)
     ctx = rng.standard_normal((11, 192)).astype(np.float32)
-    agree(m.sdxl_trans(x, ctx), sdxl_reference(m, dims, x, ctx))
+    agree(m.sdxl_trans(x, ctx), sdxl_reference(m, dims, x, ctx), 1.5e-3 if f16 else 4e-3)
+
+
+def test_sdxl_half_matrices():
+    # with f16 the matrices Engine::matrix keeps (proj_in / proj_out, to_out, attn2.to_q, ff) hold half values of the
+    # same N(0, wstd) draws, q|k|v and the context's k|v stay bf16; a half matrix's GEMM rounds its input to half
+    dims = dict(kind=R.SDXL, blocks=1, dim=128, heads=2, head_dim=64, ffn=256, text_dim=192)
+    a, b = R.Model(**dims, seed=9, f16=False), R.Model(**dims, seed=9, f16=True)
+    half = {"proj_in.weight", "proj_out.weight", "transformer_blocks.0.attn1.to_out.0.weight",
+            "transformer_blocks.0.attn2.to_q.weight", "transformer_blocks.0.attn2.to_out.0.weight",
+            "transformer_blocks.0.ff.net.0.proj.weight", "transformer_blocks.0.ff.net.2.weight"}
+    kinds = {n: k for n, _, k in b.tensors()}
+    assert {n for n, k in kinds.items() if k == 3} == half
+    for (n, wa, ka), (_, wb, kb) in zip(a.tensors(), b.tensors()):
+        if n in half:
+            assert ka == 1 and kb == 3
+            assert np.array_equal(wb, wb.astype(np.float16).astype(np.float32))  # half-exact
+            assert not np.array_equal(wa, wb)  # not the bf16 values
+            assert np.abs(wa - wb).max() <= 2 ** -8 * np.abs(wb).max()  # the same draws
+        else:
+            assert np.array_equal(wa, wb)
 
 
 # ---- VAE decoder (src/image/engine.cpp:862-954), written in the idiom of the public Wan-2.1 decoder: conv2d with
