@@ -117,6 +117,13 @@ constexpr int EK_CONVQ = 32;
 // Flag on the epilogue kind: the operands are IEEE half (v_mfma_f32_*_f16): the VAE's convolutions and products, whose
 // reference multiplies F16 weights with half activations (docs/performance.md:13, engine.cpp:766-773).
 constexpr int EK_F16 = 64;
+// Flag on the epilogue kind: a launch of at most one tile a CU (each workgroup alone on its CU) on 4-wave 128-channel
+// tiles. The operands go global -> LDS by direct loads through NSTG stages (4 for 128-token tiles, 3 for 256), each
+// k step's loads issued NSTG - 1 steps ahead of its use; the two-workgroup form stages them through registers three
+// substeps ahead, a latency a workgroup alone on its CU cannot hide.
+constexpr int EK_DEEP = 128;
+// s_waitcnt immediate (gfx9 layout): vmcnt vm (0-63: bits 3:0 and 15:14), expcnt not waited for, lgkmcnt lgkm (0-15)
+constexpr int waitcnt_bits(int vm, int lgkm) { return (vm & 15) | ((vm >> 4) << 14) | (7 << 4) | ((lgkm & 15) << 8); }
 typedef _Float16 f16x8v __attribute__((ext_vector_type(8)));
 
 // A pair of 16-bit outputs: IEEE half or bf16, round to nearest even either way.
@@ -679,6 +686,9 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
     static_assert(((EK & 7) != EK_HEADS && (EK & 7) != EK_GLU) || !(EK & EK_CONV),
                   "a convolution has no heads or GLU epilogue");
     constexpr bool kConv = (EK & EK_CONV) != 0, kConvQ = (EK & EK_CONVQ) != 0, kF16 = (EK & EK_F16) != 0;
+    constexpr bool kDeep = (EK & EK_DEEP) != 0;
+    static_assert(!kDeep || (NW == 4 && BN == 128 && !kF8 && !kConv), "deep stages: 4-wave 128-channel tiles");
+    constexpr int NSTG = kDeep ? (BM == 128 ? 4 : 3) : 2; // LDS stages of the operand tiles
     constexpr int EKE = EK & 7;                 // the epilogue kind
     constexpr int NT = 64 * NW;                 // threads
     // waves: 2 along channels x NW/2 along tokens; the 96-channel tiles 1 x NW (a wave holds whole rows)
@@ -697,7 +707,7 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
     constexpr int ND = RA + (kF8 ? 0 : RW);     // direct loads a thread issues per k step
     constexpr int LDW = WC + 4;                 // epilogue staging: a wave's 32 tokens x WC channels, padded rows
     uint16_t(*sW)[BN * 64] = reinterpret_cast<uint16_t(*)[BN * 64]>(smem);
-    uint16_t(*sA)[BM * 64] = reinterpret_cast<uint16_t(*)[BM * 64]>(smem + 2 * BN * 64);
+    uint16_t(*sA)[BM * 64] = reinterpret_cast<uint16_t(*)[BM * 64]>(smem + NSTG * BN * 64);
 
     // the wave index is uniform: readfirstlane keeps it (and the LDS bases of the direct loads) in scalar registers
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -869,7 +879,7 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
     // direct load would have filled (measured: 6-13% faster than direct loads there on K of 3072-5120; 2-8% slower
     // for the 8-wave 256-wide tiles and 5-15% for 64-channel tiles, which keep the direct loads). fp8 weights: the
     // activation chunks go by direct load, the weight chunks through registers (converted to bf16, commit_f8).
-    constexpr bool kStage = !kF8 && NW == 4 && BN == 128;
+    constexpr bool kStage = !kF8 && NW == 4 && BN == 128 && !kDeep;
     u32x4 stg[kStage ? ND : 1];
     auto gload = [&](int kt, int i) {
         if constexpr (kStage) {
@@ -967,7 +977,17 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
     using CH = std::integral_constant<int, ND / 2>;
     using CN = std::integral_constant<int, ND>;
     bf16x8 wf0[CB], af0[TB], wf1[CB], af1[TB]; // (16 x 16 x 32: wf0 is the single weight buffer)
-    if constexpr (!kStage) {
+    if constexpr (kDeep) {
+        // steps kb .. kb + NSTG - 2 into stages 0 .. NSTG - 2 (past-the-end steps clamped: a reload of the last);
+        // step kb landed (this wave's later loads may stay in flight), then every wave's
+        static_assert(NSTG == 3 || NSTG == 4, "deep stages: 3 or 4");
+        issue(min(kb, ke - 1), 0);
+        issue(min(kb + 1, ke - 1), 1);
+        if constexpr (NSTG == 4)
+            issue(min(kb + 2, ke - 1), 2);
+        __builtin_amdgcn_s_waitcnt(waitcnt_bits((NSTG - 2) * ND, 0));
+        __builtin_amdgcn_s_barrier();
+    } else if constexpr (!kStage) {
         // Software pipeline over k steps of four 16-wide substeps: step t is in LDS buffer t & 1; step t + 1 lands
         // in the other buffer during step t (the first half of its direct loads goes out with the last substep of
         // step t - 1, right after the barrier frees the buffer, the second half with the first substep of step t);
@@ -1029,6 +1049,19 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
             __syncthreads();
             load_f8(min(kt + 2, ke - 1));
             group16(wf0, af1, buf ^ 1, 0, af0, min(kt + 2, ke - 1), buf, C0{}, CN{});
+        } else if constexpr (kDeep) {
+            // step kt in stage buf; its first three substeps issue step kt + NSTG - 1 into the stage step kt - 1
+            // left (freed by the previous barrier); then step kt + 1 landed (this wave's loads of the steps after it
+            // may stay in flight), the barrier (every wave's loads of it visible, every wave done reading stage buf),
+            // and the last substep reads step kt + 1's first fragments
+            constexpr int lb = (buf + NSTG - 1) % NSTG, nb = (buf + 1) % NSTG;
+            const int kl = min(kt + NSTG - 1, ke - 1);
+            group(wf0, af0, buf, 1, wf1, af1, kl, lb, C0{}, CH{}, 0, C0{}, C0{});
+            group(wf1, af1, buf, 2, wf0, af0, kl, lb, CH{}, CN{}, 0, C0{}, C0{});
+            group(wf0, af0, buf, 3, wf1, af1, 0, 0, C0{}, C0{}, 0, C0{}, C0{});
+            __builtin_amdgcn_s_waitcnt(waitcnt_bits((NSTG - 2) * ND, 0));
+            __builtin_amdgcn_s_barrier();
+            group(wf1, af1, nb, 0, wf0, af0, 0, 0, C0{}, C0{}, 0, C0{}, C0{});
         } else if constexpr (!kStage) {
             group(wf0, af0, buf, 1, wf1, af1, min(kt + 1, ke - 1), buf ^ 1, CH{}, CN{}, 0, C0{}, C0{});
             group(wf1, af1, buf, 2, wf0, af0, 0, 0, C0{}, C0{}, 0, C0{}, C0{});
@@ -1051,12 +1084,30 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
         }
     };
     int kt = kb;
-    for (; kt + 1 < ke; kt += 2) {
-        step(kt, std::integral_constant<int, 0>{});
-        step(kt + 1, std::integral_constant<int, 1>{});
+    if constexpr (kDeep) {
+        // unrolled by NSTG: step kb + j of each round in stage j (constant LDS offsets)
+        for (; kt + NSTG - 1 < ke; kt += NSTG) {
+            step(kt, std::integral_constant<int, 0>{});
+            step(kt + 1, std::integral_constant<int, 1>{});
+            step(kt + 2, std::integral_constant<int, 2>{});
+            if constexpr (NSTG == 4)
+                step(kt + 3, std::integral_constant<int, 3 % NSTG>{});
+        }
+        if (kt < ke)
+            step(kt, std::integral_constant<int, 0>{});
+        if (kt + 1 < ke)
+            step(kt + 1, std::integral_constant<int, 1>{});
+        if constexpr (NSTG == 4)
+            if (kt + 2 < ke)
+                step(kt + 2, std::integral_constant<int, 2>{});
+    } else {
+        for (; kt + 1 < ke; kt += 2) {
+            step(kt, std::integral_constant<int, 0>{});
+            step(kt + 1, std::integral_constant<int, 1>{});
+        }
+        if (kt < ke)
+            step(kt, std::integral_constant<int, 0>{});
     }
-    if (kt < ke)
-        step(kt, std::integral_constant<int, 0>{});
     __builtin_amdgcn_s_waitcnt(0); // the last (unused) prefetch must land before the LDS is reused
     __syncthreads();
 
@@ -1284,23 +1335,26 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
 }
 
 
-template <int BM, int BN, int NW>
+template <int BM, int BN, int NW, bool DEEP = false>
 constexpr int gemm_smem()
 {
-    constexpr int LDW = BN / 2 + 4;
-    return 2 * (BN + BM) * 64 * 2 > NW * 32 * LDW * 4 ? 2 * (BN + BM) * 64 * 2 : NW * 32 * LDW * 4;
+    constexpr int LDW = BN / 2 + 4, NSTG = DEEP ? (BM == 128 ? 4 : 3) : 2;
+    return NSTG * (BN + BM) * 64 * 2 > NW * 32 * LDW * 4 ? NSTG * (BN + BM) * 64 * 2 : NW * 32 * LDW * 4;
 }
 
 // One tile a workgroup.
 // Waves a SIMD: 8-wave tiles two (one workgroup a CU), 4-wave 128 x 128 tiles two (two workgroups a CU, 64 KB of LDS
-// each), other 4-wave tiles one.
-template <int BM, int NW> constexpr int gemm_waves_per_eu() { return NW == 8 || BM == 128 ? 2 : 1; }
+// each) unless deep-staged (EK_DEEP: one workgroup a CU), other 4-wave tiles one.
+template <int BM, int NW, int EK> constexpr int gemm_waves_per_eu()
+{
+    return NW == 8 || (BM == 128 && !(EK & EK_DEEP)) ? 2 : 1;
+}
 
 template <int BM, int BN, bool kF8, int EK, int NW>
-__global__ __launch_bounds__(64 * NW, BM == 128 ? 2 : 1) __attribute__((
-    amdgpu_waves_per_eu(gemm_waves_per_eu<BM, NW>(), gemm_waves_per_eu<BM, NW>()))) void gemm_kernel(GemmG G)
+__global__ __launch_bounds__(64 * NW, BM == 128 && !(EK & EK_DEEP) ? 2 : 1) __attribute__((
+    amdgpu_waves_per_eu(gemm_waves_per_eu<BM, NW, EK>(), gemm_waves_per_eu<BM, NW, EK>()))) void gemm_kernel(GemmG G)
 {
-    __shared__ __attribute__((aligned(16))) uint16_t smem[gemm_smem<BM, BN, NW>() / 2];
+    __shared__ __attribute__((aligned(16))) uint16_t smem[gemm_smem<BM, BN, NW, (EK & EK_DEEP) != 0>() / 2];
     uint32_t z, tm, tn;
     const GemmP& p = locate(G, xcd_order(blockIdx.x, gridDim.x), z, tm, tn);
     gemm_tile<BM, BN, kF8, EK, NW>(p, z, tm, tn, 0, int(p.K) / BK, smem, nullptr, -1);
@@ -1730,6 +1784,17 @@ extern "C" mk_status mk_gemm_grouped(const mk_gemm_args* a, uint32_t count, void
         return fail(MK_ERR_UNSUPPORTED, "gemm: heads epilogue tile width does not match the head dim");
     hipStream_t s = static_cast<hipStream_t>(stream);
     mk_status e;
+    // 4-wave 128-channel tiles (128 x 128, or 256 x 128 with bn 128) of epilogue kind E: deep-staged (EK_DEEP) when
+    // the launch has at most one tile a CU, so each workgroup runs alone on its CU
+    const bool deep = !f8 && plan.tiles <= uint64_t(cus > 0 ? cus : 1);
+    auto narrow = [&](auto e_c) -> mk_status {
+        constexpr int E = decltype(e_c)::value;
+        if (plan.bm == 128)
+            return deep ? launch<128, 128, false, E | EK_DEEP, 4>(p, n, plan, s)
+                        : launch<128, 128, false, E, 4>(p, n, plan, s);
+        return deep ? launch<256, 128, false, E | EK_DEEP, 4>(p, n, plan, s)
+                    : launch<256, 128, false, E, 4>(p, n, plan, s);
+    };
     if (a[0].w_dtype == MK_F16) {
         // half operands (the VAE's 1 x 1 convolutions and attention products; SDXL's F16 matrices): plain, residual,
         // GLU / pair-sum and heads epilogues
@@ -1738,12 +1803,10 @@ extern "C" mk_status mk_gemm_grouped(const mk_gemm_args* a, uint32_t count, void
                                             "epilogues");
         auto f16 = [&](auto ek_c) -> mk_status {
             constexpr int K = decltype(ek_c)::value, E = K | EK_F16;
-            if (plan.bm == 128)
-                return launch<128, 128, false, E, 4>(p, n, plan, s);
+            if (plan.bm == 128 || bn == 128)
+                return narrow(std::integral_constant<int, E>{});
             if (bn == 256)
                 return launch<256, 256, false, E, 8>(p, n, plan, s);
-            if (bn == 128)
-                return launch<256, 128, false, E, 4>(p, n, plan, s);
             if constexpr (K == EK_GLU || K == EK_HEADS)
                 return fail(MK_ERR_UNSUPPORTED, "gemm: GLU, pair-sum and heads epilogues need N a multiple of 128");
             else
@@ -1762,18 +1825,19 @@ extern "C" mk_status mk_gemm_grouped(const mk_gemm_args* a, uint32_t count, void
 #define MK_GEMM_EK(BN, EK)                                                                                        \
     e = f8 ? launch<256, BN, true, EK, BN == 256 ? 8 : 4>(p, n, plan, s)                                           \
            : launch<256, BN, false, EK, BN == 256 ? 8 : 4>(p, n, plan, s)
-    if (plan.bm == 128) {
-        // 128 x 128 tiles (bf16 weights; launches of few tiles): two workgroups a CU (half weights: above)
+    if (plan.bm == 128 || (bn == 128 && !f8)) {
+        // 128-channel tiles with bf16 weights: 128 x 128 (launches of few tiles: two workgroups a CU, or one
+        // deep-staged) or 256 x 128 (half weights: above)
         if (ek == EK_STORE)
-            e = launch<128, 128, false, EK_STORE, 4>(p, n, plan, s);
+            e = narrow(std::integral_constant<int, EK_STORE>{});
         else if (ek == EK_HEADS)
-            e = launch<128, 128, false, EK_HEADS, 4>(p, n, plan, s);
+            e = narrow(std::integral_constant<int, EK_HEADS>{});
         else if (ek == EK_ACT)
-            e = launch<128, 128, false, EK_ACT, 4>(p, n, plan, s);
+            e = narrow(std::integral_constant<int, EK_ACT>{});
         else if (ek == EK_GLU)
-            e = launch<128, 128, false, EK_GLU, 4>(p, n, plan, s);
+            e = narrow(std::integral_constant<int, EK_GLU>{});
         else
-            e = launch<128, 128, false, EK_RMW, 4>(p, n, plan, s);
+            e = narrow(std::integral_constant<int, EK_RMW>{});
     } else if (ek == EK_HEADS) {
         if (bn == 256)
             MK_GEMM_EK(256, EK_HEADS);
