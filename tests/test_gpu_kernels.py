@@ -818,6 +818,16 @@ def test_norms(gpu, rng, n):
     for bi in range(2):
         want = R.group_norm(xg[bi], gg, b[:640], 32, 1e-6)
         assert np.abs(got[bi] - want).max() <= 2 ** -8 * np.abs(want).max() + 1e-5
+    # channels not a multiple of 4 (the one-channel-a-thread apply), a partial last chunk of rows
+    xs = (rng.standard_normal((2, 37, 90)) * 3 + 1).astype(np.float32)
+    gs, bs = (1 + 0.1 * rng.standard_normal(90)).astype(np.float32), (0.1 * rng.standard_normal(90)).astype(np.float32)
+    ys = M.Dev(2 * 37 * 90 * 2)
+    M.call("mk_group_norm", dev(xs).p, 2, 37, 90, 3, dev(gs).p, dev(bs).p, 1e-6, ys.p, None)
+    M.sync()
+    got = fetch_bf16(ys, (2, 37, 90))
+    for bi in range(2):
+        want = R.group_norm(xs[bi], gs, bs, 3, 1e-6)
+        assert np.abs(got[bi] - want).max() <= 2 ** -8 * np.abs(want).max() + 1e-5
 
 
 def test_glu(gpu, rng):
