@@ -1050,6 +1050,22 @@ def test_attention_masked_key_range(gpu, rng, d, Tq, Tk, holes, scale):
         assert dd["min_cos"] > 0.9999 and dd["max_rel"] < 1e-2, dd
 
 
+# Launches of at most one tile a CU on 128-channel tiles run deep-staged (4 LDS stages for 128 x 128 tiles, 3 for
+# 256 x 128): K of 1 to 20 k steps covers the prologue, whole unrolled rounds and every remainder length.
+@pytest.mark.parametrize("K", [64, 128, 192, 256, 320, 448, 1280])
+@pytest.mark.parametrize("Mr,N", [(256, 256), (8192, 640)])  # 4 tiles of 128 x 128; 160 of 256 x 128
+def test_gemm_deep_staged_lone_tiles(gpu, rng, Mr, N, K):
+    A = rng.standard_normal((Mr, K)).astype(np.float32)
+    W = R.bf16_round(rng.standard_normal((N, K)).astype(np.float32) * 0.05)
+    b = rng.standard_normal(N).astype(np.float32) * 0.3
+    out = dev(np.zeros(Mr * N, np.float32))
+    gemm(bdev(A), bdev(W), bias=dev(b), c=out, c_dtype=M.F32, epi=M.EPI_STORE, M_=(Mr, N, K), lda=K, ldc=N)
+    got = fetch(out, (Mr, N))
+    rows = np.sort(rng.choice(Mr, 96, replace=False))
+    rows[0], rows[-1] = 0, Mr - 1
+    assert maxrel(got[rows], R.gemm(np.ascontiguousarray(A[rows]), W, b)) < 1e-5
+
+
 # Launches of few tiles take 128 x 128 tiles (two workgroups a CU): the SDXL stage-B shapes (2 x 1024 tokens, 1280
 # channels) and a row count that leaves a partial 128-row tile, each epilogue kind against the oracle. The same
 # products through 256-row tiles (a grouped launch with an empty second problem plans the same way, so instead the
