@@ -93,14 +93,17 @@ template <> struct Elem<true> {
 // S - m comes out of the matrix core: the softmax needs no per-score multiply-add, and the row sums are taken on the
 // bf16 probabilities the P V product uses (v_dot2 against ones), which halves those adds too. m is kept
 // bf16-representable so the product subtracts it exactly.
-template <int D, bool U, bool F16, bool HOLE>
-__global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn2_kernel(AttnP p)
+// NW waves a workgroup (32 queries each): 4, or 2 for launches of few query blocks (64-dim heads), whose 64-query
+// workgroups then spread over every CU, four a CU.
+template <int D, bool U, bool F16, bool HOLE, int NW = 4>
+__global__ __launch_bounds__(64 * NW, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn2_kernel(AttnP p)
 {
     typedef Elem<F16> X;
     typedef typename X::v8 V8;
     typedef typename X::e E;
-    constexpr int DS = D / 16, DT = D / 32, KC = D / 8;
-    constexpr int RK = kKT * KC / 256, RV = D * 8 / 256;
+    constexpr int DS = D / 16, DT = D / 32, KC = D / 8, QB = 32 * NW; // QB: queries a workgroup
+    constexpr int RK = kKT * KC / (64 * NW), RV = D * 8 / (64 * NW);
+    static_assert(NW == 4 || NW == 2, "4 or 2 waves a workgroup");
     // the two buffers are separate objects, so the compiler can tell a direct load into one from the fragment reads
     // of the other (with one array indexed by the buffer it waits for the loads before each read)
     __shared__ __attribute__((aligned(16))) uint16_t sK0[kKT * D], sK1[kKT * D];
@@ -115,7 +118,7 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     // XCD-aware order: workgroup i runs on XCD i % 8 (round-robin dispatch), so give each XCD a contiguous run of
     // (batch, head, query block) items: the query blocks of one head then share its K / V in that XCD's L2, instead
     // of every XCD streaming every head's K / V.
-    const uint32_t nqb = (p.n_q + 127) / 128, total = nqb * p.heads * p.batch;
+    const uint32_t nqb = (p.n_q + QB - 1) / QB, total = nqb * p.heads * p.batch;
     uint32_t item = blockIdx.x;
     if (total % 8 == 0)
         item = (item % 8) * (total / 8) + item / 8;
@@ -137,7 +140,7 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     const uint16_t* Q = p.q + bh * p.q_pad * D;
     const uint16_t* K = p.k + bkv * p.k_pad * D;
     const uint16_t* VT = p.vt + bkv * int64_t(D) * p.k_pad;
-    const int q0 = int(qb) * 128 + wave * 32;
+    const int q0 = int(qb) * QB + wave * 32;
 
     V8 qf[DS];
     {
@@ -152,12 +155,12 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     uint32_t ok[RK], ov[RV];
 #pragma unroll
     for (int i = 0; i < RK; ++i) {
-        const int P = (i * 4 + wave) * 64 + lane, key = P / KC, c = kswz(key, P % KC);
+        const int P = (i * NW + wave) * 64 + lane, key = P / KC, c = kswz(key, P % KC);
         ok[i] = uint32_t(key * D + c * 8) * 2;
     }
 #pragma unroll
     for (int i = 0; i < RV; ++i) {
-        const int P = (i * 4 + wave) * 64 + lane, d = P >> 3, c = (P & 7) ^ ((d >> 1) & 7);
+        const int P = (i * NW + wave) * 64 + lane, d = P >> 3, c = (P & 7) ^ ((d >> 1) & 7);
         ov[i] = uint32_t(d * int(p.k_pad) + c * 8) * 2;
     }
     const int ntiles = int((p.n_k + kKT - 1) / kKT);
@@ -165,18 +168,18 @@ __global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     auto dma1 = [&](int t, int buf, int i) {
         const uint32_t k0 = uint32_t(min(t, ntiles - 1) * kKT);
         if (i < RK)
-            buf_load_lds16(rsK, (lds_void*)&sK(buf)[(i * 4 + wave_s) * 512], ok[i], k0 * D * 2);
+            buf_load_lds16(rsK, (lds_void*)&sK(buf)[(i * NW + wave_s) * 512], ok[i], k0 * D * 2);
         else if (i < RK + RV)
-            buf_load_lds16(rsV, (lds_void*)&sV(buf)[((i - RK) * 4 + wave_s) * 512], ov[i - RK], k0 * 2);
+            buf_load_lds16(rsV, (lds_void*)&sV(buf)[((i - RK) * NW + wave_s) * 512], ov[i - RK], k0 * 2);
     };
     auto issue = [&](int t, int buf) {
         const uint32_t k0 = uint32_t(min(t, ntiles - 1) * kKT);
 #pragma unroll
         for (int i = 0; i < RK; ++i)
-            buf_load_lds16(rsK, (lds_void*)&sK(buf)[(i * 4 + wave_s) * 512], ok[i], k0 * D * 2);
+            buf_load_lds16(rsK, (lds_void*)&sK(buf)[(i * NW + wave_s) * 512], ok[i], k0 * D * 2);
 #pragma unroll
         for (int i = 0; i < RV; ++i)
-            buf_load_lds16(rsV, (lds_void*)&sV(buf)[(i * 4 + wave_s) * 512], ov[i], k0 * 2);
+            buf_load_lds16(rsV, (lds_void*)&sV(buf)[(i * NW + wave_s) * 512], ov[i], k0 * 2);
     };
     // S^T of a 32-key half of a tile: value r <-> key 8(r/4) + 4hk + r%4 of the half
     V8 kone = {}, qm = {}; // U: ones at dim 0 (K side); -m at dim 0 (Q side), lanes of the first k half
@@ -587,13 +590,21 @@ mk_status attention_to(const void* q, const void* k, const void* vt, void* out, 
             if (p.hole[b][0] == 0 && p.hole[b][1] > 0)
                 return fail(MK_ERR_ARG, "attention: a masked key range must leave key 0 visible");
         }
-    const dim3 grid(cdiv(n_q, 128) * heads * batch);
     hipStream_t s = static_cast<hipStream_t>(stream);
     const bool unit = scale == 0.0f;
+    // 64-dim heads in launches of fewer 128-query blocks than two a CU take 64-query workgroups (four a CU)
+    int cus = 0, dev = 0;
+    MK_HIP(hipGetDevice(&dev));
+    MK_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    const bool narrow = d == 64 && uint64_t(cdiv(n_q, 128)) * heads * batch < 2 * uint64_t(cus > 0 ? cus : 1);
+    const dim3 grid(cdiv(n_q, 128) * heads * batch), grid2(cdiv(n_q, 64) * heads * batch);
 #define MK_ATTN(F16, HOLE)                                                                                         \
     if (d == 128)                                                                                                  \
         unit ? attn2_kernel<128, true, F16, HOLE><<<grid, 256, 0, s>>>(p)                                          \
              : attn2_kernel<128, false, F16, HOLE><<<grid, 256, 0, s>>>(p);                                        \
+    else if (narrow)                                                                                               \
+        unit ? attn2_kernel<64, true, F16, HOLE, 2><<<grid2, 128, 0, s>>>(p)                                       \
+             : attn2_kernel<64, false, F16, HOLE, 2><<<grid2, 128, 0, s>>>(p);                                     \
     else                                                                                                           \
         unit ? attn2_kernel<64, true, F16, HOLE><<<grid, 256, 0, s>>>(p)                                           \
              : attn2_kernel<64, false, F16, HOLE><<<grid, 256, 0, s>>>(p)
