@@ -539,16 +539,22 @@ __global__ __launch_bounds__(64 * NW, 2) __attribute__((amdgpu_waves_per_eu(2, 2
     if (qi >= int(p.n_q))
         return;
     uint16_t* o = p.out + int64_t(bi) * p.so + int64_t(qi) * p.ldo + int64_t(head) * D;
-    const bool of16 = p.out_f16 != 0;
-    auto pk = [&](float a, float b) { return of16 ? pack_f16x2(a, b) : cvt_bf16x2(a, b); };
+    // one branch on the output type around stores specialised for each (a test at every pair becomes a branch each)
+    auto store = [&](auto h_c) {
+        auto pk = [](float a, float b) { return decltype(h_c)::value ? pack_f16x2(a, b) : cvt_bf16x2(a, b); };
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
+        for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const f32x16& a = oacc[dt];
-            *reinterpret_cast<u32x2*>(o + dt * 32 + 8 * i + 4 * hk) =
-                u32x2{pk(a[4 * i] * inv, a[4 * i + 1] * inv), pk(a[4 * i + 2] * inv, a[4 * i + 3] * inv)};
-        }
+            for (int i = 0; i < 4; ++i) {
+                const f32x16& a = oacc[dt];
+                *reinterpret_cast<u32x2*>(o + dt * 32 + 8 * i + 4 * hk) =
+                    u32x2{pk(a[4 * i] * inv, a[4 * i + 1] * inv), pk(a[4 * i + 2] * inv, a[4 * i + 3] * inv)};
+            }
+    };
+    if (p.out_f16)
+        store(std::true_type{});
+    else
+        store(std::false_type{});
 }
 
 } // namespace

@@ -126,8 +126,18 @@ constexpr int EK_DEEP = 128;
 constexpr int waitcnt_bits(int vm, int lgkm) { return (vm & 15) | ((vm >> 4) << 14) | (7 << 4) | ((lgkm & 15) << 8); }
 typedef _Float16 f16x8v __attribute__((ext_vector_type(8)));
 
-// A pair of 16-bit outputs: IEEE half or bf16, round to nearest even either way.
-__device__ inline uint32_t pack16(float a, float b, bool half) { return half ? pack_f16x2(a, b) : pack_bf16x2(a, b); }
+// A pair of 16-bit outputs: IEEE half (H) or bf16, round to nearest even either way. The type is a template
+// argument: the epilogues test the run-time flag once and run a copy of their store code for each type (with the flag
+// tested at every pair the compiler emits a uniform branch, a scalar reload of the flag and an LDS wait per pair).
+template <bool H> __device__ inline uint32_t pack16(float a, float b) { return H ? pack_f16x2(a, b) : pack_bf16x2(a, b); }
+// f(std::bool_constant<flag>{}): one branch on a uniform flag around code specialised for each value
+template <class F> __device__ inline void with_flag(bool flag, F&& f)
+{
+    if (flag)
+        f(std::true_type{});
+    else
+        f(std::false_type{});
+}
 
 // Per-tile channel constants of a lane's 4 channels (the same for every token row it writes).
 struct EpiCh {
@@ -184,20 +194,23 @@ __device__ inline void epi_slice(const GemmP& p, const float* st, int ld, int to
 #pragma unroll
         for (int i = 0; i < NI; ++i)
             xs[i] = *reinterpret_cast<const f32x4*>(c + int64_t(min(tok0 + r0 + RPI * i, int(p.M) - 1)) * p.ldc);
+        with_flag(p.c_f16, [&](auto h_c) {
+            constexpr bool H = decltype(h_c)::value;
 #pragma unroll
-        for (int i = 0; i < NI; ++i) {
-            const int t = tok0 + r0 + RPI * i;
-            const f32x4& x = xs[i];
-            if (t < int(p.M)) {
-                const uint32_t xx = uint32_t(t) - (y + 1) * pw - 1;
-                const uint64_t r = p.up_slack + uint64_t(2 * y + 1) * p.up_pw + 2 * xx + 1;
-                const u32x2 o{pack16(x[0] + v[i][0], x[1] + v[i][1], p.c_f16), pack16(x[2] + v[i][2], x[3] + v[i][3], p.c_f16)};
-                *reinterpret_cast<u32x2*>(up + r * ld2) = o;
-                *reinterpret_cast<u32x2*>(up + (r + 1) * ld2) = o;
-                *reinterpret_cast<u32x2*>(up + (r + p.up_pw) * ld2) = o;
-                *reinterpret_cast<u32x2*>(up + (r + p.up_pw + 1) * ld2) = o;
+            for (int i = 0; i < NI; ++i) {
+                const int t = tok0 + r0 + RPI * i;
+                const f32x4& x = xs[i];
+                if (t < int(p.M)) {
+                    const uint32_t xx = uint32_t(t) - (y + 1) * pw - 1;
+                    const uint64_t r = p.up_slack + uint64_t(2 * y + 1) * p.up_pw + 2 * xx + 1;
+                    const u32x2 o{pack16<H>(x[0] + v[i][0], x[1] + v[i][1]), pack16<H>(x[2] + v[i][2], x[3] + v[i][3])};
+                    *reinterpret_cast<u32x2*>(up + r * ld2) = o;
+                    *reinterpret_cast<u32x2*>(up + (r + 1) * ld2) = o;
+                    *reinterpret_cast<u32x2*>(up + (r + p.up_pw) * ld2) = o;
+                    *reinterpret_cast<u32x2*>(up + (r + p.up_pw + 1) * ld2) = o;
+                }
             }
-        }
+        });
         return;
     }
     if constexpr (EK == EK_RMW) {
@@ -229,12 +242,14 @@ __device__ inline void epi_slice(const GemmP& p, const float* st, int ld, int to
         return;
     }
     if constexpr (EK == EK_ACT) {
-        const bool gelu = p.epi == MK_EPI_GELU_TANH;
+        // GELU or SiLU for the whole slice (one branch)
+        with_flag(p.epi == MK_EPI_GELU_TANH, [&](auto g_c) {
 #pragma unroll
-        for (int i = 0; i < NI; ++i)
+            for (int i = 0; i < NI; ++i)
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-                v[i][e] = gelu ? gelu_tanh_f(v[i][e]) : silu_f(v[i][e]);
+                for (int e = 0; e < 4; ++e)
+                    v[i][e] = decltype(g_c)::value ? gelu_tanh_f(v[i][e]) : silu_f(v[i][e]);
+        });
     }
     // the stores: straight-line when the slice is whole (row-guard branches between stores make the compiler wait
     // for each store before the next)
@@ -242,9 +257,12 @@ __device__ inline void epi_slice(const GemmP& p, const float* st, int ld, int to
     const int64_t off0 = zc + int64_t(tok0 + r0) * p.ldc + ch, step = int64_t(RPI) * p.ldc;
     if (p.c_bf16) {
         u32x2 o[NI];
+        with_flag(p.c_f16, [&](auto h_c) {
 #pragma unroll
-        for (int i = 0; i < NI; ++i)
-            o[i] = u32x2{pack16(v[i][0], v[i][1], p.c_f16), pack16(v[i][2], v[i][3], p.c_f16)};
+            for (int i = 0; i < NI; ++i)
+                o[i] = u32x2{pack16<decltype(h_c)::value>(v[i][0], v[i][1]),
+                             pack16<decltype(h_c)::value>(v[i][2], v[i][3])};
+        });
         uint16_t* c = static_cast<uint16_t*>(p.c) + off0;
         if (whole) {
 #pragma unroll
@@ -316,6 +334,9 @@ __device__ inline void rmw_finish(const GemmP& p, const float* st, int ld, int t
 //    load behind stores would wait for all of them.
 //  - v: each lane two head dims across the 32 tokens, bf16 to V^T [batch][heads][128][k_pad] rows (keys in the
 //    vt_col order).
+// (F16: the output type; MODE: the RoPE mode, 0 none, 1 half-split pairs, 2 interleaved pairs; both template
+// arguments, so the code a launch runs has no per-row tests of them)
+template <bool F16, int MODE>
 __device__ inline void epi_heads(const GemmP& p, const float* st, int ld, int tok0, int nw0, int lane, uint32_t z)
 {
     const HeadsP& h = p.hp;
@@ -341,15 +362,15 @@ __device__ inline void epi_heads(const GemmP& p, const float* st, int ld, int to
                     // physical columns 16g + 0..15 hold keys 16g + {0..3, 8..11, 4..7, 12..15}
                     const int j0 = 16 * g;
                     *reinterpret_cast<u32x4*>(dst + k0 + j0) =
-                        u32x4{pack_x2(v(j0 + 0), v(j0 + 1), h.f16), pack_x2(v(j0 + 2), v(j0 + 3), h.f16),
-                              pack_x2(v(j0 + 8), v(j0 + 9), h.f16), pack_x2(v(j0 + 10), v(j0 + 11), h.f16)};
+                        u32x4{pack_x2(v(j0 + 0), v(j0 + 1), F16), pack_x2(v(j0 + 2), v(j0 + 3), F16),
+                              pack_x2(v(j0 + 8), v(j0 + 9), F16), pack_x2(v(j0 + 10), v(j0 + 11), F16)};
                     *reinterpret_cast<u32x4*>(dst + k0 + j0 + 8) =
-                        u32x4{pack_x2(v(j0 + 4), v(j0 + 5), h.f16), pack_x2(v(j0 + 6), v(j0 + 7), h.f16),
-                              pack_x2(v(j0 + 12), v(j0 + 13), h.f16), pack_x2(v(j0 + 14), v(j0 + 15), h.f16)};
+                        u32x4{pack_x2(v(j0 + 4), v(j0 + 5), F16), pack_x2(v(j0 + 6), v(j0 + 7), F16),
+                              pack_x2(v(j0 + 12), v(j0 + 13), F16), pack_x2(v(j0 + 14), v(j0 + 15), F16)};
                 }
             } else {
                 for (int t = 0; t < 32 && tok0 + t < int(p.M); ++t)
-                    dst[vt_col(k0 + t)] = h.f16 ? f2h_bits(v(t)) : f2bf_bits(v(t));
+                    dst[vt_col(k0 + t)] = F16 ? f2h_bits(v(t)) : f2bf_bits(v(t));
             }
         }
         return;
@@ -364,7 +385,7 @@ __device__ inline void epi_heads(const GemmP& p, const float* st, int ld, int to
 #pragma unroll
     for (int e = 0; e < 4; ++e)
         wn[e] *= ks;
-    const int mode = int(h.rope_mode);
+    constexpr int mode = MODE;
     const int last = int(p.M) - 1;
     // RoPE factors of a row (clamped to the last valid row): mode 2, pairs (2c, 2c + 1) -> (cos, sin, cos, sin) of
     // the lane's 4 channels; mode 1, channel d and d + 64 pair at angle d -> cos / sin of angles 4 (c % 16) .. + 3
@@ -442,10 +463,11 @@ __device__ inline void epi_heads(const GemmP& p, const float* st, int ld, int to
                 x[e] = lo ? x[e] * co - other * si : other * si + x[e] * co;
             }
         }
-        const int t = tok0 + r0 + 2 * i;
-        if (t <= last)
-            *reinterpret_cast<u32x2*>(base + int64_t(t) * 128) =
-                u32x2{pack_x2(x[0], x[1], h.f16), pack_x2(x[2], x[3], h.f16)};
+        // a row past M stores into the last row: its A row was read as the last row's (the loads clamp), so every
+        // value it computes is the last row's, bit for bit. No row guard, so the rows' code is one straight block in
+        // which the next rows' LDS reads can go out ahead of this row's store.
+        const int t = min(tok0 + r0 + 2 * i, last);
+        *reinterpret_cast<u32x2*>(base + int64_t(t) * 128) = u32x2{pack_x2(x[0], x[1], F16), pack_x2(x[2], x[3], F16)};
     };
 #pragma unroll
     for (int i = 0; i < 8; ++i)
@@ -466,6 +488,7 @@ __device__ inline void epi_heads(const GemmP& p, const float* st, int ld, int to
 // [bh][d][k_pad] (a lane per dim, 32 keys in the vt_col order). Q-only launches (k == NULL) write Q alone, k|v-only
 // launches (q == NULL: the cross attention's context, heads_half from the fp32 projection, sdxl.cpp:697-708) K and
 // V^T, each rounded once from the fp32 accumulators.
+template <bool F16>
 __device__ inline void epi_heads64(const GemmP& p, const float* st, int ld, int tok0, int nw0, int lane, uint32_t z)
 {
     const HeadsP& h = p.hp;
@@ -485,15 +508,15 @@ __device__ inline void epi_heads64(const GemmP& p, const float* st, int ld, int 
                 // physical columns 16g + 0..15 hold keys 16g + {0..3, 8..11, 4..7, 12..15}
                 const int j0 = 16 * g;
                 *reinterpret_cast<u32x4*>(dst + k0 + j0) =
-                    u32x4{pack_x2(v(j0 + 0), v(j0 + 1), h.f16), pack_x2(v(j0 + 2), v(j0 + 3), h.f16),
-                          pack_x2(v(j0 + 8), v(j0 + 9), h.f16), pack_x2(v(j0 + 10), v(j0 + 11), h.f16)};
+                    u32x4{pack_x2(v(j0 + 0), v(j0 + 1), F16), pack_x2(v(j0 + 2), v(j0 + 3), F16),
+                          pack_x2(v(j0 + 8), v(j0 + 9), F16), pack_x2(v(j0 + 10), v(j0 + 11), F16)};
                 *reinterpret_cast<u32x4*>(dst + k0 + j0 + 8) =
-                    u32x4{pack_x2(v(j0 + 4), v(j0 + 5), h.f16), pack_x2(v(j0 + 6), v(j0 + 7), h.f16),
-                          pack_x2(v(j0 + 12), v(j0 + 13), h.f16), pack_x2(v(j0 + 14), v(j0 + 15), h.f16)};
+                    u32x4{pack_x2(v(j0 + 4), v(j0 + 5), F16), pack_x2(v(j0 + 6), v(j0 + 7), F16),
+                          pack_x2(v(j0 + 12), v(j0 + 13), F16), pack_x2(v(j0 + 14), v(j0 + 15), F16)};
             }
         } else {
             for (int t = 0; t < 32 && tok0 + t <= last; ++t)
-                dst[vt_col(k0 + t)] = h.f16 ? f2h_bits(v(t)) : f2bf_bits(v(t));
+                dst[vt_col(k0 + t)] = F16 ? f2h_bits(v(t)) : f2bf_bits(v(t));
         }
         return;
     }
@@ -505,14 +528,13 @@ __device__ inline void epi_heads64(const GemmP& p, const float* st, int ld, int 
     uint16_t* base = (which == 0 ? h.q : h.k) + (bh * pad + (which == 0 ? h.q_row0 : h.row0)) * 64 + ch;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        const int r = r0 + 4 * i, t = tok0 + r;
+        // a row past M stores into the last row, with the last row's bits (its A row was read as the last row's)
+        const int r = r0 + 4 * i, t = min(tok0 + r, last);
         f32x4 x = *reinterpret_cast<const f32x4*>(st + r * ld + ch);
 #pragma unroll
         for (int e = 0; e < 4; ++e)
             x[e] = (x[e] * sc[e] + bi[e]) * ks;
-        if (t <= last)
-            *reinterpret_cast<u32x2*>(base + int64_t(t) * 64) =
-                u32x2{pack_x2(x[0], x[1], h.f16), pack_x2(x[2], x[3], h.f16)};
+        *reinterpret_cast<u32x2*>(base + int64_t(t) * 64) = u32x2{pack_x2(x[0], x[1], F16), pack_x2(x[2], x[3], F16)};
     }
 }
 
@@ -585,7 +607,7 @@ constexpr int fixup_groups(int qn, int cap)
 // each 32-channel third), 8 rows an instruction, 4 rows a lane; a row's sum of squares over its 8 lanes by DPP. With
 // C = 192 (PAIR) the row's other 96 channels are the partner wave's (wave ^ 1): the partial sums meet in xch (32
 // floats a wave) across one barrier that waits for LDS operations only, not for the stores in flight.
-template <int EKE, bool PAIR>
+template <int EKE, bool PAIR, bool H>
 __device__ inline void epi_norm_silu(const GemmP& p, const float* st, int ld, int tok0, int chw, int lane, float* xch,
                                      int wave)
 {
@@ -658,8 +680,8 @@ __device__ inline void epi_norm_silu(const GemmP& p, const float* st, int ld, in
 #pragma unroll
             for (int e = 0; e < 4; ++e)
                 u[e] = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, silu_f(v[i][j][e] * sc * gm[j][e])) & keep);
-            o[j][0] = pack16(u[0], u[1], p.c_f16);
-            o[j][1] = pack16(u[2], u[3], p.c_f16);
+            o[j][0] = pack16<H>(u[0], u[1]);
+            o[j][1] = pack16<H>(u[2], u[3]);
         }
         if (t < int(p.M)) {
             uint16_t* y = EKE == EK_RMWN ? p.norm_out + int64_t(t) * p.norm_ld + chw + 4 * c
@@ -1220,27 +1242,36 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
         // slice of WC/2 channels
         constexpr int CH2 = CB / 2, NQ = M16 ? 1 : 4; // groups of 4 consecutive channels a lane holds in a block
         const int oc0 = int(tn) * (BN / 2) + wn * (WC / 2);
-        const bool swi = p.epi == MK_EPI_SWIGLU, sum = p.epi == MK_EPI_PAIR_SUM;
+        // one copy of the products for each kind (one branch a tile)
+        auto glu = [&](auto kind_c) {
+            constexpr int KIND = decltype(kind_c)::value; // 0 pair sum, 1 SwiGLU, 2 GEGLU
 #pragma unroll
-        for (int cb = 0; cb < CH2; ++cb)
+            for (int cb = 0; cb < CH2; ++cb)
 #pragma unroll
-            for (int q = 0; q < NQ; ++q) {
-                const int c1 = oc0 + cb * MB + (M16 ? 4 * g4 : 8 * q + 4 * hk), c2 = c1 + int(p.glu_f);
-                const f32x4 s1 = p.wscale ? *reinterpret_cast<const f32x4*>(p.wscale + c1) : f32x4{1, 1, 1, 1};
-                const f32x4 s2 = p.wscale ? *reinterpret_cast<const f32x4*>(p.wscale + c2) : f32x4{1, 1, 1, 1};
-                const f32x4 b1 = p.bias ? *reinterpret_cast<const f32x4*>(p.bias + c1) : f32x4{0, 0, 0, 0};
-                const f32x4 b2 = p.bias ? *reinterpret_cast<const f32x4*>(p.bias + c2) : f32x4{0, 0, 0, 0};
+                for (int q = 0; q < NQ; ++q) {
+                    const int c1 = oc0 + cb * MB + (M16 ? 4 * g4 : 8 * q + 4 * hk), c2 = c1 + int(p.glu_f);
+                    const f32x4 s1 = p.wscale ? *reinterpret_cast<const f32x4*>(p.wscale + c1) : f32x4{1, 1, 1, 1};
+                    const f32x4 s2 = p.wscale ? *reinterpret_cast<const f32x4*>(p.wscale + c2) : f32x4{1, 1, 1, 1};
+                    const f32x4 b1 = p.bias ? *reinterpret_cast<const f32x4*>(p.bias + c1) : f32x4{0, 0, 0, 0};
+                    const f32x4 b2 = p.bias ? *reinterpret_cast<const f32x4*>(p.bias + c2) : f32x4{0, 0, 0, 0};
 #pragma unroll
-                for (int tb = 0; tb < TB; ++tb)
+                    for (int tb = 0; tb < TB; ++tb)
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const float a = acc[cb][tb][4 * q + e] * s1[e] + b1[e];
-                        const float g = acc[cb + CH2][tb][4 * q + e] * s2[e] + b2[e];
-                        acc[cb][tb][4 * q + e] = sum ? a + g
-                                                 : swi ? silu_f(a) * g
-                                                       : a * (0.5f * g * (1.0f + erf_fit(g * 0.70710678f)));
-                    }
-            }
+                        for (int e = 0; e < 4; ++e) {
+                            const float a = acc[cb][tb][4 * q + e] * s1[e] + b1[e];
+                            const float g = acc[cb + CH2][tb][4 * q + e] * s2[e] + b2[e];
+                            acc[cb][tb][4 * q + e] = KIND == 0   ? a + g
+                                                     : KIND == 1 ? silu_f(a) * g
+                                                                 : a * (0.5f * g * (1.0f + erf_fit(g * 0.70710678f)));
+                        }
+                }
+        };
+        if (p.epi == MK_EPI_PAIR_SUM)
+            glu(std::integral_constant<int, 0>{});
+        else if (p.epi == MK_EPI_SWIGLU)
+            glu(std::integral_constant<int, 1>{});
+        else
+            glu(std::integral_constant<int, 2>{});
         constexpr int WH = WC / 2, LDH = WH + 4;
         float* sh = reinterpret_cast<float*>(smem) + wave * 32 * LDH;
         const EpiCh unit{f32x4{1, 1, 1, 1}, f32x4{0, 0, 0, 0}, f32x4{}, f32x4{}};
@@ -1265,6 +1296,7 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
         return;
     }
     if constexpr (EKE == EK_NORM || EKE == EK_RMWN) {
+        static_assert(kConv && kF16, "the norm epilogues follow half convolutions");
         // 96-channel tiles: a wave holds whole rows; 192-channel tiles: a row's channels are a wave pair's
         static_assert(WC == 96 && M16 && (BN == 96 || BN == 192), "the norm epilogues take 96- or 192-channel rows");
         constexpr bool PAIR = BN == 192;
@@ -1274,21 +1306,31 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
             stage(s);
-            epi_norm_silu<EKE, PAIR>(p, st, LDW, m0 + wm * WM + s * 32, wn * WC, lane, xch + (s & 1) * NW * 32, wave);
+            // (a convolution's 16-bit grids are IEEE half, like its operands)
+            epi_norm_silu<EKE, PAIR, true>(p, st, LDW, m0 + wm * WM + s * 32, wn * WC, lane, xch + (s & 1) * NW * 32,
+                                           wave);
         }
         return;
     }
     if constexpr (EKE == EK_HEADS) {
-        // the heads epilogue is large: one copy of it in a rolled loop over the 32-token slices, which always
-        // stages slice 0 of the accumulators and then rotates the next slice into its place (static register
-        // indices, so the accumulators stay in registers)
+        // the heads epilogue is large: one copy of it for each output type in a rolled loop over the 32-token
+        // slices, which always stages slice 0 of the accumulators and then rotates the next slice into its place
+        // (static register indices, so the accumulators stay in registers)
 #pragma unroll 1
         for (int s = 0; s < NS; ++s) {
             stage(0);
-            if constexpr (WC == 64)
-                epi_heads64(p, st, LDW, m0 + wm * WM + s * 32, n0 + wn * WC, lane, z);
-            else
-                epi_heads(p, st, LDW, m0 + wm * WM + s * 32, n0 + wn * WC, lane, z);
+            with_flag(p.hp.f16, [&](auto h_c) {
+                constexpr bool H = decltype(h_c)::value;
+                const int tok = m0 + wm * WM + s * 32, nw = n0 + wn * WC;
+                if constexpr (WC == 64)
+                    epi_heads64<H>(p, st, LDW, tok, nw, lane, z);
+                else if (p.hp.rope_mode == 2)
+                    epi_heads<H, 2>(p, st, LDW, tok, nw, lane, z);
+                else if (p.hp.rope_mode == 1)
+                    epi_heads<H, 1>(p, st, LDW, tok, nw, lane, z);
+                else
+                    epi_heads<H, 0>(p, st, LDW, tok, nw, lane, z);
+            });
 #pragma unroll
             for (int cb = 0; cb < CB; ++cb)
 #pragma unroll

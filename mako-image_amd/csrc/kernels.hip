@@ -176,17 +176,24 @@ __global__ __launch_bounds__(256) void norm_kernel(const float* __restrict__ x, 
         inv = rsqrtf(wave_sum(q) / float(n) + eps);
     }
     u32x2* yr = reinterpret_cast<u32x2*>(y + uint64_t(row) * n);
+    // one branch on the output type around stores specialised for each (a test at every pair becomes a branch each)
+    auto store = [&](auto h_c) {
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-        const uint32_t c = lane + 64u * i;
-        if (c < nv) {
-            float o[4];
+        for (int i = 0; i < NV; ++i) {
+            const uint32_t c = lane + 64u * i;
+            if (c < nv) {
+                float o[4];
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                o[j] = kRms ? v[i][j] * inv * (gg[i][j] + w_offset) : (v[i][j] - mean) * inv * gg[i][j] + bb[i][j];
-            yr[c] = u32x2{pack_x2(o[0], o[1], f16), pack_x2(o[2], o[3], f16)};
+                for (int j = 0; j < 4; ++j)
+                    o[j] = kRms ? v[i][j] * inv * (gg[i][j] + w_offset) : (v[i][j] - mean) * inv * gg[i][j] + bb[i][j];
+                yr[c] = u32x2{pack_x2(o[0], o[1], decltype(h_c)::value), pack_x2(o[2], o[3], decltype(h_c)::value)};
+            }
         }
-    }
+    };
+    if (f16)
+        store(std::true_type{});
+    else
+        store(std::false_type{});
 }
 
 // norm_kernel with the smallest NV >= nvec (1 .. kMaxVec float4s a lane)
@@ -277,12 +284,18 @@ __global__ __launch_bounds__(256) void group_apply_kernel(const float* __restric
 {
     const uint64_t n = uint64_t(rows) * c;
     const uint32_t bi = blockIdx.y;
-    for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < n; i += uint64_t(gridDim.x) * 256) {
-        const uint32_t ch = uint32_t(i % c);
-        const float2 st = stats[bi * groups + ch / (c / groups)];
-        const float v = (x[uint64_t(bi) * n + i] - st.x) * st.y * g[ch] + b[ch];
-        y[uint64_t(bi) * n + i] = f16 ? f2h_bits(v) : f2bf_bits(v);
-    }
+    auto run = [&](auto h_c) { // the loop for one output type (no test of it per element)
+        for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < n; i += uint64_t(gridDim.x) * 256) {
+            const uint32_t ch = uint32_t(i % c);
+            const float2 st = stats[bi * groups + ch / (c / groups)];
+            const float v = (x[uint64_t(bi) * n + i] - st.x) * st.y * g[ch] + b[ch];
+            y[uint64_t(bi) * n + i] = decltype(h_c)::value ? f2h_bits(v) : f2bf_bits(v);
+        }
+    };
+    if (f16)
+        run(std::true_type{});
+    else
+        run(std::false_type{});
 }
 
 // group_apply_kernel four channels a thread (c a multiple of 4; x, g, b 16-byte and y 8-byte aligned): float4 loads,
@@ -296,17 +309,24 @@ __global__ __launch_bounds__(256) void group_apply4_kernel(const float* __restri
     const f32x4* xb = reinterpret_cast<const f32x4*>(x + uint64_t(bi) * rows * c);
     u32x2* yb = reinterpret_cast<u32x2*>(y + uint64_t(bi) * rows * c);
     const float2* sb = stats + bi * groups;
-    for (uint32_t i = blockIdx.x * 256 + threadIdx.x; i < n4; i += gridDim.x * 256) {
-        const uint32_t ch = (i % c4) * 4;
-        const f32x4 v = xb[i], gg = *reinterpret_cast<const f32x4*>(g + ch), bb = *reinterpret_cast<const f32x4*>(b + ch);
-        float o[4];
+    auto run = [&](auto h_c) { // the loop for one output type (no test of it per element)
+        for (uint32_t i = blockIdx.x * 256 + threadIdx.x; i < n4; i += gridDim.x * 256) {
+            const uint32_t ch = (i % c4) * 4;
+            const f32x4 v = xb[i], gg = *reinterpret_cast<const f32x4*>(g + ch),
+                        bb = *reinterpret_cast<const f32x4*>(b + ch);
+            float o[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const float2 st = sb[(ch + j) / cg];
-            o[j] = (v[j] - st.x) * st.y * gg[j] + bb[j];
+            for (int j = 0; j < 4; ++j) {
+                const float2 st = sb[(ch + j) / cg];
+                o[j] = (v[j] - st.x) * st.y * gg[j] + bb[j];
+            }
+            yb[i] = u32x2{pack_x2(o[0], o[1], decltype(h_c)::value), pack_x2(o[2], o[3], decltype(h_c)::value)};
         }
-        yb[i] = u32x2{pack_x2(o[0], o[1], f16), pack_x2(o[2], o[3], f16)};
-    }
+    };
+    if (f16)
+        run(std::true_type{});
+    else
+        run(std::false_type{});
 }
 
 // gate_add (image.metal:55-65) with an identity or tanh gate; y fp32 or bf16.
