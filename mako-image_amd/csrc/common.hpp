@@ -310,8 +310,10 @@ __device__ inline float tanh_f(float u) { return 2.0f / (1.0f + __expf(-2.0f * u
 // GELU with the tanh approximation: 0.5 x (1 + tanh(u)) = x sigmoid(2u), u = sqrt(2/pi) (x + 0.044715 x^3)
 __device__ inline float gelu_tanh_f(float x)
 {
-    const float u = 0.7978845608028654f * (x + 0.044715f * x * x * x);
-    return x * __builtin_amdgcn_rcpf(1.0f + __expf(-2.0f * u));
+    // 0.5 x (1 + tanh u) = x / (1 + e^(-2u)), u = sqrt(2/pi) (x + 0.044715 x^3); e^(-2u) = 2^(x (c1 + c2 x^2)) with
+    // c1 = -2 sqrt(2/pi) log2(e), c2 = 0.044715 c1 folded: three multiply-adds, v_exp_f32 (2^y), v_rcp_f32, one add
+    constexpr float c1 = -2.3022082f, c2 = -0.10294324f;
+    return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * fmaf(x * x, c2, c1)));
 }
 // erf by the Numerical Recipes erfc Chebyshev fit (max error ~1.2e-7), the form the reference's geglu uses
 // (image.metal:450-463).

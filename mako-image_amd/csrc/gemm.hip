@@ -144,21 +144,31 @@ struct EpiCh {
     f32x4 scale, bias, g0, g1; // g0: the gate row, g1: the alternate gate row (rows r % seg_rows < split)
 };
 
-__device__ inline EpiCh epi_channels(const GemmP& p, int ch)
+// MK_EPI_GATE_TANH: the gates through tanh (apart from the loads, so the residual's loads can go out in between: the
+// tanh waits for the gate loads only)
+__device__ inline void epi_gate_tanh(const GemmP& p, EpiCh& c)
+{
+    if (p.gate && p.epi == MK_EPI_GATE_TANH)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            c.g0[e] = tanh_f(c.g0[e]);
+            c.g1[e] = tanh_f(c.g1[e]);
+        }
+}
+
+__device__ inline EpiCh epi_channels(const GemmP& p, int ch, bool tanh_now = true)
 {
     EpiCh c;
     c.scale = p.wscale ? *reinterpret_cast<const f32x4*>(p.wscale + ch) : f32x4{1, 1, 1, 1};
     c.bias = p.bias ? *reinterpret_cast<const f32x4*>(p.bias + ch) : f32x4{0, 0, 0, 0};
     if (p.gate) {
+        // without a split the alternate row is the gate row itself, loaded again: a copy of g0 would wait for g0's
+        // load right here, before the loads that follow could go out
         c.g0 = *reinterpret_cast<const f32x4*>(p.gate + ch);
-        c.g1 = p.split ? *reinterpret_cast<const f32x4*>(p.gate + p.gate_alt + ch) : c.g0;
-        if (p.epi == MK_EPI_GATE_TANH)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                c.g0[e] = tanh_f(c.g0[e]);
-                c.g1[e] = tanh_f(c.g1[e]);
-            }
+        c.g1 = *reinterpret_cast<const f32x4*>(p.gate + (p.split ? p.gate_alt : 0) + ch);
     }
+    if (tanh_now)
+        epi_gate_tanh(p, c);
     return c;
 }
 
@@ -1354,11 +1364,13 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
                                    kch[j]);
         }
     } else {
-        EpiCh kch = epi_channels(p, n0 + wn * WC + 4 * (lane % (WC / 4)));
+        EpiCh kch = epi_channels(p, n0 + wn * WC + 4 * (lane % (WC / 4)), EKE != EK_RMW);
         if constexpr (EKE == EK_RMW) {
-            // the residual rows of slice s + 1 load while slice s is staged, added and stored
+            // the residual rows of slice s + 1 load while slice s is staged, added and stored; slice 0's go out
+            // with the channel constants, before the gates' tanh waits for those
             f32x4 xr[2][WC / 8];
             rmw_load<WC>(p, m0 + wm * WM, n0 + wn * WC, lane, zc, xr[0]);
+            epi_gate_tanh(p, kch);
 #pragma unroll
             for (int s = 0; s < NS; ++s) {
                 stage(s);
