@@ -339,10 +339,10 @@ __device__ inline void rmw_finish(const GemmP& p, const float* st, int ld, int t
 // The q / k / v epilogue from a wave's staged slice: 32 tokens x 128 channels (one head of q, k or v) in LDS, row
 // stride ld floats, tokens tok0 .. tok0 + 31 (GEMM rows).
 //  - q, k: lanes along the head's channels (4 each, 32 lanes a row, rows r0 + 2i for i < 16): per-head RMSNorm * w
-//    (the row's sum of squares reduced across its 32 lanes), RoPE, bf16 rows to [batch][heads][pad][128]. Every
+//    (the row's sum of squares reduced across its 32 lanes), RoPE, 16-bit rows to [batch][heads][pad][128]. Every
 //    global load (channel constants, RoPE factors) is issued before the first store: vmcnt also counts stores, so a
 //    load behind stores would wait for all of them.
-//  - v: each lane two head dims across the 32 tokens, bf16 to V^T [batch][heads][128][k_pad] rows (keys in the
+//  - v: each lane two head dims across the 32 tokens, 16-bit to V^T [batch][heads][128][k_pad] rows (keys in the
 //    vt_col order).
 // (F16: the output type; MODE: the RoPE mode, 0 none, 1 half-split pairs, 2 interleaved pairs; both template
 // arguments, so the code a launch runs has no per-row tests of them)
@@ -1323,9 +1323,9 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, uint32_t z, uint32_t t
         return;
     }
     if constexpr (EKE == EK_HEADS) {
-        // the heads epilogue is large: one copy of it for each output type in a rolled loop over the 32-token
-        // slices, which always stages slice 0 of the accumulators and then rotates the next slice into its place
-        // (static register indices, so the accumulators stay in registers)
+        // the heads epilogue is large: one copy of it for each output type and RoPE mode (a launch runs one) in a
+        // rolled loop over the 32-token slices, which always stages slice 0 of the accumulators and then rotates the
+        // next slice into its place (static register indices, so the accumulators stay in registers)
 #pragma unroll 1
         for (int s = 0; s < NS; ++s) {
             stage(0);
