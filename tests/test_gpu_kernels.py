@@ -171,6 +171,22 @@ def test_gemm_gelu_bf16(gpu, rng):
     assert np.abs(got - want).max() <= 2 ** -8 * np.abs(want).max() + 1e-6
 
 
+def test_gemm_gelu_wide_range(gpu, rng):
+    # pre-activations over about +-60 (the epilogue's 2^(x (c1 + c2 x^2)) overflows to +inf for large negative x and
+    # underflows to 0 for large positive x): every element within bf16 rounding of the oracle's tanh form, all finite
+    Mr, N, K = 256, 256, 256
+    A = R.bf16_round(rng.standard_normal((Mr, K)).astype(np.float32))  # the operands the GPU multiplies
+    W = R.bf16_round(rng.standard_normal((N, K)).astype(np.float32) * 1.25)
+    out = M.Dev(Mr * N * 2)
+    gemm(bdev(A), bdev(W), c=out, c_dtype=M.BF16, epi=M.EPI_GELU_TANH, M_=(Mr, N, K), lda=K, ldc=N)
+    y = R.gemm(A, W)
+    want = R.gelu_tanh(y)
+    got = fetch_bf16(out, (Mr, N))
+    assert np.abs(y).max() > 40 and (y < -10).any()
+    assert np.isfinite(got).all()
+    assert (np.abs(got - want) <= 2 ** -7 * np.abs(want) + 1e-6).all()
+
+
 @pytest.mark.parametrize("epi", [M.EPI_GATE_ADD, M.EPI_GATE_TANH, M.EPI_ADD])
 def test_gemm_residual_epilogues(gpu, rng, epi):
     # batched with strides (rows of one batch item inside a longer sequence), gate rows split as the 2.1 graph's
