@@ -280,8 +280,9 @@ def test_gemm_heads_epilogue(gpu, rng, mode, row0, q_row0, k_scale, odt):
         for got, want in ((gq[bi][:, q_row0:q_row0 + Mr], wq), (gk[bi][:, row0:row0 + Mr], wk),
                           (gv[bi][:, :, vcols].transpose(0, 2, 1), wv)):
             assert np.abs(got - want).max() <= 2 ** -8 * np.abs(want).max() + 1e-6
-    # rows outside the written range stay zero
+    # rows outside the written range stay zero (a tile's rows past M store into the last row, with its bits)
     assert not gk[:, :, :row0].any() and not gk[:, :, row0 + Mr:].any()
+    assert not gq[:, :, :q_row0].any() and not gq[:, :, q_row0 + Mr:].any()
 
 
 # 64-dim heads (the SDXL form: half, no norm, no RoPE) on 128-channel tiles: q | k | v and Q alone, batch 2, row
