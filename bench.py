@@ -423,14 +423,14 @@ def cpu_baseline_q21(seconds_target, step_flops_):
 
 KERNEL_OF_Q21 = {"gemm.ff1": "gemm_kernel<256, 256, false, 4, 8> (SwiGLU epilogue)",
                  "gemm.ff2": "gemm_sk_kernel<256, 256, false, 2, 8>", "gemm.qkv": "gemm_kernel<256, 256, false, 3, 8>",
-                 "gemm.o": "gemm_kernel<256, 256, false, 2, 8>", "attention": "attn2_kernel<128, true, true, false> (half)"}
+                 "gemm.o": "gemm_kernel<256, 256, false, 2, 8>", "attention": "attn2_kernel<128, true, true, false, 4> (half)"}
 
 
 # The kernel each timing class of the step launches (rocprofv3's name for it), for the traffic figure.
 KERNEL_OF = {"gemm.ff2": "gemm_sk_kernel<256, 256, false, 2, 8>",
-             "gemm.ff1.img": "gemm_kernel<256, 256, false, 1, 8>", "gemm.ff1.txt": "gemm_kernel<256, 128, false, 1, 4>",
+             "gemm.ff1.img": "gemm_kernel<256, 256, false, 1, 8>", "gemm.ff1.txt": "gemm_kernel<256, 128, false, 129, 4>",
              "gemm.qkv": "gemm_kernel<256, 256, false, 3, 8>", "gemm.o": "gemm_kernel<256, 256, false, 2, 8>",
-             "attention": "attn2_kernel<128, true, false, false>"}
+             "attention": "attn2_kernel<128, true, false, false, 4>"}
 
 
 def kernel_traffic(kernel):
