@@ -71,3 +71,15 @@ def test_vae_flops_from_the_decoders_weights(base, th, tw):
     got, attn = bench.vae_flops(th, tw, b=base)
     assert attn == 4 * n0 * n0 * d0
     assert got == total
+
+
+def test_kernel_names_follow_the_profiled_launches():
+    # the kernel each timing class names (and whose traffic bench.py reports) is one the profiled step launches:
+    # a renamed or re-templated kernel would otherwise leave the roofline's traffic figure silently empty
+    prof = (bench.ROOT / "profiles" / "mmdit_step_1024_kernels.md").read_text()
+    for cls, name in bench.KERNEL_OF.items():
+        assert name in prof, (cls, name)
+        assert bench.kernel_traffic(name) is not None, (cls, name)
+    prof21 = (bench.ROOT / "profiles" / "q21_step_1024_kernels.md").read_text()
+    for cls, name in bench.KERNEL_OF_Q21.items():
+        assert name.split(" (")[0] in prof21, (cls, name)
