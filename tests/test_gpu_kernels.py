@@ -594,6 +594,40 @@ def test_gemm_rejects_bad_shapes(gpu):
     assert b"multiples of 64" in M.lib().mk_last_error()
 
 
+def test_gemm_empty_problems(gpu, rng):
+    # a problem with no rows (M = 0) or no batch items launches nothing and leaves C as it was; beside a non-empty
+    # problem in a grouped launch it drops out, and the other problem gets the bits of its own launch
+    N, K, Mr = 128, 128, 200
+    A = rng.standard_normal((Mr, K)).astype(np.float32)
+    W = R.bf16_round(rng.standard_normal((N, K)).astype(np.float32) * 0.05)
+    Ad, Wd = bdev(A), bdev(W)
+    sentinel = np.full(Mr * N, 7.5, np.float32)
+    for m, batch in ((0, 1), (Mr, 0)):
+        out = dev(sentinel)
+        gemm(Ad, Wd, c=out, M_=(m, N, K), batch=batch, lda=K, ldc=N)
+        assert np.array_equal(fetch(out, (Mr * N,)), sentinel), (m, batch)
+    solo, grp, idle = dev(sentinel), dev(sentinel), dev(sentinel)
+    gemm(Ad, Wd, c=solo, M_=(Mr, N, K), lda=K, ldc=N)
+    gemm_grouped(gemm_args(Ad, Wd, c=grp, M_=(Mr, N, K), lda=K, ldc=N),
+                 gemm_args(Ad, Wd, c=idle, M_=(0, N, K), lda=K, ldc=N))
+    assert np.array_equal(fetch(grp, (Mr, N)), fetch(solo, (Mr, N)))
+    assert np.array_equal(fetch(idle, (Mr * N,)), sentinel)
+    assert maxrel(fetch(solo, (Mr, N)), R.gemm(A, W)) < 1e-5
+
+
+def test_elementwise_empty_inputs(gpu):
+    # zero elements or rows: the call succeeds and writes nothing
+    sentinel = np.full(256, 7.5, np.float32)
+    x, y, g = dev(sentinel), dev(sentinel), dev(sentinel)
+    M.call("mk_silu", x.p, 0, None)
+    M.call("mk_gelu_tanh", x.p, 0, None)
+    M.call("mk_rms_norm", x.p, 0, 64, g.p, 0.0, 1e-6, y.p, None)
+    M.call("mk_gate_add", x.p, y.p, M.F32, 0, 64, g.p, 0, 0, 1, 0, None)
+    M.sync()
+    for d in (x, y, g):
+        assert np.array_equal(fetch(d, (256,)), sentinel)
+
+
 # ---------------------------------------------------------------------------------------------------------------
 # attention
 # ---------------------------------------------------------------------------------------------------------------
