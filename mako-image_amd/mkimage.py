@@ -633,8 +633,13 @@ class Engine:
         return b.value
 
     def begin(self, prompt, h, w, slot=0):
+        """prompt: S rows of text_dim embeddings, in any shape holding S x text_dim floats (the reference takes a flat
+        span and refuses one that is empty or not whole rows, qwen_image.cpp:117-118)."""
         prompt = np.ascontiguousarray(prompt, dtype=np.float32)
-        call("mk_begin", self.h, prompt.ctypes.data, prompt.shape[0], h, w, slot)
+        td = int(self.cfg.text_dim)
+        if prompt.size == 0 or prompt.size % td:
+            raise MkError(f"prompt embeddings must be rows of {td}")
+        call("mk_begin", self.h, prompt.ctypes.data, prompt.size // td, h, w, slot)
 
     def step(self, latents, sigma, slot=0):
         latents = np.ascontiguousarray(latents, dtype=np.float32)

@@ -180,6 +180,9 @@ def test_q21_step_errors(gpu):
         e.step(np.zeros((4, 64), np.float32), 0.5, 0)
     with pytest.raises(M.MkError, match="slot"):
         e.begin(np.zeros((3, 512), np.float32), 2, 2, 2)
+    for bad in (np.zeros((3, 500), np.float32), np.zeros((0, 512), np.float32)):
+        with pytest.raises(M.MkError, match="rows of 512"):
+            e.begin(bad, 2, 2, 0)
     e.begin(np.zeros((3, 512), np.float32), 2, 2, 0)
     with pytest.raises(M.MkError, match="latents"):
         e.step(np.zeros((5, 64), np.float32), 0.5, 0)
