@@ -510,6 +510,8 @@ class Vae:
         self.z = z
         self._mean = np.ascontiguousarray(np.zeros(z) if mean is None else mean, dtype=np.float32)
         self._std = np.ascontiguousarray(np.ones(z) if std is None else std, dtype=np.float32)
+        if self._mean.size != z or self._std.size != z:
+            raise MkError(f"vae: mean and std need {z} values each (one a latent channel)")
         cfg = VaeConfig(base, z, self._mean.ctypes.data_as(_fp), self._std.ctypes.data_as(_fp))
         p = _vp()
         call("mk_vae_create", C.byref(cfg), C.byref(p))
@@ -660,6 +662,8 @@ class Engine:
         """The Euler loop over `sigmas` (len steps + 1) from `noise` [h*w][latent]; returns the final latents."""
         noise = np.ascontiguousarray(noise, dtype=np.float32)
         sigmas = np.ascontiguousarray(sigmas, dtype=np.float32)
+        if sigmas.ndim != 1 or sigmas.size < 2:
+            raise MkError("generate: sigmas must hold steps + 1 >= 2 noise levels")
         out = np.empty_like(noise)
         call("mk_generate", self.h, noise.ctypes.data, noise.size, sigmas.ctypes.data, sigmas.size - 1, guidance,
              out.ctypes.data)

@@ -267,6 +267,9 @@ def test_generate_unguided_matches_oracle_euler(gpu):
     within(got - lat[0], x - lat[0], 64)
     with pytest.raises(M.MkError, match="begin both"):
         e.generate(lat[0], sig, 3.0)
+    for bad in (sig[:1], sig[:0]):  # no step to take: refused before the library reads sigmas[1]
+        with pytest.raises(M.MkError, match="steps \\+ 1"):
+            e.generate(lat[0], bad, 1.0)
 
 
 FULL = dict(blocks=1, dim=3072, heads=24, head_dim=128, ffn=12288, text_dim=3584)

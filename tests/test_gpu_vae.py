@@ -209,6 +209,8 @@ def test_vae_argument_errors(gpu):
         vae.load("decoder.conv_in.weight", np.zeros((64, 16, 3, 2), np.float32))
     with pytest.raises(M.MkError, match="no tensor named"):
         vae.load("decoder.nope.weight", np.zeros(4, np.float32))
+    with pytest.raises(M.MkError, match="mean and std need 16"):
+        M.Vae(16, mean=MEAN[:3], std=STD)
 
 
 def test_vae_full_size_properties(gpu):
