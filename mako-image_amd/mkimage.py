@@ -546,6 +546,8 @@ class Vae:
         return out
 
     def decode_device(self, tokens_dev, h, w, rgba_dev):
+        check_extent(tokens_dev, int(h) * int(w) * 4 * self.z * 4, "mk_vae_decode_device: tokens")
+        check_extent(rgba_dev, 16 * int(h) * 16 * int(w) * 4 * 4, "mk_vae_decode_device: rgba")
         call("mk_vae_decode_device", self.h, int(tokens_dev), h, w, int(rgba_dev))
 
     def stream(self):
@@ -574,6 +576,7 @@ class Engine:
         call("mk_engine_create", C.byref(self.cfg), C.byref(p))
         self.h = p.value
         self._probe_cb = None
+        self._grid = None  # (h, w) of the last begin: the latent extent of the device-buffer steps
 
     def close(self):
         if getattr(self, "h", None) and _lib is not None:
@@ -642,6 +645,7 @@ class Engine:
         if prompt.size == 0 or prompt.size % td:
             raise MkError(f"prompt embeddings must be rows of {td}")
         call("mk_begin", self.h, prompt.ctypes.data, prompt.size // td, h, w, slot)
+        self._grid = (int(h), int(w))
 
     def step(self, latents, sigma, slot=0):
         latents = np.ascontiguousarray(latents, dtype=np.float32)
@@ -656,6 +660,10 @@ class Engine:
         return out
 
     def step_cfg_device(self, lat, sigma, sigma_next, guidance, lat_out, stream=None):
+        if self._grid:
+            nb = self._grid[0] * self._grid[1] * int(self.cfg.latent) * 4
+            check_extent(lat, nb, "mk_step_cfg_device: lat")
+            check_extent(lat_out, nb, "mk_step_cfg_device: lat_out")
         call("mk_step_cfg_device", self.h, int(lat), sigma, sigma_next, guidance, int(lat_out), stream)
 
     def generate(self, noise, sigmas, guidance):
@@ -702,6 +710,9 @@ class Engine:
         return out
 
     def sdxl_forward(self, x_dev, batch, n, y_dev):
+        nb = int(batch) * int(n) * int(self.cfg.dim) * 4
+        check_extent(x_dev, nb, "mk_sdxl_forward: x")
+        check_extent(y_dev, nb, "mk_sdxl_forward: y")
         call("mk_sdxl_forward", self.h, int(x_dev), batch, n, int(y_dev), None)
 
 

@@ -131,3 +131,28 @@ def test_conv_and_attention_extents(stub):
         M.call("mk_attention", 0x1000, k, vt, out, M.BF16, B, H, H, d, T, pad, T, pad, H * d, T * H * d, 0, 0, 0.0,
                None, None)
     assert lib.calls == ["mk_conv3x3"]
+
+
+def test_device_buffer_steps_check_their_extents(stub):
+    # the engine and VAE entry points on caller device buffers: mk_step_cfg_device (latents of the begun grid),
+    # mk_sdxl_forward ([batch][n][c] fp32 in and out) and mk_vae_decode_device (tokens [h w][4 z], RGBA [16 h][16 w][4])
+    lib, alloc = stub
+    import numpy as np
+    e = M.Engine(M.FAMILY_DUAL, blocks=1, dim=256, heads=2, head_dim=128, ffn=512, text_dim=128)
+    e.begin(np.zeros((3, 128), np.float32), 4, 6, 0)
+    lat = alloc(4 * 6 * 64 * 4)
+    e.step_cfg_device(lat, 0.5, 0.4, 4.0, lat)
+    with pytest.raises(M.MkError, match="lat_out"):
+        e.step_cfg_device(lat, 0.5, 0.4, 4.0, alloc(4 * 6 * 64 * 4 - 4))
+    s = M.Engine(M.FAMILY_SDXL, blocks=1, dim=640, heads=10, head_dim=64, ffn=2560, text_dim=2048)
+    x, y = alloc(2 * 100 * 640 * 4), alloc(2 * 100 * 640 * 4)
+    s.sdxl_forward(x, 2, 100, y)
+    with pytest.raises(M.MkError, match="sdxl_forward: x"):
+        s.sdxl_forward(x, 2, 101, y)
+    v = M.Vae(16)
+    tok, rgba = alloc(3 * 5 * 64 * 4), alloc(48 * 80 * 4 * 4)
+    v.decode_device(tok, 3, 5, rgba)
+    with pytest.raises(M.MkError, match="rgba"):
+        v.decode_device(tok, 3, 5, alloc(48 * 80 * 4 * 4 - 16))
+    assert lib.calls.count("mk_step_cfg_device") == 1 and lib.calls.count("mk_sdxl_forward") == 1
+    assert lib.calls.count("mk_vae_decode_device") == 1
