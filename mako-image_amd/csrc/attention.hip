@@ -202,57 +202,6 @@ __global__ __launch_bounds__(64 * NW, 2) __attribute__((amdgpu_waves_per_eu(2, 2
     float m = U ? 0.0f : -1e30f, l = 0.0f;
     const int qpos = int(p.q_pos0) + q0 + r32;
     const bool wave_causal = uint32_t(int(p.q_pos0) + q0) < p.block;
-    // U: the scores arrive as S - m; the first half-tile sets m to its max (every query sees key 0), later ones move
-    // it lazily as below.
-    auto softmax_u = [&](f32x16& sacc, int k0, u32x4 (&pb)[2], bool first, f32x16* other) {
-        if (k0 + 32 > int(p.n_k) || (wave_causal && k0 + 31 > int(p.q_pos0) + q0) || hits_hole(k0, 32)) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int key = k0 + 8 * (r / 4) + 4 * hk + (r % 4);
-                if (key >= int(p.n_k) || (uint32_t(qpos) < p.block && key > qpos) || in_hole(key))
-                    sacc[r] = -__builtin_inff();
-            }
-        }
-        const float mx = max_xor32(max16(sacc));
-        if (first || __any(mx > kLazy)) {
-            const float mn = float((E)(m + (first ? mx : fmaxf(mx, 0.0f))));
-            const float dm = mn - m;
-            const float alpha = first ? 1.0f : __builtin_amdgcn_exp2f(-dm);
-            m = mn;
-            if (hk == 0)
-                qm[0] = (E)(-m);
-            l *= alpha;
-#pragma unroll
-            for (int r = 0; r < 16; ++r)
-                sacc[r] -= dm;
-            if (other) // the next half's scores, computed against the old m
-#pragma unroll
-                for (int r = 0; r < 16; ++r)
-                    (*other)[r] -= dm;
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-                for (int r = 0; r < 16; ++r)
-                    oacc[dt][r] *= alpha;
-        }
-        // row sums as four two-deep dot2 chains (one chain of eight serialises on the accumulator)
-                float ls[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int st = 0; st < 2; ++st) {
-            const int o = 8 * st;
-            u32x4 v;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                // (bit-cast from a scalar: this compiler miscompiles a bit-cast of a vector element here)
-                const uint32_t pj = X::pack(__builtin_amdgcn_exp2f(sacc[o + 2 * j]),
-                                               __builtin_amdgcn_exp2f(sacc[o + 2 * j + 1]));
-                v[j] = pj;
-                ls[j] = X::sum2(pj, ls[j]);
-            }
-            pb[st] = v;
-        }
-        l += (ls[0] + ls[1]) + (ls[2] + ls[3]);
-    };
     auto softmax = [&](f32x16& sacc, int k0, u32x4 (&pb)[2]) {
         if (k0 + 32 > int(p.n_k) || (wave_causal && k0 + 31 > int(p.q_pos0) + q0) || hits_hole(k0, 32)) {
 #pragma unroll
@@ -291,13 +240,11 @@ __global__ __launch_bounds__(64 * NW, 2) __attribute__((amdgpu_waves_per_eu(2, 2
     };
     issue(0, 0);
     f32x16 s_a, s_b;
-    // one 64-key tile from buffer `buf` (a constant: the loop is unrolled by two, so the LDS reads and the next
-    // tile's loads provably touch different buffers and the reads wait for nothing but themselves)
-    // One 64-key tile from buffer `buf` (a constant: the loop is unrolled by two, so the LDS reads and the next
-    // tile's loads provably touch different buffers and the reads wait for nothing but themselves). The tile's 32
-    // fragment reads (K of both 32-key halves interleaved, then V of each half) stream four ahead of the MFMAs that
-    // use them, in a fixed order (fenced); the two halves' S^T products alternate so neither accumulator chain
-    // waits on its previous MFMA.
+    // General scale: one 64-key tile from buffer `buf` (a constant: the loop is unrolled by two, so the LDS reads and
+    // the next tile's loads provably touch different buffers and the reads wait for nothing but themselves). The
+    // tile's 32 fragment reads (K of both 32-key halves interleaved, then V of each half) stream four ahead of the
+    // MFMAs that use them, in a fixed order (fenced); the two halves' S^T products alternate so neither accumulator
+    // chain waits on its previous MFMA.
     constexpr int LA = 4; // fragment reads in flight ahead of their MFMA
     auto tile = [&](int t, auto buf_c) {
         constexpr int buf = decltype(buf_c)::value;
@@ -322,11 +269,6 @@ __global__ __launch_bounds__(64 * NW, 2) __attribute__((amdgpu_waves_per_eu(2, 2
         __builtin_amdgcn_sched_barrier(0);
         s_a = f32x16{};
         s_b = f32x16{};
-        if constexpr (U) {
-            s_a = X::mfma(kone, qm, s_a, 0, 0, 0);
-            s_b = X::mfma(kone, qm, s_b, 0, 0, 0);
-            __builtin_amdgcn_sched_barrier(0);
-        }
 #pragma unroll
         for (int g = 0; g < 2 * DS; ++g) {
             f32x16& acc = g % 2 ? s_b : s_a;
@@ -347,15 +289,9 @@ __global__ __launch_bounds__(64 * NW, 2) __attribute__((amdgpu_waves_per_eu(2, 2
                 __builtin_amdgcn_sched_barrier(0);
             }
         };
-        if constexpr (U) {
-            softmax_u(s_a, t * kKT, pb, t == 0, &s_b);
-            pv(0);
-            softmax_u(s_b, t * kKT + 32, pb, false, nullptr);
-        } else {
-            softmax(s_a, t * kKT, pb);
-            pv(0);
-            softmax(s_b, t * kKT + 32, pb);
-        }
+        softmax(s_a, t * kKT, pb);
+        pv(0);
+        softmax(s_b, t * kKT + 32, pb);
         pv(1);
     };
     // U: one 64-key tile with the softmax work in the matrix core's shadow. The scores arrive as S - m, so each
