@@ -22,10 +22,6 @@ typedef __attribute__((__vector_size__(2 * sizeof(uint32_t)))) uint32_t u32x2;
 constexpr int kWave = 64;
 
 typedef __attribute__((address_space(3))) void lds_void;
-// 16 bytes global -> LDS without a register round trip (global_load_lds_dwordx4): lane i's bytes land at
-// lds + 16 * i (lds wave-uniform). The source goes through `const void*`: a typed pointer there makes the host pass
-// drop the kernel's launch stub without a diagnostic.
-__device__ inline void load_lds16(const void* src, lds_void* lds) { __builtin_amdgcn_global_load_lds(src, lds, 16, 0, 0); }
 
 // Buffer resource (raw, dword format) over `bytes` bytes from `base`, and a 16-byte load through it into LDS at
 // byte offset voff + soff: the buffer form of the direct-to-LDS load. Unlike the global form it does not count as
@@ -191,20 +187,6 @@ __device__ inline uint32_t pack_x2(float a, float b, bool f16) { return f16 ? pa
 __device__ inline uint32_t bf16x2_to_f16x2(uint32_t v)
 {
     return pack_f16x2(__builtin_bit_cast(float, v << 16), __builtin_bit_cast(float, v & 0xffff0000u));
-}
-
-// ---- OCP fp8 e4m3 -> float (exact) ----
-__host__ __device__ inline float e4m3_to_f32(uint8_t b)
-{
-    const uint32_t s = b >> 7, e = (b >> 3) & 15u, m = b & 7u;
-    float v;
-    if (e == 0)
-        v = float(m) * 0.001953125f; // m / 8 * 2^-6
-    else
-        v = __builtin_bit_cast(float, ((e + 120u) << 23) | (m << 20));
-    if (e == 15 && m == 7)
-        v = __builtin_nanf("");
-    return s ? -v : v;
 }
 
 // ---- wave64 reductions, every lane gets the result ----
