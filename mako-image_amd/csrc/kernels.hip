@@ -514,14 +514,16 @@ __global__ __launch_bounds__(512) void gemv1_kernel(const float* __restrict__ x,
     constexpr uint32_t K = 512 * KI;
     __shared__ __attribute__((aligned(16))) uint16_t xs[K];
     const uint32_t lane = threadIdx.x & 63, n0 = (blockIdx.x * 8 + (threadIdx.x >> 6)) * 4;
-    // the wave's 4 weight rows first (16-byte chunks, all in flight; rows past N read the last row)
+    // the wave's 4 weight rows first (16-byte chunks, all in flight; rows past N read the last row), as nontemporal
+    // loads: the stacked modulation matrix streams through once a step and is not kept in the caches
     u32x4 wv[4][KI];
     if (n0 < N)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
             for (int i = 0; i < KI; ++i)
-                wv[j][i] = *reinterpret_cast<const u32x4*>(w + uint64_t(min(n0 + j, N - 1)) * K + lane * 8 + 512 * i);
+                wv[j][i] = __builtin_nontemporal_load(
+                    reinterpret_cast<const u32x4*>(w + uint64_t(min(n0 + j, N - 1)) * K + lane * 8 + 512 * i));
     // meanwhile the input row, once a workgroup, as the GEMMs' bf16 activation operand (silu first when asked)
     for (uint32_t k = threadIdx.x; k < K / 2; k += 512) {
         float a = x[2 * k], b = x[2 * k + 1];
